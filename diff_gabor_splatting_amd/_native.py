@@ -1,0 +1,530 @@
+"""Host side of the HIP library: the reference's ``_C`` operators over the C ABI.
+
+The reference binds four pybind11 functions (``src/gabor_splatting/csrc/
+bindings.cpp:5-10``): ``rasterize_forward``, ``rasterize_backward``,
+``evaluate_sh_forward`` and ``evaluate_sh_backward``. This module exposes the
+same names, argument meaning and error behaviour (structural violations raise
+``RuntimeError`` like ``TORCH_CHECK``), implemented by allocating outputs with
+the torch caching allocator and calling ``libgabor_hip.so`` through ctypes on
+the current HIP stream. It adds the projection operators (the reference runs
+projection as PyTorch ops) and visible-pair packing.
+
+The library is loaded at import; there is no fallback path.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from pathlib import Path
+
+import torch
+
+_LIBRARY_PATH = Path(__file__).resolve().parent / "libgabor_hip.so"
+
+TILE = 16
+GEOMETRY_SIZE = 17
+MAP_SIZE = 9
+INT_MAX = 2**31 - 1
+
+_c_int = ctypes.c_int32
+_c_i64 = ctypes.c_int64
+_c_size = ctypes.c_size_t
+_c_float = ctypes.c_float
+_c_ptr = ctypes.c_void_p
+
+_SIGNATURES = {
+    "gs_last_error": (ctypes.c_char_p, []),
+    "gs_abi_version": (_c_int, []),
+    "gs_project_forward": (
+        _c_int,
+        [_c_ptr] * 5 + [_c_i64] * 3 + [_c_int, _c_int, _c_float, _c_float] + [_c_ptr] * 6,
+    ),
+    "gs_project_backward_workspace_size": (_c_size, [_c_i64] * 3),
+    "gs_project_backward": (
+        _c_int,
+        [_c_ptr] * 5 + [_c_i64] * 3 + [_c_ptr] * 9 + [_c_ptr, _c_size, _c_ptr],
+    ),
+    "gs_sh_forward": (_c_int, [_c_ptr] * 4 + [_c_i64] * 3 + [_c_int, _c_ptr]),
+    "gs_sh_backward": (_c_int, [_c_ptr] * 7 + [_c_i64] * 3 + [_c_int, _c_ptr]),
+    "gs_scan_workspace_size": (_c_size, [_c_i64]),
+    "gs_pack_visible": (_c_int, [_c_ptr, _c_i64, _c_ptr, _c_ptr, _c_ptr, _c_size, _c_ptr]),
+    "gs_count_tiles": (
+        _c_int,
+        [_c_ptr, _c_ptr, _c_i64, _c_int, _c_int, _c_ptr, _c_ptr, _c_size, _c_ptr],
+    ),
+    "gs_emit_tiles": (
+        _c_int,
+        [_c_ptr] * 4 + [_c_i64, _c_int, _c_int, _c_ptr, _c_ptr, _c_ptr],
+    ),
+    "gs_sort_workspace_size": (_c_size, [_c_i64]),
+    "gs_sort_pairs": (
+        _c_int,
+        [_c_ptr] * 4 + [_c_i64, _c_int, _c_int, _c_ptr, _c_size, _c_ptr],
+    ),
+    "gs_find_ranges": (_c_int, [_c_ptr, _c_i64, _c_ptr, _c_i64, _c_ptr]),
+    "gs_render_forward": (
+        _c_int,
+        [_c_int]
+        + [_c_ptr] * 7
+        + [_c_i64, _c_int, _c_int, _c_float, _c_float]
+        + [_c_ptr] * 4,
+    ),
+    "gs_render_backward": (
+        _c_int,
+        [_c_int]
+        + [_c_ptr] * 10
+        + [_c_i64, _c_int, _c_int, _c_float, _c_float]
+        + [_c_ptr] * 5,
+    ),
+    "gs_profile_enable": (_c_int, [_c_int]),
+    "gs_profile_read": (_c_int, [_c_int, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(_c_i64)]),
+}
+
+PROFILE_FAMILIES = {
+    "project_forward": 0,
+    "project_backward": 1,
+    "sh_forward": 2,
+    "sh_backward": 3,
+    "binning": 4,
+    "sort": 5,
+    "render_forward": 6,
+    "render_backward": 7,
+}
+
+
+def _load() -> ctypes.CDLL:
+    if not _LIBRARY_PATH.exists():
+        raise ImportError(
+            f"{_LIBRARY_PATH.name} is not built; run `python -m diff_gabor_splatting_amd.build` "
+            "(or __graft_entry__.build()) first. There is no CPU fallback."
+        )
+    library = ctypes.CDLL(str(_LIBRARY_PATH))
+    for name, (restype, argtypes) in _SIGNATURES.items():
+        function = getattr(library, name)
+        function.restype = restype
+        function.argtypes = argtypes
+    return library
+
+
+lib = _load()
+
+
+def exported_symbols() -> list[str]:
+    """Names of every C-ABI entry point this module binds."""
+    return list(_SIGNATURES)
+
+
+def _check(status: int) -> None:
+    if status != 0:
+        message = lib.gs_last_error().decode(errors="replace")
+        raise RuntimeError(message or f"gabor HIP call failed with status {status}")
+
+
+def _ptr(tensor: torch.Tensor | None) -> int | None:
+    return None if tensor is None else tensor.data_ptr()
+
+
+def _stream(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def _workspace(nbytes: int, device: torch.device) -> torch.Tensor:
+    return torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=device)
+
+
+def _require(condition: bool, message: str) -> None:
+    if not condition:
+        raise RuntimeError(message)
+
+
+def _check_float(value: torch.Tensor, geometry: torch.Tensor) -> None:
+    """Mirror of checkFloat (rasterize.cu:402-407)."""
+    _require(
+        value.is_cuda and value.dtype == torch.float32,
+        "native rendering requires CUDA float32 tensors",
+    )
+    _require(
+        value.device == geometry.device and value.is_contiguous(),
+        "native buffers must be contiguous on the geometry device",
+    )
+
+
+def _check_buffers(geometry, appearance, opacities, primitive_ids, backgrounds, neural) -> None:
+    """Mirror of checkBuffers (rasterize.cu:410-422)."""
+    for value in (geometry, appearance, opacities, backgrounds):
+        _check_float(value, geometry)
+    _require(
+        geometry.dim() == 2 and geometry.size(1) == GEOMETRY_SIZE, "invalid geometry shape"
+    )
+    _require(geometry.size(0) <= INT_MAX, "too many projected primitives")
+    _require(
+        appearance.dim() == 2 and appearance.size(1) == (57 if neural else 18),
+        "invalid appearance shape",
+    )
+    _require(
+        opacities.dim() == 1 and opacities.size(0) == appearance.size(0), "invalid opacity shape"
+    )
+    _require(
+        backgrounds.dim() == 2 and backgrounds.size(1) == 3 and backgrounds.size(0) > 0,
+        "invalid backgrounds",
+    )
+    _require(
+        primitive_ids.device == geometry.device
+        and primitive_ids.is_contiguous()
+        and primitive_ids.dtype == torch.int64
+        and primitive_ids.dim() == 1
+        and primitive_ids.size(0) == geometry.size(0),
+        "invalid primitive IDs",
+    )
+
+
+def tile_grid(width: int, height: int) -> tuple[int, int]:
+    """Tiles per row and per column: ceil(W/16) x ceil(H/16)."""
+    return (width + TILE - 1) // TILE, (height + TILE - 1) // TILE
+
+
+def sort_end_bit(tile_count: int) -> int:
+    """Highest key bit that can be set: 32 depth bits plus the tile-id width."""
+    return 32 + max(int(tile_count) - 1, 0).bit_length()
+
+
+def check_intersections(count: int) -> None:
+    """Intersection-count guard of rasterizeForward (rasterize.cu:469)."""
+    _require(count <= INT_MAX, "tile intersection count exceeds int32")
+
+
+def check_image_tiles(images: int, width: int, height: int) -> None:
+    """Image-tile guard of rasterizeForward (rasterize.cu:443-445)."""
+    tw, th = tile_grid(width, height)
+    _require(images * tw * th <= INT_MAX, "image tile count exceeds int32")
+
+
+# --------------------------------------------------------------------------
+# Binning primitives (exposed separately for bit-exact tests).
+
+
+def count_tiles(geometry: torch.Tensor, radii: torch.Tensor, width: int, height: int):
+    """Inclusive prefix sum of per-pair tile counts (int64 [Q])."""
+    device = geometry.device
+    count = geometry.size(0)
+    offsets = torch.empty(count, dtype=torch.int64, device=device)
+    if count:
+        workspace = _workspace(lib.gs_scan_workspace_size(count), device)
+        _check(
+            lib.gs_count_tiles(
+                _ptr(geometry), _ptr(radii), count, width, height, _ptr(offsets),
+                _ptr(workspace), workspace.numel(), _stream(device),
+            )
+        )
+    return offsets
+
+
+def emit_tiles(geometry, radii, image_ids, offsets, width, height, intersections):
+    """Unsorted (key, value) pairs, one per covered tile (rasterize.cu:43-56)."""
+    device = geometry.device
+    keys = torch.empty(intersections, dtype=torch.int64, device=device)
+    values = torch.empty(intersections, dtype=torch.int32, device=device)
+    if intersections:
+        _check(
+            lib.gs_emit_tiles(
+                _ptr(geometry), _ptr(radii), _ptr(image_ids), _ptr(offsets), geometry.size(0),
+                width, height, _ptr(keys), _ptr(values), _stream(device),
+            )
+        )
+    return keys, values
+
+
+def sort_pairs(keys: torch.Tensor, values: torch.Tensor, begin_bit: int = 0, end_bit: int = 64):
+    """Stable LSD radix sort of uint64 keys (stored as int64) with int32 values."""
+    device = keys.device
+    m = keys.numel()
+    sorted_keys = torch.empty_like(keys)
+    sorted_values = torch.empty_like(values)
+    if m:
+        workspace = _workspace(lib.gs_sort_workspace_size(m), device)
+        _check(
+            lib.gs_sort_pairs(
+                _ptr(keys), _ptr(sorted_keys), _ptr(values), _ptr(sorted_values), m, begin_bit,
+                end_bit, _ptr(workspace), workspace.numel(), _stream(device),
+            )
+        )
+    return sorted_keys, sorted_values
+
+
+def find_ranges(sorted_keys: torch.Tensor, tiles: int) -> torch.Tensor:
+    """Per-tile [first, last) runs of the sorted keys (int32 [tiles, 2])."""
+    device = sorted_keys.device
+    ranges = torch.empty((tiles, 2), dtype=torch.int32, device=device)
+    _check(
+        lib.gs_find_ranges(
+            _ptr(sorted_keys), sorted_keys.numel(), _ptr(ranges), tiles, _stream(device)
+        )
+    )
+    return ranges
+
+
+def pack_visible(radii: torch.Tensor) -> torch.Tensor:
+    """Ascending indices of pairs with radii > 0 (int64). Synchronises once."""
+    device = radii.device
+    flat = radii.reshape(-1)
+    count = flat.numel()
+    selected = torch.empty(max(count, 1), dtype=torch.int64, device=device)
+    total = torch.empty(1, dtype=torch.int64, device=device)
+    workspace = _workspace(lib.gs_scan_workspace_size(count), device)
+    _check(
+        lib.gs_pack_visible(
+            _ptr(flat), count, _ptr(selected), _ptr(total), _ptr(workspace), workspace.numel(),
+            _stream(device),
+        )
+    )
+    return selected[: int(total.item())]
+
+
+# --------------------------------------------------------------------------
+# Compositor operators (the reference's _C.rasterize_forward / backward).
+
+
+def rasterize_forward(
+    geometry, appearance, opacities, primitive_ids, image_ids, radii, backgrounds,
+    width, height, neural, near_plane, far_plane,
+):
+    """Bin, sort and composite: returns [maps, point_list, ranges, state, contributors].
+
+    Mirrors rasterizeForward (rasterize.cu:426-503), including its structural
+    checks, its one host synchronisation for the intersection count and its
+    output shapes: maps [I,H,W,9], point_list int32 [M], ranges int32
+    [I*tw*th, 2], state [I,H,W,3], contributors int32 [I,H,W].
+    """
+    _check_buffers(geometry, appearance, opacities, primitive_ids, backgrounds, neural)
+    _require(
+        0 < width < INT_MAX - TILE and 0 < height < INT_MAX - TILE, "invalid image dimensions"
+    )
+    _require(near_plane > 0 and far_plane > near_plane, "invalid clipping planes")
+    _require(
+        image_ids.device == geometry.device
+        and image_ids.is_contiguous()
+        and image_ids.dtype == torch.int64
+        and image_ids.dim() == 1
+        and image_ids.size(0) == geometry.size(0),
+        "invalid image IDs",
+    )
+    _require(
+        radii.device == geometry.device
+        and radii.is_contiguous()
+        and radii.dtype == torch.int32
+        and radii.dim() == 1
+        and radii.size(0) == geometry.size(0),
+        "invalid radii",
+    )
+    device = geometry.device
+    with torch.cuda.device(device):
+        stream = _stream(device)
+        count = geometry.size(0)
+        images = backgrounds.size(0)
+        tw, th = tile_grid(width, height)
+        check_image_tiles(images, width, height)
+        tiles = images * tw * th
+        maps = torch.empty((images, height, width, MAP_SIZE), dtype=torch.float32, device=device)
+        state = torch.empty((images, height, width, 3), dtype=torch.float32, device=device)
+        contributors = torch.empty((images, height, width), dtype=torch.int32, device=device)
+        point_list = torch.empty(0, dtype=torch.int32, device=device)
+        sorted_keys = torch.empty(0, dtype=torch.int64, device=device)
+        if count > 0:
+            offsets = count_tiles(geometry, radii, width, height)
+            intersections = int(offsets[-1].item())
+            check_intersections(intersections)
+            if intersections > 0:
+                keys, values = emit_tiles(
+                    geometry, radii, image_ids, offsets, width, height, intersections
+                )
+                sorted_keys, point_list = sort_pairs(keys, values, 0, sort_end_bit(tiles))
+        ranges = find_ranges(sorted_keys, tiles)
+        _check(
+            lib.gs_render_forward(
+                int(bool(neural)), _ptr(geometry), _ptr(appearance), _ptr(opacities),
+                _ptr(primitive_ids), _ptr(backgrounds), _ptr(point_list), _ptr(ranges), images,
+                width, height, near_plane, far_plane, _ptr(maps), _ptr(state),
+                _ptr(contributors), stream,
+            )
+        )
+    return [maps, point_list, ranges, state, contributors]
+
+
+def rasterize_backward(
+    geometry, appearance, opacities, primitive_ids, backgrounds, point_list, ranges, state,
+    contributors, grad_maps, width, height, neural, near_plane, far_plane,
+):
+    """Reverse compositing: returns [grad_geometry, grad_appearance, grad_opacities,
+    grad_backgrounds] (rasterize.cu:506-529)."""
+    _check_buffers(geometry, appearance, opacities, primitive_ids, backgrounds, neural)
+    _check_float(grad_maps, geometry)
+    device = geometry.device
+    images = backgrounds.size(0)
+    _require(
+        grad_maps.shape == (images, height, width, MAP_SIZE)
+        and state.shape == (images, height, width, 3)
+        and contributors.shape == (images, height, width),
+        "invalid saved compositor state",
+    )
+    with torch.cuda.device(device):
+        gg = torch.zeros_like(geometry)
+        ga = torch.zeros_like(appearance)
+        go = torch.zeros_like(opacities)
+        gb = torch.zeros_like(backgrounds)
+        _check(
+            lib.gs_render_backward(
+                int(bool(neural)), _ptr(geometry), _ptr(appearance), _ptr(opacities),
+                _ptr(primitive_ids), _ptr(backgrounds), _ptr(point_list), _ptr(ranges),
+                _ptr(state), _ptr(contributors), _ptr(grad_maps), images, width, height,
+                near_plane, far_plane, _ptr(gg), _ptr(ga), _ptr(go), _ptr(gb), _stream(device),
+            )
+        )
+    return [gg, ga, go, gb]
+
+
+# --------------------------------------------------------------------------
+# Spherical harmonics (the reference's _C.evaluate_sh_forward / backward).
+
+
+def _check_sh(first, second, directions, degree) -> None:
+    """Mirror of checkSH (spherical_harmonics.cu:88-103)."""
+    _require(0 <= degree <= 3, "SH degree must be 0 through 3")
+    for value in (first, second, directions):
+        _require(
+            value.is_cuda
+            and value.dtype == torch.float32
+            and value.is_contiguous()
+            and value.device == first.device,
+            "SH tensors must be contiguous float32 on the same CUDA device",
+        )
+    _require(
+        first.dim() == 4
+        and second.shape == first.shape
+        and first.size(2) == (degree + 1) ** 2
+        and first.size(3) == 3,
+        "SH coefficients must have shape [B, N, K, 3]",
+    )
+    _require(
+        directions.dim() == 4
+        and directions.size(0) == first.size(0)
+        and directions.size(2) == first.size(1)
+        and directions.size(3) == 3,
+        "SH directions must have shape [B, C, N, 3]",
+    )
+    _require(directions.numel() // 3 <= INT_MAX, "too many SH pairs")
+
+
+def evaluate_sh_forward(first, second, directions, degree):
+    """Both SH colours per (scene, camera, surfel): [S, C, N, 6]."""
+    _check_sh(first, second, directions, degree)
+    device = first.device
+    scenes, cameras, n = directions.shape[:3]
+    with torch.cuda.device(device):
+        colors = torch.empty((scenes, cameras, n, 6), dtype=torch.float32, device=device)
+        _check(
+            lib.gs_sh_forward(
+                _ptr(first), _ptr(second), _ptr(directions), _ptr(colors), scenes, cameras, n,
+                degree, _stream(device),
+            )
+        )
+    return colors
+
+
+def evaluate_sh_backward(first, second, directions, grad_colors, degree):
+    """Coefficient gradients summed over cameras and per-pair direction gradients."""
+    _check_sh(first, second, directions, degree)
+    _require(
+        grad_colors.device == first.device
+        and grad_colors.dtype == torch.float32
+        and grad_colors.is_contiguous()
+        and grad_colors.shape == (*directions.shape[:3], 6),
+        "invalid SH color gradients",
+    )
+    device = first.device
+    scenes, cameras, n = directions.shape[:3]
+    with torch.cuda.device(device):
+        gf = torch.empty_like(first)
+        gs = torch.empty_like(second)
+        gd = torch.empty_like(directions)
+        _check(
+            lib.gs_sh_backward(
+                _ptr(first), _ptr(second), _ptr(directions), _ptr(grad_colors), _ptr(gf),
+                _ptr(gs), _ptr(gd), scenes, cameras, n, degree, _stream(device),
+            )
+        )
+    return [gf, gs, gd]
+
+
+# --------------------------------------------------------------------------
+# Projection (the reference's PyTorch project_surfaces, rendering.py:176-218).
+
+
+def project_forward(means, quaternions, scales, view_matrices, intrinsics, width, height,
+                    near_plane, far_plane):
+    """Returns transform [S,C,N,3,3], xy [S,C,N,2], normals [S,C,N,3],
+    directions [S,C,N,3] and radii int32 [S,C,N]."""
+    device = means.device
+    scenes, n = means.shape[:2]
+    cameras = view_matrices.shape[1]
+    with torch.cuda.device(device):
+        transform = torch.empty((scenes, cameras, n, 3, 3), dtype=torch.float32, device=device)
+        xy = torch.empty((scenes, cameras, n, 2), dtype=torch.float32, device=device)
+        normals = torch.empty((scenes, cameras, n, 3), dtype=torch.float32, device=device)
+        directions = torch.empty((scenes, cameras, n, 3), dtype=torch.float32, device=device)
+        radii = torch.empty((scenes, cameras, n), dtype=torch.int32, device=device)
+        _check(
+            lib.gs_project_forward(
+                _ptr(means), _ptr(quaternions), _ptr(scales), _ptr(view_matrices),
+                _ptr(intrinsics), scenes, cameras, n, width, height, near_plane, far_plane,
+                _ptr(transform), _ptr(xy), _ptr(normals), _ptr(directions), _ptr(radii),
+                _stream(device),
+            )
+        )
+    return transform, xy, normals, directions, radii
+
+
+def project_backward(means, quaternions, scales, view_matrices, intrinsics, grad_transform,
+                     grad_xy, grad_normals, grad_directions):
+    """Gradients of (means, quaternions, scales, view_matrices, intrinsics)."""
+    device = means.device
+    scenes, n = means.shape[:2]
+    cameras = view_matrices.shape[1]
+
+    def contiguous(value):
+        return None if value is None else value.contiguous()
+
+    grad_transform, grad_xy = contiguous(grad_transform), contiguous(grad_xy)
+    grad_normals, grad_directions = contiguous(grad_normals), contiguous(grad_directions)
+    with torch.cuda.device(device):
+        g_means = torch.empty_like(means)
+        g_quats = torch.empty_like(quaternions)
+        g_scales = torch.empty_like(scales)
+        g_views = torch.empty_like(view_matrices)
+        g_intrinsics = torch.empty_like(intrinsics)
+        workspace = _workspace(lib.gs_project_backward_workspace_size(scenes, cameras, n), device)
+        _check(
+            lib.gs_project_backward(
+                _ptr(means), _ptr(quaternions), _ptr(scales), _ptr(view_matrices),
+                _ptr(intrinsics), scenes, cameras, n, _ptr(grad_transform), _ptr(grad_xy),
+                _ptr(grad_normals), _ptr(grad_directions), _ptr(g_means), _ptr(g_quats),
+                _ptr(g_scales), _ptr(g_views), _ptr(g_intrinsics), _ptr(workspace),
+                workspace.numel(), _stream(device),
+            )
+        )
+    return g_means, g_quats, g_scales, g_views, g_intrinsics
+
+
+# --------------------------------------------------------------------------
+# Kernel timing.
+
+
+def profile_enable(enable: bool) -> None:
+    _check(lib.gs_profile_enable(1 if enable else 0))
+
+
+def profile_read(family: str) -> tuple[float, int]:
+    """Total milliseconds and launch count of one kernel family."""
+    total = ctypes.c_double()
+    launches = _c_i64()
+    _check(lib.gs_profile_read(PROFILE_FAMILIES[family], ctypes.byref(total), ctypes.byref(launches)))
+    return total.value, launches.value

@@ -1,0 +1,215 @@
+// Kernel 2: visible-pair packing and tile binning, plus kernel 3's range
+// extraction.
+//
+// Tile rectangles use exactly the reference's float32 expressions
+// (src/gabor_splatting/csrc/rasterize.cu:24-30):
+//   x0 = int((x - r) / 16), x1 = int(((x + r) + 16 - 1) / 16), clamped to
+//   [0, tw] (and y likewise), evaluated left to right in float32,
+// so keys and ranges are bit-identical to the reference's for the same
+// geometry and radii. Counts are computed on the fly inside the scan
+// (never stored), then each pair emits one (key, value) per covered tile.
+#include <climits>
+
+#include "common.hpp"
+#include "scan.hpp"
+
+namespace gs {
+namespace {
+
+// C++ int(float) on the reference's hardware truncates and saturates;
+// the explicit form keeps that behaviour defined for any input.
+__device__ __forceinline__ int trunc_to_int(float v) {
+  if (v != v) return 0;
+  if (v >= 2147483648.f) return INT_MAX;
+  if (v <= -2147483648.f) return INT_MIN;
+  return int(v);
+}
+
+struct TileRect {
+  int x0, y0, x1, y1;
+};
+
+__device__ __forceinline__ TileRect tile_rect(float cx, float cy, int radius, int tw, int th) {
+  const float r = float(radius);
+  TileRect t;
+  t.x0 = max(0, min(tw, trunc_to_int((cx - r) / 16.f)));
+  t.y0 = max(0, min(th, trunc_to_int((cy - r) / 16.f)));
+  t.x1 = max(0, min(tw, trunc_to_int((((cx + r) + 16.f) - 1.f) / 16.f)));
+  t.y1 = max(0, min(th, trunc_to_int((((cy + r) + 16.f) - 1.f) / 16.f)));
+  return t;
+}
+
+struct TileCountLoad {
+  const float* geometry;
+  const int* radii;
+  int tw, th;
+  __device__ int64_t operator()(int64_t i) const {
+    const int r = radii[i];
+    if (r <= 0) return 0;
+    const TileRect t = tile_rect(geometry[i * kGeometry + 9], geometry[i * kGeometry + 10], r, tw, th);
+    return int64_t(t.x1 - t.x0) * int64_t(t.y1 - t.y0);
+  }
+};
+
+struct InclusiveStore {
+  int64_t* out;
+  __device__ void operator()(int64_t i, int64_t inclusive, int64_t) const { out[i] = inclusive; }
+};
+
+struct VisibleLoad {
+  const int* radii;
+  __device__ int64_t operator()(int64_t i) const { return radii[i] > 0 ? 1 : 0; }
+};
+
+struct SelectStore {
+  int64_t* selected;
+  int64_t* num_selected;
+  int64_t count;
+  __device__ void operator()(int64_t i, int64_t inclusive, int64_t flag) const {
+    if (flag) selected[inclusive - 1] = i;
+    if (i == count - 1) *num_selected = inclusive;
+  }
+};
+
+__global__ __launch_bounds__(256) void zero_count_kernel(int64_t* value) {
+  if (threadIdx.x == 0 && blockIdx.x == 0) *value = 0;
+}
+
+__global__ __launch_bounds__(256) void emit_tiles_kernel(
+    int64_t count, int tw, int th, const float* __restrict__ geometry,
+    const int* __restrict__ radii, const int64_t* __restrict__ image_ids,
+    const int64_t* __restrict__ offsets, uint64_t* __restrict__ keys,
+    int* __restrict__ values) {
+  const int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x;
+  if (i >= count) return;
+  const int r = radii[i];
+  if (r <= 0) return;
+  const float* g = geometry + i * kGeometry;
+  const TileRect t = tile_rect(g[9], g[10], r, tw, th);
+  int64_t out = i == 0 ? 0 : offsets[i - 1];
+  const uint64_t image_base = uint64_t(image_ids[i]) * uint64_t(tw) * uint64_t(th);
+  const uint64_t depth_bits = __float_as_uint(g[8]);
+  for (int y = t.y0; y < t.y1; ++y)
+    for (int x = t.x0; x < t.x1; ++x) {
+      const uint64_t tile = image_base + uint64_t(y * tw + x);
+      keys[out] = (tile << 32) | depth_bits;
+      values[out] = int(i);
+      ++out;
+    }
+}
+
+__global__ __launch_bounds__(256) void fill_ranges_kernel(int64_t tiles, int2* __restrict__ ranges) {
+  const int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x;
+  if (i < tiles) ranges[i] = make_int2(0, 0);
+}
+
+// Keys whose tile id lies outside [0, tiles) are ignored rather than
+// written out of bounds.
+__global__ __launch_bounds__(256) void find_ranges_kernel(int64_t m, int64_t tiles,
+                                                          const uint64_t* __restrict__ keys,
+                                                          int2* __restrict__ ranges) {
+  const int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x;
+  if (i >= m) return;
+  const uint64_t tile = keys[i] >> 32;
+  const bool own = tile < uint64_t(tiles);
+  if (i == 0) {
+    if (own) ranges[tile].x = 0;
+  } else {
+    const uint64_t previous = keys[i - 1] >> 32;
+    if (tile != previous) {
+      if (previous < uint64_t(tiles)) ranges[previous].y = int(i);
+      if (own) ranges[tile].x = int(i);
+    }
+  }
+  if (i == m - 1 && own) ranges[tile].y = int(m);
+}
+
+}  // namespace
+}  // namespace gs
+
+extern "C" {
+
+size_t gs_scan_workspace_size(int64_t count) {
+  return gs::scan_workspace_bytes(count, sizeof(int64_t));
+}
+
+int gs_pack_visible(const int32_t* radii, int64_t count, int64_t* selected,
+                    int64_t* num_selected, void* workspace, size_t workspace_bytes,
+                    void* stream) {
+  using namespace gs;
+  clear_error();
+  GS_REQUIRE(count >= 0, GS_ERR_ARGUMENT, "negative count");
+  GS_REQUIRE(num_selected, GS_ERR_ARGUMENT, "null num_selected");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  ProfileScope prof(GS_PROF_BINNING, s);
+  if (count == 0) {
+    zero_count_kernel<<<1, 64, 0, s>>>(num_selected);
+    GS_LAUNCHED("zero_count_kernel");
+    return GS_OK;
+  }
+  GS_REQUIRE(radii && selected, GS_ERR_ARGUMENT, "null pointer passed to gs_pack_visible");
+  const size_t need = gs_scan_workspace_size(count);
+  GS_REQUIRE(workspace && workspace_bytes >= need, GS_ERR_WORKSPACE,
+             "packing needs %zu workspace bytes, got %zu", need, workspace_bytes);
+  return run_scan<int64_t>(count, VisibleLoad{radii}, SelectStore{selected, num_selected, count},
+                           static_cast<int64_t*>(workspace), s);
+}
+
+int gs_count_tiles(const float* geometry, const int32_t* radii, int64_t count, int32_t width,
+                   int32_t height, int64_t* offsets, void* workspace, size_t workspace_bytes,
+                   void* stream) {
+  using namespace gs;
+  clear_error();
+  GS_REQUIRE(count >= 0 && count <= INT_MAX, GS_ERR_OVERFLOW, "too many projected primitives");
+  GS_REQUIRE(width > 0 && height > 0, GS_ERR_ARGUMENT, "invalid image dimensions");
+  if (count == 0) return GS_OK;
+  GS_REQUIRE(geometry && radii && offsets, GS_ERR_ARGUMENT,
+             "null pointer passed to gs_count_tiles");
+  const size_t need = gs_scan_workspace_size(count);
+  GS_REQUIRE(workspace && workspace_bytes >= need, GS_ERR_WORKSPACE,
+             "tile count needs %zu workspace bytes, got %zu", need, workspace_bytes);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  ProfileScope prof(GS_PROF_BINNING, s);
+  return run_scan<int64_t>(count, TileCountLoad{geometry, radii, tiles_x(width), tiles_y(height)},
+                           InclusiveStore{offsets}, static_cast<int64_t*>(workspace), s);
+}
+
+int gs_emit_tiles(const float* geometry, const int32_t* radii, const int64_t* image_ids,
+                  const int64_t* offsets, int64_t count, int32_t width, int32_t height,
+                  uint64_t* keys, int32_t* values, void* stream) {
+  using namespace gs;
+  clear_error();
+  GS_REQUIRE(count >= 0 && count <= INT_MAX, GS_ERR_OVERFLOW, "too many projected primitives");
+  GS_REQUIRE(width > 0 && height > 0, GS_ERR_ARGUMENT, "invalid image dimensions");
+  if (count == 0) return GS_OK;
+  GS_REQUIRE(geometry && radii && image_ids && offsets && keys && values, GS_ERR_ARGUMENT,
+             "null pointer passed to gs_emit_tiles");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  ProfileScope prof(GS_PROF_BINNING, s);
+  emit_tiles_kernel<<<unsigned(ceil_div(count, 256)), 256, 0, s>>>(
+      count, tiles_x(width), tiles_y(height), geometry, radii, image_ids, offsets, keys, values);
+  GS_LAUNCHED("emit_tiles_kernel");
+  return GS_OK;
+}
+
+int gs_find_ranges(const uint64_t* sorted_keys, int64_t m, int32_t* ranges, int64_t tiles,
+                   void* stream) {
+  using namespace gs;
+  clear_error();
+  GS_REQUIRE(m >= 0 && m <= INT_MAX, GS_ERR_OVERFLOW, "tile intersection count exceeds int32");
+  GS_REQUIRE(tiles >= 0 && tiles <= INT_MAX, GS_ERR_OVERFLOW, "image tile count exceeds int32");
+  if (tiles == 0) return GS_OK;
+  GS_REQUIRE(ranges, GS_ERR_ARGUMENT, "null ranges");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  ProfileScope prof(GS_PROF_BINNING, s);
+  int2* r = reinterpret_cast<int2*>(ranges);
+  fill_ranges_kernel<<<unsigned(ceil_div(tiles, 256)), 256, 0, s>>>(tiles, r);
+  GS_LAUNCHED("fill_ranges_kernel");
+  if (m == 0) return GS_OK;
+  GS_REQUIRE(sorted_keys, GS_ERR_ARGUMENT, "null sorted keys");
+  find_ranges_kernel<<<unsigned(ceil_div(m, 256)), 256, 0, s>>>(m, tiles, sorted_keys, r);
+  GS_LAUNCHED("find_ranges_kernel");
+  return GS_OK;
+}
+
+}  // extern "C"

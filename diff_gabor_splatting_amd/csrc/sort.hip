@@ -1,0 +1,258 @@
+// Kernel 3: stable LSD radix sort of (uint64 key, int32 value) pairs.
+//
+// Each pass sorts on an 8-bit digit (Merrill & Grimshaw's reduce-then-scan
+// formulation, without decoupled look-back, so no workgroup ever waits on
+// another):
+//   1. upsweep  - every 4096-key span builds a digit histogram in LDS and
+//                 stores it digit-major: counts[digit * spans + span];
+//   2. scan     - one exclusive scan over those counts yields, for every
+//                 (digit, span), the first output slot;
+//   3. downsweep- every span ranks its keys stably (wave-level digit match
+//                 via ballots, per-wave running counters in LDS), stages the
+//                 locally sorted span in LDS and writes it out so that runs
+//                 of equal digits land on consecutive addresses.
+// Only bits [begin_bit, end_bit) are sorted; the rasterizer passes
+// end_bit = 32 + bits(image*tile count), since higher key bits are zero,
+// which leaves the result identical to a full 64-bit sort.
+#include "common.hpp"
+#include "scan.hpp"
+
+namespace gs {
+namespace {
+
+constexpr int kSortBlock = 256;
+constexpr int kSortWaves = kSortBlock / 64;
+constexpr int kSortItems = 16;                         // keys per thread
+constexpr int kSortSpan = kSortBlock * kSortItems;     // keys per workgroup
+constexpr int kWaveSpan = 64 * kSortItems;             // keys per wave
+constexpr int kDigitBits = 8;
+constexpr int kBins = 1 << kDigitBits;
+
+__global__ __launch_bounds__(kSortBlock) void radix_upsweep_kernel(
+    const uint64_t* __restrict__ keys, int64_t m, int shift, uint32_t mask,
+    uint32_t* __restrict__ counts, int64_t spans) {
+  __shared__ uint32_t hist[kSortWaves][kBins];
+  const int wave = threadIdx.x >> 6;
+  for (int i = threadIdx.x; i < kSortWaves * kBins; i += kSortBlock) (&hist[0][0])[i] = 0;
+  __syncthreads();
+  const int64_t base = int64_t(blockIdx.x) * kSortSpan;
+#pragma unroll 4
+  for (int r = 0; r < kSortItems; ++r) {
+    const int64_t i = base + int64_t(r) * kSortBlock + threadIdx.x;
+    if (i < m) atomicAdd(&hist[wave][uint32_t(keys[i] >> shift) & mask], 1u);
+  }
+  __syncthreads();
+  const int d = threadIdx.x;  // kSortBlock == kBins
+  uint32_t total = 0;
+#pragma unroll
+  for (int w = 0; w < kSortWaves; ++w) total += hist[w][d];
+  counts[int64_t(d) * spans + blockIdx.x] = total;
+}
+
+struct CountLoad {
+  const uint32_t* counts;
+  __device__ uint32_t operator()(int64_t i) const { return counts[i]; }
+};
+
+struct ExclusiveStore {
+  uint32_t* out;
+  __device__ void operator()(int64_t i, uint32_t inclusive, uint32_t v) const {
+    out[i] = inclusive - v;
+  }
+};
+
+__global__ __launch_bounds__(kSortBlock) void radix_downsweep_kernel(
+    const uint64_t* __restrict__ keys_in, const int* __restrict__ values_in,
+    uint64_t* __restrict__ keys_out, int* __restrict__ values_out, int64_t m, int shift,
+    int bits, const uint32_t* __restrict__ offsets, int64_t spans) {
+  __shared__ uint32_t running[kSortWaves][kBins];   // per-wave digit counters
+  __shared__ uint32_t local_start[kBins];           // first local slot per digit
+  __shared__ uint32_t global_start[kBins];          // first output slot per digit
+  __shared__ uint64_t stage_keys[kSortSpan];
+  __shared__ int stage_values[kSortSpan];
+  const int lane = __lane_id(), wave = threadIdx.x >> 6;
+  const uint32_t mask = (1u << bits) - 1u;
+  for (int i = threadIdx.x; i < kSortWaves * kBins; i += kSortBlock) (&running[0][0])[i] = 0;
+  __syncthreads();
+
+  const int64_t wave_base = int64_t(blockIdx.x) * kSortSpan + int64_t(wave) * kWaveSpan;
+  const uint64_t lanes_below = (uint64_t(1) << lane) - 1;
+  uint64_t key[kSortItems];
+  int value[kSortItems];
+  uint32_t rank[kSortItems];
+#pragma unroll
+  for (int it = 0; it < kSortItems; ++it) {
+    const int64_t i = wave_base + int64_t(it) * 64 + lane;
+    const bool valid = i < m;
+    key[it] = valid ? keys_in[i] : 0;
+    value[it] = valid ? values_in[i] : 0;
+    const uint32_t digit = uint32_t(key[it] >> shift) & mask;
+    // Lanes holding the same digit: intersect one ballot per digit bit.
+    uint64_t peers = __ballot(valid);
+    for (int b = 0; b < bits; ++b) {
+      const bool set = (digit >> b) & 1u;
+      const uint64_t vote = __ballot(set);
+      peers &= set ? vote : ~vote;
+    }
+    rank[it] = 0;
+    if (valid) {
+      const uint32_t before = running[wave][digit];
+      rank[it] = before + uint32_t(__popcll(peers & lanes_below));
+      if ((peers & lanes_below) == 0) running[wave][digit] = before + uint32_t(__popcll(peers));
+    }
+  }
+  __syncthreads();
+  // Per digit: exclusive offsets of each wave inside the span, and the
+  // span's first local / global slot.
+  {
+    const int d = threadIdx.x;
+    uint32_t run = 0;
+#pragma unroll
+    for (int w = 0; w < kSortWaves; ++w) {
+      const uint32_t c = running[w][d];
+      running[w][d] = run;
+      run += c;
+    }
+    local_start[d] = run;  // digit total; converted to a prefix below
+    global_start[d] = offsets[int64_t(d) * spans + blockIdx.x];
+  }
+  __syncthreads();
+  // Exclusive prefix of the 256 digit totals (one value per thread).
+  {
+    __shared__ uint32_t wave_totals[kSortWaves];
+    const uint32_t v = local_start[threadIdx.x];
+    const uint32_t incl = wave_inclusive_scan(v);
+    if (lane == 63) wave_totals[wave] = incl;
+    __syncthreads();
+    uint32_t before = 0;
+    for (int w = 0; w < wave; ++w) before += wave_totals[w];
+    __syncthreads();
+    local_start[threadIdx.x] = before + incl - v;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int it = 0; it < kSortItems; ++it) {
+    const int64_t i = wave_base + int64_t(it) * 64 + lane;
+    if (i < m) {
+      const uint32_t digit = uint32_t(key[it] >> shift) & mask;
+      const uint32_t slot = local_start[digit] + running[wave][digit] + rank[it];
+      if (slot < uint32_t(kSortSpan)) {  // always true when ranking is consistent
+        stage_keys[slot] = key[it];
+        stage_values[slot] = value[it];
+      }
+    }
+  }
+  __syncthreads();
+  const int64_t span_base = int64_t(blockIdx.x) * kSortSpan;
+  const int span_count = int(min<int64_t>(kSortSpan, m - span_base));
+  for (int slot = threadIdx.x; slot < span_count; slot += kSortBlock) {
+    const uint64_t k = stage_keys[slot];
+    const uint32_t digit = uint32_t(k >> shift) & mask;
+    const int64_t dst = int64_t(global_start[digit]) + (slot - int64_t(local_start[digit]));
+    if (dst >= 0 && dst < m) {  // always true when the histograms are consistent
+      keys_out[dst] = k;
+      values_out[dst] = stage_values[slot];
+    }
+  }
+}
+
+__global__ __launch_bounds__(256) void copy_pairs_kernel(const uint64_t* __restrict__ keys_in,
+                                                         const int* __restrict__ values_in,
+                                                         uint64_t* __restrict__ keys_out,
+                                                         int* __restrict__ values_out, int64_t m) {
+  const int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x;
+  if (i < m) {
+    keys_out[i] = keys_in[i];
+    values_out[i] = values_in[i];
+  }
+}
+
+struct SortWorkspace {
+  uint32_t* counts;       // kBins * spans
+  uint32_t* scan_sums;    // scan span totals
+  uint64_t* keys_tmp;     // m
+  int* values_tmp;        // m
+  size_t bytes;
+};
+
+SortWorkspace layout(void* base, int64_t m) {
+  const int64_t spans = ceil_div(m, kSortSpan);
+  const int64_t count_items = int64_t(kBins) * spans;
+  SortWorkspace w;
+  size_t offset = 0;
+  char* p = static_cast<char*>(base);
+  w.counts = reinterpret_cast<uint32_t*>(p + offset);
+  offset = align_up(offset + size_t(count_items) * 4, 256);
+  w.scan_sums = reinterpret_cast<uint32_t*>(p + offset);
+  offset = align_up(offset + scan_workspace_bytes(count_items, 4), 256);
+  w.keys_tmp = reinterpret_cast<uint64_t*>(p + offset);
+  offset = align_up(offset + size_t(m) * 8, 256);
+  w.values_tmp = reinterpret_cast<int*>(p + offset);
+  offset = align_up(offset + size_t(m) * 4, 256);
+  w.bytes = offset;
+  return w;
+}
+
+}  // namespace
+}  // namespace gs
+
+extern "C" {
+
+size_t gs_sort_workspace_size(int64_t m) {
+  if (m < 0) m = 0;
+  return gs::layout(nullptr, m).bytes + 256;
+}
+
+int gs_sort_pairs(const uint64_t* keys_in, uint64_t* keys_out, const int32_t* values_in,
+                  int32_t* values_out, int64_t m, int32_t begin_bit, int32_t end_bit,
+                  void* workspace, size_t workspace_bytes, void* stream) {
+  using namespace gs;
+  clear_error();
+  GS_REQUIRE(m >= 0 && m <= 0x7fffffffLL, GS_ERR_OVERFLOW, "sort size exceeds int32");
+  GS_REQUIRE(0 <= begin_bit && begin_bit <= end_bit && end_bit <= 64, GS_ERR_ARGUMENT,
+             "invalid bit range [%d, %d)", begin_bit, end_bit);
+  if (m == 0) return GS_OK;
+  GS_REQUIRE(keys_in && keys_out && values_in && values_out, GS_ERR_ARGUMENT,
+             "null pointer passed to gs_sort_pairs");
+  GS_REQUIRE(keys_in != keys_out && values_in != values_out, GS_ERR_ARGUMENT,
+             "sort outputs must not alias inputs");
+  const size_t need = gs_sort_workspace_size(m);
+  GS_REQUIRE(workspace && workspace_bytes >= need, GS_ERR_WORKSPACE,
+             "sort needs %zu workspace bytes, got %zu", need, workspace_bytes);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  ProfileScope prof(GS_PROF_SORT, s);
+  SortWorkspace w = layout(workspace, m);
+  const int64_t spans = ceil_div(m, kSortSpan);
+  const int passes = int(ceil_div(end_bit - begin_bit, kDigitBits));
+  if (passes == 0) {
+    copy_pairs_kernel<<<unsigned(ceil_div(m, 256)), 256, 0, s>>>(keys_in, values_in, keys_out,
+                                                                  values_out, m);
+    GS_LAUNCHED("copy_pairs_kernel");
+    return GS_OK;
+  }
+  // Ping-pong so that the last pass writes the caller's output.
+  const uint64_t* src_k = keys_in;
+  const int* src_v = values_in;
+  for (int pass = 0; pass < passes; ++pass) {
+    const int shift = begin_bit + pass * kDigitBits;
+    const int bits = min(kDigitBits, end_bit - shift);
+    const bool to_output = ((passes - 1 - pass) % 2) == 0;
+    uint64_t* dst_k = to_output ? keys_out : w.keys_tmp;
+    int* dst_v = to_output ? values_out : w.values_tmp;
+    radix_upsweep_kernel<<<unsigned(spans), kSortBlock, 0, s>>>(src_k, m, shift,
+                                                                 (1u << bits) - 1u, w.counts,
+                                                                 spans);
+    GS_LAUNCHED("radix_upsweep_kernel");
+    int status = run_scan<uint32_t>(int64_t(kBins) * spans, CountLoad{w.counts},
+                                    ExclusiveStore{w.counts}, w.scan_sums, s);
+    if (status != GS_OK) return status;
+    radix_downsweep_kernel<<<unsigned(spans), kSortBlock, 0, s>>>(
+        src_k, src_v, dst_k, dst_v, m, shift, bits, w.counts, spans);
+    GS_LAUNCHED("radix_downsweep_kernel");
+    src_k = dst_k;
+    src_v = dst_v;
+  }
+  return GS_OK;
+}
+
+}  // extern "C"

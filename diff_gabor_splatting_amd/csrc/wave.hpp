@@ -1,0 +1,120 @@
+// Wave64 cross-lane primitives for gfx950.
+//
+// wave_reduce_scatter<N> sums an N-value per-lane vector over the 64 lanes
+// of a wavefront by recursive halving: at each of the six lane bits the
+// vector is split in two halves, lanes with the bit clear keep the lower
+// half and lanes with the bit set keep the upper half, and each lane adds
+// its partner's copy of the half it keeps. After six steps lane L holds the
+// complete wave sum of parameter rs_param<N>(L) (values >= N are padding).
+// That costs about 2N cross-lane moves + adds instead of 6N for N separate
+// butterfly reductions, and the final sums sit one per lane, so a single
+// vector atomic (LDS or global) publishes all N of them.
+//
+// Bits 5 and 4 use the gfx950 v_permlane32_swap / v_permlane16_swap
+// instructions (one instruction exchanges two halves); bits 3..0 use DPP
+// row_mirror, row_half_mirror and quad permutations, each of which pairs
+// every lane with bit B clear with a lane that has bit B set inside the
+// same group, which is all the reduction needs.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+namespace gs {
+
+__device__ __forceinline__ int lane_id() { return __lane_id(); }
+
+// DPP control codes (GFX9 encoding).
+constexpr int kDppRowMirror = 0x140;
+constexpr int kDppRowHalfMirror = 0x141;
+constexpr int kDppQuadXor2 = 0x4E;  // quad_perm [2,3,0,1]
+constexpr int kDppQuadXor1 = 0xB1;  // quad_perm [1,0,3,2]
+
+template <int Ctrl>
+__device__ __forceinline__ float dpp_move(float v) {
+  return __builtin_amdgcn_update_dpp(0.0f, v, Ctrl, 0xf, 0xf, false);
+}
+
+// Combine halves `lo` and `hi` across the lane pair split by bit B:
+// lanes with bit B clear return lo + partner's lo, the others hi + partner's hi.
+template <int B>
+__device__ __forceinline__ float exchange_add(float lo, float hi, int lane) {
+  if constexpr (B == 5) {
+    auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(lo), __float_as_uint(hi), false,
+                                              false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  } else if constexpr (B == 4) {
+    auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(lo), __float_as_uint(hi), false,
+                                              false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  } else {
+    const bool upper = (lane >> B) & 1;
+    const float send = upper ? lo : hi;
+    const float keep = upper ? hi : lo;
+    constexpr int ctrl = B == 3 ? kDppRowMirror
+                         : B == 2 ? kDppRowHalfMirror
+                         : B == 1 ? kDppQuadXor2
+                                  : kDppQuadXor1;
+    return keep + dpp_move<ctrl>(send);
+  }
+}
+
+template <int B, int N>
+__device__ __forceinline__ void rs_step(const float* in, float* out, int lane) {
+  constexpr int H = (N + 1) / 2;
+#pragma unroll
+  for (int i = 0; i < H; ++i) {
+    const float lo = in[i];
+    const float hi = (i + H < N) ? in[i + H] : 0.0f;
+    out[i] = exchange_add<B>(lo, hi, lane);
+  }
+}
+
+// Half sizes at each step for an N-value reduction.
+template <int N>
+struct RsShape {
+  static constexpr int h5 = (N + 1) / 2;
+  static constexpr int h4 = (h5 + 1) / 2;
+  static constexpr int h3 = (h4 + 1) / 2;
+  static constexpr int h2 = (h3 + 1) / 2;
+  static constexpr int h1 = (h2 + 1) / 2;
+  static constexpr int h0 = (h1 + 1) / 2;
+};
+
+// Parameter index whose total lane `lane` holds after wave_reduce_scatter<N>.
+template <int N>
+__device__ __forceinline__ int rs_param(int lane) {
+  using S = RsShape<N>;
+  return ((lane >> 5) & 1) * S::h5 + ((lane >> 4) & 1) * S::h4 + ((lane >> 3) & 1) * S::h3 +
+         ((lane >> 2) & 1) * S::h2 + ((lane >> 1) & 1) * S::h1 + (lane & 1) * S::h0;
+}
+
+// All 64 lanes must be active. Returns this lane's total (see rs_param).
+template <int N>
+__device__ __forceinline__ float wave_reduce_scatter(const float (&v)[N], int lane) {
+  static_assert(N >= 1 && N <= 64, "one reduce-scatter covers at most 64 values");
+  using S = RsShape<N>;
+  float a[S::h5], b[S::h4], c[S::h3], d[S::h2], e[S::h1], f[S::h0];
+  rs_step<5, N>(v, a, lane);
+  rs_step<4, S::h5>(a, b, lane);
+  rs_step<3, S::h4>(b, c, lane);
+  rs_step<2, S::h3>(c, d, lane);
+  rs_step<1, S::h2>(d, e, lane);
+  rs_step<0, S::h1>(e, f, lane);
+  return f[0];
+}
+
+// Full-wave integer maximum (all lanes receive the result).
+__device__ __forceinline__ int wave_max(int v) {
+#pragma unroll
+  for (int offset = 32; offset > 0; offset >>= 1) v = max(v, __shfl_xor(v, offset, 64));
+  return v;
+}
+
+// Full-wave float sum (all lanes receive the result).
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int offset = 32; offset > 0; offset >>= 1) v += __shfl_xor(v, offset, 64);
+  return v;
+}
+
+}  // namespace gs

@@ -1,0 +1,427 @@
+"""Public surface renderers and explicit tensor contracts (MI355X HIP backend).
+
+Drop-in counterpart of the reference's ``src/gabor_splatting/rendering.py``:
+the same public functions, keyword options and defaults, error types and
+messages, ``[..., C, H, W, ch]`` outputs and ``meta`` dict. Projection, SH,
+packing, binning, sorting and both compositors run as hand-written gfx950
+HIP kernels (``libgabor_hip.so``, bound in ``_native``); PyTorch only
+allocates memory, provides the stream and joins the autograd graph.
+"""
+
+from __future__ import annotations
+
+import math
+from typing import Any
+
+import torch
+from torch.autograd.function import once_differentiable
+
+from . import _native
+
+
+class Composite(torch.autograd.Function):
+    """Tile compositor with first-order reverse mode (rendering.py:14-71)."""
+
+    @staticmethod
+    def forward(
+        ctx: Any, geometry, appearance, opacities, primitive_ids, image_ids, radii,
+        backgrounds, width, height, neural, near_plane, far_plane,
+    ):
+        maps, points, ranges, state, contributors = _native.rasterize_forward(
+            geometry, appearance, opacities, primitive_ids, image_ids, radii, backgrounds,
+            width, height, neural, near_plane, far_plane,
+        )
+        # Binning and early termination are discrete: only the saved sorted
+        # lists and per-pixel state are needed to replay the tiles backwards.
+        ctx.save_for_backward(
+            geometry, appearance, opacities, primitive_ids, backgrounds, points, ranges, state,
+            contributors,
+        )
+        ctx.options = (width, height, neural, near_plane, far_plane)
+        return maps
+
+    @staticmethod
+    @once_differentiable
+    def backward(ctx: Any, grad_maps):
+        gg, ga, go, gb = _native.rasterize_backward(
+            *ctx.saved_tensors, grad_maps.contiguous(), *ctx.options
+        )
+        return gg, ga, go, None, None, None, gb, None, None, None, None, None
+
+
+class ProjectSurfaces(torch.autograd.Function):
+    """HIP projection of every (scene, camera, surfel) pair and its adjoint.
+
+    Replaces the PyTorch ops of project_surfaces (rendering.py:176-218) and
+    the autograd graph PyTorch builds through them.
+    """
+
+    @staticmethod
+    def forward(ctx: Any, means, quaternions, scales, view_matrices, intrinsics, width,
+                height, near_plane, far_plane):
+        transform, xy, normals, directions, radii = _native.project_forward(
+            means, quaternions, scales, view_matrices, intrinsics, width, height, near_plane,
+            far_plane,
+        )
+        ctx.save_for_backward(means, quaternions, scales, view_matrices, intrinsics)
+        ctx.mark_non_differentiable(radii)
+        ctx.set_materialize_grads(False)
+        return transform, xy, normals, directions, radii
+
+    @staticmethod
+    @once_differentiable
+    def backward(ctx: Any, g_transform, g_xy, g_normals, g_directions, _g_radii):
+        if all(g is None for g in (g_transform, g_xy, g_normals, g_directions)):
+            return (None,) * 9
+        grads = _native.project_backward(
+            *ctx.saved_tensors, g_transform, g_xy, g_normals, g_directions
+        )
+        return (*grads, None, None, None, None)
+
+
+class SHColors(torch.autograd.Function):
+    """Both classic SH colours from one direction per pair (rendering.py:221-238)."""
+
+    @staticmethod
+    def forward(ctx: Any, first, second, directions, degree):
+        ctx.save_for_backward(first, second, directions)
+        ctx.degree = degree
+        return _native.evaluate_sh_forward(first, second, directions, degree)
+
+    @staticmethod
+    @once_differentiable
+    def backward(ctx: Any, grad_colors):
+        gradients = _native.evaluate_sh_backward(
+            *ctx.saved_tensors, grad_colors.contiguous(), ctx.degree
+        )
+        return *gradients, None
+
+
+def check_tensor(
+    name: str, value: torch.Tensor, shape: tuple[int, ...], device: torch.device
+) -> None:
+    """Require a contiguous float32 GPU tensor of an exact shape on `device`."""
+    if not isinstance(value, torch.Tensor):
+        raise TypeError(f"{name} must be a torch.Tensor")
+    if not (value.is_cuda and value.dtype == torch.float32 and value.device == device):
+        raise ValueError(f"{name} must be float32 on {device}")
+    if value.shape != shape:
+        raise ValueError(f"{name} must have shape {shape}, got {tuple(value.shape)}")
+    if not value.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+
+
+def _all_close(value: torch.Tensor, target, **tolerances) -> torch.Tensor:
+    return torch.isclose(value, value.new_tensor(target), **tolerances).all()
+
+
+@torch.no_grad()
+def check_values(
+    tensors, quaternions, scales, opacities, view_matrices, intrinsics, appearance, neural
+):
+    """Numerical contracts, evaluated on the device and read back once.
+
+    Raises ValueError naming every violated contract (rendering.py:88-153).
+    """
+    unit = {"atol": 1e-4, "rtol": 1e-4}
+    checks: list[tuple[str, torch.Tensor]] = []
+    for name, (value, _) in tensors.items():
+        checks.append((f"{name} must contain only finite values", torch.isfinite(value).all()))
+    checks.append(("scales must be strictly positive", (scales > 0).all()))
+    checks.append(
+        ("opacities must lie in [0, 1]", ((opacities >= 0) & (opacities <= 1)).all())
+    )
+    checks.append(
+        (
+            "quaternions must be unit wxyz vectors",
+            _all_close(quaternions.square().sum(-1), 1.0, **unit),
+        )
+    )
+    checks.append(
+        (
+            "view_matrices must have last row [0, 0, 0, 1]",
+            _all_close(view_matrices[..., 3, :], [0.0, 0.0, 0.0, 1.0]),
+        )
+    )
+    checks.append(
+        (
+            "intrinsics must have last row [0, 0, 1]",
+            _all_close(intrinsics[..., 2, :], [0.0, 0.0, 1.0]),
+        )
+    )
+    checks.append(
+        (
+            "intrinsics fx and fy must be positive",
+            ((intrinsics[..., 0, 0] > 0) & (intrinsics[..., 1, 1] > 0)).all(),
+        )
+    )
+    rotation = view_matrices[..., :3, :3]
+    identity = torch.eye(3, device=rotation.device, dtype=rotation.dtype)
+    checks.append(
+        (
+            "view_matrices rotations must be orthonormal",
+            torch.isclose(rotation.transpose(-1, -2) @ rotation, identity, **unit).all(),
+        )
+    )
+    checks.append(
+        (
+            "view_matrices rotations must have determinant +1",
+            _all_close(torch.linalg.det(rotation), 1.0, **unit),
+        )
+    )
+    if not neural:
+        weights, magnitudes = appearance[2], appearance[3]
+        checks.append(("frequency_weights must be nonnegative", (weights >= 0).all()))
+        checks.append(("frequency_magnitudes must be nonnegative", (magnitudes >= 0).all()))
+        checks.append(
+            ("frequency_weights must sum to one", _all_close(weights.sum(-1), 1.0, **unit))
+        )
+    passed = torch.stack([ok for _, ok in checks]).tolist()
+    if not all(passed):
+        raise ValueError("; ".join(message for (message, _), ok in zip(checks, passed) if not ok))
+
+
+def quaternion_matrix(q: torch.Tensor) -> torch.Tensor:
+    """Normalised wxyz quaternions to rotation matrices (rendering.py:156-173)."""
+    q = q / torch.linalg.vector_norm(q, dim=-1, keepdim=True)
+    w, x, y, z = q.unbind(-1)
+    rows = (
+        (1 - 2 * (y * y + z * z), 2 * (x * y - w * z), 2 * (x * z + w * y)),
+        (2 * (x * y + w * z), 1 - 2 * (x * x + z * z), 2 * (y * z - w * x)),
+        (2 * (x * z - w * y), 2 * (y * z + w * x), 1 - 2 * (x * x + y * y)),
+    )
+    return torch.stack([torch.stack(row, -1) for row in rows], -2)
+
+
+def project_surfaces(
+    means, quaternions, scales, view_matrices, intrinsics, width, height, near_plane, far_plane
+):
+    """Projected planes T, conic centres, facing normals, world directions and radii."""
+    return ProjectSurfaces.apply(
+        means, quaternions, scales, view_matrices, intrinsics, width, height, near_plane,
+        far_plane,
+    )
+
+
+_NEURAL_FIELDS = (
+    ("input_weights", (6, 5)),
+    ("input_biases", (6,)),
+    ("output_weights", (3, 6)),
+    ("output_biases", (3,)),
+)
+
+
+def render(
+    means, quaternions, scales, opacities, appearance, view_matrices, intrinsics, width,
+    height, backgrounds, packed, near_plane, far_plane, neural, sh_degree, validate,
+):
+    """Validate, project every (scene, camera) pair, and composite in one launch."""
+    if not isinstance(means, torch.Tensor) or means.ndim < 2 or means.shape[-1] != 3:
+        raise ValueError("means must have shape [..., N, 3]")
+    if not means.is_cuda or means.dtype != torch.float32:
+        raise ValueError("means must be a CUDA float32 tensor")
+    sizes_ok = type(width) is int and type(height) is int
+    if not (sizes_ok and 0 < width < 2**30 and 0 < height < 2**30):
+        raise ValueError("width and height must be positive integers smaller than 2**30")
+    planes_ok = math.isfinite(near_plane) and math.isfinite(far_plane)
+    if not (planes_ok and 0 < near_plane < far_plane):
+        raise ValueError("clipping planes must be finite and satisfy 0 < near_plane < far_plane")
+    if type(packed) is not bool:
+        raise TypeError("packed must be bool")
+    batch = tuple(means.shape[:-2])
+    n = means.shape[-2]
+    if not isinstance(view_matrices, torch.Tensor) or view_matrices.ndim != len(batch) + 3:
+        raise ValueError("view_matrices must have shape [..., C, 4, 4]")
+    cameras = view_matrices.shape[-3]
+    scenes = math.prod(batch)
+    if scenes < 1 or cameras < 1:
+        raise ValueError("scene and camera dimensions must be nonempty")
+    device = means.device
+    if backgrounds is None:
+        backgrounds = means.new_zeros(batch + (cameras, 3))
+    tensors = {
+        "means": (means, batch + (n, 3)),
+        "quaternions": (quaternions, batch + (n, 4)),
+        "scales": (scales, batch + (n, 2)),
+        "opacities": (opacities, batch + (n,)),
+        "view_matrices": (view_matrices, batch + (cameras, 4, 4)),
+        "intrinsics": (intrinsics, batch + (cameras, 3, 3)),
+        "backgrounds": (backgrounds, batch + (cameras, 3)),
+    }
+    if neural:
+        fields = _NEURAL_FIELDS
+    else:
+        if sh_degree is not None and (type(sh_degree) is not int or not 0 <= sh_degree <= 3):
+            raise ValueError("sh_degree must be None or an integer from 0 to 3")
+        color = (3,) if sh_degree is None else ((sh_degree + 1) ** 2, 3)
+        fields = (
+            ("colors", color),
+            ("secondary_colors", color),
+            ("frequency_weights", (4,)),
+            ("frequency_magnitudes", (4,)),
+            ("phases", (4,)),
+        )
+    for (name, shape), value in zip(fields, appearance):
+        tensors[name] = (value, batch + (n,) + shape)
+    for name, (value, shape) in tensors.items():
+        check_tensor(name, value, shape, device)
+    if type(validate) is not bool:
+        raise TypeError("validate must be bool")
+    if validate:
+        check_values(
+            tensors, quaternions, scales, opacities, view_matrices, intrinsics, appearance, neural
+        )
+
+    transform, xy, normals, directions, radii = project_surfaces(
+        means.reshape(scenes, n, 3),
+        quaternions.reshape(scenes, n, 4),
+        scales.reshape(scenes, n, 2),
+        view_matrices.reshape(scenes, cameras, 4, 4),
+        intrinsics.reshape(scenes, cameras, 3, 3),
+        width,
+        height,
+        near_plane,
+        far_plane,
+    )
+    pairs = scenes * cameras * n
+    if sh_degree is not None:
+        # Camera-specific SH colours, so appearance rows are per pair.
+        k = (sh_degree + 1) ** 2
+        colors = SHColors.apply(
+            appearance[0].reshape(scenes, n, k, 3),
+            appearance[1].reshape(scenes, n, k, 3),
+            directions,
+            sh_degree,
+        )
+        shared = [t.reshape(scenes, 1, n, 4).expand(scenes, cameras, n, 4) for t in appearance[2:]]
+        parameters = torch.cat((colors, *shared), dim=-1).reshape(pairs, 18).contiguous()
+        opacity_rows = opacities.reshape(scenes, 1, n).expand(scenes, cameras, n)
+        opacity_rows = opacity_rows.reshape(pairs).contiguous()
+        primitive_ids = torch.arange(pairs, device=device)
+    else:
+        # One appearance row per surfel, shared by every camera of its scene.
+        width_of_row = 57 if neural else 18
+        flat = [t.reshape(scenes, n, math.prod(shape)) for t, (_, shape) in zip(appearance, fields)]
+        parameters = torch.cat(flat, dim=-1).reshape(scenes * n, width_of_row).contiguous()
+        opacity_rows = opacities.reshape(scenes * n)
+        primitive_ids = torch.arange(scenes * n, device=device).reshape(scenes, 1, n)
+        primitive_ids = primitive_ids.expand(scenes, cameras, n).reshape(pairs).contiguous()
+    image_ids = torch.arange(scenes * cameras, device=device).reshape(scenes, cameras, 1)
+    image_ids = image_ids.expand(scenes, cameras, n).reshape(pairs).contiguous()
+    flat_radii = radii.reshape(pairs)
+    if packed:
+        selected = _native.pack_visible(flat_radii)
+    else:
+        selected = torch.arange(pairs, device=device)
+    projected_means = xy.reshape(pairs, 2)[selected]
+    geometry = torch.cat(
+        (
+            transform.reshape(pairs, 9)[selected],
+            projected_means,
+            normals.reshape(pairs, 3)[selected],
+            directions.reshape(pairs, 3)[selected],
+        ),
+        dim=-1,
+    ).contiguous()
+    maps = Composite.apply(
+        geometry,
+        parameters,
+        opacity_rows,
+        primitive_ids[selected],
+        image_ids[selected],
+        flat_radii[selected].contiguous(),
+        backgrounds.reshape(scenes * cameras, 3),
+        width,
+        height,
+        neural,
+        near_plane,
+        far_plane,
+    ).reshape(batch + (cameras, height, width, 9))
+    stride = max(n, 1)
+    meta = {
+        "radii": flat_radii[selected] if packed else radii.reshape(batch + (cameras, n)),
+        "projected_means": projected_means,
+        "scene_ids": selected // (cameras * stride),
+        "camera_ids": selected // stride % cameras,
+        "primitive_ids": selected % stride,
+        "packed": packed,
+        "accumulated_depth": maps[..., 4:5],
+        "normals": maps[..., 5:8],
+        "distortion": maps[..., 8:9],
+    }
+    return maps[..., :3], maps[..., 3:4], meta
+
+
+def rasterize_gabors(
+    means: torch.Tensor,
+    quaternions: torch.Tensor,
+    scales: torch.Tensor,
+    opacities: torch.Tensor,
+    colors: torch.Tensor,
+    secondary_colors: torch.Tensor,
+    frequency_weights: torch.Tensor,
+    frequency_magnitudes: torch.Tensor,
+    phases: torch.Tensor,
+    view_matrices: torch.Tensor,
+    intrinsics: torch.Tensor,
+    width: int,
+    height: int,
+    *,
+    backgrounds: torch.Tensor | None = None,
+    packed: bool = False,
+    near_plane: float = 0.2,
+    far_plane: float = 100.0,
+    sh_degree: int | None = None,
+    validate: bool = True,
+) -> tuple[torch.Tensor, torch.Tensor, dict[str, Any]]:
+    """Render four-frequency Gabor surfaces over scene and camera batches.
+
+    Geometry: means [..., N, 3], unit wxyz quaternions [..., N, 4], positive
+    tangent scales [..., N, 2], activated opacities [..., N]. Colours are
+    [..., N, 3] or, with ``sh_degree``, SH coefficients [..., N, (d+1)**2, 3].
+    Frequency weights (nonnegative, summing to one), magnitudes (cycles per
+    scaled local unit) and phases (radians) are [..., N, 4]. Cameras are
+    rigid world-to-camera [..., C, 4, 4] and pinhole [..., C, 3, 3]. All
+    tensors are contiguous float32 on one GPU. Returns RGB [..., C, H, W, 3],
+    alpha [..., C, H, W, 1] and metadata (rendering.py:403-456).
+    """
+    return render(
+        means, quaternions, scales, opacities,
+        (colors, secondary_colors, frequency_weights, frequency_magnitudes, phases),
+        view_matrices, intrinsics, width, height, backgrounds, packed, near_plane, far_plane,
+        False, sh_degree, validate,
+    )
+
+
+def rasterize_neural_gabors(
+    means: torch.Tensor,
+    quaternions: torch.Tensor,
+    scales: torch.Tensor,
+    opacities: torch.Tensor,
+    input_weights: torch.Tensor,
+    input_biases: torch.Tensor,
+    output_weights: torch.Tensor,
+    output_biases: torch.Tensor,
+    view_matrices: torch.Tensor,
+    intrinsics: torch.Tensor,
+    width: int,
+    height: int,
+    *,
+    backgrounds: torch.Tensor | None = None,
+    packed: bool = False,
+    near_plane: float = 0.2,
+    far_plane: float = 100.0,
+    validate: bool = True,
+) -> tuple[torch.Tensor, torch.Tensor, dict[str, Any]]:
+    """Render per-surfel 5->6->3 SIRENs (sine frequency 30, sigmoid RGB).
+
+    Input weights/biases are [..., N, 6, 5] / [..., N, 6]; output weights/
+    biases [..., N, 3, 6] / [..., N, 3]. The network input is (u/3, v/3)
+    followed by the world direction camera -> centre (rendering.py:459-507).
+    """
+    return render(
+        means, quaternions, scales, opacities,
+        (input_weights, input_biases, output_weights, output_biases),
+        view_matrices, intrinsics, width, height, backgrounds, packed, near_plane, far_plane,
+        True, None, validate,
+    )

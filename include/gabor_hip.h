@@ -1,0 +1,194 @@
+/*
+ * gabor_hip.h - C ABI of the MI355X (gfx950) Gabor-surface tile rasterizer.
+ *
+ * Every entry point takes plain device pointers, element counts and a HIP
+ * stream (passed as void*, a hipStream_t), launches its kernels on that
+ * stream and returns a status code. Nothing here allocates device memory:
+ * buffers whose size depends on data (tile intersections, sort scratch) are
+ * sized by the *_workspace_size queries and owned by the caller. No function
+ * throws across the ABI; on failure gs_last_error() names the problem.
+ *
+ * Tensor layouts (all row-major, contiguous, float32 unless stated):
+ *   means [S,N,3]  quaternions [S,N,4] (wxyz)  scales [S,N,2]
+ *   view_matrices [S,C,4,4] (world->camera)  intrinsics [S,C,3,3]
+ *   geometry [Q,17] = T(3x3 row-major) | xy(2) | normal(3) | direction(3)
+ *   appearance [P,18] classic: color(3) color2(3) weights(4) magnitudes(4) phases(4)
+ *   appearance [P,57] neural: W1(6x5) b1(6) W2(3x6) b2(3)
+ *   maps [I,H,W,9] = rgb(3) alpha depth normal(3) distortion
+ *   state [I,H,W,3] = final transmittance, m1, m2;  contributors [I,H,W] int32
+ *   keys uint64: (image*tw*th + tile_y*tw + tile_x) << 32 | float bits of depth
+ *   ranges [I*tw*th, 2] int32 = [first, last) into the sorted list
+ *
+ * Reference interfaces replaced (paths relative to the reference checkout):
+ *   gabor_splatting._C pybind11 module, src/gabor_splatting/csrc/bindings.cpp:5-10,
+ *   declared in src/gabor_splatting/csrc/rasterize.h:6-21, and the PyTorch
+ *   projection in src/gabor_splatting/rendering.py:156-218.
+ */
+#ifndef GABOR_HIP_H
+#define GABOR_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Status codes returned by every entry point. */
+#define GS_OK 0
+#define GS_ERR_ARGUMENT 1 /* invalid size, pointer or option */
+#define GS_ERR_OVERFLOW 2 /* an int32 index space would overflow */
+#define GS_ERR_HIP 3      /* a HIP runtime call or launch failed */
+#define GS_ERR_WORKSPACE 4 /* caller workspace smaller than required */
+
+/* Message of the last failure on the calling thread ("" if none). */
+const char* gs_last_error(void);
+
+/* ABI version, bumped on any signature change. */
+int gs_abi_version(void);
+
+/* ------------------------------------------------------------------ */
+/* Kernel 1: projection (replaces rendering.py:156-218 project_surfaces,
+ * which the reference runs as PyTorch ops) and its adjoint (the reference
+ * relies on PyTorch autograd through those ops).                      */
+
+/* Project every (scene, camera, surfel) pair: T = K [Rc tu*su, Rc tv*sv,
+ * Rc mu + t], conic centre xy, facing camera-space normal, unit world
+ * direction camera->centre and the integer screen radius (0 = culled).
+ * Outputs are [S,C,N,*]: transform 9, xy 2, normals 3, directions 3,
+ * radii int32. */
+int gs_project_forward(const float* means, const float* quaternions, const float* scales,
+                       const float* view_matrices, const float* intrinsics, int64_t scenes,
+                       int64_t cameras, int64_t n, int32_t width, int32_t height,
+                       float near_plane, float far_plane, float* transform, float* xy,
+                       float* normals, float* directions, int32_t* radii, void* stream);
+
+/* Scratch bytes needed by gs_project_backward (per-block camera partials). */
+size_t gs_project_backward_workspace_size(int64_t scenes, int64_t cameras, int64_t n);
+
+/* Adjoint of gs_project_forward. Any of grad_transform / grad_xy /
+ * grad_normals / grad_directions may be NULL (treated as zero). Outputs are
+ * overwritten (not accumulated): grad_means [S,N,3], grad_quaternions
+ * [S,N,4], grad_scales [S,N,2], grad_view_matrices [S,C,4,4] (last row 0),
+ * grad_intrinsics [S,C,3,3]. Per-camera sums use a deterministic two-stage
+ * reduction through the workspace. */
+int gs_project_backward(const float* means, const float* quaternions, const float* scales,
+                        const float* view_matrices, const float* intrinsics, int64_t scenes,
+                        int64_t cameras, int64_t n, const float* grad_transform,
+                        const float* grad_xy, const float* grad_normals,
+                        const float* grad_directions, float* grad_means,
+                        float* grad_quaternions, float* grad_scales,
+                        float* grad_view_matrices, float* grad_intrinsics, void* workspace,
+                        size_t workspace_bytes, void* stream);
+
+/* Replaces _C.evaluate_sh_forward (spherical_harmonics.cu:107-126):
+ * colors [S,C,N,6] = max(0.5 + sum_k Y_k(dir) coef[k], 0) for both colour
+ * sets first/second [S,N,K,3], K = (degree+1)^2, directions [S,C,N,3]. */
+int gs_sh_forward(const float* first, const float* second, const float* directions,
+                  float* colors, int64_t scenes, int64_t cameras, int64_t n, int32_t degree,
+                  void* stream);
+
+/* Replaces _C.evaluate_sh_backward (spherical_harmonics.cu:129-150).
+ * grad_first/grad_second [S,N,K,3] are overwritten with the sum over
+ * cameras (no atomics); grad_directions [S,C,N,3] is overwritten. */
+int gs_sh_backward(const float* first, const float* second, const float* directions,
+                   const float* grad_colors, float* grad_first, float* grad_second,
+                   float* grad_directions, int64_t scenes, int64_t cameras, int64_t n,
+                   int32_t degree, void* stream);
+
+/* ------------------------------------------------------------------ */
+/* Kernel 2: visible-pair packing and tile binning.                    */
+
+/* Scratch bytes for gs_pack_visible / gs_count_tiles over `count` items. */
+size_t gs_scan_workspace_size(int64_t count);
+
+/* Packed mode (rendering.py:362-364, `arange(Q)[radii > 0]`): writes the
+ * ascending indices of pairs with radii > 0 to selected[0..V) and V to
+ * *num_selected (a device int64). selected must hold `count` entries. */
+int gs_pack_visible(const int32_t* radii, int64_t count, int64_t* selected,
+                    int64_t* num_selected, void* workspace, size_t workspace_bytes,
+                    void* stream);
+
+/* countTiles + cub::DeviceScan::InclusiveSum (rasterize.cu:33-40, 459-464):
+ * offsets[i] = inclusive prefix sum of each pair's tile-rectangle area
+ * (0 when radii[i] <= 0). offsets [count] int64. */
+int gs_count_tiles(const float* geometry, const int32_t* radii, int64_t count, int32_t width,
+                   int32_t height, int64_t* offsets, void* workspace, size_t workspace_bytes,
+                   void* stream);
+
+/* emitTiles (rasterize.cu:43-56): for each visible pair, one key/value per
+ * covered tile in row-major tile order, starting at offsets[i-1].
+ * keys/values hold offsets[count-1] entries. */
+int gs_emit_tiles(const float* geometry, const int32_t* radii, const int64_t* image_ids,
+                  const int64_t* offsets, int64_t count, int32_t width, int32_t height,
+                  uint64_t* keys, int32_t* values, void* stream);
+
+/* ------------------------------------------------------------------ */
+/* Kernel 3: LSD radix sort and tile ranges.                           */
+
+/* Scratch bytes for gs_sort_pairs over m pairs. */
+size_t gs_sort_workspace_size(int64_t m);
+
+/* Stable ascending sort of (key, value) pairs on key bits [begin_bit,
+ * end_bit) (cub::DeviceRadixSort::SortPairs, rasterize.cu:478-487). Inputs
+ * are not modified; outputs must not alias inputs. */
+int gs_sort_pairs(const uint64_t* keys_in, uint64_t* keys_out, const int32_t* values_in,
+                  int32_t* values_out, int64_t m, int32_t begin_bit, int32_t end_bit,
+                  void* workspace, size_t workspace_bytes, void* stream);
+
+/* findRanges (rasterize.cu:59-69): ranges [tiles,2] = [first,last) of each
+ * tile's run in sorted_keys; tiles with no entries get (0,0). */
+int gs_find_ranges(const uint64_t* sorted_keys, int64_t m, int32_t* ranges, int64_t tiles,
+                   void* stream);
+
+/* ------------------------------------------------------------------ */
+/* Kernels 4 and 5: tile compositors (renderForward / renderBackward,
+ * rasterize.cu:230-399). neural = 0 selects the four-frequency Gabor
+ * appearance (18 floats per row), 1 the per-surfel SIREN (57 floats).     */
+
+int gs_render_forward(int32_t neural, const float* geometry, const float* appearance,
+                      const float* opacities, const int64_t* primitive_ids,
+                      const float* backgrounds, const int32_t* point_list,
+                      const int32_t* ranges, int64_t images, int32_t width, int32_t height,
+                      float near_plane, float far_plane, float* maps, float* state,
+                      int32_t* contributors, void* stream);
+
+/* Gradients are ACCUMULATED (global float atomics) into grad_geometry
+ * [Q,17], grad_appearance [P,A], grad_opacities [P], grad_backgrounds
+ * [I,3]; the caller zero-initialises them. */
+int gs_render_backward(int32_t neural, const float* geometry, const float* appearance,
+                       const float* opacities, const int64_t* primitive_ids,
+                       const float* backgrounds, const int32_t* point_list,
+                       const int32_t* ranges, const float* state,
+                       const int32_t* contributors, const float* grad_maps, int64_t images,
+                       int32_t width, int32_t height, float near_plane, float far_plane,
+                       float* grad_geometry, float* grad_appearance, float* grad_opacities,
+                       float* grad_backgrounds, void* stream);
+
+/* ------------------------------------------------------------------ */
+/* Kernel timing for measurement: when enabled, each compositor / sort /
+ * projection launch is bracketed by HIP events on its own stream.        */
+
+/* Kernel families reported by gs_profile_read. */
+#define GS_PROF_PROJECT_FWD 0
+#define GS_PROF_PROJECT_BWD 1
+#define GS_PROF_SH_FWD 2
+#define GS_PROF_SH_BWD 3
+#define GS_PROF_BINNING 4
+#define GS_PROF_SORT 5
+#define GS_PROF_RENDER_FWD 6
+#define GS_PROF_RENDER_BWD 7
+#define GS_PROF_COUNT 8
+
+/* Enable (1) or disable (0) event timing; enabling clears the totals. */
+int gs_profile_enable(int32_t enable);
+
+/* Synchronise pending events and report total milliseconds and launch
+ * count of one kernel family since the last enable. */
+int gs_profile_read(int32_t family, double* total_ms, int64_t* launches);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* GABOR_HIP_H */
