@@ -1,0 +1,372 @@
+"""Benchmark of the HIP Gabor rasterizer: fwd+bwd ms/iter and Mpix/s on one MI355X.
+
+Default workload is BASELINE config 4: classic Gabor, B=1 C=1, N=1M SH-3
+surfels drawn from 64 Gaussian clusters, 1920x1080, all nine output maps in
+a mean-square loss, forward + backward through the public API. A step is one
+forward + loss + backward over inputs already resident in HBM.
+
+Prints ONE JSON line. Besides the driver's contract fields it carries:
+  roofline      for the dominant kernel family (largest share of the timed
+                region): algorithmic bytes per launch / average launch time,
+                both measured in this run (HIP events on the launch stream);
+  cpu_baseline  the CPU oracle (torch fp32, autograd backward) timed on this
+                host over a bounded crop of the same workload;
+  kernels       per-family average milliseconds per step.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import platform
+import sys
+import time
+
+import torch
+
+HBM_PEAK_GBS = 8000.0
+FP32_VALU_PEAK_TFLOPS = 157.3
+
+CONFIGS = {
+    0: dict(name="config0: classic SH0, N=1024, 64x64", n=1024, width=64, height=64, scenes=1,
+            cameras=1, sh=0, neural=False, packed=False, channels=9),
+    1: dict(name="config1: classic SH3, N=100k, 1024x768, rgb+alpha+depth loss", n=100_000,
+            width=1024, height=768, scenes=1, cameras=1, sh=3, neural=False, packed=False,
+            channels=5),
+    2: dict(name="config2: neural SIREN, N=100k, 800x800", n=100_000, width=800, height=800,
+            scenes=1, cameras=1, sh=None, neural=True, packed=False, channels=9),
+    3: dict(name="config3: classic SH3, 8 scenes x 4 cameras, N=50k/scene, 512x512, packed",
+            n=50_000, width=512, height=512, scenes=8, cameras=4, sh=3, neural=False,
+            packed=True, channels=9),
+    4: dict(name="config4: classic SH3, N=1M surfels, 1920x1080, all 9 maps in loss",
+            n=1_000_000, width=1920, height=1080, scenes=1, cameras=1, sh=3, neural=False,
+            packed=False, channels=9),
+}
+
+
+def _uniform(generator, shape, low, high):
+    return torch.rand(shape, generator=generator) * (high - low) + low
+
+
+def _log_uniform(generator, shape, low, high):
+    return torch.exp(_uniform(generator, shape, math.log(low), math.log(high)))
+
+
+def _ring_cameras(generator, scenes, cameras, radius=5.0):
+    """Rigid world->camera views on a ring around the origin, looking at it."""
+    views = torch.zeros(scenes, cameras, 4, 4)
+    for s in range(scenes):
+        for c in range(cameras):
+            yaw = float(_uniform(generator, (), 0.0, 2 * math.pi))
+            centre = torch.tensor([radius * math.sin(yaw), 0.0, -radius * math.cos(yaw)])
+            forward = -centre / centre.norm()
+            down = torch.tensor([0.0, 1.0, 0.0])
+            right = torch.linalg.cross(down, forward)
+            right = right / right.norm()
+            down = torch.linalg.cross(forward, right)
+            R = torch.stack([right, down, forward])  # rows: camera axes in world
+            views[s, c, :3, :3] = R
+            views[s, c, :3, 3] = -R @ centre
+            views[s, c, 3, 3] = 1.0
+    return views
+
+
+def make_scene(index: int, seed: int | None = None, n: int | None = None):
+    """Seeded CPU tensors of one BASELINE config (see BASELINE.json `configs`)."""
+    cfg = CONFIGS[index]
+    g = torch.Generator().manual_seed(index if seed is None else seed)
+    S, C = cfg["scenes"], cfg["cameras"]
+    N = cfg["n"] if n is None else n
+    W, H = cfg["width"], cfg["height"]
+    if index == 0:
+        means = torch.cat([_uniform(g, (S, N, 2), -1, 1), _uniform(g, (S, N, 1), 2, 4)], -1)
+    elif index in (1, 2):
+        means = torch.cat([_uniform(g, (S, N, 2), -3, 3), _uniform(g, (S, N, 1), 2, 8)], -1)
+    elif index == 3:
+        means = _uniform(g, (S, N, 3), -2, 2)
+    else:
+        centres = torch.cat([_uniform(g, (64, 2), -5, 5), _uniform(g, (64, 1), 2, 12)], -1)
+        which = torch.randint(0, 64, (S, N), generator=g)
+        means = centres[which] + torch.randn(S, N, 3, generator=g) * 0.3
+    quats = torch.randn(S, N, 4, generator=g)
+    quats = quats / quats.norm(dim=-1, keepdim=True)
+    low, high = (0.005, 0.1) if index == 4 else (0.02, 0.2)
+    scales = _log_uniform(g, (S, N, 2), low, high)
+    opacities = _uniform(g, (S, N), 0.1, 0.9)
+    if index == 3:
+        views = _ring_cameras(g, S, C)
+    else:
+        views = torch.eye(4).expand(S, C, 4, 4).clone()
+    focal = {0: 80.0, 1: 900.0, 2: 900.0, 3: 600.0, 4: 1500.0}[index]
+    cx, cy = (32.0, 32.0) if index == 0 else ((W - 1) / 2, (H - 1) / 2)
+    K = torch.tensor([[focal, 0.0, cx], [0.0, focal, cy], [0.0, 0.0, 1.0]])
+    values = dict(means=means, quaternions=quats, scales=scales, opacities=opacities,
+                  view_matrices=views, intrinsics=K.expand(S, C, 3, 3).clone())
+    if cfg["neural"]:
+        values.update(
+            input_weights=_uniform(g, (S, N, 6, 5), -1 / 5, 1 / 5),
+            input_biases=torch.zeros(S, N, 6),
+            output_weights=_uniform(g, (S, N, 3, 6), -1 / 30, 1 / 30),
+            output_biases=torch.zeros(S, N, 3),
+        )
+    else:
+        k = (cfg["sh"] + 1) ** 2
+        weights = _uniform(g, (S, N, 4), 0, 1)
+        values.update(
+            colors=_uniform(g, (S, N, k, 3), 0, 1),
+            secondary_colors=_uniform(g, (S, N, k, 3), 0, 1),
+            frequency_weights=weights / weights.sum(-1, keepdim=True),
+            frequency_magnitudes=_uniform(g, (S, N, 4), 0, 8),
+            phases=_uniform(g, (S, N, 4), 0, 2 * math.pi),
+        )
+    return values
+
+
+CAMERA_KEYS = ("view_matrices", "intrinsics")
+
+
+def crop(values, x0: int, y0: int):
+    """The same scene seen through a window whose top-left pixel is (x0, y0)."""
+    out = dict(values)
+    K = values["intrinsics"].clone()
+    K[..., 0, 2] -= x0
+    K[..., 1, 2] -= y0
+    out["intrinsics"] = K
+    return out
+
+
+def _loss(rgb, alpha, meta, channels):
+    maps = torch.cat(
+        (rgb, alpha, meta["accumulated_depth"], meta["normals"], meta["distortion"]), -1
+    )
+    return maps[..., :channels].square().mean()
+
+
+def algorithmic_bytes(kind: str, neural: bool, pixels: int, records: int, pairs: int,
+                      rows: int) -> int:
+    """Compulsory HBM bytes of one compositor launch.
+
+    pixels: output pixels; records: tile-records the kernel walks (each gathers
+    point_list 4 B + primitive id 8 B + geometry 68 B + appearance 4A B +
+    opacity 4 B); pairs/rows: gradient rows written once by the backward.
+    Forward writes maps 36 B + state 12 B + contributors 4 B per pixel; the
+    backward reads the same 52 B per pixel.
+    """
+    appearance = 57 if neural else 18
+    record = 4 + 8 + 68 + 4 * appearance + 4
+    total = pixels * 52 + records * record
+    if kind == "render_backward":
+        total += pairs * 68 + rows * (4 * appearance + 4)
+    return int(total)
+
+
+def main(argv=None):
+    parser = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    parser.add_argument("--gpus", type=int, default=1)
+    parser.add_argument("--steps", type=int, default=10)
+    parser.add_argument("--warmup", type=int, default=3)
+    parser.add_argument("--config", type=int, default=4, choices=sorted(CONFIGS))
+    parser.add_argument("--validate", action="store_true",
+                        help="run the numerical input checks inside every step")
+    parser.add_argument("--cpu-baseline", type=int, default=1,
+                        help="1: time the CPU oracle on a crop of the workload (rank 0)")
+    parser.add_argument("--cpu-crop", type=int, default=32, help="crop edge in pixels")
+    parser.add_argument("--cpu-surfels", type=int, default=0,
+                        help="surfels used by the CPU baseline (0 = all of the workload)")
+    args = parser.parse_args(argv)
+    if args.gpus != 1:
+        print(
+            f"bench.py runs on exactly one GPU (got --gpus {args.gpus}); multi-GPU runs are "
+            "not part of this build",
+            file=sys.stderr,
+        )
+        return 2
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        return 2
+    from diff_gabor_splatting_amd import _native, rasterize_gabors, rasterize_neural_gabors
+
+    cfg = CONFIGS[args.config]
+    device = torch.device("cuda:0")
+    cpu_values = make_scene(args.config)
+    values = {k: v.to(device).contiguous() for k, v in cpu_values.items()}
+    for k, v in values.items():
+        v.requires_grad_(k not in CAMERA_KEYS)
+    renderer = rasterize_neural_gabors if cfg["neural"] else rasterize_gabors
+    options = dict(width=cfg["width"], height=cfg["height"], packed=cfg["packed"],
+                   validate=args.validate)
+    if not cfg["neural"]:
+        options["sh_degree"] = cfg["sh"]
+    params = [v for v in values.values() if v.requires_grad]
+
+    def step():
+        for p in params:
+            p.grad = None
+        rgb, alpha, meta = renderer(**values, **options)
+        _loss(rgb, alpha, meta, cfg["channels"]).backward()
+        return meta
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    _native.profile_enable(True)
+    torch.cuda.synchronize()
+    start = time.perf_counter()
+    for _ in range(args.steps):
+        meta = step()
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - start
+    kernels = {}
+    for family in _native.PROFILE_FAMILIES:
+        total_ms, launches = _native.profile_read(family)
+        kernels[family] = {"ms_per_step": total_ms / args.steps, "launches": launches,
+                           "avg_launch_ms": total_ms / launches if launches else 0.0}
+    _native.profile_enable(False)
+    ms_per_step = elapsed * 1000 / args.steps
+    images = cfg["scenes"] * cfg["cameras"]
+    pixels = images * cfg["width"] * cfg["height"]
+    mpix = pixels / (ms_per_step / 1000) / 1e6
+
+    # Workload statistics of the last step (outside the timed region).
+    stats = workload_stats(values, renderer, options)
+    dominant = max(("render_forward", "render_backward"), key=lambda f: kernels[f]["ms_per_step"])
+    walked = stats["records_backward" if dominant == "render_backward" else "records_forward"]
+    algo = algorithmic_bytes(dominant, cfg["neural"], pixels, walked, stats["pairs"],
+                             stats["rows"])
+    avg_ms = kernels[dominant]["avg_launch_ms"]
+    achieved = algo / (avg_ms / 1000) / 1e9 if avg_ms else 0.0
+    result = {
+        "metric": "fwd+bwd Mpix/s (1M surfels at 1080p); fwd+bwd ms/iter; HBM roofline",
+        "value": round(mpix, 3),
+        "unit": "Mpix/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded BASELINE distributions, generated on the CPU)",
+        "config": {
+            "workload": cfg["name"],
+            "surfels_per_scene": cfg["n"],
+            "images": images,
+            "width": cfg["width"],
+            "height": cfg["height"],
+            "sh_degree": cfg["sh"],
+            "neural": cfg["neural"],
+            "packed": cfg["packed"],
+            "validate": args.validate,
+            "tile_intersections": stats["intersections"],
+            "visible_pairs": stats["visible"],
+            "pixel_record_pairs_walked_per_s": round(
+                (stats["evals_forward"] + stats["evals_backward"]) / (ms_per_step / 1000), 1
+            ),
+        },
+        "roofline": {
+            "kernel": dominant,
+            "bound": "hbm",
+            "achieved": round(achieved, 2),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 5),
+            "traffic": None,
+            "algorithmic_bytes_per_launch": algo,
+            "avg_launch_ms": round(avg_ms, 4),
+            "note": "compositors are VALU-bound (transcendentals); see valu_estimate",
+        },
+        "kernels": {k: round(v["ms_per_step"], 4) for k, v in kernels.items()},
+        "gpu": torch.cuda.get_device_name(device),
+    }
+    if args.cpu_baseline:
+        result["cpu_baseline"] = cpu_baseline(cpu_values, cfg, args)
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+def workload_stats(values, renderer, options):
+    """Intersections, visible pairs and surfel-pixel evaluation counts of one call."""
+    from diff_gabor_splatting_amd import _native
+
+    with torch.no_grad():
+        captured = {}
+        original = _native.rasterize_forward
+
+        def spy(*a, **k):
+            out = original(*a, **k)
+            captured["out"] = out
+            captured["args"] = a
+            return out
+
+        _native.rasterize_forward = spy
+        try:
+            rgb, alpha, meta = renderer(**values, **options)
+        finally:
+            _native.rasterize_forward = original
+    maps, point_list, ranges, state, contributors = captured["out"]
+    geometry, appearance = captured["args"][0], captured["args"][1]
+    width, height = options["width"], options["height"]
+    tw, th = _native.tile_grid(width, height)
+    lengths = (ranges[:, 1] - ranges[:, 0]).long()
+    images = contributors.shape[0]
+    pad_h, pad_w = th * 16 - height, tw * 16 - width
+    contrib = torch.nn.functional.pad(contributors, (0, pad_w, 0, pad_h))
+    per_tile = contrib.reshape(images, th, 16, tw, 16).permute(0, 1, 3, 2, 4).reshape(-1, 256)
+    tile_max = per_tile.max(-1).values.long()
+    # (pixel, record) pairs walked: the backward walks every tile up to its
+    # largest contributor count; the forward at most the whole tile list.
+    return {
+        "intersections": int(point_list.numel()),
+        "visible": int((captured["args"][5] > 0).sum()),
+        "pairs": int(geometry.shape[0]),
+        "rows": int(appearance.shape[0]),
+        "records_forward": int(lengths.sum()),
+        "records_backward": int(tile_max.sum()),
+        "evals_forward": int(lengths.sum()) * 256,
+        "evals_backward": int(tile_max.sum()) * 256,
+    }
+
+
+def cpu_baseline(cpu_values, cfg, args):
+    """CPU oracle (fp32, autograd) fwd+bwd over a crop of the same workload."""
+    import oracle.render as oracle_render
+
+    threads = max(1, min(os.cpu_count() or 1, 16))
+    torch.set_num_threads(threads)
+    edge = args.cpu_crop
+    x0 = (cfg["width"] - edge) // 2
+    y0 = (cfg["height"] - edge) // 2
+    values = crop(cpu_values, x0, y0)
+    if args.cpu_surfels:
+        values = {k: (v if k in CAMERA_KEYS else v[:, : args.cpu_surfels].contiguous())
+                  for k, v in values.items()}
+    values = {k: v.clone().requires_grad_(k not in CAMERA_KEYS) for k, v in values.items()}
+    function = (oracle_render.rasterize_neural_gabors if cfg["neural"]
+                else oracle_render.rasterize_gabors)
+    options = dict(width=edge, height=edge, packed=cfg["packed"])
+    if not cfg["neural"]:
+        options["sh_degree"] = cfg["sh"]
+    params = [v for v in values.values() if v.requires_grad]
+    start = time.perf_counter()
+    maps, _, _ = function(**values, **options)
+    loss = maps[..., : cfg["channels"]].square().mean()
+    torch.autograd.grad(loss, params)
+    seconds = time.perf_counter() - start
+    pixels = cfg["scenes"] * cfg["cameras"] * edge * edge
+    return {
+        "value": round(pixels / seconds / 1e6, 6),
+        "unit": "Mpix/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": (f"{edge}x{edge} centre crop of the same scene and camera (all "
+                   f"{values['means'].shape[1]} surfels projected, SH evaluated, binned), "
+                   f"fp32 torch oracle forward + autograd backward, one step, "
+                   f"{seconds:.2f} s per step on {platform.processor() or 'host CPU'}"),
+    }
+
+
+if __name__ == "__main__":
+    sys.exit(main())

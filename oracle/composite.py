@@ -48,12 +48,16 @@ def appearance_color(a: torch.Tensor, s: torch.Tensor, dirs: torch.Tensor, neura
 
 
 def composite(geometry, appearance, opacities, primitive_ids, image_ids, radii, backgrounds,
-              width, height, neural, near_plane, far_plane, lists=None):
+              width, height, neural, near_plane, far_plane, lists=None, margins=None):
     """Differentiable forward compositor.
 
     Returns maps [I,H,W,9], point_list (np.int32), ranges (np.int32 [tiles,2]),
     state [I,H,W,3] (T, m1, m2) and contributors (np.int32 [I,H,W]).
     ``lists`` = (point_list, ranges) replaces the oracle's own binning.
+    If ``margins`` is a dict, margins["pixels"] receives [I,H,W] the smallest
+    relative distance, over the samples a pixel evaluated, of any discrete
+    decision from its threshold (alpha vs 1/255, T(1-alpha) vs 1e-4, the
+    surface/screen branch rho3 vs rho2, depth vs near, p.z vs 0).
     """
     dtype = geometry.dtype
     images = backgrounds.shape[0]
@@ -91,6 +95,7 @@ def composite(geometry, appearance, opacities, primitive_ids, image_ids, radii, 
     m2 = torch.zeros(tiles, TILE * TILE, dtype=dtype)
     done = ~inside
     last = torch.zeros(tiles, TILE * TILE, dtype=torch.int64)
+    margin = torch.full((tiles, TILE * TILE), math.inf, dtype=torch.float64)
     mscale = far_plane / (far_plane - near_plane)
     for k in range(longest):
         rec = table[:, k]
@@ -117,6 +122,20 @@ def composite(geometry, appearance, opacities, primitive_ids, image_ids, radii, 
         e = torch.exp(-0.5 * torch.minimum(rho3, rho2))
         alpha = (o * e).clamp_max(0.99)
         accept = ok & (alpha >= 1.0 / 255.0) & has[:, None] & ~done
+        if margins is not None:
+            with torch.no_grad():
+                walked = has[:, None] & ~done & inside
+                tiny = 1e-300
+                candidates = [
+                    (p[..., 2].abs() / (p.norm(dim=-1) + tiny)).double(),
+                    ((o * e - 1 / 255).abs() * 255).double(),
+                    ((depth - near_plane).abs() / near_plane).double(),
+                    torch.where(accept, ((T * (1 - alpha) - 1e-4).abs() / 1e-4), torch.inf).double(),
+                ]
+                if not neural:
+                    candidates.append(((rho3 - rho2).abs() / (rho3 + rho2 + tiny)).double())
+                local = torch.stack(candidates).amin(0)
+                margin = torch.where(walked, torch.minimum(margin, local), margin)
         stop = accept & (T * (1 - alpha) < 1e-4)
         done = done | stop
         take = accept & ~stop
@@ -151,4 +170,6 @@ def composite(geometry, appearance, opacities, primitive_ids, image_ids, radii, 
     maps = out.reshape(-1, 9)[keep][order].reshape(images, height, width, 9)
     state = torch.stack([T, m1, m2], -1).reshape(-1, 3)[keep][order].reshape(images, height, width, 3)
     contributors = last.reshape(-1)[keep][order].reshape(images, height, width)
+    if margins is not None:
+        margins["pixels"] = margin.reshape(-1)[keep][order].reshape(images, height, width)
     return maps, point_list, ranges, state, contributors.numpy().astype(np.int32)

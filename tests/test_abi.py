@@ -1,0 +1,73 @@
+"""The C-ABI library loads and exports every entry point include/*.h declares.
+
+Only argument-validation paths are called here: they return before any HIP
+call, so no GPU is needed.
+"""
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parents[1]
+
+
+def declared_symbols():
+    names = set()
+    for header in (ROOT / "include").glob("*.h"):
+        text = header.read_text()
+        names |= set(re.findall(r"^\s*(?:const\s+)?[\w\s\*]*?\b(gs_\w+)\s*\(", text, re.M))
+    return names
+
+
+def test_header_declares_the_api():
+    names = declared_symbols()
+    for required in ("gs_project_forward", "gs_project_backward", "gs_sh_forward",
+                     "gs_sh_backward", "gs_pack_visible", "gs_count_tiles", "gs_emit_tiles",
+                     "gs_sort_pairs", "gs_find_ranges", "gs_render_forward",
+                     "gs_render_backward", "gs_last_error"):
+        assert required in names
+
+
+def test_library_exports_every_declared_symbol():
+    from diff_gabor_splatting_amd import _native
+
+    library = ctypes.CDLL(str(_native._LIBRARY_PATH))
+    for name in sorted(declared_symbols()):
+        assert hasattr(library, name), name
+    assert set(_native.exported_symbols()) == declared_symbols()
+    assert _native.lib.gs_abi_version() == 1
+
+
+def test_argument_errors_return_status_and_message():
+    from diff_gabor_splatting_amd import _native
+
+    lib = _native.lib
+    status = lib.gs_sort_pairs(None, None, None, None, 10, 0, 70, None, 0, None)
+    assert status == 1 and b"bit range" in lib.gs_last_error()
+    status = lib.gs_project_forward(*([None] * 5), 0, 1, 4, 8, 8, 0.2, 100.0, *([None] * 6))
+    assert status == 1 and b"scenes" in lib.gs_last_error()
+    status = lib.gs_sh_forward(None, None, None, None, 1, 1, 4, 5, None)
+    assert status == 1 and b"degree" in lib.gs_last_error()
+    status = lib.gs_find_ranges(None, -1, None, 4, None)
+    assert status == 2
+    status = lib.gs_render_forward(0, *([None] * 7), 1, 16, 16, 1.0, 0.5, *([None] * 4))
+    assert status == 1 and b"clipping" in lib.gs_last_error()
+    # Workspace smaller than required is rejected before any launch.
+    need = lib.gs_scan_workspace_size(1000)
+    dummy = ctypes.c_void_p(16)
+    status = lib.gs_count_tiles(dummy, dummy, 1000, 16, 16, dummy, dummy, need - 1, None)
+    assert status == 4 and b"workspace" in lib.gs_last_error()
+    # Zero-sized work is a successful no-op.
+    assert lib.gs_sort_pairs(None, None, None, None, 0, 0, 64, None, 0, None) == 0
+    assert lib.gs_last_error() == b""
+
+
+@pytest.mark.parametrize("m", [0, 1, 4096, 4097, 10**6])
+def test_workspace_sizes_grow_with_input(m):
+    from diff_gabor_splatting_amd import _native
+
+    lib = _native.lib
+    assert lib.gs_sort_workspace_size(m) >= 12 * m
+    assert lib.gs_scan_workspace_size(m) >= 8 * ((m + 4095) // 4096)

@@ -1,0 +1,179 @@
+"""BASELINE configs on the GPU.
+
+Config 0 is compared with the float64 oracle outright. Configs 1-4 run at
+their full sizes and are checked through properties that do not need a full
+CPU render: binning bit-exact against the numpy oracle on the GPU's own
+geometry, dense == packed, a 16-pixel-aligned window of the full image
+equals a render through a camera cropped to that window, dropping surfels
+that miss the window changes nothing, and the cropped render of those
+surfels matches the float64 oracle (maps and gradients).
+"""
+
+import numpy as np
+import pytest
+import torch
+
+import bench
+from oracle import binning as oracle_binning
+from oracle import render as oracle_render
+from scenes import assert_gradients_close, fp32_conditioned, maps_from_result, oracle_reference
+
+pytestmark = [
+    pytest.mark.gpu,
+    pytest.mark.skipif(not torch.cuda.is_available(), reason="needs a GPU"),
+]
+DEVICE = torch.device("cuda:0")
+FORWARD_TOL = dict(atol=1e-5, rtol=1e-4)
+# Largest share of pixels that may be ill-conditioned at float32 precision.
+MAX_FLAGGED = 0.03
+
+
+def renderer(cfg):
+    from diff_gabor_splatting_amd import rasterize_gabors, rasterize_neural_gabors
+
+    return rasterize_neural_gabors if cfg["neural"] else rasterize_gabors
+
+
+def options(cfg, width=None, height=None, packed=None):
+    out = dict(width=width or cfg["width"], height=height or cfg["height"],
+               packed=cfg["packed"] if packed is None else packed)
+    if not cfg["neural"]:
+        out["sh_degree"] = cfg["sh"]
+    return out
+
+
+def gpu_values(values, grad=True):
+    return {k: v.to(DEVICE).contiguous().requires_grad_(grad) for k, v in values.items()}
+
+
+def capture_forward(function, values, opts):
+    """Run the public API and capture the compositor call's inputs/outputs."""
+    from diff_gabor_splatting_amd import _native
+
+    captured = {}
+    original = _native.rasterize_forward
+
+    def spy(*args):
+        captured["args"] = args
+        captured["out"] = original(*args)
+        return captured["out"]
+
+    _native.rasterize_forward = spy
+    try:
+        result = function(**values, **opts)
+    finally:
+        _native.rasterize_forward = original
+    return result, captured
+
+
+def oracle_fn(cfg):
+    return oracle_render.rasterize_neural_gabors if cfg["neural"] else oracle_render.rasterize_gabors
+
+
+def oracle_with_grads(cfg, values, opts, radii, weights):
+    leaves = {k: v.detach().cpu().double().requires_grad_() for k, v in values.items()}
+    maps, _, _ = oracle_fn(cfg)(**leaves, radii=radii, **opts)
+    out = torch.autograd.grad((maps * weights).sum(), list(leaves.values()), allow_unused=True)
+    return maps.detach(), [torch.zeros_like(l) if g is None else g for g, l in zip(out, leaves.values())]
+
+
+def compare_with_oracle(cfg, values, opts, result, seed):
+    """Maps on well-conditioned pixels within 1e-5/1e-4; gradients of a loss
+    restricted to those pixels within 1e-3 (conditioning-aware, see
+    scenes.assert_gradients_close)."""
+    maps = maps_from_result(result)
+    radii = result[2]["radii"].cpu()
+    _, mask = fp32_conditioned(oracle_fn(cfg), values, radii=radii, **opts)
+    assert float((~mask).float().mean()) <= MAX_FLAGGED, float((~mask).float().mean())
+    weights = torch.randn(maps.shape, generator=torch.Generator().manual_seed(seed))
+    weights = weights * mask[..., None]
+    actual = torch.autograd.grad((maps * weights.to(DEVICE)).sum(), list(values.values()))
+    expected_maps, expected, sensitivity = oracle_reference(oracle_fn(cfg), values, weights,
+                                                            radii=radii, **opts)
+    torch.testing.assert_close(maps.detach().cpu().double()[mask], expected_maps[mask], **FORWARD_TOL)
+    for name, a in zip(values, actual):
+        assert torch.isfinite(a).all(), name
+        assert_gradients_close(a, expected[name], name, sensitivity[name])
+
+
+def check_grads(names, actual, expected):
+    for name, a, e in zip(names, actual, expected):
+        assert torch.isfinite(a).all(), name
+        assert_gradients_close(a, e, name)
+
+
+def test_config0_matches_oracle():
+    cfg = bench.CONFIGS[0]
+    values = gpu_values(bench.make_scene(0))
+    opts = options(cfg)
+    result = renderer(cfg)(**values, **opts)
+    compare_with_oracle(cfg, values, opts, result, seed=0)
+
+
+@pytest.mark.parametrize("index", [1, 2, 3, 4])
+def test_config_binning_is_bit_exact(index):
+    cfg = bench.CONFIGS[index]
+    values = gpu_values(bench.make_scene(index), grad=False)
+    with torch.no_grad():
+        _, captured = capture_forward(renderer(cfg), values, options(cfg))
+    geometry, _, _, _, image_ids, radii, backgrounds = captured["args"][:7]
+    maps, point_list, ranges, state, contributors = captured["out"]
+    images = backgrounds.shape[0]
+    keys, ok_list, ok_ranges = oracle_binning.bin_pairs(
+        geometry.cpu().numpy(), radii.cpu().numpy(), image_ids.cpu().numpy(), images,
+        cfg["width"], cfg["height"],
+    )
+    assert len(ok_list) > 100_000
+    np.testing.assert_array_equal(point_list.cpu().numpy(), ok_list)
+    np.testing.assert_array_equal(ranges.cpu().numpy(), ok_ranges)
+    # Contributor counts never exceed the tile list they index.
+    assert int(contributors.min()) >= 0
+    assert torch.isfinite(maps).all() and torch.isfinite(state).all()
+
+
+@pytest.mark.parametrize("index", [1, 2, 3, 4])
+def test_config_dense_equals_packed(index):
+    cfg = bench.CONFIGS[index]
+    values = gpu_values(bench.make_scene(index))
+    outputs = {}
+    for packed in (False, True):
+        maps = maps_from_result(renderer(cfg)(**values, **options(cfg, packed=packed)))
+        grads = torch.autograd.grad(maps.square().mean(), list(values.values()))
+        outputs[packed] = (maps.detach(), grads)
+    # Packing keeps the relative pair order, so tile lists - and maps - are identical.
+    assert torch.equal(outputs[False][0], outputs[True][0])
+    for name, a, b in zip(values, outputs[False][1], outputs[True][1]):
+        assert torch.isfinite(a).all(), name
+        # Only the order of float32 atomic additions differs.
+        assert_gradients_close(a, b, name)
+
+
+@pytest.mark.parametrize("index", [1, 2, 3, 4])
+def test_config_crop_matches_full_image_and_oracle(index):
+    cfg = bench.CONFIGS[index]
+    cpu = bench.make_scene(index)
+    full = gpu_values(cpu, grad=False)
+    with torch.no_grad():
+        full_maps = maps_from_result(renderer(cfg)(**full, **options(cfg)))
+    edge = 32
+    x0 = (cfg["width"] // 2) // 16 * 16
+    y0 = (cfg["height"] // 2) // 16 * 16
+    cropped = bench.crop(cpu, x0, y0)
+    crop_values = gpu_values(cropped, grad=False)
+    with torch.no_grad():
+        crop_maps, crop_alpha, crop_meta = renderer(cfg)(**crop_values, **options(cfg, edge, edge, packed=False))
+        crop_all = maps_from_result((crop_maps, crop_alpha, crop_meta))
+    window = full_maps[..., y0:y0 + edge, x0:x0 + edge, :]
+    torch.testing.assert_close(crop_all, window, atol=2e-5, rtol=2e-4)
+    # Keep only surfels visible in the window (in every camera of a scene
+    # that needs them), in their original order.
+    visible = (crop_meta["radii"] > 0).reshape(cfg["scenes"], cfg["cameras"], -1).any(1).any(0)
+    keep = torch.nonzero(visible.cpu()).reshape(-1)
+    assert len(keep) > 0
+    subset = {k: (v if k in ("view_matrices", "intrinsics") else v[:, keep].contiguous())
+              for k, v in cropped.items()}
+    subset_values = gpu_values(subset)
+    opts = options(cfg, edge, edge, packed=False)
+    result = renderer(cfg)(**subset_values, **opts)
+    assert torch.equal(maps_from_result(result).detach(), crop_all)
+    compare_with_oracle(cfg, subset_values, opts, result, seed=index)

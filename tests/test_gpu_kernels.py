@@ -1,0 +1,175 @@
+"""Kernel-level parity: binning, sort and ranges bit-exact; projection and SH
+within float tolerance of the float64 oracle."""
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import binning as oracle_binning
+from oracle.projection import project, radius_before_ceil
+from oracle.sh import sh_colors
+from scenes import assert_gradients_close, describe_mismatch, perturbation_sensitivity
+
+pytestmark = [
+    pytest.mark.gpu,
+    pytest.mark.skipif(not torch.cuda.is_available(), reason="needs a GPU"),
+]
+DEVICE = torch.device("cuda:0")
+
+
+@pytest.fixture(scope="module")
+def native():
+    from diff_gabor_splatting_amd import _native
+
+    return _native
+
+
+def to_u64(t):
+    return t.cpu().numpy().view(np.uint64)
+
+
+@pytest.mark.parametrize("m", [1, 5, 4095, 4096, 4097, 100_003, 2_000_000])
+@pytest.mark.parametrize("bits", [(0, 64), (0, 45), (32, 45), (3, 17)])
+def test_sort_is_stable_radix_order(native, m, bits):
+    rng = np.random.default_rng(m + bits[0])
+    keys = rng.integers(0, 2**63, m, dtype=np.uint64) | (rng.integers(0, 2, m, dtype=np.uint64) << np.uint64(63))
+    keys[rng.integers(0, m, m // 3)] = keys[0]  # many exact ties
+    values = np.arange(m, dtype=np.int32)[::-1].copy()
+    sk, sv = native.sort_pairs(torch.from_numpy(keys.view(np.int64)).to(DEVICE),
+                               torch.from_numpy(values).to(DEVICE), *bits)
+    begin, end = bits
+    digit = (keys >> np.uint64(begin)) & np.uint64((1 << (end - begin)) - 1 if end - begin < 64 else 2**64 - 1)
+    order = np.argsort(digit, kind="stable")
+    np.testing.assert_array_equal(to_u64(sk), keys[order])
+    np.testing.assert_array_equal(sv.cpu().numpy(), values[order])
+
+
+def random_geometry(seed, q, width, height, images):
+    rng = np.random.default_rng(seed)
+    geometry = rng.normal(size=(q, 17)).astype(np.float32)
+    geometry[:, 9] = rng.uniform(-60, width + 60, q)
+    geometry[:, 10] = rng.uniform(-60, height + 60, q)
+    geometry[:, 8] = rng.choice(rng.uniform(0.3, 50, max(q // 3, 1)).astype(np.float32), q)
+    radii = rng.integers(-3, 70, q).astype(np.int32)
+    image_ids = np.sort(rng.integers(0, images, q)).astype(np.int64)
+    return geometry, radii, image_ids
+
+
+@pytest.mark.parametrize("seed, q, width, height, images", [
+    (0, 1, 16, 16, 1), (1, 700, 100, 61, 3), (2, 20_000, 640, 480, 2), (3, 5000, 1920, 1080, 1),
+])
+def test_binning_pipeline_is_bit_exact(native, seed, q, width, height, images):
+    geometry, radii, image_ids = random_geometry(seed, q, width, height, images)
+    g, r, ids = (torch.from_numpy(a).to(DEVICE) for a in (geometry, radii, image_ids))
+    offsets = native.count_tiles(g, r, width, height)
+    expected_counts = oracle_binning.tile_counts(geometry, radii, width, height)
+    np.testing.assert_array_equal(offsets.cpu().numpy(), np.cumsum(expected_counts))
+    m = int(offsets[-1])
+    keys, values = native.emit_tiles(g, r, ids, offsets, width, height, m)
+    expected_keys, expected_values = oracle_binning.emit(geometry, radii, image_ids, width, height)
+    np.testing.assert_array_equal(to_u64(keys), expected_keys)
+    np.testing.assert_array_equal(values.cpu().numpy(), expected_values)
+    tw, th = native.tile_grid(width, height)
+    tiles = images * tw * th
+    sorted_keys, point_list = native.sort_pairs(keys, values, 0, native.sort_end_bit(tiles))
+    ok_keys, ok_list, ok_ranges = oracle_binning.bin_pairs(geometry, radii, image_ids, images, width, height)
+    np.testing.assert_array_equal(to_u64(sorted_keys), ok_keys)
+    np.testing.assert_array_equal(point_list.cpu().numpy(), ok_list)
+    np.testing.assert_array_equal(native.find_ranges(sorted_keys, tiles).cpu().numpy(), ok_ranges)
+
+
+def test_ranges_of_empty_list_are_zero(native):
+    ranges = native.find_ranges(torch.empty(0, dtype=torch.int64, device=DEVICE), 37)
+    assert ranges.shape == (37, 2) and int(ranges.abs().sum()) == 0
+
+
+@pytest.mark.parametrize("count", [0, 1, 4096, 4097, 1_000_000])
+def test_pack_visible(native, count):
+    rng = np.random.default_rng(count)
+    radii = rng.integers(-1, 3, count).astype(np.int32)
+    selected = native.pack_visible(torch.from_numpy(radii).to(DEVICE))
+    np.testing.assert_array_equal(selected.cpu().numpy(), oracle_binning.pack_visible(radii))
+
+
+def projection_inputs(seed, S=2, C=3, N=777, width=64, height=48, z_low=-0.5):
+    g = torch.Generator().manual_seed(seed)
+    means = torch.cat([torch.rand(S, N, 2, generator=g) * 3 - 1.5,
+                       torch.rand(S, N, 1, generator=g) * (5.5 - z_low) + z_low], -1)
+    quats = torch.randn(S, N, 4, generator=g)
+    quats = quats / quats.norm(dim=-1, keepdim=True)
+    scales = torch.exp(torch.rand(S, N, 2, generator=g) * math.log(10) + math.log(0.02))
+    views = torch.eye(4).expand(S, C, 4, 4).clone()
+    angle = torch.rand(S, C, generator=g) * 0.4 - 0.2
+    views[..., 0, 0], views[..., 0, 2] = angle.cos(), angle.sin()
+    views[..., 2, 0], views[..., 2, 2] = -angle.sin(), angle.cos()
+    views[..., :3, 3] = torch.randn(S, C, 3, generator=g) * 0.2
+    K = torch.tensor([[50.0, 0.5, (width - 1) / 2], [0, 52.0, (height - 1) / 2], [0, 0, 1]])
+    return [means, quats, scales, views, K.expand(S, C, 3, 3).clone()], width, height
+
+
+def test_projection_forward_matches_oracle(native):
+    inputs, width, height = projection_inputs(0)
+    gpu = native.project_forward(*(t.to(DEVICE) for t in inputs), width, height, 0.2, 100.0)
+    ref = project(*(t.double() for t in inputs), width, height, 0.2, 100.0)
+    # Per-element bound: 1e-6 relative plus four times the float64 output's
+    # sensitivity to float32-sized input perturbations (the conic centre of a
+    # nearly edge-on surfel is ill-conditioned).
+    sens = perturbation_sensitivity(lambda *x: project(*x, width, height, 0.2, 100.0)[:4], inputs)
+    for name, a, b, d in zip(("transform", "xy", "normals", "directions"), gpu[:4], ref[:4], sens):
+        a = a.cpu().double()
+        ok = (a - b).abs() <= 1e-6 * (1 + b.abs()) + 4 * d
+        assert bool(ok.all()), f"{name}: {describe_mismatch(a, b)}"
+    # Radii are integers from a ceiling: they must agree except where the
+    # float64 pre-ceiling radius lies within 1e-4 of an integer (margin rule),
+    # and the float32 oracle must agree exactly off those margins too.
+    radii32 = project(*inputs, width, height, 0.2, 100.0)[4]
+    before = radius_before_ceil(*(t.double() for t in inputs))
+    wobble = perturbation_sensitivity(radius_before_ceil, inputs)[0]
+    margin = (before - before.round()).abs() <= 4 * wobble + 1e-4
+    differ = gpu[4].cpu() != radii32
+    assert not bool((differ & ~margin).any()), int(differ.sum())
+    assert int((gpu[4].cpu() > 0).sum()) > 100
+
+
+def test_projection_backward_matches_autograd(native):
+    # Depths in [1, 5.5]: away from the camera plane, where the conic centre
+    # and its derivatives blow up.
+    inputs, width, height = projection_inputs(1, S=2, C=2, N=300, z_low=1.0)
+    leaves = [t.double().requires_grad_() for t in inputs]
+    outs = project(*leaves, width, height, 0.2, 100.0)[:4]
+    g = torch.Generator().manual_seed(5)
+    grads = [torch.randn(o.shape, generator=g, dtype=torch.float64) for o in outs]
+    expected = torch.autograd.grad(sum((o * w).sum() for o, w in zip(outs, grads)), leaves,
+                                   retain_graph=True)
+    actual = native.project_backward(*(t.to(DEVICE) for t in inputs),
+                                     *(w.float().to(DEVICE) for w in grads))
+    for name, a, e in zip(("means", "quaternions", "scales", "views", "intrinsics"), actual, expected):
+        assert_gradients_close(a, e, name, rel_norm=1e-5, elem=1e-5, rtol=1e-5)
+    # Missing output gradients are treated as zero.
+    partial = native.project_backward(*(t.to(DEVICE) for t in inputs), None, grads[1].float().to(DEVICE), None, None)
+    expected_partial = torch.autograd.grad((outs[1] * grads[1]).sum(), leaves)
+    torch.testing.assert_close(partial[0].cpu().double(), expected_partial[0], atol=1e-4, rtol=1e-4)
+
+
+@pytest.mark.parametrize("degree", [0, 1, 2, 3])
+@pytest.mark.parametrize("cameras", [1, 3])
+def test_sh_values_and_derivatives(native, degree, cameras):
+    g = torch.Generator().manual_seed(31)
+    k = (degree + 1) ** 2
+    first = torch.randn(2, 7, k, 3, generator=g)
+    second = torch.randn(2, 7, k, 3, generator=g)
+    d = torch.randn(2, cameras, 7, 3, generator=g)
+    d = d / d.norm(dim=-1, keepdim=True)
+    colors = native.evaluate_sh_forward(first.to(DEVICE), second.to(DEVICE), d.to(DEVICE), degree)
+    leaves = [t.double().requires_grad_() for t in (first, second, d)]
+    expected = sh_colors(*leaves, degree)
+    torch.testing.assert_close(colors.cpu().double(), expected, atol=3e-6, rtol=3e-5)
+    weights = torch.randn(expected.shape, generator=g, dtype=torch.float64)
+    eg = torch.autograd.grad((expected * weights).sum(), leaves, allow_unused=True)
+    ag = native.evaluate_sh_backward(first.to(DEVICE), second.to(DEVICE), d.to(DEVICE),
+                                     weights.float().to(DEVICE), degree)
+    for a, e, leaf in zip(ag, eg, leaves):
+        e = torch.zeros_like(leaf) if e is None else e
+        torch.testing.assert_close(a.cpu().double(), e, atol=3e-5, rtol=2e-4)

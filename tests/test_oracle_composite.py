@@ -1,0 +1,163 @@
+"""Pins oracle/composite.py and oracle/render.py on the CPU (float64)."""
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import render as oracle_render
+from scenes import _surfel_samples, make_inputs, pixel_reference
+
+RENDER = {"classic": oracle_render.rasterize_gabors, "neural": oracle_render.rasterize_neural_gabors}
+
+
+def oracle_maps(method, values, width=9, height=9, **options):
+    values = dict(values)
+    backgrounds = values.pop("backgrounds")
+    maps, meta, aux = RENDER[method](**values, width=width, height=height,
+                                     backgrounds=backgrounds, **options)
+    return maps, meta, aux
+
+
+def as64(values):
+    return {k: v.double().requires_grad_() for k, v in values.items()}
+
+
+# The oracle keeps the reference's float32 pi and frequency directions
+# (cos(pi f / 4) with f = 2 is -4.4e-8, not 0); the pixel reference uses
+# exact ones, so maps agree to ~1e-7 rather than to double rounding.
+TOLERANCE = dict(atol=2e-7, rtol=1e-6)
+
+
+@pytest.mark.parametrize("method", ["classic", "neural"])
+@pytest.mark.parametrize("packed", [False, True])
+@pytest.mark.parametrize("scenes, cameras", [(1, 2), (2, 3)])
+def test_oracle_matches_pixel_reference(method, packed, scenes, cameras):
+    values = as64(make_inputs(method, scenes=scenes, cameras=cameras))
+    actual, _, _ = oracle_maps(method, values, packed=packed)
+    expected = pixel_reference(method, values)
+    torch.testing.assert_close(actual, expected, **TOLERANCE)
+    weights = torch.linspace(-0.4, 0.7, actual.numel(), dtype=torch.float64).reshape(actual.shape)
+    grads = torch.autograd.grad((actual * weights).sum(), list(values.values()), retain_graph=True)
+    expected_grads = torch.autograd.grad((expected * weights).sum(), list(values.values()))
+    for name, a, e in zip(values, grads, expected_grads):
+        torch.testing.assert_close(a, e, atol=2e-6, rtol=1e-5, msg=name)
+
+
+@pytest.mark.parametrize("method", ["classic", "neural"])
+@pytest.mark.parametrize("opacity", [0.0, 1.0])
+def test_opacity_cutoff_and_saturation(method, opacity):
+    values = make_inputs(method, cameras=1, primitives=7)
+    values["opacities"].fill_(0.85 if opacity == 1.0 else opacity)
+    values["opacities"][..., 0] = opacity
+    values["quaternions"].zero_()
+    values["quaternions"][..., 0] = 1
+    values["means"][..., :2] = 0
+    values = as64(values)
+    actual, _, aux = oracle_maps(method, values)
+    torch.testing.assert_close(actual, pixel_reference(method, values), **TOLERANCE)
+    if opacity == 1.0:
+        # Alpha 0.99 then 0.85s: T goes 1 -> 1e-2 -> 1.5e-3 -> 2.25e-4; the
+        # fourth would take it to 3.4e-5 < 1e-4, so exactly three contribute
+        # at the centre pixel and the next stops it.
+        assert int(aux["contributors"][0, 4, 4]) == 3
+
+
+@pytest.mark.parametrize("method", ["classic", "neural"])
+def test_lowpass_and_batch_boundary(method):
+    tiny = make_inputs(method, cameras=1, primitives=1)
+    tiny["scales"].fill_(0.02)
+    tiny["quaternions"].zero_()
+    tiny["quaternions"][..., 0] = 1
+    many = make_inputs(method, cameras=1, primitives=65)
+    many["opacities"].fill_(0.03)
+    for values in (tiny, many):
+        values = as64(values)
+        actual, _, _ = oracle_maps(method, values)
+        torch.testing.assert_close(actual, pixel_reference(method, values), **TOLERANCE)
+
+
+def test_single_surfel_closed_form():
+    # Fronto-parallel surfel whose mean projects exactly on pixel (4, 4):
+    # rho = 0 there, so alpha = min(0.99, o); magnitudes 0 make every wave
+    # cos(phase), i.e. h1 = sum w (1 + cos phase) / 2.
+    values = make_inputs("classic", cameras=1, primitives=1)
+    values["means"][:] = torch.tensor([0.0, 0.0, 3.0])
+    values["quaternions"][:] = torch.tensor([1.0, 0, 0, 0])
+    values["view_matrices"][..., :3, 3] = 0.0
+    values["frequency_magnitudes"].zero_()
+    values["opacities"].fill_(0.6)
+    values = as64(values)
+    maps, meta, aux = oracle_maps("classic", values)
+    px = maps[0, 0, 4, 4]
+    phases, weights = values["phases"][0, 0], values["frequency_weights"][0, 0]
+    h1 = (weights * (1 + phases.cos()) / 2).sum()
+    h2 = (weights * (1 - phases.cos()) / 2).sum()
+    color = h1 * values["colors"][0, 0] + h2 * values["secondary_colors"][0, 0]
+    expected_rgb = 0.6 * color + 0.4 * values["backgrounds"][0, 0]
+    torch.testing.assert_close(px[:3], expected_rgb.detach())
+    torch.testing.assert_close(px[3], torch.tensor(0.6, dtype=torch.float64))
+    torch.testing.assert_close(px[4], torch.tensor(0.6 * 3.0, dtype=torch.float64))
+    torch.testing.assert_close(px[5:8], torch.tensor([0.0, 0.0, -0.6], dtype=torch.float64))
+    assert float(px[8]) == 0.0  # one surfel: no distortion
+    assert int(aux["contributors"][0, 4, 4]) == 1
+    assert int(meta["radii"][0, 0, 0]) > 0
+
+
+@pytest.mark.parametrize("method", ["classic", "neural"])
+def test_distortion_is_pairwise_sum(method):
+    values = as64(make_inputs(method, cameras=1, primitives=5))
+    maps, _, _ = oracle_maps(method, values)
+    near, far = 0.2, 100.0
+    py, px = torch.meshgrid(torch.arange(9.0, dtype=torch.float64), torch.arange(9.0, dtype=torch.float64), indexing="ij")
+    transmittance = torch.ones_like(px)
+    weights, ms = [], []
+    for i in range(5):
+        alpha, depth, _, _ = _surfel_samples(method, {k: v.detach() for k, v in values.items()}, 0, 0, i, px, py)
+        alpha = torch.where((alpha >= 1 / 255) & (depth >= near), alpha, 0)
+        weights.append(transmittance * alpha)
+        ms.append(far / (far - near) * (1 - near / depth))
+        transmittance = transmittance * (1 - alpha)
+    pairwise = sum(weights[i] * weights[j] * (ms[i] - ms[j]) ** 2 for i in range(5) for j in range(i))
+    torch.testing.assert_close(maps[0, 0, ..., 8].detach(), pairwise, atol=1e-12, rtol=1e-9)
+
+
+@pytest.mark.parametrize("method", ["classic", "neural"])
+def test_oracle_gradients_match_finite_differences(method):
+    values = as64(make_inputs(method, cameras=2, primitives=3))
+    names = ["means", "scales", "opacities", "quaternions", "view_matrices", "intrinsics",
+             "phases" if method == "classic" else "input_biases"]
+    weights = torch.linspace(-0.2, 0.4, 2 * 81 * 9, dtype=torch.float64).reshape(1, 2, 9, 9, 9)
+
+    def objective():
+        return (oracle_maps(method, values)[0] * weights).sum()
+
+    grads = torch.autograd.grad(objective(), [values[n] for n in names])
+    step = 1e-6
+    for name, grad in zip(names, grads):
+        value = values[name]
+        flat = value.detach().view(-1)
+        for index in range(0, flat.numel(), max(1, flat.numel() // 4)):
+            original = float(flat[index])
+            with torch.no_grad():
+                flat[index] = original + step
+                plus = float(objective())
+                flat[index] = original - step
+                minus = float(objective())
+                flat[index] = original
+            numeric = (plus - minus) / (2 * step)
+            analytic = float(grad.reshape(-1)[index])
+            assert abs(analytic - numeric) <= 1e-5 + 1e-5 * abs(numeric), (name, index, analytic, numeric)
+
+
+def test_empty_and_invisible_scenes_are_background():
+    for n, z in ((0, 3.0), (3, -2.0)):
+        values = make_inputs("classic", primitives=n)
+        if n:
+            values["means"][..., 2] = z
+        values = as64(values)
+        maps, meta, aux = oracle_maps("classic", values)
+        torch.testing.assert_close(maps[..., :3], values["backgrounds"][:, :, None, None, :].expand(1, 2, 9, 9, 3))
+        assert maps[..., 3].count_nonzero() == 0
+        assert len(aux["point_list"]) == 0
