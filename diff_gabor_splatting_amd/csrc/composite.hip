@@ -12,14 +12,26 @@
 //  * backward replays each tile in reverse from its largest contributor
 //    count, recovering T by division.
 //
-// MI355X layout: one workgroup of four wave64s per 16x16 tile, each wave
-// owning an 8x8 quadrant (compact footprint for divergence). Records are
-// gathered into LDS in batches of 64 (geometry | opacity | appearance, 16-B
-// aligned rows, read as broadcasts). In the backward, each wave sums its 64
-// pixels' gradients with one reduce-scatter (see wave.hpp) and adds them to
-// a per-batch LDS accumulator with one ds_add per wave; after the batch the
-// workgroup flushes nonzero totals with one global atomic per (tile,
-// record, parameter) instead of one per (wave, record, parameter).
+// MI355X design. Both kernels are bound by VALU issue (rocprof: ~95% of one
+// wave64 VALU instruction per CU per cycle), so the work per (pixel,
+// record) sample is what matters:
+//  * one workgroup of four wave64s per 16x16 tile, each wave owning an 8x8
+//    quadrant; records are staged in LDS in batches of 64 and read as
+//    broadcasts;
+//  * while staging, one thread per record derives per-record constants once
+//    for all 256 pixels: a conservative rejection threshold on rho (2 ln(255
+//    o), slightly enlarged) so most rejected samples cost ~25 instructions
+//    and no division or exp; the four Gabor phases in revolutions,
+//    t_f = A_f u + B_f v + C_f with A_f, B_f = m_f d_f and C_f = phase/2pi,
+//    evaluated with the hardware sin/cos on fract(t_f); the colour mix
+//    folded to W/2 (c1 + c2) + S (c1 - c2) with S = sum w_f/2 cos; the SIREN
+//    pre-activations folded to zc + U u + V v;
+//  * reciprocals (v_rcp) replace the IEEE divisions and exp2 replaces expf
+//    (both within two float32 ulps);
+//  * in the backward, each wave sums its 64 pixels' gradients with one
+//    reduce-scatter (wave.hpp), adds them to a per-batch LDS accumulator with
+//    one ds_add per wave, and after the batch the workgroup flushes nonzero
+//    totals with one global atomic per (tile, record, parameter).
 #include <climits>
 #include <cmath>
 
@@ -30,99 +42,148 @@ namespace gs {
 namespace {
 
 constexpr int kBatch = 64;
-constexpr float kPi = 3.14159265358979323846f;
+constexpr float kTwoPi = 6.28318530717958647692f;
+constexpr float kInvTwoPi = 0.15915494309189533577f;
+constexpr float kNegHalfLog2e = -0.72134752044448170368f;  // -log2(e) / 2
+constexpr float kLog2e = 1.44269504088896340736f;
+constexpr float kSirenRevolutions = 30.f * kInvTwoPi;        // sin(30 z) = sin(2 pi z 30/2pi)
+constexpr float kMinAlpha = 1.0f / 255.0f;
 
 // Directions (cos(pi f / 4), sin(pi f / 4)) of the four Gabor frequencies,
 // evaluated the way the reference does: float angle pi*f/4, float cos/sin.
 __device__ constexpr float kDirX[4] = {1.0f, 0.70710677f, -4.371139e-08f, -0.70710677f};
 __device__ constexpr float kDirY[4] = {0.0f, 0.70710677f, 1.0f, 0.70710677f};
 
-template <bool Neural>
-struct Layout {
-  static constexpr int A = Neural ? kNeural : kClassic;  // appearance floats
-  static constexpr int OP = 17;                          // opacity slot in a row
-  static constexpr int AP = 18;                          // first appearance slot
-  static constexpr int RS = Neural ? 76 : 36;            // LDS row stride (16-B multiple)
-  static constexpr int NP = kGeometry + A + 1;           // gradient values per record
+__device__ __forceinline__ float rcp(float x) { return __builtin_amdgcn_rcpf(x); }
+__device__ __forceinline__ float sin_rev(float t) { return __builtin_amdgcn_sinf(t); }
+__device__ __forceinline__ float cos_rev(float t) { return __builtin_amdgcn_cosf(t); }
+__device__ __forceinline__ float fract(float t) { return __builtin_amdgcn_fractf(t); }
+
+// LDS row layouts (floats). Geometry first in both: T 0-8, xy 9-10,
+// normal 11-13.
+struct ClassicRow {
+  static constexpr int OP = 14, THR = 15;
+  static constexpr int A = 16, B = 20, C = 24, HW = 28;  // 4 each
+  static constexpr int HALF_W = 32, SUM = 33, DIFF = 36;  // 1, 3, 3
+  static constexpr int STRIDE = 40;
+};
+struct NeuralRow {
+  static constexpr int DIR = 14, OP = 17, THR = 18;
+  static constexpr int ZC = 19, U = 25, V = 31;  // 6 each
+  static constexpr int WDIR = 37;                // W1[h][2..4], 18
+  static constexpr int W2 = 55, B2 = 73;         // 18, 3
+  static constexpr int STRIDE = 76;
 };
 
+template <bool Neural>
+struct Layout {
+  static constexpr int A = Neural ? kNeural : kClassic;  // raw appearance floats
+  static constexpr int RAW = kGeometry + 1 + A;          // raw staging floats
+  static constexpr int RAW_STRIDE = Neural ? 76 : 36;
+  static constexpr int STRIDE = Neural ? NeuralRow::STRIDE : ClassicRow::STRIDE;
+  // Gradient values per record: geometry (classic skips the unused
+  // direction columns), appearance, opacity.
+  static constexpr int NG = Neural ? kGeometry : 14;
+  static constexpr int NP = NG + A + 1;
+};
+
+// Rejection threshold on rho: alpha = min(0.99, o exp(-rho/2)) < 1/255
+// whenever rho > 2 ln(255 o). The relative and absolute slack keep the test
+// conservative against float32 rounding, so it only ever skips samples the
+// exact test rejects.
+__device__ __forceinline__ float reject_threshold(float opacity) {
+  return 2.f * logf(255.f * opacity) * (1.f + 1e-4f) + 1e-4f;
+}
+
 struct Sample {
-  float k[3], l[3], p[3], s[2], depth, e, alpha;
+  float k[3], l[3], p[3], s[2], inv_pz, depth, e, alpha;
   bool surface;
 };
 
-__device__ __forceinline__ void cross3(const float* a, const float* b, float* c) {
-  c[0] = a[1] * b[2] - a[2] * b[1];
-  c[1] = a[2] * b[0] - a[0] * b[2];
-  c[2] = a[0] * b[1] - a[1] * b[0];
-}
-
-// Intersect the pixel ray with the surfel plane and evaluate filtered alpha.
 template <bool Neural>
-__device__ __forceinline__ bool sample_surface(const float* g, float opacity, float x, float y,
+__device__ __forceinline__ bool sample_surface(const float* r, float x, float y,
                                                float near_plane, Sample& v) {
+  constexpr int OP = Neural ? NeuralRow::OP : ClassicRow::OP;
+  constexpr int THR = Neural ? NeuralRow::THR : ClassicRow::THR;
 #pragma unroll
   for (int i = 0; i < 3; ++i) {
-    v.k[i] = x * g[6 + i] - g[i];
-    v.l[i] = y * g[6 + i] - g[3 + i];
+    v.k[i] = x * r[6 + i] - r[i];
+    v.l[i] = y * r[6 + i] - r[3 + i];
   }
-  cross3(v.k, v.l, v.p);
-  if (v.p[2] == 0.f) return false;
-  v.s[0] = v.p[0] / v.p[2];
-  v.s[1] = v.p[1] / v.p[2];
-  const float rho3 = v.s[0] * v.s[0] + v.s[1] * v.s[1];
-  const float dx = g[9] - x, dy = g[10] - y;
+  v.p[0] = v.k[1] * v.l[2] - v.k[2] * v.l[1];
+  v.p[1] = v.k[2] * v.l[0] - v.k[0] * v.l[2];
+  v.p[2] = v.k[0] * v.l[1] - v.k[1] * v.l[0];
+  const float dx = r[9] - x, dy = r[10] - y;
   const float rho2 = 2.f * (dx * dx + dy * dy);
+  const float thr = r[THR];
+  // min(rho3, rho2) > thr without dividing: rho3 = |p.xy|^2 / p.z^2.
+  if (rho2 > thr && v.p[0] * v.p[0] + v.p[1] * v.p[1] > thr * (v.p[2] * v.p[2])) return false;
+  if (v.p[2] == 0.f) return false;
+  v.inv_pz = rcp(v.p[2]);
+  v.s[0] = v.p[0] * v.inv_pz;
+  v.s[1] = v.p[1] * v.inv_pz;
+  const float rho3 = v.s[0] * v.s[0] + v.s[1] * v.s[1];
   v.surface = rho3 <= rho2;
-  v.depth = (Neural || v.surface) ? v.s[0] * g[6] + v.s[1] * g[7] + g[8] : g[8];
-  if (v.depth < near_plane || !isfinite(v.depth)) return false;
-  v.e = expf(-0.5f * fminf(rho3, rho2));
-  v.alpha = fminf(0.99f, opacity * v.e);
-  return v.alpha >= 1.0f / 255.0f;
+  v.depth = (Neural || v.surface) ? v.s[0] * r[6] + v.s[1] * r[7] + r[8] : r[8];
+  if (!(v.depth >= near_plane) || !isfinite(v.depth)) return false;
+  v.e = __builtin_amdgcn_exp2f(fminf(rho3, rho2) * kNegHalfLog2e);
+  v.alpha = fminf(0.99f, r[OP] * v.e);
+  return v.alpha >= kMinAlpha;
 }
 
-// Classic: two colours mixed by four cosine waves. Neural: 5->6->3 SIREN.
-template <bool Neural>
-__device__ __forceinline__ void appearance_forward(const float* a, const float* g,
-                                                   const Sample& v, float* color,
-                                                   float* hidden, float* pre) {
+// Appearance at local coordinates s. Classic keeps the per-frequency
+// cos/sin for the backward; neural keeps the hidden sin/cos.
+struct Shade {
+  float color[3];
+  float c[6], sn[6];  // classic: cos/sin of the 4 waves; neural: cos/sin of 6 units
+  float S;            // classic: sum_f (w_f / 2) cos_f
+};
+
+template <bool Neural, bool Backward>
+__device__ __forceinline__ void shade(const float* r, const float* s, Shade& a) {
   if constexpr (Neural) {
-    const float in[5] = {v.s[0] / 3.f, v.s[1] / 3.f, g[14], g[15], g[16]};
+    float hidden[6];
 #pragma unroll
     for (int h = 0; h < 6; ++h) {
-      float z = a[30 + h];
-#pragma unroll
-      for (int k = 0; k < 5; ++k) z += a[h * 5 + k] * in[k];
-      pre[h] = z;
-      hidden[h] = sinf(30.f * z);
+      const float z = r[NeuralRow::ZC + h] + r[NeuralRow::U + h] * s[0] + r[NeuralRow::V + h] * s[1];
+      const float t = fract(z * kSirenRevolutions);
+      hidden[h] = sin_rev(t);
+      a.sn[h] = hidden[h];
+      if constexpr (Backward) a.c[h] = cos_rev(t);
     }
 #pragma unroll
     for (int c = 0; c < 3; ++c) {
-      float z = a[54 + c];
+      float z = r[NeuralRow::B2 + c];
 #pragma unroll
-      for (int h = 0; h < 6; ++h) z += a[36 + c * 6 + h] * hidden[h];
-      color[c] = 1.f / (1.f + expf(-z));
+      for (int h = 0; h < 6; ++h) z += r[NeuralRow::W2 + c * 6 + h] * hidden[h];
+      a.color[c] = rcp(1.f + __builtin_amdgcn_exp2f(-z * kLog2e));
     }
   } else {
-    float h1 = 0.f, h2 = 0.f;
+    float S = 0.f;
 #pragma unroll
     for (int f = 0; f < 4; ++f) {
-      const float dot = kDirX[f] * v.s[0] + kDirY[f] * v.s[1];
-      const float wave = cosf(2.f * kPi * a[10 + f] * dot + a[14 + f]);
-      h1 += a[6 + f] * 0.5f * (1.f + wave);
-      h2 += a[6 + f] * 0.5f * (1.f - wave);
+      const float t = fract(r[ClassicRow::A + f] * s[0] + r[ClassicRow::B + f] * s[1] +
+                            r[ClassicRow::C + f]);
+      a.c[f] = cos_rev(t);
+      if constexpr (Backward) a.sn[f] = sin_rev(t);
+      S += r[ClassicRow::HW + f] * a.c[f];
     }
+    a.S = S;
 #pragma unroll
-    for (int c = 0; c < 3; ++c) color[c] = h1 * a[c] + h2 * a[3 + c];
+    for (int c = 0; c < 3; ++c)
+      a.color[c] = r[ClassicRow::HALF_W] * r[ClassicRow::SUM + c] + S * r[ClassicRow::DIFF + c];
   }
 }
 
-// Gather `count` records (list positions first, first+step, ...) into LDS.
+// Stage `count` records (list positions first, first + step, ...): gather
+// the raw fields into LDS with every thread, then derive each row's
+// constants with one thread per record.
 template <bool Neural>
-__device__ __forceinline__ void load_batch(float* rows, int* ids, int64_t* prims, int first,
-                                           int step, int count, const int* point_list,
-                                           const int64_t* primitive_ids, const float* geometry,
-                                           const float* appearance, const float* opacities) {
+__device__ __forceinline__ void load_batch(float* rows, float* raw, int* ids, int64_t* prims,
+                                           int first, int step, int count,
+                                           const int* point_list, const int64_t* primitive_ids,
+                                           const float* geometry, const float* appearance,
+                                           const float* opacities) {
   using L = Layout<Neural>;
   const int t = threadIdx.x;
   if (t < count) {
@@ -131,18 +192,66 @@ __device__ __forceinline__ void load_batch(float* rows, int* ids, int64_t* prims
     prims[t] = primitive_ids[id];
   }
   __syncthreads();
-  for (int idx = t; idx < count * L::RS; idx += kTilePixels) {
-    const int j = idx / L::RS;
-    const int f = idx - j * L::RS;
+  for (int idx = t; idx < count * L::RAW_STRIDE; idx += kTilePixels) {
+    const int j = idx / L::RAW_STRIDE;
+    const int f = idx - j * L::RAW_STRIDE;
     float value = 0.f;
     if (f < kGeometry) {
       value = geometry[int64_t(ids[j]) * kGeometry + f];
-    } else if (f == L::OP) {
+    } else if (f == kGeometry) {
       value = opacities[prims[j]];
-    } else if (f - L::AP < L::A) {
-      value = appearance[prims[j] * L::A + (f - L::AP)];
+    } else if (f - kGeometry - 1 < L::A) {
+      value = appearance[prims[j] * L::A + (f - kGeometry - 1)];
     }
-    rows[idx] = value;
+    raw[idx] = value;
+  }
+  __syncthreads();
+  if (t < count) {
+    const float* g = raw + t * L::RAW_STRIDE;
+    const float opacity = g[kGeometry];
+    const float* a = g + kGeometry + 1;
+    float* r = rows + t * L::STRIDE;
+#pragma unroll
+    for (int i = 0; i < 14; ++i) r[i] = g[i];
+    if constexpr (Neural) {
+      using R = NeuralRow;
+#pragma unroll
+      for (int i = 0; i < 3; ++i) r[R::DIR + i] = g[14 + i];
+      r[R::OP] = opacity;
+      r[R::THR] = reject_threshold(opacity);
+#pragma unroll
+      for (int h = 0; h < 6; ++h) {
+        const float* w1 = a + h * 5;
+        r[R::ZC + h] = a[30 + h] + w1[2] * g[14] + w1[3] * g[15] + w1[4] * g[16];
+        r[R::U + h] = w1[0] / 3.f;
+        r[R::V + h] = w1[1] / 3.f;
+#pragma unroll
+        for (int k = 0; k < 3; ++k) r[R::WDIR + h * 3 + k] = w1[2 + k];
+      }
+#pragma unroll
+      for (int i = 0; i < 18; ++i) r[R::W2 + i] = a[36 + i];
+#pragma unroll
+      for (int i = 0; i < 3; ++i) r[R::B2 + i] = a[54 + i];
+    } else {
+      using R = ClassicRow;
+      r[R::OP] = opacity;
+      r[R::THR] = reject_threshold(opacity);
+      float half_w = 0.f;
+#pragma unroll
+      for (int f = 0; f < 4; ++f) {
+        r[R::A + f] = a[10 + f] * kDirX[f];
+        r[R::B + f] = a[10 + f] * kDirY[f];
+        r[R::C + f] = a[14 + f] * kInvTwoPi;
+        r[R::HW + f] = 0.5f * a[6 + f];
+        half_w += 0.5f * a[6 + f];
+      }
+      r[R::HALF_W] = half_w;
+#pragma unroll
+      for (int c = 0; c < 3; ++c) {
+        r[R::SUM + c] = a[c] + a[3 + c];
+        r[R::DIFF + c] = a[c] - a[3 + c];
+      }
+    }
   }
   __syncthreads();
 }
@@ -175,7 +284,8 @@ __global__ __launch_bounds__(kTilePixels) void render_forward_kernel(
     float far_plane, float* __restrict__ maps, float* __restrict__ state,
     int* __restrict__ contributors) {
   using L = Layout<Neural>;
-  __shared__ __align__(16) float rows[kBatch * L::RS];
+  __shared__ __align__(16) float rows[kBatch * L::STRIDE];
+  __shared__ __align__(16) float raw[kBatch * L::RAW_STRIDE];
   __shared__ int ids[kBatch];
   __shared__ int64_t prims[kBatch];
   const int tile = blockIdx.x;
@@ -189,28 +299,29 @@ __global__ __launch_bounds__(kTilePixels) void render_forward_kernel(
   int last = 0;
   const int2 range = ranges[tile];
   const float mscale = far_plane / (far_plane - near_plane);
+  const float mnear = mscale * near_plane;
   for (int start = range.x; start < range.y; start += kBatch) {
     if (__syncthreads_count(done) == kTilePixels) break;
     const int count = min(kBatch, range.y - start);
-    load_batch<Neural>(rows, ids, prims, start, 1, count, point_list, primitive_ids, geometry,
-                       appearance, opacities);
+    load_batch<Neural>(rows, raw, ids, prims, start, 1, count, point_list, primitive_ids,
+                       geometry, appearance, opacities);
     for (int j = 0; j < count && !done; ++j) {
-      const float* g = rows + j * L::RS;
+      const float* r = rows + j * L::STRIDE;
       Sample v;
-      if (!sample_surface<Neural>(g, g[L::OP], x, y, near_plane, v)) continue;
+      if (!sample_surface<Neural>(r, x, y, near_plane, v)) continue;
       const float next = T * (1.f - v.alpha);
       if (next < 0.0001f) {
         done = true;
         break;
       }
-      float color[3], hidden[6], pre[6];
-      appearance_forward<Neural>(g + L::AP, g, v, color, hidden, pre);
+      Shade a;
+      shade<Neural, false>(r, v.s, a);
       const float w = T * v.alpha;
-      const float m = mscale * (1.f - near_plane / v.depth);
+      const float m = mscale - mnear * rcp(v.depth);
 #pragma unroll
       for (int c = 0; c < 3; ++c) {
-        out[c] += w * color[c];
-        out[5 + c] += w * g[11 + c];
+        out[c] += w * a.color[c];
+        out[5 + c] += w * r[11 + c];
       }
       out[4] += w * v.depth;
       out[8] += w * (m * m * (1.f - T) + m2 - 2.f * m * m1);
@@ -233,63 +344,65 @@ __global__ __launch_bounds__(kTilePixels) void render_forward_kernel(
   }
 }
 
-// Appearance adjoint. Classic writes 18 gradients into ga and (u,v)
-// gradients into gs; neural writes 57 into ga, (u,v) into gs and the
-// direction gradients into gdir.
+// Appearance adjoint given dL/dcolor = gc. Writes the raw appearance
+// gradients into ga (classic 18, neural 57), accumulates d/d(u, v) into gs
+// and, for neural, d/d(direction) into gdir.
 template <bool Neural>
-__device__ __forceinline__ void appearance_backward(const float* a, const float* g,
-                                                    const Sample& v, const float* color,
-                                                    const float* hidden, const float* pre,
-                                                    const float* gc, float* ga, float* gs,
-                                                    float* gdir) {
+__device__ __forceinline__ void shade_backward(const float* r, const float* s, const Shade& a,
+                                               const float* gc, float* ga, float* gs,
+                                               float* gdir) {
   if constexpr (Neural) {
-    const float in[5] = {v.s[0] / 3.f, v.s[1] / 3.f, g[14], g[15], g[16]};
+    using R = NeuralRow;
     float gh[6] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int c = 0; c < 3; ++c) {
-      const float gz = gc[c] * color[c] * (1.f - color[c]);
+      const float gz = gc[c] * a.color[c] * (1.f - a.color[c]);
       ga[54 + c] = gz;
 #pragma unroll
       for (int h = 0; h < 6; ++h) {
-        ga[36 + c * 6 + h] = gz * hidden[h];
-        gh[h] += gz * a[36 + c * 6 + h];
+        ga[36 + c * 6 + h] = gz * a.sn[h];
+        gh[h] += gz * r[R::W2 + c * 6 + h];
       }
     }
-    float gi[5] = {0.f, 0.f, 0.f, 0.f, 0.f};
+    const float in0 = s[0] / 3.f, in1 = s[1] / 3.f;
 #pragma unroll
     for (int h = 0; h < 6; ++h) {
-      const float gz = gh[h] * 30.f * cosf(30.f * pre[h]);
+      const float gz = gh[h] * 30.f * a.c[h];
       ga[30 + h] = gz;
+      ga[h * 5 + 0] = gz * in0;
+      ga[h * 5 + 1] = gz * in1;
+      ga[h * 5 + 2] = gz * r[R::DIR + 0];
+      ga[h * 5 + 3] = gz * r[R::DIR + 1];
+      ga[h * 5 + 4] = gz * r[R::DIR + 2];
+      gs[0] += gz * r[R::U + h];
+      gs[1] += gz * r[R::V + h];
 #pragma unroll
-      for (int k = 0; k < 5; ++k) {
-        ga[h * 5 + k] = gz * in[k];
-        gi[k] += gz * a[h * 5 + k];
-      }
+      for (int k = 0; k < 3; ++k) gdir[k] += gz * r[R::WDIR + h * 3 + k];
     }
-    gs[0] += gi[0] / 3.f;
-    gs[1] += gi[1] / 3.f;
-#pragma unroll
-    for (int k = 0; k < 3; ++k) gdir[k] += gi[2 + k];
   } else {
+    using R = ClassicRow;
+    float g_sum = 0.f, g_diff = 0.f;
+#pragma unroll
+    for (int c = 0; c < 3; ++c) {
+      g_sum += gc[c] * r[R::SUM + c];
+      g_diff += gc[c] * r[R::DIFF + c];
+    }
+    const float h1 = r[R::HALF_W] + a.S, h2 = r[R::HALF_W] - a.S;
+#pragma unroll
+    for (int c = 0; c < 3; ++c) {
+      ga[c] = gc[c] * h1;
+      ga[3 + c] = gc[c] * h2;
+    }
 #pragma unroll
     for (int f = 0; f < 4; ++f) {
-      const float dot = kDirX[f] * v.s[0] + kDirY[f] * v.s[1];
-      const float angle = 2.f * kPi * a[10 + f] * dot + a[14 + f];
-      float sn, cs;
-      sincosf(angle, &sn, &cs);
-      float gw = 0.f, gt = 0.f;
-#pragma unroll
-      for (int c = 0; c < 3; ++c) {
-        ga[c] += gc[c] * a[6 + f] * 0.5f * (1.f + cs);
-        ga[3 + c] += gc[c] * a[6 + f] * 0.5f * (1.f - cs);
-        gw += gc[c] * 0.5f * ((1.f + cs) * a[c] + (1.f - cs) * a[3 + c]);
-        gt += gc[c] * a[6 + f] * 0.5f * sn * (a[3 + c] - a[c]);
-      }
-      ga[6 + f] += gw;
-      ga[10 + f] += gt * 2.f * kPi * dot;
-      ga[14 + f] += gt;
-      gs[0] += gt * 2.f * kPi * a[10 + f] * kDirX[f];
-      gs[1] += gt * 2.f * kPi * a[10 + f] * kDirY[f];
+      // colour_c = h1 c1_c + h2 c2_c with h1/h2 = sum_f w_f (1 +/- cos_f) / 2.
+      ga[6 + f] = 0.5f * (g_sum + a.c[f] * g_diff);
+      const float gt = -r[R::HW + f] * a.sn[f] * g_diff;  // d/d(phase_f)
+      const float dot = kDirX[f] * s[0] + kDirY[f] * s[1];
+      ga[10 + f] = gt * kTwoPi * dot;
+      ga[14 + f] = gt;
+      gs[0] += gt * kTwoPi * r[R::A + f];
+      gs[1] += gt * kTwoPi * r[R::B + f];
     }
   }
 }
@@ -306,7 +419,10 @@ __global__ __launch_bounds__(kTilePixels) void render_backward_kernel(
     float* __restrict__ grad_opacities, float* __restrict__ grad_backgrounds) {
   using L = Layout<Neural>;
   constexpr int NP = L::NP;
-  __shared__ __align__(16) float rows[kBatch * L::RS];
+  constexpr int NG = L::NG;
+  constexpr int OP = Neural ? NeuralRow::OP : ClassicRow::OP;
+  __shared__ __align__(16) float rows[kBatch * L::STRIDE];
+  __shared__ __align__(16) float raw[kBatch * L::RAW_STRIDE];
   __shared__ float acc[kBatch * NP];
   __shared__ int ids[kBatch];
   __shared__ int64_t prims[kBatch];
@@ -334,6 +450,8 @@ __global__ __launch_bounds__(kTilePixels) void render_backward_kernel(
   float background_dot = 0.f;
 #pragma unroll
   for (int c = 0; c < 3; ++c) background_dot += go[c] * backgrounds[tp.image * 3 + c];
+  // dL/dalpha_i picks up final_t (go_alpha - background . go_rgb) / (1 - alpha_i).
+  const float final_term = final_t * (go[3] - background_dot);
   __syncthreads();
   // Background gradient: sum over the tile of final T * dL/drgb.
   {
@@ -345,74 +463,81 @@ __global__ __launch_bounds__(kTilePixels) void render_backward_kernel(
   const int block_last = max(max(wave_last[0], wave_last[1]), max(wave_last[2], wave_last[3]));
   const int2 range = ranges[tile];
   const float mscale = far_plane / (far_plane - near_plane);
+  const float mnear = mscale * near_plane;
   float suffix = 0.f;
 
   for (int start = block_last; start > 0; start -= kBatch) {
     const int count = min(kBatch, start);
-    load_batch<Neural>(rows, ids, prims, range.x + start - 1, -1, count, point_list,
+    load_batch<Neural>(rows, raw, ids, prims, range.x + start - 1, -1, count, point_list,
                        primitive_ids, geometry, appearance, opacities);
     for (int j = 0; j < count; ++j) {
-      const float* g = rows + j * L::RS;
-      const float opacity = g[L::OP];
+      const float* r = rows + j * L::STRIDE;
       Sample v;
       bool active = tp.inside && (start - j) <= last;
-      if (active) active = sample_surface<Neural>(g, opacity, x, y, near_plane, v);
+      if (active) active = sample_surface<Neural>(r, x, y, near_plane, v);
       if (!__any(active)) continue;
-      float grad[NP];  // geometry 17 | appearance A | opacity
+      float grad[NP];  // geometry NG | appearance A | opacity
 #pragma unroll
       for (int k = 0; k < NP; ++k) grad[k] = 0.f;
       if (active) {
         float* gg = grad;
-        float* ga = grad + kGeometry;
-        T /= 1.f - v.alpha;
+        float* ga = grad + NG;
+        const float inv_keep = rcp(1.f - v.alpha);
+        T *= inv_keep;
         const float w = T * v.alpha;
-        float color[3], hidden[6], pre[6];
-        appearance_forward<Neural>(g + L::AP, g, v, color, hidden, pre);
-        const float m = mscale * (1.f - near_plane / v.depth);
+        Shade a;
+        shade<Neural, true>(r, v.s, a);
+        const float inv_depth = rcp(v.depth);
+        const float m = mscale - mnear * inv_depth;
         float gw = go[4] * v.depth + go[8] * (m * m * total_a + m2 - 2.f * m * m1);
         float gc[3];
 #pragma unroll
         for (int c = 0; c < 3; ++c) {
-          gw += go[c] * color[c] + go[5 + c] * g[11 + c];
+          gw += go[c] * a.color[c] + go[5 + c] * r[11 + c];
           gc[c] = w * go[c];
-          gg[11 + c] += w * go[5 + c];
+          gg[11 + c] = w * go[5 + c];
         }
-        const float one_minus = 1.f - v.alpha;
-        const float galpha =
-            T * gw - suffix / one_minus + final_t * (go[3] - background_dot) / one_minus;
+        const float galpha = T * gw + (final_term - suffix) * inv_keep;
         suffix += w * gw;
         float gs[2] = {0.f, 0.f};
-        appearance_backward<Neural>(g + L::AP, g, v, color, hidden, pre, gc, ga, gs, gg + 14);
-        const float gz = w * go[4] + go[8] * 2.f * w * (m * total_a - m1) * mscale * near_plane /
-                                         (v.depth * v.depth);
-        if (Neural || v.surface) {
-          gs[0] += gz * g[6];
-          gs[1] += gz * g[7];
-          gg[6] += gz * v.s[0];
-          gg[7] += gz * v.s[1];
+        float gdir[3] = {0.f, 0.f, 0.f};
+        shade_backward<Neural>(r, v.s, a, gc, ga, gs, gdir);
+        if constexpr (Neural) {
+#pragma unroll
+          for (int k = 0; k < 3; ++k) gg[14 + k] = gdir[k];
         }
-        gg[8] += gz;
+        const float gz = w * go[4] + go[8] * 2.f * w * (m * total_a - m1) * mnear *
+                                         (inv_depth * inv_depth);
+        if (Neural || v.surface) {
+          gs[0] += gz * r[6];
+          gs[1] += gz * r[7];
+          gg[6] = gz * v.s[0];
+          gg[7] = gz * v.s[1];
+        }
+        gg[8] = gz;
         float grho = 0.f;
-        if (opacity * v.e < 0.99f) {
+        if (r[OP] * v.e < 0.99f) {
           grad[NP - 1] = galpha * v.e;
-          grho = -0.5f * galpha * opacity * v.e;
+          grho = -0.5f * galpha * r[OP] * v.e;
         }
         if (v.surface) {
           gs[0] += 2.f * v.s[0] * grho;
           gs[1] += 2.f * v.s[1] * grho;
         } else {
-          gg[9] += 4.f * (g[9] - x) * grho;
-          gg[10] += 4.f * (g[10] - y) * grho;
+          gg[9] = 4.f * (r[9] - x) * grho;
+          gg[10] = 4.f * (r[10] - y) * grho;
         }
-        const float gp[3] = {gs[0] / v.p[2], gs[1] / v.p[2],
-                             -(gs[0] * v.s[0] + gs[1] * v.s[1]) / v.p[2]};
-        float gk[3], gl[3];
-        cross3(v.l, gp, gk);
-        cross3(gp, v.k, gl);
+        const float gp[3] = {gs[0] * v.inv_pz, gs[1] * v.inv_pz,
+                             -(gs[0] * v.s[0] + gs[1] * v.s[1]) * v.inv_pz};
+        // p = k x l  =>  dk = l x gp, dl = gp x k.
+        const float gk[3] = {v.l[1] * gp[2] - v.l[2] * gp[1], v.l[2] * gp[0] - v.l[0] * gp[2],
+                             v.l[0] * gp[1] - v.l[1] * gp[0]};
+        const float gl[3] = {gp[1] * v.k[2] - gp[2] * v.k[1], gp[2] * v.k[0] - gp[0] * v.k[2],
+                             gp[0] * v.k[1] - gp[1] * v.k[0]};
 #pragma unroll
         for (int k = 0; k < 3; ++k) {
-          gg[k] -= gk[k];
-          gg[3 + k] -= gl[k];
+          gg[k] = -gk[k];
+          gg[3 + k] = -gl[k];
           gg[6 + k] += x * gk[k] + y * gl[k];
         }
       }
@@ -444,10 +569,10 @@ __global__ __launch_bounds__(kTilePixels) void render_backward_kernel(
       if (value != 0.f) {
         const int j = idx / NP;
         const int p = idx - j * NP;
-        if (p < kGeometry) {
+        if (p < NG) {
           atomicAdd(grad_geometry + int64_t(ids[j]) * kGeometry + p, value);
-        } else if (p < kGeometry + L::A) {
-          atomicAdd(grad_appearance + prims[j] * L::A + (p - kGeometry), value);
+        } else if (p < NG + L::A) {
+          atomicAdd(grad_appearance + prims[j] * L::A + (p - NG), value);
         } else {
           atomicAdd(grad_opacities + prims[j], value);
         }
