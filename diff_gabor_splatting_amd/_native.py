@@ -47,7 +47,18 @@ _SIGNATURES = {
     "gs_sh_forward": (_c_int, [_c_ptr] * 4 + [_c_i64] * 3 + [_c_int, _c_ptr]),
     "gs_sh_backward": (_c_int, [_c_ptr] * 7 + [_c_i64] * 3 + [_c_int, _c_ptr]),
     "gs_scan_workspace_size": (_c_size, [_c_i64]),
-    "gs_pack_visible": (_c_int, [_c_ptr, _c_i64, _c_ptr, _c_ptr, _c_ptr, _c_size, _c_ptr]),
+    "gs_pack_visible": (_c_int, [_c_ptr, _c_i64, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_size, _c_ptr]),
+    "gs_records_forward": (
+        _c_int,
+        [_c_ptr] * 11
+        + [_c_int, _c_i64, _c_i64, _c_i64, _c_int, _c_int, _c_float, _c_float]
+        + [_c_ptr] * 10,
+    ),
+    "gs_records_backward_workspace_size": (_c_size, [_c_i64, _c_i64, _c_i64, _c_int]),
+    "gs_records_backward": (
+        _c_int,
+        [_c_ptr] * 7 + [_c_int, _c_i64, _c_i64, _c_i64] + [_c_ptr] * 18 + [_c_size, _c_ptr],
+    ),
     "gs_count_tiles": (
         _c_int,
         [_c_ptr, _c_ptr, _c_i64, _c_int, _c_int, _c_ptr, _c_ptr, _c_size, _c_ptr],
@@ -263,21 +274,139 @@ def find_ranges(sorted_keys: torch.Tensor, tiles: int) -> torch.Tensor:
     return ranges
 
 
-def pack_visible(radii: torch.Tensor) -> torch.Tensor:
-    """Ascending indices of pairs with radii > 0 (int64). Synchronises once."""
+def pack_visible(radii: torch.Tensor, with_rows: bool = False):
+    """Ascending indices of pairs with radii > 0 (int64). Synchronises once.
+
+    With ``with_rows`` also returns row_of_pair (int32, the packed row of
+    every pair or -1)."""
     device = radii.device
     flat = radii.reshape(-1)
     count = flat.numel()
     selected = torch.empty(max(count, 1), dtype=torch.int64, device=device)
+    rows = torch.empty(max(count, 1), dtype=torch.int32, device=device) if with_rows else None
     total = torch.empty(1, dtype=torch.int64, device=device)
     workspace = _workspace(lib.gs_scan_workspace_size(count), device)
     _check(
         lib.gs_pack_visible(
-            _ptr(flat), count, _ptr(selected), _ptr(total), _ptr(workspace), workspace.numel(),
-            _stream(device),
+            _ptr(flat), count, _ptr(selected), _ptr(rows), _ptr(total), _ptr(workspace),
+            workspace.numel(), _stream(device),
         )
     )
-    return selected[: int(total.item())]
+    selected = selected[: int(total.item())]
+    return (selected, rows[:count]) if with_rows else selected
+
+
+# --------------------------------------------------------------------------
+# Fused projection + SH + record assembly (the renderer's front end).
+
+
+def records_forward(means, quaternions, scales, opacities, view_matrices, intrinsics, sh,
+                    shared, sh_degree, width, height, near_plane, far_plane, packed):
+    """Compositor rows for every visible (packed) or every (dense) pair.
+
+    means/quaternions/scales [S,N,*], view_matrices [S,C,4,4], intrinsics
+    [S,C,3,3]; with SH (sh_degree >= 0) also opacities [S,N], sh = (first,
+    second) [S,N,K,3] and shared = (weights, magnitudes, phases) [S,N,4].
+    Returns a dict of geometry [Q,17], projected_means [Q,2], row_radii [Q],
+    primitive_ids [Q], image_ids [Q], dense_radii [S,C,N], row_of_pair
+    ([S*C*N] int32 or None) and selected (packed pair indices or None), plus
+    appearance [Q,18] and opacity_rows [Q] with SH.
+    """
+    device = means.device
+    scenes, n = means.shape[:2]
+    cameras = view_matrices.shape[1]
+    pairs = scenes * cameras * n
+    first, second = sh if sh is not None else (None, None)
+    weights, magnitudes, phases = shared if shared is not None else (None, None, None)
+    degree = -1 if sh_degree is None else int(sh_degree)
+
+    def launch(row_of_pair, dense_radii, out):
+        _check(
+            lib.gs_records_forward(
+                _ptr(means), _ptr(quaternions), _ptr(scales), _ptr(opacities),
+                _ptr(view_matrices), _ptr(intrinsics), _ptr(first), _ptr(second),
+                _ptr(weights), _ptr(magnitudes), _ptr(phases), degree, scenes, cameras, n,
+                width, height, near_plane, far_plane, _ptr(row_of_pair), _ptr(dense_radii),
+                _ptr(out.get("geometry")), _ptr(out.get("projected_means")),
+                _ptr(out.get("row_radii")), _ptr(out.get("primitive_ids")),
+                _ptr(out.get("image_ids")), _ptr(out.get("appearance")),
+                _ptr(out.get("opacity_rows")), _stream(device),
+            )
+        )
+
+    with torch.cuda.device(device):
+        dense_radii = torch.empty((scenes, cameras, n), dtype=torch.int32, device=device)
+        row_of_pair = selected = None
+        if packed:
+            launch(None, dense_radii, {})
+            selected, row_of_pair = pack_visible(dense_radii, with_rows=True)
+            rows = selected.numel()
+        else:
+            rows = pairs
+        f32 = dict(dtype=torch.float32, device=device)
+        out = {
+            "geometry": torch.empty((rows, GEOMETRY_SIZE), **f32),
+            "projected_means": torch.empty((rows, 2), **f32),
+            "row_radii": torch.empty(rows, dtype=torch.int32, device=device),
+            "primitive_ids": torch.empty(rows, dtype=torch.int64, device=device),
+            "image_ids": torch.empty(rows, dtype=torch.int64, device=device),
+        }
+        if degree >= 0:
+            out["appearance"] = torch.empty((rows, 18), **f32)
+            out["opacity_rows"] = torch.empty(rows, **f32)
+        if rows:
+            launch(row_of_pair, None if packed else dense_radii, out)
+    out.update(dense_radii=dense_radii, row_of_pair=row_of_pair, selected=selected)
+    return out
+
+
+def records_backward(means, quaternions, scales, view_matrices, intrinsics, sh, sh_degree,
+                     row_of_pair, geometry, grad_geometry, grad_projected_means,
+                     grad_appearance, grad_opacity_rows):
+    """Gradients of (means, quaternions, scales, view_matrices, intrinsics) and,
+    with SH, of (first, second, weights, magnitudes, phases, opacities)."""
+    device = means.device
+    scenes, n = means.shape[:2]
+    cameras = view_matrices.shape[1]
+    degree = -1 if sh_degree is None else int(sh_degree)
+    first, second = sh if sh is not None else (None, None)
+
+    def contiguous(value):
+        return None if value is None else value.contiguous()
+
+    grad_geometry = contiguous(grad_geometry)
+    grad_projected_means = contiguous(grad_projected_means)
+    grad_appearance = contiguous(grad_appearance)
+    grad_opacity_rows = contiguous(grad_opacity_rows)
+    with torch.cuda.device(device):
+        g_means = torch.empty_like(means)
+        g_quats = torch.empty_like(quaternions)
+        g_scales = torch.empty_like(scales)
+        g_views = torch.empty_like(view_matrices)
+        g_intrinsics = torch.empty_like(intrinsics)
+        sh_grads = [None] * 6
+        if degree >= 0:
+            if grad_appearance is None:
+                grad_appearance = torch.zeros((geometry.shape[0], 18), dtype=torch.float32,
+                                              device=device)
+            sh_grads = [torch.empty_like(first), torch.empty_like(second)] + [
+                torch.empty((scenes, n, 4), dtype=torch.float32, device=device) for _ in range(3)
+            ] + [torch.empty((scenes, n), dtype=torch.float32, device=device)]
+        workspace = _workspace(
+            lib.gs_records_backward_workspace_size(scenes, cameras, n, degree), device
+        )
+        _check(
+            lib.gs_records_backward(
+                _ptr(means), _ptr(quaternions), _ptr(scales), _ptr(view_matrices),
+                _ptr(intrinsics), _ptr(first), _ptr(second), degree, scenes, cameras, n,
+                _ptr(row_of_pair), _ptr(geometry), _ptr(grad_geometry),
+                _ptr(grad_projected_means), _ptr(grad_appearance), _ptr(grad_opacity_rows),
+                _ptr(g_means), _ptr(g_quats), _ptr(g_scales), _ptr(g_views), _ptr(g_intrinsics),
+                *(_ptr(t) for t in sh_grads), _ptr(workspace), workspace.numel(),
+                _stream(device),
+            )
+        )
+    return (g_means, g_quats, g_scales, g_views, g_intrinsics, *sh_grads)
 
 
 # --------------------------------------------------------------------------

@@ -63,10 +63,12 @@ struct VisibleLoad {
 
 struct SelectStore {
   int64_t* selected;
+  int* row_of_pair;  // optional inverse map: row of pair i, or -1
   int64_t* num_selected;
   int64_t count;
   __device__ void operator()(int64_t i, int64_t inclusive, int64_t flag) const {
     if (flag) selected[inclusive - 1] = i;
+    if (row_of_pair) row_of_pair[i] = flag ? int(inclusive - 1) : -1;
     if (i == count - 1) *num_selected = inclusive;
   }
 };
@@ -134,11 +136,11 @@ size_t gs_scan_workspace_size(int64_t count) {
 }
 
 int gs_pack_visible(const int32_t* radii, int64_t count, int64_t* selected,
-                    int64_t* num_selected, void* workspace, size_t workspace_bytes,
-                    void* stream) {
+                    int32_t* row_of_pair, int64_t* num_selected, void* workspace,
+                    size_t workspace_bytes, void* stream) {
   using namespace gs;
   clear_error();
-  GS_REQUIRE(count >= 0, GS_ERR_ARGUMENT, "negative count");
+  GS_REQUIRE(count >= 0 && count <= INT_MAX, GS_ERR_OVERFLOW, "too many pairs to pack");
   GS_REQUIRE(num_selected, GS_ERR_ARGUMENT, "null num_selected");
   hipStream_t s = static_cast<hipStream_t>(stream);
   ProfileScope prof(GS_PROF_BINNING, s);
@@ -151,7 +153,8 @@ int gs_pack_visible(const int32_t* radii, int64_t count, int64_t* selected,
   const size_t need = gs_scan_workspace_size(count);
   GS_REQUIRE(workspace && workspace_bytes >= need, GS_ERR_WORKSPACE,
              "packing needs %zu workspace bytes, got %zu", need, workspace_bytes);
-  return run_scan<int64_t>(count, VisibleLoad{radii}, SelectStore{selected, num_selected, count},
+  return run_scan<int64_t>(count, VisibleLoad{radii},
+                           SelectStore{selected, row_of_pair, num_selected, count},
                            static_cast<int64_t*>(workspace), s);
 }
 

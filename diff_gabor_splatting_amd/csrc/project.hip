@@ -1,11 +1,9 @@
-// Kernel 1: per-(scene, camera, surfel) projection and its adjoint.
+// Kernel 1: dense per-(scene, camera, surfel) projection and its adjoint.
 //
-// Forward follows the reference's PyTorch projection
-// (src/gabor_splatting/rendering.py:156-218): a surfel with unit wxyz
-// quaternion q, tangent scales (su, sv) and mean mu maps its local scaled
-// plane to pixels through T = K [Rc R[:,0] su, Rc R[:,1] sv, Rc mu + t].
-// The conic centre and three-sigma extent follow the upstream bound with
-// f = [9, 9, -1] / sum([9, 9, -1] * T[2,:]^2).
+// The C-ABI twin of the reference's PyTorch projection (src/gabor_splatting/
+// rendering.py:176-218): separate transform / xy / normal / direction /
+// radius arrays of shape [S, C, N, *]. The renderer itself uses the fused
+// record kernels in records.hip, which share this math (projection.hpp).
 //
 // One thread owns one (scene, surfel) and loops over the cameras of its
 // scene: surfel parameters are read once, camera parameters are uniform per
@@ -13,136 +11,18 @@
 // in registers (no atomics). Per-camera gradients (view and intrinsics) are
 // reduced per workgroup with the wave64 reduce-scatter and summed across
 // workgroups by a second deterministic kernel.
-#include <cmath>
-
-#include "common.hpp"
-#include "wave.hpp"
+#include "projection.hpp"
 
 namespace gs {
 namespace {
 
-constexpr int kBlock = 256;
-constexpr int kCameraGrads = 21;  // 9 rotation + 3 translation + 9 intrinsics
-
-__device__ __forceinline__ float nan_max(float a, float b) {
-  // torch.maximum / amax propagate NaN, fmaxf does not.
-  if (a != a) return a;
-  if (b != b) return b;
-  return a > b ? a : b;
-}
-
-__device__ __forceinline__ void quaternion_rotation(float w, float x, float y, float z,
-                                                    float R[9]) {
-  R[0] = 1.f - 2.f * (y * y + z * z);
-  R[1] = 2.f * (x * y - w * z);
-  R[2] = 2.f * (x * z + w * y);
-  R[3] = 2.f * (x * y + w * z);
-  R[4] = 1.f - 2.f * (x * x + z * z);
-  R[5] = 2.f * (y * z - w * x);
-  R[6] = 2.f * (x * z - w * y);
-  R[7] = 2.f * (y * z + w * x);
-  R[8] = 1.f - 2.f * (x * x + y * y);
-}
-
-// Quantities shared by forward and adjoint for one (surfel, camera).
-struct Projection {
-  float P[9];   // plane [Rc tu su | Rc tv sv | Rc mu + t], row-major
-  float T[9];   // K P
-  float D;      // conic denominator
-  bool valid;   // D != 0
-  float f[3];   // [9, 9, -1] / D (or / 1 when invalid)
-  float xy[2];
-  float nraw[3];  // Rc R[:,2] before facing flip
-  float facing;
-  float dvec[3];  // mu - camera centre
-  float dlen;
-};
-
-__device__ __forceinline__ void project_pair(const float R[9], const float mu[3],
-                                             const float sc[2], const float* V,
-                                             const float* K, Projection& p) {
-  float Rc[9], t[3];
-#pragma unroll
-  for (int i = 0; i < 3; ++i) {
-#pragma unroll
-    for (int j = 0; j < 3; ++j) Rc[i * 3 + j] = V[i * 4 + j];
-    t[i] = V[i * 4 + 3];
-  }
-  // Columns of the local plane in camera space.
-#pragma unroll
-  for (int i = 0; i < 3; ++i) {
-    float c0 = 0.f, c1 = 0.f, c2 = 0.f;
-#pragma unroll
-    for (int k = 0; k < 3; ++k) {
-      c0 += Rc[i * 3 + k] * (R[k * 3 + 0] * sc[0]);
-      c1 += Rc[i * 3 + k] * (R[k * 3 + 1] * sc[1]);
-      c2 += Rc[i * 3 + k] * mu[k];
-    }
-    p.P[i * 3 + 0] = c0;
-    p.P[i * 3 + 1] = c1;
-    p.P[i * 3 + 2] = c2 + t[i];
-  }
-#pragma unroll
-  for (int i = 0; i < 3; ++i)
-#pragma unroll
-    for (int j = 0; j < 3; ++j) {
-      float acc = 0.f;
-#pragma unroll
-      for (int k = 0; k < 3; ++k) acc += K[i * 3 + k] * p.P[k * 3 + j];
-      p.T[i * 3 + j] = acc;
-    }
-  const float tv[3] = {9.f, 9.f, -1.f};
-  p.D = tv[0] * p.T[6] * p.T[6] + tv[1] * p.T[7] * p.T[7] + tv[2] * p.T[8] * p.T[8];
-  p.valid = p.D != 0.f;
-  const float safe = p.valid ? p.D : 1.f;
-#pragma unroll
-  for (int k = 0; k < 3; ++k) p.f[k] = tv[k] / safe;
-#pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    float acc = 0.f;
-#pragma unroll
-    for (int k = 0; k < 3; ++k) acc += p.f[k] * p.T[i * 3 + k] * p.T[6 + k];
-    p.xy[i] = acc;
-  }
-  // Camera-space normal from the third rotation column.
-#pragma unroll
-  for (int i = 0; i < 3; ++i)
-    p.nraw[i] = Rc[i * 3 + 0] * R[2] + Rc[i * 3 + 1] * R[5] + Rc[i * 3 + 2] * R[8];
-  p.facing = -(p.P[2] * p.nraw[0] + p.P[5] * p.nraw[1] + p.P[8] * p.nraw[2]);
-  // World direction camera centre -> mean; centre = -Rc^T t.
-#pragma unroll
-  for (int i = 0; i < 3; ++i) {
-    const float centre = -(Rc[0 * 3 + i] * t[0] + Rc[1 * 3 + i] * t[1] + Rc[2 * 3 + i] * t[2]);
-    p.dvec[i] = mu[i] - centre;
-  }
-  p.dlen = sqrtf(p.dvec[0] * p.dvec[0] + p.dvec[1] * p.dvec[1] + p.dvec[2] * p.dvec[2]);
-}
-
-struct Surfel {
-  float mu[3], q[4], qn[4], qlen, sc[2], R[9];
-};
-
-__device__ __forceinline__ void load_surfel(const float* means, const float* quats,
-                                            const float* scales, int64_t i, Surfel& s) {
-#pragma unroll
-  for (int k = 0; k < 3; ++k) s.mu[k] = means[i * 3 + k];
-#pragma unroll
-  for (int k = 0; k < 4; ++k) s.q[k] = quats[i * 4 + k];
-  s.sc[0] = scales[i * 2 + 0];
-  s.sc[1] = scales[i * 2 + 1];
-  s.qlen = sqrtf(s.q[0] * s.q[0] + s.q[1] * s.q[1] + s.q[2] * s.q[2] + s.q[3] * s.q[3]);
-#pragma unroll
-  for (int k = 0; k < 4; ++k) s.qn[k] = s.q[k] / s.qlen;
-  quaternion_rotation(s.qn[0], s.qn[1], s.qn[2], s.qn[3], s.R);
-}
-
-__global__ __launch_bounds__(kBlock) void project_forward_kernel(
+__global__ __launch_bounds__(kProjectBlock) void project_forward_kernel(
     const float* __restrict__ means, const float* __restrict__ quats,
     const float* __restrict__ scales, const float* __restrict__ views,
     const float* __restrict__ intrinsics, int64_t cameras, int64_t n, int tw, int th,
     float near_plane, float far_plane, float* __restrict__ transform, float* __restrict__ xy,
     float* __restrict__ normals, float* __restrict__ directions, int* __restrict__ radii) {
-  const int64_t i = int64_t(blockIdx.x) * kBlock + threadIdx.x;
+  const int64_t i = int64_t(blockIdx.x) * kProjectBlock + threadIdx.x;
   const int64_t scene = blockIdx.y;
   if (i >= n) return;
   Surfel s;
@@ -156,274 +36,39 @@ __global__ __launch_bounds__(kBlock) void project_forward_kernel(
     for (int k = 0; k < 9; ++k) transform[pair * 9 + k] = p.T[k];
     xy[pair * 2 + 0] = p.xy[0];
     xy[pair * 2 + 1] = p.xy[1];
-    const float sign = p.facing > 0.f ? 1.f : -1.f;
+    const float sign = facing_sign(p);
 #pragma unroll
     for (int k = 0; k < 3; ++k) normals[pair * 3 + k] = p.nraw[k] * sign;
-    const float inv = 1.f / fmaxf(p.dlen, 1e-12f);
+    float d[3];
+    unit_direction(p, d);
 #pragma unroll
-    for (int k = 0; k < 3; ++k) directions[pair * 3 + k] = p.dvec[k] * inv;
-
-    // Integer screen radius and visibility (rendering.py:207-217).
-    float extent[2];
-#pragma unroll
-    for (int k = 0; k < 2; ++k) {
-      float sq = p.xy[k] * p.xy[k] -
-                 (p.f[0] * p.T[k * 3 + 0] * p.T[k * 3 + 0] +
-                  p.f[1] * p.T[k * 3 + 1] * p.T[k * 3 + 1] +
-                  p.f[2] * p.T[k * 3 + 2] * p.T[k * 3 + 2]);
-      sq = (sq != sq) ? sq : fmaxf(sq, 1e-4f);
-      extent[k] = sqrtf(sq);
-    }
-    const float radius = ceilf(nan_max(nan_max(extent[0], extent[1]), 2.121318f));
-    const float fx_tiles = float(tw), fy_tiles = float(th);
-    const float lx = fmaxf(truncf((p.xy[0] - radius) / 16.f), 0.f);
-    const float ly = fmaxf(truncf((p.xy[1] - radius) / 16.f), 0.f);
-    const float ux = fmaxf(truncf((p.xy[0] + radius + 15.f) / 16.f), 0.f);
-    const float uy = fmaxf(truncf((p.xy[1] + radius + 15.f) / 16.f), 0.f);
-    bool visible = p.valid && p.facing != 0.f && p.P[8] > near_plane && p.P[8] < far_plane;
-    visible = visible && isfinite(radius) && radius < 1073741824.f;
-    visible = visible && isfinite(p.xy[0]) && isfinite(p.xy[1]);
-    visible = visible && fminf(ux, fx_tiles) > fminf(lx, fx_tiles);
-    visible = visible && fminf(uy, fy_tiles) > fminf(ly, fy_tiles);
-    radii[pair] = visible ? int(radius) : 0;
+    for (int k = 0; k < 3; ++k) directions[pair * 3 + k] = d[k];
+    radii[pair] = screen_radius(p, tw, th, near_plane, far_plane);
   }
 }
 
-__global__ __launch_bounds__(kBlock) void project_backward_kernel(
-    const float* __restrict__ means, const float* __restrict__ quats,
-    const float* __restrict__ scales, const float* __restrict__ views,
-    const float* __restrict__ intrinsics, int64_t cameras, int64_t n,
-    const float* __restrict__ g_transform, const float* __restrict__ g_xy,
-    const float* __restrict__ g_normals, const float* __restrict__ g_dirs,
-    float* __restrict__ grad_means, float* __restrict__ grad_quats,
-    float* __restrict__ grad_scales, float* __restrict__ partials) {
-  __shared__ float wave_sums[kBlock / 64][kCameraGrads];
-  const int64_t i = int64_t(blockIdx.x) * kBlock + threadIdx.x;
-  const int64_t scene = blockIdx.y;
-  const bool valid = i < n;
-  const int lane = lane_id();
-  const int wave = threadIdx.x >> 6;
-  Surfel s;
-  if (valid) {
-    load_surfel(means, quats, scales, scene * n + i, s);
-  } else {
-    // Idle lanes still join the block reductions with zero gradients.
+// Output gradients held in separate dense [S, C, N, *] arrays (any may be null).
+struct DenseGrads {
+  const float* transform;
+  const float* xy;
+  const float* normals;
+  const float* directions;
+  __device__ bool fetch(int64_t pair, PairGrads& g) const {
 #pragma unroll
-    for (int k = 0; k < 3; ++k) s.mu[k] = 0.f;
-    s.q[0] = s.qn[0] = 1.f;
-    s.q[1] = s.q[2] = s.q[3] = s.qn[1] = s.qn[2] = s.qn[3] = 0.f;
-    s.qlen = 1.f;
-    s.sc[0] = s.sc[1] = 0.f;
-    quaternion_rotation(1.f, 0.f, 0.f, 0.f, s.R);
-  }
-  float gmu[3] = {0.f, 0.f, 0.f}, gR[9] = {}, gs[2] = {0.f, 0.f};
-
-  for (int64_t c = 0; c < cameras; ++c) {
-    const int64_t cam = scene * cameras + c;
-    const float* V = views + cam * 16;
-    const float* K = intrinsics + cam * 9;
-    float cam_grad[kCameraGrads];  // gRc[9], gt[3], gK[9]
+    for (int k = 0; k < 9; ++k) g.gT[k] = transform ? transform[pair * 9 + k] : 0.f;
+    g.has_xy = xy != nullptr;
+    g.has_n = normals != nullptr;
+    g.has_d = directions != nullptr;
 #pragma unroll
-    for (int k = 0; k < kCameraGrads; ++k) cam_grad[k] = 0.f;
-    if (valid) {
-      Projection p;
-      project_pair(s.R, s.mu, s.sc, V, K, p);
-      const int64_t pair = cam * n + i;
-      float Rc[9], t[3];
+    for (int k = 0; k < 2; ++k) g.gxy[k] = xy ? xy[pair * 2 + k] : 0.f;
 #pragma unroll
-      for (int a = 0; a < 3; ++a) {
-#pragma unroll
-        for (int b = 0; b < 3; ++b) Rc[a * 3 + b] = V[a * 4 + b];
-        t[a] = V[a * 4 + 3];
-      }
-      float gT[9];
-#pragma unroll
-      for (int k = 0; k < 9; ++k) gT[k] = g_transform ? g_transform[pair * 9 + k] : 0.f;
-      // Conic centre xy_i = sum_k f_k T_ik T_2k with f = tv / D.
-      if (g_xy) {
-        const float gx[2] = {g_xy[pair * 2 + 0], g_xy[pair * 2 + 1]};
-        const float tv[3] = {9.f, 9.f, -1.f};
-        float gf[3];
-#pragma unroll
-        for (int k = 0; k < 3; ++k) {
-          gf[k] = 0.f;
-#pragma unroll
-          for (int a = 0; a < 2; ++a) {
-            gT[a * 3 + k] += gx[a] * p.f[k] * p.T[6 + k];
-            gT[6 + k] += gx[a] * p.f[k] * p.T[a * 3 + k];
-            gf[k] += gx[a] * p.T[a * 3 + k] * p.T[6 + k];
-          }
-        }
-        if (p.valid) {
-          // f_k = tv_k / D  =>  dL/dD = -sum_k gf_k f_k / D, D = sum tv_k T_2k^2.
-          const float gD = -(gf[0] * p.f[0] + gf[1] * p.f[1] + gf[2] * p.f[2]) / p.D;
-#pragma unroll
-          for (int k = 0; k < 3; ++k) gT[6 + k] += gD * 2.f * tv[k] * p.T[6 + k];
-        }
-      }
-      // T = K P: dK = gT P^T, dP = K^T gT.
-      float gP[9];
-#pragma unroll
-      for (int a = 0; a < 3; ++a)
-#pragma unroll
-        for (int b = 0; b < 3; ++b) {
-          float acc_k = 0.f, acc_p = 0.f;
-#pragma unroll
-          for (int k = 0; k < 3; ++k) {
-            acc_k += gT[a * 3 + k] * p.P[b * 3 + k];
-            acc_p += K[k * 3 + a] * gT[k * 3 + b];
-          }
-          cam_grad[12 + a * 3 + b] = acc_k;
-          gP[a * 3 + b] = acc_p;
-        }
-      float* gRc = cam_grad;
-      float* gt = cam_grad + 9;
-      // Plane column 2: camera mean Rc mu + t.
-      // Plane column j < 2: Rc (R[:,j] s_j).
-#pragma unroll
-      for (int a = 0; a < 3; ++a) {
-        gt[a] += gP[a * 3 + 2];
-#pragma unroll
-        for (int b = 0; b < 3; ++b) {
-          gRc[a * 3 + b] += gP[a * 3 + 2] * s.mu[b] + gP[a * 3 + 0] * s.R[b * 3 + 0] * s.sc[0] +
-                            gP[a * 3 + 1] * s.R[b * 3 + 1] * s.sc[1];
-        }
-      }
-#pragma unroll
-      for (int b = 0; b < 3; ++b) {
-        float g_mean = 0.f, g_t0 = 0.f, g_t1 = 0.f;
-#pragma unroll
-        for (int a = 0; a < 3; ++a) {
-          g_mean += Rc[a * 3 + b] * gP[a * 3 + 2];
-          g_t0 += Rc[a * 3 + b] * gP[a * 3 + 0];
-          g_t1 += Rc[a * 3 + b] * gP[a * 3 + 1];
-        }
-        gmu[b] += g_mean;
-        gR[b * 3 + 0] += g_t0 * s.sc[0];
-        gR[b * 3 + 1] += g_t1 * s.sc[1];
-        gs[0] += g_t0 * s.R[b * 3 + 0];
-        gs[1] += g_t1 * s.R[b * 3 + 1];
-      }
-      // Facing normal sign * Rc R[:,2]; the sign is piecewise constant.
-      if (g_normals) {
-        const float sign = p.facing > 0.f ? 1.f : -1.f;
-        float gn[3];
-#pragma unroll
-        for (int a = 0; a < 3; ++a) gn[a] = sign * g_normals[pair * 3 + a];
-#pragma unroll
-        for (int a = 0; a < 3; ++a)
-#pragma unroll
-          for (int b = 0; b < 3; ++b) {
-            gRc[a * 3 + b] += gn[a] * s.R[b * 3 + 2];
-            gR[b * 3 + 2] += Rc[a * 3 + b] * gn[a];
-          }
-      }
-      // Unit direction d / max(|d|, 1e-12), d = mu + Rc^T t.
-      if (g_dirs) {
-        float gd[3], gvec[3];
-#pragma unroll
-        for (int a = 0; a < 3; ++a) gd[a] = g_dirs[pair * 3 + a];
-        if (p.dlen > 1e-12f) {
-          const float inv = 1.f / p.dlen;
-          const float dot = (p.dvec[0] * gd[0] + p.dvec[1] * gd[1] + p.dvec[2] * gd[2]) * inv;
-#pragma unroll
-          for (int a = 0; a < 3; ++a) gvec[a] = (gd[a] - p.dvec[a] * inv * dot) * inv;
-        } else {
-#pragma unroll
-          for (int a = 0; a < 3; ++a) gvec[a] = gd[a] / 1e-12f;
-        }
-#pragma unroll
-        for (int a = 0; a < 3; ++a) {
-          gmu[a] += gvec[a];
-          // centre = -Rc^T t and d = mu - centre: dt = Rc gvec, dRc = t gvec^T.
-          gt[a] += Rc[a * 3 + 0] * gvec[0] + Rc[a * 3 + 1] * gvec[1] + Rc[a * 3 + 2] * gvec[2];
-#pragma unroll
-          for (int b = 0; b < 3; ++b) gRc[a * 3 + b] += t[a] * gvec[b];
-        }
-      }
+    for (int k = 0; k < 3; ++k) {
+      g.gn[k] = normals ? normals[pair * 3 + k] : 0.f;
+      g.gd[k] = directions ? directions[pair * 3 + k] : 0.f;
     }
-    // Workgroup sum of the per-camera gradients.
-    const float total = wave_reduce_scatter<kCameraGrads>(cam_grad, lane);
-    const int param = rs_param<kCameraGrads>(lane);
-    if (param < kCameraGrads) wave_sums[wave][param] = total;
-    __syncthreads();
-    if (threadIdx.x < kCameraGrads) {
-      float acc = 0.f;
-#pragma unroll
-      for (int w = 0; w < kBlock / 64; ++w) acc += wave_sums[w][threadIdx.x];
-      partials[(cam * gridDim.x + blockIdx.x) * kCameraGrads + threadIdx.x] = acc;
-    }
-    __syncthreads();
+    return true;
   }
-  if (!valid) return;
-  // Rotation -> normalised quaternion -> raw quaternion.
-  const float w = s.qn[0], x = s.qn[1], y = s.qn[2], z = s.qn[3];
-  float gq[4];
-  gq[0] = 2.f * (-z * gR[1] + y * gR[2] + z * gR[3] - x * gR[5] - y * gR[6] + x * gR[7]);
-  gq[1] = 2.f * (y * gR[1] + z * gR[2] + y * gR[3] - 2.f * x * gR[4] - w * gR[5] + z * gR[6] +
-                 w * gR[7] - 2.f * x * gR[8]);
-  gq[2] = 2.f * (-2.f * y * gR[0] + x * gR[1] + w * gR[2] + x * gR[3] + z * gR[5] - w * gR[6] +
-                 z * gR[7] - 2.f * y * gR[8]);
-  gq[3] = 2.f * (-2.f * z * gR[0] - w * gR[1] + x * gR[2] + w * gR[3] - 2.f * z * gR[4] +
-                 y * gR[5] + x * gR[6] + y * gR[7]);
-  const float proj = gq[0] * w + gq[1] * x + gq[2] * y + gq[3] * z;
-  const int64_t idx = scene * n + i;
-#pragma unroll
-  for (int k = 0; k < 4; ++k) grad_quats[idx * 4 + k] = (gq[k] - s.qn[k] * proj) / s.qlen;
-#pragma unroll
-  for (int k = 0; k < 3; ++k) grad_means[idx * 3 + k] = gmu[k];
-  grad_scales[idx * 2 + 0] = gs[0];
-  grad_scales[idx * 2 + 1] = gs[1];
-}
-
-// Sum the per-workgroup camera partials [cams, blocks, 21] into the view
-// matrix (rotation + translation, last row zero) and intrinsics gradients.
-__global__ __launch_bounds__(kBlock) void camera_reduce_kernel(
-    const float* __restrict__ partials, int64_t blocks, float* __restrict__ grad_views,
-    float* __restrict__ grad_intrinsics) {
-  __shared__ float wave_sums[kBlock / 64][kCameraGrads];
-  const int64_t cam = blockIdx.x;
-  const int lane = lane_id();
-  const int wave = threadIdx.x >> 6;
-  float acc[kCameraGrads];
-#pragma unroll
-  for (int k = 0; k < kCameraGrads; ++k) acc[k] = 0.f;
-  for (int64_t b = threadIdx.x; b < blocks; b += kBlock) {
-    const float* row = partials + (cam * blocks + b) * kCameraGrads;
-#pragma unroll
-    for (int k = 0; k < kCameraGrads; ++k) acc[k] += row[k];
-  }
-  const float total = wave_reduce_scatter<kCameraGrads>(acc, lane);
-  const int param = rs_param<kCameraGrads>(lane);
-  if (param < kCameraGrads) wave_sums[wave][param] = total;
-  __syncthreads();
-  if (threadIdx.x < 16) {
-    const int r = threadIdx.x / 4, col = threadIdx.x % 4;
-    float v = 0.f;
-    if (r < 3) {
-      const int k = col < 3 ? r * 3 + col : 9 + r;
-#pragma unroll
-      for (int w = 0; w < kBlock / 64; ++w) v += wave_sums[w][k];
-    }
-    grad_views[cam * 16 + threadIdx.x] = v;
-  } else if (threadIdx.x >= 32 && threadIdx.x < 41) {
-    const int k = 12 + threadIdx.x - 32;
-    float v = 0.f;
-#pragma unroll
-    for (int w = 0; w < kBlock / 64; ++w) v += wave_sums[w][k];
-    grad_intrinsics[cam * 9 + threadIdx.x - 32] = v;
-  }
-}
-
-int check_projection_sizes(int64_t scenes, int64_t cameras, int64_t n) {
-  GS_REQUIRE(scenes >= 1 && cameras >= 1 && n >= 0, GS_ERR_ARGUMENT,
-             "projection needs scenes >= 1, cameras >= 1, n >= 0 (got %lld, %lld, %lld)",
-             (long long)scenes, (long long)cameras, (long long)n);
-  GS_REQUIRE(scenes <= 65535, GS_ERR_ARGUMENT, "at most 65535 scenes per call (got %lld)",
-             (long long)scenes);
-  GS_REQUIRE(ceil_div(n, kBlock) <= 0x7fffffff, GS_ERR_OVERFLOW, "too many surfels");
-  return GS_OK;
-}
+};
 
 }  // namespace
 }  // namespace gs
@@ -446,8 +91,8 @@ int gs_project_forward(const float* means, const float* quaternions, const float
              GS_ERR_ARGUMENT, "null pointer passed to gs_project_forward");
   hipStream_t s = static_cast<hipStream_t>(stream);
   ProfileScope prof(GS_PROF_PROJECT_FWD, s);
-  dim3 grid(unsigned(ceil_div(n, kBlock)), unsigned(scenes));
-  project_forward_kernel<<<grid, kBlock, 0, s>>>(
+  dim3 grid(static_cast<unsigned>(ceil_div(n, kProjectBlock)), static_cast<unsigned>(scenes));
+  project_forward_kernel<<<grid, kProjectBlock, 0, s>>>(
       means, quaternions, scales, view_matrices, intrinsics, cameras, n, tiles_x(width),
       tiles_y(height), near_plane, far_plane, transform, xy, normals, directions, radii);
   GS_LAUNCHED("project_forward_kernel");
@@ -455,8 +100,7 @@ int gs_project_forward(const float* means, const float* quaternions, const float
 }
 
 size_t gs_project_backward_workspace_size(int64_t scenes, int64_t cameras, int64_t n) {
-  const int64_t blocks = gs::ceil_div(n > 0 ? n : 0, gs::kBlock);
-  return size_t(scenes * cameras * blocks * gs::kCameraGrads) * sizeof(float) + 256;
+  return gs::camera_partials_bytes(scenes, cameras, n);
 }
 
 int gs_project_backward(const float* means, const float* quaternions, const float* scales,
@@ -478,20 +122,20 @@ int gs_project_backward(const float* means, const float* quaternions, const floa
              "projection backward needs %zu workspace bytes, got %zu", need, workspace_bytes);
   hipStream_t s = static_cast<hipStream_t>(stream);
   ProfileScope prof(GS_PROF_PROJECT_BWD, s);
-  const int64_t blocks = ceil_div(n, kBlock);
+  const int64_t blocks = ceil_div(n, kProjectBlock);
   float* partials = static_cast<float*>(workspace);
   if (n > 0) {
     GS_REQUIRE(means && quaternions && scales && view_matrices && intrinsics && grad_means &&
                    grad_quaternions && grad_scales,
                GS_ERR_ARGUMENT, "null pointer passed to gs_project_backward");
     dim3 grid(static_cast<unsigned>(blocks), static_cast<unsigned>(scenes));
-    project_backward_kernel<<<grid, kBlock, 0, s>>>(
-        means, quaternions, scales, view_matrices, intrinsics, cameras, n, grad_transform,
-        grad_xy, grad_normals, grad_directions, grad_means, grad_quaternions, grad_scales,
-        partials);
-    GS_LAUNCHED("project_backward_kernel");
+    projection_backward_kernel<DenseGrads><<<grid, kProjectBlock, 0, s>>>(
+        means, quaternions, scales, view_matrices, intrinsics, cameras, n,
+        DenseGrads{grad_transform, grad_xy, grad_normals, grad_directions}, grad_means,
+        grad_quaternions, grad_scales, partials);
+    GS_LAUNCHED("projection_backward_kernel");
   }
-  camera_reduce_kernel<<<unsigned(scenes * cameras), kBlock, 0, s>>>(
+  camera_reduce_kernel<<<static_cast<unsigned>(scenes * cameras), kProjectBlock, 0, s>>>(
       partials, blocks, grad_view_matrices, grad_intrinsics);
   GS_LAUNCHED("camera_reduce_kernel");
   return GS_OK;

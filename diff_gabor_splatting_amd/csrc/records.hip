@@ -1,0 +1,352 @@
+// Kernel 1 (fused): projection + SH + record assembly, and its adjoint.
+//
+// Replaces the reference's host-side chain (src/gabor_splatting/rendering.py:
+// 323-374): project_surfaces, SHColors, the per-camera expansion of the
+// shared appearance and opacity, the packing gathers and the geometry
+// concatenation. One thread per (scene, surfel) loops over the cameras of
+// its scene and writes each pair's compositor rows directly:
+//   geometry [Q,17] = T | xy | facing normal | unit direction,
+//   projected means [Q,2], radii [Q], image ids [Q], primitive ids [Q],
+//   and with SH: appearance rows [Q,18] = colour(3) colour2(3) weights(4)
+//   magnitudes(4) phases(4) and opacity rows [Q] (camera-specific colours).
+// Rows are dense (row = pair index (s*C + c)*N + n) or, in packed mode,
+// compacted through row_of_pair (visible pairs only, in ascending pair
+// order, exactly the reference's `arange(Q)[radii > 0]`). Packed SH rows are
+// compacted too (the reference keeps them dense), and each row's
+// primitive id is then the row itself.
+//
+// The adjoint reads the compositor's gradient rows: an SH pass sums colour
+// and shared-parameter gradients over cameras per surfel (no atomics) and
+// leaves per-pair direction gradients in the workspace; the projection
+// adjoint (projection.hpp) then consumes transform / normal / direction rows
+// and the projected-mean gradients.
+#include "projection.hpp"
+#include "sh_basis.hpp"
+
+namespace gs {
+namespace {
+
+constexpr int kRow = kClassic;  // SH appearance row width
+
+template <int Degree>  // -1: no SH rows
+__global__ __launch_bounds__(kProjectBlock) void records_forward_kernel(
+    const float* __restrict__ means, const float* __restrict__ quats,
+    const float* __restrict__ scales, const float* __restrict__ opacities,
+    const float* __restrict__ views, const float* __restrict__ intrinsics,
+    const float* __restrict__ sh_first, const float* __restrict__ sh_second,
+    const float* __restrict__ weights, const float* __restrict__ magnitudes,
+    const float* __restrict__ phases, int64_t cameras, int64_t n, int tw, int th,
+    float near_plane, float far_plane, const int* __restrict__ row_of_pair,
+    int* __restrict__ dense_radii, float* __restrict__ geometry,
+    float* __restrict__ projected_means, int* __restrict__ row_radii,
+    int64_t* __restrict__ primitive_ids, int64_t* __restrict__ image_ids,
+    float* __restrict__ appearance, float* __restrict__ opacity_rows) {
+  constexpr int K = Degree >= 0 ? (Degree + 1) * (Degree + 1) : 1;
+  const int64_t i = int64_t(blockIdx.x) * kProjectBlock + threadIdx.x;
+  const int64_t scene = blockIdx.y;
+  if (i >= n) return;
+  const int64_t surfel = scene * n + i;
+  Surfel s;
+  load_surfel(means, quats, scales, surfel, s);
+  for (int64_t c = 0; c < cameras; ++c) {
+    const int64_t cam = scene * cameras + c;
+    Projection p;
+    project_pair(s.R, s.mu, s.sc, views + cam * 16, intrinsics + cam * 9, p);
+    const int64_t pair = cam * n + i;
+    const int radius = screen_radius(p, tw, th, near_plane, far_plane);
+    if (dense_radii) dense_radii[pair] = radius;
+    if (!geometry) continue;  // radii-only pass
+    const int64_t row = row_of_pair ? int64_t(row_of_pair[pair]) : pair;
+    if (row < 0) continue;
+    float* g = geometry + row * kGeometry;
+#pragma unroll
+    for (int k = 0; k < 9; ++k) g[k] = p.T[k];
+    g[9] = p.xy[0];
+    g[10] = p.xy[1];
+    const float sign = facing_sign(p);
+#pragma unroll
+    for (int k = 0; k < 3; ++k) g[11 + k] = p.nraw[k] * sign;
+    float d[3];
+    unit_direction(p, d);
+#pragma unroll
+    for (int k = 0; k < 3; ++k) g[14 + k] = d[k];
+    projected_means[row * 2 + 0] = p.xy[0];
+    projected_means[row * 2 + 1] = p.xy[1];
+    row_radii[row] = radius;
+    image_ids[row] = cam;
+    if constexpr (Degree >= 0) {
+      primitive_ids[row] = row;
+      float Y[K];
+      sh_basis<(Degree >= 0 ? Degree : 0), false>(d[0], d[1], d[2], Y, nullptr, nullptr,
+                                                  nullptr);
+      float* a = appearance + row * kRow;
+      const float* coef[2] = {sh_first + surfel * K * 3, sh_second + surfel * K * 3};
+#pragma unroll
+      for (int set = 0; set < 2; ++set)
+#pragma unroll
+        for (int ch = 0; ch < 3; ++ch) {
+          float raw = 0.5f;
+#pragma unroll
+          for (int k = 0; k < K; ++k) raw += Y[k] * coef[set][k * 3 + ch];
+          a[set * 3 + ch] = fmaxf(raw, 0.f);
+        }
+#pragma unroll
+      for (int f = 0; f < 4; ++f) {
+        a[6 + f] = weights[surfel * 4 + f];
+        a[10 + f] = magnitudes[surfel * 4 + f];
+        a[14 + f] = phases[surfel * 4 + f];
+      }
+      opacity_rows[row] = opacities[surfel];
+    } else {
+      primitive_ids[row] = surfel;
+    }
+  }
+}
+
+// SH part of the adjoint: per surfel, sum over cameras the colour gradients
+// pushed through the basis (coefficients), the shared weight / magnitude /
+// phase and opacity gradients; write per-pair direction gradients.
+template <int Degree>
+__global__ __launch_bounds__(kProjectBlock) void sh_rows_backward_kernel(
+    const float* __restrict__ sh_first, const float* __restrict__ sh_second, int64_t cameras,
+    int64_t n, const int* __restrict__ row_of_pair, const float* __restrict__ geometry,
+    const float* __restrict__ grad_rows, const float* __restrict__ grad_opacity_rows,
+    float* __restrict__ grad_first, float* __restrict__ grad_second,
+    float* __restrict__ grad_weights, float* __restrict__ grad_magnitudes,
+    float* __restrict__ grad_phases, float* __restrict__ grad_opacities,
+    float* __restrict__ grad_directions) {
+  constexpr int K = (Degree + 1) * (Degree + 1);
+  const int64_t i = int64_t(blockIdx.x) * kProjectBlock + threadIdx.x;
+  const int64_t scene = blockIdx.y;
+  if (i >= n) return;
+  const int64_t surfel = scene * n + i;
+  const float* coef[2] = {sh_first + surfel * K * 3, sh_second + surfel * K * 3};
+  float acc[2][K * 3];
+#pragma unroll
+  for (int set = 0; set < 2; ++set)
+#pragma unroll
+    for (int k = 0; k < K * 3; ++k) acc[set][k] = 0.f;
+  float shared[12];
+#pragma unroll
+  for (int k = 0; k < 12; ++k) shared[k] = 0.f;
+  float g_opacity = 0.f;
+  for (int64_t c = 0; c < cameras; ++c) {
+    const int64_t pair = (scene * cameras + c) * n + i;
+    const int64_t row = row_of_pair ? int64_t(row_of_pair[pair]) : pair;
+    if (row < 0) continue;
+    const float* d = geometry + row * kGeometry + 14;
+    const float* gr = grad_rows + row * kRow;
+    float Y[K], dx[K], dy[K], dz[K];
+    sh_basis<Degree, true>(d[0], d[1], d[2], Y, dx, dy, dz);
+    float gd[3] = {0.f, 0.f, 0.f};
+#pragma unroll
+    for (int set = 0; set < 2; ++set)
+#pragma unroll
+      for (int ch = 0; ch < 3; ++ch) {
+        float raw = 0.5f;
+#pragma unroll
+        for (int k = 0; k < K; ++k) raw += Y[k] * coef[set][k * 3 + ch];
+        const float g = raw >= 0.f ? gr[set * 3 + ch] : 0.f;
+#pragma unroll
+        for (int k = 0; k < K; ++k) {
+          const float cv = coef[set][k * 3 + ch];
+          acc[set][k * 3 + ch] += g * Y[k];
+          gd[0] += g * cv * dx[k];
+          gd[1] += g * cv * dy[k];
+          gd[2] += g * cv * dz[k];
+        }
+      }
+#pragma unroll
+    for (int k = 0; k < 3; ++k) grad_directions[pair * 3 + k] = gd[k];
+#pragma unroll
+    for (int k = 0; k < 12; ++k) shared[k] += gr[6 + k];
+    if (grad_opacity_rows) g_opacity += grad_opacity_rows[row];
+  }
+#pragma unroll
+  for (int k = 0; k < K * 3; ++k) {
+    grad_first[surfel * K * 3 + k] = acc[0][k];
+    grad_second[surfel * K * 3 + k] = acc[1][k];
+  }
+#pragma unroll
+  for (int f = 0; f < 4; ++f) {
+    grad_weights[surfel * 4 + f] = shared[f];
+    grad_magnitudes[surfel * 4 + f] = shared[4 + f];
+    grad_phases[surfel * 4 + f] = shared[8 + f];
+  }
+  grad_opacities[surfel] = g_opacity;
+}
+
+// Per-pair output gradients read from compositor rows.
+struct RowGrads {
+  const int* row_of_pair;       // null: row = pair
+  const float* geometry;        // [Q,17] dL/d(geometry row), or null
+  const float* projected;       // [Q,2] dL/d(projected means), or null
+  const float* sh_directions;   // [S*C*N,3] direction gradients from SH, or null
+  __device__ bool fetch(int64_t pair, PairGrads& g) const {
+    const int64_t row = row_of_pair ? int64_t(row_of_pair[pair]) : pair;
+    if (row < 0) return false;
+    const float* gg = geometry ? geometry + row * kGeometry : nullptr;
+#pragma unroll
+    for (int k = 0; k < 9; ++k) g.gT[k] = gg ? gg[k] : 0.f;
+    // The geometry row's own xy columns duplicate the projected means;
+    // their gradient arrives through `projected` only.
+    g.has_xy = projected != nullptr;
+    g.gxy[0] = projected ? projected[row * 2 + 0] : 0.f;
+    g.gxy[1] = projected ? projected[row * 2 + 1] : 0.f;
+    g.has_n = gg != nullptr;
+    g.has_d = gg != nullptr || sh_directions != nullptr;
+#pragma unroll
+    for (int k = 0; k < 3; ++k) {
+      g.gn[k] = gg ? gg[11 + k] : 0.f;
+      g.gd[k] = (gg ? gg[14 + k] : 0.f) + (sh_directions ? sh_directions[pair * 3 + k] : 0.f);
+    }
+    return true;
+  }
+};
+
+struct BackwardWorkspace {
+  float* partials;
+  float* directions;
+  size_t bytes;
+};
+
+BackwardWorkspace backward_layout(void* base, int64_t scenes, int64_t cameras, int64_t n,
+                                  int sh_degree) {
+  BackwardWorkspace w;
+  char* p = static_cast<char*>(base);
+  size_t offset = 0;
+  w.partials = reinterpret_cast<float*>(p);
+  offset = align_up(camera_partials_bytes(scenes, cameras, n), 256);
+  w.directions = sh_degree >= 0 ? reinterpret_cast<float*>(p + offset) : nullptr;
+  if (sh_degree >= 0) offset = align_up(offset + size_t(scenes * cameras * n) * 12, 256);
+  w.bytes = offset;
+  return w;
+}
+
+}  // namespace
+}  // namespace gs
+
+extern "C" {
+
+int gs_records_forward(const float* means, const float* quaternions, const float* scales,
+                       const float* opacities, const float* view_matrices,
+                       const float* intrinsics, const float* sh_first, const float* sh_second,
+                       const float* frequency_weights, const float* frequency_magnitudes,
+                       const float* phases, int32_t sh_degree, int64_t scenes,
+                       int64_t cameras, int64_t n, int32_t width, int32_t height,
+                       float near_plane, float far_plane, const int32_t* row_of_pair,
+                       int32_t* dense_radii, float* geometry, float* projected_means,
+                       int32_t* row_radii, int64_t* primitive_ids, int64_t* image_ids,
+                       float* appearance_rows, float* opacity_rows, void* stream) {
+  using namespace gs;
+  clear_error();
+  int status = check_projection_sizes(scenes, cameras, n);
+  if (status != GS_OK) return status;
+  GS_REQUIRE(width > 0 && height > 0, GS_ERR_ARGUMENT, "invalid image size %dx%d", width, height);
+  GS_REQUIRE(sh_degree >= -1 && sh_degree <= 3, GS_ERR_ARGUMENT,
+             "SH degree must be -1 (none) or 0 through 3");
+  if (n == 0) return GS_OK;
+  GS_REQUIRE(means && quaternions && scales && view_matrices && intrinsics, GS_ERR_ARGUMENT,
+             "null geometry input passed to gs_records_forward");
+  GS_REQUIRE(geometry || dense_radii, GS_ERR_ARGUMENT, "gs_records_forward has no output");
+  if (geometry) {
+    GS_REQUIRE(projected_means && row_radii && primitive_ids && image_ids, GS_ERR_ARGUMENT,
+               "null row output passed to gs_records_forward");
+    if (sh_degree >= 0)
+      GS_REQUIRE(opacities && sh_first && sh_second && frequency_weights &&
+                     frequency_magnitudes && phases && appearance_rows && opacity_rows,
+                 GS_ERR_ARGUMENT, "null SH input or output passed to gs_records_forward");
+  }
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  ProfileScope prof(GS_PROF_PROJECT_FWD, s);
+  dim3 grid(static_cast<unsigned>(ceil_div(n, kProjectBlock)), static_cast<unsigned>(scenes));
+  const int tw = tiles_x(width), th = tiles_y(height);
+#define GS_RECORDS(D)                                                                        \
+  records_forward_kernel<D><<<grid, kProjectBlock, 0, s>>>(                                  \
+      means, quaternions, scales, opacities, view_matrices, intrinsics, sh_first, sh_second, \
+      frequency_weights, frequency_magnitudes, phases, cameras, n, tw, th, near_plane,      \
+      far_plane, row_of_pair, dense_radii, geometry, projected_means, row_radii,             \
+      primitive_ids, image_ids, appearance_rows, opacity_rows)
+  switch (sh_degree) {
+    case -1: GS_RECORDS(-1); break;
+    case 0: GS_RECORDS(0); break;
+    case 1: GS_RECORDS(1); break;
+    case 2: GS_RECORDS(2); break;
+    default: GS_RECORDS(3); break;
+  }
+#undef GS_RECORDS
+  GS_LAUNCHED("records_forward_kernel");
+  return GS_OK;
+}
+
+size_t gs_records_backward_workspace_size(int64_t scenes, int64_t cameras, int64_t n,
+                                          int32_t sh_degree) {
+  return gs::backward_layout(nullptr, scenes, cameras, n, sh_degree).bytes + 256;
+}
+
+int gs_records_backward(const float* means, const float* quaternions, const float* scales,
+                        const float* view_matrices, const float* intrinsics,
+                        const float* sh_first, const float* sh_second, int32_t sh_degree,
+                        int64_t scenes, int64_t cameras, int64_t n,
+                        const int32_t* row_of_pair, const float* geometry,
+                        const float* grad_geometry, const float* grad_projected_means,
+                        const float* grad_appearance_rows, const float* grad_opacity_rows,
+                        float* grad_means, float* grad_quaternions, float* grad_scales,
+                        float* grad_view_matrices, float* grad_intrinsics,
+                        float* grad_sh_first, float* grad_sh_second, float* grad_weights,
+                        float* grad_magnitudes, float* grad_phases, float* grad_opacities,
+                        void* workspace, size_t workspace_bytes, void* stream) {
+  using namespace gs;
+  clear_error();
+  int status = check_projection_sizes(scenes, cameras, n);
+  if (status != GS_OK) return status;
+  GS_REQUIRE(sh_degree >= -1 && sh_degree <= 3, GS_ERR_ARGUMENT,
+             "SH degree must be -1 (none) or 0 through 3");
+  GS_REQUIRE(grad_view_matrices && grad_intrinsics, GS_ERR_ARGUMENT,
+             "null camera gradient pointer");
+  const size_t need = gs_records_backward_workspace_size(scenes, cameras, n, sh_degree);
+  GS_REQUIRE(workspace && workspace_bytes >= need, GS_ERR_WORKSPACE,
+             "record backward needs %zu workspace bytes, got %zu", need, workspace_bytes);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  ProfileScope prof(GS_PROF_PROJECT_BWD, s);
+  BackwardWorkspace w = backward_layout(workspace, scenes, cameras, n, sh_degree);
+  const int64_t blocks = ceil_div(n, kProjectBlock);
+  if (n > 0) {
+    GS_REQUIRE(means && quaternions && scales && view_matrices && intrinsics && grad_means &&
+                   grad_quaternions && grad_scales,
+               GS_ERR_ARGUMENT, "null pointer passed to gs_records_backward");
+    dim3 grid(static_cast<unsigned>(blocks), static_cast<unsigned>(scenes));
+    const float* sh_dirs = nullptr;
+    if (sh_degree >= 0) {
+      GS_REQUIRE(sh_first && sh_second && geometry && grad_appearance_rows && grad_sh_first &&
+                     grad_sh_second && grad_weights && grad_magnitudes && grad_phases &&
+                     grad_opacities,
+                 GS_ERR_ARGUMENT, "null SH pointer passed to gs_records_backward");
+#define GS_SH_ROWS(D)                                                                        \
+  sh_rows_backward_kernel<D><<<grid, kProjectBlock, 0, s>>>(                                 \
+      sh_first, sh_second, cameras, n, row_of_pair, geometry, grad_appearance_rows,          \
+      grad_opacity_rows, grad_sh_first, grad_sh_second, grad_weights, grad_magnitudes,       \
+      grad_phases, grad_opacities, w.directions)
+      switch (sh_degree) {
+        case 0: GS_SH_ROWS(0); break;
+        case 1: GS_SH_ROWS(1); break;
+        case 2: GS_SH_ROWS(2); break;
+        default: GS_SH_ROWS(3); break;
+      }
+#undef GS_SH_ROWS
+      GS_LAUNCHED("sh_rows_backward_kernel");
+      sh_dirs = w.directions;
+    }
+    projection_backward_kernel<RowGrads><<<grid, kProjectBlock, 0, s>>>(
+        means, quaternions, scales, view_matrices, intrinsics, cameras, n,
+        RowGrads{row_of_pair, grad_geometry, grad_projected_means, sh_dirs}, grad_means,
+        grad_quaternions, grad_scales, w.partials);
+    GS_LAUNCHED("projection_backward_kernel");
+  }
+  camera_reduce_kernel<<<static_cast<unsigned>(scenes * cameras), kProjectBlock, 0, s>>>(
+      w.partials, blocks, grad_view_matrices, grad_intrinsics);
+  GS_LAUNCHED("camera_reduce_kernel");
+  return GS_OK;
+}
+
+}  // extern "C"

@@ -20,12 +20,18 @@ from . import _native
 
 
 class Composite(torch.autograd.Function):
-    """Tile compositor with first-order reverse mode (rendering.py:14-71)."""
+    """Tile compositor with first-order reverse mode (rendering.py:14-71).
+
+    ``projected_means`` holds the same values as the geometry rows' xy
+    columns; it is an input only so that the compositor's screen-filter
+    gradient (gg[:, 9:11]) reaches it as an autograd node, as in the
+    reference where ``meta["projected_means"]`` feeds the geometry.
+    """
 
     @staticmethod
     def forward(
-        ctx: Any, geometry, appearance, opacities, primitive_ids, image_ids, radii,
-        backgrounds, width, height, neural, near_plane, far_plane,
+        ctx: Any, geometry, projected_means, appearance, opacities, primitive_ids, image_ids,
+        radii, backgrounds, width, height, neural, near_plane, far_plane,
     ):
         maps, points, ranges, state, contributors = _native.rasterize_forward(
             geometry, appearance, opacities, primitive_ids, image_ids, radii, backgrounds,
@@ -46,7 +52,64 @@ class Composite(torch.autograd.Function):
         gg, ga, go, gb = _native.rasterize_backward(
             *ctx.saved_tensors, grad_maps.contiguous(), *ctx.options
         )
-        return gg, ga, go, None, None, None, gb, None, None, None, None, None
+        return gg, gg[:, 9:11], ga, go, None, None, None, gb, None, None, None, None, None
+
+
+class ProjectRecords(torch.autograd.Function):
+    """Projection, SH and compositor-record assembly as one HIP node.
+
+    Replaces the reference's chain of PyTorch ops between its inputs and
+    Composite (rendering.py:323-374): project_surfaces, SHColors, the
+    per-camera expansion of shared appearance/opacity, the packing gathers
+    and the geometry concatenation. Outputs: geometry rows [Q,17], projected
+    means [Q,2], (with SH: appearance rows [Q,18], opacity rows [Q]), radii
+    rows [Q], primitive ids [Q], image ids [Q], dense radii [S,C,N] and the
+    packed pair indices (or an empty tensor in dense mode).
+    """
+
+    @staticmethod
+    def forward(ctx: Any, means, quaternions, scales, opacities, view_matrices, intrinsics,
+                first, second, weights, magnitudes, phases, sh_degree, width, height,
+                near_plane, far_plane, packed):
+        sh = None if sh_degree is None else (first, second)
+        shared = None if sh_degree is None else (weights, magnitudes, phases)
+        out = _native.records_forward(
+            means, quaternions, scales, opacities, view_matrices, intrinsics, sh, shared,
+            sh_degree, width, height, near_plane, far_plane, packed,
+        )
+        row_of_pair = out["row_of_pair"]
+        ctx.save_for_backward(means, quaternions, scales, view_matrices, intrinsics, first,
+                              second, out["geometry"], row_of_pair)
+        ctx.sh_degree = sh_degree
+        ctx.set_materialize_grads(False)
+        selected = out["selected"]
+        if selected is None:
+            selected = torch.empty(0, dtype=torch.int64, device=means.device)
+        discrete = (out["row_radii"], out["primitive_ids"], out["image_ids"],
+                    out["dense_radii"], selected)
+        ctx.mark_non_differentiable(*discrete)
+        if sh_degree is None:
+            return (out["geometry"], out["projected_means"], *discrete)
+        return (out["geometry"], out["projected_means"], out["appearance"],
+                out["opacity_rows"], *discrete)
+
+    @staticmethod
+    @once_differentiable
+    def backward(ctx: Any, g_geometry, g_projected, *rest):
+        means, quats, scales, views, intrinsics, first, second, geometry, rows = ctx.saved_tensors
+        sh_degree = ctx.sh_degree
+        g_appearance, g_opacity = (rest[0], rest[1]) if sh_degree is not None else (None, None)
+        if all(g is None for g in (g_geometry, g_projected, g_appearance, g_opacity)):
+            return (None,) * 17
+        grads = _native.records_backward(
+            means, quats, scales, views, intrinsics,
+            None if sh_degree is None else (first, second), sh_degree, rows, geometry,
+            g_geometry, g_projected, g_appearance, g_opacity,
+        )
+        g_means, g_quats, g_scales, g_views, g_intrinsics = grads[:5]
+        g_first, g_second, g_weights, g_magnitudes, g_phases, g_opacities = grads[5:]
+        return (g_means, g_quats, g_scales, g_opacities, g_views, g_intrinsics, g_first,
+                g_second, g_weights, g_magnitudes, g_phases) + (None,) * 6
 
 
 class ProjectSurfaces(torch.autograd.Function):
@@ -272,64 +335,44 @@ def render(
             tensors, quaternions, scales, opacities, view_matrices, intrinsics, appearance, neural
         )
 
-    transform, xy, normals, directions, radii = project_surfaces(
-        means.reshape(scenes, n, 3),
-        quaternions.reshape(scenes, n, 4),
-        scales.reshape(scenes, n, 2),
-        view_matrices.reshape(scenes, cameras, 4, 4),
-        intrinsics.reshape(scenes, cameras, 3, 3),
-        width,
-        height,
-        near_plane,
-        far_plane,
-    )
+    views = view_matrices.reshape(scenes, cameras, 4, 4)
+    cameras_k = intrinsics.reshape(scenes, cameras, 3, 3)
     pairs = scenes * cameras * n
     if sh_degree is not None:
-        # Camera-specific SH colours, so appearance rows are per pair.
+        # Camera-specific SH colours: appearance and opacity rows per pair,
+        # written by the HIP record kernel.
         k = (sh_degree + 1) ** 2
-        colors = SHColors.apply(
-            appearance[0].reshape(scenes, n, k, 3),
-            appearance[1].reshape(scenes, n, k, 3),
-            directions,
-            sh_degree,
+        (geometry, projected_means, parameters, opacity_rows, row_radii, primitive_ids,
+         image_ids, dense_radii, selected) = ProjectRecords.apply(
+            means.reshape(scenes, n, 3), quaternions.reshape(scenes, n, 4),
+            scales.reshape(scenes, n, 2), opacities.reshape(scenes, n), views, cameras_k,
+            appearance[0].reshape(scenes, n, k, 3), appearance[1].reshape(scenes, n, k, 3),
+            appearance[2].reshape(scenes, n, 4), appearance[3].reshape(scenes, n, 4),
+            appearance[4].reshape(scenes, n, 4), sh_degree, width, height, near_plane,
+            far_plane, packed,
         )
-        shared = [t.reshape(scenes, 1, n, 4).expand(scenes, cameras, n, 4) for t in appearance[2:]]
-        parameters = torch.cat((colors, *shared), dim=-1).reshape(pairs, 18).contiguous()
-        opacity_rows = opacities.reshape(scenes, 1, n).expand(scenes, cameras, n)
-        opacity_rows = opacity_rows.reshape(pairs).contiguous()
-        primitive_ids = torch.arange(pairs, device=device)
     else:
         # One appearance row per surfel, shared by every camera of its scene.
+        (geometry, projected_means, row_radii, primitive_ids, image_ids, dense_radii,
+         selected) = ProjectRecords.apply(
+            means.reshape(scenes, n, 3), quaternions.reshape(scenes, n, 4),
+            scales.reshape(scenes, n, 2), None, views, cameras_k, None, None, None, None, None,
+            None, width, height, near_plane, far_plane, packed,
+        )
         width_of_row = 57 if neural else 18
         flat = [t.reshape(scenes, n, math.prod(shape)) for t, (_, shape) in zip(appearance, fields)]
-        parameters = torch.cat(flat, dim=-1).reshape(scenes * n, width_of_row).contiguous()
+        parameters = torch.cat(flat, dim=-1).reshape(scenes * n, width_of_row)
         opacity_rows = opacities.reshape(scenes * n)
-        primitive_ids = torch.arange(scenes * n, device=device).reshape(scenes, 1, n)
-        primitive_ids = primitive_ids.expand(scenes, cameras, n).reshape(pairs).contiguous()
-    image_ids = torch.arange(scenes * cameras, device=device).reshape(scenes, cameras, 1)
-    image_ids = image_ids.expand(scenes, cameras, n).reshape(pairs).contiguous()
-    flat_radii = radii.reshape(pairs)
-    if packed:
-        selected = _native.pack_visible(flat_radii)
-    else:
+    if not packed:
         selected = torch.arange(pairs, device=device)
-    projected_means = xy.reshape(pairs, 2)[selected]
-    geometry = torch.cat(
-        (
-            transform.reshape(pairs, 9)[selected],
-            projected_means,
-            normals.reshape(pairs, 3)[selected],
-            directions.reshape(pairs, 3)[selected],
-        ),
-        dim=-1,
-    ).contiguous()
     maps = Composite.apply(
         geometry,
+        projected_means,
         parameters,
         opacity_rows,
-        primitive_ids[selected],
-        image_ids[selected],
-        flat_radii[selected].contiguous(),
+        primitive_ids,
+        image_ids,
+        row_radii,
         backgrounds.reshape(scenes * cameras, 3),
         width,
         height,
@@ -339,7 +382,7 @@ def render(
     ).reshape(batch + (cameras, height, width, 9))
     stride = max(n, 1)
     meta = {
-        "radii": flat_radii[selected] if packed else radii.reshape(batch + (cameras, n)),
+        "radii": row_radii if packed else dense_radii.reshape(batch + (cameras, n)),
         "projected_means": projected_means,
         "scene_ids": selected // (cameras * stride),
         "camera_ids": selected // stride % cameras,

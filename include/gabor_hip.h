@@ -81,6 +81,56 @@ int gs_project_backward(const float* means, const float* quaternions, const floa
                         float* grad_view_matrices, float* grad_intrinsics, void* workspace,
                         size_t workspace_bytes, void* stream);
 
+/* Fused projection, SH and compositor-record assembly. Replaces the
+ * reference's host chain rendering.py:323-374 (project_surfaces, SHColors,
+ * per-camera expansion of shared appearance/opacity, packing gathers and the
+ * geometry torch.cat). For every (scene, camera, surfel) pair it writes
+ * dense_radii[pair] (if non-null) and, unless geometry is null (a radii-only
+ * pass), the pair's compositor row: row = pair when row_of_pair is null,
+ * else row_of_pair[pair] (-1: skipped). Rows: geometry [Q,17],
+ * projected_means [Q,2], row_radii [Q], image_ids [Q] (= s*C + c),
+ * primitive_ids [Q] (= s*N + n without SH; = row with SH). With
+ * sh_degree 0..3 the colours are camera-specific and the row also gets
+ * appearance_rows [Q,18] (SH colours, then the surfel's weights, magnitudes
+ * and phases) and opacity_rows [Q]; sh_degree -1 writes neither (the caller
+ * supplies per-surfel appearance). */
+int gs_records_forward(const float* means, const float* quaternions, const float* scales,
+                       const float* opacities, const float* view_matrices,
+                       const float* intrinsics, const float* sh_first, const float* sh_second,
+                       const float* frequency_weights, const float* frequency_magnitudes,
+                       const float* phases, int32_t sh_degree, int64_t scenes,
+                       int64_t cameras, int64_t n, int32_t width, int32_t height,
+                       float near_plane, float far_plane, const int32_t* row_of_pair,
+                       int32_t* dense_radii, float* geometry, float* projected_means,
+                       int32_t* row_radii, int64_t* primitive_ids, int64_t* image_ids,
+                       float* appearance_rows, float* opacity_rows, void* stream);
+
+/* Scratch bytes needed by gs_records_backward. */
+size_t gs_records_backward_workspace_size(int64_t scenes, int64_t cameras, int64_t n,
+                                          int32_t sh_degree);
+
+/* Adjoint of gs_records_forward given the compositor's row gradients:
+ * grad_geometry [Q,17] (its xy columns are ignored: the projected-means
+ * gradient arrives in grad_projected_means [Q,2]), and with SH
+ * grad_appearance_rows [Q,18] and grad_opacity_rows [Q]; any may be null.
+ * geometry is the forward's row output (SH reads the directions). Surfel and
+ * camera gradients are overwritten: means, quaternions, scales,
+ * view_matrices [S,C,4,4], intrinsics [S,C,3,3], and with SH the
+ * coefficients [S,N,K,3] x2, weights/magnitudes/phases [S,N,4] and
+ * opacities [S,N], each summed over cameras without atomics. */
+int gs_records_backward(const float* means, const float* quaternions, const float* scales,
+                        const float* view_matrices, const float* intrinsics,
+                        const float* sh_first, const float* sh_second, int32_t sh_degree,
+                        int64_t scenes, int64_t cameras, int64_t n,
+                        const int32_t* row_of_pair, const float* geometry,
+                        const float* grad_geometry, const float* grad_projected_means,
+                        const float* grad_appearance_rows, const float* grad_opacity_rows,
+                        float* grad_means, float* grad_quaternions, float* grad_scales,
+                        float* grad_view_matrices, float* grad_intrinsics,
+                        float* grad_sh_first, float* grad_sh_second, float* grad_weights,
+                        float* grad_magnitudes, float* grad_phases, float* grad_opacities,
+                        void* workspace, size_t workspace_bytes, void* stream);
+
 /* Replaces _C.evaluate_sh_forward (spherical_harmonics.cu:107-126):
  * colors [S,C,N,6] = max(0.5 + sum_k Y_k(dir) coef[k], 0) for both colour
  * sets first/second [S,N,K,3], K = (degree+1)^2, directions [S,C,N,3]. */
@@ -104,10 +154,12 @@ size_t gs_scan_workspace_size(int64_t count);
 
 /* Packed mode (rendering.py:362-364, `arange(Q)[radii > 0]`): writes the
  * ascending indices of pairs with radii > 0 to selected[0..V) and V to
- * *num_selected (a device int64). selected must hold `count` entries. */
+ * *num_selected (a device int64). selected must hold `count` entries.
+ * row_of_pair (optional, [count] int32) receives each pair's row in the
+ * packed order, or -1 for culled pairs. */
 int gs_pack_visible(const int32_t* radii, int64_t count, int64_t* selected,
-                    int64_t* num_selected, void* workspace, size_t workspace_bytes,
-                    void* stream);
+                    int32_t* row_of_pair, int64_t* num_selected, void* workspace,
+                    size_t workspace_bytes, void* stream);
 
 /* countTiles + cub::DeviceScan::InclusiveSum (rasterize.cu:33-40, 459-464):
  * offsets[i] = inclusive prefix sum of each pair's tile-rectangle area

@@ -71,3 +71,37 @@ def test_workspace_sizes_grow_with_input(m):
     lib = _native.lib
     assert lib.gs_sort_workspace_size(m) >= 12 * m
     assert lib.gs_scan_workspace_size(m) >= 8 * ((m + 4095) // 4096)
+
+
+def _declarations():
+    """Parameter type lists of every gs_* prototype in include/*.h."""
+    out = {}
+    for header in (ROOT / "include").glob("*.h"):
+        text = re.sub(r"/\*.*?\*/", "", header.read_text(), flags=re.S)
+        for match in re.finditer(r"\b(gs_\w+)\s*\(([^)]*)\)\s*;", text):
+            params = [p.strip() for p in match.group(2).split(",") if p.strip() not in ("", "void")]
+            out[match.group(1)] = params
+    return out
+
+
+def _ctype_class(param):
+    if "*" in param:
+        return "pointer"
+    kind = param.rsplit(" ", 1)[0].replace("const ", "").strip()
+    return {"int32_t": "int32", "int": "int32", "int64_t": "int64", "size_t": "size",
+            "float": "float", "double": "double"}[kind]
+
+
+def test_ctypes_signatures_match_the_header():
+    from diff_gabor_splatting_amd import _native
+
+    classes = {ctypes.c_void_p: "pointer", ctypes.c_int32: "int32", ctypes.c_int64: "int64",
+               ctypes.c_size_t: "size", ctypes.c_float: "float", ctypes.c_double: "double"}
+    declared = _declarations()
+    for name, (_, argtypes) in _native._SIGNATURES.items():
+        params = declared[name]
+        assert len(params) == len(argtypes), (name, len(params), len(argtypes))
+        for index, (param, argtype) in enumerate(zip(params, argtypes)):
+            expected = _ctype_class(param)
+            actual = classes.get(argtype, "pointer")
+            assert expected == actual, (name, index, param, argtype)

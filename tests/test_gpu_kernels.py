@@ -173,3 +173,100 @@ def test_sh_values_and_derivatives(native, degree, cameras):
     for a, e, leaf in zip(ag, eg, leaves):
         e = torch.zeros_like(leaf) if e is None else e
         torch.testing.assert_close(a.cpu().double(), e, atol=3e-5, rtol=2e-4)
+
+
+@pytest.mark.parametrize("packed", [False, True])
+@pytest.mark.parametrize("sh", [None, 0, 3])
+def test_records_match_oracle(native, packed, sh):
+    from oracle import render as oracle_render
+    from scenes import random_scene
+
+    width, height = 48, 40
+    v = random_scene("classic", scenes=2, cameras=3, n=300, width=width, height=height, seed=8,
+                     sh=sh)
+    v["view_matrices"][..., 2, 3] = torch.linspace(-1.0, 0.5, 3)  # some surfels behind near
+    S, N = v["means"].shape[:2]
+    C = v["view_matrices"].shape[1]
+    gpu = {k: t.to(DEVICE) for k, t in v.items()}
+    sh_args = None if sh is None else (gpu["colors"], gpu["secondary_colors"])
+    shared = None if sh is None else (gpu["frequency_weights"], gpu["frequency_magnitudes"],
+                                      gpu["phases"])
+    out = native.records_forward(gpu["means"], gpu["quaternions"], gpu["scales"],
+                                 gpu["opacities"], gpu["view_matrices"], gpu["intrinsics"],
+                                 sh_args, shared, sh, width, height, 0.2, 100.0, packed)
+    radii = out["dense_radii"].cpu()
+    leaves = {k: t.double().requires_grad_() for k, t in v.items() if k != "backgrounds"}
+    appearance = tuple(leaves[k] for k in ("colors", "secondary_colors", "frequency_weights",
+                                          "frequency_magnitudes", "phases"))
+    rec = oracle_render.records(leaves["means"], leaves["quaternions"], leaves["scales"],
+                                leaves["opacities"], appearance, leaves["view_matrices"],
+                                leaves["intrinsics"], width, height, packed=packed,
+                                sh_degree=sh, radii=radii)
+    oracle32 = oracle_render.records(*(v[k] for k in ("means", "quaternions", "scales", "opacities")),
+                                     tuple(v[k] for k in ("colors", "secondary_colors",
+                                                          "frequency_weights",
+                                                          "frequency_magnitudes", "phases")),
+                                     v["view_matrices"], v["intrinsics"], width, height,
+                                     packed=packed, sh_degree=sh)
+    before = radius_before_ceil(*(v[k].double() for k in ("means", "quaternions", "scales",
+                                                         "view_matrices", "intrinsics")))
+    wobble = perturbation_sensitivity(radius_before_ceil, [v[k] for k in (
+        "means", "quaternions", "scales", "view_matrices", "intrinsics")])[0]
+    margin = (before - before.round()).abs() <= 4 * wobble + 1e-4
+    assert not bool(((radii != oracle32["dense_radii"]) & ~margin).any())
+    selected = rec["selected"].numpy()
+    if packed:
+        np.testing.assert_array_equal(out["selected"].cpu().numpy(), selected)
+        rows = out["row_of_pair"].cpu().numpy()
+        expect_rows = np.full(S * C * N, -1)
+        expect_rows[selected] = np.arange(len(selected))
+        np.testing.assert_array_equal(rows, expect_rows)
+    np.testing.assert_array_equal(out["image_ids"].cpu().numpy(), rec["image_ids"].numpy())
+    np.testing.assert_array_equal(out["row_radii"].cpu().numpy(), rec["radii"].numpy())
+    expect_prims = np.arange(len(selected)) if sh is not None else rec["primitive_ids"].numpy()
+    np.testing.assert_array_equal(out["primitive_ids"].cpu().numpy(), expect_prims)
+    geometry = rec["geometry"].detach()
+    sens = perturbation_sensitivity(
+        lambda *x: oracle_render.records(*x[:4], tuple(x[4:9]), x[9], x[10], width, height,
+                                         packed=packed, sh_degree=sh, radii=radii)["geometry"],
+        [v[k] for k in ("means", "quaternions", "scales", "opacities", "colors",
+                        "secondary_colors", "frequency_weights", "frequency_magnitudes",
+                        "phases", "view_matrices", "intrinsics")])[0]
+    a = out["geometry"].cpu().double()
+    assert bool(((a - geometry).abs() <= 1e-6 * (1 + geometry.abs()) + 4 * sens).all()), \
+        describe_mismatch(a, geometry)
+    if sh is not None:
+        rows_ref = rec["appearance"].detach()[selected] if packed else rec["appearance"].detach()
+        torch.testing.assert_close(out["appearance"].cpu().double(), rows_ref, atol=2e-6, rtol=1e-5)
+        op_ref = rec["opacities"].detach()[selected] if packed else rec["opacities"].detach()
+        torch.testing.assert_close(out["opacity_rows"].cpu().double(), op_ref)
+    # Adjoint: random row gradients (geometry xy columns excluded: that
+    # gradient enters through the projected means).
+    g = torch.Generator().manual_seed(4)
+    Q = a.shape[0]
+    g_geometry = torch.randn(Q, 17, generator=g, dtype=torch.float64)
+    g_geometry[:, 9:11] = 0
+    g_projected = torch.randn(Q, 2, generator=g, dtype=torch.float64)
+    loss = (rec["geometry"] * g_geometry).sum() + (rec["projected_means"] * g_projected).sum()
+    g_app = g_op = None
+    if sh is not None:
+        g_app = torch.randn(Q, 18, generator=g, dtype=torch.float64)
+        g_op = torch.randn(Q, generator=g, dtype=torch.float64)
+        app = rec["appearance"][selected] if packed else rec["appearance"]
+        ops = rec["opacities"][selected] if packed else rec["opacities"]
+        loss = loss + (app * g_app).sum() + (ops * g_op).sum()
+    names = ["means", "quaternions", "scales", "view_matrices", "intrinsics"]
+    if sh is not None:
+        names += ["colors", "secondary_colors", "frequency_weights", "frequency_magnitudes",
+                  "phases", "opacities"]
+    expected = torch.autograd.grad(loss, [leaves[k] for k in names], allow_unused=True)
+    to_gpu = lambda t: None if t is None else t.float().to(DEVICE)  # noqa: E731
+    got = native.records_backward(
+        gpu["means"], gpu["quaternions"], gpu["scales"], gpu["view_matrices"],
+        gpu["intrinsics"], sh_args, sh, out["row_of_pair"], out["geometry"],
+        to_gpu(g_geometry), to_gpu(g_projected), to_gpu(g_app), to_gpu(g_op))
+    order = [0, 1, 2, 3, 4] + ([5, 6, 7, 8, 9, 10] if sh is not None else [])
+    for name, index, e in zip(names, order, expected):
+        e = torch.zeros_like(leaves[name]) if e is None else e
+        assert_gradients_close(got[index], e.reshape(got[index].shape), name, rel_norm=1e-4,
+                               elem=1e-4, rtol=1e-4)
