@@ -73,19 +73,22 @@ _SIGNATURES = {
         [_c_ptr] * 4 + [_c_i64, _c_int, _c_int, _c_ptr, _c_size, _c_ptr],
     ),
     "gs_find_ranges": (_c_int, [_c_ptr, _c_i64, _c_ptr, _c_i64, _c_ptr]),
+    "gs_render_workspace_size": (_c_size, [_c_i64, _c_int, _c_int]),
     "gs_render_forward": (
         _c_int,
         [_c_int]
         + [_c_ptr] * 7
         + [_c_i64, _c_int, _c_int, _c_float, _c_float]
-        + [_c_ptr] * 4,
+        + [_c_ptr] * 4
+        + [_c_size, _c_ptr],
     ),
     "gs_render_backward": (
         _c_int,
         [_c_int]
         + [_c_ptr] * 10
         + [_c_i64, _c_int, _c_int, _c_float, _c_float]
-        + [_c_ptr] * 5,
+        + [_c_ptr] * 5
+        + [_c_size, _c_ptr],
     ),
     "gs_profile_enable": (_c_int, [_c_int]),
     "gs_profile_read": (_c_int, [_c_int, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(_c_i64)]),
@@ -468,12 +471,13 @@ def rasterize_forward(
                 )
                 sorted_keys, point_list = sort_pairs(keys, values, 0, sort_end_bit(tiles))
         ranges = find_ranges(sorted_keys, tiles)
+        workspace = _workspace(lib.gs_render_workspace_size(images, width, height), device)
         _check(
             lib.gs_render_forward(
                 int(bool(neural)), _ptr(geometry), _ptr(appearance), _ptr(opacities),
                 _ptr(primitive_ids), _ptr(backgrounds), _ptr(point_list), _ptr(ranges), images,
                 width, height, near_plane, far_plane, _ptr(maps), _ptr(state),
-                _ptr(contributors), stream,
+                _ptr(contributors), _ptr(workspace), workspace.numel(), stream,
             )
         )
     return [maps, point_list, ranges, state, contributors]
@@ -500,12 +504,14 @@ def rasterize_backward(
         ga = torch.zeros_like(appearance)
         go = torch.zeros_like(opacities)
         gb = torch.zeros_like(backgrounds)
+        workspace = _workspace(lib.gs_render_workspace_size(images, width, height), device)
         _check(
             lib.gs_render_backward(
                 int(bool(neural)), _ptr(geometry), _ptr(appearance), _ptr(opacities),
                 _ptr(primitive_ids), _ptr(backgrounds), _ptr(point_list), _ptr(ranges),
                 _ptr(state), _ptr(contributors), _ptr(grad_maps), images, width, height,
-                near_plane, far_plane, _ptr(gg), _ptr(ga), _ptr(go), _ptr(gb), _stream(device),
+                near_plane, far_plane, _ptr(gg), _ptr(ga), _ptr(go), _ptr(gb),
+                _ptr(workspace), workspace.numel(), _stream(device),
             )
         )
     return [gg, ga, go, gb]

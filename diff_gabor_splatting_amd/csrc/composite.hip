@@ -275,20 +275,83 @@ __device__ __forceinline__ TilePixel tile_pixel(int tile, int width, int height,
   return t;
 }
 
+// Longest-first tile scheduling. Tiles are independent, so their dispatch
+// order changes no result; issuing the most expensive tiles first keeps a
+// heavy tile that would otherwise start late from setting the kernel's
+// length. One workgroup buckets tiles by log2(cost) (256 buckets, 1/16
+// octave) and writes the permutation heaviest bucket first.
+constexpr int kOrderBlock = 1024;
+constexpr int kOrderBuckets = 256;
+
+__device__ __forceinline__ int cost_bucket(int cost) {
+  if (cost <= 0) return 0;
+  return min(kOrderBuckets - 1, int(__log2f(float(cost) + 1.f) * 16.f));
+}
+
+// cost: per-tile cost, or null to use the tile's list length from ranges.
+__global__ __launch_bounds__(kOrderBlock) void tile_order_kernel(const int* __restrict__ cost,
+                                                                 const int2* __restrict__ ranges,
+                                                                 int tiles,
+                                                                 int* __restrict__ order) {
+  __shared__ int count[kOrderBuckets];
+  __shared__ int next[kOrderBuckets];
+  for (int b = threadIdx.x; b < kOrderBuckets; b += kOrderBlock) count[b] = 0;
+  __syncthreads();
+  for (int t = threadIdx.x; t < tiles; t += kOrderBlock) {
+    const int c = cost ? cost[t] : ranges[t].y - ranges[t].x;
+    atomicAdd(&count[cost_bucket(c)], 1);
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    int run = 0;
+    for (int b = kOrderBuckets - 1; b >= 0; --b) {
+      next[b] = run;
+      run += count[b];
+    }
+  }
+  __syncthreads();
+  for (int t = threadIdx.x; t < tiles; t += kOrderBlock) {
+    const int c = cost ? cost[t] : ranges[t].y - ranges[t].x;
+    order[atomicAdd(&next[cost_bucket(c)], 1)] = t;
+  }
+}
+
+// Largest contributor count of each tile (where the backward starts).
+__global__ __launch_bounds__(kTilePixels) void tile_last_kernel(int width, int height, int tw,
+                                                                int th,
+                                                                const int* __restrict__ contributors,
+                                                                int* __restrict__ tile_last) {
+  __shared__ int wave_max_last[kTilePixels / 64];
+  const int tile = blockIdx.x;
+  const int image = tile / (tw * th);
+  const int local = tile - image * (tw * th);
+  const int px = (local % tw) * kTile + (threadIdx.x & 15);
+  const int py = (local / tw) * kTile + (threadIdx.x >> 4);
+  const int last = (px < width && py < height)
+                       ? contributors[(int64_t(image) * height + py) * width + px]
+                       : 0;
+  const int w = wave_max(last);
+  if (lane_id() == 0) wave_max_last[threadIdx.x >> 6] = w;
+  __syncthreads();
+  if (threadIdx.x == 0)
+    tile_last[tile] = max(max(wave_max_last[0], wave_max_last[1]),
+                          max(wave_max_last[2], wave_max_last[3]));
+}
+
 template <bool Neural>
 __global__ __launch_bounds__(kTilePixels) void render_forward_kernel(
     int width, int height, int tw, int th, const float* __restrict__ geometry,
     const float* __restrict__ appearance, const float* __restrict__ opacities,
     const int64_t* __restrict__ primitive_ids, const float* __restrict__ backgrounds,
-    const int* __restrict__ point_list, const int2* __restrict__ ranges, float near_plane,
-    float far_plane, float* __restrict__ maps, float* __restrict__ state,
-    int* __restrict__ contributors) {
+    const int* __restrict__ point_list, const int2* __restrict__ ranges,
+    const int* __restrict__ order, float near_plane, float far_plane, float* __restrict__ maps,
+    float* __restrict__ state, int* __restrict__ contributors) {
   using L = Layout<Neural>;
   __shared__ __align__(16) float rows[kBatch * L::STRIDE];
   __shared__ __align__(16) float raw[kBatch * L::RAW_STRIDE];
   __shared__ int ids[kBatch];
   __shared__ int64_t prims[kBatch];
-  const int tile = blockIdx.x;
+  const int tile = order[blockIdx.x];
   const TilePixel tp = tile_pixel(tile, width, height, tw, th);
   const float x = float(tp.px), y = float(tp.py);
   bool done = !tp.inside;
@@ -413,6 +476,7 @@ __global__ __launch_bounds__(kTilePixels) void render_backward_kernel(
     const float* __restrict__ appearance, const float* __restrict__ opacities,
     const int64_t* __restrict__ primitive_ids, const float* __restrict__ backgrounds,
     const int* __restrict__ point_list, const int2* __restrict__ ranges,
+    const int* __restrict__ order, const int* __restrict__ tile_last,
     const float* __restrict__ state, const int* __restrict__ contributors,
     const float* __restrict__ grad_maps, float near_plane, float far_plane,
     float* __restrict__ grad_geometry, float* __restrict__ grad_appearance,
@@ -426,18 +490,15 @@ __global__ __launch_bounds__(kTilePixels) void render_backward_kernel(
   __shared__ float acc[kBatch * NP];
   __shared__ int ids[kBatch];
   __shared__ int64_t prims[kBatch];
-  __shared__ int wave_last[4];
   __shared__ float bg_acc[3];
-  const int lane = lane_id(), wave = threadIdx.x >> 6;
-  const int tile = blockIdx.x;
+  const int lane = lane_id();
+  const int tile = order[blockIdx.x];
   const TilePixel tp = tile_pixel(tile, width, height, tw, th);
   const float x = float(tp.px), y = float(tp.py);
   const int last = tp.inside ? contributors[tp.pixel] : 0;
 
   for (int i = threadIdx.x; i < kBatch * NP; i += kTilePixels) acc[i] = 0.f;
   if (threadIdx.x < 3) bg_acc[threadIdx.x] = 0.f;
-  const int wmax = wave_max(last);
-  if (lane == 0) wave_last[wave] = wmax;
 
   float go[kMaps];
 #pragma unroll
@@ -460,7 +521,7 @@ __global__ __launch_bounds__(kTilePixels) void render_backward_kernel(
     const int param = rs_param<3>(lane);
     if (param < 3 && total != 0.f) atomicAdd(&bg_acc[param], total);
   }
-  const int block_last = max(max(wave_last[0], wave_last[1]), max(wave_last[2], wave_last[3]));
+  const int block_last = tile_last[tile];
   const int2 range = ranges[tile];
   const float mscale = far_plane / (far_plane - near_plane);
   const float mnear = mscale * near_plane;
@@ -587,6 +648,22 @@ __global__ __launch_bounds__(kTilePixels) void render_backward_kernel(
     atomicAdd(grad_backgrounds + tp.image * 3 + threadIdx.x, bg_acc[threadIdx.x]);
 }
 
+struct RenderWorkspace {
+  int* order;      // [tiles]
+  int* tile_last;  // [tiles]
+  size_t bytes;
+};
+
+RenderWorkspace render_layout(void* base, int64_t tiles) {
+  RenderWorkspace w;
+  char* p = static_cast<char*>(base);
+  w.order = reinterpret_cast<int*>(p);
+  const size_t half = align_up(size_t(tiles) * sizeof(int), 256);
+  w.tile_last = reinterpret_cast<int*>(p + half);
+  w.bytes = 2 * half;
+  return w;
+}
+
 int check_render(int64_t images, int width, int height, float near_plane, float far_plane) {
   GS_REQUIRE(width > 0 && height > 0 && width < INT_MAX - kTile && height < INT_MAX - kTile,
              GS_ERR_ARGUMENT, "invalid image dimensions");
@@ -603,31 +680,43 @@ int check_render(int64_t images, int width, int height, float near_plane, float 
 
 extern "C" {
 
+size_t gs_render_workspace_size(int64_t images, int32_t width, int32_t height) {
+  if (images < 0 || width <= 0 || height <= 0) return 256;
+  return gs::render_layout(nullptr, images * gs::tiles_x(width) * gs::tiles_y(height)).bytes + 256;
+}
+
 int gs_render_forward(int32_t neural, const float* geometry, const float* appearance,
                       const float* opacities, const int64_t* primitive_ids,
                       const float* backgrounds, const int32_t* point_list,
                       const int32_t* ranges, int64_t images, int32_t width, int32_t height,
                       float near_plane, float far_plane, float* maps, float* state,
-                      int32_t* contributors, void* stream) {
+                      int32_t* contributors, void* workspace, size_t workspace_bytes,
+                      void* stream) {
   using namespace gs;
   clear_error();
   int status = check_render(images, width, height, near_plane, far_plane);
   if (status != GS_OK) return status;
   GS_REQUIRE(backgrounds && ranges && maps && state && contributors, GS_ERR_ARGUMENT,
              "null pointer passed to gs_render_forward");
+  const size_t need = gs_render_workspace_size(images, width, height);
+  GS_REQUIRE(workspace && workspace_bytes >= need, GS_ERR_WORKSPACE,
+             "render forward needs %zu workspace bytes, got %zu", need, workspace_bytes);
   hipStream_t s = static_cast<hipStream_t>(stream);
   ProfileScope prof(GS_PROF_RENDER_FWD, s);
   const int tw = tiles_x(width), th = tiles_y(height);
-  const unsigned blocks = unsigned(images * tw * th);
+  const int tiles = int(images * tw * th);
   const int2* r = reinterpret_cast<const int2*>(ranges);
+  RenderWorkspace w = render_layout(workspace, tiles);
+  tile_order_kernel<<<1, kOrderBlock, 0, s>>>(nullptr, r, tiles, w.order);
+  GS_LAUNCHED("tile_order_kernel");
   if (neural) {
-    render_forward_kernel<true><<<blocks, kTilePixels, 0, s>>>(
+    render_forward_kernel<true><<<unsigned(tiles), kTilePixels, 0, s>>>(
         width, height, tw, th, geometry, appearance, opacities, primitive_ids, backgrounds,
-        point_list, r, near_plane, far_plane, maps, state, contributors);
+        point_list, r, w.order, near_plane, far_plane, maps, state, contributors);
   } else {
-    render_forward_kernel<false><<<blocks, kTilePixels, 0, s>>>(
+    render_forward_kernel<false><<<unsigned(tiles), kTilePixels, 0, s>>>(
         width, height, tw, th, geometry, appearance, opacities, primitive_ids, backgrounds,
-        point_list, r, near_plane, far_plane, maps, state, contributors);
+        point_list, r, w.order, near_plane, far_plane, maps, state, contributors);
   }
   GS_LAUNCHED("render_forward_kernel");
   return GS_OK;
@@ -640,28 +729,38 @@ int gs_render_backward(int32_t neural, const float* geometry, const float* appea
                        const int32_t* contributors, const float* grad_maps, int64_t images,
                        int32_t width, int32_t height, float near_plane, float far_plane,
                        float* grad_geometry, float* grad_appearance, float* grad_opacities,
-                       float* grad_backgrounds, void* stream) {
+                       float* grad_backgrounds, void* workspace, size_t workspace_bytes,
+                       void* stream) {
   using namespace gs;
   clear_error();
   int status = check_render(images, width, height, near_plane, far_plane);
   if (status != GS_OK) return status;
   GS_REQUIRE(backgrounds && ranges && state && contributors && grad_maps && grad_backgrounds,
              GS_ERR_ARGUMENT, "null pointer passed to gs_render_backward");
+  const size_t need = gs_render_workspace_size(images, width, height);
+  GS_REQUIRE(workspace && workspace_bytes >= need, GS_ERR_WORKSPACE,
+             "render backward needs %zu workspace bytes, got %zu", need, workspace_bytes);
   hipStream_t s = static_cast<hipStream_t>(stream);
   ProfileScope prof(GS_PROF_RENDER_BWD, s);
   const int tw = tiles_x(width), th = tiles_y(height);
-  const unsigned blocks = unsigned(images * tw * th);
+  const int tiles = int(images * tw * th);
   const int2* r = reinterpret_cast<const int2*>(ranges);
+  RenderWorkspace w = render_layout(workspace, tiles);
+  tile_last_kernel<<<unsigned(tiles), kTilePixels, 0, s>>>(width, height, tw, th, contributors,
+                                                           w.tile_last);
+  GS_LAUNCHED("tile_last_kernel");
+  tile_order_kernel<<<1, kOrderBlock, 0, s>>>(w.tile_last, r, tiles, w.order);
+  GS_LAUNCHED("tile_order_kernel");
   if (neural) {
-    render_backward_kernel<true><<<blocks, kTilePixels, 0, s>>>(
+    render_backward_kernel<true><<<unsigned(tiles), kTilePixels, 0, s>>>(
         width, height, tw, th, geometry, appearance, opacities, primitive_ids, backgrounds,
-        point_list, r, state, contributors, grad_maps, near_plane, far_plane, grad_geometry,
-        grad_appearance, grad_opacities, grad_backgrounds);
+        point_list, r, w.order, w.tile_last, state, contributors, grad_maps, near_plane,
+        far_plane, grad_geometry, grad_appearance, grad_opacities, grad_backgrounds);
   } else {
-    render_backward_kernel<false><<<blocks, kTilePixels, 0, s>>>(
+    render_backward_kernel<false><<<unsigned(tiles), kTilePixels, 0, s>>>(
         width, height, tw, th, geometry, appearance, opacities, primitive_ids, backgrounds,
-        point_list, r, state, contributors, grad_maps, near_plane, far_plane, grad_geometry,
-        grad_appearance, grad_opacities, grad_backgrounds);
+        point_list, r, w.order, w.tile_last, state, contributors, grad_maps, near_plane,
+        far_plane, grad_geometry, grad_appearance, grad_opacities, grad_backgrounds);
   }
   GS_LAUNCHED("render_backward_kernel");
   return GS_OK;

@@ -198,12 +198,17 @@ int gs_find_ranges(const uint64_t* sorted_keys, int64_t m, int32_t* ranges, int6
  * rasterize.cu:230-399). neural = 0 selects the four-frequency Gabor
  * appearance (18 floats per row), 1 the per-surfel SIREN (57 floats).     */
 
+/* Scratch bytes for gs_render_forward / gs_render_backward: the tile
+ * dispatch order (heaviest tiles first) and per-tile contributor maxima. */
+size_t gs_render_workspace_size(int64_t images, int32_t width, int32_t height);
+
 int gs_render_forward(int32_t neural, const float* geometry, const float* appearance,
                       const float* opacities, const int64_t* primitive_ids,
                       const float* backgrounds, const int32_t* point_list,
                       const int32_t* ranges, int64_t images, int32_t width, int32_t height,
                       float near_plane, float far_plane, float* maps, float* state,
-                      int32_t* contributors, void* stream);
+                      int32_t* contributors, void* workspace, size_t workspace_bytes,
+                      void* stream);
 
 /* Gradients are ACCUMULATED (global float atomics) into grad_geometry
  * [Q,17], grad_appearance [P,A], grad_opacities [P], grad_backgrounds
@@ -215,7 +220,8 @@ int gs_render_backward(int32_t neural, const float* geometry, const float* appea
                        const int32_t* contributors, const float* grad_maps, int64_t images,
                        int32_t width, int32_t height, float near_plane, float far_plane,
                        float* grad_geometry, float* grad_appearance, float* grad_opacities,
-                       float* grad_backgrounds, void* stream);
+                       float* grad_backgrounds, void* workspace, size_t workspace_bytes,
+                       void* stream);
 
 /* ------------------------------------------------------------------ */
 /* Kernel timing for measurement: when enabled, each compositor / sort /
