@@ -27,6 +27,7 @@ import time
 import torch
 
 HBM_PEAK_GBS = 8000.0
+COPY_BYTES = 1 << 30
 FP32_VALU_PEAK_TFLOPS = 157.3
 
 CONFIGS = {
@@ -175,6 +176,9 @@ def main(argv=None):
     parser.add_argument("--cpu-crop", type=int, default=32, help="crop edge in pixels")
     parser.add_argument("--cpu-surfels", type=int, default=0,
                         help="surfels used by the CPU baseline (0 = all of the workload)")
+    parser.add_argument("--copy-calibration", action="store_true",
+                        help="only copy 1 GiB device-to-device three times and exit; the "
+                             "rocprof FETCH_SIZE/WRITE_SIZE of this copy scales the counters")
     args = parser.parse_args(argv)
     if args.gpus != 1:
         print(
@@ -186,6 +190,8 @@ def main(argv=None):
     if not torch.cuda.is_available():
         print("bench.py needs a GPU", file=sys.stderr)
         return 2
+    if args.copy_calibration:
+        return copy_calibration()
     from diff_gabor_splatting_amd import _native, rasterize_gabors, rasterize_neural_gabors
 
     cfg = CONFIGS[args.config]
@@ -273,7 +279,7 @@ def main(argv=None):
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 5),
-            "traffic": None,
+            "traffic": measured_traffic(dominant, cfg["name"]),
             "algorithmic_bytes_per_launch": algo,
             "avg_launch_ms": round(avg_ms, 4),
             "note": "compositors are VALU-bound (transcendentals); see valu_estimate",
@@ -285,6 +291,38 @@ def main(argv=None):
         result["cpu_baseline"] = cpu_baseline(cpu_values, cfg, args)
     print(json.dumps(result), flush=True)
     return 0
+
+
+def copy_calibration() -> int:
+    """A plain copy of known size: 1 GiB read and 1 GiB written per launch."""
+    source = torch.ones(COPY_BYTES // 4, device="cuda:0")
+    target = torch.empty_like(source)
+    torch.cuda.synchronize()
+    for _ in range(3):
+        target.copy_(source)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_bytes": COPY_BYTES, "launches": 3}), flush=True)
+    return 0
+
+
+def measured_traffic(kernel: str, workload: str):
+    """HBM bytes per launch of ``kernel`` from the committed rocprof counter summary.
+
+    The summary records FETCH_SIZE and WRITE_SIZE (KiB per dispatch) of the
+    same bench command and the factors that turn each into bytes, taken from
+    the copy calibration above. None when no summary covers this workload.
+    """
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
+                        f"{kernel}_traffic.json")
+    try:
+        with open(path) as handle:
+            summary = json.load(handle)
+    except (OSError, ValueError):
+        return None
+    if summary.get("kernel") != kernel or summary.get("workload") != workload:
+        return None
+    return int(summary["fetch_kib"] * 1024 * summary["fetch_factor"]
+               + summary["write_kib"] * 1024 * summary["write_factor"])
 
 
 def workload_stats(values, renderer, options):

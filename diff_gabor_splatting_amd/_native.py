@@ -73,19 +73,25 @@ _SIGNATURES = {
         [_c_ptr] * 4 + [_c_i64, _c_int, _c_int, _c_ptr, _c_size, _c_ptr],
     ),
     "gs_find_ranges": (_c_int, [_c_ptr, _c_i64, _c_ptr, _c_i64, _c_ptr]),
+    "gs_bin_workspace_size": (_c_size, [_c_i64, _c_i64]),
+    "gs_bin_tiles": (
+        _c_int,
+        [_c_ptr] * 4 + [_c_i64, _c_i64, _c_i64, _c_int, _c_int, _c_ptr, _c_ptr, _c_ptr, _c_size,
+                        _c_ptr],
+    ),
     "gs_render_workspace_size": (_c_size, [_c_i64, _c_int, _c_int]),
     "gs_render_forward": (
         _c_int,
         [_c_int]
         + [_c_ptr] * 7
         + [_c_i64, _c_int, _c_int, _c_float, _c_float]
-        + [_c_ptr] * 4
+        + [_c_ptr] * 5
         + [_c_size, _c_ptr],
     ),
     "gs_render_backward": (
         _c_int,
         [_c_int]
-        + [_c_ptr] * 10
+        + [_c_ptr] * 11
         + [_c_i64, _c_int, _c_int, _c_float, _c_float]
         + [_c_ptr] * 5
         + [_c_size, _c_ptr],
@@ -277,6 +283,27 @@ def find_ranges(sorted_keys: torch.Tensor, tiles: int) -> torch.Tensor:
     return ranges
 
 
+def bin_tiles(geometry, radii, image_ids, offsets, images, width, height, intersections):
+    """Depth-first binning: (point_list int32 [M], ranges int32 [I*tw*th, 2]).
+
+    Same result as emit_tiles + sort_pairs + find_ranges (rasterize.cu:43-69,
+    470-501) from the inclusive offsets of count_tiles."""
+    device = geometry.device
+    count = geometry.size(0)
+    tw, th = tile_grid(width, height)
+    point_list = torch.empty(intersections, dtype=torch.int32, device=device)
+    ranges = torch.empty((images * tw * th, 2), dtype=torch.int32, device=device)
+    workspace = _workspace(lib.gs_bin_workspace_size(count, intersections), device)
+    _check(
+        lib.gs_bin_tiles(
+            _ptr(geometry), _ptr(radii), _ptr(image_ids), _ptr(offsets), count, intersections,
+            images, width, height, _ptr(point_list), _ptr(ranges), _ptr(workspace),
+            workspace.numel(), _stream(device),
+        )
+    )
+    return point_list, ranges
+
+
 def pack_visible(radii: torch.Tensor, with_rows: bool = False):
     """Ascending indices of pairs with radii > 0 (int64). Synchronises once.
 
@@ -416,9 +443,59 @@ def records_backward(means, quaternions, scales, view_matrices, intrinsics, sh, 
 # Compositor operators (the reference's _C.rasterize_forward / backward).
 
 
+# Map channel groups in map order: rgb, alpha, depth, normals, distortion.
+MAP_GROUPS = (3, 1, 1, 3, 1)
+
+
+def split_map_groups(maps: torch.Tensor) -> list:
+    """The five channel-group views [..., k] of a [..., 9] map tensor."""
+    groups, first = [], 0
+    for k in MAP_GROUPS:
+        groups.append(maps[..., first:first + k])
+        first += k
+    return groups
+
+
+def _flat_pixel_stride(t: torch.Tensor):
+    """(pixel stride, channel stride) in elements when every pixel of the
+    [I,H,W,k] tensor t sits at p * pixel_stride from t's first element,
+    p = (i*H + y)*W + x; None otherwise."""
+    *pixel_dims, k = t.shape
+    strides = t.stride()
+    stride = None
+    inner = 1
+    for size, step in reversed(list(zip(pixel_dims, strides[:-1]))):
+        if size > 1:
+            if stride is None:
+                stride = step // inner if step % inner == 0 else -1
+            if stride < 0 or step != stride * inner:
+                return None
+        inner *= size
+    return (0 if stride is None else stride), (strides[-1] if k > 1 else 0)
+
+
+def _pixel_strided(t: torch.Tensor) -> torch.Tensor:
+    """t itself when its pixels are uniformly strided, else a contiguous copy."""
+    return t if _flat_pixel_stride(t) is not None else t.contiguous()
+
+
+def _map_group_args(groups, what: str):
+    """ctypes arrays (device pointers, [pixel, channel] strides) of the groups."""
+    pointers = (ctypes.c_void_p * len(MAP_GROUPS))()
+    strides = (ctypes.c_int64 * (2 * len(MAP_GROUPS)))()
+    for g, t in enumerate(groups):
+        if t is None:
+            continue
+        layout = _flat_pixel_stride(t)
+        _require(layout is not None, f"{what} must have uniformly strided pixels")
+        pointers[g] = t.data_ptr()
+        strides[2 * g], strides[2 * g + 1] = layout
+    return pointers, strides
+
+
 def rasterize_forward(
     geometry, appearance, opacities, primitive_ids, image_ids, radii, backgrounds,
-    width, height, neural, near_plane, far_plane,
+    width, height, neural, near_plane, far_plane, outputs=None,
 ):
     """Bin, sort and composite: returns [maps, point_list, ranges, state, contributors].
 
@@ -426,6 +503,10 @@ def rasterize_forward(
     checks, its one host synchronisation for the intersection count and its
     output shapes: maps [I,H,W,9], point_list int32 [M], ranges int32
     [I*tw*th, 2], state [I,H,W,3], contributors int32 [I,H,W].
+
+    ``outputs`` (an addition): five float32 tensors [I,H,W,k], k in
+    MAP_GROUPS, that receive the map channel groups instead of one maps
+    tensor; the first returned item is then that tuple.
     """
     _check_buffers(geometry, appearance, opacities, primitive_ids, backgrounds, neural)
     _require(
@@ -456,27 +537,40 @@ def rasterize_forward(
         tw, th = tile_grid(width, height)
         check_image_tiles(images, width, height)
         tiles = images * tw * th
-        maps = torch.empty((images, height, width, MAP_SIZE), dtype=torch.float32, device=device)
         state = torch.empty((images, height, width, 3), dtype=torch.float32, device=device)
         contributors = torch.empty((images, height, width), dtype=torch.int32, device=device)
-        point_list = torch.empty(0, dtype=torch.int32, device=device)
-        sorted_keys = torch.empty(0, dtype=torch.int64, device=device)
+        intersections = 0
+        offsets = None
         if count > 0:
             offsets = count_tiles(geometry, radii, width, height)
             intersections = int(offsets[-1].item())
             check_intersections(intersections)
-            if intersections > 0:
-                keys, values = emit_tiles(
-                    geometry, radii, image_ids, offsets, width, height, intersections
-                )
-                sorted_keys, point_list = sort_pairs(keys, values, 0, sort_end_bit(tiles))
-        ranges = find_ranges(sorted_keys, tiles)
+        point_list, ranges = bin_tiles(
+            geometry, radii, image_ids, offsets, images, width, height, intersections
+        )
+        if outputs is None:
+            maps = torch.empty((images, height, width, MAP_SIZE), dtype=torch.float32,
+                               device=device)
+            groups = split_map_groups(maps)
+        else:
+            groups = list(outputs)
+            _require(
+                len(groups) == len(MAP_GROUPS)
+                and all(
+                    t.shape == (images, height, width, k) and t.dtype == torch.float32
+                    and t.device == device
+                    for t, k in zip(groups, MAP_GROUPS)
+                ),
+                "invalid map outputs",
+            )
+            maps = tuple(groups)
+        data, strides = _map_group_args(groups, "map outputs")
         workspace = _workspace(lib.gs_render_workspace_size(images, width, height), device)
         _check(
             lib.gs_render_forward(
                 int(bool(neural)), _ptr(geometry), _ptr(appearance), _ptr(opacities),
                 _ptr(primitive_ids), _ptr(backgrounds), _ptr(point_list), _ptr(ranges), images,
-                width, height, near_plane, far_plane, _ptr(maps), _ptr(state),
+                width, height, near_plane, far_plane, data, strides, _ptr(state),
                 _ptr(contributors), _ptr(workspace), workspace.numel(), stream,
             )
         )
@@ -488,14 +582,32 @@ def rasterize_backward(
     contributors, grad_maps, width, height, neural, near_plane, far_plane,
 ):
     """Reverse compositing: returns [grad_geometry, grad_appearance, grad_opacities,
-    grad_backgrounds] (rasterize.cu:506-529)."""
+    grad_backgrounds] (rasterize.cu:506-529).
+
+    ``grad_maps`` is the reference's [I,H,W,9] tensor or (an addition) a
+    sequence of five per-group gradients [I,H,W,k] in MAP_GROUPS order, each
+    a tensor of any strides or None (zero); strided views are read in place.
+    """
     _check_buffers(geometry, appearance, opacities, primitive_ids, backgrounds, neural)
-    _check_float(grad_maps, geometry)
     device = geometry.device
     images = backgrounds.size(0)
+    if isinstance(grad_maps, torch.Tensor):
+        _check_float(grad_maps, geometry)
+        _require(grad_maps.shape == (images, height, width, MAP_SIZE), "invalid map gradient")
+        groups = split_map_groups(grad_maps)
+    else:
+        groups = list(grad_maps)
+        _require(
+            len(groups) == len(MAP_GROUPS)
+            and all(
+                g is None or (g.shape == (images, height, width, k) and g.dtype == torch.float32
+                              and g.device == device)
+                for g, k in zip(groups, MAP_GROUPS)
+            ),
+            "invalid map gradient",
+        )
     _require(
-        grad_maps.shape == (images, height, width, MAP_SIZE)
-        and state.shape == (images, height, width, 3)
+        state.shape == (images, height, width, 3)
         and contributors.shape == (images, height, width),
         "invalid saved compositor state",
     )
@@ -504,12 +616,14 @@ def rasterize_backward(
         ga = torch.zeros_like(appearance)
         go = torch.zeros_like(opacities)
         gb = torch.zeros_like(backgrounds)
+        groups = [g if g is None else _pixel_strided(g) for g in groups]
+        data, strides = _map_group_args(groups, "map gradients")
         workspace = _workspace(lib.gs_render_workspace_size(images, width, height), device)
         _check(
             lib.gs_render_backward(
                 int(bool(neural)), _ptr(geometry), _ptr(appearance), _ptr(opacities),
                 _ptr(primitive_ids), _ptr(backgrounds), _ptr(point_list), _ptr(ranges),
-                _ptr(state), _ptr(contributors), _ptr(grad_maps), images, width, height,
+                _ptr(state), _ptr(contributors), data, strides, images, width, height,
                 near_plane, far_plane, _ptr(gg), _ptr(ga), _ptr(go), _ptr(gb),
                 _ptr(workspace), workspace.numel(), _stream(device),
             )

@@ -7,11 +7,24 @@
 //   [0, tw] (and y likewise), evaluated left to right in float32,
 // so keys and ranges are bit-identical to the reference's for the same
 // geometry and radii. Counts are computed on the fly inside the scan
-// (never stored), then each pair emits one (key, value) per covered tile.
+// (never stored).
+//
+// Two binning pipelines give the same point list and ranges:
+//  * reference order (gs_emit_tiles, gs_sort_pairs, gs_find_ranges): every
+//    pair emits one 64-bit (image|tile) << 32 | depth-bits key per covered
+//    tile, and the M keys are radix-sorted on 32 + bits(tiles) bits;
+//  * depth first (gs_bin_tiles), used by the renderer: the Q pairs are
+//    stably sorted on their 32 depth bits, each pair then emits its tiles in
+//    that order as 32-bit tile ids, and a stable sort on only bits(tiles)
+//    bits groups them by tile. A stable sort of depth-ordered entries by tile
+//    leaves each tile's entries ordered by (depth bits, pair index) - the
+//    order of the 64-bit sort - while the M entries move through two 8-bit
+//    passes of 8 bytes instead of 5-6 passes of 12 bytes.
 #include <climits>
 
 #include "common.hpp"
 #include "scan.hpp"
+#include "sort.hpp"
 
 namespace gs {
 namespace {
@@ -126,6 +139,128 @@ __global__ __launch_bounds__(256) void find_ranges_kernel(int64_t m, int64_t til
   if (i == m - 1 && own) ranges[tile].y = int(m);
 }
 
+// Depth-first binning, step 1: per pair its tile count (from the inclusive
+// offsets) and its depth key; pairs without tiles sort last.
+__global__ __launch_bounds__(256) void depth_keys_kernel(int64_t count,
+                                                         const float* __restrict__ geometry,
+                                                         const int64_t* __restrict__ offsets,
+                                                         uint32_t* __restrict__ keys,
+                                                         int* __restrict__ values,
+                                                         int* __restrict__ counts) {
+  const int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x;
+  if (i >= count) return;
+  const int c = int(offsets[i] - (i == 0 ? 0 : offsets[i - 1]));
+  counts[i] = c;
+  keys[i] = c > 0 ? __float_as_uint(geometry[i * kGeometry + 8]) : 0xffffffffu;
+  values[i] = int(i);
+}
+
+struct SortedCountLoad {
+  const int* counts;
+  const int* order;
+  __device__ int64_t operator()(int64_t j) const { return counts[order[j]]; }
+};
+
+struct ExclusiveStartStore {
+  int* starts;
+  __device__ void operator()(int64_t j, int64_t inclusive, int64_t v) const {
+    starts[j] = int(inclusive - v);
+  }
+};
+
+// Step 3: the pair at depth rank j writes its tiles (row-major) as 32-bit
+// tile ids from starts[j] on. Writes past m (inconsistent offsets) are
+// dropped.
+__global__ __launch_bounds__(256) void emit_sorted_kernel(
+    int64_t count, int64_t m, int tw, int th, const float* __restrict__ geometry,
+    const int* __restrict__ radii, const int64_t* __restrict__ image_ids,
+    const int* __restrict__ order, const int* __restrict__ counts,
+    const int* __restrict__ starts, uint32_t* __restrict__ tile_ids,
+    int* __restrict__ values) {
+  const int64_t j = int64_t(blockIdx.x) * 256 + threadIdx.x;
+  if (j >= count) return;
+  const int p = order[j];
+  if (counts[p] <= 0) return;
+  const int r = radii[p];
+  const float* g = geometry + int64_t(p) * kGeometry;
+  const TileRect t = tile_rect(g[9], g[10], r, tw, th);
+  int64_t out = starts[j];
+  const uint32_t image_base = uint32_t(image_ids[p]) * uint32_t(tw) * uint32_t(th);
+  for (int y = t.y0; y < t.y1; ++y)
+    for (int x = t.x0; x < t.x1; ++x) {
+      if (out < m) {
+        tile_ids[out] = image_base + uint32_t(y * tw + x);
+        values[out] = p;
+      }
+      ++out;
+    }
+}
+
+__global__ __launch_bounds__(256) void find_tile_ranges_kernel(int64_t m, int64_t tiles,
+                                                               const uint32_t* __restrict__ ids,
+                                                               int2* __restrict__ ranges) {
+  const int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x;
+  if (i >= m) return;
+  const uint32_t tile = ids[i];
+  const bool own = tile < uint64_t(tiles);
+  if (i == 0) {
+    if (own) ranges[tile].x = 0;
+  } else {
+    const uint32_t previous = ids[i - 1];
+    if (tile != previous) {
+      if (previous < uint64_t(tiles)) ranges[previous].y = int(i);
+      if (own) ranges[tile].x = int(i);
+    }
+  }
+  if (i == m - 1 && own) ranges[tile].y = int(m);
+}
+
+struct BinWorkspace {
+  uint32_t* depth_keys;     // count
+  uint32_t* depth_sorted;   // count
+  int* pair_ids;            // count
+  int* order;               // count: pairs by (depth bits, pair index)
+  int* counts;              // count
+  int* starts;              // count: first entry of each depth rank
+  int64_t* scan_sums;
+  uint32_t* tile_ids;       // m, depth order
+  int* tile_values;         // m
+  uint32_t* tile_sorted;    // m, tile order
+  void* sort;               // radix sort scratch for max(count, m)
+  size_t bytes;
+};
+
+BinWorkspace bin_layout(void* base, int64_t count, int64_t m) {
+  BinWorkspace w;
+  char* p = static_cast<char*>(base);
+  size_t offset = 0;
+  auto take = [&](size_t bytes) {
+    char* at = p + offset;
+    offset = align_up(offset + bytes, 256);
+    return at;
+  };
+  w.depth_keys = reinterpret_cast<uint32_t*>(take(size_t(count) * 4));
+  w.depth_sorted = reinterpret_cast<uint32_t*>(take(size_t(count) * 4));
+  w.pair_ids = reinterpret_cast<int*>(take(size_t(count) * 4));
+  w.order = reinterpret_cast<int*>(take(size_t(count) * 4));
+  w.counts = reinterpret_cast<int*>(take(size_t(count) * 4));
+  w.starts = reinterpret_cast<int*>(take(size_t(count) * 4));
+  w.scan_sums = reinterpret_cast<int64_t*>(take(scan_workspace_bytes(count, 8)));
+  w.tile_ids = reinterpret_cast<uint32_t*>(take(size_t(m) * 4));
+  w.tile_values = reinterpret_cast<int*>(take(size_t(m) * 4));
+  w.tile_sorted = reinterpret_cast<uint32_t*>(take(size_t(m) * 4));
+  w.sort = take(radix_sort_workspace_bytes(count > m ? count : m, 4));
+  w.bytes = offset;
+  return w;
+}
+
+// Bits needed for ids below `tiles`.
+int id_bits(int64_t tiles) {
+  int bits = 0;
+  while (bits < 63 && (int64_t(1) << bits) < tiles) ++bits;
+  return bits;
+}
+
 }  // namespace
 }  // namespace gs
 
@@ -212,6 +347,72 @@ int gs_find_ranges(const uint64_t* sorted_keys, int64_t m, int32_t* ranges, int6
   GS_REQUIRE(sorted_keys, GS_ERR_ARGUMENT, "null sorted keys");
   find_ranges_kernel<<<unsigned(ceil_div(m, 256)), 256, 0, s>>>(m, tiles, sorted_keys, r);
   GS_LAUNCHED("find_ranges_kernel");
+  return GS_OK;
+}
+
+size_t gs_bin_workspace_size(int64_t count, int64_t m) {
+  if (count < 0) count = 0;
+  if (m < 0) m = 0;
+  return gs::bin_layout(nullptr, count, m).bytes + 256;
+}
+
+int gs_bin_tiles(const float* geometry, const int32_t* radii, const int64_t* image_ids,
+                 const int64_t* offsets, int64_t count, int64_t m, int64_t images,
+                 int32_t width, int32_t height, int32_t* point_list, int32_t* ranges,
+                 void* workspace, size_t workspace_bytes, void* stream) {
+  using namespace gs;
+  clear_error();
+  GS_REQUIRE(count >= 0 && count <= INT_MAX, GS_ERR_OVERFLOW, "too many projected primitives");
+  GS_REQUIRE(m >= 0 && m <= INT_MAX, GS_ERR_OVERFLOW, "tile intersection count exceeds int32");
+  GS_REQUIRE(width > 0 && height > 0 && images >= 0, GS_ERR_ARGUMENT,
+             "invalid image dimensions");
+  const int tw = tiles_x(width), th = tiles_y(height);
+  const int64_t tiles = images * int64_t(tw) * int64_t(th);
+  GS_REQUIRE(tiles <= INT_MAX, GS_ERR_OVERFLOW, "image tile count exceeds int32");
+  if (tiles == 0) return GS_OK;
+  GS_REQUIRE(ranges, GS_ERR_ARGUMENT, "null ranges");
+  const size_t need = gs_bin_workspace_size(count, m);
+  GS_REQUIRE(workspace && workspace_bytes >= need, GS_ERR_WORKSPACE,
+             "binning needs %zu workspace bytes, got %zu", need, workspace_bytes);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  int2* r = reinterpret_cast<int2*>(ranges);
+  BinWorkspace w = bin_layout(workspace, count, m);
+  {
+    ProfileScope prof(GS_PROF_BINNING, s);
+    fill_ranges_kernel<<<unsigned(ceil_div(tiles, 256)), 256, 0, s>>>(tiles, r);
+    GS_LAUNCHED("fill_ranges_kernel");
+  }
+  if (m == 0 || count == 0) return GS_OK;
+  GS_REQUIRE(geometry && radii && image_ids && offsets && point_list, GS_ERR_ARGUMENT,
+             "null pointer passed to gs_bin_tiles");
+  {
+    ProfileScope prof(GS_PROF_SORT, s);
+    depth_keys_kernel<<<unsigned(ceil_div(count, 256)), 256, 0, s>>>(
+        count, geometry, offsets, w.depth_keys, w.pair_ids, w.counts);
+    GS_LAUNCHED("depth_keys_kernel");
+    int status = radix_sort<uint32_t>(w.depth_keys, w.depth_sorted, w.pair_ids, w.order, count,
+                                      0, 32, w.sort, s);
+    if (status != GS_OK) return status;
+  }
+  {
+    ProfileScope prof(GS_PROF_BINNING, s);
+    int status = run_scan<int64_t>(count, SortedCountLoad{w.counts, w.order},
+                                   ExclusiveStartStore{w.starts}, w.scan_sums, s);
+    if (status != GS_OK) return status;
+    emit_sorted_kernel<<<unsigned(ceil_div(count, 256)), 256, 0, s>>>(
+        count, m, tw, th, geometry, radii, image_ids, w.order, w.counts, w.starts, w.tile_ids,
+        w.tile_values);
+    GS_LAUNCHED("emit_sorted_kernel");
+  }
+  {
+    ProfileScope prof(GS_PROF_SORT, s);
+    int status = radix_sort<uint32_t>(w.tile_ids, w.tile_sorted, w.tile_values, point_list, m,
+                                      0, id_bits(tiles), w.sort, s);
+    if (status != GS_OK) return status;
+  }
+  ProfileScope prof(GS_PROF_BINNING, s);
+  find_tile_ranges_kernel<<<unsigned(ceil_div(m, 256)), 256, 0, s>>>(m, tiles, w.tile_sorted, r);
+  GS_LAUNCHED("find_tile_ranges_kernel");
   return GS_OK;
 }
 

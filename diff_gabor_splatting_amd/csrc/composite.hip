@@ -275,6 +275,31 @@ __device__ __forceinline__ TilePixel tile_pixel(int tile, int width, int height,
   return t;
 }
 
+// The nine map channels in five groups - rgb (channels 0-2), alpha (3),
+// depth (4), normals (5-7), distortion (8) - each with its own base pointer
+// and element strides: channel k of group g at pixel p is
+// data[g][p * pixel_stride[g] + k * channel_stride[g]]. One [I,H,W,9]
+// tensor, five separate tensors and strided gradient views all fit.
+constexpr int kMapGroups = GS_MAP_GROUPS;
+__host__ __device__ constexpr int map_group(int c) {
+  return c < 3 ? 0 : c == 3 ? 1 : c == 4 ? 2 : c < 8 ? 3 : 4;
+}
+__host__ __device__ constexpr int map_group_first(int g) {
+  return g == 0 ? 0 : g == 1 ? 3 : g == 2 ? 4 : g == 3 ? 5 : 8;
+}
+
+template <typename T>
+struct MapGroups {
+  T* data[kMapGroups];
+  int64_t pixel_stride[kMapGroups];
+  int64_t channel_stride[kMapGroups];
+
+  __device__ __forceinline__ int64_t offset(int c, int64_t pixel) const {
+    const int g = map_group(c);
+    return pixel * pixel_stride[g] + int64_t(c - map_group_first(g)) * channel_stride[g];
+  }
+};
+
 // Longest-first tile scheduling. Tiles are independent, so their dispatch
 // order changes no result; issuing the most expensive tiles first keeps a
 // heavy tile that would otherwise start late from setting the kernel's
@@ -344,7 +369,7 @@ __global__ __launch_bounds__(kTilePixels) void render_forward_kernel(
     const float* __restrict__ appearance, const float* __restrict__ opacities,
     const int64_t* __restrict__ primitive_ids, const float* __restrict__ backgrounds,
     const int* __restrict__ point_list, const int2* __restrict__ ranges,
-    const int* __restrict__ order, float near_plane, float far_plane, float* __restrict__ maps,
+    const int* __restrict__ order, float near_plane, float far_plane, MapGroups<float> maps,
     float* __restrict__ state, int* __restrict__ contributors) {
   using L = Layout<Neural>;
   __shared__ __align__(16) float rows[kBatch * L::STRIDE];
@@ -399,7 +424,7 @@ __global__ __launch_bounds__(kTilePixels) void render_forward_kernel(
     for (int c = 0; c < 3; ++c) out[c] += T * backgrounds[tp.image * 3 + c];
     out[3] = 1.f - T;
 #pragma unroll
-    for (int c = 0; c < kMaps; ++c) maps[tp.pixel * kMaps + c] = out[c];
+    for (int c = 0; c < kMaps; ++c) maps.data[map_group(c)][maps.offset(c, tp.pixel)] = out[c];
     state[tp.pixel * 3 + 0] = T;
     state[tp.pixel * 3 + 1] = m1;
     state[tp.pixel * 3 + 2] = m2;
@@ -478,7 +503,7 @@ __global__ __launch_bounds__(kTilePixels) void render_backward_kernel(
     const int* __restrict__ point_list, const int2* __restrict__ ranges,
     const int* __restrict__ order, const int* __restrict__ tile_last,
     const float* __restrict__ state, const int* __restrict__ contributors,
-    const float* __restrict__ grad_maps, float near_plane, float far_plane,
+    MapGroups<const float> grad_maps, float near_plane, float far_plane,
     float* __restrict__ grad_geometry, float* __restrict__ grad_appearance,
     float* __restrict__ grad_opacities, float* __restrict__ grad_backgrounds) {
   using L = Layout<Neural>;
@@ -502,7 +527,10 @@ __global__ __launch_bounds__(kTilePixels) void render_backward_kernel(
 
   float go[kMaps];
 #pragma unroll
-  for (int c = 0; c < kMaps; ++c) go[c] = tp.inside ? grad_maps[tp.pixel * kMaps + c] : 0.f;
+  for (int c = 0; c < kMaps; ++c) {
+    const float* g = grad_maps.data[map_group(c)];  // null: no gradient for the group
+    go[c] = (tp.inside && g) ? g[grad_maps.offset(c, tp.pixel)] : 0.f;
+  }
   const float final_t = tp.inside ? state[tp.pixel * 3 + 0] : 0.f;
   const float m1 = tp.inside ? state[tp.pixel * 3 + 1] : 0.f;
   const float m2 = tp.inside ? state[tp.pixel * 3 + 2] : 0.f;
@@ -664,6 +692,17 @@ RenderWorkspace render_layout(void* base, int64_t tiles) {
   return w;
 }
 
+template <typename T>
+MapGroups<T> map_groups(T* const* data, const int64_t* strides) {
+  MapGroups<T> m;
+  for (int g = 0; g < kMapGroups; ++g) {
+    m.data[g] = data[g];
+    m.pixel_stride[g] = strides[2 * g];
+    m.channel_stride[g] = strides[2 * g + 1];
+  }
+  return m;
+}
+
 int check_render(int64_t images, int width, int height, float near_plane, float far_plane) {
   GS_REQUIRE(width > 0 && height > 0 && width < INT_MAX - kTile && height < INT_MAX - kTile,
              GS_ERR_ARGUMENT, "invalid image dimensions");
@@ -689,15 +728,18 @@ int gs_render_forward(int32_t neural, const float* geometry, const float* appear
                       const float* opacities, const int64_t* primitive_ids,
                       const float* backgrounds, const int32_t* point_list,
                       const int32_t* ranges, int64_t images, int32_t width, int32_t height,
-                      float near_plane, float far_plane, float* maps, float* state,
-                      int32_t* contributors, void* workspace, size_t workspace_bytes,
-                      void* stream) {
+                      float near_plane, float far_plane, float* const* maps,
+                      const int64_t* map_strides, float* state, int32_t* contributors,
+                      void* workspace, size_t workspace_bytes, void* stream) {
   using namespace gs;
   clear_error();
   int status = check_render(images, width, height, near_plane, far_plane);
   if (status != GS_OK) return status;
-  GS_REQUIRE(backgrounds && ranges && maps && state && contributors, GS_ERR_ARGUMENT,
-             "null pointer passed to gs_render_forward");
+  GS_REQUIRE(backgrounds && ranges && maps && map_strides && state && contributors,
+             GS_ERR_ARGUMENT, "null pointer passed to gs_render_forward");
+  for (int g = 0; g < kMapGroups; ++g)
+    GS_REQUIRE(maps[g], GS_ERR_ARGUMENT, "null map output group %d", g);
+  const MapGroups<float> out = map_groups(maps, map_strides);
   const size_t need = gs_render_workspace_size(images, width, height);
   GS_REQUIRE(workspace && workspace_bytes >= need, GS_ERR_WORKSPACE,
              "render forward needs %zu workspace bytes, got %zu", need, workspace_bytes);
@@ -712,11 +754,11 @@ int gs_render_forward(int32_t neural, const float* geometry, const float* appear
   if (neural) {
     render_forward_kernel<true><<<unsigned(tiles), kTilePixels, 0, s>>>(
         width, height, tw, th, geometry, appearance, opacities, primitive_ids, backgrounds,
-        point_list, r, w.order, near_plane, far_plane, maps, state, contributors);
+        point_list, r, w.order, near_plane, far_plane, out, state, contributors);
   } else {
     render_forward_kernel<false><<<unsigned(tiles), kTilePixels, 0, s>>>(
         width, height, tw, th, geometry, appearance, opacities, primitive_ids, backgrounds,
-        point_list, r, w.order, near_plane, far_plane, maps, state, contributors);
+        point_list, r, w.order, near_plane, far_plane, out, state, contributors);
   }
   GS_LAUNCHED("render_forward_kernel");
   return GS_OK;
@@ -726,7 +768,8 @@ int gs_render_backward(int32_t neural, const float* geometry, const float* appea
                        const float* opacities, const int64_t* primitive_ids,
                        const float* backgrounds, const int32_t* point_list,
                        const int32_t* ranges, const float* state,
-                       const int32_t* contributors, const float* grad_maps, int64_t images,
+                       const int32_t* contributors, const float* const* grad_maps,
+                       const int64_t* grad_map_strides, int64_t images,
                        int32_t width, int32_t height, float near_plane, float far_plane,
                        float* grad_geometry, float* grad_appearance, float* grad_opacities,
                        float* grad_backgrounds, void* workspace, size_t workspace_bytes,
@@ -735,8 +778,10 @@ int gs_render_backward(int32_t neural, const float* geometry, const float* appea
   clear_error();
   int status = check_render(images, width, height, near_plane, far_plane);
   if (status != GS_OK) return status;
-  GS_REQUIRE(backgrounds && ranges && state && contributors && grad_maps && grad_backgrounds,
+  GS_REQUIRE(backgrounds && ranges && state && contributors && grad_maps && grad_map_strides &&
+                 grad_backgrounds,
              GS_ERR_ARGUMENT, "null pointer passed to gs_render_backward");
+  const MapGroups<const float> grads = map_groups(grad_maps, grad_map_strides);
   const size_t need = gs_render_workspace_size(images, width, height);
   GS_REQUIRE(workspace && workspace_bytes >= need, GS_ERR_WORKSPACE,
              "render backward needs %zu workspace bytes, got %zu", need, workspace_bytes);
@@ -754,12 +799,12 @@ int gs_render_backward(int32_t neural, const float* geometry, const float* appea
   if (neural) {
     render_backward_kernel<true><<<unsigned(tiles), kTilePixels, 0, s>>>(
         width, height, tw, th, geometry, appearance, opacities, primitive_ids, backgrounds,
-        point_list, r, w.order, w.tile_last, state, contributors, grad_maps, near_plane,
+        point_list, r, w.order, w.tile_last, state, contributors, grads, near_plane,
         far_plane, grad_geometry, grad_appearance, grad_opacities, grad_backgrounds);
   } else {
     render_backward_kernel<false><<<unsigned(tiles), kTilePixels, 0, s>>>(
         width, height, tw, th, geometry, appearance, opacities, primitive_ids, backgrounds,
-        point_list, r, w.order, w.tile_last, state, contributors, grad_maps, near_plane,
+        point_list, r, w.order, w.tile_last, state, contributors, grads, near_plane,
         far_plane, grad_geometry, grad_appearance, grad_opacities, grad_backgrounds);
   }
   GS_LAUNCHED("render_backward_kernel");

@@ -1,4 +1,5 @@
-// Kernel 3: stable LSD radix sort of (uint64 key, int32 value) pairs.
+// Kernel 3: stable LSD radix sort of (uint32 or uint64 key, int32 value)
+// pairs.
 //
 // Each pass sorts on an 8-bit digit (Merrill & Grimshaw's reduce-then-scan
 // formulation, without decoupled look-back, so no workgroup ever waits on
@@ -11,10 +12,11 @@
 //                 via ballots, per-wave running counters in LDS), stages the
 //                 locally sorted span in LDS and writes it out so that runs
 //                 of equal digits land on consecutive addresses.
-// Only bits [begin_bit, end_bit) are sorted; the rasterizer passes
-// end_bit = 32 + bits(image*tile count), since higher key bits are zero,
-// which leaves the result identical to a full 64-bit sort.
-#include "common.hpp"
+// Only bits [begin_bit, end_bit) are sorted. gs_sort_pairs sorts the
+// reference's 64-bit image|tile|depth keys; the depth-first binning
+// pipeline (binning.hip) sorts 32-bit depth keys and then 32-bit tile ids.
+#include "sort.hpp"
+
 #include "scan.hpp"
 
 namespace gs {
@@ -28,18 +30,44 @@ constexpr int kWaveSpan = 64 * kSortItems;             // keys per wave
 constexpr int kDigitBits = 8;
 constexpr int kBins = 1 << kDigitBits;
 
+// Lanes of the wave whose `digit` equals this lane's: one ballot per digit
+// bit, intersected. Invalid lanes belong to no group.
+__device__ __forceinline__ uint64_t digit_peers(uint32_t digit, bool valid, int bits) {
+  uint64_t peers = __ballot(valid);
+  for (int b = 0; b < bits; ++b) {
+    const bool set = (digit >> b) & 1u;
+    const uint64_t vote = __ballot(set);
+    peers &= set ? vote : ~vote;
+  }
+  return peers;
+}
+
+// Digit histogram of one span, stored digit-major: counts[digit * spans +
+// span]. Each wave counts into its own LDS row; per key group the lowest
+// lane adds the group's size, so skewed digits cost no atomic conflicts.
+template <typename Key>
 __global__ __launch_bounds__(kSortBlock) void radix_upsweep_kernel(
-    const uint64_t* __restrict__ keys, int64_t m, int shift, uint32_t mask,
+    const Key* __restrict__ keys, int64_t m, int shift, int bits,
     uint32_t* __restrict__ counts, int64_t spans) {
   __shared__ uint32_t hist[kSortWaves][kBins];
-  const int wave = threadIdx.x >> 6;
+  const int lane = __lane_id(), wave = threadIdx.x >> 6;
   for (int i = threadIdx.x; i < kSortWaves * kBins; i += kSortBlock) (&hist[0][0])[i] = 0;
   __syncthreads();
-  const int64_t base = int64_t(blockIdx.x) * kSortSpan;
-#pragma unroll 4
-  for (int r = 0; r < kSortItems; ++r) {
-    const int64_t i = base + int64_t(r) * kSortBlock + threadIdx.x;
-    if (i < m) atomicAdd(&hist[wave][uint32_t(keys[i] >> shift) & mask], 1u);
+  const uint32_t mask = (1u << bits) - 1u;
+  const uint64_t lanes_below = (uint64_t(1) << lane) - 1;
+  const int64_t wave_base = int64_t(blockIdx.x) * kSortSpan + int64_t(wave) * kWaveSpan;
+  Key key[kSortItems];
+#pragma unroll
+  for (int it = 0; it < kSortItems; ++it) {
+    const int64_t i = wave_base + int64_t(it) * 64 + lane;
+    key[it] = i < m ? keys[i] : Key(0);
+  }
+#pragma unroll
+  for (int it = 0; it < kSortItems; ++it) {
+    const bool valid = wave_base + int64_t(it) * 64 + lane < m;
+    const uint32_t digit = uint32_t(key[it] >> shift) & mask;
+    const uint64_t peers = digit_peers(digit, valid, bits);
+    if (valid && (peers & lanes_below) == 0) hist[wave][digit] += uint32_t(__popcll(peers));
   }
   __syncthreads();
   const int d = threadIdx.x;  // kSortBlock == kBins
@@ -61,14 +89,15 @@ struct ExclusiveStore {
   }
 };
 
+template <typename Key>
 __global__ __launch_bounds__(kSortBlock) void radix_downsweep_kernel(
-    const uint64_t* __restrict__ keys_in, const int* __restrict__ values_in,
-    uint64_t* __restrict__ keys_out, int* __restrict__ values_out, int64_t m, int shift,
-    int bits, const uint32_t* __restrict__ offsets, int64_t spans) {
+    const Key* __restrict__ keys_in, const int* __restrict__ values_in,
+    Key* __restrict__ keys_out, int* __restrict__ values_out, int64_t m, int shift, int bits,
+    const uint32_t* __restrict__ offsets, int64_t spans) {
   __shared__ uint32_t running[kSortWaves][kBins];   // per-wave digit counters
   __shared__ uint32_t local_start[kBins];           // first local slot per digit
   __shared__ uint32_t global_start[kBins];          // first output slot per digit
-  __shared__ uint64_t stage_keys[kSortSpan];
+  __shared__ Key stage_keys[kSortSpan];
   __shared__ int stage_values[kSortSpan];
   const int lane = __lane_id(), wave = threadIdx.x >> 6;
   const uint32_t mask = (1u << bits) - 1u;
@@ -77,23 +106,21 @@ __global__ __launch_bounds__(kSortBlock) void radix_downsweep_kernel(
 
   const int64_t wave_base = int64_t(blockIdx.x) * kSortSpan + int64_t(wave) * kWaveSpan;
   const uint64_t lanes_below = (uint64_t(1) << lane) - 1;
-  uint64_t key[kSortItems];
+  Key key[kSortItems];
   int value[kSortItems];
   uint32_t rank[kSortItems];
 #pragma unroll
   for (int it = 0; it < kSortItems; ++it) {
     const int64_t i = wave_base + int64_t(it) * 64 + lane;
     const bool valid = i < m;
-    key[it] = valid ? keys_in[i] : 0;
+    key[it] = valid ? keys_in[i] : Key(0);
     value[it] = valid ? values_in[i] : 0;
+  }
+#pragma unroll
+  for (int it = 0; it < kSortItems; ++it) {
+    const bool valid = wave_base + int64_t(it) * 64 + lane < m;
     const uint32_t digit = uint32_t(key[it] >> shift) & mask;
-    // Lanes holding the same digit: intersect one ballot per digit bit.
-    uint64_t peers = __ballot(valid);
-    for (int b = 0; b < bits; ++b) {
-      const bool set = (digit >> b) & 1u;
-      const uint64_t vote = __ballot(set);
-      peers &= set ? vote : ~vote;
-    }
+    const uint64_t peers = digit_peers(digit, valid, bits);
     rank[it] = 0;
     if (valid) {
       const uint32_t before = running[wave][digit];
@@ -146,7 +173,7 @@ __global__ __launch_bounds__(kSortBlock) void radix_downsweep_kernel(
   const int64_t span_base = int64_t(blockIdx.x) * kSortSpan;
   const int span_count = int(min<int64_t>(kSortSpan, m - span_base));
   for (int slot = threadIdx.x; slot < span_count; slot += kSortBlock) {
-    const uint64_t k = stage_keys[slot];
+    const Key k = stage_keys[slot];
     const uint32_t digit = uint32_t(k >> shift) & mask;
     const int64_t dst = int64_t(global_start[digit]) + (slot - int64_t(local_start[digit]));
     if (dst >= 0 && dst < m) {  // always true when the histograms are consistent
@@ -156,9 +183,10 @@ __global__ __launch_bounds__(kSortBlock) void radix_downsweep_kernel(
   }
 }
 
-__global__ __launch_bounds__(256) void copy_pairs_kernel(const uint64_t* __restrict__ keys_in,
+template <typename Key>
+__global__ __launch_bounds__(256) void copy_pairs_kernel(const Key* __restrict__ keys_in,
                                                          const int* __restrict__ values_in,
-                                                         uint64_t* __restrict__ keys_out,
+                                                         Key* __restrict__ keys_out,
                                                          int* __restrict__ values_out, int64_t m) {
   const int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x;
   if (i < m) {
@@ -170,12 +198,12 @@ __global__ __launch_bounds__(256) void copy_pairs_kernel(const uint64_t* __restr
 struct SortWorkspace {
   uint32_t* counts;       // kBins * spans
   uint32_t* scan_sums;    // scan span totals
-  uint64_t* keys_tmp;     // m
+  void* keys_tmp;         // m keys
   int* values_tmp;        // m
   size_t bytes;
 };
 
-SortWorkspace layout(void* base, int64_t m) {
+SortWorkspace layout(void* base, int64_t m, int key_bytes) {
   const int64_t spans = ceil_div(m, kSortSpan);
   const int64_t count_items = int64_t(kBins) * spans;
   SortWorkspace w;
@@ -185,8 +213,8 @@ SortWorkspace layout(void* base, int64_t m) {
   offset = align_up(offset + size_t(count_items) * 4, 256);
   w.scan_sums = reinterpret_cast<uint32_t*>(p + offset);
   offset = align_up(offset + scan_workspace_bytes(count_items, 4), 256);
-  w.keys_tmp = reinterpret_cast<uint64_t*>(p + offset);
-  offset = align_up(offset + size_t(m) * 8, 256);
+  w.keys_tmp = p + offset;
+  offset = align_up(offset + size_t(m) * size_t(key_bytes), 256);
   w.values_tmp = reinterpret_cast<int*>(p + offset);
   offset = align_up(offset + size_t(m) * 4, 256);
   w.bytes = offset;
@@ -194,14 +222,59 @@ SortWorkspace layout(void* base, int64_t m) {
 }
 
 }  // namespace
+
+size_t radix_sort_workspace_bytes(int64_t m, int key_bytes) {
+  if (m < 0) m = 0;
+  return layout(nullptr, m, key_bytes).bytes + 256;
+}
+
+template <typename Key>
+int radix_sort(const Key* keys_in, Key* keys_out, const int* values_in, int* values_out,
+               int64_t m, int begin_bit, int end_bit, void* workspace, hipStream_t s) {
+  if (m == 0) return GS_OK;
+  SortWorkspace w = layout(workspace, m, int(sizeof(Key)));
+  const int64_t spans = ceil_div(m, kSortSpan);
+  const int passes = int(ceil_div(end_bit - begin_bit, kDigitBits));
+  if (passes == 0) {
+    copy_pairs_kernel<Key><<<unsigned(ceil_div(m, 256)), 256, 0, s>>>(keys_in, values_in,
+                                                                       keys_out, values_out, m);
+    GS_LAUNCHED("copy_pairs_kernel");
+    return GS_OK;
+  }
+  // Ping-pong so that the last pass writes the caller's output.
+  const Key* src_k = keys_in;
+  const int* src_v = values_in;
+  for (int pass = 0; pass < passes; ++pass) {
+    const int shift = begin_bit + pass * kDigitBits;
+    const int bits = min(kDigitBits, end_bit - shift);
+    const bool to_output = ((passes - 1 - pass) % 2) == 0;
+    Key* dst_k = to_output ? keys_out : static_cast<Key*>(w.keys_tmp);
+    int* dst_v = to_output ? values_out : w.values_tmp;
+    radix_upsweep_kernel<Key><<<unsigned(spans), kSortBlock, 0, s>>>(src_k, m, shift, bits,
+                                                                      w.counts, spans);
+    GS_LAUNCHED("radix_upsweep_kernel");
+    int status = run_scan<uint32_t>(int64_t(kBins) * spans, CountLoad{w.counts},
+                                    ExclusiveStore{w.counts}, w.scan_sums, s);
+    if (status != GS_OK) return status;
+    radix_downsweep_kernel<Key><<<unsigned(spans), kSortBlock, 0, s>>>(
+        src_k, src_v, dst_k, dst_v, m, shift, bits, w.counts, spans);
+    GS_LAUNCHED("radix_downsweep_kernel");
+    src_k = dst_k;
+    src_v = dst_v;
+  }
+  return GS_OK;
+}
+
+template int radix_sort<uint32_t>(const uint32_t*, uint32_t*, const int*, int*, int64_t, int,
+                                  int, void*, hipStream_t);
+template int radix_sort<uint64_t>(const uint64_t*, uint64_t*, const int*, int*, int64_t, int,
+                                  int, void*, hipStream_t);
+
 }  // namespace gs
 
 extern "C" {
 
-size_t gs_sort_workspace_size(int64_t m) {
-  if (m < 0) m = 0;
-  return gs::layout(nullptr, m).bytes + 256;
-}
+size_t gs_sort_workspace_size(int64_t m) { return gs::radix_sort_workspace_bytes(m, 8); }
 
 int gs_sort_pairs(const uint64_t* keys_in, uint64_t* keys_out, const int32_t* values_in,
                   int32_t* values_out, int64_t m, int32_t begin_bit, int32_t end_bit,
@@ -221,38 +294,8 @@ int gs_sort_pairs(const uint64_t* keys_in, uint64_t* keys_out, const int32_t* va
              "sort needs %zu workspace bytes, got %zu", need, workspace_bytes);
   hipStream_t s = static_cast<hipStream_t>(stream);
   ProfileScope prof(GS_PROF_SORT, s);
-  SortWorkspace w = layout(workspace, m);
-  const int64_t spans = ceil_div(m, kSortSpan);
-  const int passes = int(ceil_div(end_bit - begin_bit, kDigitBits));
-  if (passes == 0) {
-    copy_pairs_kernel<<<unsigned(ceil_div(m, 256)), 256, 0, s>>>(keys_in, values_in, keys_out,
-                                                                  values_out, m);
-    GS_LAUNCHED("copy_pairs_kernel");
-    return GS_OK;
-  }
-  // Ping-pong so that the last pass writes the caller's output.
-  const uint64_t* src_k = keys_in;
-  const int* src_v = values_in;
-  for (int pass = 0; pass < passes; ++pass) {
-    const int shift = begin_bit + pass * kDigitBits;
-    const int bits = min(kDigitBits, end_bit - shift);
-    const bool to_output = ((passes - 1 - pass) % 2) == 0;
-    uint64_t* dst_k = to_output ? keys_out : w.keys_tmp;
-    int* dst_v = to_output ? values_out : w.values_tmp;
-    radix_upsweep_kernel<<<unsigned(spans), kSortBlock, 0, s>>>(src_k, m, shift,
-                                                                 (1u << bits) - 1u, w.counts,
-                                                                 spans);
-    GS_LAUNCHED("radix_upsweep_kernel");
-    int status = run_scan<uint32_t>(int64_t(kBins) * spans, CountLoad{w.counts},
-                                    ExclusiveStore{w.counts}, w.scan_sums, s);
-    if (status != GS_OK) return status;
-    radix_downsweep_kernel<<<unsigned(spans), kSortBlock, 0, s>>>(
-        src_k, src_v, dst_k, dst_v, m, shift, bits, w.counts, spans);
-    GS_LAUNCHED("radix_downsweep_kernel");
-    src_k = dst_k;
-    src_v = dst_v;
-  }
-  return GS_OK;
+  return radix_sort<uint64_t>(keys_in, keys_out, values_in, values_out, m, begin_bit, end_bit,
+                              workspace, s);
 }
 
 }  // extern "C"

@@ -26,6 +26,14 @@ class Composite(torch.autograd.Function):
     columns; it is an input only so that the compositor's screen-filter
     gradient (gg[:, 9:11]) reaches it as an autograd node, as in the
     reference where ``meta["projected_means"]`` feeds the geometry.
+
+    The nine map channels come out as five tensors - rgb, alpha, depth,
+    normals, distortion, each [I,H,W,k] - rather than as slices of one
+    [I,H,W,9] tensor: autograd would scatter the gradient of every slice
+    into its own zero-filled full-size tensor and sum the five, while here
+    the backward kernel reads each group's gradient where it lies (for a
+    loss over ``torch.cat`` of the maps, straight out of the concatenated
+    gradient) and missing groups cost nothing.
     """
 
     @staticmethod
@@ -33,9 +41,14 @@ class Composite(torch.autograd.Function):
         ctx: Any, geometry, projected_means, appearance, opacities, primitive_ids, image_ids,
         radii, backgrounds, width, height, neural, near_plane, far_plane,
     ):
-        maps, points, ranges, state, contributors = _native.rasterize_forward(
+        images = backgrounds.size(0)
+        outputs = tuple(
+            torch.empty((images, height, width, k), dtype=torch.float32, device=geometry.device)
+            for k in _native.MAP_GROUPS
+        )
+        _, points, ranges, state, contributors = _native.rasterize_forward(
             geometry, appearance, opacities, primitive_ids, image_ids, radii, backgrounds,
-            width, height, neural, near_plane, far_plane,
+            width, height, neural, near_plane, far_plane, outputs=outputs,
         )
         # Binning and early termination are discrete: only the saved sorted
         # lists and per-pixel state are needed to replay the tiles backwards.
@@ -44,13 +57,14 @@ class Composite(torch.autograd.Function):
             contributors,
         )
         ctx.options = (width, height, neural, near_plane, far_plane)
-        return maps
+        ctx.set_materialize_grads(False)
+        return outputs
 
     @staticmethod
     @once_differentiable
-    def backward(ctx: Any, grad_maps):
+    def backward(ctx: Any, *grad_groups):
         gg, ga, go, gb = _native.rasterize_backward(
-            *ctx.saved_tensors, grad_maps.contiguous(), *ctx.options
+            *ctx.saved_tensors, list(grad_groups), *ctx.options
         )
         return gg, gg[:, 9:11], ga, go, None, None, None, gb, None, None, None, None, None
 
@@ -365,7 +379,7 @@ def render(
         opacity_rows = opacities.reshape(scenes * n)
     if not packed:
         selected = torch.arange(pairs, device=device)
-    maps = Composite.apply(
+    rgb, alpha, depth, normals, distortion = Composite.apply(
         geometry,
         projected_means,
         parameters,
@@ -379,7 +393,8 @@ def render(
         neural,
         near_plane,
         far_plane,
-    ).reshape(batch + (cameras, height, width, 9))
+    )
+    image_shape = batch + (cameras, height, width)
     stride = max(n, 1)
     meta = {
         "radii": row_radii if packed else dense_radii.reshape(batch + (cameras, n)),
@@ -388,11 +403,11 @@ def render(
         "camera_ids": selected // stride % cameras,
         "primitive_ids": selected % stride,
         "packed": packed,
-        "accumulated_depth": maps[..., 4:5],
-        "normals": maps[..., 5:8],
-        "distortion": maps[..., 8:9],
+        "accumulated_depth": depth.reshape(image_shape + (1,)),
+        "normals": normals.reshape(image_shape + (3,)),
+        "distortion": distortion.reshape(image_shape + (1,)),
     }
-    return maps[..., :3], maps[..., 3:4], meta
+    return rgb.reshape(image_shape + (3,)), alpha.reshape(image_shape + (1,)), meta
 
 
 def rasterize_gabors(

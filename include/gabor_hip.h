@@ -193,6 +193,22 @@ int gs_sort_pairs(const uint64_t* keys_in, uint64_t* keys_out, const int32_t* va
 int gs_find_ranges(const uint64_t* sorted_keys, int64_t m, int32_t* ranges, int64_t tiles,
                    void* stream);
 
+/* Scratch bytes for gs_bin_tiles over `count` pairs and m intersections. */
+size_t gs_bin_workspace_size(int64_t count, int64_t m);
+
+/* Depth-first binning: the point list and ranges of emitTiles + the 64-bit
+ * cub::DeviceRadixSort::SortPairs + findRanges (rasterize.cu:43-69,
+ * 470-501), bit for bit, from the offsets of gs_count_tiles (m =
+ * offsets[count-1]). Pairs are stably sorted on their depth bits, emit their
+ * tiles in that order as 32-bit tile ids, and a stable sort on bits(tiles)
+ * bits groups the entries by tile, which leaves each tile ordered by (depth
+ * bits, pair index) as the 64-bit sort does. point_list [m] int32, ranges
+ * [images*tw*th, 2] int32 (tiles without entries get (0,0)). */
+int gs_bin_tiles(const float* geometry, const int32_t* radii, const int64_t* image_ids,
+                 const int64_t* offsets, int64_t count, int64_t m, int64_t images,
+                 int32_t width, int32_t height, int32_t* point_list, int32_t* ranges,
+                 void* workspace, size_t workspace_bytes, void* stream);
+
 /* ------------------------------------------------------------------ */
 /* Kernels 4 and 5: tile compositors (renderForward / renderBackward,
  * rasterize.cu:230-399). neural = 0 selects the four-frequency Gabor
@@ -202,22 +218,35 @@ int gs_find_ranges(const uint64_t* sorted_keys, int64_t m, int32_t* ranges, int6
  * dispatch order (heaviest tiles first) and per-tile contributor maxima. */
 size_t gs_render_workspace_size(int64_t images, int32_t width, int32_t height);
 
+/* Map outputs and map gradients are passed as five channel groups in map
+ * order - rgb (channels 0-2), alpha (3), depth (4), normals (5-7),
+ * distortion (8) - as a host array of GS_MAP_GROUPS device pointers plus a
+ * host array of 2*GS_MAP_GROUPS element strides (pixel stride, channel
+ * stride per group): channel k of group g at pixel p is
+ * data[g][p * strides[2g] + k * strides[2g+1]], p = (image*H + y)*W + x.
+ * One [I,H,W,9] tensor is data[g] = maps + first channel of g with strides
+ * (9, 1); separate [I,H,W,k] tensors and strided gradient views of a
+ * caller's loss are passed the same way, without copies. */
+#define GS_MAP_GROUPS 5
+
 int gs_render_forward(int32_t neural, const float* geometry, const float* appearance,
                       const float* opacities, const int64_t* primitive_ids,
                       const float* backgrounds, const int32_t* point_list,
                       const int32_t* ranges, int64_t images, int32_t width, int32_t height,
-                      float near_plane, float far_plane, float* maps, float* state,
-                      int32_t* contributors, void* workspace, size_t workspace_bytes,
-                      void* stream);
+                      float near_plane, float far_plane, float* const* maps,
+                      const int64_t* map_strides, float* state, int32_t* contributors,
+                      void* workspace, size_t workspace_bytes, void* stream);
 
 /* Gradients are ACCUMULATED (global float atomics) into grad_geometry
  * [Q,17], grad_appearance [P,A], grad_opacities [P], grad_backgrounds
- * [I,3]; the caller zero-initialises them. */
+ * [I,3]; the caller zero-initialises them. grad_maps uses the channel-group
+ * form above; a null group pointer means a zero gradient for that group. */
 int gs_render_backward(int32_t neural, const float* geometry, const float* appearance,
                        const float* opacities, const int64_t* primitive_ids,
                        const float* backgrounds, const int32_t* point_list,
                        const int32_t* ranges, const float* state,
-                       const int32_t* contributors, const float* grad_maps, int64_t images,
+                       const int32_t* contributors, const float* const* grad_maps,
+                       const int64_t* grad_map_strides, int64_t images,
                        int32_t width, int32_t height, float near_plane, float far_plane,
                        float* grad_geometry, float* grad_appearance, float* grad_opacities,
                        float* grad_backgrounds, void* workspace, size_t workspace_bytes,

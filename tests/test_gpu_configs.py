@@ -53,10 +53,12 @@ def capture_forward(function, values, opts):
     captured = {}
     original = _native.rasterize_forward
 
-    def spy(*args):
+    def spy(*args, **kwargs):
         captured["args"] = args
-        captured["out"] = original(*args)
-        return captured["out"]
+        out = original(*args, **kwargs)
+        maps = out[0] if isinstance(out[0], torch.Tensor) else torch.cat(out[0], -1)
+        captured["out"] = [maps, *out[1:]]
+        return out
 
     _native.rasterize_forward = spy
     try:

@@ -78,6 +78,33 @@ def test_binning_pipeline_is_bit_exact(native, seed, q, width, height, images):
     np.testing.assert_array_equal(to_u64(sorted_keys), ok_keys)
     np.testing.assert_array_equal(point_list.cpu().numpy(), ok_list)
     np.testing.assert_array_equal(native.find_ranges(sorted_keys, tiles).cpu().numpy(), ok_ranges)
+    # The renderer's depth-first pipeline gives the same list and ranges.
+    bin_list, bin_ranges = native.bin_tiles(g, r, ids, offsets, images, width, height, m)
+    np.testing.assert_array_equal(bin_list.cpu().numpy(), ok_list)
+    np.testing.assert_array_equal(bin_ranges.cpu().numpy(), ok_ranges)
+
+
+@pytest.mark.parametrize("seed, q, width, height, images, culled", [
+    (5, 3000, 64, 64, 1, True),         # every pair culled: m = 0
+    (6, 40_000, 1920, 1080, 40, False),  # 326,400 tiles: 19 id bits, three tile passes
+    (7, 300_000, 512, 512, 32, False),  # config-3-like: 32,768 tiles, 1e5+ equal depths
+])
+def test_depth_first_binning_is_bit_exact(native, seed, q, width, height, images, culled):
+    geometry, radii, image_ids = random_geometry(seed, q, width, height, images)
+    if culled:
+        radii[:] = np.minimum(radii, 0)
+    if seed == 7:
+        geometry[:, 8] = np.float32(3.5)  # all depths tie: order is by pair index
+        geometry[::5, 8] = np.float32(2.0)
+    g, r, ids = (torch.from_numpy(a).to(DEVICE) for a in (geometry, radii, image_ids))
+    offsets = native.count_tiles(g, r, width, height)
+    m = int(offsets[-1])
+    assert (m == 0) == culled
+    _, ok_list, ok_ranges = oracle_binning.bin_pairs(geometry, radii, image_ids, images, width,
+                                                     height)
+    point_list, ranges = native.bin_tiles(g, r, ids, offsets, images, width, height, m)
+    np.testing.assert_array_equal(point_list.cpu().numpy(), ok_list)
+    np.testing.assert_array_equal(ranges.cpu().numpy(), ok_ranges)
 
 
 def test_ranges_of_empty_list_are_zero(native):
