@@ -73,10 +73,15 @@ _SIGNATURES = {
         [_c_ptr] * 4 + [_c_i64, _c_int, _c_int, _c_ptr, _c_size, _c_ptr],
     ),
     "gs_find_ranges": (_c_int, [_c_ptr, _c_i64, _c_ptr, _c_i64, _c_ptr]),
-    "gs_bin_workspace_size": (_c_size, [_c_i64, _c_i64]),
+    "gs_bin_order_workspace_size": (_c_size, [_c_i64]),
+    "gs_bin_order": (
+        _c_int,
+        [_c_ptr] * 3 + [_c_i64, _c_int, _c_int] + [_c_ptr] * 5 + [_c_size, _c_ptr],
+    ),
+    "gs_bin_tiles_workspace_size": (_c_size, [_c_i64]),
     "gs_bin_tiles": (
         _c_int,
-        [_c_ptr] * 4 + [_c_i64, _c_i64, _c_i64, _c_int, _c_int, _c_ptr, _c_ptr, _c_ptr, _c_size,
+        [_c_ptr] * 3 + [_c_i64, _c_i64, _c_i64, _c_int, _c_int, _c_ptr, _c_ptr, _c_ptr, _c_size,
                         _c_ptr],
     ),
     "gs_render_workspace_size": (_c_size, [_c_i64, _c_int, _c_int]),
@@ -283,25 +288,54 @@ def find_ranges(sorted_keys: torch.Tensor, tiles: int) -> torch.Tensor:
     return ranges
 
 
-def bin_tiles(geometry, radii, image_ids, offsets, images, width, height, intersections):
-    """Depth-first binning: (point_list int32 [M], ranges int32 [I*tw*th, 2]).
-
-    Same result as emit_tiles + sort_pairs + find_ranges (rasterize.cu:43-69,
-    470-501) from the inclusive offsets of count_tiles."""
+def bin_order(geometry: torch.Tensor, radii: torch.Tensor, image_ids: torch.Tensor,
+              width: int, height: int):
+    """Depth-first binning, stage 1: (order int32 [Q], starts int64 [Q], rects
+    int32 [Q, 4], intersections int64 [1] on the device). No host
+    synchronisation."""
     device = geometry.device
     count = geometry.size(0)
+    order = torch.empty(count, dtype=torch.int32, device=device)
+    starts = torch.empty(count, dtype=torch.int64, device=device)
+    rects = torch.empty((count, 4), dtype=torch.int32, device=device)
+    total = torch.empty(1, dtype=torch.int64, device=device)
+    workspace = _workspace(lib.gs_bin_order_workspace_size(count), device)
+    _check(
+        lib.gs_bin_order(
+            _ptr(geometry), _ptr(radii), _ptr(image_ids), count, width, height, _ptr(order),
+            _ptr(starts), _ptr(rects), _ptr(total), _ptr(workspace), workspace.numel(),
+            _stream(device),
+        )
+    )
+    return order, starts, rects, total
+
+
+def bin_tiles(order, starts, rects, images, width, height, intersections):
+    """Depth-first binning, stage 2: (point_list int32 [M], ranges int32
+    [I*tw*th, 2]), the result of emit_tiles + sort_pairs + find_ranges
+    (rasterize.cu:43-69, 470-501)."""
+    device = order.device
+    count = order.size(0)
     tw, th = tile_grid(width, height)
     point_list = torch.empty(intersections, dtype=torch.int32, device=device)
     ranges = torch.empty((images * tw * th, 2), dtype=torch.int32, device=device)
-    workspace = _workspace(lib.gs_bin_workspace_size(count, intersections), device)
+    workspace = _workspace(lib.gs_bin_tiles_workspace_size(intersections), device)
     _check(
         lib.gs_bin_tiles(
-            _ptr(geometry), _ptr(radii), _ptr(image_ids), _ptr(offsets), count, intersections,
-            images, width, height, _ptr(point_list), _ptr(ranges), _ptr(workspace),
-            workspace.numel(), _stream(device),
+            _ptr(order), _ptr(starts), _ptr(rects), count, intersections, images, width, height,
+            _ptr(point_list), _ptr(ranges), _ptr(workspace), workspace.numel(), _stream(device),
         )
     )
     return point_list, ranges
+
+
+def bin_depth_first(geometry, radii, image_ids, images, width, height):
+    """Both binning stages with the one host synchronisation for M between
+    them (rasterize.cu:466-469): (point_list, ranges)."""
+    order, starts, rects, total = bin_order(geometry, radii, image_ids, width, height)
+    intersections = int(total.item())
+    check_intersections(intersections)
+    return bin_tiles(order, starts, rects, images, width, height, intersections)
 
 
 def pack_visible(radii: torch.Tensor, with_rows: bool = False):
@@ -539,15 +573,7 @@ def rasterize_forward(
         tiles = images * tw * th
         state = torch.empty((images, height, width, 3), dtype=torch.float32, device=device)
         contributors = torch.empty((images, height, width), dtype=torch.int32, device=device)
-        intersections = 0
-        offsets = None
-        if count > 0:
-            offsets = count_tiles(geometry, radii, width, height)
-            intersections = int(offsets[-1].item())
-            check_intersections(intersections)
-        point_list, ranges = bin_tiles(
-            geometry, radii, image_ids, offsets, images, width, height, intersections
-        )
+        point_list, ranges = bin_depth_first(geometry, radii, image_ids, images, width, height)
         if outputs is None:
             maps = torch.empty((images, height, width, MAP_SIZE), dtype=torch.float32,
                                device=device)

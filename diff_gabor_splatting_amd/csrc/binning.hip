@@ -13,10 +13,11 @@
 //  * reference order (gs_emit_tiles, gs_sort_pairs, gs_find_ranges): every
 //    pair emits one 64-bit (image|tile) << 32 | depth-bits key per covered
 //    tile, and the M keys are radix-sorted on 32 + bits(tiles) bits;
-//  * depth first (gs_bin_tiles), used by the renderer: the Q pairs are
-//    stably sorted on their 32 depth bits, each pair then emits its tiles in
-//    that order as 32-bit tile ids, and a stable sort on only bits(tiles)
-//    bits groups them by tile. A stable sort of depth-ordered entries by tile
+//  * depth first (gs_bin_order, then gs_bin_tiles), used by the renderer:
+//    the Q pairs are stably sorted on their 32 depth bits, each pair then
+//    emits its tiles in that order as 32-bit tile ids, and a stable sort on
+//    only bits(tiles) bits groups them by tile. The first stage needs no
+//    intersection count, so it runs while the host waits for M. A stable sort of depth-ordered entries by tile
 //    leaves each tile's entries ordered by (depth bits, pair index) - the
 //    order of the 64-bit sort - while the M entries move through two 8-bit
 //    passes of 8 bytes instead of 5-6 passes of 12 bytes.
@@ -139,20 +140,37 @@ __global__ __launch_bounds__(256) void find_ranges_kernel(int64_t m, int64_t til
   if (i == m - 1 && own) ranges[tile].y = int(m);
 }
 
-// Depth-first binning, step 1: per pair its tile count (from the inclusive
-// offsets) and its depth key; pairs without tiles sort last.
-__global__ __launch_bounds__(256) void depth_keys_kernel(int64_t count,
-                                                         const float* __restrict__ geometry,
-                                                         const int64_t* __restrict__ offsets,
-                                                         uint32_t* __restrict__ keys,
-                                                         int* __restrict__ values,
-                                                         int* __restrict__ counts) {
+// Depth-first binning, stage 1, step 1: each pair's tile rectangle
+// (x0, y0, width, first tile id of its image) for stage 2, its tile count
+// (the rectangle area of countTiles) and its depth key; pairs without
+// tiles sort last.
+__global__ __launch_bounds__(256) void pair_keys_kernel(int64_t count, int tw, int th,
+                                                        const float* __restrict__ geometry,
+                                                        const int* __restrict__ radii,
+                                                        const int64_t* __restrict__ image_ids,
+                                                        uint32_t* __restrict__ keys,
+                                                        int* __restrict__ values,
+                                                        int* __restrict__ counts,
+                                                        int4* __restrict__ rects) {
   const int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x;
   if (i >= count) return;
-  const int c = int(offsets[i] - (i == 0 ? 0 : offsets[i - 1]));
+  const int r = radii[i];
+  int c = 0;
+  uint32_t key = 0xffffffffu;
+  int4 rect = make_int4(0, 0, 1, 0);
+  if (r > 0) {
+    const float* g = geometry + i * kGeometry;
+    const TileRect t = tile_rect(g[9], g[10], r, tw, th);
+    c = (t.x1 - t.x0) * (t.y1 - t.y0);
+    if (c > 0) {
+      key = __float_as_uint(g[8]);
+      rect = make_int4(t.x0, t.y0, t.x1 - t.x0, int(image_ids[i] * int64_t(tw) * th));
+    }
+  }
   counts[i] = c;
-  keys[i] = c > 0 ? __float_as_uint(geometry[i * kGeometry + 8]) : 0xffffffffu;
+  keys[i] = key;
   values[i] = int(i);
+  rects[i] = rect;
 }
 
 struct SortedCountLoad {
@@ -161,39 +179,77 @@ struct SortedCountLoad {
   __device__ int64_t operator()(int64_t j) const { return counts[order[j]]; }
 };
 
+// starts[j] = entries of all lower depth ranks; the total is M.
 struct ExclusiveStartStore {
-  int* starts;
+  int64_t* starts;
+  int64_t* total;
+  int64_t count;
   __device__ void operator()(int64_t j, int64_t inclusive, int64_t v) const {
-    starts[j] = int(inclusive - v);
+    starts[j] = inclusive - v;
+    if (j == count - 1) *total = inclusive;
   }
 };
 
-// Step 3: the pair at depth rank j writes its tiles (row-major) as 32-bit
-// tile ids from starts[j] on. Writes past m (inconsistent offsets) are
-// dropped.
+// Stage 2, step 1: lane j of the grid takes depth rank j (its pair, the
+// rectangle stage 1 stored and its first entry) and writes the pair's tiles
+// row-major as 32-bit tile ids plus the pair index. A pair with at most
+// kLaneTiles tiles is written by its own lane; larger ones are written by
+// the whole wave, one pair at a time, 64 consecutive entries per store, so
+// that a few huge rectangles do not serialise their wave. Entries at or
+// past m (inconsistent inputs) are dropped.
+constexpr int kLaneTiles = 32;
+
 __global__ __launch_bounds__(256) void emit_sorted_kernel(
-    int64_t count, int64_t m, int tw, int th, const float* __restrict__ geometry,
-    const int* __restrict__ radii, const int64_t* __restrict__ image_ids,
-    const int* __restrict__ order, const int* __restrict__ counts,
-    const int* __restrict__ starts, uint32_t* __restrict__ tile_ids,
-    int* __restrict__ values) {
+    int64_t count, int64_t m, int tw, const int* __restrict__ order,
+    const int64_t* __restrict__ starts, const int4* __restrict__ rects,
+    uint32_t* __restrict__ tile_ids, int* __restrict__ values) {
+  const int lane = __lane_id();
   const int64_t j = int64_t(blockIdx.x) * 256 + threadIdx.x;
-  if (j >= count) return;
-  const int p = order[j];
-  if (counts[p] <= 0) return;
-  const int r = radii[p];
-  const float* g = geometry + int64_t(p) * kGeometry;
-  const TileRect t = tile_rect(g[9], g[10], r, tw, th);
-  int64_t out = starts[j];
-  const uint32_t image_base = uint32_t(image_ids[p]) * uint32_t(tw) * uint32_t(th);
-  for (int y = t.y0; y < t.y1; ++y)
-    for (int x = t.x0; x < t.x1; ++x) {
-      if (out < m) {
-        tile_ids[out] = image_base + uint32_t(y * tw + x);
-        values[out] = p;
+  if (j - lane >= count) return;  // uniform per wave
+  int pair = 0, area = 0;
+  int4 rect = make_int4(0, 0, 1, 0);
+  int64_t first = 0;
+  if (j < count) {
+    pair = order[j];
+    first = starts[j];
+    const int64_t next = j + 1 < count ? starts[j + 1] : m;
+    area = int(min<int64_t>(next - first, INT_MAX));
+    if (area > 0) rect = rects[pair];
+  }
+  if (area <= kLaneTiles) {
+    int x = rect.x, y = rect.y;
+    for (int k = 0; k < area; ++k) {
+      const int64_t e = first + k;
+      if (e < m) {
+        tile_ids[e] = uint32_t(rect.w) + uint32_t(y * tw + x);
+        values[e] = pair;
       }
-      ++out;
+      if (++x == rect.x + rect.z) {
+        x = rect.x;
+        ++y;
+      }
     }
+  }
+  uint64_t big = __ballot(area > kLaneTiles);
+  while (big) {  // uniform: every lane sees the same mask
+    const int owner = __ffsll((unsigned long long)big) - 1;
+    big &= big - 1;
+    const int64_t owner_first = __shfl(first, owner);
+    const int owner_area = __shfl(area, owner);
+    const int owner_x0 = __shfl(rect.x, owner);
+    const int owner_y0 = __shfl(rect.y, owner);
+    const int owner_span = __shfl(rect.z, owner);
+    const uint32_t owner_base = uint32_t(__shfl(rect.w, owner));
+    const int owner_pair = __shfl(pair, owner);
+    for (int k = lane; k < owner_area; k += 64) {
+      const int64_t e = owner_first + k;
+      if (e < m) {
+        tile_ids[e] = owner_base + uint32_t((owner_y0 + k / owner_span) * tw + owner_x0 +
+                                            k % owner_span);
+        values[e] = owner_pair;
+      }
+    }
+  }
 }
 
 __global__ __launch_bounds__(256) void find_tile_ranges_kernel(int64_t m, int64_t tiles,
@@ -215,23 +271,18 @@ __global__ __launch_bounds__(256) void find_tile_ranges_kernel(int64_t m, int64_
   if (i == m - 1 && own) ranges[tile].y = int(m);
 }
 
-struct BinWorkspace {
-  uint32_t* depth_keys;     // count
-  uint32_t* depth_sorted;   // count
-  int* pair_ids;            // count
-  int* order;               // count: pairs by (depth bits, pair index)
-  int* counts;              // count
-  int* starts;              // count: first entry of each depth rank
+struct OrderWorkspace {
+  uint32_t* keys;      // count
+  uint32_t* sorted;    // count
+  int* pair_ids;       // count
+  int* counts;         // count
   int64_t* scan_sums;
-  uint32_t* tile_ids;       // m, depth order
-  int* tile_values;         // m
-  uint32_t* tile_sorted;    // m, tile order
-  void* sort;               // radix sort scratch for max(count, m)
+  void* sort;          // radix sort scratch for count keys
   size_t bytes;
 };
 
-BinWorkspace bin_layout(void* base, int64_t count, int64_t m) {
-  BinWorkspace w;
+OrderWorkspace order_layout(void* base, int64_t count) {
+  OrderWorkspace w;
   char* p = static_cast<char*>(base);
   size_t offset = 0;
   auto take = [&](size_t bytes) {
@@ -239,17 +290,37 @@ BinWorkspace bin_layout(void* base, int64_t count, int64_t m) {
     offset = align_up(offset + bytes, 256);
     return at;
   };
-  w.depth_keys = reinterpret_cast<uint32_t*>(take(size_t(count) * 4));
-  w.depth_sorted = reinterpret_cast<uint32_t*>(take(size_t(count) * 4));
+  w.keys = reinterpret_cast<uint32_t*>(take(size_t(count) * 4));
+  w.sorted = reinterpret_cast<uint32_t*>(take(size_t(count) * 4));
   w.pair_ids = reinterpret_cast<int*>(take(size_t(count) * 4));
-  w.order = reinterpret_cast<int*>(take(size_t(count) * 4));
   w.counts = reinterpret_cast<int*>(take(size_t(count) * 4));
-  w.starts = reinterpret_cast<int*>(take(size_t(count) * 4));
   w.scan_sums = reinterpret_cast<int64_t*>(take(scan_workspace_bytes(count, 8)));
+  w.sort = take(radix_sort_workspace_bytes(count, 4));
+  w.bytes = offset;
+  return w;
+}
+
+struct TilesWorkspace {
+  uint32_t* tile_ids;     // m, depth order
+  int* tile_values;       // m
+  uint32_t* tile_sorted;  // m, tile order
+  void* sort;             // radix sort scratch for m keys
+  size_t bytes;
+};
+
+TilesWorkspace tiles_layout(void* base, int64_t m) {
+  TilesWorkspace w;
+  char* p = static_cast<char*>(base);
+  size_t offset = 0;
+  auto take = [&](size_t bytes) {
+    char* at = p + offset;
+    offset = align_up(offset + bytes, 256);
+    return at;
+  };
   w.tile_ids = reinterpret_cast<uint32_t*>(take(size_t(m) * 4));
   w.tile_values = reinterpret_cast<int*>(take(size_t(m) * 4));
   w.tile_sorted = reinterpret_cast<uint32_t*>(take(size_t(m) * 4));
-  w.sort = take(radix_sort_workspace_bytes(count > m ? count : m, 4));
+  w.sort = take(radix_sort_workspace_bytes(m, 4));
   w.bytes = offset;
   return w;
 }
@@ -350,16 +421,59 @@ int gs_find_ranges(const uint64_t* sorted_keys, int64_t m, int32_t* ranges, int6
   return GS_OK;
 }
 
-size_t gs_bin_workspace_size(int64_t count, int64_t m) {
+size_t gs_bin_order_workspace_size(int64_t count) {
   if (count < 0) count = 0;
-  if (m < 0) m = 0;
-  return gs::bin_layout(nullptr, count, m).bytes + 256;
+  return gs::order_layout(nullptr, count).bytes + 256;
 }
 
-int gs_bin_tiles(const float* geometry, const int32_t* radii, const int64_t* image_ids,
-                 const int64_t* offsets, int64_t count, int64_t m, int64_t images,
-                 int32_t width, int32_t height, int32_t* point_list, int32_t* ranges,
-                 void* workspace, size_t workspace_bytes, void* stream) {
+int gs_bin_order(const float* geometry, const int32_t* radii, const int64_t* image_ids,
+                 int64_t count, int32_t width, int32_t height, int32_t* order, int64_t* starts,
+                 int32_t* rects, int64_t* intersections, void* workspace,
+                 size_t workspace_bytes, void* stream) {
+  using namespace gs;
+  clear_error();
+  GS_REQUIRE(count >= 0 && count <= INT_MAX, GS_ERR_OVERFLOW, "too many projected primitives");
+  GS_REQUIRE(width > 0 && height > 0, GS_ERR_ARGUMENT, "invalid image dimensions");
+  GS_REQUIRE(intersections, GS_ERR_ARGUMENT, "null intersections");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (count == 0) {
+    zero_count_kernel<<<1, 64, 0, s>>>(intersections);
+    GS_LAUNCHED("zero_count_kernel");
+    return GS_OK;
+  }
+  GS_REQUIRE(geometry && radii && image_ids && order && starts && rects, GS_ERR_ARGUMENT,
+             "null pointer passed to gs_bin_order");
+  const size_t need = gs_bin_order_workspace_size(count);
+  GS_REQUIRE(workspace && workspace_bytes >= need, GS_ERR_WORKSPACE,
+             "binning needs %zu workspace bytes, got %zu", need, workspace_bytes);
+  OrderWorkspace w = order_layout(workspace, count);
+  {
+    ProfileScope prof(GS_PROF_BINNING, s);
+    pair_keys_kernel<<<unsigned(ceil_div(count, 256)), 256, 0, s>>>(
+        count, tiles_x(width), tiles_y(height), geometry, radii, image_ids, w.keys, w.pair_ids,
+        w.counts, reinterpret_cast<int4*>(rects));
+    GS_LAUNCHED("pair_keys_kernel");
+  }
+  {
+    ProfileScope prof(GS_PROF_SORT, s);
+    int status = radix_sort<uint32_t>(w.keys, w.sorted, w.pair_ids, order, count, 0, 32, w.sort,
+                                      s);
+    if (status != GS_OK) return status;
+  }
+  ProfileScope prof(GS_PROF_BINNING, s);
+  return run_scan<int64_t>(count, SortedCountLoad{w.counts, order},
+                           ExclusiveStartStore{starts, intersections, count}, w.scan_sums, s);
+}
+
+size_t gs_bin_tiles_workspace_size(int64_t m) {
+  if (m < 0) m = 0;
+  return gs::tiles_layout(nullptr, m).bytes + 256;
+}
+
+int gs_bin_tiles(const int32_t* order, const int64_t* starts, const int32_t* rects,
+                 int64_t count, int64_t m, int64_t images, int32_t width, int32_t height,
+                 int32_t* point_list, int32_t* ranges, void* workspace, size_t workspace_bytes,
+                 void* stream) {
   using namespace gs;
   clear_error();
   GS_REQUIRE(count >= 0 && count <= INT_MAX, GS_ERR_OVERFLOW, "too many projected primitives");
@@ -371,36 +485,21 @@ int gs_bin_tiles(const float* geometry, const int32_t* radii, const int64_t* ima
   GS_REQUIRE(tiles <= INT_MAX, GS_ERR_OVERFLOW, "image tile count exceeds int32");
   if (tiles == 0) return GS_OK;
   GS_REQUIRE(ranges, GS_ERR_ARGUMENT, "null ranges");
-  const size_t need = gs_bin_workspace_size(count, m);
+  const size_t need = gs_bin_tiles_workspace_size(m);
   GS_REQUIRE(workspace && workspace_bytes >= need, GS_ERR_WORKSPACE,
              "binning needs %zu workspace bytes, got %zu", need, workspace_bytes);
   hipStream_t s = static_cast<hipStream_t>(stream);
   int2* r = reinterpret_cast<int2*>(ranges);
-  BinWorkspace w = bin_layout(workspace, count, m);
+  TilesWorkspace w = tiles_layout(workspace, m);
   {
     ProfileScope prof(GS_PROF_BINNING, s);
     fill_ranges_kernel<<<unsigned(ceil_div(tiles, 256)), 256, 0, s>>>(tiles, r);
     GS_LAUNCHED("fill_ranges_kernel");
-  }
-  if (m == 0 || count == 0) return GS_OK;
-  GS_REQUIRE(geometry && radii && image_ids && offsets && point_list, GS_ERR_ARGUMENT,
-             "null pointer passed to gs_bin_tiles");
-  {
-    ProfileScope prof(GS_PROF_SORT, s);
-    depth_keys_kernel<<<unsigned(ceil_div(count, 256)), 256, 0, s>>>(
-        count, geometry, offsets, w.depth_keys, w.pair_ids, w.counts);
-    GS_LAUNCHED("depth_keys_kernel");
-    int status = radix_sort<uint32_t>(w.depth_keys, w.depth_sorted, w.pair_ids, w.order, count,
-                                      0, 32, w.sort, s);
-    if (status != GS_OK) return status;
-  }
-  {
-    ProfileScope prof(GS_PROF_BINNING, s);
-    int status = run_scan<int64_t>(count, SortedCountLoad{w.counts, w.order},
-                                   ExclusiveStartStore{w.starts}, w.scan_sums, s);
-    if (status != GS_OK) return status;
+    if (m == 0 || count == 0) return GS_OK;
+    GS_REQUIRE(order && starts && rects && point_list, GS_ERR_ARGUMENT,
+               "null pointer passed to gs_bin_tiles");
     emit_sorted_kernel<<<unsigned(ceil_div(count, 256)), 256, 0, s>>>(
-        count, m, tw, th, geometry, radii, image_ids, w.order, w.counts, w.starts, w.tile_ids,
+        count, m, tw, order, starts, reinterpret_cast<const int4*>(rects), w.tile_ids,
         w.tile_values);
     GS_LAUNCHED("emit_sorted_kernel");
   }

@@ -95,14 +95,93 @@ __device__ __forceinline__ float reject_threshold(float opacity) {
   return 2.f * logf(255.f * opacity) * (1.f + 1e-4f) + 1e-4f;
 }
 
+// Screen box (x0, x1, y0, y1) outside which no pixel can accept the record.
+// sample_surface rejects a pixel unless rho2 <= thr or rho3 <= thr:
+//  * rho2 = 2 |xy - pixel|^2 <= thr is a disc of radius sqrt(thr / 2);
+//  * rho3 = u^2 + v^2 of the ray's hit on the surface plane (u, v in the
+//    plane's scaled axes, columns of T) is <= thr on the image of the disc
+//    u^2 + v^2 <= thr. With the whole disc in front of the camera
+//    (T22 > sqrt(thr) |(T20, T21)|) that image is an ellipse whose box
+//    follows from the dual conic C = T diag(thr, thr, -1) T^T: centre
+//    C02 / C22 and half width sqrt(C02^2 - C00 C22) / |C22| (y alike).
+//    The numerator is expanded into 2x2 minors of rows 0 and 2 of T,
+//    C02^2 - C00 C22 = thr (m02^2 + m12^2) - thr^2 m01^2, which avoids the
+//    cancellation of two squared pixel coordinates. Otherwise the image is
+//    unbounded and nothing is culled.
+// A margin of 2% of the half extent plus one pixel keeps float rounding in
+// here and in sample_surface from excluding an accepted pixel. Non-finite
+// values give an unbounded box, thr <= 0 (no pixel can reach alpha >=
+// 1/255) an empty one.
+__device__ float4 footprint_box(const float* g, float thr) {
+  constexpr float kHuge = 1e30f;
+  if (!(thr > 0.f)) return make_float4(kHuge, -kHuge, kHuge, -kHuge);
+  const float c = thr;
+  const float disc = sqrtf(0.5f * c);
+  float x0 = g[9] - disc, x1 = g[9] + disc, y0 = g[10] - disc, y1 = g[10] + disc;
+  const float a = c * (g[6] * g[6] + g[7] * g[7]);
+  const float c22 = a - g[8] * g[8];
+  if (g[8] > 0.f && c22 < -1e-3f * (a + g[8] * g[8])) {
+    const float inv = 1.f / c22;
+    // Row r of T against row 2: centre and half extent along that axis.
+#pragma unroll
+    for (int axis = 0; axis < 2; ++axis) {
+      const float* t = g + 3 * axis;
+      const float c02 = c * (t[0] * g[6] + t[1] * g[7]) - t[2] * g[8];
+      const float m01 = t[0] * g[7] - t[1] * g[6];
+      const float m02 = t[0] * g[8] - t[2] * g[6];
+      const float m12 = t[1] * g[8] - t[2] * g[7];
+      const float centre = c02 * inv;
+      const float half = sqrtf(fmaxf(c * (m02 * m02 + m12 * m12) - c * c * m01 * m01, 0.f)) *
+                         fabsf(inv);
+      if (axis == 0) {
+        x0 = fminf(x0, centre - half);
+        x1 = fmaxf(x1, centre + half);
+      } else {
+        y0 = fminf(y0, centre - half);
+        y1 = fmaxf(y1, centre + half);
+      }
+    }
+  } else {
+    x0 = y0 = -kHuge;  // the disc's image is unbounded: cull nothing
+    x1 = y1 = kHuge;
+  }
+  const float mx = 1.f + 0.01f * (x1 - x0), my = 1.f + 0.01f * (y1 - y0);
+  x0 -= mx;
+  x1 += mx;
+  y0 -= my;
+  y1 += my;
+  if (isfinite(x0) && isfinite(x1) && isfinite(y0) && isfinite(y1))
+    return make_float4(x0, x1, y0, y1);
+  return make_float4(-kHuge, kHuge, -kHuge, kHuge);
+}
+
+// A value that is the same in every lane, moved to scalar registers so
+// that loops and branches over it are scalar.
+__device__ __forceinline__ uint64_t wave_uniform(uint64_t v) {
+  const uint32_t lo = __builtin_amdgcn_readfirstlane(uint32_t(v));
+  const uint32_t hi = __builtin_amdgcn_readfirstlane(uint32_t(v >> 32));
+  return (uint64_t(hi) << 32) | lo;
+}
+
+// Whether box (x0, x1, y0, y1) meets the 8x8 pixels [qx, qx+7] x [qy, qy+7].
+__device__ __forceinline__ bool box_meets(float4 b, float qx, float qy) {
+  return (b.y >= qx) & (b.x <= qx + 7.f) & (b.w >= qy) & (b.z <= qy + 7.f);
+}
+
 struct Sample {
   float k[3], l[3], p[3], s[2], inv_pz, depth, e, alpha;
   bool surface;
 };
 
+// Intersection of the pixel ray with the record's surface, the low-pass
+// filter and alpha (rasterize.cu:71-103). Returns whether this lane
+// accepts the sample; lanes with live = false never do. Written without
+// early returns so that the wave's control flow stays scalar: after the
+// cheap rejection test (no division, no exp) the whole wave leaves at once
+// when no lane can accept.
 template <bool Neural>
 __device__ __forceinline__ bool sample_surface(const float* r, float x, float y,
-                                               float near_plane, Sample& v) {
+                                               float near_plane, bool live, Sample& v) {
   constexpr int OP = Neural ? NeuralRow::OP : ClassicRow::OP;
   constexpr int THR = Neural ? NeuralRow::THR : ClassicRow::THR;
 #pragma unroll
@@ -117,18 +196,18 @@ __device__ __forceinline__ bool sample_surface(const float* r, float x, float y,
   const float rho2 = 2.f * (dx * dx + dy * dy);
   const float thr = r[THR];
   // min(rho3, rho2) > thr without dividing: rho3 = |p.xy|^2 / p.z^2.
-  if (rho2 > thr && v.p[0] * v.p[0] + v.p[1] * v.p[1] > thr * (v.p[2] * v.p[2])) return false;
-  if (v.p[2] == 0.f) return false;
+  const bool far = (rho2 > thr) & (v.p[0] * v.p[0] + v.p[1] * v.p[1] > thr * (v.p[2] * v.p[2]));
+  const bool pass = live & !far & (v.p[2] != 0.f);
+  if (!__any(pass)) return false;
   v.inv_pz = rcp(v.p[2]);
   v.s[0] = v.p[0] * v.inv_pz;
   v.s[1] = v.p[1] * v.inv_pz;
   const float rho3 = v.s[0] * v.s[0] + v.s[1] * v.s[1];
   v.surface = rho3 <= rho2;
   v.depth = (Neural || v.surface) ? v.s[0] * r[6] + v.s[1] * r[7] + r[8] : r[8];
-  if (!(v.depth >= near_plane) || !isfinite(v.depth)) return false;
   v.e = __builtin_amdgcn_exp2f(fminf(rho3, rho2) * kNegHalfLog2e);
   v.alpha = fminf(0.99f, r[OP] * v.e);
-  return v.alpha >= kMinAlpha;
+  return pass & (v.depth >= near_plane) & isfinite(v.depth) & (v.alpha >= kMinAlpha);
 }
 
 // Appearance at local coordinates s. Classic keeps the per-frequency
@@ -180,6 +259,7 @@ __device__ __forceinline__ void shade(const float* r, const float* s, Shade& a) 
 // constants with one thread per record.
 template <bool Neural>
 __device__ __forceinline__ void load_batch(float* rows, float* raw, int* ids, int64_t* prims,
+                                           uint64_t* masks, float tile_x, float tile_y,
                                            int first, int step, int count,
                                            const int* point_list, const int64_t* primitive_ids,
                                            const float* geometry, const float* appearance,
@@ -206,6 +286,27 @@ __device__ __forceinline__ void load_batch(float* rows, float* raw, int* ids, in
     raw[idx] = value;
   }
   __syncthreads();
+  // Wave 1, while wave 0 derives the row constants: record j's footprint
+  // box against the tile's four 8x8 quadrants (one per wave), as four
+  // 64-bit masks whose bit j says that record j may touch the quadrant.
+  if ((t >> 6) == 1) {
+    const int j = t - 64;
+    float4 box = make_float4(1.f, -1.f, 1.f, -1.f);  // empty
+    if (j < count) {
+      const float* g = raw + j * L::RAW_STRIDE;
+      box = footprint_box(g, reject_threshold(g[kGeometry]));
+    }
+    const uint64_t m0 = __ballot(box_meets(box, tile_x, tile_y));
+    const uint64_t m1 = __ballot(box_meets(box, tile_x + 8.f, tile_y));
+    const uint64_t m2 = __ballot(box_meets(box, tile_x, tile_y + 8.f));
+    const uint64_t m3 = __ballot(box_meets(box, tile_x + 8.f, tile_y + 8.f));
+    if (j == 0) {
+      masks[0] = m0;
+      masks[1] = m1;
+      masks[2] = m2;
+      masks[3] = m3;
+    }
+  }
   if (t < count) {
     const float* g = raw + t * L::RAW_STRIDE;
     const float opacity = g[kGeometry];
@@ -376,9 +477,13 @@ __global__ __launch_bounds__(kTilePixels) void render_forward_kernel(
   __shared__ __align__(16) float raw[kBatch * L::RAW_STRIDE];
   __shared__ int ids[kBatch];
   __shared__ int64_t prims[kBatch];
+  __shared__ uint64_t masks[4];
   const int tile = order[blockIdx.x];
   const TilePixel tp = tile_pixel(tile, width, height, tw, th);
   const float x = float(tp.px), y = float(tp.py);
+  const int wave = threadIdx.x >> 6;
+  const float tile_x = float(tp.px - (wave & 1) * 8 - (lane_id() & 7));
+  const float tile_y = float(tp.py - (wave >> 1) * 8 - (lane_id() >> 3));
   bool done = !tp.inside;
   float out[kMaps];
 #pragma unroll
@@ -391,32 +496,45 @@ __global__ __launch_bounds__(kTilePixels) void render_forward_kernel(
   for (int start = range.x; start < range.y; start += kBatch) {
     if (__syncthreads_count(done) == kTilePixels) break;
     const int count = min(kBatch, range.y - start);
-    load_batch<Neural>(rows, raw, ids, prims, start, 1, count, point_list, primitive_ids,
-                       geometry, appearance, opacities);
-    for (int j = 0; j < count && !done; ++j) {
+    load_batch<Neural>(rows, raw, ids, prims, masks, tile_x, tile_y, start, 1, count,
+                       point_list, primitive_ids, geometry, appearance, opacities);
+    // Only the records whose footprint meets this wave's quadrant, in list
+    // order. The loop runs in lockstep across the wave: finished lanes are
+    // masked through `done` rather than leaving the loop, so that every
+    // branch below is on a wave-wide (scalar) condition.
+    uint64_t todo = __all(done) ? 0 : wave_uniform(masks[wave]);
+    while (todo) {
+      const int j = __builtin_ctzll(todo);
+      todo &= todo - 1;
       const float* r = rows + j * L::STRIDE;
       Sample v;
-      if (!sample_surface<Neural>(r, x, y, near_plane, v)) continue;
+      const bool ok = sample_surface<Neural>(r, x, y, near_plane, !done, v);
+      if (!__any(ok)) continue;
       const float next = T * (1.f - v.alpha);
-      if (next < 0.0001f) {
-        done = true;
-        break;
+      const bool stop = ok & (next < 0.0001f);
+      const bool take = ok & !stop;
+      if (__any(stop)) {
+        done |= stop;
+        if (__all(done)) break;
       }
+      if (!__any(take)) continue;
       Shade a;
       shade<Neural, false>(r, v.s, a);
-      const float w = T * v.alpha;
-      const float m = mscale - mnear * rcp(v.depth);
+      if (take) {
+        const float w = T * v.alpha;
+        const float m = mscale - mnear * rcp(v.depth);
 #pragma unroll
-      for (int c = 0; c < 3; ++c) {
-        out[c] += w * a.color[c];
-        out[5 + c] += w * r[11 + c];
+        for (int c = 0; c < 3; ++c) {
+          out[c] += w * a.color[c];
+          out[5 + c] += w * r[11 + c];
+        }
+        out[4] += w * v.depth;
+        out[8] += w * (m * m * (1.f - T) + m2 - 2.f * m * m1);
+        m1 += w * m;
+        m2 += w * m * m;
+        T = next;
+        last = start + j - range.x + 1;
       }
-      out[4] += w * v.depth;
-      out[8] += w * (m * m * (1.f - T) + m2 - 2.f * m * m1);
-      m1 += w * m;
-      m2 += w * m * m;
-      T = next;
-      last = start + j - range.x + 1;
     }
   }
   if (tp.inside) {
@@ -516,10 +634,14 @@ __global__ __launch_bounds__(kTilePixels) void render_backward_kernel(
   __shared__ int ids[kBatch];
   __shared__ int64_t prims[kBatch];
   __shared__ float bg_acc[3];
+  __shared__ uint64_t masks[4];
   const int lane = lane_id();
   const int tile = order[blockIdx.x];
   const TilePixel tp = tile_pixel(tile, width, height, tw, th);
   const float x = float(tp.px), y = float(tp.py);
+  const int wave = threadIdx.x >> 6;
+  const float tile_x = float(tp.px - (wave & 1) * 8 - (lane & 7));
+  const float tile_y = float(tp.py - (wave >> 1) * 8 - (lane >> 3));
   const int last = tp.inside ? contributors[tp.pixel] : 0;
 
   for (int i = threadIdx.x; i < kBatch * NP; i += kTilePixels) acc[i] = 0.f;
@@ -557,13 +679,17 @@ __global__ __launch_bounds__(kTilePixels) void render_backward_kernel(
 
   for (int start = block_last; start > 0; start -= kBatch) {
     const int count = min(kBatch, start);
-    load_batch<Neural>(rows, raw, ids, prims, range.x + start - 1, -1, count, point_list,
+    load_batch<Neural>(rows, raw, ids, prims, masks, tile_x, tile_y, range.x + start - 1, -1,
+                       count, point_list,
                        primitive_ids, geometry, appearance, opacities);
-    for (int j = 0; j < count; ++j) {
+    uint64_t todo = wave_uniform(masks[wave]);
+    while (todo) {
+      const int j = __builtin_ctzll(todo);
+      todo &= todo - 1;
       const float* r = rows + j * L::STRIDE;
       Sample v;
-      bool active = tp.inside && (start - j) <= last;
-      if (active) active = sample_surface<Neural>(r, x, y, near_plane, v);
+      const bool active =
+          sample_surface<Neural>(r, x, y, near_plane, tp.inside && (start - j) <= last, v);
       if (!__any(active)) continue;
       float grad[NP];  // geometry NG | appearance A | opacity
 #pragma unroll

@@ -13,7 +13,10 @@
 // compacted through row_of_pair (visible pairs only, in ascending pair
 // order, exactly the reference's `arange(Q)[radii > 0]`). Packed SH rows are
 // compacted too (the reference keeps them dense), and each row's
-// primitive id is then the row itself.
+// primitive id is then the row itself. A dense row whose pair is culled
+// (radius 0) is referenced by no tile list: it gets its radius, projected
+// mean and ids, while its geometry, appearance and opacity entries are left
+// unwritten.
 //
 // The adjoint reads the compositor's gradient rows: an SH pass sums colour
 // and shared-parameter gradients over cameras per surfel (no atomics) and
@@ -28,7 +31,36 @@ namespace {
 
 constexpr int kRow = kClassic;  // SH appearance row width
 
-template <int Degree>  // -1: no SH rows
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// One thread per (scene, surfel) loops over the cameras of its scene. Every
+// pair gets its radius, projected mean and ids; pairs that reach a tile
+// (radius > 0) also get their geometry row and, with SH, their appearance
+// and opacity rows. Rows of culled pairs are referenced by no tile list,
+// so their geometry, appearance and opacity entries are left unwritten and
+// their SH coefficients are never read. Coefficients are read one colour
+// set at a time, in 16-byte vectors when the set's length allows.
+template <int KC, bool Vec>
+__device__ __forceinline__ void load_coefficients(const float* __restrict__ src, float* dst) {
+  if constexpr (Vec && KC % 4 == 0) {
+    const float4* v = reinterpret_cast<const float4*>(src);
+#pragma unroll
+    for (int i = 0; i < KC / 4; ++i) {
+      const float4 q = v[i];
+      dst[4 * i + 0] = q.x;
+      dst[4 * i + 1] = q.y;
+      dst[4 * i + 2] = q.z;
+      dst[4 * i + 3] = q.w;
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < KC; ++i) dst[i] = src[i];
+  }
+}
+
+// Vec: the SH coefficient and shared-parameter arrays start on 16-byte
+// boundaries, so that 16-byte vector loads are legal.
+template <int Degree, bool Vec>  // Degree -1: no SH rows
 __global__ __launch_bounds__(kProjectBlock) void records_forward_kernel(
     const float* __restrict__ means, const float* __restrict__ quats,
     const float* __restrict__ scales, const float* __restrict__ opacities,
@@ -41,7 +73,9 @@ __global__ __launch_bounds__(kProjectBlock) void records_forward_kernel(
     float* __restrict__ projected_means, int* __restrict__ row_radii,
     int64_t* __restrict__ primitive_ids, int64_t* __restrict__ image_ids,
     float* __restrict__ appearance, float* __restrict__ opacity_rows) {
-  constexpr int K = Degree >= 0 ? (Degree + 1) * (Degree + 1) : 1;
+  constexpr bool kSH = Degree >= 0;
+  constexpr int K = kSH ? (Degree + 1) * (Degree + 1) : 1;
+  constexpr int KC = K * 3;
   const int64_t i = int64_t(blockIdx.x) * kProjectBlock + threadIdx.x;
   const int64_t scene = blockIdx.y;
   if (i >= n) return;
@@ -58,6 +92,12 @@ __global__ __launch_bounds__(kProjectBlock) void records_forward_kernel(
     if (!geometry) continue;  // radii-only pass
     const int64_t row = row_of_pair ? int64_t(row_of_pair[pair]) : pair;
     if (row < 0) continue;
+    projected_means[row * 2 + 0] = p.xy[0];
+    projected_means[row * 2 + 1] = p.xy[1];
+    row_radii[row] = radius;
+    image_ids[row] = cam;
+    primitive_ids[row] = kSH ? row : surfel;
+    if (radius <= 0) continue;
     float* g = geometry + row * kGeometry;
 #pragma unroll
     for (int k = 0; k < 9; ++k) g[k] = p.T[k];
@@ -70,35 +110,29 @@ __global__ __launch_bounds__(kProjectBlock) void records_forward_kernel(
     unit_direction(p, d);
 #pragma unroll
     for (int k = 0; k < 3; ++k) g[14 + k] = d[k];
-    projected_means[row * 2 + 0] = p.xy[0];
-    projected_means[row * 2 + 1] = p.xy[1];
-    row_radii[row] = radius;
-    image_ids[row] = cam;
-    if constexpr (Degree >= 0) {
-      primitive_ids[row] = row;
+    if constexpr (kSH) {
       float Y[K];
-      sh_basis<(Degree >= 0 ? Degree : 0), false>(d[0], d[1], d[2], Y, nullptr, nullptr,
-                                                  nullptr);
+      sh_basis<(kSH ? Degree : 0), false>(d[0], d[1], d[2], Y, nullptr, nullptr, nullptr);
       float* a = appearance + row * kRow;
-      const float* coef[2] = {sh_first + surfel * K * 3, sh_second + surfel * K * 3};
 #pragma unroll
-      for (int set = 0; set < 2; ++set)
+      for (int set = 0; set < 2; ++set) {
+        float coef[KC];
+        load_coefficients<KC, Vec>((set ? sh_second : sh_first) + surfel * KC, coef);
 #pragma unroll
         for (int ch = 0; ch < 3; ++ch) {
           float raw = 0.5f;
 #pragma unroll
-          for (int k = 0; k < K; ++k) raw += Y[k] * coef[set][k * 3 + ch];
+          for (int k = 0; k < K; ++k) raw += Y[k] * coef[k * 3 + ch];
           a[set * 3 + ch] = fmaxf(raw, 0.f);
         }
-#pragma unroll
-      for (int f = 0; f < 4; ++f) {
-        a[6 + f] = weights[surfel * 4 + f];
-        a[10 + f] = magnitudes[surfel * 4 + f];
-        a[14 + f] = phases[surfel * 4 + f];
       }
+      float shared[12];
+      load_coefficients<4, Vec>(weights + surfel * 4, shared);
+      load_coefficients<4, Vec>(magnitudes + surfel * 4, shared + 4);
+      load_coefficients<4, Vec>(phases + surfel * 4, shared + 8);
+#pragma unroll
+      for (int k = 0; k < 12; ++k) a[6 + k] = shared[k];
       opacity_rows[row] = opacities[surfel];
-    } else {
-      primitive_ids[row] = surfel;
     }
   }
 }
@@ -106,8 +140,17 @@ __global__ __launch_bounds__(kProjectBlock) void records_forward_kernel(
 // SH part of the adjoint: per surfel, sum over cameras the colour gradients
 // pushed through the basis (coefficients), the shared weight / magnitude /
 // phase and opacity gradients; write per-pair direction gradients.
+//
+// One wave handles 64 consecutive surfels. Their coefficients (2 x 3K
+// floats each, contiguous across the wave) are read with coalesced loads
+// into LDS, rows of odd pitch so that every lane then reads its own surfel
+// without bank conflicts, and the coefficient gradients leave the same way.
+// Surfels whose colour gradients are all zero in every camera (culled or
+// unseen) skip the coefficient load: their gradients are exactly zero.
+constexpr int kShBlock = 64;
+
 template <int Degree>
-__global__ __launch_bounds__(kProjectBlock) void sh_rows_backward_kernel(
+__global__ __launch_bounds__(kShBlock) void sh_rows_backward_kernel(
     const float* __restrict__ sh_first, const float* __restrict__ sh_second, int64_t cameras,
     int64_t n, const int* __restrict__ row_of_pair, const float* __restrict__ geometry,
     const float* __restrict__ grad_rows, const float* __restrict__ grad_opacity_rows,
@@ -116,64 +159,111 @@ __global__ __launch_bounds__(kProjectBlock) void sh_rows_backward_kernel(
     float* __restrict__ grad_phases, float* __restrict__ grad_opacities,
     float* __restrict__ grad_directions) {
   constexpr int K = (Degree + 1) * (Degree + 1);
-  const int64_t i = int64_t(blockIdx.x) * kProjectBlock + threadIdx.x;
+  constexpr int KC = K * 3;           // floats per surfel and colour set
+  constexpr int PITCH = 2 * KC + 1;   // both sets, odd pitch
+  __shared__ float stage[kShBlock * PITCH];
+  __shared__ int needs[kShBlock];
+  const int t = threadIdx.x;
+  const int64_t first = int64_t(blockIdx.x) * kShBlock;
   const int64_t scene = blockIdx.y;
-  if (i >= n) return;
+  const int count = int(min<int64_t>(kShBlock, n - first));
+  const int64_t i = first + t;
+  const bool own = t < count;
   const int64_t surfel = scene * n + i;
-  const float* coef[2] = {sh_first + surfel * K * 3, sh_second + surfel * K * 3};
-  float acc[2][K * 3];
+  // Pass 1: the colour gradients decide whether the coefficients matter.
+  bool any = false;
+  if (own) {
+    for (int64_t c = 0; c < cameras && !any; ++c) {
+      const int64_t pair = (scene * cameras + c) * n + i;
+      const int64_t row = row_of_pair ? int64_t(row_of_pair[pair]) : pair;
+      if (row < 0) continue;
+      const float* gr = grad_rows + row * kRow;
+#pragma unroll
+      for (int k = 0; k < 6; ++k) any |= gr[k] != 0.f;
+    }
+  }
+  needs[t] = any;
+  __syncthreads();
+  const int64_t base = (scene * n + first) * KC;
+  for (int e = t; e < count * KC; e += kShBlock) {
+    const int sl = e / KC, k = e - sl * KC;
+    if (needs[sl]) {
+      stage[sl * PITCH + k] = sh_first[base + e];
+      stage[sl * PITCH + KC + k] = sh_second[base + e];
+    }
+  }
+  __syncthreads();
+  float* coef = stage + t * PITCH;  // coef[set * KC + k * 3 + ch]
+  float acc[2][KC];
 #pragma unroll
   for (int set = 0; set < 2; ++set)
 #pragma unroll
-    for (int k = 0; k < K * 3; ++k) acc[set][k] = 0.f;
+    for (int k = 0; k < KC; ++k) acc[set][k] = 0.f;
   float shared[12];
 #pragma unroll
   for (int k = 0; k < 12; ++k) shared[k] = 0.f;
   float g_opacity = 0.f;
-  for (int64_t c = 0; c < cameras; ++c) {
+  for (int64_t c = 0; c < cameras && own; ++c) {
     const int64_t pair = (scene * cameras + c) * n + i;
     const int64_t row = row_of_pair ? int64_t(row_of_pair[pair]) : pair;
     if (row < 0) continue;
-    const float* d = geometry + row * kGeometry + 14;
     const float* gr = grad_rows + row * kRow;
-    float Y[K], dx[K], dy[K], dz[K];
-    sh_basis<Degree, true>(d[0], d[1], d[2], Y, dx, dy, dz);
     float gd[3] = {0.f, 0.f, 0.f};
+    float g[6];
+    bool nonzero = false;
 #pragma unroll
-    for (int set = 0; set < 2; ++set)
+    for (int k = 0; k < 6; ++k) {
+      g[k] = gr[k];
+      nonzero |= g[k] != 0.f;
+    }
+    if (nonzero) {
+      const float* d = geometry + row * kGeometry + 14;
+      float Y[K], dx[K], dy[K], dz[K];
+      sh_basis<Degree, true>(d[0], d[1], d[2], Y, dx, dy, dz);
 #pragma unroll
-      for (int ch = 0; ch < 3; ++ch) {
-        float raw = 0.5f;
+      for (int set = 0; set < 2; ++set)
 #pragma unroll
-        for (int k = 0; k < K; ++k) raw += Y[k] * coef[set][k * 3 + ch];
-        const float g = raw >= 0.f ? gr[set * 3 + ch] : 0.f;
+        for (int ch = 0; ch < 3; ++ch) {
+          float raw = 0.5f;
 #pragma unroll
-        for (int k = 0; k < K; ++k) {
-          const float cv = coef[set][k * 3 + ch];
-          acc[set][k * 3 + ch] += g * Y[k];
-          gd[0] += g * cv * dx[k];
-          gd[1] += g * cv * dy[k];
-          gd[2] += g * cv * dz[k];
+          for (int k = 0; k < K; ++k) raw += Y[k] * coef[set * KC + k * 3 + ch];
+          const float gc = raw >= 0.f ? g[set * 3 + ch] : 0.f;
+#pragma unroll
+          for (int k = 0; k < K; ++k) {
+            const float cv = coef[set * KC + k * 3 + ch];
+            acc[set][k * 3 + ch] += gc * Y[k];
+            gd[0] += gc * cv * dx[k];
+            gd[1] += gc * cv * dy[k];
+            gd[2] += gc * cv * dz[k];
+          }
         }
-      }
+    }
 #pragma unroll
     for (int k = 0; k < 3; ++k) grad_directions[pair * 3 + k] = gd[k];
 #pragma unroll
     for (int k = 0; k < 12; ++k) shared[k] += gr[6 + k];
     if (grad_opacity_rows) g_opacity += grad_opacity_rows[row];
   }
+  __syncthreads();  // every lane is done reading its coefficients
 #pragma unroll
-  for (int k = 0; k < K * 3; ++k) {
-    grad_first[surfel * K * 3 + k] = acc[0][k];
-    grad_second[surfel * K * 3 + k] = acc[1][k];
-  }
+  for (int set = 0; set < 2; ++set)
 #pragma unroll
-  for (int f = 0; f < 4; ++f) {
-    grad_weights[surfel * 4 + f] = shared[f];
-    grad_magnitudes[surfel * 4 + f] = shared[4 + f];
-    grad_phases[surfel * 4 + f] = shared[8 + f];
+    for (int k = 0; k < KC; ++k) coef[set * KC + k] = acc[set][k];
+  __syncthreads();
+  for (int e = t; e < count * KC; e += kShBlock) {
+    const int sl = e / KC, k = e - sl * KC;
+    grad_first[base + e] = stage[sl * PITCH + k];
+    grad_second[base + e] = stage[sl * PITCH + KC + k];
   }
-  grad_opacities[surfel] = g_opacity;
+  if (own) {
+#pragma unroll
+    for (int f = 0; f < 4; ++f) {
+      grad_weights[surfel * 4 + f] = shared[f];
+      grad_magnitudes[surfel * 4 + f] = shared[4 + f];
+      grad_phases[surfel * 4 + f] = shared[8 + f];
+    }
+    grad_opacities[surfel] = g_opacity;
+  }
 }
 
 // Per-pair output gradients read from compositor rows.
@@ -261,12 +351,17 @@ int gs_records_forward(const float* means, const float* quaternions, const float
   ProfileScope prof(GS_PROF_PROJECT_FWD, s);
   dim3 grid(static_cast<unsigned>(ceil_div(n, kProjectBlock)), static_cast<unsigned>(scenes));
   const int tw = tiles_x(width), th = tiles_y(height);
+  const bool vec = sh_degree < 0 || (aligned16(sh_first) && aligned16(sh_second) &&
+                                      aligned16(frequency_weights) &&
+                                      aligned16(frequency_magnitudes) && aligned16(phases));
 #define GS_RECORDS(D)                                                                        \
-  records_forward_kernel<D><<<grid, kProjectBlock, 0, s>>>(                                  \
+  if (vec) GS_RECORDS_V(D, true) else GS_RECORDS_V(D, false)
+#define GS_RECORDS_V(D, V)                                                                   \
+  records_forward_kernel<D, V><<<grid, kProjectBlock, 0, s>>>(                               \
       means, quaternions, scales, opacities, view_matrices, intrinsics, sh_first, sh_second, \
       frequency_weights, frequency_magnitudes, phases, cameras, n, tw, th, near_plane,      \
       far_plane, row_of_pair, dense_radii, geometry, projected_means, row_radii,             \
-      primitive_ids, image_ids, appearance_rows, opacity_rows)
+      primitive_ids, image_ids, appearance_rows, opacity_rows);
   switch (sh_degree) {
     case -1: GS_RECORDS(-1); break;
     case 0: GS_RECORDS(0); break;
@@ -275,6 +370,7 @@ int gs_records_forward(const float* means, const float* quaternions, const float
     default: GS_RECORDS(3); break;
   }
 #undef GS_RECORDS
+#undef GS_RECORDS_V
   GS_LAUNCHED("records_forward_kernel");
   return GS_OK;
 }
@@ -322,8 +418,9 @@ int gs_records_backward(const float* means, const float* quaternions, const floa
                      grad_sh_second && grad_weights && grad_magnitudes && grad_phases &&
                      grad_opacities,
                  GS_ERR_ARGUMENT, "null SH pointer passed to gs_records_backward");
+      dim3 sh_grid(static_cast<unsigned>(ceil_div(n, kShBlock)), static_cast<unsigned>(scenes));
 #define GS_SH_ROWS(D)                                                                        \
-  sh_rows_backward_kernel<D><<<grid, kProjectBlock, 0, s>>>(                                 \
+  sh_rows_backward_kernel<D><<<sh_grid, kShBlock, 0, s>>>(                                   \
       sh_first, sh_second, cameras, n, row_of_pair, geometry, grad_appearance_rows,          \
       grad_opacity_rows, grad_sh_first, grad_sh_second, grad_weights, grad_magnitudes,       \
       grad_phases, grad_opacities, w.directions)

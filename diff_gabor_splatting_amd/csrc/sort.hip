@@ -235,6 +235,10 @@ int radix_sort(const Key* keys_in, Key* keys_out, const int* values_in, int* val
   SortWorkspace w = layout(workspace, m, int(sizeof(Key)));
   const int64_t spans = ceil_div(m, kSortSpan);
   const int passes = int(ceil_div(end_bit - begin_bit, kDigitBits));
+  // Spread the bits evenly over the passes (13 bits: 7 + 6, not 8 + 5):
+  // fewer digits per pass means longer runs of equal digits per span and
+  // fewer ballots per key.
+  const int digit_bits = passes ? int(ceil_div(end_bit - begin_bit, passes)) : 0;
   if (passes == 0) {
     copy_pairs_kernel<Key><<<unsigned(ceil_div(m, 256)), 256, 0, s>>>(keys_in, values_in,
                                                                        keys_out, values_out, m);
@@ -245,8 +249,8 @@ int radix_sort(const Key* keys_in, Key* keys_out, const int* values_in, int* val
   const Key* src_k = keys_in;
   const int* src_v = values_in;
   for (int pass = 0; pass < passes; ++pass) {
-    const int shift = begin_bit + pass * kDigitBits;
-    const int bits = min(kDigitBits, end_bit - shift);
+    const int shift = begin_bit + pass * digit_bits;
+    const int bits = min(digit_bits, end_bit - shift);
     const bool to_output = ((passes - 1 - pass) % 2) == 0;
     Key* dst_k = to_output ? keys_out : static_cast<Key*>(w.keys_tmp);
     int* dst_v = to_output ? values_out : w.values_tmp;

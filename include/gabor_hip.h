@@ -193,21 +193,39 @@ int gs_sort_pairs(const uint64_t* keys_in, uint64_t* keys_out, const int32_t* va
 int gs_find_ranges(const uint64_t* sorted_keys, int64_t m, int32_t* ranges, int64_t tiles,
                    void* stream);
 
-/* Scratch bytes for gs_bin_tiles over `count` pairs and m intersections. */
-size_t gs_bin_workspace_size(int64_t count, int64_t m);
-
 /* Depth-first binning: the point list and ranges of emitTiles + the 64-bit
  * cub::DeviceRadixSort::SortPairs + findRanges (rasterize.cu:43-69,
- * 470-501), bit for bit, from the offsets of gs_count_tiles (m =
- * offsets[count-1]). Pairs are stably sorted on their depth bits, emit their
- * tiles in that order as 32-bit tile ids, and a stable sort on bits(tiles)
- * bits groups the entries by tile, which leaves each tile ordered by (depth
- * bits, pair index) as the 64-bit sort does. point_list [m] int32, ranges
- * [images*tw*th, 2] int32 (tiles without entries get (0,0)). */
-int gs_bin_tiles(const float* geometry, const int32_t* radii, const int64_t* image_ids,
-                 const int64_t* offsets, int64_t count, int64_t m, int64_t images,
-                 int32_t width, int32_t height, int32_t* point_list, int32_t* ranges,
-                 void* workspace, size_t workspace_bytes, void* stream);
+ * 470-501), bit for bit, in two stages. A stable sort of the pairs on their
+ * depth bits, emission of each pair's tiles in that order as 32-bit tile
+ * ids and a stable sort of those on bits(tiles) bits leaves every tile's
+ * entries ordered by (depth bits, pair index), as the 64-bit sort does. */
+
+/* Scratch bytes for gs_bin_order over `count` pairs. */
+size_t gs_bin_order_workspace_size(int64_t count);
+
+/* Stage 1, which needs no intersection count and so can run while the host
+ * waits for it: each pair's tile rectangle (tileBounds, rasterize.cu:24-30)
+ * and area (countTiles, :33-40), the stable depth-bit order of the pairs,
+ * order [count] int32 (pair at depth rank j), starts [count] int64 (first
+ * entry of rank j: entries of all lower ranks), rects [count, 4] int32
+ * (x0, y0, width in tiles, image*tw*th, for stage 2) and *intersections
+ * (one device int64) = M, the total that rasterize.cu:466-468 copies to the
+ * host. */
+int gs_bin_order(const float* geometry, const int32_t* radii, const int64_t* image_ids,
+                 int64_t count, int32_t width, int32_t height, int32_t* order, int64_t* starts,
+                 int32_t* rects, int64_t* intersections, void* workspace,
+                 size_t workspace_bytes, void* stream);
+
+/* Scratch bytes for gs_bin_tiles over m intersections. */
+size_t gs_bin_tiles_workspace_size(int64_t m);
+
+/* Stage 2 from stage 1's order, starts and rects: emit in depth order,
+ * sort by tile id, find ranges. point_list [m] int32, ranges
+ * [images*tw*th, 2] int32 ((0,0) for empty tiles). */
+int gs_bin_tiles(const int32_t* order, const int64_t* starts, const int32_t* rects,
+                 int64_t count, int64_t m, int64_t images, int32_t width, int32_t height,
+                 int32_t* point_list, int32_t* ranges, void* workspace, size_t workspace_bytes,
+                 void* stream);
 
 /* ------------------------------------------------------------------ */
 /* Kernels 4 and 5: tile compositors (renderForward / renderBackward,

@@ -79,7 +79,7 @@ def test_binning_pipeline_is_bit_exact(native, seed, q, width, height, images):
     np.testing.assert_array_equal(point_list.cpu().numpy(), ok_list)
     np.testing.assert_array_equal(native.find_ranges(sorted_keys, tiles).cpu().numpy(), ok_ranges)
     # The renderer's depth-first pipeline gives the same list and ranges.
-    bin_list, bin_ranges = native.bin_tiles(g, r, ids, offsets, images, width, height, m)
+    bin_list, bin_ranges = native.bin_depth_first(g, r, ids, images, width, height)
     np.testing.assert_array_equal(bin_list.cpu().numpy(), ok_list)
     np.testing.assert_array_equal(bin_ranges.cpu().numpy(), ok_ranges)
 
@@ -102,7 +102,9 @@ def test_depth_first_binning_is_bit_exact(native, seed, q, width, height, images
     assert (m == 0) == culled
     _, ok_list, ok_ranges = oracle_binning.bin_pairs(geometry, radii, image_ids, images, width,
                                                      height)
-    point_list, ranges = native.bin_tiles(g, r, ids, offsets, images, width, height, m)
+    order, starts, rects, total = native.bin_order(g, r, ids, width, height)
+    assert int(total) == m
+    point_list, ranges = native.bin_tiles(order, starts, rects, images, width, height, m)
     np.testing.assert_array_equal(point_list.cpu().numpy(), ok_list)
     np.testing.assert_array_equal(ranges.cpu().numpy(), ok_ranges)
 
@@ -252,6 +254,9 @@ def test_records_match_oracle(native, packed, sh):
     np.testing.assert_array_equal(out["row_radii"].cpu().numpy(), rec["radii"].numpy())
     expect_prims = np.arange(len(selected)) if sh is not None else rec["primitive_ids"].numpy()
     np.testing.assert_array_equal(out["primitive_ids"].cpu().numpy(), expect_prims)
+    # Rows of culled pairs (radius 0) are referenced by no tile list: only
+    # their radius, projected mean and ids are defined.
+    visible = rec["radii"] > 0
     geometry = rec["geometry"].detach()
     sens = perturbation_sensitivity(
         lambda *x: oracle_render.records(*x[:4], tuple(x[4:9]), x[9], x[10], width, height,
@@ -260,25 +265,31 @@ def test_records_match_oracle(native, packed, sh):
                         "secondary_colors", "frequency_weights", "frequency_magnitudes",
                         "phases", "view_matrices", "intrinsics")])[0]
     a = out["geometry"].cpu().double()
-    assert bool(((a - geometry).abs() <= 1e-6 * (1 + geometry.abs()) + 4 * sens).all()), \
-        describe_mismatch(a, geometry)
+    xy = out["projected_means"].cpu().double()
+    xy_ok = (xy - geometry[:, 9:11]).abs() <= 1e-6 * (1 + geometry[:, 9:11].abs()) + 4 * sens[:, 9:11]
+    assert bool((xy_ok | (xy == geometry[:, 9:11])).all()), describe_mismatch(xy, geometry[:, 9:11])
+    a_vis, g_vis, s_vis = a[visible], geometry[visible], sens[visible]
+    assert bool(((a_vis - g_vis).abs() <= 1e-6 * (1 + g_vis.abs()) + 4 * s_vis).all()), \
+        describe_mismatch(a_vis, g_vis)
     if sh is not None:
         rows_ref = rec["appearance"].detach()[selected] if packed else rec["appearance"].detach()
-        torch.testing.assert_close(out["appearance"].cpu().double(), rows_ref, atol=2e-6, rtol=1e-5)
+        torch.testing.assert_close(out["appearance"].cpu().double()[visible], rows_ref[visible],
+                                   atol=2e-6, rtol=1e-5)
         op_ref = rec["opacities"].detach()[selected] if packed else rec["opacities"].detach()
-        torch.testing.assert_close(out["opacity_rows"].cpu().double(), op_ref)
+        torch.testing.assert_close(out["opacity_rows"].cpu().double()[visible], op_ref[visible])
     # Adjoint: random row gradients (geometry xy columns excluded: that
     # gradient enters through the projected means).
     g = torch.Generator().manual_seed(4)
     Q = a.shape[0]
     g_geometry = torch.randn(Q, 17, generator=g, dtype=torch.float64)
     g_geometry[:, 9:11] = 0
+    g_geometry[~visible] = 0  # the compositor never writes culled rows
     g_projected = torch.randn(Q, 2, generator=g, dtype=torch.float64)
     loss = (rec["geometry"] * g_geometry).sum() + (rec["projected_means"] * g_projected).sum()
     g_app = g_op = None
     if sh is not None:
-        g_app = torch.randn(Q, 18, generator=g, dtype=torch.float64)
-        g_op = torch.randn(Q, generator=g, dtype=torch.float64)
+        g_app = torch.randn(Q, 18, generator=g, dtype=torch.float64) * visible[:, None]
+        g_op = torch.randn(Q, generator=g, dtype=torch.float64) * visible
         app = rec["appearance"][selected] if packed else rec["appearance"]
         ops = rec["opacities"][selected] if packed else rec["opacities"]
         loss = loss + (app * g_app).sum() + (ops * g_op).sum()

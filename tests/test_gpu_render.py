@@ -1,6 +1,8 @@
 """Public-API parity on the GPU: the reference's own test cases
 (tests/test_rendering.py) against the float64 oracle, plus drop-in contracts."""
 
+import math
+
 import numpy as np
 import pytest
 import torch
@@ -339,6 +341,61 @@ def test_multi_tile_scenes_match_oracle(method, sh, packed):
                                                 height=height, **options)
     for name, a in zip(values, grads(actual, weights.to(DEVICE), values)):
         assert_gradients_close(a, expected[name], name, sensitivity[name])
+
+
+@pytest.mark.parametrize("method", ["classic", "neural"])
+def test_extreme_views_match_oracle(method):
+    """Surfels that straddle the camera plane, lie nearly edge-on, or are huge
+    and thin: the per-wave footprint cull must keep every pixel the oracle
+    accepts, forward and backward."""
+    width, height, n = 48, 40, 160
+    g = torch.Generator().manual_seed(23)
+    raw = random_scene(method, n=n, width=width, height=height, seed=23)
+    raw["means"][..., :2] = (torch.rand(1, n, 2, generator=g) * 2 - 1) * 1.2
+    raw["means"][..., 2] = torch.rand(1, n, generator=g) * 3.9 + 0.1
+    raw["scales"] = torch.exp(torch.rand(1, n, 2, generator=g) * math.log(200) + math.log(0.01))
+    # A quarter nearly edge-on: normal (local z) close to the image plane.
+    tilt = torch.rand(n // 4, generator=g) * 0.02 + math.pi / 2 - 0.01
+    axis = torch.zeros(n // 4, 3)
+    axis[:, 0] = 1.0
+    half = tilt / 2
+    raw["quaternions"][0, : n // 4] = torch.cat(
+        [half.cos()[:, None], axis * half.sin()[:, None]], -1)
+    values = on_gpu(raw)
+    actual = maps_from_result(renderer(method)(**values, width=width, height=height))
+    oracle, _, _, _ = oracle_maps(method, values, width, height)
+    rest = {k: v for k, v in values.items() if k != "backgrounds"}
+    _, mask = fp32_conditioned(
+        lambda backgrounds, **kw: ORACLE[method](**kw, backgrounds=backgrounds),
+        {**rest, "backgrounds": values["backgrounds"]}, width=width, height=height)
+    assert float((~mask).float().mean()) <= 0.05
+    torch.testing.assert_close(actual.detach().cpu().double()[mask], oracle.detach()[mask],
+                               atol=1e-5, rtol=1e-4)
+    weights = torch.randn(actual.shape, generator=torch.Generator().manual_seed(4)) * mask[..., None]
+    _, expected, sensitivity = oracle_reference(ORACLE[method], values, weights, width=width,
+                                                height=height)
+    for name, a in zip(values, grads(actual, weights.to(DEVICE), values)):
+        assert_gradients_close(a, expected[name], name, sensitivity[name])
+
+
+def test_unaligned_inputs_match_aligned():
+    """Contiguous inputs need not start on a 16-byte boundary: vector loads
+    are only used when every array allows them."""
+    from diff_gabor_splatting_amd import rasterize_gabors
+
+    values = on_gpu(random_scene("classic", n=200, width=40, height=32, seed=9, sh=3))
+    shifted = {}
+    for key, value in values.items():
+        storage = torch.empty(value.numel() + 1, dtype=value.dtype, device=value.device)
+        view = storage[1:].view(value.shape)  # 4 bytes past an aligned start
+        view.copy_(value.detach())
+        shifted[key] = view.requires_grad_(value.requires_grad)
+    first = maps_from_result(rasterize_gabors(**values, width=40, height=32, sh_degree=3))
+    second = maps_from_result(rasterize_gabors(**shifted, width=40, height=32, sh_degree=3))
+    assert torch.equal(first, second)
+    weights = torch.randn(first.shape, generator=torch.Generator().manual_seed(2)).to(DEVICE)
+    for name, a, b in zip(values, grads(first, weights, values), grads(second, weights, shifted)):
+        assert_gradients_close(a, b, name)
 
 
 def test_forward_is_bitwise_deterministic():
