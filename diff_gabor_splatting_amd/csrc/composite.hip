@@ -272,18 +272,32 @@ __device__ __forceinline__ void load_batch(float* rows, float* raw, int* ids, in
     prims[t] = primitive_ids[id];
   }
   __syncthreads();
-  for (int idx = t; idx < count * L::RAW_STRIDE; idx += kTilePixels) {
-    const int j = idx / L::RAW_STRIDE;
-    const int f = idx - j * L::RAW_STRIDE;
-    float value = 0.f;
-    if (f < kGeometry) {
-      value = geometry[int64_t(ids[j]) * kGeometry + f];
-    } else if (f == kGeometry) {
-      value = opacities[prims[j]];
-    } else if (f - kGeometry - 1 < L::A) {
-      value = appearance[prims[j] * L::A + (f - kGeometry - 1)];
+  // One loop per source array, consecutive threads on consecutive floats of
+  // a row: geometry (17 floats), opacity, appearance (pairs of floats when
+  // the row width is even and the array starts on an 8-byte boundary, as
+  // every row then does).
+  for (int idx = t; idx < count * kGeometry; idx += kTilePixels) {
+    const int j = idx / kGeometry;
+    const int f = idx - j * kGeometry;
+    raw[j * L::RAW_STRIDE + f] = geometry[int64_t(ids[j]) * kGeometry + f];
+  }
+  if (t < count) raw[t * L::RAW_STRIDE + kGeometry] = opacities[prims[t]];
+  const bool pairs = L::A % 2 == 0 && (reinterpret_cast<uintptr_t>(appearance) & 7u) == 0;
+  if (pairs) {
+    constexpr int kPairs = L::A / 2;
+    for (int idx = t; idx < count * kPairs; idx += kTilePixels) {
+      const int j = idx / kPairs;
+      const int f = idx - j * kPairs;
+      const float2 v = reinterpret_cast<const float2*>(appearance + prims[j] * L::A)[f];
+      raw[j * L::RAW_STRIDE + kGeometry + 1 + 2 * f] = v.x;
+      raw[j * L::RAW_STRIDE + kGeometry + 2 + 2 * f] = v.y;
     }
-    raw[idx] = value;
+  } else {
+    for (int idx = t; idx < count * L::A; idx += kTilePixels) {
+      const int j = idx / L::A;
+      const int f = idx - j * L::A;
+      raw[j * L::RAW_STRIDE + kGeometry + 1 + f] = appearance[prims[j] * L::A + f];
+    }
   }
   __syncthreads();
   // Wave 1, while wave 0 derives the row constants: record j's footprint
@@ -672,6 +686,8 @@ __global__ __launch_bounds__(kTilePixels) void render_backward_kernel(
     if (param < 3 && total != 0.f) atomicAdd(&bg_acc[param], total);
   }
   const int block_last = tile_last[tile];
+  // Records past every lane's last contributor are inactive in this wave.
+  const int wave_last = __builtin_amdgcn_readfirstlane(wave_max(last));
   const int2 range = ranges[tile];
   const float mscale = far_plane / (far_plane - near_plane);
   const float mnear = mscale * near_plane;
@@ -683,6 +699,10 @@ __global__ __launch_bounds__(kTilePixels) void render_backward_kernel(
                        count, point_list,
                        primitive_ids, geometry, appearance, opacities);
     uint64_t todo = wave_uniform(masks[wave]);
+    // Row j holds list position start - j (counted from 1).
+    const int beyond = start - wave_last;  // rows j < beyond lie past wave_last
+    if (beyond >= 64) todo = 0;
+    else if (beyond > 0) todo &= ~((uint64_t(1) << beyond) - 1);
     while (todo) {
       const int j = __builtin_ctzll(todo);
       todo &= todo - 1;
@@ -691,70 +711,75 @@ __global__ __launch_bounds__(kTilePixels) void render_backward_kernel(
       const bool active =
           sample_surface<Neural>(r, x, y, near_plane, tp.inside && (start - j) <= last, v);
       if (!__any(active)) continue;
+      // Every lane runs the adjoint. A lane that does not take the sample
+      // contributes exact zeros: its map gradients are masked to zero and
+      // the sample's own values are replaced by finite stand-ins, so every
+      // term below is a product with a zero and never 0 * inf. Taking lanes
+      // compute exactly what a branch would; the masking replaces
+      // zero-filling all NP values ahead of a divergent branch.
+      float gom[kMaps];
+#pragma unroll
+      for (int c = 0; c < kMaps; ++c) gom[c] = active ? go[c] : 0.f;
+      const float alpha = active ? v.alpha : 0.f;
+      const float depth = active ? v.depth : 1.f;
+      const float e = active ? v.e : 0.f;
+      const float inv_pz = active ? v.inv_pz : 0.f;
+      const float s_[2] = {active ? v.s[0] : 0.f, active ? v.s[1] : 0.f};
+      const bool surface = active & v.surface;
       float grad[NP];  // geometry NG | appearance A | opacity
+      float* gg = grad;
+      float* ga = grad + NG;
+      const float inv_keep = rcp(1.f - alpha);
+      T = active ? T * inv_keep : T;
+      const float w = T * alpha;
+      Shade a;
+      shade<Neural, true>(r, s_, a);
+      const float inv_depth = rcp(depth);
+      const float m = mscale - mnear * inv_depth;
+      float gw = gom[4] * depth + gom[8] * (m * m * total_a + m2 - 2.f * m * m1);
+      float gc[3];
 #pragma unroll
-      for (int k = 0; k < NP; ++k) grad[k] = 0.f;
-      if (active) {
-        float* gg = grad;
-        float* ga = grad + NG;
-        const float inv_keep = rcp(1.f - v.alpha);
-        T *= inv_keep;
-        const float w = T * v.alpha;
-        Shade a;
-        shade<Neural, true>(r, v.s, a);
-        const float inv_depth = rcp(v.depth);
-        const float m = mscale - mnear * inv_depth;
-        float gw = go[4] * v.depth + go[8] * (m * m * total_a + m2 - 2.f * m * m1);
-        float gc[3];
+      for (int c = 0; c < 3; ++c) {
+        gw += gom[c] * a.color[c] + gom[5 + c] * r[11 + c];
+        gc[c] = w * gom[c];
+        gg[11 + c] = w * gom[5 + c];
+      }
+      const float galpha = active ? T * gw + (final_term - suffix) * inv_keep : 0.f;
+      suffix += w * gw;
+      float gs[2] = {0.f, 0.f};
+      float gdir[3] = {0.f, 0.f, 0.f};
+      shade_backward<Neural>(r, s_, a, gc, ga, gs, gdir);
+      if constexpr (Neural) {
 #pragma unroll
-        for (int c = 0; c < 3; ++c) {
-          gw += go[c] * a.color[c] + go[5 + c] * r[11 + c];
-          gc[c] = w * go[c];
-          gg[11 + c] = w * go[5 + c];
-        }
-        const float galpha = T * gw + (final_term - suffix) * inv_keep;
-        suffix += w * gw;
-        float gs[2] = {0.f, 0.f};
-        float gdir[3] = {0.f, 0.f, 0.f};
-        shade_backward<Neural>(r, v.s, a, gc, ga, gs, gdir);
-        if constexpr (Neural) {
+        for (int k = 0; k < 3; ++k) gg[14 + k] = gdir[k];
+      }
+      const float gz = w * gom[4] + gom[8] * 2.f * w * (m * total_a - m1) * mnear *
+                                       (inv_depth * inv_depth);
+      const bool tilt = Neural || surface;
+      gs[0] = tilt ? gs[0] + gz * r[6] : gs[0];
+      gs[1] = tilt ? gs[1] + gz * r[7] : gs[1];
+      gg[6] = tilt ? gz * s_[0] : 0.f;
+      gg[7] = tilt ? gz * s_[1] : 0.f;
+      gg[8] = gz;
+      const bool below = r[OP] * e < 0.99f;
+      grad[NP - 1] = below ? galpha * e : 0.f;
+      const float grho = below ? -0.5f * galpha * r[OP] * e : 0.f;
+      gs[0] = surface ? gs[0] + 2.f * s_[0] * grho : gs[0];
+      gs[1] = surface ? gs[1] + 2.f * s_[1] * grho : gs[1];
+      gg[9] = surface ? 0.f : 4.f * (r[9] - x) * grho;
+      gg[10] = surface ? 0.f : 4.f * (r[10] - y) * grho;
+      const float gp[3] = {gs[0] * inv_pz, gs[1] * inv_pz,
+                           -(gs[0] * s_[0] + gs[1] * s_[1]) * inv_pz};
+      // p = k x l  =>  dk = l x gp, dl = gp x k.
+      const float gk[3] = {v.l[1] * gp[2] - v.l[2] * gp[1], v.l[2] * gp[0] - v.l[0] * gp[2],
+                           v.l[0] * gp[1] - v.l[1] * gp[0]};
+      const float gl[3] = {gp[1] * v.k[2] - gp[2] * v.k[1], gp[2] * v.k[0] - gp[0] * v.k[2],
+                           gp[0] * v.k[1] - gp[1] * v.k[0]};
 #pragma unroll
-          for (int k = 0; k < 3; ++k) gg[14 + k] = gdir[k];
-        }
-        const float gz = w * go[4] + go[8] * 2.f * w * (m * total_a - m1) * mnear *
-                                         (inv_depth * inv_depth);
-        if (Neural || v.surface) {
-          gs[0] += gz * r[6];
-          gs[1] += gz * r[7];
-          gg[6] = gz * v.s[0];
-          gg[7] = gz * v.s[1];
-        }
-        gg[8] = gz;
-        float grho = 0.f;
-        if (r[OP] * v.e < 0.99f) {
-          grad[NP - 1] = galpha * v.e;
-          grho = -0.5f * galpha * r[OP] * v.e;
-        }
-        if (v.surface) {
-          gs[0] += 2.f * v.s[0] * grho;
-          gs[1] += 2.f * v.s[1] * grho;
-        } else {
-          gg[9] = 4.f * (r[9] - x) * grho;
-          gg[10] = 4.f * (r[10] - y) * grho;
-        }
-        const float gp[3] = {gs[0] * v.inv_pz, gs[1] * v.inv_pz,
-                             -(gs[0] * v.s[0] + gs[1] * v.s[1]) * v.inv_pz};
-        // p = k x l  =>  dk = l x gp, dl = gp x k.
-        const float gk[3] = {v.l[1] * gp[2] - v.l[2] * gp[1], v.l[2] * gp[0] - v.l[0] * gp[2],
-                             v.l[0] * gp[1] - v.l[1] * gp[0]};
-        const float gl[3] = {gp[1] * v.k[2] - gp[2] * v.k[1], gp[2] * v.k[0] - gp[0] * v.k[2],
-                             gp[0] * v.k[1] - gp[1] * v.k[0]};
-#pragma unroll
-        for (int k = 0; k < 3; ++k) {
-          gg[k] = -gk[k];
-          gg[3 + k] = -gl[k];
-          gg[6 + k] += x * gk[k] + y * gl[k];
-        }
+      for (int k = 0; k < 3; ++k) {
+        gg[k] = -gk[k];
+        gg[3 + k] = -gl[k];
+        gg[6 + k] += x * gk[k] + y * gl[k];
       }
       // Wave totals, one per lane, added into the batch accumulator.
       float* dst = acc + j * NP;

@@ -149,7 +149,78 @@ __global__ __launch_bounds__(kProjectBlock) void records_forward_kernel(
 // unseen) skip the coefficient load: their gradients are exactly zero.
 constexpr int kShBlock = 64;
 
-template <int Degree>
+// Moves `count` (<= kShBlock) rows of KC floats between global memory
+// (contiguous rows) and LDS rows of `Pitch` floats. Every lane issues all of
+// its loads before the first LDS write, 16 bytes at a time when Vec (the
+// global rows are 16-byte aligned and KC % 4 == 0). stage_rows skips rows
+// whose `needs` flag is clear.
+template <int KC, int Pitch, bool Vec>
+__device__ __forceinline__ void stage_rows(const float* __restrict__ src, float* lds, int count,
+                                           const int* needs, int t) {
+  if constexpr (Vec && KC % 4 == 0) {
+    constexpr int kPer = KC / 4;  // float4 per lane: kShBlock * KC / 4 / kShBlock
+    float4 v[kPer];
+#pragma unroll
+    for (int it = 0; it < kPer; ++it) {
+      const int q = it * kShBlock + t;  // float4 index in the block's rows
+      const int row = (4 * q) / KC;
+      v[it] = (row < count && needs[row]) ? reinterpret_cast<const float4*>(src)[q]
+                                          : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+#pragma unroll
+    for (int it = 0; it < kPer; ++it) {
+      const int q = it * kShBlock + t;
+      const int row = (4 * q) / KC, k = 4 * q - row * KC;
+      float* d = lds + row * Pitch + k;
+      if (row < count) {
+        d[0] = v[it].x;
+        d[1] = v[it].y;
+        d[2] = v[it].z;
+        d[3] = v[it].w;
+      }
+    }
+  } else {
+    float v[KC];
+#pragma unroll
+    for (int it = 0; it < KC; ++it) {
+      const int e = it * kShBlock + t;
+      const int row = e / KC;
+      v[it] = (row < count && needs[row]) ? src[e] : 0.f;
+    }
+#pragma unroll
+    for (int it = 0; it < KC; ++it) {
+      const int e = it * kShBlock + t;
+      const int row = e / KC, k = e - row * KC;
+      if (row < count) lds[row * Pitch + k] = v[it];
+    }
+  }
+}
+
+template <int KC, int Pitch, bool Vec>
+__device__ __forceinline__ void unstage_rows(const float* lds, float* __restrict__ dst, int count,
+                                             int t) {
+  if constexpr (Vec && KC % 4 == 0) {
+#pragma unroll
+    for (int it = 0; it < KC / 4; ++it) {
+      const int q = it * kShBlock + t;
+      const int row = (4 * q) / KC, k = 4 * q - row * KC;
+      if (row < count) {
+        const float* s = lds + row * Pitch + k;
+        reinterpret_cast<float4*>(dst)[q] = make_float4(s[0], s[1], s[2], s[3]);
+      }
+    }
+  } else {
+#pragma unroll
+    for (int it = 0; it < KC; ++it) {
+      const int e = it * kShBlock + t;
+      const int row = e / KC, k = e - row * KC;
+      if (row < count) dst[e] = lds[row * Pitch + k];
+    }
+  }
+}
+
+// Vec: coefficient arrays and their gradients start on 16-byte boundaries.
+template <int Degree, bool Vec>
 __global__ __launch_bounds__(kShBlock) void sh_rows_backward_kernel(
     const float* __restrict__ sh_first, const float* __restrict__ sh_second, int64_t cameras,
     int64_t n, const int* __restrict__ row_of_pair, const float* __restrict__ geometry,
@@ -185,13 +256,8 @@ __global__ __launch_bounds__(kShBlock) void sh_rows_backward_kernel(
   needs[t] = any;
   __syncthreads();
   const int64_t base = (scene * n + first) * KC;
-  for (int e = t; e < count * KC; e += kShBlock) {
-    const int sl = e / KC, k = e - sl * KC;
-    if (needs[sl]) {
-      stage[sl * PITCH + k] = sh_first[base + e];
-      stage[sl * PITCH + KC + k] = sh_second[base + e];
-    }
-  }
+  stage_rows<KC, PITCH, Vec>(sh_first + base, stage, count, needs, t);
+  stage_rows<KC, PITCH, Vec>(sh_second + base, stage + KC, count, needs, t);
   __syncthreads();
   float* coef = stage + t * PITCH;  // coef[set * KC + k * 3 + ch]
   float acc[2][KC];
@@ -250,11 +316,8 @@ __global__ __launch_bounds__(kShBlock) void sh_rows_backward_kernel(
 #pragma unroll
     for (int k = 0; k < KC; ++k) coef[set * KC + k] = acc[set][k];
   __syncthreads();
-  for (int e = t; e < count * KC; e += kShBlock) {
-    const int sl = e / KC, k = e - sl * KC;
-    grad_first[base + e] = stage[sl * PITCH + k];
-    grad_second[base + e] = stage[sl * PITCH + KC + k];
-  }
+  unstage_rows<KC, PITCH, Vec>(stage, grad_first + base, count, t);
+  unstage_rows<KC, PITCH, Vec>(stage + KC, grad_second + base, count, t);
   if (own) {
 #pragma unroll
     for (int f = 0; f < 4; ++f) {
@@ -419,11 +482,15 @@ int gs_records_backward(const float* means, const float* quaternions, const floa
                      grad_opacities,
                  GS_ERR_ARGUMENT, "null SH pointer passed to gs_records_backward");
       dim3 sh_grid(static_cast<unsigned>(ceil_div(n, kShBlock)), static_cast<unsigned>(scenes));
+      const bool vec = aligned16(sh_first) && aligned16(sh_second) &&
+                       aligned16(grad_sh_first) && aligned16(grad_sh_second);
 #define GS_SH_ROWS(D)                                                                        \
-  sh_rows_backward_kernel<D><<<sh_grid, kShBlock, 0, s>>>(                                   \
+  if (vec) GS_SH_ROWS_V(D, true) else GS_SH_ROWS_V(D, false)
+#define GS_SH_ROWS_V(D, V)                                                                   \
+  sh_rows_backward_kernel<D, V><<<sh_grid, kShBlock, 0, s>>>(                                \
       sh_first, sh_second, cameras, n, row_of_pair, geometry, grad_appearance_rows,          \
       grad_opacity_rows, grad_sh_first, grad_sh_second, grad_weights, grad_magnitudes,       \
-      grad_phases, grad_opacities, w.directions)
+      grad_phases, grad_opacities, w.directions);
       switch (sh_degree) {
         case 0: GS_SH_ROWS(0); break;
         case 1: GS_SH_ROWS(1); break;
@@ -431,6 +498,7 @@ int gs_records_backward(const float* means, const float* quaternions, const floa
         default: GS_SH_ROWS(3); break;
       }
 #undef GS_SH_ROWS
+#undef GS_SH_ROWS_V
       GS_LAUNCHED("sh_rows_backward_kernel");
       sh_dirs = w.directions;
     }
