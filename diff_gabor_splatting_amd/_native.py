@@ -52,7 +52,7 @@ _SIGNATURES = {
         _c_int,
         [_c_ptr] * 11
         + [_c_int, _c_i64, _c_i64, _c_i64, _c_int, _c_int, _c_float, _c_float]
-        + [_c_ptr] * 10,
+        + [_c_ptr] * 13,
     ),
     "gs_records_backward_workspace_size": (_c_size, [_c_i64, _c_i64, _c_i64, _c_int]),
     "gs_records_backward": (
@@ -372,9 +372,10 @@ def records_forward(means, quaternions, scales, opacities, view_matrices, intrin
     [S,C,3,3]; with SH (sh_degree >= 0) also opacities [S,N], sh = (first,
     second) [S,N,K,3] and shared = (weights, magnitudes, phases) [S,N,4].
     Returns a dict of geometry [Q,17], projected_means [Q,2], row_radii [Q],
-    primitive_ids [Q], image_ids [Q], dense_radii [S,C,N], row_of_pair
-    ([S*C*N] int32 or None) and selected (packed pair indices or None), plus
-    appearance [Q,18] and opacity_rows [Q] with SH.
+    primitive_ids [Q], image_ids [Q], the meta ids scene_ids / camera_ids /
+    surfel_ids [Q], dense_radii [S,C,N], row_of_pair ([S*C*N] int32 or None)
+    and selected (packed pair indices or None), plus appearance [Q,18] and
+    opacity_rows [Q] with SH.
     """
     device = means.device
     scenes, n = means.shape[:2]
@@ -394,7 +395,8 @@ def records_forward(means, quaternions, scales, opacities, view_matrices, intrin
                 _ptr(out.get("geometry")), _ptr(out.get("projected_means")),
                 _ptr(out.get("row_radii")), _ptr(out.get("primitive_ids")),
                 _ptr(out.get("image_ids")), _ptr(out.get("appearance")),
-                _ptr(out.get("opacity_rows")), _stream(device),
+                _ptr(out.get("opacity_rows")), _ptr(out.get("scene_ids")),
+                _ptr(out.get("camera_ids")), _ptr(out.get("surfel_ids")), _stream(device),
             )
         )
 
@@ -418,6 +420,8 @@ def records_forward(means, quaternions, scales, opacities, view_matrices, intrin
         if degree >= 0:
             out["appearance"] = torch.empty((rows, 18), **f32)
             out["opacity_rows"] = torch.empty(rows, **f32)
+        meta_ids = torch.empty((3, rows), dtype=torch.int64, device=device)
+        out.update(scene_ids=meta_ids[0], camera_ids=meta_ids[1], surfel_ids=meta_ids[2])
         if rows:
             launch(row_of_pair, None if packed else dense_radii, out)
     out.update(dense_radii=dense_radii, row_of_pair=row_of_pair, selected=selected)

@@ -60,6 +60,22 @@ __device__ __forceinline__ void load_coefficients(const float* __restrict__ src,
 
 // Vec: the SH coefficient and shared-parameter arrays start on 16-byte
 // boundaries, so that 16-byte vector loads are legal.
+// Row staging: each thread leaves its pair's geometry row (17 floats) and,
+// with SH, appearance row (18) in LDS at an odd pitch, and the workgroup
+// then writes the rows of its 256 consecutive pairs with consecutive
+// threads on consecutive floats - the rows of consecutive pairs are
+// consecutive in both dense and packed mode - skipping culled pairs.
+template <int Width>
+__device__ __forceinline__ void unstage_pair_rows(const float* stage, int pitch, int offset,
+                                                  const int64_t* rows, float* __restrict__ out) {
+#pragma unroll 4
+  for (int e = threadIdx.x; e < kProjectBlock * Width; e += kProjectBlock) {
+    const int local = e / Width, f = e - local * Width;
+    const int64_t row = rows[local];
+    if (row >= 0) out[row * Width + f] = stage[local * pitch + offset + f];
+  }
+}
+
 template <int Degree, bool Vec>  // Degree -1: no SH rows
 __global__ __launch_bounds__(kProjectBlock) void records_forward_kernel(
     const float* __restrict__ means, const float* __restrict__ quats,
@@ -72,68 +88,90 @@ __global__ __launch_bounds__(kProjectBlock) void records_forward_kernel(
     int* __restrict__ dense_radii, float* __restrict__ geometry,
     float* __restrict__ projected_means, int* __restrict__ row_radii,
     int64_t* __restrict__ primitive_ids, int64_t* __restrict__ image_ids,
-    float* __restrict__ appearance, float* __restrict__ opacity_rows) {
+    float* __restrict__ appearance, float* __restrict__ opacity_rows,
+    int64_t* __restrict__ meta_scene_ids, int64_t* __restrict__ meta_camera_ids,
+    int64_t* __restrict__ meta_surfel_ids) {
   constexpr bool kSH = Degree >= 0;
   constexpr int K = kSH ? (Degree + 1) * (Degree + 1) : 1;
   constexpr int KC = K * 3;
-  const int64_t i = int64_t(blockIdx.x) * kProjectBlock + threadIdx.x;
+  constexpr int kPitch = kSH ? kGeometry + kRow : kGeometry;  // 35 or 17: odd
+  __shared__ float stage[kProjectBlock * kPitch];
+  __shared__ int64_t stage_rows[kProjectBlock];
+  const int t = threadIdx.x;
+  const int64_t i = int64_t(blockIdx.x) * kProjectBlock + t;
   const int64_t scene = blockIdx.y;
-  if (i >= n) return;
+  const bool own = i < n;
   const int64_t surfel = scene * n + i;
   Surfel s;
-  load_surfel(means, quats, scales, surfel, s);
-  for (int64_t c = 0; c < cameras; ++c) {
+  if (own) load_surfel(means, quats, scales, surfel, s);
+  for (int64_t c = 0; c < cameras; ++c) {  // uniform: every thread takes part in the staging
     const int64_t cam = scene * cameras + c;
-    Projection p;
-    project_pair(s.R, s.mu, s.sc, views + cam * 16, intrinsics + cam * 9, p);
-    const int64_t pair = cam * n + i;
-    const int radius = screen_radius(p, tw, th, near_plane, far_plane);
-    if (dense_radii) dense_radii[pair] = radius;
-    if (!geometry) continue;  // radii-only pass
-    const int64_t row = row_of_pair ? int64_t(row_of_pair[pair]) : pair;
-    if (row < 0) continue;
-    projected_means[row * 2 + 0] = p.xy[0];
-    projected_means[row * 2 + 1] = p.xy[1];
-    row_radii[row] = radius;
-    image_ids[row] = cam;
-    primitive_ids[row] = kSH ? row : surfel;
-    if (radius <= 0) continue;
-    float* g = geometry + row * kGeometry;
-#pragma unroll
-    for (int k = 0; k < 9; ++k) g[k] = p.T[k];
-    g[9] = p.xy[0];
-    g[10] = p.xy[1];
-    const float sign = facing_sign(p);
-#pragma unroll
-    for (int k = 0; k < 3; ++k) g[11 + k] = p.nraw[k] * sign;
-    float d[3];
-    unit_direction(p, d);
-#pragma unroll
-    for (int k = 0; k < 3; ++k) g[14 + k] = d[k];
-    if constexpr (kSH) {
-      float Y[K];
-      sh_basis<(kSH ? Degree : 0), false>(d[0], d[1], d[2], Y, nullptr, nullptr, nullptr);
-      float* a = appearance + row * kRow;
-#pragma unroll
-      for (int set = 0; set < 2; ++set) {
-        float coef[KC];
-        load_coefficients<KC, Vec>((set ? sh_second : sh_first) + surfel * KC, coef);
-#pragma unroll
-        for (int ch = 0; ch < 3; ++ch) {
-          float raw = 0.5f;
-#pragma unroll
-          for (int k = 0; k < K; ++k) raw += Y[k] * coef[k * 3 + ch];
-          a[set * 3 + ch] = fmaxf(raw, 0.f);
+    int64_t staged = -1;
+    if (own) {
+      Projection p;
+      project_pair(s.R, s.mu, s.sc, views + cam * 16, intrinsics + cam * 9, p);
+      const int64_t pair = cam * n + i;
+      const int radius = screen_radius(p, tw, th, near_plane, far_plane);
+      if (dense_radii) dense_radii[pair] = radius;
+      const int64_t row = !geometry ? -1 : row_of_pair ? int64_t(row_of_pair[pair]) : pair;
+      if (row >= 0) {
+        projected_means[row * 2 + 0] = p.xy[0];
+        projected_means[row * 2 + 1] = p.xy[1];
+        row_radii[row] = radius;
+        image_ids[row] = cam;
+        primitive_ids[row] = kSH ? row : surfel;
+        if (meta_scene_ids) {
+          meta_scene_ids[row] = scene;
+          meta_camera_ids[row] = c;
+          meta_surfel_ids[row] = i;
         }
       }
-      float shared[12];
-      load_coefficients<4, Vec>(weights + surfel * 4, shared);
-      load_coefficients<4, Vec>(magnitudes + surfel * 4, shared + 4);
-      load_coefficients<4, Vec>(phases + surfel * 4, shared + 8);
+      if (row >= 0 && radius > 0) {
+        staged = row;
+        float* g = stage + t * kPitch;
 #pragma unroll
-      for (int k = 0; k < 12; ++k) a[6 + k] = shared[k];
-      opacity_rows[row] = opacities[surfel];
+        for (int k = 0; k < 9; ++k) g[k] = p.T[k];
+        g[9] = p.xy[0];
+        g[10] = p.xy[1];
+        const float sign = facing_sign(p);
+#pragma unroll
+        for (int k = 0; k < 3; ++k) g[11 + k] = p.nraw[k] * sign;
+        float d[3];
+        unit_direction(p, d);
+#pragma unroll
+        for (int k = 0; k < 3; ++k) g[14 + k] = d[k];
+        if constexpr (kSH) {
+          float Y[K];
+          sh_basis<(kSH ? Degree : 0), false>(d[0], d[1], d[2], Y, nullptr, nullptr, nullptr);
+          float* a = g + kGeometry;
+#pragma unroll
+          for (int set = 0; set < 2; ++set) {
+            float coef[KC];
+            load_coefficients<KC, Vec>((set ? sh_second : sh_first) + surfel * KC, coef);
+#pragma unroll
+            for (int ch = 0; ch < 3; ++ch) {
+              float raw = 0.5f;
+#pragma unroll
+              for (int k = 0; k < K; ++k) raw += Y[k] * coef[k * 3 + ch];
+              a[set * 3 + ch] = fmaxf(raw, 0.f);
+            }
+          }
+          float shared[12];
+          load_coefficients<4, Vec>(weights + surfel * 4, shared);
+          load_coefficients<4, Vec>(magnitudes + surfel * 4, shared + 4);
+          load_coefficients<4, Vec>(phases + surfel * 4, shared + 8);
+#pragma unroll
+          for (int k = 0; k < 12; ++k) a[6 + k] = shared[k];
+          opacity_rows[row] = opacities[surfel];
+        }
+      }
     }
+    if (!geometry) continue;  // uniform: a radii-only pass writes no rows
+    stage_rows[t] = staged;
+    __syncthreads();
+    unstage_pair_rows<kGeometry>(stage, kPitch, 0, stage_rows, geometry);
+    if constexpr (kSH) unstage_pair_rows<kRow>(stage, kPitch, kGeometry, stage_rows, appearance);
+    __syncthreads();  // the next camera overwrites the stage
   }
 }
 
@@ -390,7 +428,8 @@ int gs_records_forward(const float* means, const float* quaternions, const float
                        float near_plane, float far_plane, const int32_t* row_of_pair,
                        int32_t* dense_radii, float* geometry, float* projected_means,
                        int32_t* row_radii, int64_t* primitive_ids, int64_t* image_ids,
-                       float* appearance_rows, float* opacity_rows, void* stream) {
+                       float* appearance_rows, float* opacity_rows, int64_t* meta_scene_ids,
+                       int64_t* meta_camera_ids, int64_t* meta_surfel_ids, void* stream) {
   using namespace gs;
   clear_error();
   int status = check_projection_sizes(scenes, cameras, n);
@@ -405,6 +444,9 @@ int gs_records_forward(const float* means, const float* quaternions, const float
   if (geometry) {
     GS_REQUIRE(projected_means && row_radii && primitive_ids && image_ids, GS_ERR_ARGUMENT,
                "null row output passed to gs_records_forward");
+    GS_REQUIRE((meta_scene_ids && meta_camera_ids && meta_surfel_ids) ||
+                   (!meta_scene_ids && !meta_camera_ids && !meta_surfel_ids),
+               GS_ERR_ARGUMENT, "meta id outputs must be given together");
     if (sh_degree >= 0)
       GS_REQUIRE(opacities && sh_first && sh_second && frequency_weights &&
                      frequency_magnitudes && phases && appearance_rows && opacity_rows,
@@ -424,7 +466,8 @@ int gs_records_forward(const float* means, const float* quaternions, const float
       means, quaternions, scales, opacities, view_matrices, intrinsics, sh_first, sh_second, \
       frequency_weights, frequency_magnitudes, phases, cameras, n, tw, th, near_plane,      \
       far_plane, row_of_pair, dense_radii, geometry, projected_means, row_radii,             \
-      primitive_ids, image_ids, appearance_rows, opacity_rows);
+      primitive_ids, image_ids, appearance_rows, opacity_rows, meta_scene_ids, meta_camera_ids, \
+      meta_surfel_ids);
   switch (sh_degree) {
     case -1: GS_RECORDS(-1); break;
     case 0: GS_RECORDS(0); break;

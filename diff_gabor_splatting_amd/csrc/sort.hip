@@ -54,7 +54,6 @@ __global__ __launch_bounds__(kSortBlock) void radix_upsweep_kernel(
   for (int i = threadIdx.x; i < kSortWaves * kBins; i += kSortBlock) (&hist[0][0])[i] = 0;
   __syncthreads();
   const uint32_t mask = (1u << bits) - 1u;
-  const uint64_t lanes_below = (uint64_t(1) << lane) - 1;
   const int64_t wave_base = int64_t(blockIdx.x) * kSortSpan + int64_t(wave) * kWaveSpan;
   Key key[kSortItems];
 #pragma unroll
@@ -62,12 +61,21 @@ __global__ __launch_bounds__(kSortBlock) void radix_upsweep_kernel(
     const int64_t i = wave_base + int64_t(it) * 64 + lane;
     key[it] = i < m ? keys[i] : Key(0);
   }
+  // One LDS atomic per key, without a return value, so that a lane's 16
+  // updates do not wait on each other; when every valid lane of the wave
+  // holds the same digit (common in the high digits of depth keys) a single
+  // add replaces 64 colliding ones.
 #pragma unroll
   for (int it = 0; it < kSortItems; ++it) {
     const bool valid = wave_base + int64_t(it) * 64 + lane < m;
     const uint32_t digit = uint32_t(key[it] >> shift) & mask;
-    const uint64_t peers = digit_peers(digit, valid, bits);
-    if (valid && (peers & lanes_below) == 0) hist[wave][digit] += uint32_t(__popcll(peers));
+    const uint64_t live = __ballot(valid);
+    const uint32_t first = __builtin_amdgcn_readfirstlane(digit);
+    if (__all(!valid || digit == first)) {
+      if (lane == 0 && live) atomicAdd(&hist[wave][first], uint32_t(__popcll(live)));
+    } else if (valid) {
+      atomicAdd(&hist[wave][digit], 1u);
+    }
   }
   __syncthreads();
   const int d = threadIdx.x;  // kSortBlock == kBins
@@ -116,18 +124,26 @@ __global__ __launch_bounds__(kSortBlock) void radix_downsweep_kernel(
     key[it] = valid ? keys_in[i] : Key(0);
     value[it] = valid ? values_in[i] : 0;
   }
+  // Rank = keys of the same digit earlier in this wave's span: the group
+  // leader reserves the group's slots with an LDS atomic that returns the
+  // previous count (the 16 atomics of a lane are issued back to back, in
+  // item order, so the counts stay in key order), then every lane reads its
+  // leader's value.
+  uint32_t before[kSortItems];
+  int leader[kSortItems];
 #pragma unroll
   for (int it = 0; it < kSortItems; ++it) {
     const bool valid = wave_base + int64_t(it) * 64 + lane < m;
     const uint32_t digit = uint32_t(key[it] >> shift) & mask;
     const uint64_t peers = digit_peers(digit, valid, bits);
-    rank[it] = 0;
-    if (valid) {
-      const uint32_t before = running[wave][digit];
-      rank[it] = before + uint32_t(__popcll(peers & lanes_below));
-      if ((peers & lanes_below) == 0) running[wave][digit] = before + uint32_t(__popcll(peers));
-    }
+    leader[it] = peers ? __builtin_ctzll(peers) : lane;
+    rank[it] = uint32_t(__popcll(peers & lanes_below));
+    before[it] = 0;
+    if (valid && (peers & lanes_below) == 0)
+      before[it] = atomicAdd(&running[wave][digit], uint32_t(__popcll(peers)));
   }
+#pragma unroll
+  for (int it = 0; it < kSortItems; ++it) rank[it] += uint32_t(__shfl(int(before[it]), leader[it]));
   __syncthreads();
   // Per digit: exclusive offsets of each wave inside the span, and the
   // span's first local / global slot.

@@ -77,8 +77,9 @@ class ProjectRecords(torch.autograd.Function):
     per-camera expansion of shared appearance/opacity, the packing gathers
     and the geometry concatenation. Outputs: geometry rows [Q,17], projected
     means [Q,2], (with SH: appearance rows [Q,18], opacity rows [Q]), radii
-    rows [Q], primitive ids [Q], image ids [Q], dense radii [S,C,N] and the
-    packed pair indices (or an empty tensor in dense mode).
+    rows [Q], primitive ids [Q], image ids [Q], dense radii [S,C,N] and each
+    row's scene, camera and surfel index [Q] (the meta ids of
+    rendering.py:389-392).
     """
 
     @staticmethod
@@ -96,11 +97,8 @@ class ProjectRecords(torch.autograd.Function):
                               second, out["geometry"], row_of_pair)
         ctx.sh_degree = sh_degree
         ctx.set_materialize_grads(False)
-        selected = out["selected"]
-        if selected is None:
-            selected = torch.empty(0, dtype=torch.int64, device=means.device)
         discrete = (out["row_radii"], out["primitive_ids"], out["image_ids"],
-                    out["dense_radii"], selected)
+                    out["dense_radii"], out["scene_ids"], out["camera_ids"], out["surfel_ids"])
         ctx.mark_non_differentiable(*discrete)
         if sh_degree is None:
             return (out["geometry"], out["projected_means"], *discrete)
@@ -351,13 +349,12 @@ def render(
 
     views = view_matrices.reshape(scenes, cameras, 4, 4)
     cameras_k = intrinsics.reshape(scenes, cameras, 3, 3)
-    pairs = scenes * cameras * n
     if sh_degree is not None:
         # Camera-specific SH colours: appearance and opacity rows per pair,
         # written by the HIP record kernel.
         k = (sh_degree + 1) ** 2
         (geometry, projected_means, parameters, opacity_rows, row_radii, primitive_ids,
-         image_ids, dense_radii, selected) = ProjectRecords.apply(
+         image_ids, dense_radii, scene_ids, camera_ids, surfel_ids) = ProjectRecords.apply(
             means.reshape(scenes, n, 3), quaternions.reshape(scenes, n, 4),
             scales.reshape(scenes, n, 2), opacities.reshape(scenes, n), views, cameras_k,
             appearance[0].reshape(scenes, n, k, 3), appearance[1].reshape(scenes, n, k, 3),
@@ -368,7 +365,7 @@ def render(
     else:
         # One appearance row per surfel, shared by every camera of its scene.
         (geometry, projected_means, row_radii, primitive_ids, image_ids, dense_radii,
-         selected) = ProjectRecords.apply(
+         scene_ids, camera_ids, surfel_ids) = ProjectRecords.apply(
             means.reshape(scenes, n, 3), quaternions.reshape(scenes, n, 4),
             scales.reshape(scenes, n, 2), None, views, cameras_k, None, None, None, None, None,
             None, width, height, near_plane, far_plane, packed,
@@ -377,8 +374,6 @@ def render(
         flat = [t.reshape(scenes, n, math.prod(shape)) for t, (_, shape) in zip(appearance, fields)]
         parameters = torch.cat(flat, dim=-1).reshape(scenes * n, width_of_row)
         opacity_rows = opacities.reshape(scenes * n)
-    if not packed:
-        selected = torch.arange(pairs, device=device)
     rgb, alpha, depth, normals, distortion = Composite.apply(
         geometry,
         projected_means,
@@ -395,13 +390,12 @@ def render(
         far_plane,
     )
     image_shape = batch + (cameras, height, width)
-    stride = max(n, 1)
     meta = {
         "radii": row_radii if packed else dense_radii.reshape(batch + (cameras, n)),
         "projected_means": projected_means,
-        "scene_ids": selected // (cameras * stride),
-        "camera_ids": selected // stride % cameras,
-        "primitive_ids": selected % stride,
+        "scene_ids": scene_ids,
+        "camera_ids": camera_ids,
+        "primitive_ids": surfel_ids,
         "packed": packed,
         "accumulated_depth": depth.reshape(image_shape + (1,)),
         "normals": normals.reshape(image_shape + (3,)),

@@ -93,7 +93,11 @@ int gs_project_backward(const float* means, const float* quaternions, const floa
  * sh_degree 0..3 the colours are camera-specific and the row also gets
  * appearance_rows [Q,18] (SH colours, then the surfel's weights, magnitudes
  * and phases) and opacity_rows [Q]; sh_degree -1 writes neither (the caller
- * supplies per-surfel appearance). */
+ * supplies per-surfel appearance). Rows of pairs with radius 0 (referenced
+ * by no tile list) get only their radius, projected mean and ids. When
+ * given (all three or none), meta_scene_ids / meta_camera_ids /
+ * meta_surfel_ids [Q] int64 receive each row's scene, camera and surfel
+ * index: the reference's meta ids (rendering.py:389-392). */
 int gs_records_forward(const float* means, const float* quaternions, const float* scales,
                        const float* opacities, const float* view_matrices,
                        const float* intrinsics, const float* sh_first, const float* sh_second,
@@ -103,7 +107,8 @@ int gs_records_forward(const float* means, const float* quaternions, const float
                        float near_plane, float far_plane, const int32_t* row_of_pair,
                        int32_t* dense_radii, float* geometry, float* projected_means,
                        int32_t* row_radii, int64_t* primitive_ids, int64_t* image_ids,
-                       float* appearance_rows, float* opacity_rows, void* stream);
+                       float* appearance_rows, float* opacity_rows, int64_t* meta_scene_ids,
+                       int64_t* meta_camera_ids, int64_t* meta_surfel_ids, void* stream);
 
 /* Scratch bytes needed by gs_records_backward. */
 size_t gs_records_backward_workspace_size(int64_t scenes, int64_t cameras, int64_t n,
