@@ -254,22 +254,22 @@ __device__ __forceinline__ void shade(const float* r, const float* s, Shade& a) 
   }
 }
 
-// Stage `count` records (list positions first, first + step, ...): gather
-// the raw fields into LDS with every thread, then derive each row's
-// constants with one thread per record.
+// Stage `count` records: thread t < count brings record t's point-list
+// entry and primitive id (read one batch ahead by the caller, so that the
+// two dependent loads overlap the previous batch); every thread then
+// gathers raw fields into LDS, and one thread per record derives the row's
+// constants.
 template <bool Neural>
 __device__ __forceinline__ void load_batch(float* rows, float* raw, int* ids, int64_t* prims,
                                            uint64_t* masks, float tile_x, float tile_y,
-                                           int first, int step, int count,
-                                           const int* point_list, const int64_t* primitive_ids,
+                                           int count, int id, int64_t prim,
                                            const float* geometry, const float* appearance,
                                            const float* opacities) {
   using L = Layout<Neural>;
   const int t = threadIdx.x;
-  if (t < count) {
-    const int id = point_list[first + step * t];
+  if (t < count) {  // (id, prim): this thread's record, fetched by the caller ahead of time
     ids[t] = id;
-    prims[t] = primitive_ids[id];
+    prims[t] = prim;
   }
   __syncthreads();
   // One loop per source array, consecutive threads on consecutive floats of
@@ -507,11 +507,25 @@ __global__ __launch_bounds__(kTilePixels) void render_forward_kernel(
   const int2 range = ranges[tile];
   const float mscale = far_plane / (far_plane - near_plane);
   const float mnear = mscale * near_plane;
+  // Point-list entry and primitive id of record threadIdx.x of the next
+  // batch, read ahead: the entry while this batch is gathered, the id while
+  // its records are composited.
+  int next_id = 0;
+  int64_t next_prim = 0;
+  if (int(threadIdx.x) < min(kBatch, range.y - range.x)) {
+    next_id = point_list[range.x + threadIdx.x];
+    next_prim = primitive_ids[next_id];
+  }
   for (int start = range.x; start < range.y; start += kBatch) {
     if (__syncthreads_count(done) == kTilePixels) break;
     const int count = min(kBatch, range.y - start);
-    load_batch<Neural>(rows, raw, ids, prims, masks, tile_x, tile_y, start, 1, count,
-                       point_list, primitive_ids, geometry, appearance, opacities);
+    const int id = next_id;
+    const int64_t prim = next_prim;
+    const bool ahead = int(threadIdx.x) < min(kBatch, range.y - start - kBatch);
+    if (ahead) next_id = point_list[start + kBatch + threadIdx.x];
+    load_batch<Neural>(rows, raw, ids, prims, masks, tile_x, tile_y, count, id, prim, geometry,
+                       appearance, opacities);
+    if (ahead) next_prim = primitive_ids[next_id];
     // Only the records whose footprint meets this wave's quadrant, in list
     // order. The loop runs in lockstep across the wave: finished lanes are
     // masked through `done` rather than leaving the loop, so that every
@@ -693,11 +707,24 @@ __global__ __launch_bounds__(kTilePixels) void render_backward_kernel(
   const float mnear = mscale * near_plane;
   float suffix = 0.f;
 
+  // Record threadIdx.x of a batch starting at `start` is list position
+  // range.x + start - 1 - threadIdx.x; the next batch's entry and id are
+  // read ahead as in the forward.
+  int next_id = 0;
+  int64_t next_prim = 0;
+  if (int(threadIdx.x) < min(kBatch, block_last)) {
+    next_id = point_list[range.x + block_last - 1 - threadIdx.x];
+    next_prim = primitive_ids[next_id];
+  }
   for (int start = block_last; start > 0; start -= kBatch) {
     const int count = min(kBatch, start);
-    load_batch<Neural>(rows, raw, ids, prims, masks, tile_x, tile_y, range.x + start - 1, -1,
-                       count, point_list,
-                       primitive_ids, geometry, appearance, opacities);
+    const int id = next_id;
+    const int64_t prim = next_prim;
+    const bool ahead = int(threadIdx.x) < min(kBatch, start - kBatch);
+    if (ahead) next_id = point_list[range.x + start - kBatch - 1 - threadIdx.x];
+    load_batch<Neural>(rows, raw, ids, prims, masks, tile_x, tile_y, count, id, prim, geometry,
+                       appearance, opacities);
+    if (ahead) next_prim = primitive_ids[next_id];
     uint64_t todo = wave_uniform(masks[wave]);
     // Row j holds list position start - j (counted from 1).
     const int beyond = start - wave_last;  // rows j < beyond lie past wave_last
