@@ -1,0 +1,93 @@
+"""The loop / fused-dense / fused-packed benchmark harness.
+
+CPU: command-line defaults and errors, and that the parity gate rejects an
+implementation whose maps or gradients differ from the per-camera loop (the
+renderer replaced by a small differentiable CPU function). GPU: a tiny
+end-to-end run whose report carries the reference harness's keys.
+"""
+
+import json
+
+import pytest
+import torch
+
+from diff_gabor_splatting_amd import benchmark_rasterization as harness
+
+
+def test_defaults_follow_the_reference_harness():
+    args = harness._parse([])
+    assert (args.method, args.num_primitives, args.num_scenes, args.num_cameras) == (
+        "both", 10_000, 1, 4)
+    assert (args.image_width, args.image_height) == (256, 256)
+    assert (args.warmup_iterations, args.measurement_iterations, args.seed) == (5, 20, 42)
+    assert args.profile_iterations == 0 and not args.skip_validation
+    assert args.output_json is None
+
+
+@pytest.mark.parametrize("flag", ["--num-primitives", "--num-cameras", "--image-width",
+                                  "--measurement-iterations"])
+def test_nonpositive_sizes_are_rejected(flag):
+    with pytest.raises(SystemExit):
+        harness._parse([flag, "0"])
+
+
+def test_negative_warmup_is_rejected():
+    with pytest.raises(SystemExit):
+        harness._parse(["--warmup-iterations", "-1"])
+
+
+def _fake_renderer(offsets):
+    """Stand-in for render_maps: maps = f(parameters) + an implementation offset."""
+    def render(scene, args, method, implementation):
+        base = torch.outer(scene["means"].sin(), scene["scales"].exp())
+        return base + offsets.get(implementation, 0.0) * scene["means"].sum()
+    return render
+
+
+def _fake_scene():
+    gen = torch.Generator().manual_seed(3)
+    scene = {
+        "means": torch.rand(5, generator=gen, dtype=torch.float64),
+        "scales": torch.rand(4, generator=gen, dtype=torch.float64),
+        "backgrounds": torch.rand(3, generator=gen, dtype=torch.float64),
+    }
+    for name, value in scene.items():
+        value.requires_grad_(name != "backgrounds")
+    return scene
+
+
+def test_parity_gate_accepts_equal_implementations(monkeypatch):
+    monkeypatch.setattr(harness, "render_maps", _fake_renderer({}))
+    harness.check_parity(_fake_scene(), harness._parse([]), "classic")
+
+
+@pytest.mark.parametrize("implementation", ["fused_dense", "fused_packed"])
+def test_parity_gate_rejects_a_differing_implementation(monkeypatch, implementation):
+    monkeypatch.setattr(harness, "render_maps", _fake_renderer({implementation: 1e-3}))
+    with pytest.raises(AssertionError):
+        harness.check_parity(_fake_scene(), harness._parse([]), "classic")
+
+
+@pytest.mark.gpu
+@pytest.mark.skipif(not torch.cuda.is_available(), reason="needs a GPU")
+def test_tiny_run_reports_every_implementation(tmp_path):
+    output = tmp_path / "report.json"
+    harness.run([
+        "--num-primitives", "1500", "--num-scenes", "2", "--num-cameras", "2",
+        "--image-width", "80", "--image-height", "48", "--warmup-iterations", "1",
+        "--measurement-iterations", "2", "--profile-iterations", "1",
+        "--output-json", str(output),
+    ])
+    report = json.loads(output.read_text())
+    assert set(report) >= {"environment", "workload", "timing", "results"}
+    assert report["workload"]["num_primitives"] == 1500
+    rows = {(r["method"], r["implementation"]): r for r in report["results"]}
+    assert set(rows) == {(m, i) for m in ("classic", "neural") for i in harness.IMPLEMENTATIONS}
+    for (method, implementation), row in rows.items():
+        for key in ("forward_ms", "backward_ms", "forward_backward_ms", "images_per_second",
+                    "peak_allocated_memory_mb", "forward_kernel_ms", "backward_kernel_ms"):
+            assert row[key] > 0, (method, implementation, key)
+        assert row["forward_backward_ms"] == pytest.approx(row["forward_ms"] + row["backward_ms"])
+        assert row["images_per_second"] == pytest.approx(4000 / row["forward_backward_ms"])
+    for method in ("classic", "neural"):
+        assert rows[(method, "single_view_loop")]["speedup_vs_single_view_loop"] == 1.0
