@@ -46,6 +46,11 @@ _SIGNATURES = {
     ),
     "gs_sh_forward": (_c_int, [_c_ptr] * 4 + [_c_i64] * 3 + [_c_int, _c_ptr]),
     "gs_sh_backward": (_c_int, [_c_ptr] * 7 + [_c_i64] * 3 + [_c_int, _c_ptr]),
+    "gs_check_values": (
+        _c_int,
+        [_c_ptr, _c_ptr, _c_int] + [_c_ptr] * 5 + [_c_i64] + [_c_ptr] * 2 + [_c_i64]
+        + [_c_ptr, _c_ptr],
+    ),
     "gs_scan_workspace_size": (_c_size, [_c_i64]),
     "gs_pack_visible": (_c_int, [_c_ptr, _c_i64, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_size, _c_ptr]),
     "gs_records_forward": (
@@ -114,6 +119,7 @@ PROFILE_FAMILIES = {
     "sort": 5,
     "render_forward": 6,
     "render_backward": 7,
+    "validate": 8,
 }
 
 
@@ -358,6 +364,50 @@ def pack_visible(radii: torch.Tensor, with_rows: bool = False):
     )
     selected = selected[: int(total.item())]
     return (selected, rows[:count]) if with_rows else selected
+
+
+# --------------------------------------------------------------------------
+# Input value contracts (rendering.py:88-153).
+
+CHECK_MAX_TENSORS = 16
+
+
+def check_values(tensors, quaternions, scales, opacities, view_matrices, intrinsics,
+                 weights=None, magnitudes=None) -> int:
+    """Violated-contract bits of gs_check_values over the given inputs.
+
+    Bit k < 16: tensors[k] is not finite; the GS_CHECK_* bits above that
+    name the value contracts. One launch and one read-back of the word."""
+    _require(len(tensors) <= CHECK_MAX_TENSORS, "too many tensors to check")
+    surfels = quaternions.numel() // 4
+    images = view_matrices.numel() // 16
+    inputs = [*tensors, quaternions, scales, opacities, view_matrices, intrinsics]
+    for value in inputs + [v for v in (weights, magnitudes) if v is not None]:
+        _check_float(value, quaternions)
+    _require(
+        quaternions.numel() == 4 * surfels and scales.numel() == 2 * surfels
+        and opacities.numel() == surfels
+        and all(v is None or v.numel() == 4 * surfels for v in (weights, magnitudes)),
+        "surfel tensors disagree in size",
+    )
+    _require(
+        view_matrices.numel() == 16 * images and intrinsics.numel() == 9 * images,
+        "camera tensors disagree in size",
+    )
+    count = len(tensors)
+    pointers = (_c_ptr * max(count, 1))(*[t.data_ptr() for t in tensors])
+    sizes = (_c_i64 * max(count, 1))(*[t.numel() for t in tensors])
+    device = quaternions.device
+    with torch.cuda.device(device):
+        violations = torch.zeros(1, dtype=torch.int32, device=device)
+        _check(
+            lib.gs_check_values(
+                pointers, sizes, count, _ptr(quaternions), _ptr(scales), _ptr(opacities),
+                _ptr(weights), _ptr(magnitudes), surfels, _ptr(view_matrices), _ptr(intrinsics),
+                images, _ptr(violations), _stream(device),
+            )
+        )
+        return int(violations.item()) & 0xFFFFFFFF
 
 
 # --------------------------------------------------------------------------

@@ -186,74 +186,56 @@ def check_tensor(
         raise ValueError(f"{name} must be contiguous")
 
 
-def _all_close(value: torch.Tensor, target, **tolerances) -> torch.Tensor:
-    return torch.isclose(value, value.new_tensor(target), **tolerances).all()
+# Value contracts in the order the reference lists them (rendering.py:95-148),
+# one bit each above the per-tensor finiteness bits of gs_check_values.
+VALUE_CONTRACTS = (
+    "scales must be strictly positive",
+    "opacities must lie in [0, 1]",
+    "quaternions must be unit wxyz vectors",
+    "view_matrices must have last row [0, 0, 0, 1]",
+    "intrinsics must have last row [0, 0, 1]",
+    "intrinsics fx and fy must be positive",
+    "view_matrices rotations must be orthonormal",
+    "view_matrices rotations must have determinant +1",
+    "frequency_weights must be nonnegative",
+    "frequency_magnitudes must be nonnegative",
+    "frequency_weights must sum to one",
+)
+
+
+def describe_violations(names, violations: int) -> list[str]:
+    """Messages of the contracts set in a gs_check_values word, in order."""
+    messages = [
+        f"{name} must contain only finite values"
+        for bit, name in enumerate(names)
+        if violations >> bit & 1
+    ]
+    first = _native.CHECK_MAX_TENSORS
+    messages += [text for k, text in enumerate(VALUE_CONTRACTS) if violations >> (first + k) & 1]
+    return messages
 
 
 @torch.no_grad()
 def check_values(
     tensors, quaternions, scales, opacities, view_matrices, intrinsics, appearance, neural
 ):
-    """Numerical contracts, evaluated on the device and read back once.
+    """Numerical contracts, evaluated by one HIP kernel and read back once.
 
-    Raises ValueError naming every violated contract (rendering.py:88-153).
+    Every tensor in ``tensors`` must be finite; scales positive; opacities
+    in [0, 1]; quaternions unit; views rigid with last row [0, 0, 0, 1];
+    intrinsics with last row [0, 0, 1] and positive focal lengths; classic
+    frequency weights nonnegative and summing to one and magnitudes
+    nonnegative. Raises ValueError naming every violated contract
+    (rendering.py:88-153).
     """
-    unit = {"atol": 1e-4, "rtol": 1e-4}
-    checks: list[tuple[str, torch.Tensor]] = []
-    for name, (value, _) in tensors.items():
-        checks.append((f"{name} must contain only finite values", torch.isfinite(value).all()))
-    checks.append(("scales must be strictly positive", (scales > 0).all()))
-    checks.append(
-        ("opacities must lie in [0, 1]", ((opacities >= 0) & (opacities <= 1)).all())
+    weights, magnitudes = (None, None) if neural else (appearance[2], appearance[3])
+    violations = _native.check_values(
+        [value for value, _ in tensors.values()], quaternions, scales, opacities,
+        view_matrices, intrinsics, weights, magnitudes,
     )
-    checks.append(
-        (
-            "quaternions must be unit wxyz vectors",
-            _all_close(quaternions.square().sum(-1), 1.0, **unit),
-        )
-    )
-    checks.append(
-        (
-            "view_matrices must have last row [0, 0, 0, 1]",
-            _all_close(view_matrices[..., 3, :], [0.0, 0.0, 0.0, 1.0]),
-        )
-    )
-    checks.append(
-        (
-            "intrinsics must have last row [0, 0, 1]",
-            _all_close(intrinsics[..., 2, :], [0.0, 0.0, 1.0]),
-        )
-    )
-    checks.append(
-        (
-            "intrinsics fx and fy must be positive",
-            ((intrinsics[..., 0, 0] > 0) & (intrinsics[..., 1, 1] > 0)).all(),
-        )
-    )
-    rotation = view_matrices[..., :3, :3]
-    identity = torch.eye(3, device=rotation.device, dtype=rotation.dtype)
-    checks.append(
-        (
-            "view_matrices rotations must be orthonormal",
-            torch.isclose(rotation.transpose(-1, -2) @ rotation, identity, **unit).all(),
-        )
-    )
-    checks.append(
-        (
-            "view_matrices rotations must have determinant +1",
-            _all_close(torch.linalg.det(rotation), 1.0, **unit),
-        )
-    )
-    if not neural:
-        weights, magnitudes = appearance[2], appearance[3]
-        checks.append(("frequency_weights must be nonnegative", (weights >= 0).all()))
-        checks.append(("frequency_magnitudes must be nonnegative", (magnitudes >= 0).all()))
-        checks.append(
-            ("frequency_weights must sum to one", _all_close(weights.sum(-1), 1.0, **unit))
-        )
-    passed = torch.stack([ok for _, ok in checks]).tolist()
-    if not all(passed):
-        raise ValueError("; ".join(message for (message, _), ok in zip(checks, passed) if not ok))
+    messages = describe_violations(list(tensors), violations)
+    if messages:
+        raise ValueError("; ".join(messages))
 
 
 def quaternion_matrix(q: torch.Tensor) -> torch.Tensor:

@@ -152,6 +152,40 @@ int gs_sh_backward(const float* first, const float* second, const float* directi
                    int32_t degree, void* stream);
 
 /* ------------------------------------------------------------------ */
+/* Input value contracts (replaces check_values, rendering.py:88-153,
+ * which the reference evaluates as a chain of PyTorch ops).           */
+
+/* One bit per violated contract, in the order the reference lists them:
+ * bit k (k < GS_CHECK_MAX_TENSORS) = tensors[k] holds a NaN or infinity,
+ * then the value contracts below. */
+#define GS_CHECK_MAX_TENSORS 16
+#define GS_CHECK_SCALES_POSITIVE (1u << 16)        /* scales > 0 */
+#define GS_CHECK_OPACITIES_RANGE (1u << 17)        /* 0 <= opacities <= 1 */
+#define GS_CHECK_QUATERNIONS_UNIT (1u << 18)       /* |q|^2 close to 1 */
+#define GS_CHECK_VIEW_LAST_ROW (1u << 19)          /* view row 3 = [0,0,0,1] */
+#define GS_CHECK_INTRINSICS_LAST_ROW (1u << 20)    /* K row 2 = [0,0,1] */
+#define GS_CHECK_FOCAL_POSITIVE (1u << 21)         /* fx > 0 and fy > 0 */
+#define GS_CHECK_ROTATION_ORTHONORMAL (1u << 22)   /* R^T R close to I */
+#define GS_CHECK_ROTATION_DETERMINANT (1u << 23)   /* det R close to +1 */
+#define GS_CHECK_WEIGHTS_NONNEGATIVE (1u << 24)    /* frequency_weights >= 0 */
+#define GS_CHECK_MAGNITUDES_NONNEGATIVE (1u << 25) /* frequency_magnitudes >= 0 */
+#define GS_CHECK_WEIGHTS_SUM (1u << 26)            /* frequency weights sum to 1 */
+
+/* ORs the violated contracts into *violations (a device uint32 the caller
+ * zeroes first) in one launch that reads every value once: finiteness of
+ * tensors[0..tensor_count) (sizes[k] floats each); per surfel (quaternions
+ * [surfels,4], scales [surfels,2], opacities [surfels], and, when not null,
+ * frequency_weights / frequency_magnitudes [surfels,4]); per image
+ * (view_matrices [images,4,4], intrinsics [images,3,3]). Closeness is
+ * torch.isclose's |x - t| <= atol + |rtol t| in float32: rtol 1e-5 / atol
+ * 1e-8 for the last rows, 1e-4 / 1e-4 for the other closeness contracts. */
+int gs_check_values(const float* const* tensors, const int64_t* sizes, int32_t tensor_count,
+                    const float* quaternions, const float* scales, const float* opacities,
+                    const float* frequency_weights, const float* frequency_magnitudes,
+                    int64_t surfels, const float* view_matrices, const float* intrinsics,
+                    int64_t images, uint32_t* violations, void* stream);
+
+/* ------------------------------------------------------------------ */
 /* Kernel 2: visible-pair packing and tile binning.                    */
 
 /* Scratch bytes for gs_pack_visible / gs_count_tiles over `count` items. */
@@ -288,7 +322,8 @@ int gs_render_backward(int32_t neural, const float* geometry, const float* appea
 #define GS_PROF_SORT 5
 #define GS_PROF_RENDER_FWD 6
 #define GS_PROF_RENDER_BWD 7
-#define GS_PROF_COUNT 8
+#define GS_PROF_VALIDATE 8
+#define GS_PROF_COUNT 9
 
 /* Enable (1) or disable (0) event timing; enabling clears the totals. */
 int gs_profile_enable(int32_t enable);

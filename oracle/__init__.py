@@ -14,6 +14,7 @@ path, so the HIP implementation can be checked against it:
                  appearance, front-to-back compositing, early termination),
                  vectorised over tiles; gradients come from torch autograd
   render.py      rendering.py:241-400 (record layout, packing, meta)
+  validate.py    rendering.py:88-153 (value contracts and their messages)
 
 Only ``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s
 ``cpu_baseline`` leg may import this package, and only as the checker or the
@@ -28,7 +29,8 @@ orthonormality on the sphere; binning against brute force over every tile;
 the compositor against a per-pixel float64 evaluation that solves the ray/
 plane system with ``torch.linalg.solve`` (as the reference's own test does),
 against closed forms (single opaque surfel, zero opacity, early stop) and
-against pairwise distortion; gradients against central finite differences.
+against pairwise distortion; gradients against central finite differences;
+the value contracts against planted violations with known answers.
 No function is "parity unpinned" except the equal-depth tie order, which the
 reference specifies (stable sort by pair index) but none of its tests pins.
 """

@@ -41,30 +41,6 @@ def test_check_tensor_messages():
         rendering.check_tensor("scales", torch.zeros(2, dtype=torch.float64), (2,), device)
 
 
-def test_check_values_names_every_violation():
-    values = make_inputs("classic")
-    values["scales"] = -values["scales"]
-    values["opacities"] = torch.full_like(values["opacities"], 2.0)
-    tensors = {k: (v, tuple(v.shape)) for k, v in values.items()}
-    appearance = tuple(values[k] for k in ("colors", "secondary_colors", "frequency_weights",
-                                            "frequency_magnitudes", "phases"))
-    with pytest.raises(ValueError) as error:
-        rendering.check_values(tensors, values["quaternions"], values["scales"],
-                               values["opacities"], values["view_matrices"],
-                               values["intrinsics"], appearance, False)
-    message = str(error.value)
-    assert "scales must be strictly positive" in message
-    assert "opacities must lie in [0, 1]" in message
-    assert "quaternions" not in message
-    values = make_inputs("classic")
-    values["intrinsics"] = values["intrinsics"].transpose(-1, -2).contiguous()
-    tensors = {k: (v, tuple(v.shape)) for k, v in values.items()}
-    with pytest.raises(ValueError, match="last row"):
-        rendering.check_values(tensors, values["quaternions"], values["scales"],
-                               values["opacities"], values["view_matrices"],
-                               values["intrinsics"], appearance, False)
-
-
 def test_quaternion_matrix_is_a_rotation():
     q = torch.randn(10, 4, dtype=torch.float64)
     R = rendering.quaternion_matrix(q)
