@@ -271,8 +271,14 @@ _NEURAL_FIELDS = (
 def render(
     means, quaternions, scales, opacities, appearance, view_matrices, intrinsics, width,
     height, backgrounds, packed, near_plane, far_plane, neural, sh_degree, validate,
+    screen_points=None,
 ):
-    """Validate, project every (scene, camera) pair, and composite in one launch."""
+    """Validate, project every (scene, camera) pair, and composite in one launch.
+
+    ``screen_points`` (optional, [Q, 2] float32, one row per projected pair)
+    receives the gradient of the projected means, the screen-space gradient
+    the upstream rasterizers write into their ``means2D`` argument; its
+    values are not used."""
     if not isinstance(means, torch.Tensor) or means.ndim < 2 or means.shape[-1] != 3:
         raise ValueError("means must have shape [..., N, 3]")
     if not means.is_cuda or means.dtype != torch.float32:
@@ -356,9 +362,14 @@ def render(
         flat = [t.reshape(scenes, n, math.prod(shape)) for t, (_, shape) in zip(appearance, fields)]
         parameters = torch.cat(flat, dim=-1).reshape(scenes * n, width_of_row)
         opacity_rows = opacities.reshape(scenes * n)
+    screen_means = projected_means
+    if screen_points is not None:
+        if screen_points.shape != projected_means.shape:
+            raise ValueError(f"screen_points must have shape {tuple(projected_means.shape)}")
+        screen_means = projected_means + (screen_points - screen_points.detach())
     rgb, alpha, depth, normals, distortion = Composite.apply(
         geometry,
-        projected_means,
+        screen_means,
         parameters,
         opacity_rows,
         primitive_ids,
