@@ -95,26 +95,38 @@ __device__ __forceinline__ float reject_threshold(float opacity) {
   return 2.f * logf(255.f * opacity) * (1.f + 1e-4f) + 1e-4f;
 }
 
-// Screen box (x0, x1, y0, y1) outside which no pixel can accept the record.
-// sample_surface rejects a pixel unless rho2 <= thr or rho3 <= thr:
+// Screen footprint of a record: the region where sample_surface can pass
+// its footprint test, rho2 <= thr or rho3 <= thr.
 //  * rho2 = 2 |xy - pixel|^2 <= thr is a disc of radius sqrt(thr / 2);
 //  * rho3 = u^2 + v^2 of the ray's hit on the surface plane (u, v in the
 //    plane's scaled axes, columns of T) is <= thr on the image of the disc
 //    u^2 + v^2 <= thr. With the whole disc in front of the camera
-//    (T22 > sqrt(thr) |(T20, T21)|) that image is an ellipse whose box
-//    follows from the dual conic C = T diag(thr, thr, -1) T^T: centre
+//    (T22 > sqrt(thr) |(T20, T21)|) that image is an ellipse whose centre
+//    and box follow from the dual conic C = T diag(thr, thr, -1) T^T: centre
 //    C02 / C22 and half width sqrt(C02^2 - C00 C22) / |C22| (y alike).
 //    The numerator is expanded into 2x2 minors of rows 0 and 2 of T,
 //    C02^2 - C00 C22 = thr (m02^2 + m12^2) - thr^2 m01^2, which avoids the
 //    cancellation of two squared pixel coordinates. Otherwise the image is
-//    unbounded and nothing is culled.
-// A margin of 2% of the half extent plus one pixel keeps float rounding in
-// here and in sample_surface from excluding an accepted pixel. Non-finite
-// values give an unbounded box, thr <= 0 (no pixel can reach alpha >=
-// 1/255) an empty one.
-__device__ float4 footprint_box(const float* g, float thr) {
+//    unbounded.
+// The box (x0, x1, y0, y1) bounds the union with a margin of 2% of the half
+// extent plus one pixel, which keeps float rounding in here and in
+// sample_surface from excluding an accepted pixel. Non-finite values give an
+// unbounded box, thr <= 0 (no pixel can reach alpha >= 1/255) an empty one.
+struct Footprint {
+  float4 box;
+  float cx, cy;  // ellipse centre (bounded footprints)
+  bool bounded;  // the rho3 region is an ellipse
+};
+
+__device__ Footprint footprint(const float* g, float thr) {
   constexpr float kHuge = 1e30f;
-  if (!(thr > 0.f)) return make_float4(kHuge, -kHuge, kHuge, -kHuge);
+  Footprint f;
+  f.bounded = false;
+  f.cx = f.cy = 0.f;
+  if (!(thr > 0.f)) {
+    f.box = make_float4(kHuge, -kHuge, kHuge, -kHuge);
+    return f;
+  }
   const float c = thr;
   const float disc = sqrtf(0.5f * c);
   float x0 = g[9] - disc, x1 = g[9] + disc, y0 = g[10] - disc, y1 = g[10] + disc;
@@ -134,13 +146,16 @@ __device__ float4 footprint_box(const float* g, float thr) {
       const float half = sqrtf(fmaxf(c * (m02 * m02 + m12 * m12) - c * c * m01 * m01, 0.f)) *
                          fabsf(inv);
       if (axis == 0) {
+        f.cx = centre;
         x0 = fminf(x0, centre - half);
         x1 = fmaxf(x1, centre + half);
       } else {
+        f.cy = centre;
         y0 = fminf(y0, centre - half);
         y1 = fmaxf(y1, centre + half);
       }
     }
+    f.bounded = true;
   } else {
     x0 = y0 = -kHuge;  // the disc's image is unbounded: cull nothing
     x1 = y1 = kHuge;
@@ -150,9 +165,78 @@ __device__ float4 footprint_box(const float* g, float thr) {
   x1 += mx;
   y0 -= my;
   y1 += my;
-  if (isfinite(x0) && isfinite(x1) && isfinite(y0) && isfinite(y1))
-    return make_float4(x0, x1, y0, y1);
-  return make_float4(-kHuge, kHuge, -kHuge, kHuge);
+  if (isfinite(x0) && isfinite(x1) && isfinite(y0) && isfinite(y1) && isfinite(f.cx) &&
+      isfinite(f.cy)) {
+    f.box = make_float4(x0, x1, y0, y1);
+  } else {
+    f.box = make_float4(-kHuge, kHuge, -kHuge, kHuge);
+    f.bounded = false;
+  }
+  return f;
+}
+
+// Whether box (x0, x1, y0, y1) meets the 8x8 pixels [qx, qx+7] x [qy, qy+7].
+__device__ __forceinline__ bool box_meets(float4 b, float qx, float qy) {
+  return (b.y >= qx) & (b.x <= qx + 7.f) & (b.w >= qy) & (b.z <= qy + 7.f);
+}
+
+// Whether any pixel of the 8x8 quadrant at (qx, qy) can pass the footprint
+// test, decided on the rectangle R = [qx - 1/2, qx + 7 + 1/2] x (y alike):
+//  * the disc meets R when the point of R nearest its centre lies in it;
+//  * for a bounded footprint, the ellipse is {Q <= 0} with Q = p0^2 + p1^2 -
+//    thr p2^2 and p = x a + y b + c, the affine function sample_surface
+//    evaluates as k x l (a = t1 x t2, b = t2 x t0, c = t0 x t1 for the rows
+//    t of T). Q is convex, so it meets R when its centre lies in R or when
+//    the minimum of Q over an edge of R facing the centre is <= 0; along an
+//    edge Q is a parabola, minimised at its clamped vertex.
+// The half-pixel growth and a relative slack of 1e-3 on both comparisons
+// keep float rounding from excluding a pixel the per-pixel test accepts.
+// Unbounded footprints fall back to the box.
+__device__ bool quadrant_reachable(const float* g, float thr, float qx, float qy) {
+  const Footprint f = footprint(g, thr);
+  if (!box_meets(f.box, qx, qy)) return false;
+  if (!f.bounded) return true;
+  constexpr float kGrow = 0.5f, kSlack = 1e-3f;
+  const float x0 = qx - kGrow, x1 = qx + 7.f + kGrow;
+  const float y0 = qy - kGrow, y1 = qy + 7.f + kGrow;
+  const float dx = fminf(fmaxf(g[9], x0), x1) - g[9];
+  const float dy = fminf(fmaxf(g[10], y0), y1) - g[10];
+  if (2.f * (dx * dx + dy * dy) <= thr * (1.f + kSlack)) return true;
+  const bool out_x = (f.cx < x0) | (f.cx > x1);
+  const bool out_y = (f.cy < y0) | (f.cy > y1);
+  if (!out_x && !out_y) return true;
+  const float* t0 = g;
+  const float* t1 = g + 3;
+  const float* t2 = g + 6;
+  const float a[3] = {t1[1] * t2[2] - t1[2] * t2[1], t1[2] * t2[0] - t1[0] * t2[2],
+                      t1[0] * t2[1] - t1[1] * t2[0]};
+  const float b[3] = {t2[1] * t0[2] - t2[2] * t0[1], t2[2] * t0[0] - t2[0] * t0[2],
+                      t2[0] * t0[1] - t2[1] * t0[0]};
+  const float c[3] = {t0[1] * t1[2] - t0[2] * t1[1], t0[2] * t1[0] - t0[0] * t1[2],
+                      t0[0] * t1[1] - t0[1] * t1[0]};
+  const float qaa = a[0] * a[0] + a[1] * a[1] - thr * a[2] * a[2];
+  const float qbb = b[0] * b[0] + b[1] * b[1] - thr * b[2] * b[2];
+  if (!(qaa > 0.f && qbb > 0.f)) return true;
+  bool hit = false;
+  if (out_x) {  // edge x = ex, vertex of Q(ex, y) clamped to [y0, y1]
+    const float ex = f.cx < x0 ? x0 : x1;
+    const float u[3] = {ex * a[0] + c[0], ex * a[1] + c[1], ex * a[2] + c[2]};
+    const float ub = u[0] * b[0] + u[1] * b[1] - thr * u[2] * b[2];
+    const float y = fminf(fmaxf(-ub / qbb, y0), y1);
+    const float p[3] = {u[0] + y * b[0], u[1] + y * b[1], u[2] + y * b[2]};
+    const float plane = p[0] * p[0] + p[1] * p[1], axial = thr * p[2] * p[2];
+    hit = plane - axial <= kSlack * (plane + axial);
+  }
+  if (out_y) {  // edge y = ey, vertex of Q(x, ey) clamped to [x0, x1]
+    const float ey = f.cy < y0 ? y0 : y1;
+    const float u[3] = {ey * b[0] + c[0], ey * b[1] + c[1], ey * b[2] + c[2]};
+    const float ua = u[0] * a[0] + u[1] * a[1] - thr * u[2] * a[2];
+    const float x = fminf(fmaxf(-ua / qaa, x0), x1);
+    const float p[3] = {u[0] + x * a[0], u[1] + x * a[1], u[2] + x * a[2]};
+    const float plane = p[0] * p[0] + p[1] * p[1], axial = thr * p[2] * p[2];
+    hit = hit | (plane - axial <= kSlack * (plane + axial));
+  }
+  return hit;
 }
 
 // A value that is the same in every lane, moved to scalar registers so
@@ -161,11 +245,6 @@ __device__ __forceinline__ uint64_t wave_uniform(uint64_t v) {
   const uint32_t lo = __builtin_amdgcn_readfirstlane(uint32_t(v));
   const uint32_t hi = __builtin_amdgcn_readfirstlane(uint32_t(v >> 32));
   return (uint64_t(hi) << 32) | lo;
-}
-
-// Whether box (x0, x1, y0, y1) meets the 8x8 pixels [qx, qx+7] x [qy, qy+7].
-__device__ __forceinline__ bool box_meets(float4 b, float qx, float qy) {
-  return (b.y >= qx) & (b.x <= qx + 7.f) & (b.w >= qy) & (b.z <= qy + 7.f);
 }
 
 struct Sample {
@@ -260,11 +339,11 @@ __device__ __forceinline__ void shade(const float* r, const float* s, Shade& a) 
 // gathers raw fields into LDS, and one thread per record derives the row's
 // constants.
 template <bool Neural>
-__device__ __forceinline__ void load_batch(float* rows, float* raw, int* ids, int64_t* prims,
-                                           uint64_t* masks, float tile_x, float tile_y,
-                                           int count, int id, int64_t prim,
-                                           const float* geometry, const float* appearance,
-                                           const float* opacities) {
+__device__ __forceinline__ uint64_t load_batch(float* rows, float* raw, int* ids,
+                                               int64_t* prims, float tile_x, float tile_y,
+                                               int count, int id, int64_t prim,
+                                               const float* geometry, const float* appearance,
+                                               const float* opacities) {
   using L = Layout<Neural>;
   const int t = threadIdx.x;
   if (t < count) {  // (id, prim): this thread's record, fetched by the caller ahead of time
@@ -300,27 +379,18 @@ __device__ __forceinline__ void load_batch(float* rows, float* raw, int* ids, in
     }
   }
   __syncthreads();
-  // Wave 1, while wave 0 derives the row constants: record j's footprint
-  // box against the tile's four 8x8 quadrants (one per wave), as four
-  // 64-bit masks whose bit j says that record j may touch the quadrant.
-  if ((t >> 6) == 1) {
-    const int j = t - 64;
-    float4 box = make_float4(1.f, -1.f, 1.f, -1.f);  // empty
-    if (j < count) {
-      const float* g = raw + j * L::RAW_STRIDE;
-      box = footprint_box(g, reject_threshold(g[kGeometry]));
-    }
-    const uint64_t m0 = __ballot(box_meets(box, tile_x, tile_y));
-    const uint64_t m1 = __ballot(box_meets(box, tile_x + 8.f, tile_y));
-    const uint64_t m2 = __ballot(box_meets(box, tile_x, tile_y + 8.f));
-    const uint64_t m3 = __ballot(box_meets(box, tile_x + 8.f, tile_y + 8.f));
-    if (j == 0) {
-      masks[0] = m0;
-      masks[1] = m1;
-      masks[2] = m2;
-      masks[3] = m3;
-    }
+  // Every wave tests the batch's records (one per lane) against its own 8x8
+  // quadrant of the tile; bit j of the ballot says that record j may touch
+  // the quadrant. Wave 0 then also derives the row constants.
+  const int wave = t >> 6;
+  const int j = t & 63;
+  bool reach = false;
+  if (j < count) {
+    const float* g = raw + j * L::RAW_STRIDE;
+    reach = quadrant_reachable(g, reject_threshold(g[kGeometry]), tile_x + float(wave & 1) * 8.f,
+                               tile_y + float(wave >> 1) * 8.f);
   }
+  const uint64_t mask = __ballot(reach);
   if (t < count) {
     const float* g = raw + t * L::RAW_STRIDE;
     const float opacity = g[kGeometry];
@@ -369,6 +439,7 @@ __device__ __forceinline__ void load_batch(float* rows, float* raw, int* ids, in
     }
   }
   __syncthreads();
+  return mask;
 }
 
 struct TilePixel {
@@ -491,7 +562,6 @@ __global__ __launch_bounds__(kTilePixels) void render_forward_kernel(
   __shared__ __align__(16) float raw[kBatch * L::RAW_STRIDE];
   __shared__ int ids[kBatch];
   __shared__ int64_t prims[kBatch];
-  __shared__ uint64_t masks[4];
   const int tile = order[blockIdx.x];
   const TilePixel tp = tile_pixel(tile, width, height, tw, th);
   const float x = float(tp.px), y = float(tp.py);
@@ -523,14 +593,14 @@ __global__ __launch_bounds__(kTilePixels) void render_forward_kernel(
     const int64_t prim = next_prim;
     const bool ahead = int(threadIdx.x) < min(kBatch, range.y - start - kBatch);
     if (ahead) next_id = point_list[start + kBatch + threadIdx.x];
-    load_batch<Neural>(rows, raw, ids, prims, masks, tile_x, tile_y, count, id, prim, geometry,
-                       appearance, opacities);
+    const uint64_t reach = load_batch<Neural>(rows, raw, ids, prims, tile_x, tile_y, count, id,
+                                              prim, geometry, appearance, opacities);
     if (ahead) next_prim = primitive_ids[next_id];
     // Only the records whose footprint meets this wave's quadrant, in list
     // order. The loop runs in lockstep across the wave: finished lanes are
     // masked through `done` rather than leaving the loop, so that every
     // branch below is on a wave-wide (scalar) condition.
-    uint64_t todo = __all(done) ? 0 : wave_uniform(masks[wave]);
+    uint64_t todo = __all(done) ? 0 : wave_uniform(reach);
     while (todo) {
       const int j = __builtin_ctzll(todo);
       todo &= todo - 1;
@@ -662,7 +732,6 @@ __global__ __launch_bounds__(kTilePixels) void render_backward_kernel(
   __shared__ int ids[kBatch];
   __shared__ int64_t prims[kBatch];
   __shared__ float bg_acc[3];
-  __shared__ uint64_t masks[4];
   const int lane = lane_id();
   const int tile = order[blockIdx.x];
   const TilePixel tp = tile_pixel(tile, width, height, tw, th);
@@ -722,10 +791,10 @@ __global__ __launch_bounds__(kTilePixels) void render_backward_kernel(
     const int64_t prim = next_prim;
     const bool ahead = int(threadIdx.x) < min(kBatch, start - kBatch);
     if (ahead) next_id = point_list[range.x + start - kBatch - 1 - threadIdx.x];
-    load_batch<Neural>(rows, raw, ids, prims, masks, tile_x, tile_y, count, id, prim, geometry,
-                       appearance, opacities);
+    const uint64_t reach = load_batch<Neural>(rows, raw, ids, prims, tile_x, tile_y, count, id,
+                                              prim, geometry, appearance, opacities);
     if (ahead) next_prim = primitive_ids[next_id];
-    uint64_t todo = wave_uniform(masks[wave]);
+    uint64_t todo = wave_uniform(reach);
     // Row j holds list position start - j (counted from 1).
     const int beyond = start - wave_last;  // rows j < beyond lie past wave_last
     if (beyond >= 64) todo = 0;
