@@ -62,7 +62,8 @@ _SIGNATURES = {
     "gs_records_backward_workspace_size": (_c_size, [_c_i64, _c_i64, _c_i64, _c_int]),
     "gs_records_backward": (
         _c_int,
-        [_c_ptr] * 7 + [_c_int, _c_i64, _c_i64, _c_i64] + [_c_ptr] * 18 + [_c_size, _c_ptr],
+        [_c_ptr] * 7 + [_c_int, _c_i64, _c_i64, _c_i64] + [_c_ptr] * 4 + [_c_i64]
+        + [_c_ptr] * 14 + [_c_size, _c_ptr],
     ),
     "gs_count_tiles": (
         _c_int,
@@ -335,11 +336,23 @@ def bin_tiles(order, starts, rects, images, width, height, intersections):
     return point_list, ranges
 
 
-def bin_depth_first(geometry, radii, image_ids, images, width, height):
+def bin_depth_first(geometry, radii, image_ids, images, width, height, overlap=None):
     """Both binning stages with the one host synchronisation for M between
-    them (rasterize.cu:466-469): (point_list, ranges)."""
+    them (rasterize.cu:466-469): (point_list, ranges).
+
+    M is copied to pinned host memory behind stage 1 and the host waits on
+    an event recorded after that copy, not on the stream, so GPU work that
+    ``overlap()`` queues (independent of M) runs while the host waits."""
     order, starts, rects, total = bin_order(geometry, radii, image_ids, width, height)
-    intersections = int(total.item())
+    stream = torch.cuda.current_stream(geometry.device)
+    host = torch.empty(1, dtype=torch.int64, pin_memory=True)
+    host.copy_(total, non_blocking=True)
+    ready = torch.cuda.Event()
+    ready.record(stream)
+    if overlap is not None:
+        overlap()
+    ready.synchronize()
+    intersections = int(host[0])
     check_intersections(intersections)
     return bin_tiles(order, starts, rects, images, width, height, intersections)
 
@@ -493,7 +506,14 @@ def records_backward(means, quaternions, scales, view_matrices, intrinsics, sh, 
         return None if value is None else value.contiguous()
 
     grad_geometry = contiguous(grad_geometry)
-    grad_projected_means = contiguous(grad_projected_means)
+    # The compositor's gradient of the projected means is the xy columns of
+    # its geometry gradient; rows of any stride are read in place.
+    if grad_projected_means is not None and not (
+        grad_projected_means.dim() == 2 and grad_projected_means.stride(1) == 1
+        and grad_projected_means.stride(0) >= 2
+    ):
+        grad_projected_means = grad_projected_means.contiguous()
+    projected_stride = 2 if grad_projected_means is None else grad_projected_means.stride(0)
     grad_appearance = contiguous(grad_appearance)
     grad_opacity_rows = contiguous(grad_opacity_rows)
     with torch.cuda.device(device):
@@ -518,7 +538,8 @@ def records_backward(means, quaternions, scales, view_matrices, intrinsics, sh, 
                 _ptr(means), _ptr(quaternions), _ptr(scales), _ptr(view_matrices),
                 _ptr(intrinsics), _ptr(first), _ptr(second), degree, scenes, cameras, n,
                 _ptr(row_of_pair), _ptr(geometry), _ptr(grad_geometry),
-                _ptr(grad_projected_means), _ptr(grad_appearance), _ptr(grad_opacity_rows),
+                _ptr(grad_projected_means), projected_stride, _ptr(grad_appearance),
+                _ptr(grad_opacity_rows),
                 _ptr(g_means), _ptr(g_quats), _ptr(g_scales), _ptr(g_views), _ptr(g_intrinsics),
                 *(_ptr(t) for t in sh_grads), _ptr(workspace), workspace.numel(),
                 _stream(device),
@@ -583,7 +604,7 @@ def _map_group_args(groups, what: str):
 
 def rasterize_forward(
     geometry, appearance, opacities, primitive_ids, image_ids, radii, backgrounds,
-    width, height, neural, near_plane, far_plane, outputs=None,
+    width, height, neural, near_plane, far_plane, outputs=None, overlap=None,
 ):
     """Bin, sort and composite: returns [maps, point_list, ranges, state, contributors].
 
@@ -594,7 +615,9 @@ def rasterize_forward(
 
     ``outputs`` (an addition): five float32 tensors [I,H,W,k], k in
     MAP_GROUPS, that receive the map channel groups instead of one maps
-    tensor; the first returned item is then that tuple.
+    tensor; the first returned item is then that tuple. ``overlap`` (an
+    addition): called once while the host waits for M, to queue GPU work
+    that does not depend on it.
     """
     _check_buffers(geometry, appearance, opacities, primitive_ids, backgrounds, neural)
     _require(
@@ -627,7 +650,8 @@ def rasterize_forward(
         tiles = images * tw * th
         state = torch.empty((images, height, width, 3), dtype=torch.float32, device=device)
         contributors = torch.empty((images, height, width), dtype=torch.int32, device=device)
-        point_list, ranges = bin_depth_first(geometry, radii, image_ids, images, width, height)
+        point_list, ranges = bin_depth_first(geometry, radii, image_ids, images, width, height,
+                                             overlap)
         if outputs is None:
             maps = torch.empty((images, height, width, MAP_SIZE), dtype=torch.float32,
                                device=device)
@@ -657,9 +681,15 @@ def rasterize_forward(
     return [maps, point_list, ranges, state, contributors]
 
 
+def zero_accumulators(geometry, appearance, opacities, backgrounds):
+    """Zeroed gradient accumulators for rasterize_backward."""
+    return (torch.zeros_like(geometry), torch.zeros_like(appearance),
+            torch.zeros_like(opacities), torch.zeros_like(backgrounds))
+
+
 def rasterize_backward(
     geometry, appearance, opacities, primitive_ids, backgrounds, point_list, ranges, state,
-    contributors, grad_maps, width, height, neural, near_plane, far_plane,
+    contributors, grad_maps, width, height, neural, near_plane, far_plane, accumulators=None,
 ):
     """Reverse compositing: returns [grad_geometry, grad_appearance, grad_opacities,
     grad_backgrounds] (rasterize.cu:506-529).
@@ -667,6 +697,8 @@ def rasterize_backward(
     ``grad_maps`` is the reference's [I,H,W,9] tensor or (an addition) a
     sequence of five per-group gradients [I,H,W,k] in MAP_GROUPS order, each
     a tensor of any strides or None (zero); strided views are read in place.
+    ``accumulators`` (an addition): zeroed tensors from zero_accumulators,
+    cleared ahead of time, that receive and are returned as the gradients.
     """
     _check_buffers(geometry, appearance, opacities, primitive_ids, backgrounds, neural)
     device = geometry.device
@@ -692,10 +724,16 @@ def rasterize_backward(
         "invalid saved compositor state",
     )
     with torch.cuda.device(device):
-        gg = torch.zeros_like(geometry)
-        ga = torch.zeros_like(appearance)
-        go = torch.zeros_like(opacities)
-        gb = torch.zeros_like(backgrounds)
+        if accumulators is None:
+            accumulators = zero_accumulators(geometry, appearance, opacities, backgrounds)
+        gg, ga, go, gb = accumulators
+        _require(
+            gg.shape == geometry.shape and ga.shape == appearance.shape
+            and go.shape == opacities.shape and gb.shape == backgrounds.shape
+            and all(t.is_contiguous() and t.dtype == torch.float32 and t.device == device
+                    for t in accumulators),
+            "invalid gradient accumulators",
+        )
         groups = [g if g is None else _pixel_strided(g) for g in groups]
         data, strides = _map_group_args(groups, "map gradients")
         workspace = _workspace(lib.gs_render_workspace_size(images, width, height), device)

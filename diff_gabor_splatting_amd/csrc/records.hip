@@ -371,7 +371,8 @@ __global__ __launch_bounds__(kShBlock) void sh_rows_backward_kernel(
 struct RowGrads {
   const int* row_of_pair;       // null: row = pair
   const float* geometry;        // [Q,17] dL/d(geometry row), or null
-  const float* projected;       // [Q,2] dL/d(projected means), or null
+  const float* projected;       // dL/d(projected means), row r at projected + r * stride
+  int64_t projected_stride;     // floats between rows of `projected` (2 when contiguous)
   const float* sh_directions;   // [S*C*N,3] direction gradients from SH, or null
   __device__ bool fetch(int64_t pair, PairGrads& g) const {
     const int64_t row = row_of_pair ? int64_t(row_of_pair[pair]) : pair;
@@ -382,8 +383,8 @@ struct RowGrads {
     // The geometry row's own xy columns duplicate the projected means;
     // their gradient arrives through `projected` only.
     g.has_xy = projected != nullptr;
-    g.gxy[0] = projected ? projected[row * 2 + 0] : 0.f;
-    g.gxy[1] = projected ? projected[row * 2 + 1] : 0.f;
+    g.gxy[0] = projected ? projected[row * projected_stride + 0] : 0.f;
+    g.gxy[1] = projected ? projected[row * projected_stride + 1] : 0.f;
     g.has_n = gg != nullptr;
     g.has_d = gg != nullptr || sh_directions != nullptr;
 #pragma unroll
@@ -492,8 +493,8 @@ int gs_records_backward(const float* means, const float* quaternions, const floa
                         int64_t scenes, int64_t cameras, int64_t n,
                         const int32_t* row_of_pair, const float* geometry,
                         const float* grad_geometry, const float* grad_projected_means,
-                        const float* grad_appearance_rows, const float* grad_opacity_rows,
-                        float* grad_means, float* grad_quaternions, float* grad_scales,
+                        int64_t grad_projected_stride, const float* grad_appearance_rows,
+                        const float* grad_opacity_rows, float* grad_means, float* grad_quaternions, float* grad_scales,
                         float* grad_view_matrices, float* grad_intrinsics,
                         float* grad_sh_first, float* grad_sh_second, float* grad_weights,
                         float* grad_magnitudes, float* grad_phases, float* grad_opacities,
@@ -506,6 +507,9 @@ int gs_records_backward(const float* means, const float* quaternions, const floa
              "SH degree must be -1 (none) or 0 through 3");
   GS_REQUIRE(grad_view_matrices && grad_intrinsics, GS_ERR_ARGUMENT,
              "null camera gradient pointer");
+  GS_REQUIRE(!grad_projected_means || grad_projected_stride >= 2, GS_ERR_ARGUMENT,
+             "projected-means gradient rows must be at least 2 floats apart, got %lld",
+             static_cast<long long>(grad_projected_stride));
   const size_t need = gs_records_backward_workspace_size(scenes, cameras, n, sh_degree);
   GS_REQUIRE(workspace && workspace_bytes >= need, GS_ERR_WORKSPACE,
              "record backward needs %zu workspace bytes, got %zu", need, workspace_bytes);
@@ -547,8 +551,9 @@ int gs_records_backward(const float* means, const float* quaternions, const floa
     }
     projection_backward_kernel<RowGrads><<<grid, kProjectBlock, 0, s>>>(
         means, quaternions, scales, view_matrices, intrinsics, cameras, n,
-        RowGrads{row_of_pair, grad_geometry, grad_projected_means, sh_dirs}, grad_means,
-        grad_quaternions, grad_scales, w.partials);
+        RowGrads{row_of_pair, grad_geometry, grad_projected_means, grad_projected_stride,
+                 sh_dirs},
+        grad_means, grad_quaternions, grad_scales, w.partials);
     GS_LAUNCHED("projection_backward_kernel");
   }
   camera_reduce_kernel<<<static_cast<unsigned>(scenes * cameras), kProjectBlock, 0, s>>>(

@@ -46,9 +46,18 @@ class Composite(torch.autograd.Function):
             torch.empty((images, height, width, k), dtype=torch.float32, device=geometry.device)
             for k in _native.MAP_GROUPS
         )
+        # The backward's zeroed accumulators are cleared while the host waits
+        # for the intersection count, when the GPU would otherwise idle.
+        ctx.accumulators = None
+
+        def clear_accumulators():
+            ctx.accumulators = _native.zero_accumulators(geometry, appearance, opacities,
+                                                         backgrounds)
+
+        overlap = clear_accumulators if any(ctx.needs_input_grad) else None
         _, points, ranges, state, contributors = _native.rasterize_forward(
             geometry, appearance, opacities, primitive_ids, image_ids, radii, backgrounds,
-            width, height, neural, near_plane, far_plane, outputs=outputs,
+            width, height, neural, near_plane, far_plane, outputs=outputs, overlap=overlap,
         )
         # Binning and early termination are discrete: only the saved sorted
         # lists and per-pixel state are needed to replay the tiles backwards.
@@ -63,8 +72,10 @@ class Composite(torch.autograd.Function):
     @staticmethod
     @once_differentiable
     def backward(ctx: Any, *grad_groups):
+        # A second backward through a retained graph gets fresh accumulators.
+        accumulators, ctx.accumulators = ctx.accumulators, None
         gg, ga, go, gb = _native.rasterize_backward(
-            *ctx.saved_tensors, list(grad_groups), *ctx.options
+            *ctx.saved_tensors, list(grad_groups), *ctx.options, accumulators=accumulators
         )
         return gg, gg[:, 9:11], ga, go, None, None, None, gb, None, None, None, None, None
 

@@ -116,7 +116,9 @@ size_t gs_records_backward_workspace_size(int64_t scenes, int64_t cameras, int64
 
 /* Adjoint of gs_records_forward given the compositor's row gradients:
  * grad_geometry [Q,17] (its xy columns are ignored: the projected-means
- * gradient arrives in grad_projected_means [Q,2]), and with SH
+ * gradient arrives in grad_projected_means, Q rows of 2 floats that start
+ * grad_projected_stride floats apart: 2 for a [Q,2] array, 17 for the xy
+ * columns of a [Q,17] one), and with SH
  * grad_appearance_rows [Q,18] and grad_opacity_rows [Q]; any may be null.
  * geometry is the forward's row output (SH reads the directions). Surfel and
  * camera gradients are overwritten: means, quaternions, scales,
@@ -129,7 +131,8 @@ int gs_records_backward(const float* means, const float* quaternions, const floa
                         int64_t scenes, int64_t cameras, int64_t n,
                         const int32_t* row_of_pair, const float* geometry,
                         const float* grad_geometry, const float* grad_projected_means,
-                        const float* grad_appearance_rows, const float* grad_opacity_rows,
+                        int64_t grad_projected_stride, const float* grad_appearance_rows,
+                        const float* grad_opacity_rows,
                         float* grad_means, float* grad_quaternions, float* grad_scales,
                         float* grad_view_matrices, float* grad_intrinsics,
                         float* grad_sh_first, float* grad_sh_second, float* grad_weights,

@@ -405,3 +405,19 @@ def test_forward_is_bitwise_deterministic():
     first = maps_from_result(rasterize_gabors(**values, width=64, height=64, sh_degree=3))
     second = maps_from_result(rasterize_gabors(**values, width=64, height=64, sh_degree=3))
     assert torch.equal(first, second)
+
+
+@pytest.mark.parametrize("method", ["classic", "neural"])
+def test_retained_graph_backward_twice(method):
+    """The compositor's accumulators are cleared ahead of the first backward;
+    a second backward through a retained graph must see fresh ones."""
+    values = on_gpu(make_inputs(method, cameras=2, primitives=9))
+    maps = maps_from_result(renderer(method)(**values, width=19, height=13))
+    weights = torch.linspace(-1.0, 1.0, maps.numel(), device=DEVICE).reshape(maps.shape)
+    first = torch.autograd.grad((maps * weights).sum(), list(values.values()), retain_graph=True)
+    second = torch.autograd.grad((maps * weights).sum(), list(values.values()))
+    for name, a, b in zip(values, first, second):
+        torch.testing.assert_close(a, b, atol=1e-6, rtol=1e-5, msg=name)
+    with torch.no_grad():
+        plain = maps_from_result(renderer(method)(**values, width=19, height=13))
+    torch.testing.assert_close(plain, maps.detach())
