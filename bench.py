@@ -142,7 +142,11 @@ def _loss(rgb, alpha, meta, channels):
     maps = torch.cat(
         (rgb, alpha, meta["accumulated_depth"], meta["normals"], meta["distortion"]), -1
     )
-    return maps[..., :channels].square().mean()
+    # A slice, even of every channel, would add a zero-fill and a copy to the
+    # backward; take it only when some channels are left out.
+    if channels != maps.shape[-1]:
+        maps = maps[..., :channels]
+    return maps.square().mean()
 
 
 def algorithmic_bytes(kind: str, neural: bool, pixels: int, records: int, pairs: int,

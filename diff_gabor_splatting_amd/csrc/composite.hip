@@ -108,32 +108,50 @@ __device__ __forceinline__ float reject_threshold(float opacity) {
 //    C02^2 - C00 C22 = thr (m02^2 + m12^2) - thr^2 m01^2, which avoids the
 //    cancellation of two squared pixel coordinates. Otherwise the image is
 //    unbounded.
+//  * Inside the box, the ellipse is {Q <= 0} with Q = p0^2 + p1^2 - thr p2^2
+//    and p = x a + y b + c, the affine function sample_surface evaluates as
+//    k x l (a = t1 x t2, b = t2 x t0, c = t0 x t1 for the rows t of T).
 // The box (x0, x1, y0, y1) bounds the union with a margin of 2% of the half
 // extent plus one pixel, which keeps float rounding in here and in
 // sample_surface from excluding an accepted pixel. Non-finite values give an
 // unbounded box, thr <= 0 (no pixel can reach alpha >= 1/255) an empty one.
-struct Footprint {
-  float4 box;
-  float cx, cy;  // ellipse centre (bounded footprints)
-  bool bounded;  // the rho3 region is an ellipse
+//
+// record_reach derives these per-record constants once per batch into an
+// LDS row of kReachPitch floats; quadrant_reach tests them against one wave's
+// 8x8 quadrant.
+struct ReachRow {
+  static constexpr int BOX = 0;        // x0, x1, y0, y1
+  static constexpr int CX = 4, CY = 5;  // ellipse centre
+  static constexpr int A = 6, B = 9, C = 12;  // p = x a + y b + c
+  static constexpr int QAA = 15, QBB = 16;    // Q's x^2 and y^2 coefficients
+  static constexpr int THR = 17, X = 18, Y = 19;
+  static constexpr int BOUNDED = 20;  // 1: test the ellipse exactly; 0: the box decides
 };
+constexpr int kReachPitch = 21;
 
-__device__ Footprint footprint(const float* g, float thr) {
+__device__ void record_reach(const float* g, float thr, float* out) {
   constexpr float kHuge = 1e30f;
-  Footprint f;
-  f.bounded = false;
-  f.cx = f.cy = 0.f;
+  using R = ReachRow;
+  out[R::THR] = thr;
+  out[R::X] = g[9];
+  out[R::Y] = g[10];
+  out[R::BOUNDED] = 0.f;
   if (!(thr > 0.f)) {
-    f.box = make_float4(kHuge, -kHuge, kHuge, -kHuge);
-    return f;
+    out[R::BOX + 0] = kHuge;
+    out[R::BOX + 1] = -kHuge;
+    out[R::BOX + 2] = kHuge;
+    out[R::BOX + 3] = -kHuge;
+    return;
   }
   const float c = thr;
-  const float disc = sqrtf(0.5f * c);
+  const float disc = __builtin_amdgcn_sqrtf(0.5f * c);
   float x0 = g[9] - disc, x1 = g[9] + disc, y0 = g[10] - disc, y1 = g[10] + disc;
+  float cx = 0.f, cy = 0.f;
   const float a = c * (g[6] * g[6] + g[7] * g[7]);
   const float c22 = a - g[8] * g[8];
+  bool bounded = false;
   if (g[8] > 0.f && c22 < -1e-3f * (a + g[8] * g[8])) {
-    const float inv = 1.f / c22;
+    const float inv = rcp(c22);
     // Row r of T against row 2: centre and half extent along that axis.
 #pragma unroll
     for (int axis = 0; axis < 2; ++axis) {
@@ -143,19 +161,20 @@ __device__ Footprint footprint(const float* g, float thr) {
       const float m02 = t[0] * g[8] - t[2] * g[6];
       const float m12 = t[1] * g[8] - t[2] * g[7];
       const float centre = c02 * inv;
-      const float half = sqrtf(fmaxf(c * (m02 * m02 + m12 * m12) - c * c * m01 * m01, 0.f)) *
-                         fabsf(inv);
+      const float half =
+          __builtin_amdgcn_sqrtf(fmaxf(c * (m02 * m02 + m12 * m12) - c * c * m01 * m01, 0.f)) *
+          fabsf(inv);
       if (axis == 0) {
-        f.cx = centre;
+        cx = centre;
         x0 = fminf(x0, centre - half);
         x1 = fmaxf(x1, centre + half);
       } else {
-        f.cy = centre;
+        cy = centre;
         y0 = fminf(y0, centre - half);
         y1 = fmaxf(y1, centre + half);
       }
     }
-    f.bounded = true;
+    bounded = true;
   } else {
     x0 = y0 = -kHuge;  // the disc's image is unbounded: cull nothing
     x1 = y1 = kHuge;
@@ -165,73 +184,86 @@ __device__ Footprint footprint(const float* g, float thr) {
   x1 += mx;
   y0 -= my;
   y1 += my;
-  if (isfinite(x0) && isfinite(x1) && isfinite(y0) && isfinite(y1) && isfinite(f.cx) &&
-      isfinite(f.cy)) {
-    f.box = make_float4(x0, x1, y0, y1);
-  } else {
-    f.box = make_float4(-kHuge, kHuge, -kHuge, kHuge);
-    f.bounded = false;
+  if (!(isfinite(x0) && isfinite(x1) && isfinite(y0) && isfinite(y1) && isfinite(cx) &&
+        isfinite(cy))) {
+    x0 = y0 = -kHuge;
+    x1 = y1 = kHuge;
+    bounded = false;
   }
-  return f;
-}
-
-// Whether box (x0, x1, y0, y1) meets the 8x8 pixels [qx, qx+7] x [qy, qy+7].
-__device__ __forceinline__ bool box_meets(float4 b, float qx, float qy) {
-  return (b.y >= qx) & (b.x <= qx + 7.f) & (b.w >= qy) & (b.z <= qy + 7.f);
+  out[R::BOX + 0] = x0;
+  out[R::BOX + 1] = x1;
+  out[R::BOX + 2] = y0;
+  out[R::BOX + 3] = y1;
+  if (!bounded) return;
+  const float* t0 = g;
+  const float* t1 = g + 3;
+  const float* t2 = g + 6;
+  const float va[3] = {t1[1] * t2[2] - t1[2] * t2[1], t1[2] * t2[0] - t1[0] * t2[2],
+                       t1[0] * t2[1] - t1[1] * t2[0]};
+  const float vb[3] = {t2[1] * t0[2] - t2[2] * t0[1], t2[2] * t0[0] - t2[0] * t0[2],
+                       t2[0] * t0[1] - t2[1] * t0[0]};
+  const float vc[3] = {t0[1] * t1[2] - t0[2] * t1[1], t0[2] * t1[0] - t0[0] * t1[2],
+                       t0[0] * t1[1] - t0[1] * t1[0]};
+  const float qaa = va[0] * va[0] + va[1] * va[1] - thr * va[2] * va[2];
+  const float qbb = vb[0] * vb[0] + vb[1] * vb[1] - thr * vb[2] * vb[2];
+  if (!(qaa > 0.f && qbb > 0.f)) return;  // not elliptic after all: the box decides
+#pragma unroll
+  for (int k = 0; k < 3; ++k) {
+    out[R::A + k] = va[k];
+    out[R::B + k] = vb[k];
+    out[R::C + k] = vc[k];
+  }
+  out[R::CX] = cx;
+  out[R::CY] = cy;
+  out[R::QAA] = qaa;
+  out[R::QBB] = qbb;
+  out[R::BOUNDED] = 1.f;
 }
 
 // Whether any pixel of the 8x8 quadrant at (qx, qy) can pass the footprint
 // test, decided on the rectangle R = [qx - 1/2, qx + 7 + 1/2] x (y alike):
+//  * the box must meet the quadrant;
 //  * the disc meets R when the point of R nearest its centre lies in it;
-//  * for a bounded footprint, the ellipse is {Q <= 0} with Q = p0^2 + p1^2 -
-//    thr p2^2 and p = x a + y b + c, the affine function sample_surface
-//    evaluates as k x l (a = t1 x t2, b = t2 x t0, c = t0 x t1 for the rows
-//    t of T). Q is convex, so it meets R when its centre lies in R or when
+//  * Q is convex, so the ellipse meets R when its centre lies in R or when
 //    the minimum of Q over an edge of R facing the centre is <= 0; along an
 //    edge Q is a parabola, minimised at its clamped vertex.
 // The half-pixel growth and a relative slack of 1e-3 on both comparisons
 // keep float rounding from excluding a pixel the per-pixel test accepts.
-// Unbounded footprints fall back to the box.
-__device__ bool quadrant_reachable(const float* g, float thr, float qx, float qy) {
-  const Footprint f = footprint(g, thr);
-  if (!box_meets(f.box, qx, qy)) return false;
-  if (!f.bounded) return true;
+__device__ bool quadrant_reach(const float* r, float qx, float qy) {
+  using R = ReachRow;
+  const bool in_box = (r[R::BOX + 1] >= qx) & (r[R::BOX + 0] <= qx + 7.f) &
+                      (r[R::BOX + 3] >= qy) & (r[R::BOX + 2] <= qy + 7.f);
+  if (!in_box) return false;
+  if (r[R::BOUNDED] == 0.f) return true;
   constexpr float kGrow = 0.5f, kSlack = 1e-3f;
+  const float thr = r[R::THR];
   const float x0 = qx - kGrow, x1 = qx + 7.f + kGrow;
   const float y0 = qy - kGrow, y1 = qy + 7.f + kGrow;
-  const float dx = fminf(fmaxf(g[9], x0), x1) - g[9];
-  const float dy = fminf(fmaxf(g[10], y0), y1) - g[10];
+  const float dx = fminf(fmaxf(r[R::X], x0), x1) - r[R::X];
+  const float dy = fminf(fmaxf(r[R::Y], y0), y1) - r[R::Y];
   if (2.f * (dx * dx + dy * dy) <= thr * (1.f + kSlack)) return true;
-  const bool out_x = (f.cx < x0) | (f.cx > x1);
-  const bool out_y = (f.cy < y0) | (f.cy > y1);
+  const float cx = r[R::CX], cy = r[R::CY];
+  const bool out_x = (cx < x0) | (cx > x1);
+  const bool out_y = (cy < y0) | (cy > y1);
   if (!out_x && !out_y) return true;
-  const float* t0 = g;
-  const float* t1 = g + 3;
-  const float* t2 = g + 6;
-  const float a[3] = {t1[1] * t2[2] - t1[2] * t2[1], t1[2] * t2[0] - t1[0] * t2[2],
-                      t1[0] * t2[1] - t1[1] * t2[0]};
-  const float b[3] = {t2[1] * t0[2] - t2[2] * t0[1], t2[2] * t0[0] - t2[0] * t0[2],
-                      t2[0] * t0[1] - t2[1] * t0[0]};
-  const float c[3] = {t0[1] * t1[2] - t0[2] * t1[1], t0[2] * t1[0] - t0[0] * t1[2],
-                      t0[0] * t1[1] - t0[1] * t1[0]};
-  const float qaa = a[0] * a[0] + a[1] * a[1] - thr * a[2] * a[2];
-  const float qbb = b[0] * b[0] + b[1] * b[1] - thr * b[2] * b[2];
-  if (!(qaa > 0.f && qbb > 0.f)) return true;
+  const float* a = r + R::A;
+  const float* b = r + R::B;
+  const float* c = r + R::C;
   bool hit = false;
   if (out_x) {  // edge x = ex, vertex of Q(ex, y) clamped to [y0, y1]
-    const float ex = f.cx < x0 ? x0 : x1;
+    const float ex = cx < x0 ? x0 : x1;
     const float u[3] = {ex * a[0] + c[0], ex * a[1] + c[1], ex * a[2] + c[2]};
     const float ub = u[0] * b[0] + u[1] * b[1] - thr * u[2] * b[2];
-    const float y = fminf(fmaxf(-ub / qbb, y0), y1);
+    const float y = fminf(fmaxf(-ub * rcp(r[R::QBB]), y0), y1);
     const float p[3] = {u[0] + y * b[0], u[1] + y * b[1], u[2] + y * b[2]};
     const float plane = p[0] * p[0] + p[1] * p[1], axial = thr * p[2] * p[2];
     hit = plane - axial <= kSlack * (plane + axial);
   }
   if (out_y) {  // edge y = ey, vertex of Q(x, ey) clamped to [x0, x1]
-    const float ey = f.cy < y0 ? y0 : y1;
+    const float ey = cy < y0 ? y0 : y1;
     const float u[3] = {ey * b[0] + c[0], ey * b[1] + c[1], ey * b[2] + c[2]};
     const float ua = u[0] * a[0] + u[1] * a[1] - thr * u[2] * a[2];
-    const float x = fminf(fmaxf(-ua / qaa, x0), x1);
+    const float x = fminf(fmaxf(-ua * rcp(r[R::QAA]), x0), x1);
     const float p[3] = {u[0] + x * a[0], u[1] + x * a[1], u[2] + x * a[2]};
     const float plane = p[0] * p[0] + p[1] * p[1], axial = thr * p[2] * p[2];
     hit = hit | (plane - axial <= kSlack * (plane + axial));
@@ -339,8 +371,9 @@ __device__ __forceinline__ void shade(const float* r, const float* s, Shade& a) 
 // gathers raw fields into LDS, and one thread per record derives the row's
 // constants.
 template <bool Neural>
-__device__ __forceinline__ uint64_t load_batch(float* rows, float* raw, int* ids,
-                                               int64_t* prims, float tile_x, float tile_y,
+__device__ __forceinline__ uint64_t load_batch(float* rows, float* raw, float* reach_rows,
+                                               int* ids, int64_t* prims, float tile_x,
+                                               float tile_y,
                                                int count, int id, int64_t prim,
                                                const float* geometry, const float* appearance,
                                                const float* opacities) {
@@ -379,18 +412,15 @@ __device__ __forceinline__ uint64_t load_batch(float* rows, float* raw, int* ids
     }
   }
   __syncthreads();
-  // Every wave tests the batch's records (one per lane) against its own 8x8
-  // quadrant of the tile; bit j of the ballot says that record j may touch
-  // the quadrant. Wave 0 then also derives the row constants.
+  // Wave 1 derives each record's footprint constants while wave 0 derives
+  // the row constants; after the barrier every wave tests the records (one
+  // per lane) against its own 8x8 quadrant of the tile.
   const int wave = t >> 6;
   const int j = t & 63;
-  bool reach = false;
-  if (j < count) {
+  if (wave == 1 && j < count) {
     const float* g = raw + j * L::RAW_STRIDE;
-    reach = quadrant_reachable(g, reject_threshold(g[kGeometry]), tile_x + float(wave & 1) * 8.f,
-                               tile_y + float(wave >> 1) * 8.f);
+    record_reach(g, reject_threshold(g[kGeometry]), reach_rows + j * kReachPitch);
   }
-  const uint64_t mask = __ballot(reach);
   if (t < count) {
     const float* g = raw + t * L::RAW_STRIDE;
     const float opacity = g[kGeometry];
@@ -439,7 +469,11 @@ __device__ __forceinline__ uint64_t load_batch(float* rows, float* raw, int* ids
     }
   }
   __syncthreads();
-  return mask;
+  // Bit j of the ballot says that record j may touch this wave's quadrant.
+  const bool reach = j < count && quadrant_reach(reach_rows + j * kReachPitch,
+                                                 tile_x + float(wave & 1) * 8.f,
+                                                 tile_y + float(wave >> 1) * 8.f);
+  return __ballot(reach);
 }
 
 struct TilePixel {
@@ -550,7 +584,7 @@ __global__ __launch_bounds__(kTilePixels) void tile_last_kernel(int width, int h
 }
 
 template <bool Neural>
-__global__ __launch_bounds__(kTilePixels) void render_forward_kernel(
+__global__ __launch_bounds__(kTilePixels, Neural ? 3 : 5) void render_forward_kernel(
     int width, int height, int tw, int th, const float* __restrict__ geometry,
     const float* __restrict__ appearance, const float* __restrict__ opacities,
     const int64_t* __restrict__ primitive_ids, const float* __restrict__ backgrounds,
@@ -560,6 +594,7 @@ __global__ __launch_bounds__(kTilePixels) void render_forward_kernel(
   using L = Layout<Neural>;
   __shared__ __align__(16) float rows[kBatch * L::STRIDE];
   __shared__ __align__(16) float raw[kBatch * L::RAW_STRIDE];
+  __shared__ float reach_rows[kBatch * kReachPitch];
   __shared__ int ids[kBatch];
   __shared__ int64_t prims[kBatch];
   const int tile = order[blockIdx.x];
@@ -593,8 +628,9 @@ __global__ __launch_bounds__(kTilePixels) void render_forward_kernel(
     const int64_t prim = next_prim;
     const bool ahead = int(threadIdx.x) < min(kBatch, range.y - start - kBatch);
     if (ahead) next_id = point_list[start + kBatch + threadIdx.x];
-    const uint64_t reach = load_batch<Neural>(rows, raw, ids, prims, tile_x, tile_y, count, id,
-                                              prim, geometry, appearance, opacities);
+    const uint64_t reach = load_batch<Neural>(rows, raw, reach_rows, ids, prims, tile_x, tile_y,
+                                              count, id, prim, geometry, appearance,
+                                              opacities);
     if (ahead) next_prim = primitive_ids[next_id];
     // Only the records whose footprint meets this wave's quadrant, in list
     // order. The loop runs in lockstep across the wave: finished lanes are
@@ -712,7 +748,7 @@ __device__ __forceinline__ void shade_backward(const float* r, const float* s, c
 }
 
 template <bool Neural>
-__global__ __launch_bounds__(kTilePixels) void render_backward_kernel(
+__global__ __launch_bounds__(kTilePixels, Neural ? 2 : 4) void render_backward_kernel(
     int width, int height, int tw, int th, const float* __restrict__ geometry,
     const float* __restrict__ appearance, const float* __restrict__ opacities,
     const int64_t* __restrict__ primitive_ids, const float* __restrict__ backgrounds,
@@ -728,6 +764,7 @@ __global__ __launch_bounds__(kTilePixels) void render_backward_kernel(
   constexpr int OP = Neural ? NeuralRow::OP : ClassicRow::OP;
   __shared__ __align__(16) float rows[kBatch * L::STRIDE];
   __shared__ __align__(16) float raw[kBatch * L::RAW_STRIDE];
+  __shared__ float reach_rows[kBatch * kReachPitch];
   __shared__ float acc[kBatch * NP];
   __shared__ int ids[kBatch];
   __shared__ int64_t prims[kBatch];
@@ -791,8 +828,9 @@ __global__ __launch_bounds__(kTilePixels) void render_backward_kernel(
     const int64_t prim = next_prim;
     const bool ahead = int(threadIdx.x) < min(kBatch, start - kBatch);
     if (ahead) next_id = point_list[range.x + start - kBatch - 1 - threadIdx.x];
-    const uint64_t reach = load_batch<Neural>(rows, raw, ids, prims, tile_x, tile_y, count, id,
-                                              prim, geometry, appearance, opacities);
+    const uint64_t reach = load_batch<Neural>(rows, raw, reach_rows, ids, prims, tile_x, tile_y,
+                                              count, id, prim, geometry, appearance,
+                                              opacities);
     if (ahead) next_prim = primitive_ids[next_id];
     uint64_t todo = wave_uniform(reach);
     // Row j holds list position start - j (counted from 1).
