@@ -4,8 +4,9 @@
 // Each pass sorts on an 8-bit digit (Merrill & Grimshaw's reduce-then-scan
 // formulation, without decoupled look-back, so no workgroup ever waits on
 // another):
-//   1. upsweep  - every 4096-key span builds a digit histogram in LDS and
-//                 stores it digit-major: counts[digit * spans + span];
+//   1. upsweep  - every 4096-key span (2048 for short sorts) builds a digit
+//                 histogram in LDS and stores it digit-major:
+//                 counts[digit * spans + span];
 //   2. scan     - one exclusive scan over those counts yields, for every
 //                 (digit, span), the first output slot;
 //   3. downsweep- every span ranks its keys stably (wave-level digit match
@@ -24,9 +25,12 @@ namespace {
 
 constexpr int kSortBlock = 256;
 constexpr int kSortWaves = kSortBlock / 64;
-constexpr int kSortItems = 16;                         // keys per thread
-constexpr int kSortSpan = kSortBlock * kSortItems;     // keys per workgroup
-constexpr int kWaveSpan = 64 * kSortItems;             // keys per wave
+// Keys per thread: 16 (4096-key spans), or 8 for sorts of up to
+// kShortSort keys, which then spread over twice as many workgroups - a
+// 1M-key sort otherwise leaves a 256-CU device with one span per CU.
+constexpr int64_t kShortSort = int64_t(1) << 22;
+__host__ __device__ constexpr int span_keys(int items) { return kSortBlock * items; }
+int sort_items(int64_t m) { return m <= kShortSort ? 8 : 16; }
 constexpr int kDigitBits = 8;
 constexpr int kBins = 1 << kDigitBits;
 
@@ -45,10 +49,13 @@ __device__ __forceinline__ uint64_t digit_peers(uint32_t digit, bool valid, int 
 // Digit histogram of one span, stored digit-major: counts[digit * spans +
 // span]. Each wave counts into its own LDS row; per key group the lowest
 // lane adds the group's size, so skewed digits cost no atomic conflicts.
-template <typename Key>
+template <typename Key, int Items>
 __global__ __launch_bounds__(kSortBlock) void radix_upsweep_kernel(
     const Key* __restrict__ keys, int64_t m, int shift, int bits,
     uint32_t* __restrict__ counts, int64_t spans) {
+  constexpr int kSortItems = Items;
+  constexpr int kSortSpan = span_keys(Items);
+  constexpr int kWaveSpan = 64 * Items;
   __shared__ uint32_t hist[kSortWaves][kBins];
   const int lane = __lane_id(), wave = threadIdx.x >> 6;
   for (int i = threadIdx.x; i < kSortWaves * kBins; i += kSortBlock) (&hist[0][0])[i] = 0;
@@ -97,11 +104,14 @@ struct ExclusiveStore {
   }
 };
 
-template <typename Key>
+template <typename Key, int Items>
 __global__ __launch_bounds__(kSortBlock) void radix_downsweep_kernel(
     const Key* __restrict__ keys_in, const int* __restrict__ values_in,
     Key* __restrict__ keys_out, int* __restrict__ values_out, int64_t m, int shift, int bits,
     const uint32_t* __restrict__ offsets, int64_t spans) {
+  constexpr int kSortItems = Items;
+  constexpr int kSortSpan = span_keys(Items);
+  constexpr int kWaveSpan = 64 * Items;
   __shared__ uint32_t running[kSortWaves][kBins];   // per-wave digit counters
   __shared__ uint32_t local_start[kBins];           // first local slot per digit
   __shared__ uint32_t global_start[kBins];          // first output slot per digit
@@ -220,7 +230,7 @@ struct SortWorkspace {
 };
 
 SortWorkspace layout(void* base, int64_t m, int key_bytes) {
-  const int64_t spans = ceil_div(m, kSortSpan);
+  const int64_t spans = ceil_div(m, span_keys(sort_items(m)));
   const int64_t count_items = int64_t(kBins) * spans;
   SortWorkspace w;
   size_t offset = 0;
@@ -249,7 +259,8 @@ int radix_sort(const Key* keys_in, Key* keys_out, const int* values_in, int* val
                int64_t m, int begin_bit, int end_bit, void* workspace, hipStream_t s) {
   if (m == 0) return GS_OK;
   SortWorkspace w = layout(workspace, m, int(sizeof(Key)));
-  const int64_t spans = ceil_div(m, kSortSpan);
+  const int items = sort_items(m);
+  const int64_t spans = ceil_div(m, span_keys(items));
   const int passes = int(ceil_div(end_bit - begin_bit, kDigitBits));
   // Spread the bits evenly over the passes (13 bits: 7 + 6, not 8 + 5):
   // fewer digits per pass means longer runs of equal digits per span and
@@ -270,14 +281,24 @@ int radix_sort(const Key* keys_in, Key* keys_out, const int* values_in, int* val
     const bool to_output = ((passes - 1 - pass) % 2) == 0;
     Key* dst_k = to_output ? keys_out : static_cast<Key*>(w.keys_tmp);
     int* dst_v = to_output ? values_out : w.values_tmp;
-    radix_upsweep_kernel<Key><<<unsigned(spans), kSortBlock, 0, s>>>(src_k, m, shift, bits,
-                                                                      w.counts, spans);
+    if (items == 8) {
+      radix_upsweep_kernel<Key, 8><<<unsigned(spans), kSortBlock, 0, s>>>(src_k, m, shift, bits,
+                                                                         w.counts, spans);
+    } else {
+      radix_upsweep_kernel<Key, 16><<<unsigned(spans), kSortBlock, 0, s>>>(src_k, m, shift,
+                                                                          bits, w.counts, spans);
+    }
     GS_LAUNCHED("radix_upsweep_kernel");
     int status = run_scan<uint32_t>(int64_t(kBins) * spans, CountLoad{w.counts},
                                     ExclusiveStore{w.counts}, w.scan_sums, s);
     if (status != GS_OK) return status;
-    radix_downsweep_kernel<Key><<<unsigned(spans), kSortBlock, 0, s>>>(
-        src_k, src_v, dst_k, dst_v, m, shift, bits, w.counts, spans);
+    if (items == 8) {
+      radix_downsweep_kernel<Key, 8><<<unsigned(spans), kSortBlock, 0, s>>>(
+          src_k, src_v, dst_k, dst_v, m, shift, bits, w.counts, spans);
+    } else {
+      radix_downsweep_kernel<Key, 16><<<unsigned(spans), kSortBlock, 0, s>>>(
+          src_k, src_v, dst_k, dst_v, m, shift, bits, w.counts, spans);
+    }
     GS_LAUNCHED("radix_downsweep_kernel");
     src_k = dst_k;
     src_v = dst_v;
