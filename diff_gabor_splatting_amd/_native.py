@@ -90,6 +90,11 @@ _SIGNATURES = {
         [_c_ptr] * 3 + [_c_i64, _c_i64, _c_i64, _c_int, _c_int, _c_ptr, _c_ptr, _c_ptr, _c_size,
                         _c_ptr],
     ),
+    "gs_bin_tiles_bounded": (
+        _c_int,
+        [_c_ptr] * 3 + [_c_i64, _c_i64, _c_ptr, _c_i64, _c_int, _c_int] + [_c_ptr] * 4
+        + [_c_size, _c_ptr],
+    ),
     "gs_render_workspace_size": (_c_size, [_c_i64, _c_int, _c_int]),
     "gs_render_forward": (
         _c_int,
@@ -336,14 +341,49 @@ def bin_tiles(order, starts, rects, images, width, height, intersections):
     return point_list, ranges
 
 
-def bin_depth_first(geometry, radii, image_ids, images, width, height, overlap=None):
+def bin_tiles_bounded(order, starts, rects, images, width, height, capacity, intersections):
+    """Depth-first binning, stage 2, without reading M on the host: a point
+    list of `capacity` entries and the live count `intersections` (int64 [1]
+    on the device). Returns (point_list, ranges, overflow) with overflow an
+    int32 [1] device flag, 1 when M exceeded the capacity."""
+    device = order.device
+    count = order.size(0)
+    tw, th = tile_grid(width, height)
+    point_list = torch.empty(capacity, dtype=torch.int32, device=device)
+    ranges = torch.empty((images * tw * th, 2), dtype=torch.int32, device=device)
+    overflow = torch.empty(1, dtype=torch.int32, device=device)
+    workspace = _workspace(lib.gs_bin_tiles_workspace_size(capacity), device)
+    _check(
+        lib.gs_bin_tiles_bounded(
+            _ptr(order), _ptr(starts), _ptr(rects), count, capacity, _ptr(intersections),
+            images, width, height, _ptr(point_list), _ptr(ranges), _ptr(overflow),
+            _ptr(workspace), workspace.numel(), _stream(device),
+        )
+    )
+    return point_list, ranges, overflow
+
+
+def bin_depth_first(geometry, radii, image_ids, images, width, height, overlap=None,
+                    capacity=None, flags=None):
     """Both binning stages with the one host synchronisation for M between
     them (rasterize.cu:466-469): (point_list, ranges).
 
     M is copied to pinned host memory behind stage 1 and the host waits on
     an event recorded after that copy, not on the stream, so GPU work that
-    ``overlap()`` queues (independent of M) runs while the host waits."""
+    ``overlap()`` queues (independent of M) runs while the host waits.
+    With ``capacity`` there is no synchronisation at all: the point list
+    has that many entries, and (overflow flag, live count M) of
+    bin_tiles_bounded are appended to ``flags``."""
     order, starts, rects, total = bin_order(geometry, radii, image_ids, width, height)
+    if capacity is not None:
+        if overlap is not None:
+            overlap()
+        point_list, ranges, overflow = bin_tiles_bounded(
+            order, starts, rects, images, width, height, capacity, total
+        )
+        if flags is not None:
+            flags.append((overflow, total))
+        return point_list, ranges
     stream = torch.cuda.current_stream(geometry.device)
     host = torch.empty(1, dtype=torch.int64, pin_memory=True)
     host.copy_(total, non_blocking=True)
@@ -391,6 +431,14 @@ def check_values(tensors, quaternions, scales, opacities, view_matrices, intrins
 
     Bit k < 16: tensors[k] is not finite; the GS_CHECK_* bits above that
     name the value contracts. One launch and one read-back of the word."""
+    word = check_values_word(tensors, quaternions, scales, opacities, view_matrices,
+                             intrinsics, weights, magnitudes)
+    return int(word.item()) & 0xFFFFFFFF
+
+
+def check_values_word(tensors, quaternions, scales, opacities, view_matrices, intrinsics,
+                      weights=None, magnitudes=None) -> torch.Tensor:
+    """check_values without the read-back: the int32 [1] device word."""
     _require(len(tensors) <= CHECK_MAX_TENSORS, "too many tensors to check")
     surfels = quaternions.numel() // 4
     images = view_matrices.numel() // 16
@@ -412,7 +460,7 @@ def check_values(tensors, quaternions, scales, opacities, view_matrices, intrins
     sizes = (_c_i64 * max(count, 1))(*[t.numel() for t in tensors])
     device = quaternions.device
     with torch.cuda.device(device):
-        violations = torch.zeros(1, dtype=torch.int32, device=device)
+        violations = torch.empty(1, dtype=torch.int32, device=device)
         _check(
             lib.gs_check_values(
                 pointers, sizes, count, _ptr(quaternions), _ptr(scales), _ptr(opacities),
@@ -420,7 +468,7 @@ def check_values(tensors, quaternions, scales, opacities, view_matrices, intrins
                 images, _ptr(violations), _stream(device),
             )
         )
-        return int(violations.item()) & 0xFFFFFFFF
+    return violations
 
 
 # --------------------------------------------------------------------------
@@ -604,7 +652,8 @@ def _map_group_args(groups, what: str):
 
 def rasterize_forward(
     geometry, appearance, opacities, primitive_ids, image_ids, radii, backgrounds,
-    width, height, neural, near_plane, far_plane, outputs=None, overlap=None,
+    width, height, neural, near_plane, far_plane, outputs=None, overlap=None, capacity=None,
+    flags=None,
 ):
     """Bin, sort and composite: returns [maps, point_list, ranges, state, contributors].
 
@@ -617,7 +666,9 @@ def rasterize_forward(
     MAP_GROUPS, that receive the map channel groups instead of one maps
     tensor; the first returned item is then that tuple. ``overlap`` (an
     addition): called once while the host waits for M, to queue GPU work
-    that does not depend on it.
+    that does not depend on it. ``capacity`` / ``flags`` (additions): bin
+    into a point list of fixed capacity without reading M on the host (see
+    bin_depth_first).
     """
     _check_buffers(geometry, appearance, opacities, primitive_ids, backgrounds, neural)
     _require(
@@ -651,7 +702,7 @@ def rasterize_forward(
         state = torch.empty((images, height, width, 3), dtype=torch.float32, device=device)
         contributors = torch.empty((images, height, width), dtype=torch.int32, device=device)
         point_list, ranges = bin_depth_first(geometry, radii, image_ids, images, width, height,
-                                             overlap)
+                                             overlap, capacity, flags)
         if outputs is None:
             maps = torch.empty((images, height, width, MAP_SIZE), dtype=torch.float32,
                                device=device)

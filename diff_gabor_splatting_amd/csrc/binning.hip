@@ -114,6 +114,10 @@ __global__ __launch_bounds__(256) void emit_tiles_kernel(
     }
 }
 
+__global__ __launch_bounds__(64) void clear_flag_kernel(uint32_t* flag) {
+  if (threadIdx.x == 0) *flag = 0u;
+}
+
 __global__ __launch_bounds__(256) void fill_ranges_kernel(int64_t tiles, int2* __restrict__ ranges) {
   const int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x;
   if (i < tiles) ranges[i] = make_int2(0, 0);
@@ -199,20 +203,25 @@ struct ExclusiveStartStore {
 // past m (inconsistent inputs) are dropped.
 constexpr int kLaneTiles = 32;
 
+// `m` is the capacity of tile_ids/values; `total` (a device int64, or null
+// when it equals m) the emission's full length, which may exceed it: entries
+// past the capacity are dropped and `overflow` (if given) is set.
 __global__ __launch_bounds__(256) void emit_sorted_kernel(
-    int64_t count, int64_t m, int tw, const int* __restrict__ order,
-    const int64_t* __restrict__ starts, const int4* __restrict__ rects,
-    uint32_t* __restrict__ tile_ids, int* __restrict__ values) {
+    int64_t count, int64_t m, const int64_t* __restrict__ total_count, uint32_t* overflow,
+    int tw, const int* __restrict__ order, const int64_t* __restrict__ starts,
+    const int4* __restrict__ rects, uint32_t* __restrict__ tile_ids, int* __restrict__ values) {
   const int lane = __lane_id();
   const int64_t j = int64_t(blockIdx.x) * 256 + threadIdx.x;
   if (j - lane >= count) return;  // uniform per wave
+  const int64_t total = total_count ? *total_count : m;
+  if (overflow && j == 0 && total > m) *overflow = 1u;
   int pair = 0, area = 0;
   int4 rect = make_int4(0, 0, 1, 0);
   int64_t first = 0;
   if (j < count) {
     pair = order[j];
     first = starts[j];
-    const int64_t next = j + 1 < count ? starts[j + 1] : m;
+    const int64_t next = j + 1 < count ? starts[j + 1] : total;
     area = int(min<int64_t>(next - first, INT_MAX));
     if (area > 0) rect = rects[pair];
   }
@@ -252,9 +261,12 @@ __global__ __launch_bounds__(256) void emit_sorted_kernel(
   }
 }
 
-__global__ __launch_bounds__(256) void find_tile_ranges_kernel(int64_t m, int64_t tiles,
+__global__ __launch_bounds__(256) void find_tile_ranges_kernel(int64_t capacity,
+                                                               const int64_t* __restrict__ live,
+                                                               int64_t tiles,
                                                                const uint32_t* __restrict__ ids,
                                                                int2* __restrict__ ranges) {
+  const int64_t m = live ? min(capacity, max(*live, int64_t(0))) : capacity;
   const int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x;
   if (i >= m) return;
   const uint32_t tile = ids[i];
@@ -470,12 +482,17 @@ size_t gs_bin_tiles_workspace_size(int64_t m) {
   return gs::tiles_layout(nullptr, m).bytes + 256;
 }
 
-int gs_bin_tiles(const int32_t* order, const int64_t* starts, const int32_t* rects,
-                 int64_t count, int64_t m, int64_t images, int32_t width, int32_t height,
-                 int32_t* point_list, int32_t* ranges, void* workspace, size_t workspace_bytes,
-                 void* stream) {
-  using namespace gs;
-  clear_error();
+}  // extern "C"
+
+namespace gs {
+namespace {
+
+// Shared by gs_bin_tiles (m known on the host) and gs_bin_tiles_bounded (m
+// a capacity, the live length in `live` on the device).
+int bin_tiles(const int32_t* order, const int64_t* starts, const int32_t* rects, int64_t count,
+              int64_t m, const int64_t* live, uint32_t* overflow, int64_t images, int32_t width,
+              int32_t height, int32_t* point_list, int32_t* ranges, void* workspace,
+              size_t workspace_bytes, hipStream_t s) {
   GS_REQUIRE(count >= 0 && count <= INT_MAX, GS_ERR_OVERFLOW, "too many projected primitives");
   GS_REQUIRE(m >= 0 && m <= INT_MAX, GS_ERR_OVERFLOW, "tile intersection count exceeds int32");
   GS_REQUIRE(width > 0 && height > 0 && images >= 0, GS_ERR_ARGUMENT,
@@ -483,36 +500,75 @@ int gs_bin_tiles(const int32_t* order, const int64_t* starts, const int32_t* rec
   const int tw = tiles_x(width), th = tiles_y(height);
   const int64_t tiles = images * int64_t(tw) * int64_t(th);
   GS_REQUIRE(tiles <= INT_MAX, GS_ERR_OVERFLOW, "image tile count exceeds int32");
+  if (overflow) {
+    clear_flag_kernel<<<1, 64, 0, s>>>(overflow);
+    GS_LAUNCHED("clear_flag_kernel");
+  }
   if (tiles == 0) return GS_OK;
   GS_REQUIRE(ranges, GS_ERR_ARGUMENT, "null ranges");
   const size_t need = gs_bin_tiles_workspace_size(m);
   GS_REQUIRE(workspace && workspace_bytes >= need, GS_ERR_WORKSPACE,
              "binning needs %zu workspace bytes, got %zu", need, workspace_bytes);
-  hipStream_t s = static_cast<hipStream_t>(stream);
   int2* r = reinterpret_cast<int2*>(ranges);
   TilesWorkspace w = tiles_layout(workspace, m);
   {
     ProfileScope prof(GS_PROF_BINNING, s);
     fill_ranges_kernel<<<unsigned(ceil_div(tiles, 256)), 256, 0, s>>>(tiles, r);
     GS_LAUNCHED("fill_ranges_kernel");
-    if (m == 0 || count == 0) return GS_OK;
-    GS_REQUIRE(order && starts && rects && point_list, GS_ERR_ARGUMENT,
-               "null pointer passed to gs_bin_tiles");
+    if (count == 0 || (m == 0 && !live)) return GS_OK;
+    GS_REQUIRE(order && starts && rects, GS_ERR_ARGUMENT, "null pointer passed to gs_bin_tiles");
+    if (m == 0) {  // a zero capacity still reports an overflowing emission
+      emit_sorted_kernel<<<unsigned(ceil_div(count, 256)), 256, 0, s>>>(
+          count, 0, live, overflow, tw, order, starts, reinterpret_cast<const int4*>(rects),
+          nullptr, nullptr);
+      GS_LAUNCHED("emit_sorted_kernel");
+      return GS_OK;
+    }
+    GS_REQUIRE(point_list, GS_ERR_ARGUMENT, "null point list");
     emit_sorted_kernel<<<unsigned(ceil_div(count, 256)), 256, 0, s>>>(
-        count, m, tw, order, starts, reinterpret_cast<const int4*>(rects), w.tile_ids,
-        w.tile_values);
+        count, m, live, overflow, tw, order, starts, reinterpret_cast<const int4*>(rects),
+        w.tile_ids, w.tile_values);
     GS_LAUNCHED("emit_sorted_kernel");
   }
   {
     ProfileScope prof(GS_PROF_SORT, s);
     int status = radix_sort<uint32_t>(w.tile_ids, w.tile_sorted, w.tile_values, point_list, m,
-                                      0, id_bits(tiles), w.sort, s);
+                                      0, id_bits(tiles), w.sort, s, live);
     if (status != GS_OK) return status;
   }
   ProfileScope prof(GS_PROF_BINNING, s);
-  find_tile_ranges_kernel<<<unsigned(ceil_div(m, 256)), 256, 0, s>>>(m, tiles, w.tile_sorted, r);
+  find_tile_ranges_kernel<<<unsigned(ceil_div(m, 256)), 256, 0, s>>>(m, live, tiles,
+                                                                     w.tile_sorted, r);
   GS_LAUNCHED("find_tile_ranges_kernel");
   return GS_OK;
+}
+
+}  // namespace
+}  // namespace gs
+
+extern "C" {
+
+int gs_bin_tiles(const int32_t* order, const int64_t* starts, const int32_t* rects,
+                 int64_t count, int64_t m, int64_t images, int32_t width, int32_t height,
+                 int32_t* point_list, int32_t* ranges, void* workspace, size_t workspace_bytes,
+                 void* stream) {
+  gs::clear_error();
+  return gs::bin_tiles(order, starts, rects, count, m, nullptr, nullptr, images, width, height,
+                       point_list, ranges, workspace, workspace_bytes,
+                       static_cast<hipStream_t>(stream));
+}
+
+int gs_bin_tiles_bounded(const int32_t* order, const int64_t* starts, const int32_t* rects,
+                         int64_t count, int64_t capacity, const int64_t* intersections,
+                         int64_t images, int32_t width, int32_t height, int32_t* point_list,
+                         int32_t* ranges, uint32_t* overflow, void* workspace,
+                         size_t workspace_bytes, void* stream) {
+  gs::clear_error();
+  GS_REQUIRE(intersections && overflow, GS_ERR_ARGUMENT,
+             "bounded binning needs the device intersection count and an overflow flag");
+  return gs::bin_tiles(order, starts, rects, count, capacity, intersections, overflow, images,
+                       width, height, point_list, ranges, workspace, workspace_bytes,
+                       static_cast<hipStream_t>(stream));
 }
 
 }  // extern "C"

@@ -49,10 +49,17 @@ __device__ __forceinline__ uint64_t digit_peers(uint32_t digit, bool valid, int 
 // Digit histogram of one span, stored digit-major: counts[digit * spans +
 // span]. Each wave counts into its own LDS row; per key group the lowest
 // lane adds the group's size, so skewed digits cost no atomic conflicts.
+// Sorts whose length is known only on the device pass it as `live` (the
+// grid then covers the capacity m and spans past the live length are empty).
+__device__ __forceinline__ int64_t live_length(int64_t m, const int64_t* live) {
+  return live ? min(m, max(*live, int64_t(0))) : m;
+}
+
 template <typename Key, int Items>
 __global__ __launch_bounds__(kSortBlock) void radix_upsweep_kernel(
-    const Key* __restrict__ keys, int64_t m, int shift, int bits,
-    uint32_t* __restrict__ counts, int64_t spans) {
+    const Key* __restrict__ keys, int64_t capacity, const int64_t* __restrict__ live, int shift,
+    int bits, uint32_t* __restrict__ counts, int64_t spans) {
+  const int64_t m = live_length(capacity, live);
   constexpr int kSortItems = Items;
   constexpr int kSortSpan = span_keys(Items);
   constexpr int kWaveSpan = 64 * Items;
@@ -107,8 +114,10 @@ struct ExclusiveStore {
 template <typename Key, int Items>
 __global__ __launch_bounds__(kSortBlock) void radix_downsweep_kernel(
     const Key* __restrict__ keys_in, const int* __restrict__ values_in,
-    Key* __restrict__ keys_out, int* __restrict__ values_out, int64_t m, int shift, int bits,
-    const uint32_t* __restrict__ offsets, int64_t spans) {
+    Key* __restrict__ keys_out, int* __restrict__ values_out, int64_t capacity,
+    const int64_t* __restrict__ live, int shift, int bits, const uint32_t* __restrict__ offsets,
+    int64_t spans) {
+  const int64_t m = live_length(capacity, live);
   constexpr int kSortItems = Items;
   constexpr int kSortSpan = span_keys(Items);
   constexpr int kWaveSpan = 64 * Items;
@@ -213,7 +222,10 @@ template <typename Key>
 __global__ __launch_bounds__(256) void copy_pairs_kernel(const Key* __restrict__ keys_in,
                                                          const int* __restrict__ values_in,
                                                          Key* __restrict__ keys_out,
-                                                         int* __restrict__ values_out, int64_t m) {
+                                                         int* __restrict__ values_out,
+                                                         int64_t capacity,
+                                                         const int64_t* __restrict__ live) {
+  const int64_t m = live_length(capacity, live);
   const int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x;
   if (i < m) {
     keys_out[i] = keys_in[i];
@@ -256,7 +268,8 @@ size_t radix_sort_workspace_bytes(int64_t m, int key_bytes) {
 
 template <typename Key>
 int radix_sort(const Key* keys_in, Key* keys_out, const int* values_in, int* values_out,
-               int64_t m, int begin_bit, int end_bit, void* workspace, hipStream_t s) {
+               int64_t m, int begin_bit, int end_bit, void* workspace, hipStream_t s,
+               const int64_t* live) {
   if (m == 0) return GS_OK;
   SortWorkspace w = layout(workspace, m, int(sizeof(Key)));
   const int items = sort_items(m);
@@ -267,8 +280,8 @@ int radix_sort(const Key* keys_in, Key* keys_out, const int* values_in, int* val
   // fewer ballots per key.
   const int digit_bits = passes ? int(ceil_div(end_bit - begin_bit, passes)) : 0;
   if (passes == 0) {
-    copy_pairs_kernel<Key><<<unsigned(ceil_div(m, 256)), 256, 0, s>>>(keys_in, values_in,
-                                                                       keys_out, values_out, m);
+    copy_pairs_kernel<Key><<<unsigned(ceil_div(m, 256)), 256, 0, s>>>(
+        keys_in, values_in, keys_out, values_out, m, live);
     GS_LAUNCHED("copy_pairs_kernel");
     return GS_OK;
   }
@@ -282,11 +295,11 @@ int radix_sort(const Key* keys_in, Key* keys_out, const int* values_in, int* val
     Key* dst_k = to_output ? keys_out : static_cast<Key*>(w.keys_tmp);
     int* dst_v = to_output ? values_out : w.values_tmp;
     if (items == 8) {
-      radix_upsweep_kernel<Key, 8><<<unsigned(spans), kSortBlock, 0, s>>>(src_k, m, shift, bits,
-                                                                         w.counts, spans);
+      radix_upsweep_kernel<Key, 8><<<unsigned(spans), kSortBlock, 0, s>>>(
+          src_k, m, live, shift, bits, w.counts, spans);
     } else {
-      radix_upsweep_kernel<Key, 16><<<unsigned(spans), kSortBlock, 0, s>>>(src_k, m, shift,
-                                                                          bits, w.counts, spans);
+      radix_upsweep_kernel<Key, 16><<<unsigned(spans), kSortBlock, 0, s>>>(
+          src_k, m, live, shift, bits, w.counts, spans);
     }
     GS_LAUNCHED("radix_upsweep_kernel");
     int status = run_scan<uint32_t>(int64_t(kBins) * spans, CountLoad{w.counts},
@@ -294,10 +307,10 @@ int radix_sort(const Key* keys_in, Key* keys_out, const int* values_in, int* val
     if (status != GS_OK) return status;
     if (items == 8) {
       radix_downsweep_kernel<Key, 8><<<unsigned(spans), kSortBlock, 0, s>>>(
-          src_k, src_v, dst_k, dst_v, m, shift, bits, w.counts, spans);
+          src_k, src_v, dst_k, dst_v, m, live, shift, bits, w.counts, spans);
     } else {
       radix_downsweep_kernel<Key, 16><<<unsigned(spans), kSortBlock, 0, s>>>(
-          src_k, src_v, dst_k, dst_v, m, shift, bits, w.counts, spans);
+          src_k, src_v, dst_k, dst_v, m, live, shift, bits, w.counts, spans);
     }
     GS_LAUNCHED("radix_downsweep_kernel");
     src_k = dst_k;
@@ -307,9 +320,9 @@ int radix_sort(const Key* keys_in, Key* keys_out, const int* values_in, int* val
 }
 
 template int radix_sort<uint32_t>(const uint32_t*, uint32_t*, const int*, int*, int64_t, int,
-                                  int, void*, hipStream_t);
+                                  int, void*, hipStream_t, const int64_t*);
 template int radix_sort<uint64_t>(const uint64_t*, uint64_t*, const int*, int*, int64_t, int,
-                                  int, void*, hipStream_t);
+                                  int, void*, hipStream_t, const int64_t*);
 
 }  // namespace gs
 

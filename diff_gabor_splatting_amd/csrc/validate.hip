@@ -1,11 +1,12 @@
-// Value contracts of the renderer's inputs in one launch.
+// Value contracts of the renderer's inputs in one pass over them.
 //
 // The reference evaluates every contract of check_values
 // (src/gabor_splatting/rendering.py:88-153) as its own chain of PyTorch ops
 // (isfinite/all per tensor, isclose, a batched matmul, an LU determinant) and
 // reads the stacked verdicts back once. Here one kernel reads each input
 // once, evaluates every contract on the elements it owns and ORs the
-// violated contracts into one 32-bit word; the caller reads that word back.
+// violated contracts into one 32-bit word (cleared by a one-thread kernel
+// first); the caller reads that word back when it chooses.
 //
 // The launch is a flat list of blocks split into jobs: job 0 checks the
 // per-surfel contracts, job 1 the per-image (camera) contracts and jobs
@@ -150,6 +151,12 @@ __global__ __launch_bounds__(kCheckThreads) void check_values_kernel(CheckJobs j
   }
 }
 
+// A kernel rather than a memset, so that the checks can run inside a
+// captured HIP graph.
+__global__ __launch_bounds__(64) void clear_violations_kernel(uint32_t* violations) {
+  if (threadIdx.x == 0) *violations = 0u;
+}
+
 }  // namespace
 }  // namespace gs
 
@@ -199,9 +206,11 @@ int gs_check_values(const float* const* tensors, const int64_t* sizes, int32_t t
   jobs.views = view_matrices;
   jobs.intrinsics = intrinsics;
   jobs.images = images;
-  if (blocks == 0) return GS_OK;
   hipStream_t s = static_cast<hipStream_t>(stream);
   ProfileScope prof(GS_PROF_VALIDATE, s);
+  clear_violations_kernel<<<1, 64, 0, s>>>(violations);
+  GS_LAUNCHED("clear_violations_kernel");
+  if (blocks == 0) return GS_OK;
   check_values_kernel<<<unsigned(blocks), kCheckThreads, 0, s>>>(jobs, violations);
   GS_LAUNCHED("check_values_kernel");
   return GS_OK;

@@ -39,7 +39,7 @@ class Composite(torch.autograd.Function):
     @staticmethod
     def forward(
         ctx: Any, geometry, projected_means, appearance, opacities, primitive_ids, image_ids,
-        radii, backgrounds, width, height, neural, near_plane, far_plane,
+        radii, backgrounds, width, height, neural, near_plane, far_plane, bounded=None,
     ):
         images = backgrounds.size(0)
         outputs = tuple(
@@ -58,6 +58,8 @@ class Composite(torch.autograd.Function):
         _, points, ranges, state, contributors = _native.rasterize_forward(
             geometry, appearance, opacities, primitive_ids, image_ids, radii, backgrounds,
             width, height, neural, near_plane, far_plane, outputs=outputs, overlap=overlap,
+            capacity=None if bounded is None else bounded.max_intersections,
+            flags=None if bounded is None else bounded._overflows,
         )
         # Binning and early termination are discrete: only the saved sorted
         # lists and per-pixel state are needed to replay the tiles backwards.
@@ -77,7 +79,7 @@ class Composite(torch.autograd.Function):
         gg, ga, go, gb = _native.rasterize_backward(
             *ctx.saved_tensors, list(grad_groups), *ctx.options, accumulators=accumulators
         )
-        return gg, gg[:, 9:11], ga, go, None, None, None, gb, None, None, None, None, None
+        return gg, gg[:, 9:11], ga, go, None, None, None, gb, None, None, None, None, None, None
 
 
 class ProjectRecords(torch.autograd.Function):
@@ -249,6 +251,77 @@ def check_values(
         raise ValueError("; ".join(messages))
 
 
+class FixedCapacity:
+    """Rendering without host synchronisation, for HIP graph capture.
+
+    The reference reads the tile-intersection count on the host to size its
+    point list (rasterize.cu:466-469) and reads the value checks' verdict
+    back (rendering.py:149); neither can happen inside a captured graph, and
+    both stall the host. While this context is active (``with
+    fixed_capacity(max_intersections) as capacity:``), renders:
+
+    * bin into a point list of ``max_intersections`` entries, the count
+      staying on the device; if it exceeds the capacity the deepest records
+      of the affected tiles are dropped and a device flag is raised;
+    * run the value checks (``validate=True``) on the device and keep the
+      verdict instead of raising;
+    * refuse ``packed=True``, whose outputs have a data-dependent length.
+
+    ``check()``, called outside any capture, reads every recorded verdict
+    and flag in one synchronisation and raises ValueError (violated value
+    contracts, as ``check_values`` would) or RuntimeError (capacity
+    exceeded); it then forgets them and returns the largest intersection
+    count it saw (0 if none), a guide for sizing the capacity.
+    """
+
+    def __init__(self, max_intersections: int):
+        if type(max_intersections) is not int or not 0 < max_intersections <= _native.INT_MAX:
+            raise ValueError("max_intersections must be a positive int32 integer")
+        self.max_intersections = max_intersections
+        self._overflows: list[tuple[torch.Tensor, torch.Tensor]] = []
+        self._values: list[tuple[torch.Tensor, list[str]]] = []
+
+    def __enter__(self) -> "FixedCapacity":
+        _FIXED_CAPACITY.append(self)
+        return self
+
+    def __exit__(self, *exc) -> None:
+        _FIXED_CAPACITY.remove(self)
+
+    def check(self) -> int:
+        words = [word for word, _ in self._values]
+        for overflow, total in self._overflows:
+            words += [overflow, total]
+        if not words:
+            return 0
+        host = torch.cat([w.reshape(1).to(torch.int64) for w in words]).tolist()
+        values, rest = host[: len(self._values)], host[len(self._values):]
+        overflows, totals = rest[0::2], rest[1::2]
+        names = [n for _, n in self._values]
+        self._values, self._overflows = [], []
+        messages = []
+        for word, tensor_names in zip(values, names):
+            for message in describe_violations(tensor_names, word & 0xFFFFFFFF):
+                if message not in messages:
+                    messages.append(message)
+        if messages:
+            raise ValueError("; ".join(messages))
+        if any(overflows):
+            raise RuntimeError(
+                f"tile intersections ({max(totals)}) exceeded the fixed capacity of "
+                f"{self.max_intersections}; the affected renders dropped their deepest records"
+            )
+        return max(totals, default=0)
+
+
+_FIXED_CAPACITY: list[FixedCapacity] = []
+
+
+def fixed_capacity(max_intersections: int) -> FixedCapacity:
+    """Context manager: render without host synchronisation (see FixedCapacity)."""
+    return FixedCapacity(max_intersections)
+
+
 def quaternion_matrix(q: torch.Tensor) -> torch.Tensor:
     """Normalised wxyz quaternions to rotation matrices (rendering.py:156-173)."""
     q = q / torch.linalg.vector_norm(q, dim=-1, keepdim=True)
@@ -341,10 +414,24 @@ def render(
         check_tensor(name, value, shape, device)
     if type(validate) is not bool:
         raise TypeError("validate must be bool")
-    if validate:
+    bounded = _FIXED_CAPACITY[-1] if _FIXED_CAPACITY else None
+    if bounded is not None and packed:
+        raise ValueError(
+            "packed=True is unavailable at a fixed intersection capacity: its outputs have a "
+            "data-dependent length"
+        )
+    if validate and bounded is None:
         check_values(
             tensors, quaternions, scales, opacities, view_matrices, intrinsics, appearance, neural
         )
+    elif validate:
+        weights, magnitudes = (None, None) if neural else (appearance[2], appearance[3])
+        with torch.no_grad():
+            word = _native.check_values_word(
+                [value for value, _ in tensors.values()], quaternions, scales, opacities,
+                view_matrices, intrinsics, weights, magnitudes,
+            )
+        bounded._values.append((word, list(tensors)))
 
     views = view_matrices.reshape(scenes, cameras, 4, 4)
     cameras_k = intrinsics.reshape(scenes, cameras, 3, 3)
@@ -392,6 +479,7 @@ def render(
         neural,
         near_plane,
         far_plane,
+        bounded,
     )
     image_shape = batch + (cameras, height, width)
     meta = {

@@ -174,11 +174,12 @@ int gs_sh_backward(const float* first, const float* second, const float* directi
 #define GS_CHECK_MAGNITUDES_NONNEGATIVE (1u << 25) /* frequency_magnitudes >= 0 */
 #define GS_CHECK_WEIGHTS_SUM (1u << 26)            /* frequency weights sum to 1 */
 
-/* ORs the violated contracts into *violations (a device uint32 the caller
- * zeroes first) in one launch that reads every value once: finiteness of
- * tensors[0..tensor_count) (sizes[k] floats each); per surfel (quaternions
- * [surfels,4], scales [surfels,2], opacities [surfels], and, when not null,
- * frequency_weights / frequency_magnitudes [surfels,4]); per image
+/* Writes the violated contracts to *violations (a device uint32, cleared
+ * by a one-thread launch first) in one launch that reads every value once:
+ * finiteness of tensors[0..tensor_count) (sizes[k] floats each); per
+ * surfel (quaternions [surfels,4], scales [surfels,2], opacities [surfels],
+ * and, when not null, frequency_weights / frequency_magnitudes
+ * [surfels,4]); per image
  * (view_matrices [images,4,4], intrinsics [images,3,3]). Closeness is
  * torch.isclose's |x - t| <= atol + |rtol t| in float32: rtol 1e-5 / atol
  * 1e-8 for the last rows, 1e-4 / 1e-4 for the other closeness contracts. */
@@ -268,6 +269,22 @@ int gs_bin_tiles(const int32_t* order, const int64_t* starts, const int32_t* rec
                  int64_t count, int64_t m, int64_t images, int32_t width, int32_t height,
                  int32_t* point_list, int32_t* ranges, void* workspace, size_t workspace_bytes,
                  void* stream);
+
+/* gs_bin_tiles without the host's intersection count, for callers that
+ * cannot synchronise (HIP graph capture): the point list and workspace are
+ * sized for `capacity` entries (point_list [capacity], workspace
+ * gs_bin_tiles_workspace_size(capacity)); the live count is read from
+ * *intersections, the device word gs_bin_order wrote. The first
+ * min(count, capacity) entries of the depth-first emission are binned and
+ * ranges cover exactly those. *overflow (a device uint32) is cleared, then
+ * set to 1 when the count exceeds the capacity: the deepest records were
+ * then dropped from their tiles. No counterpart in the reference, which
+ * reads the count on the host (rasterize.cu:466-469). */
+int gs_bin_tiles_bounded(const int32_t* order, const int64_t* starts, const int32_t* rects,
+                         int64_t count, int64_t capacity, const int64_t* intersections,
+                         int64_t images, int32_t width, int32_t height, int32_t* point_list,
+                         int32_t* ranges, uint32_t* overflow, void* workspace,
+                         size_t workspace_bytes, void* stream);
 
 /* ------------------------------------------------------------------ */
 /* Kernels 4 and 5: tile compositors (renderForward / renderBackward,

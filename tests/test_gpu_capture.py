@@ -1,0 +1,128 @@
+"""Rendering without host synchronisation, and inside a captured HIP graph.
+
+Within ``fixed_capacity`` the point list has a fixed capacity and the
+intersection count stays on the device (gs_bin_tiles_bounded), value checks
+are deferred to ``check()``, and a whole forward + backward can be captured
+in a graph. Each graph replay is compared with an eager render of the same
+inputs, with eager work and synchronisations between the replays.
+"""
+
+import math
+
+import pytest
+import torch
+
+from scenes import maps_from_result, random_scene
+
+pytestmark = [
+    pytest.mark.gpu,
+    pytest.mark.skipif(not torch.cuda.is_available(), reason="needs a GPU"),
+]
+DEVICE = torch.device("cuda:0")
+
+
+def renderer(method):
+    from diff_gabor_splatting_amd import rasterize_gabors, rasterize_neural_gabors
+
+    return rasterize_gabors if method == "classic" else rasterize_neural_gabors
+
+
+def scene(method, seed, n=300, width=70, height=45):
+    raw = random_scene(method, scenes=1, cameras=2, n=n, width=width, height=height, seed=seed)
+    return {k: v.to(DEVICE) for k, v in raw.items()}, dict(width=width, height=height)
+
+
+def maps_and_grads(method, values, options, weights, **kwargs):
+    leaves = {k: v.detach().clone().requires_grad_() for k, v in values.items()}
+    maps = maps_from_result(renderer(method)(**leaves, **options, **kwargs))
+    grads = torch.autograd.grad(maps, list(leaves.values()), grad_outputs=weights)
+    return maps.detach(), grads
+
+
+@pytest.mark.parametrize("method", ["classic", "neural"])
+def test_bounded_render_matches_synchronised_render(method):
+    from diff_gabor_splatting_amd import fixed_capacity
+
+    values, options = scene(method, seed=3)
+    plain = maps_from_result(renderer(method)(**values, **options))
+    weights = torch.linspace(-1, 1, plain.numel(), device=DEVICE).reshape(plain.shape)
+    expected, expected_grads = maps_and_grads(method, values, options, weights)
+    with fixed_capacity(1 << 20) as capacity:
+        actual, grads = maps_and_grads(method, values, options, weights)
+    peak = capacity.check()
+    assert 0 < peak < 1 << 20
+    with fixed_capacity(peak) as exact:  # a capacity of exactly M suffices
+        tight, _ = maps_and_grads(method, values, options, weights)
+    assert exact.check() == peak
+    assert torch.equal(tight, expected)
+    assert torch.equal(actual, expected)
+    for a, e in zip(grads, expected_grads):
+        torch.testing.assert_close(a, e, atol=1e-6, rtol=1e-5)
+
+
+def test_overflow_is_reported_by_check():
+    from diff_gabor_splatting_amd import fixed_capacity
+
+    values, options = scene("classic", seed=5)
+    with fixed_capacity(7) as capacity:
+        renderer("classic")(**values, **options)
+    with pytest.raises(RuntimeError, match=r"tile intersections \(\d+\) exceeded the fixed capacity of 7"):
+        capacity.check()
+    assert capacity.check() == 0  # the flags were consumed
+
+
+def test_value_checks_are_deferred():
+    from diff_gabor_splatting_amd import fixed_capacity
+
+    values, options = scene("classic", seed=6)
+    values["scales"][0, 3, 1] = -1.0
+    values["means"][0, 7, 0] = math.nan
+    with fixed_capacity(1 << 20) as capacity:
+        renderer("classic")(**values, **options)  # does not raise here
+        with pytest.raises(ValueError, match="packed=True is unavailable"):
+            renderer("classic")(**values, **options, packed=True)
+    with pytest.raises(ValueError) as error:
+        capacity.check()
+    assert str(error.value) == ("means must contain only finite values; "
+                                "scales must be strictly positive")
+
+
+@pytest.mark.parametrize("method", ["classic", "neural"])
+def test_graph_replays_match_eager(method):
+    from diff_gabor_splatting_amd import fixed_capacity
+
+    base, options = scene(method, seed=11)
+    static = {k: v.detach().clone().requires_grad_() for k, v in base.items()}
+    probe = maps_from_result(renderer(method)(**base, **options))
+    weights = torch.linspace(-1, 1, probe.numel(), device=DEVICE).reshape(probe.shape)
+
+    def step():
+        maps = maps_from_result(renderer(method)(**static, **options, validate=False))
+        grads = torch.autograd.grad(maps, list(static.values()), grad_outputs=weights)
+        return maps, grads
+
+    capacity = fixed_capacity(1 << 20)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with capacity, torch.cuda.stream(side):
+        for _ in range(2):
+            step()
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with capacity, torch.cuda.graph(graph):
+        static_maps, static_grads = step()
+    capacity.check()
+
+    for replay, seed in enumerate((11, 12, 13)):
+        values, _ = scene(method, seed=seed)
+        with torch.no_grad():
+            for name, value in values.items():
+                static[name].copy_(value)
+        print(f"graph replay {method} {replay}", flush=True)
+        graph.replay()
+        torch.cuda.synchronize()
+        expected, expected_grads = maps_and_grads(method, values, options, weights)
+        assert torch.equal(static_maps, expected), replay
+        for name, a, e in zip(values, static_grads, expected_grads):
+            torch.testing.assert_close(a, e, atol=1e-6, rtol=1e-5, msg=f"{name} replay {replay}")
+        capacity.check()

@@ -56,3 +56,19 @@ def test_overflow_guards_are_pure_host_functions():
         _native.check_image_tiles(2**20, 2**16, 2**16)
     assert _native.tile_grid(1920, 1080) == (120, 68)
     assert _native.sort_end_bit(120 * 68) == 45
+
+
+def test_fixed_capacity_arguments_and_nesting():
+    from diff_gabor_splatting_amd import fixed_capacity
+
+    for bad in (0, -5, 2**31, 3.0, True):
+        with pytest.raises(ValueError, match="max_intersections"):
+            fixed_capacity(bad)
+    outer, inner = fixed_capacity(10), fixed_capacity(20)
+    with outer:
+        assert rendering._FIXED_CAPACITY[-1] is outer
+        with inner:
+            assert rendering._FIXED_CAPACITY[-1] is inner
+        assert rendering._FIXED_CAPACITY[-1] is outer
+    assert rendering._FIXED_CAPACITY == []
+    outer.check()  # nothing recorded: no synchronisation, no error
