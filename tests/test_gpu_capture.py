@@ -32,6 +32,15 @@ def scene(method, seed, n=300, width=70, height=45):
     return {k: v.to(DEVICE) for k, v in raw.items()}, dict(width=width, height=height)
 
 
+def assert_grads_close(actual, expected, names, what):
+    """Float atomics sum the gradients in a run-dependent order, so elements
+    are compared at the scale of their tensor (1e-6 of its largest value)."""
+    for name, a, e in zip(names, actual, expected):
+        scale = float(e.abs().max()) if e.numel() else 0.0
+        torch.testing.assert_close(a, e, atol=1e-6 * max(scale, 1.0), rtol=1e-5,
+                                   msg=lambda m, name=name: f"{name} {what}: {m}")
+
+
 def maps_and_grads(method, values, options, weights, **kwargs):
     leaves = {k: v.detach().clone().requires_grad_() for k, v in values.items()}
     maps = maps_from_result(renderer(method)(**leaves, **options, **kwargs))
@@ -56,8 +65,7 @@ def test_bounded_render_matches_synchronised_render(method):
     assert exact.check() == peak
     assert torch.equal(tight, expected)
     assert torch.equal(actual, expected)
-    for a, e in zip(grads, expected_grads):
-        torch.testing.assert_close(a, e, atol=1e-6, rtol=1e-5)
+    assert_grads_close(grads, expected_grads, list(values), "bounded")
 
 
 def test_overflow_is_reported_by_check():
@@ -123,6 +131,5 @@ def test_graph_replays_match_eager(method):
         torch.cuda.synchronize()
         expected, expected_grads = maps_and_grads(method, values, options, weights)
         assert torch.equal(static_maps, expected), replay
-        for name, a, e in zip(values, static_grads, expected_grads):
-            torch.testing.assert_close(a, e, atol=1e-6, rtol=1e-5, msg=f"{name} replay {replay}")
+        assert_grads_close(static_grads, expected_grads, list(values), f"replay {replay}")
         capacity.check()

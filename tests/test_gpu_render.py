@@ -417,7 +417,9 @@ def test_retained_graph_backward_twice(method):
     first = torch.autograd.grad((maps * weights).sum(), list(values.values()), retain_graph=True)
     second = torch.autograd.grad((maps * weights).sum(), list(values.values()))
     for name, a, b in zip(values, first, second):
-        torch.testing.assert_close(a, b, atol=1e-6, rtol=1e-5, msg=name)
+        # float atomics: compare at the scale of the tensor
+        scale = max(float(b.abs().max()), 1.0)
+        torch.testing.assert_close(a, b, atol=1e-6 * scale, rtol=1e-5, msg=name)
     with torch.no_grad():
         plain = maps_from_result(renderer(method)(**values, width=19, height=13))
     torch.testing.assert_close(plain, maps.detach())
