@@ -763,9 +763,14 @@ __global__ __launch_bounds__(kTilePixels, Neural ? 2 : 4) void render_backward_k
   constexpr int NG = L::NG;
   constexpr int OP = Neural ? NeuralRow::OP : ClassicRow::OP;
   __shared__ __align__(16) float rows[kBatch * L::STRIDE];
-  __shared__ __align__(16) float raw[kBatch * L::RAW_STRIDE];
+  // The raw staging rows are dead once a batch's rows are derived, and the
+  // gradient accumulator is needed only after that: they share LDS, which
+  // keeps the neural kernel at three workgroups per CU.
+  constexpr int kRawFloats = kBatch * L::RAW_STRIDE, kAccFloats = kBatch * NP;
+  __shared__ __align__(16) float raw_acc[kRawFloats > kAccFloats ? kRawFloats : kAccFloats];
+  float* raw = raw_acc;
+  float* acc = raw_acc;
   __shared__ float reach_rows[kBatch * kReachPitch];
-  __shared__ float acc[kBatch * NP];
   __shared__ int ids[kBatch];
   __shared__ int64_t prims[kBatch];
   __shared__ float bg_acc[3];
@@ -778,7 +783,6 @@ __global__ __launch_bounds__(kTilePixels, Neural ? 2 : 4) void render_backward_k
   const float tile_y = float(tp.py - (wave >> 1) * 8 - (lane >> 3));
   const int last = tp.inside ? contributors[tp.pixel] : 0;
 
-  for (int i = threadIdx.x; i < kBatch * NP; i += kTilePixels) acc[i] = 0.f;
   if (threadIdx.x < 3) bg_acc[threadIdx.x] = 0.f;
 
   float go[kMaps];
@@ -832,6 +836,9 @@ __global__ __launch_bounds__(kTilePixels, Neural ? 2 : 4) void render_backward_k
                                               count, id, prim, geometry, appearance,
                                               opacities);
     if (ahead) next_prim = primitive_ids[next_id];
+    // The raw rows are dead: clear the accumulator that shares their LDS.
+    for (int i = threadIdx.x; i < count * NP; i += kTilePixels) acc[i] = 0.f;
+    __syncthreads();
     uint64_t todo = wave_uniform(reach);
     // Row j holds list position start - j (counted from 1).
     const int beyond = start - wave_last;  // rows j < beyond lie past wave_last
@@ -950,7 +957,6 @@ __global__ __launch_bounds__(kTilePixels, Neural ? 2 : 4) void render_backward_k
         } else {
           atomicAdd(grad_opacities + prims[j], value);
         }
-        acc[idx] = 0.f;
       }
     }
     // The next batch overwrites ids/prims/rows; every flush must finish first.
