@@ -291,7 +291,8 @@ def main(argv=None):
             "traffic": measured_traffic(dominant, cfg["name"]),
             "algorithmic_bytes_per_launch": algo,
             "avg_launch_ms": round(avg_ms, 4),
-            "note": "compositors are VALU-bound (transcendentals); see valu_estimate",
+            "note": "the compositors are bound by VALU issue, not HBM: see valu",
+            "valu": measured_valu(dominant, cfg["name"], avg_ms),
         },
         "kernels": {k: round(v["ms_per_step"], 4) for k, v in kernels.items()},
         "gpu": torch.cuda.get_device_name(device),
@@ -312,6 +313,30 @@ def copy_calibration() -> int:
     torch.cuda.synchronize()
     print(json.dumps({"copy_bytes": COPY_BYTES, "launches": 3}), flush=True)
     return 0
+
+
+# One wave64 VALU instruction issues per SIMD every 4 cycles: 256 CUs x 4
+# SIMDs at 2.4 GHz.
+VALU_ISSUE_PER_S = 256 * 4 * 2.4e9 / 4
+
+
+def measured_valu(kernel: str, workload: str, avg_ms: float):
+    """VALU issue of ``kernel`` from the committed rocprof counter summary:
+    SQ_INSTS_VALU per launch, the time issuing them takes at one wave64
+    instruction per SIMD every 4 cycles, and that time as a fraction of the
+    launch time measured in this run. None when no summary covers it."""
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
+                        f"{kernel}_valu.json")
+    try:
+        with open(path) as handle:
+            summary = json.load(handle)
+    except (OSError, ValueError):
+        return None
+    if summary.get("kernel") != kernel or summary.get("workload") != workload or not avg_ms:
+        return None
+    issue_ms = summary["valu_instructions"] / VALU_ISSUE_PER_S * 1e3
+    return {"instructions": summary["valu_instructions"], "issue_ms": round(issue_ms, 4),
+            "frac": round(issue_ms / avg_ms, 4), "source": summary.get("source")}
 
 
 def measured_traffic(kernel: str, workload: str):

@@ -911,16 +911,18 @@ __global__ __launch_bounds__(kTilePixels, Neural ? 2 : 4) void render_backward_k
       gg[10] = surface ? 0.f : 4.f * (r[10] - y) * grho;
       const float gp[3] = {gs[0] * inv_pz, gs[1] * inv_pz,
                            -(gs[0] * s_[0] + gs[1] * s_[1]) * inv_pz};
-      // p = k x l  =>  dk = l x gp, dl = gp x k.
-      const float gk[3] = {v.l[1] * gp[2] - v.l[2] * gp[1], v.l[2] * gp[0] - v.l[0] * gp[2],
-                           v.l[0] * gp[1] - v.l[1] * gp[0]};
-      const float gl[3] = {gp[1] * v.k[2] - gp[2] * v.k[1], gp[2] * v.k[0] - gp[0] * v.k[2],
-                           gp[0] * v.k[1] - gp[1] * v.k[0]};
+      // p = k x l  =>  dk = l x gp, dl = gp x k; k = x T2 - T0 and l = y T2 - T1,
+      // so the T rows receive -dk, -dl and x dk + y dl: computed directly as
+      // gp x l = -dk and k x gp = -dl.
+      const float nk[3] = {gp[1] * v.l[2] - gp[2] * v.l[1], gp[2] * v.l[0] - gp[0] * v.l[2],
+                           gp[0] * v.l[1] - gp[1] * v.l[0]};
+      const float nl[3] = {v.k[1] * gp[2] - v.k[2] * gp[1], v.k[2] * gp[0] - v.k[0] * gp[2],
+                           v.k[0] * gp[1] - v.k[1] * gp[0]};
 #pragma unroll
       for (int k = 0; k < 3; ++k) {
-        gg[k] = -gk[k];
-        gg[3 + k] = -gl[k];
-        gg[6 + k] += x * gk[k] + y * gl[k];
+        gg[k] = nk[k];
+        gg[3 + k] = nl[k];
+        gg[6 + k] -= x * nk[k] + y * nl[k];
       }
       // Wave totals, one per lane, added into the batch accumulator.
       float* dst = acc + j * NP;

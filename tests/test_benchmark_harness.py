@@ -91,3 +91,18 @@ def test_tiny_run_reports_every_implementation(tmp_path):
         assert row["images_per_second"] == pytest.approx(4000 / row["forward_backward_ms"])
     for method in ("classic", "neural"):
         assert rows[(method, "single_view_loop")]["speedup_vs_single_view_loop"] == 1.0
+
+
+def test_bench_reads_committed_counter_summaries():
+    import bench
+
+    workload = bench.CONFIGS[4]["name"]
+    traffic = bench.measured_traffic("render_backward", workload)
+    assert traffic is None or traffic > 0
+    valu = bench.measured_valu("render_backward", workload, 1.9)
+    if valu is not None:
+        assert valu["issue_ms"] == pytest.approx(valu["instructions"] / bench.VALU_ISSUE_PER_S * 1e3,
+                                                 rel=1e-3)
+        assert valu["frac"] == pytest.approx(valu["issue_ms"] / 1.9, rel=1e-3)
+    assert bench.measured_valu("render_backward", "another workload", 1.9) is None
+    assert bench.measured_traffic("render_backward", "another workload") is None
