@@ -370,7 +370,7 @@ __device__ __forceinline__ void shade(const float* r, const float* s, Shade& a) 
 // two dependent loads overlap the previous batch); every thread then
 // gathers raw fields into LDS, and one thread per record derives the row's
 // constants.
-template <bool Neural>
+template <bool Neural, bool Quarters>
 __device__ __forceinline__ uint64_t load_batch(float* rows, float* raw, float* reach_rows,
                                                int* ids, int64_t* prims, float tile_x,
                                                float tile_y,
@@ -384,31 +384,93 @@ __device__ __forceinline__ uint64_t load_batch(float* rows, float* raw, float* r
     prims[t] = prim;
   }
   __syncthreads();
-  // One loop per source array, consecutive threads on consecutive floats of
-  // a row: geometry (17 floats), opacity, appearance (pairs of floats when
-  // the row width is even and the array starts on an 8-byte boundary, as
-  // every row then does).
-  for (int idx = t; idx < count * kGeometry; idx += kTilePixels) {
-    const int j = idx / kGeometry;
-    const int f = idx - j * kGeometry;
-    raw[j * L::RAW_STRIDE + f] = geometry[int64_t(ids[j]) * kGeometry + f];
-  }
-  if (t < count) raw[t * L::RAW_STRIDE + kGeometry] = opacities[prims[t]];
-  const bool pairs = L::A % 2 == 0 && (reinterpret_cast<uintptr_t>(appearance) & 7u) == 0;
-  if (pairs) {
-    constexpr int kPairs = L::A / 2;
-    for (int idx = t; idx < count * kPairs; idx += kTilePixels) {
-      const int j = idx / kPairs;
-      const int f = idx - j * kPairs;
-      const float2 v = reinterpret_cast<const float2*>(appearance + prims[j] * L::A)[f];
-      raw[j * L::RAW_STRIDE + kGeometry + 1 + 2 * f] = v.x;
-      raw[j * L::RAW_STRIDE + kGeometry + 2 + 2 * f] = v.y;
+  if constexpr (Quarters) {
+    // Four threads per record (record t / 4, quarter t % 4), each bringing a
+    // fixed slice of the record's geometry row (17 floats), its appearance row
+    // (pairs of floats when the row width is even and the array starts on an
+    // 8-byte boundary, as every row then does) and, for the last quarter, its
+    // opacity: no divisions, one base address per array, every load issued
+    // before the first LDS write.
+    constexpr int kParts = kTilePixels / kBatch;
+    const int record = t / kParts, q = t % kParts;
+    if (record < count) {
+      float* dst = raw + record * L::RAW_STRIDE;
+      constexpr int kGeo = (kGeometry + kParts - 1) / kParts;
+      const float* g = geometry + int64_t(ids[record]) * kGeometry;
+      const int64_t prim_j = prims[record];
+      float gv[kGeo];
+  #pragma unroll
+      for (int k = 0; k < kGeo; ++k) {
+        const int f = q * kGeo + k;
+        gv[k] = f < kGeometry ? g[f] : 0.f;
+      }
+      const float opacity = q == kParts - 1 ? opacities[prim_j] : 0.f;
+      const float* a = appearance + prim_j * L::A;
+      const bool pairs = L::A % 2 == 0 && (reinterpret_cast<uintptr_t>(appearance) & 7u) == 0;
+      if (pairs) {
+        constexpr int kPairs = L::A / 2, kPer = (kPairs + kParts - 1) / kParts;
+        float2 av[kPer];
+  #pragma unroll
+        for (int k = 0; k < kPer; ++k) {
+          const int f = q * kPer + k;
+          av[k] = f < kPairs ? reinterpret_cast<const float2*>(a)[f] : make_float2(0.f, 0.f);
+        }
+  #pragma unroll
+        for (int k = 0; k < kPer; ++k) {
+          const int f = q * kPer + k;
+          if (f < kPairs) {
+            dst[kGeometry + 1 + 2 * f] = av[k].x;
+            dst[kGeometry + 2 + 2 * f] = av[k].y;
+          }
+        }
+      } else {
+        constexpr int kPer = (L::A + kParts - 1) / kParts;
+        float av[kPer];
+  #pragma unroll
+        for (int k = 0; k < kPer; ++k) {
+          const int f = q * kPer + k;
+          av[k] = f < L::A ? a[f] : 0.f;
+        }
+  #pragma unroll
+        for (int k = 0; k < kPer; ++k) {
+          const int f = q * kPer + k;
+          if (f < L::A) dst[kGeometry + 1 + f] = av[k];
+        }
+      }
+  #pragma unroll
+      for (int k = 0; k < kGeo; ++k) {
+        const int f = q * kGeo + k;
+        if (f < kGeometry) dst[f] = gv[k];
+      }
+      if (q == kParts - 1) dst[kGeometry] = opacity;
     }
   } else {
-    for (int idx = t; idx < count * L::A; idx += kTilePixels) {
-      const int j = idx / L::A;
-      const int f = idx - j * L::A;
-      raw[j * L::RAW_STRIDE + kGeometry + 1 + f] = appearance[prims[j] * L::A + f];
+    // One loop per source array, consecutive threads on consecutive floats of
+    // a row: geometry (17 floats), opacity, appearance (pairs of floats when
+    // the row width is even and the array starts on an 8-byte boundary, as
+    // every row then does).
+    for (int idx = t; idx < count * kGeometry; idx += kTilePixels) {
+      const int j = idx / kGeometry;
+      const int f = idx - j * kGeometry;
+      raw[j * L::RAW_STRIDE + f] = geometry[int64_t(ids[j]) * kGeometry + f];
+    }
+    if (t < count) raw[t * L::RAW_STRIDE + kGeometry] = opacities[prims[t]];
+    const bool pairs = L::A % 2 == 0 && (reinterpret_cast<uintptr_t>(appearance) & 7u) == 0;
+    if (pairs) {
+      constexpr int kPairs = L::A / 2;
+      for (int idx = t; idx < count * kPairs; idx += kTilePixels) {
+        const int j = idx / kPairs;
+        const int f = idx - j * kPairs;
+        const float2 v = reinterpret_cast<const float2*>(appearance + prims[j] * L::A)[f];
+        raw[j * L::RAW_STRIDE + kGeometry + 1 + 2 * f] = v.x;
+        raw[j * L::RAW_STRIDE + kGeometry + 2 + 2 * f] = v.y;
+      }
+    } else {
+      for (int idx = t; idx < count * L::A; idx += kTilePixels) {
+        const int j = idx / L::A;
+        const int f = idx - j * L::A;
+        raw[j * L::RAW_STRIDE + kGeometry + 1 + f] = appearance[prims[j] * L::A + f];
+      }
     }
   }
   __syncthreads();
@@ -628,9 +690,9 @@ __global__ __launch_bounds__(kTilePixels, Neural ? 3 : 5) void render_forward_ke
     const int64_t prim = next_prim;
     const bool ahead = int(threadIdx.x) < min(kBatch, range.y - start - kBatch);
     if (ahead) next_id = point_list[start + kBatch + threadIdx.x];
-    const uint64_t reach = load_batch<Neural>(rows, raw, reach_rows, ids, prims, tile_x, tile_y,
-                                              count, id, prim, geometry, appearance,
-                                              opacities);
+    const uint64_t reach =
+        load_batch<Neural, true>(rows, raw, reach_rows, ids, prims, tile_x, tile_y, count, id,
+                                  prim, geometry, appearance, opacities);
     if (ahead) next_prim = primitive_ids[next_id];
     // Only the records whose footprint meets this wave's quadrant, in list
     // order. The loop runs in lockstep across the wave: finished lanes are
@@ -832,9 +894,9 @@ __global__ __launch_bounds__(kTilePixels, Neural ? 2 : 4) void render_backward_k
     const int64_t prim = next_prim;
     const bool ahead = int(threadIdx.x) < min(kBatch, start - kBatch);
     if (ahead) next_id = point_list[range.x + start - kBatch - 1 - threadIdx.x];
-    const uint64_t reach = load_batch<Neural>(rows, raw, reach_rows, ids, prims, tile_x, tile_y,
-                                              count, id, prim, geometry, appearance,
-                                              opacities);
+    const uint64_t reach =
+        load_batch<Neural, false>(rows, raw, reach_rows, ids, prims, tile_x, tile_y, count, id,
+                                  prim, geometry, appearance, opacities);
     if (ahead) next_prim = primitive_ids[next_id];
     // The raw rows are dead: clear the accumulator that shares their LDS.
     for (int i = threadIdx.x; i < count * NP; i += kTilePixels) acc[i] = 0.f;
