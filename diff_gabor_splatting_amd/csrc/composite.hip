@@ -370,7 +370,14 @@ __device__ __forceinline__ void shade(const float* r, const float* s, Shade& a) 
 // two dependent loads overlap the previous batch); every thread then
 // gathers raw fields into LDS, and one thread per record derives the row's
 // constants.
-template <bool Neural, bool Quarters>
+// How a batch's rows are gathered: kGatherQuarters gives each record four
+// threads with fixed slices and issues all their loads before the LDS
+// writes (the forward); kGatherLoops strides the threads over the
+// concatenated rows, which holds fewer registers where the loop around it
+// already needs many (the backward).
+enum Gather { kGatherLoops, kGatherQuarters };
+
+template <bool Neural, Gather Mode>
 __device__ __forceinline__ uint64_t load_batch(float* rows, float* raw, float* reach_rows,
                                                int* ids, int64_t* prims, float tile_x,
                                                float tile_y,
@@ -384,7 +391,7 @@ __device__ __forceinline__ uint64_t load_batch(float* rows, float* raw, float* r
     prims[t] = prim;
   }
   __syncthreads();
-  if constexpr (Quarters) {
+  if constexpr (Mode == kGatherQuarters) {
     // Four threads per record (record t / 4, quarter t % 4), each bringing a
     // fixed slice of the record's geometry row (17 floats), its appearance row
     // (pairs of floats when the row width is even and the array starts on an
@@ -399,7 +406,7 @@ __device__ __forceinline__ uint64_t load_batch(float* rows, float* raw, float* r
       const float* g = geometry + int64_t(ids[record]) * kGeometry;
       const int64_t prim_j = prims[record];
       float gv[kGeo];
-  #pragma unroll
+#pragma unroll
       for (int k = 0; k < kGeo; ++k) {
         const int f = q * kGeo + k;
         gv[k] = f < kGeometry ? g[f] : 0.f;
@@ -410,12 +417,12 @@ __device__ __forceinline__ uint64_t load_batch(float* rows, float* raw, float* r
       if (pairs) {
         constexpr int kPairs = L::A / 2, kPer = (kPairs + kParts - 1) / kParts;
         float2 av[kPer];
-  #pragma unroll
+#pragma unroll
         for (int k = 0; k < kPer; ++k) {
           const int f = q * kPer + k;
           av[k] = f < kPairs ? reinterpret_cast<const float2*>(a)[f] : make_float2(0.f, 0.f);
         }
-  #pragma unroll
+#pragma unroll
         for (int k = 0; k < kPer; ++k) {
           const int f = q * kPer + k;
           if (f < kPairs) {
@@ -426,18 +433,18 @@ __device__ __forceinline__ uint64_t load_batch(float* rows, float* raw, float* r
       } else {
         constexpr int kPer = (L::A + kParts - 1) / kParts;
         float av[kPer];
-  #pragma unroll
+#pragma unroll
         for (int k = 0; k < kPer; ++k) {
           const int f = q * kPer + k;
           av[k] = f < L::A ? a[f] : 0.f;
         }
-  #pragma unroll
+#pragma unroll
         for (int k = 0; k < kPer; ++k) {
           const int f = q * kPer + k;
           if (f < L::A) dst[kGeometry + 1 + f] = av[k];
         }
       }
-  #pragma unroll
+#pragma unroll
       for (int k = 0; k < kGeo; ++k) {
         const int f = q * kGeo + k;
         if (f < kGeometry) dst[f] = gv[k];
@@ -690,9 +697,9 @@ __global__ __launch_bounds__(kTilePixels, Neural ? 3 : 5) void render_forward_ke
     const int64_t prim = next_prim;
     const bool ahead = int(threadIdx.x) < min(kBatch, range.y - start - kBatch);
     if (ahead) next_id = point_list[start + kBatch + threadIdx.x];
-    const uint64_t reach =
-        load_batch<Neural, true>(rows, raw, reach_rows, ids, prims, tile_x, tile_y, count, id,
-                                  prim, geometry, appearance, opacities);
+    const uint64_t reach = load_batch<Neural, kGatherQuarters>(
+        rows, raw, reach_rows, ids, prims, tile_x, tile_y, count, id, prim, geometry, appearance,
+        opacities);
     if (ahead) next_prim = primitive_ids[next_id];
     // Only the records whose footprint meets this wave's quadrant, in list
     // order. The loop runs in lockstep across the wave: finished lanes are
@@ -894,9 +901,9 @@ __global__ __launch_bounds__(kTilePixels, Neural ? 2 : 4) void render_backward_k
     const int64_t prim = next_prim;
     const bool ahead = int(threadIdx.x) < min(kBatch, start - kBatch);
     if (ahead) next_id = point_list[range.x + start - kBatch - 1 - threadIdx.x];
-    const uint64_t reach =
-        load_batch<Neural, false>(rows, raw, reach_rows, ids, prims, tile_x, tile_y, count, id,
-                                  prim, geometry, appearance, opacities);
+    const uint64_t reach = load_batch<Neural, kGatherLoops>(
+        rows, raw, reach_rows, ids, prims, tile_x, tile_y, count, id, prim, geometry, appearance,
+        opacities);
     if (ahead) next_prim = primitive_ids[next_id];
     // The raw rows are dead: clear the accumulator that shares their LDS.
     for (int i = threadIdx.x; i < count * NP; i += kTilePixels) acc[i] = 0.f;
