@@ -133,3 +133,19 @@ def test_graph_replays_match_eager(method):
         assert torch.equal(static_maps, expected), replay
         assert_grads_close(static_grads, expected_grads, list(values), f"replay {replay}")
         capacity.check()
+
+
+@pytest.mark.parametrize("method", ["classic", "neural"])
+def test_bounded_render_of_an_empty_view(method):
+    """No surfel in front of the camera: zero intersections on the device."""
+    from diff_gabor_splatting_amd import fixed_capacity
+
+    values, options = scene(method, seed=8, n=20)
+    values["means"][..., 2] = -3.0  # behind every camera
+    expected = maps_from_result(renderer(method)(**values, **options))
+    with fixed_capacity(64) as capacity:
+        actual = maps_from_result(renderer(method)(**values, **options))
+    assert capacity.check() == 0
+    assert torch.equal(actual, expected)
+    background = values["backgrounds"][:, :, None, None, :].expand_as(actual[..., :3])
+    torch.testing.assert_close(actual[..., :3], background)
