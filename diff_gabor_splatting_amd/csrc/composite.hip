@@ -65,7 +65,8 @@ struct ClassicRow {
   static constexpr int OP = 14, THR = 15;
   static constexpr int A = 16, B = 20, C = 24, HW = 28;  // 4 each
   static constexpr int HALF_W = 32, SUM = 33, DIFF = 36;  // 1, 3, 3
-  static constexpr int STRIDE = 40;
+  static constexpr int AP = 40, BP = 44;  // -2 pi HW_f A_f, -2 pi HW_f B_f (backward)
+  static constexpr int STRIDE = 48;
 };
 struct NeuralRow {
   static constexpr int DIR = 14, OP = 17, THR = 18;
@@ -290,7 +291,10 @@ struct Sample {
 // early returns so that the wave's control flow stays scalar: after the
 // cheap rejection test (no division, no exp) the whole wave leaves at once
 // when no lane can accept.
-template <bool Neural>
+// StandIns: lanes that do not accept leave with finite stand-ins (alpha, e,
+// inv_pz and s zero, depth one, surface false), so that an adjoint run by
+// every lane of the wave multiplies them only by zeros.
+template <bool Neural, bool StandIns = false>
 __device__ __forceinline__ bool sample_surface(const float* r, float x, float y,
                                                float near_plane, bool live, Sample& v) {
   constexpr int OP = Neural ? NeuralRow::OP : ClassicRow::OP;
@@ -318,7 +322,17 @@ __device__ __forceinline__ bool sample_surface(const float* r, float x, float y,
   v.depth = (Neural || v.surface) ? v.s[0] * r[6] + v.s[1] * r[7] + r[8] : r[8];
   v.e = __builtin_amdgcn_exp2f(fminf(rho3, rho2) * kNegHalfLog2e);
   v.alpha = fminf(0.99f, r[OP] * v.e);
-  return pass & (v.depth >= near_plane) & isfinite(v.depth) & (v.alpha >= kMinAlpha);
+  const bool ok = pass & (v.depth >= near_plane) & isfinite(v.depth) & (v.alpha >= kMinAlpha);
+  if constexpr (StandIns) {
+    v.alpha = ok ? v.alpha : 0.f;
+    v.depth = ok ? v.depth : 1.f;
+    v.e = ok ? v.e : 0.f;
+    v.inv_pz = ok ? v.inv_pz : 0.f;
+    v.s[0] = ok ? v.s[0] : 0.f;
+    v.s[1] = ok ? v.s[1] : 0.f;
+    v.surface = ok & v.surface;
+  }
+  return ok;
 }
 
 // Appearance at local coordinates s. Classic keeps the per-frequency
@@ -527,6 +541,8 @@ __device__ __forceinline__ uint64_t load_batch(float* rows, float* raw, float* r
         r[R::B + f] = a[10 + f] * kDirY[f];
         r[R::C + f] = a[14 + f] * kInvTwoPi;
         r[R::HW + f] = 0.5f * a[6 + f];
+        r[R::AP + f] = -kTwoPi * (0.5f * a[6 + f]) * r[R::A + f];
+        r[R::BP + f] = -kTwoPi * (0.5f * a[6 + f]) * r[R::B + f];
         half_w += 0.5f * a[6 + f];
       }
       r[R::HALF_W] = half_w;
@@ -789,31 +805,54 @@ __device__ __forceinline__ void shade_backward(const float* r, const float* s, c
       for (int k = 0; k < 3; ++k) gdir[k] += gz * r[R::WDIR + h * 3 + k];
     }
   } else {
+    // colour_c = h1 c1_c + h2 c2_c with h1/h2 = W/2 +/- S, S = sum_f HW_f cos_f.
+    // Factors that are constant over the record stay out of the per-pixel
+    // terms: ga receives the summands of the pixel sums listed at
+    // classic_appearance_gradient, which applies them once per record.
     using R = ClassicRow;
-    float g_sum = 0.f, g_diff = 0.f;
+    float g_diff = 0.f;
+#pragma unroll
+    for (int c = 0; c < 3; ++c) g_diff += gc[c] * r[R::DIFF + c];
 #pragma unroll
     for (int c = 0; c < 3; ++c) {
-      g_sum += gc[c] * r[R::SUM + c];
-      g_diff += gc[c] * r[R::DIFF + c];
-    }
-    const float h1 = r[R::HALF_W] + a.S, h2 = r[R::HALF_W] - a.S;
-#pragma unroll
-    for (int c = 0; c < 3; ++c) {
-      ga[c] = gc[c] * h1;
-      ga[3 + c] = gc[c] * h2;
+      ga[c] = gc[c];
+      ga[3 + c] = gc[c] * a.S;
     }
 #pragma unroll
     for (int f = 0; f < 4; ++f) {
-      // colour_c = h1 c1_c + h2 c2_c with h1/h2 = sum_f w_f (1 +/- cos_f) / 2.
-      ga[6 + f] = 0.5f * (g_sum + a.c[f] * g_diff);
-      const float gt = -r[R::HW + f] * a.sn[f] * g_diff;  // d/d(phase_f)
-      const float dot = kDirX[f] * s[0] + kDirY[f] * s[1];
-      ga[10 + f] = gt * kTwoPi * dot;
-      ga[14 + f] = gt;
-      gs[0] += gt * kTwoPi * r[R::A + f];
-      gs[1] += gt * kTwoPi * r[R::B + f];
+      ga[6 + f] = a.c[f] * g_diff;
+      // d/d(phase_f) = -HW_f sin_f g_diff, phase in radians; the magnitude
+      // and local-coordinate derivatives carry 2 pi (revolutions) times dt/d.
+      const float gq = a.sn[f] * g_diff;
+      ga[10 + f] = gq * (kDirX[f] * s[0] + kDirY[f] * s[1]);
+      ga[14 + f] = gq;
+      gs[0] += gq * r[R::AP + f];
+      gs[1] += gq * r[R::BP + f];
     }
   }
+}
+
+// Gradient of classic appearance column k of one record from the pixel
+// sums that the classic adjoint accumulates (shade_backward):
+//   k 0-2   sum gc_c                -> colour_c   = W/2 sum gc_c + sum gc_c S
+//   k 3-5   sum gc_c S              -> colour2_c  = W/2 sum gc_c - sum gc_c S
+//   k 6-9   sum cos_f g_diff        -> weight_f   = (sum_c SUM_c sum gc_c + sum) / 2
+//   k 10-13 sum sin_f g_diff dot_f  -> magnitude_f = -2 pi HW_f sum
+//   k 14-17 sum sin_f g_diff        -> phase_f    = -HW_f sum
+// (W/2 = sum_f HW_f, SUM_c = c1_c + c2_c, dot_f = the wave direction . s).
+__device__ __forceinline__ float classic_appearance_gradient(const float* sums, const float* r,
+                                                             int k) {
+  using R = ClassicRow;
+  if (k < 6) {
+    const int c = k < 3 ? k : k - 3;
+    return k < 3 ? r[R::HALF_W] * sums[c] + sums[3 + c] : r[R::HALF_W] * sums[c] - sums[3 + c];
+  }
+  if (k < 10) {
+    const float g_sum = r[R::SUM] * sums[0] + r[R::SUM + 1] * sums[1] + r[R::SUM + 2] * sums[2];
+    return 0.5f * (g_sum + sums[k]);
+  }
+  if (k < 14) return -kTwoPi * r[R::HW + k - 10] * sums[k];
+  return -r[R::HW + k - 14] * sums[k];
 }
 
 template <bool Neural>
@@ -919,23 +958,23 @@ __global__ __launch_bounds__(kTilePixels, Neural ? 2 : 4) void render_backward_k
       const float* r = rows + j * L::STRIDE;
       Sample v;
       const bool active =
-          sample_surface<Neural>(r, x, y, near_plane, tp.inside && (start - j) <= last, v);
+          sample_surface<Neural, true>(r, x, y, near_plane, tp.inside && (start - j) <= last, v);
       if (!__any(active)) continue;
       // Every lane runs the adjoint. A lane that does not take the sample
       // contributes exact zeros: its map gradients are masked to zero and
-      // the sample's own values are replaced by finite stand-ins, so every
-      // term below is a product with a zero and never 0 * inf. Taking lanes
-      // compute exactly what a branch would; the masking replaces
-      // zero-filling all NP values ahead of a divergent branch.
+      // the sample's own values are finite stand-ins, so every term below
+      // is a product with a zero and never 0 * inf. Taking lanes compute
+      // exactly what a branch would; the masking replaces zero-filling all
+      // NP values ahead of a divergent branch.
       float gom[kMaps];
 #pragma unroll
       for (int c = 0; c < kMaps; ++c) gom[c] = active ? go[c] : 0.f;
-      const float alpha = active ? v.alpha : 0.f;
-      const float depth = active ? v.depth : 1.f;
-      const float e = active ? v.e : 0.f;
-      const float inv_pz = active ? v.inv_pz : 0.f;
-      const float s_[2] = {active ? v.s[0] : 0.f, active ? v.s[1] : 0.f};
-      const bool surface = active & v.surface;
+      const float alpha = v.alpha;
+      const float depth = v.depth;
+      const float e = v.e;
+      const float inv_pz = v.inv_pz;
+      const float s_[2] = {v.s[0], v.s[1]};
+      const bool surface = v.surface;
       float grad[NP];  // geometry NG | appearance A | opacity
       float* gg = grad;
       float* ga = grad + NG;
@@ -1017,10 +1056,14 @@ __global__ __launch_bounds__(kTilePixels, Neural ? 2 : 4) void render_backward_k
     __syncthreads();
     // Flush this batch: one global atomic per nonzero (record, parameter).
     for (int idx = threadIdx.x; idx < count * NP; idx += kTilePixels) {
-      const float value = acc[idx];
+      const int j = idx / NP;
+      const int p = idx - j * NP;
+      float value = acc[idx];
+      if constexpr (!Neural) {
+        if (p >= NG && p < NG + L::A)
+          value = classic_appearance_gradient(acc + j * NP + NG, rows + j * L::STRIDE, p - NG);
+      }
       if (value != 0.f) {
-        const int j = idx / NP;
-        const int p = idx - j * NP;
         if (p < NG) {
           atomicAdd(grad_geometry + int64_t(ids[j]) * kGeometry + p, value);
         } else if (p < NG + L::A) {

@@ -46,6 +46,27 @@ __device__ __forceinline__ float exchange_add(float lo, float hi, int lane) {
     auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(lo), __float_as_uint(hi), false,
                                               false);
     return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  } else if constexpr (B == 3 || B == 2) {
+    // Mirror pairs never leave a bank pair: bit 3 splits every 16-lane row
+    // into banks {0,1} | {2,3}, bit 2 into banks {0,2} | {1,3}. Two DPP adds,
+    // each writing only the banks that keep its half, replace the per-lane
+    // selects. The s_nop gives the two wait states a DPP source read needs
+    // after a VALU write.
+    float r;
+    if constexpr (B == 3) {
+      asm("s_nop 1\n\t"
+          "v_add_f32_dpp %0, %2, %2 row_mirror row_mask:0xf bank_mask:0xc\n\t"
+          "v_add_f32_dpp %0, %1, %1 row_mirror row_mask:0xf bank_mask:0x3"
+          : "=&v"(r)
+          : "v"(lo), "v"(hi));
+    } else {
+      asm("s_nop 1\n\t"
+          "v_add_f32_dpp %0, %2, %2 row_half_mirror row_mask:0xf bank_mask:0xa\n\t"
+          "v_add_f32_dpp %0, %1, %1 row_half_mirror row_mask:0xf bank_mask:0x5"
+          : "=&v"(r)
+          : "v"(lo), "v"(hi));
+    }
+    return r;
   } else {
     const bool upper = (lane >> B) & 1;
     const float send = upper ? lo : hi;
