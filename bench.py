@@ -139,14 +139,30 @@ def crop(values, x0: int, y0: int):
 
 
 def _loss(rgb, alpha, meta, channels):
-    maps = torch.cat(
-        (rgb, alpha, meta["accumulated_depth"], meta["normals"], meta["distortion"]), -1
-    )
-    # A slice, even of every channel, would add a zero-fill and a copy to the
-    # backward; take it only when some channels are left out.
-    if channels != maps.shape[-1]:
-        maps = maps[..., :channels]
-    return maps.square().mean()
+    """Mean of squares of the first `channels` map channels in the reference
+    benchmark's order - rgb, alpha, depth, normals, distortion - its objective
+    ``torch.cat(maps, -1).square().mean()`` (benchmarks/
+    benchmark_rasterization.py:80-82, 133).
+
+    Same value and gradient, less glue: the maps are flattened to
+    [pixels, k] before the concatenation (above four dimensions torch's cat
+    falls back to one strided copy per input, while 2-D inputs take its
+    single batched-copy kernel), groups past `channels` are left out rather
+    than sliced off (a slice adds a zero-filled full-size gradient), and the
+    mean of squares is mse_loss against zero, whose backward is one fused
+    kernel (2 x / n) where square().mean() runs pow, mul, mul and div over the
+    whole map.
+    """
+    flat, left = [], channels
+    for t in (rgb, alpha, meta["accumulated_depth"], meta["normals"], meta["distortion"]):
+        if left <= 0:
+            break
+        k = t.shape[-1]
+        t = t.reshape(-1, k)
+        flat.append(t if k <= left else t[:, :left])
+        left -= k
+    maps = torch.cat(flat, -1) if len(flat) > 1 else flat[0]
+    return torch.nn.functional.mse_loss(maps, maps.new_zeros(()).expand_as(maps))
 
 
 def algorithmic_bytes(kind: str, neural: bool, pixels: int, records: int, pairs: int,

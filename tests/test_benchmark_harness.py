@@ -106,3 +106,26 @@ def test_bench_reads_committed_counter_summaries():
         assert valu["frac"] == pytest.approx(valu["issue_ms"] / 1.9, rel=1e-3)
     assert bench.measured_valu("render_backward", "another workload", 1.9) is None
     assert bench.measured_traffic("render_backward", "another workload") is None
+
+
+@pytest.mark.parametrize("channels", [9, 5])
+def test_bench_loss_is_the_reference_objective(channels):
+    import bench
+
+    g = torch.Generator().manual_seed(3)
+    shape = (1, 2, 5, 7)
+    groups = [torch.randn(shape + (k,), generator=g, dtype=torch.float64, requires_grad=True)
+              for k in (3, 1, 1, 3, 1)]
+    rgb, alpha, depth, normals, distortion = groups
+    meta = {"accumulated_depth": depth, "normals": normals, "distortion": distortion}
+    loss = bench._loss(rgb, alpha, meta, channels)
+    got = torch.autograd.grad(loss, groups, allow_unused=True)
+    # The reference benchmark's form: concatenate, keep the channels, mean of squares.
+    expected = torch.cat(groups, -1)[..., :channels].square().mean()
+    want = torch.autograd.grad(expected, groups)
+    assert loss.item() == pytest.approx(expected.item(), rel=1e-12)
+    for g_got, g_want in zip(got, want):
+        if g_got is None:  # groups past `channels` get no gradient (zero in the reference form)
+            assert not g_want.any()
+        else:
+            torch.testing.assert_close(g_got, g_want, rtol=1e-12, atol=0)
