@@ -34,6 +34,7 @@
 //    totals with one global atomic per (tile, record, parameter).
 #include <climits>
 #include <cmath>
+#include <type_traits>
 
 #include "common.hpp"
 #include "wave.hpp"
@@ -909,6 +910,12 @@ __global__ __launch_bounds__(kTilePixels, Neural ? 2 : 4) void render_backward_k
   for (int c = 0; c < 3; ++c) background_dot += go[c] * backgrounds[tp.image * 3 + c];
   // dL/dalpha_i picks up final_t (go_alpha - background . go_rgb) / (1 - alpha_i).
   const float final_term = final_t * (go[3] - background_dot);
+  // Whether every map gradient and saved state value of the wave's pixels is
+  // finite (selects the adjoint without per-lane masking).
+  bool finite = isfinite(final_term) && isfinite(m1) && isfinite(m2);
+#pragma unroll
+  for (int c = 0; c < kMaps; ++c) finite = finite && isfinite(go[c]);
+  const bool finite_pixels = __all(finite);
   __syncthreads();
   // Background gradient: sum over the tile of final T * dL/drgb.
   {
@@ -961,97 +968,113 @@ __global__ __launch_bounds__(kTilePixels, Neural ? 2 : 4) void render_backward_k
           sample_surface<Neural, true>(r, x, y, near_plane, tp.inside && (start - j) <= last, v);
       if (!__any(active)) continue;
       // Every lane runs the adjoint. A lane that does not take the sample
-      // contributes exact zeros: its map gradients are masked to zero and
-      // the sample's own values are finite stand-ins, so every term below
-      // is a product with a zero and never 0 * inf. Taking lanes compute
-      // exactly what a branch would; the masking replaces zero-filling all
-      // NP values ahead of a divergent branch.
-      float gom[kMaps];
+      // contributes exact zeros: the sample's values are finite stand-ins
+      // (alpha, e, s and 1/p_z zero, depth one), so its weight w and every
+      // term carrying e or 1/p_z vanish, and with finite map gradients and
+      // pixel state every term below is a product with a zero. A wave with
+      // a non-finite one (0 * inf) takes the Masked copy, which also zeroes
+      // the lane's map gradients and dL/dalpha. Taking lanes compute exactly
+      // what a branch would; the stand-ins replace zero-filling all NP
+      // values ahead of a divergent branch.
+      auto adjoint = [&](auto masked) {
+        constexpr bool kMasked = decltype(masked)::value;
+        float gom[kMaps];
 #pragma unroll
-      for (int c = 0; c < kMaps; ++c) gom[c] = active ? go[c] : 0.f;
-      const float alpha = v.alpha;
-      const float depth = v.depth;
-      const float e = v.e;
-      const float inv_pz = v.inv_pz;
-      const float s_[2] = {v.s[0], v.s[1]};
-      const bool surface = v.surface;
-      float grad[NP];  // geometry NG | appearance A | opacity
-      float* gg = grad;
-      float* ga = grad + NG;
-      const float inv_keep = rcp(1.f - alpha);
-      T = active ? T * inv_keep : T;
-      const float w = T * alpha;
-      Shade a;
-      shade<Neural, true>(r, s_, a);
-      const float inv_depth = rcp(depth);
-      const float m = mscale - mnear * inv_depth;
-      float gw = gom[4] * depth + gom[8] * (m * m * total_a + m2 - 2.f * m * m1);
-      float gc[3];
+        for (int c = 0; c < kMaps; ++c) gom[c] = kMasked ? (active ? go[c] : 0.f) : go[c];
+        const float alpha = v.alpha;
+        const float depth = v.depth;
+        const float e = v.e;
+        const float inv_pz = v.inv_pz;
+        const float s_[2] = {v.s[0], v.s[1]};
+        const bool surface = v.surface;
+        float grad[NP];  // geometry NG | appearance A | opacity
+        float* gg = grad;
+        float* ga = grad + NG;
+        const float inv_keep = rcp(1.f - alpha);
+        T *= inv_keep;  // alpha = 0, inv_keep = 1 where the lane does not take the sample
+        const float w = T * alpha;
+        Shade a;
+        shade<Neural, true>(r, s_, a);
+        const float inv_depth = rcp(depth);
+        const float m = mscale - mnear * inv_depth;
+        float gw = gom[4] * depth + gom[8] * (m * m * total_a + m2 - 2.f * m * m1);
+        float gc[3];
 #pragma unroll
-      for (int c = 0; c < 3; ++c) {
-        gw += gom[c] * a.color[c] + gom[5 + c] * r[11 + c];
-        gc[c] = w * gom[c];
-        gg[11 + c] = w * gom[5 + c];
-      }
-      const float galpha = active ? T * gw + (final_term - suffix) * inv_keep : 0.f;
-      suffix += w * gw;
-      float gs[2] = {0.f, 0.f};
-      float gdir[3] = {0.f, 0.f, 0.f};
-      shade_backward<Neural>(r, s_, a, gc, ga, gs, gdir);
-      if constexpr (Neural) {
+        for (int c = 0; c < 3; ++c) {
+          gw += gom[c] * a.color[c] + gom[5 + c] * r[11 + c];
+          gc[c] = w * gom[c];
+          gg[11 + c] = w * gom[5 + c];
+        }
+        const float galpha_lane = T * gw + (final_term - suffix) * inv_keep;
+        const float galpha = kMasked ? (active ? galpha_lane : 0.f) : galpha_lane;
+        suffix += w * gw;
+        float gs[2] = {0.f, 0.f};
+        float gdir[3] = {0.f, 0.f, 0.f};
+        shade_backward<Neural>(r, s_, a, gc, ga, gs, gdir);
+        if constexpr (Neural) {
 #pragma unroll
-        for (int k = 0; k < 3; ++k) gg[14 + k] = gdir[k];
-      }
-      const float gz = w * gom[4] + gom[8] * 2.f * w * (m * total_a - m1) * mnear *
-                                       (inv_depth * inv_depth);
-      const bool tilt = Neural || surface;
-      gs[0] = tilt ? gs[0] + gz * r[6] : gs[0];
-      gs[1] = tilt ? gs[1] + gz * r[7] : gs[1];
-      gg[6] = tilt ? gz * s_[0] : 0.f;
-      gg[7] = tilt ? gz * s_[1] : 0.f;
-      gg[8] = gz;
-      const bool below = r[OP] * e < 0.99f;
-      grad[NP - 1] = below ? galpha * e : 0.f;
-      const float grho = below ? -0.5f * galpha * r[OP] * e : 0.f;
-      gs[0] = surface ? gs[0] + 2.f * s_[0] * grho : gs[0];
-      gs[1] = surface ? gs[1] + 2.f * s_[1] * grho : gs[1];
-      gg[9] = surface ? 0.f : 4.f * (r[9] - x) * grho;
-      gg[10] = surface ? 0.f : 4.f * (r[10] - y) * grho;
-      const float gp[3] = {gs[0] * inv_pz, gs[1] * inv_pz,
-                           -(gs[0] * s_[0] + gs[1] * s_[1]) * inv_pz};
-      // p = k x l  =>  dk = l x gp, dl = gp x k; k = x T2 - T0 and l = y T2 - T1,
-      // so the T rows receive -dk, -dl and x dk + y dl: computed directly as
-      // gp x l = -dk and k x gp = -dl.
-      const float nk[3] = {gp[1] * v.l[2] - gp[2] * v.l[1], gp[2] * v.l[0] - gp[0] * v.l[2],
-                           gp[0] * v.l[1] - gp[1] * v.l[0]};
-      const float nl[3] = {v.k[1] * gp[2] - v.k[2] * gp[1], v.k[2] * gp[0] - v.k[0] * gp[2],
-                           v.k[0] * gp[1] - v.k[1] * gp[0]};
+          for (int k = 0; k < 3; ++k) gg[14 + k] = gdir[k];
+        }
+        const float gz = w * gom[4] + gom[8] * 2.f * w * (m * total_a - m1) * mnear *
+                                         (inv_depth * inv_depth);
+        // The depth tilts with s only where a classic sample lies on the surface.
+        const float gz_tilt = (Neural || surface) ? gz : 0.f;
+        gs[0] += gz_tilt * r[6];
+        gs[1] += gz_tilt * r[7];
+        gg[6] = gz_tilt * s_[0];
+        gg[7] = gz_tilt * s_[1];
+        gg[8] = gz;
+        const bool below = r[OP] * e < 0.99f;
+        grad[NP - 1] = below ? galpha * e : 0.f;
+        const float grho = below ? -0.5f * galpha * r[OP] * e : 0.f;
+        // rho is rho3 = |s|^2 on the surface (d/ds = 2 s) and otherwise
+        // rho2 = 2 |xy - pixel|^2 (d/dxy = 4 (xy - pixel)).
+        const float grho3 = surface ? 2.f * grho : 0.f;
+        const float grho2 = surface ? 0.f : 4.f * grho;
+        gs[0] += s_[0] * grho3;
+        gs[1] += s_[1] * grho3;
+        gg[9] = (r[9] - x) * grho2;
+        gg[10] = (r[10] - y) * grho2;
+        const float gp[3] = {gs[0] * inv_pz, gs[1] * inv_pz,
+                             -(gs[0] * s_[0] + gs[1] * s_[1]) * inv_pz};
+        // p = k x l  =>  dk = l x gp, dl = gp x k; k = x T2 - T0 and l = y T2 - T1,
+        // so the T rows receive -dk, -dl and x dk + y dl: computed directly as
+        // gp x l = -dk and k x gp = -dl.
+        const float nk[3] = {gp[1] * v.l[2] - gp[2] * v.l[1], gp[2] * v.l[0] - gp[0] * v.l[2],
+                             gp[0] * v.l[1] - gp[1] * v.l[0]};
+        const float nl[3] = {v.k[1] * gp[2] - v.k[2] * gp[1], v.k[2] * gp[0] - v.k[0] * gp[2],
+                             v.k[0] * gp[1] - v.k[1] * gp[0]};
 #pragma unroll
-      for (int k = 0; k < 3; ++k) {
-        gg[k] = nk[k];
-        gg[3 + k] = nl[k];
-        gg[6 + k] -= x * nk[k] + y * nl[k];
-      }
-      // Wave totals, one per lane, added into the batch accumulator.
-      float* dst = acc + j * NP;
-      if constexpr (NP <= 64) {
-        const float total = wave_reduce_scatter<NP>(grad, lane);
-        const int param = rs_param<NP>(lane);
-        if (param < NP && total != 0.f) atomicAdd(dst + param, total);
-      } else {
-        constexpr int H = NP / 2;
-        float lo[H], hi[NP - H];
+        for (int k = 0; k < 3; ++k) {
+          gg[k] = nk[k];
+          gg[3 + k] = nl[k];
+          gg[6 + k] -= x * nk[k] + y * nl[k];
+        }
+        // Wave totals, one per lane, added into the batch accumulator.
+        float* dst = acc + j * NP;
+        if constexpr (NP <= 64) {
+          const float total = wave_reduce_scatter<NP>(grad, lane);
+          const int param = rs_param<NP>(lane);
+          if (param < NP && total != 0.f) atomicAdd(dst + param, total);
+        } else {
+          constexpr int H = NP / 2;
+          float lo[H], hi[NP - H];
 #pragma unroll
-        for (int k = 0; k < H; ++k) lo[k] = grad[k];
+          for (int k = 0; k < H; ++k) lo[k] = grad[k];
 #pragma unroll
-        for (int k = 0; k < NP - H; ++k) hi[k] = grad[H + k];
-        const float t0 = wave_reduce_scatter<H>(lo, lane);
-        const int p0 = rs_param<H>(lane);
-        if (p0 < H && t0 != 0.f) atomicAdd(dst + p0, t0);
-        const float t1 = wave_reduce_scatter<NP - H>(hi, lane);
-        const int p1 = rs_param<NP - H>(lane);
-        if (p1 < NP - H && t1 != 0.f) atomicAdd(dst + H + p1, t1);
-      }
+          for (int k = 0; k < NP - H; ++k) hi[k] = grad[H + k];
+          const float t0 = wave_reduce_scatter<H>(lo, lane);
+          const int p0 = rs_param<H>(lane);
+          if (p0 < H && t0 != 0.f) atomicAdd(dst + p0, t0);
+          const float t1 = wave_reduce_scatter<NP - H>(hi, lane);
+          const int p1 = rs_param<NP - H>(lane);
+          if (p1 < NP - H && t1 != 0.f) atomicAdd(dst + H + p1, t1);
+        }
+      };
+      if (finite_pixels)
+        adjoint(std::false_type{});
+      else
+        adjoint(std::true_type{});
     }
     __syncthreads();
     // Flush this batch: one global atomic per nonzero (record, parameter).

@@ -10,11 +10,12 @@
 // butterfly reductions, and the final sums sit one per lane, so a single
 // vector atomic (LDS or global) publishes all N of them.
 //
-// Bits 5 and 4 use the gfx950 v_permlane32_swap / v_permlane16_swap
-// instructions (one instruction exchanges two halves); bits 3..0 use DPP
-// row_mirror, row_half_mirror and quad permutations, each of which pairs
-// every lane with bit B clear with a lane that has bit B set inside the
-// same group, which is all the reduction needs.
+// Bits 3..0 use DPP row_mirror, row_half_mirror and quad permutations, each
+// of which pairs every lane with bit B clear with a lane that has bit B set
+// inside the same group; bits 5 and 4 use the gfx950 v_permlane32_swap /
+// v_permlane16_swap instructions (one instruction exchanges two halves).
+// Any pairing that flips bit B and keeps the bits already reduced is all
+// the reduction needs.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -90,23 +91,46 @@ __device__ __forceinline__ void rs_step(const float* in, float* out, int lane) {
   }
 }
 
-// Half sizes at each step for an N-value reduction.
+// The lane bits are reduced in the order 3, 2, 1, 0, 5, 4: the first steps
+// move the most values, so they take the cheapest exchange (two bank-masked
+// DPP adds per pair), the quad steps with their per-lane selects follow,
+// and the row-crossing permlane swaps, which cost more than a plain VALU
+// instruction, come last, once the vector has shrunk to a few values. The
+// swaps then read values written by compiler-visible instructions, whose
+// hazards the compiler resolves (it does not see into inline assembly).
+// Half sizes after each step of an N-value reduction:
 template <int N>
 struct RsShape {
-  static constexpr int h5 = (N + 1) / 2;
-  static constexpr int h4 = (h5 + 1) / 2;
-  static constexpr int h3 = (h4 + 1) / 2;
+  static constexpr int h3 = (N + 1) / 2;
   static constexpr int h2 = (h3 + 1) / 2;
   static constexpr int h1 = (h2 + 1) / 2;
   static constexpr int h0 = (h1 + 1) / 2;
+  static constexpr int h5 = (h0 + 1) / 2;
+  static constexpr int h4 = (h5 + 1) / 2;
 };
 
-// Parameter index whose total lane `lane` holds after wave_reduce_scatter<N>.
+// Parameter index whose total lane `lane` holds after wave_reduce_scatter<N>,
+// or N for a lane left with padding. Every step splits the vector at its
+// fixed half size (RsShape); the lane's share of real values, a prefix of
+// its vector, is followed through the steps, and a lane whose share runs
+// out holds padding (exactly zero).
 template <int N>
 __device__ __forceinline__ int rs_param(int lane) {
   using S = RsShape<N>;
-  return ((lane >> 5) & 1) * S::h5 + ((lane >> 4) & 1) * S::h4 + ((lane >> 3) & 1) * S::h3 +
-         ((lane >> 2) & 1) * S::h2 + ((lane >> 1) & 1) * S::h1 + (lane & 1) * S::h0;
+  constexpr int kBits[6] = {3, 2, 1, 0, 5, 4};
+  constexpr int kHalf[6] = {S::h3, S::h2, S::h1, S::h0, S::h5, S::h4};
+  int first = 0, count = N;
+#pragma unroll
+  for (int step = 0; step < 6; ++step) {
+    const int half = kHalf[step];
+    if ((lane >> kBits[step]) & 1) {
+      first += half;
+      count = count > half ? count - half : 0;
+    } else {
+      count = count < half ? count : half;
+    }
+  }
+  return count > 0 ? first : N;
 }
 
 // All 64 lanes must be active. Returns this lane's total (see rs_param).
@@ -114,13 +138,13 @@ template <int N>
 __device__ __forceinline__ float wave_reduce_scatter(const float (&v)[N], int lane) {
   static_assert(N >= 1 && N <= 64, "one reduce-scatter covers at most 64 values");
   using S = RsShape<N>;
-  float a[S::h5], b[S::h4], c[S::h3], d[S::h2], e[S::h1], f[S::h0];
-  rs_step<5, N>(v, a, lane);
-  rs_step<4, S::h5>(a, b, lane);
-  rs_step<3, S::h4>(b, c, lane);
-  rs_step<2, S::h3>(c, d, lane);
-  rs_step<1, S::h2>(d, e, lane);
-  rs_step<0, S::h1>(e, f, lane);
+  float a[S::h3], b[S::h2], c[S::h1], d[S::h0], e[S::h5], f[S::h4];
+  rs_step<3, N>(v, a, lane);
+  rs_step<2, S::h3>(a, b, lane);
+  rs_step<1, S::h2>(b, c, lane);
+  rs_step<0, S::h1>(c, d, lane);
+  rs_step<5, S::h0>(d, e, lane);
+  rs_step<4, S::h5>(e, f, lane);
   return f[0];
 }
 
