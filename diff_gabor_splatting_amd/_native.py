@@ -25,6 +25,8 @@ TILE = 16
 GEOMETRY_SIZE = 17
 MAP_SIZE = 9
 INT_MAX = 2**31 - 1
+# Replay-list entries carry a tile-list position in 28 bits.
+REPLAY_MAX_ENTRIES = 2**28 - 1
 
 _c_int = ctypes.c_int32
 _c_i64 = ctypes.c_int64
@@ -102,12 +104,14 @@ _SIGNATURES = {
         + [_c_ptr] * 7
         + [_c_i64, _c_int, _c_int, _c_float, _c_float]
         + [_c_ptr] * 5
+        + [_c_i64]
+        + [_c_ptr] * 2
         + [_c_size, _c_ptr],
     ),
     "gs_render_backward": (
         _c_int,
         [_c_int]
-        + [_c_ptr] * 11
+        + [_c_ptr] * 13
         + [_c_i64, _c_int, _c_int, _c_float, _c_float]
         + [_c_ptr] * 5
         + [_c_size, _c_ptr],
@@ -653,7 +657,7 @@ def _map_group_args(groups, what: str):
 def rasterize_forward(
     geometry, appearance, opacities, primitive_ids, image_ids, radii, backgrounds,
     width, height, neural, near_plane, far_plane, outputs=None, overlap=None, capacity=None,
-    flags=None,
+    flags=None, replay=False,
 ):
     """Bin, sort and composite: returns [maps, point_list, ranges, state, contributors].
 
@@ -668,7 +672,11 @@ def rasterize_forward(
     addition): called once while the host waits for M, to queue GPU work
     that does not depend on it. ``capacity`` / ``flags`` (additions): bin
     into a point list of fixed capacity without reading M on the host (see
-    bin_depth_first).
+    bin_depth_first). ``replay`` (an addition): also return, as a sixth item,
+    the tiles' replay lists for rasterize_backward - (lists [M, 2] int32,
+    counts [I*tw*th] int32): per tile, the point-list entries that some pixel
+    took, in list order - or None when the point list is too long for them
+    (2^28 entries or more).
     """
     _check_buffers(geometry, appearance, opacities, primitive_ids, backgrounds, neural)
     _require(
@@ -720,15 +728,23 @@ def rasterize_forward(
             )
             maps = tuple(groups)
         data, strides = _map_group_args(groups, "map outputs")
+        lists = None
+        if replay and point_list.numel() < REPLAY_MAX_ENTRIES:
+            lists = (torch.empty((max(point_list.numel(), 1), 2), dtype=torch.int32,
+                                 device=device),
+                     torch.empty(tiles, dtype=torch.int32, device=device))
         workspace = _workspace(lib.gs_render_workspace_size(images, width, height), device)
         _check(
             lib.gs_render_forward(
                 int(bool(neural)), _ptr(geometry), _ptr(appearance), _ptr(opacities),
                 _ptr(primitive_ids), _ptr(backgrounds), _ptr(point_list), _ptr(ranges), images,
                 width, height, near_plane, far_plane, data, strides, _ptr(state),
-                _ptr(contributors), _ptr(workspace), workspace.numel(), stream,
+                _ptr(contributors), _ptr(lists and lists[0]), point_list.numel(),
+                _ptr(lists and lists[1]), _ptr(workspace), workspace.numel(), stream,
             )
         )
+    if replay:
+        return [maps, point_list, ranges, state, contributors, lists]
     return [maps, point_list, ranges, state, contributors]
 
 
@@ -741,6 +757,7 @@ def zero_accumulators(geometry, appearance, opacities, backgrounds):
 def rasterize_backward(
     geometry, appearance, opacities, primitive_ids, backgrounds, point_list, ranges, state,
     contributors, grad_maps, width, height, neural, near_plane, far_plane, accumulators=None,
+    replay=None,
 ):
     """Reverse compositing: returns [grad_geometry, grad_appearance, grad_opacities,
     grad_backgrounds] (rasterize.cu:506-529).
@@ -750,6 +767,8 @@ def rasterize_backward(
     a tensor of any strides or None (zero); strided views are read in place.
     ``accumulators`` (an addition): zeroed tensors from zero_accumulators,
     cleared ahead of time, that receive and are returned as the gradients.
+    ``replay`` (an addition): the replay lists returned by rasterize_forward
+    (or None); the gradients are the same, computed from fewer records.
     """
     _check_buffers(geometry, appearance, opacities, primitive_ids, backgrounds, neural)
     device = geometry.device
@@ -774,6 +793,18 @@ def rasterize_backward(
         and contributors.shape == (images, height, width),
         "invalid saved compositor state",
     )
+    if replay is not None:
+        tw, th = tile_grid(width, height)
+        lists, counts = replay
+        _require(
+            lists.dtype == torch.int32 and counts.dtype == torch.int32
+            and lists.device == device and counts.device == device
+            and lists.is_contiguous() and counts.is_contiguous()
+            and lists.dim() == 2 and lists.size(1) == 2
+            and lists.size(0) >= point_list.numel()
+            and counts.shape == (images * tw * th,),
+            "invalid replay lists",
+        )
     with torch.cuda.device(device):
         if accumulators is None:
             accumulators = zero_accumulators(geometry, appearance, opacities, backgrounds)
@@ -792,7 +823,8 @@ def rasterize_backward(
             lib.gs_render_backward(
                 int(bool(neural)), _ptr(geometry), _ptr(appearance), _ptr(opacities),
                 _ptr(primitive_ids), _ptr(backgrounds), _ptr(point_list), _ptr(ranges),
-                _ptr(state), _ptr(contributors), data, strides, images, width, height,
+                _ptr(state), _ptr(contributors), _ptr(replay and replay[0]),
+                _ptr(replay and replay[1]), data, strides, images, width, height,
                 near_plane, far_plane, _ptr(gg), _ptr(ga), _ptr(go), _ptr(gb),
                 _ptr(workspace), workspace.numel(), _stream(device),
             )

@@ -392,18 +392,26 @@ __device__ __forceinline__ void shade(const float* r, const float* s, Shade& a) 
 // already needs many (the backward).
 enum Gather { kGatherLoops, kGatherQuarters };
 
-template <bool Neural, Gather Mode>
+// Which records a wave composites: kReachTest tests every record's footprint
+// against the wave's quadrant; kReplayMask reads the quadrant bits of a
+// replay entry (bit 28 + w: wave w's quadrant took the record in the
+// forward), staged per record in `entries`.
+enum Select { kReachTest, kReplayMask };
+
+template <bool Neural, Gather Mode, Select Which = kReachTest>
 __device__ __forceinline__ uint64_t load_batch(float* rows, float* raw, float* reach_rows,
                                                int* ids, int64_t* prims, float tile_x,
                                                float tile_y,
                                                int count, int id, int64_t prim,
                                                const float* geometry, const float* appearance,
-                                               const float* opacities) {
+                                               const float* opacities, int entry = 0,
+                                               int* entries = nullptr) {
   using L = Layout<Neural>;
   const int t = threadIdx.x;
   if (t < count) {  // (id, prim): this thread's record, fetched by the caller ahead of time
     ids[t] = id;
     prims[t] = prim;
+    if constexpr (Which == kReplayMask) entries[t] = entry;
   }
   __syncthreads();
   if constexpr (Mode == kGatherQuarters) {
@@ -501,7 +509,7 @@ __device__ __forceinline__ uint64_t load_batch(float* rows, float* raw, float* r
   // per lane) against its own 8x8 quadrant of the tile.
   const int wave = t >> 6;
   const int j = t & 63;
-  if (wave == 1 && j < count) {
+  if (Which == kReachTest && wave == 1 && j < count) {
     const float* g = raw + j * L::RAW_STRIDE;
     record_reach(g, reject_threshold(g[kGeometry]), reach_rows + j * kReachPitch);
   }
@@ -555,11 +563,47 @@ __device__ __forceinline__ uint64_t load_batch(float* rows, float* raw, float* r
     }
   }
   __syncthreads();
-  // Bit j of the ballot says that record j may touch this wave's quadrant.
-  const bool reach = j < count && quadrant_reach(reach_rows + j * kReachPitch,
-                                                 tile_x + float(wave & 1) * 8.f,
-                                                 tile_y + float(wave >> 1) * 8.f);
-  return __ballot(reach);
+  if constexpr (Which == kReplayMask) {
+    // Bit j of the ballot says that this wave's quadrant took record j.
+    return __ballot(j < count && ((uint32_t(entries[j]) >> (28 + wave)) & 1u));
+  } else {
+    // Bit j of the ballot says that record j may touch this wave's quadrant.
+    const bool reach = j < count && quadrant_reach(reach_rows + j * kReachPitch,
+                                                   tile_x + float(wave & 1) * 8.f,
+                                                   tile_y + float(wave >> 1) * 8.f);
+    return __ballot(reach);
+  }
+}
+
+// Replay lists. The forward records, per tile, the list entries that at
+// least one pixel took, in list order, as int2 {point-list entry (pair
+// index), position in the tile's list | quadrant bits << 28}: bit 28 + w is
+// set when a pixel of wave w's 8x8 quadrant took the record. Taken records
+// are exactly the ones the backward replays (a pixel takes every accepted
+// record up to its last contributor), so the backward walks this list
+// instead of the tile's whole list and skips the footprint tests.
+constexpr int kReplayPositionBits = 28;
+constexpr int kReplayPositionMask = (1 << kReplayPositionBits) - 1;
+
+// Wave 0 appends the taken records of one batch (count records from list
+// position first, their entry ids still staged in ids) to the tile's replay
+// list, which holds n entries so far. Returns the new length.
+__device__ __forceinline__ int append_replay(const uint64_t* wave_taken, const int* ids,
+                                             int2* list, int n, int first, int count) {
+  const int j = lane_id();
+  uint32_t quads = 0;
+#pragma unroll
+  for (int w = 0; w < kTilePixels / 64; ++w)
+    quads |= uint32_t((wave_taken[w] >> j) & 1u) << w;
+  const bool keep = j < count && quads != 0u;
+  const uint64_t kept = __ballot(keep);
+  if (keep) {
+    const int slot =
+        n + int(__builtin_amdgcn_mbcnt_hi(uint32_t(kept >> 32),
+                                          __builtin_amdgcn_mbcnt_lo(uint32_t(kept), 0u)));
+    list[slot] = make_int2(ids[j], int(uint32_t(first + j) | (quads << kReplayPositionBits)));
+  }
+  return n + __popcll(kept);
 }
 
 struct TilePixel {
@@ -669,20 +713,24 @@ __global__ __launch_bounds__(kTilePixels) void tile_last_kernel(int width, int h
                           max(wave_max_last[2], wave_max_last[3]));
 }
 
-template <bool Neural>
+// Replay: also write the tile's replay list (replay + range start, see
+// append_replay) and its length (replay_counts[tile]).
+template <bool Neural, bool Replay>
 __global__ __launch_bounds__(kTilePixels, Neural ? 3 : 5) void render_forward_kernel(
     int width, int height, int tw, int th, const float* __restrict__ geometry,
     const float* __restrict__ appearance, const float* __restrict__ opacities,
     const int64_t* __restrict__ primitive_ids, const float* __restrict__ backgrounds,
     const int* __restrict__ point_list, const int2* __restrict__ ranges,
     const int* __restrict__ order, float near_plane, float far_plane, MapGroups<float> maps,
-    float* __restrict__ state, int* __restrict__ contributors) {
+    float* __restrict__ state, int* __restrict__ contributors, int2* __restrict__ replay,
+    int* __restrict__ replay_counts) {
   using L = Layout<Neural>;
   __shared__ __align__(16) float rows[kBatch * L::STRIDE];
   __shared__ __align__(16) float raw[kBatch * L::RAW_STRIDE];
   __shared__ float reach_rows[kBatch * kReachPitch];
   __shared__ int ids[kBatch];
   __shared__ int64_t prims[kBatch];
+  __shared__ uint64_t wave_taken[kTilePixels / 64];
   const int tile = order[blockIdx.x];
   const TilePixel tp = tile_pixel(tile, width, height, tw, th);
   const float x = float(tp.px), y = float(tp.py);
@@ -707,8 +755,15 @@ __global__ __launch_bounds__(kTilePixels, Neural ? 3 : 5) void render_forward_ke
     next_id = point_list[range.x + threadIdx.x];
     next_prim = primitive_ids[next_id];
   }
+  // Replay bookkeeping (wave 0): entries written so far, and the previous
+  // batch, whose taken records are appended once every wave has finished it
+  // (before the next batch overwrites its staged ids).
+  int replay_n = 0, batch_first = 0, batch_count = 0;
   for (int start = range.x; start < range.y; start += kBatch) {
     if (__syncthreads_count(done) == kTilePixels) break;
+    if (Replay && wave == 0)
+      replay_n = append_replay(wave_taken, ids, replay + range.x, replay_n, batch_first,
+                               batch_count);
     const int count = min(kBatch, range.y - start);
     const int id = next_id;
     const int64_t prim = next_prim;
@@ -718,11 +773,14 @@ __global__ __launch_bounds__(kTilePixels, Neural ? 3 : 5) void render_forward_ke
         rows, raw, reach_rows, ids, prims, tile_x, tile_y, count, id, prim, geometry, appearance,
         opacities);
     if (ahead) next_prim = primitive_ids[next_id];
+    batch_first = start - range.x;
+    batch_count = count;
     // Only the records whose footprint meets this wave's quadrant, in list
     // order. The loop runs in lockstep across the wave: finished lanes are
     // masked through `done` rather than leaving the loop, so that every
     // branch below is on a wave-wide (scalar) condition.
     uint64_t todo = __all(done) ? 0 : wave_uniform(reach);
+    uint64_t taken = 0;  // records that a lane of this wave took
     while (todo) {
       const int j = __builtin_ctzll(todo);
       todo &= todo - 1;
@@ -738,6 +796,7 @@ __global__ __launch_bounds__(kTilePixels, Neural ? 3 : 5) void render_forward_ke
         if (__all(done)) break;
       }
       if (!__any(take)) continue;
+      taken |= uint64_t(1) << j;
       Shade a;
       shade<Neural, false>(r, v.s, a);
       if (take) {
@@ -755,6 +814,15 @@ __global__ __launch_bounds__(kTilePixels, Neural ? 3 : 5) void render_forward_ke
         T = next;
         last = start + j - range.x + 1;
       }
+    }
+    if (Replay && lane_id() == 0) wave_taken[wave] = taken;
+  }
+  if constexpr (Replay) {
+    __syncthreads();
+    if (wave == 0) {
+      replay_n = append_replay(wave_taken, ids, replay + range.x, replay_n, batch_first,
+                               batch_count);
+      if (threadIdx.x == 0) replay_counts[tile] = replay_n;
     }
   }
   if (tp.inside) {
@@ -856,13 +924,18 @@ __device__ __forceinline__ float classic_appearance_gradient(const float* sums, 
   return -r[R::HW + k - 14] * sums[k];
 }
 
-template <bool Neural>
+// Replay: walk the tile's replay list written by the forward (replay +
+// range start, replay_counts[tile] entries) instead of its point list up to
+// tile_last[tile], compositing each record only in the quadrants that took
+// it; tile_last is then unused.
+template <bool Neural, bool Replay>
 __global__ __launch_bounds__(kTilePixels, Neural ? 2 : 4) void render_backward_kernel(
     int width, int height, int tw, int th, const float* __restrict__ geometry,
     const float* __restrict__ appearance, const float* __restrict__ opacities,
     const int64_t* __restrict__ primitive_ids, const float* __restrict__ backgrounds,
     const int* __restrict__ point_list, const int2* __restrict__ ranges,
     const int* __restrict__ order, const int* __restrict__ tile_last,
+    const int2* __restrict__ replay, const int* __restrict__ replay_counts,
     const float* __restrict__ state, const int* __restrict__ contributors,
     MapGroups<const float> grad_maps, float near_plane, float far_plane,
     float* __restrict__ grad_geometry, float* __restrict__ grad_appearance,
@@ -882,6 +955,7 @@ __global__ __launch_bounds__(kTilePixels, Neural ? 2 : 4) void render_backward_k
   __shared__ float reach_rows[kBatch * kReachPitch];
   __shared__ int ids[kBatch];
   __shared__ int64_t prims[kBatch];
+  __shared__ int entries[kBatch];  // replay entries (position | quadrant bits) of the batch
   __shared__ float bg_acc[3];
   const int lane = lane_id();
   const int tile = order[blockIdx.x];
@@ -924,48 +998,68 @@ __global__ __launch_bounds__(kTilePixels, Neural ? 2 : 4) void render_backward_k
     const int param = rs_param<3>(lane);
     if (param < 3 && total != 0.f) atomicAdd(&bg_acc[param], total);
   }
-  const int block_last = tile_last[tile];
+  // Records walked backwards: list positions up to the tile's largest
+  // contributor count, or the replay list's entries.
+  const int2 range = ranges[tile];
+  const int block_last = Replay ? replay_counts[tile] : tile_last[tile];
   // Records past every lane's last contributor are inactive in this wave.
   const int wave_last = __builtin_amdgcn_readfirstlane(wave_max(last));
-  const int2 range = ranges[tile];
   const float mscale = far_plane / (far_plane - near_plane);
   const float mnear = mscale * near_plane;
   float suffix = 0.f;
 
-  // Record threadIdx.x of a batch starting at `start` is list position
-  // range.x + start - 1 - threadIdx.x; the next batch's entry and id are
-  // read ahead as in the forward.
-  int next_id = 0;
+  // Record threadIdx.x of a batch starting at `start` is list position (or
+  // replay entry) range.x + start - 1 - threadIdx.x; the next batch's entry
+  // and id are read ahead as in the forward.
+  int next_id = 0, next_entry = 0;
   int64_t next_prim = 0;
   if (int(threadIdx.x) < min(kBatch, block_last)) {
-    next_id = point_list[range.x + block_last - 1 - threadIdx.x];
+    if constexpr (Replay) {
+      const int2 e = replay[range.x + block_last - 1 - threadIdx.x];
+      next_id = e.x;
+      next_entry = e.y;
+    } else {
+      next_id = point_list[range.x + block_last - 1 - threadIdx.x];
+    }
     next_prim = primitive_ids[next_id];
   }
   for (int start = block_last; start > 0; start -= kBatch) {
     const int count = min(kBatch, start);
-    const int id = next_id;
+    const int id = next_id, entry = next_entry;
     const int64_t prim = next_prim;
     const bool ahead = int(threadIdx.x) < min(kBatch, start - kBatch);
-    if (ahead) next_id = point_list[range.x + start - kBatch - 1 - threadIdx.x];
-    const uint64_t reach = load_batch<Neural, kGatherLoops>(
+    if (ahead) {
+      if constexpr (Replay) {
+        const int2 e = replay[range.x + start - kBatch - 1 - threadIdx.x];
+        next_id = e.x;
+        next_entry = e.y;
+      } else {
+        next_id = point_list[range.x + start - kBatch - 1 - threadIdx.x];
+      }
+    }
+    const uint64_t reach = load_batch<Neural, kGatherLoops, Replay ? kReplayMask : kReachTest>(
         rows, raw, reach_rows, ids, prims, tile_x, tile_y, count, id, prim, geometry, appearance,
-        opacities);
+        opacities, entry, entries);
     if (ahead) next_prim = primitive_ids[next_id];
     // The raw rows are dead: clear the accumulator that shares their LDS.
     for (int i = threadIdx.x; i < count * NP; i += kTilePixels) acc[i] = 0.f;
     __syncthreads();
     uint64_t todo = wave_uniform(reach);
-    // Row j holds list position start - j (counted from 1).
-    const int beyond = start - wave_last;  // rows j < beyond lie past wave_last
-    if (beyond >= 64) todo = 0;
-    else if (beyond > 0) todo &= ~((uint64_t(1) << beyond) - 1);
+    if constexpr (!Replay) {
+      // Row j holds list position start - j (counted from 1).
+      const int beyond = start - wave_last;  // rows j < beyond lie past wave_last
+      if (beyond >= 64) todo = 0;
+      else if (beyond > 0) todo &= ~((uint64_t(1) << beyond) - 1);
+    }
     while (todo) {
       const int j = __builtin_ctzll(todo);
       todo &= todo - 1;
       const float* r = rows + j * L::STRIDE;
+      // List position of row j, counted from 1.
+      const int position = Replay ? (entries[j] & kReplayPositionMask) + 1 : start - j;
       Sample v;
       const bool active =
-          sample_surface<Neural, true>(r, x, y, near_plane, tp.inside && (start - j) <= last, v);
+          sample_surface<Neural, true>(r, x, y, near_plane, tp.inside && position <= last, v);
       if (!__any(active)) continue;
       // Every lane runs the adjoint. A lane that does not take the sample
       // contributes exact zeros: the sample's values are finite stand-ins
@@ -1158,6 +1252,7 @@ int gs_render_forward(int32_t neural, const float* geometry, const float* appear
                       const int32_t* ranges, int64_t images, int32_t width, int32_t height,
                       float near_plane, float far_plane, float* const* maps,
                       const int64_t* map_strides, float* state, int32_t* contributors,
+                      int32_t* replay, int64_t replay_capacity, int32_t* replay_counts,
                       void* workspace, size_t workspace_bytes, void* stream) {
   using namespace gs;
   clear_error();
@@ -1165,6 +1260,11 @@ int gs_render_forward(int32_t neural, const float* geometry, const float* appear
   if (status != GS_OK) return status;
   GS_REQUIRE(backgrounds && ranges && maps && map_strides && state && contributors,
              GS_ERR_ARGUMENT, "null pointer passed to gs_render_forward");
+  GS_REQUIRE(!replay == !replay_counts, GS_ERR_ARGUMENT,
+             "replay and replay_counts must both be given or both be null");
+  GS_REQUIRE(!replay || (replay_capacity >= 0 && replay_capacity <= kReplayPositionMask),
+             GS_ERR_OVERFLOW, "replay lists need a point list of at most %d entries, got %lld",
+             kReplayPositionMask, static_cast<long long>(replay_capacity));
   for (int g = 0; g < kMapGroups; ++g)
     GS_REQUIRE(maps[g], GS_ERR_ARGUMENT, "null map output group %d", g);
   const MapGroups<float> out = map_groups(maps, map_strides);
@@ -1179,14 +1279,19 @@ int gs_render_forward(int32_t neural, const float* geometry, const float* appear
   RenderWorkspace w = render_layout(workspace, tiles);
   tile_order_kernel<<<1, kOrderBlock, 0, s>>>(nullptr, r, tiles, w.order);
   GS_LAUNCHED("tile_order_kernel");
+  int2* lists = reinterpret_cast<int2*>(replay);
+  auto launch = [&](auto kernel) {
+    kernel<<<unsigned(tiles), kTilePixels, 0, s>>>(
+        width, height, tw, th, geometry, appearance, opacities, primitive_ids, backgrounds,
+        point_list, r, w.order, near_plane, far_plane, out, state, contributors, lists,
+        replay_counts);
+  };
   if (neural) {
-    render_forward_kernel<true><<<unsigned(tiles), kTilePixels, 0, s>>>(
-        width, height, tw, th, geometry, appearance, opacities, primitive_ids, backgrounds,
-        point_list, r, w.order, near_plane, far_plane, out, state, contributors);
+    if (replay) launch(render_forward_kernel<true, true>);
+    else launch(render_forward_kernel<true, false>);
   } else {
-    render_forward_kernel<false><<<unsigned(tiles), kTilePixels, 0, s>>>(
-        width, height, tw, th, geometry, appearance, opacities, primitive_ids, backgrounds,
-        point_list, r, w.order, near_plane, far_plane, out, state, contributors);
+    if (replay) launch(render_forward_kernel<false, true>);
+    else launch(render_forward_kernel<false, false>);
   }
   GS_LAUNCHED("render_forward_kernel");
   return GS_OK;
@@ -1196,7 +1301,8 @@ int gs_render_backward(int32_t neural, const float* geometry, const float* appea
                        const float* opacities, const int64_t* primitive_ids,
                        const float* backgrounds, const int32_t* point_list,
                        const int32_t* ranges, const float* state,
-                       const int32_t* contributors, const float* const* grad_maps,
+                       const int32_t* contributors, const int32_t* replay,
+                       const int32_t* replay_counts, const float* const* grad_maps,
                        const int64_t* grad_map_strides, int64_t images,
                        int32_t width, int32_t height, float near_plane, float far_plane,
                        float* grad_geometry, float* grad_appearance, float* grad_opacities,
@@ -1209,6 +1315,8 @@ int gs_render_backward(int32_t neural, const float* geometry, const float* appea
   GS_REQUIRE(backgrounds && ranges && state && contributors && grad_maps && grad_map_strides &&
                  grad_backgrounds,
              GS_ERR_ARGUMENT, "null pointer passed to gs_render_backward");
+  GS_REQUIRE(!replay == !replay_counts, GS_ERR_ARGUMENT,
+             "replay and replay_counts must both be given or both be null");
   const MapGroups<const float> grads = map_groups(grad_maps, grad_map_strides);
   const size_t need = gs_render_workspace_size(images, width, height);
   GS_REQUIRE(workspace && workspace_bytes >= need, GS_ERR_WORKSPACE,
@@ -1219,21 +1327,30 @@ int gs_render_backward(int32_t neural, const float* geometry, const float* appea
   const int tiles = int(images * tw * th);
   const int2* r = reinterpret_cast<const int2*>(ranges);
   RenderWorkspace w = render_layout(workspace, tiles);
-  tile_last_kernel<<<unsigned(tiles), kTilePixels, 0, s>>>(width, height, tw, th, contributors,
-                                                           w.tile_last);
-  GS_LAUNCHED("tile_last_kernel");
-  tile_order_kernel<<<1, kOrderBlock, 0, s>>>(w.tile_last, r, tiles, w.order);
+  // Tiles are ordered by the records they replay: the replay list's length,
+  // or the largest contributor count.
+  if (!replay) {
+    tile_last_kernel<<<unsigned(tiles), kTilePixels, 0, s>>>(width, height, tw, th,
+                                                             contributors, w.tile_last);
+    GS_LAUNCHED("tile_last_kernel");
+  }
+  tile_order_kernel<<<1, kOrderBlock, 0, s>>>(replay ? replay_counts : w.tile_last, r, tiles,
+                                              w.order);
   GS_LAUNCHED("tile_order_kernel");
+  const int2* lists = reinterpret_cast<const int2*>(replay);
+  auto launch = [&](auto kernel) {
+    kernel<<<unsigned(tiles), kTilePixels, 0, s>>>(
+        width, height, tw, th, geometry, appearance, opacities, primitive_ids, backgrounds,
+        point_list, r, w.order, w.tile_last, lists, replay_counts, state, contributors, grads,
+        near_plane, far_plane, grad_geometry, grad_appearance, grad_opacities,
+        grad_backgrounds);
+  };
   if (neural) {
-    render_backward_kernel<true><<<unsigned(tiles), kTilePixels, 0, s>>>(
-        width, height, tw, th, geometry, appearance, opacities, primitive_ids, backgrounds,
-        point_list, r, w.order, w.tile_last, state, contributors, grads, near_plane,
-        far_plane, grad_geometry, grad_appearance, grad_opacities, grad_backgrounds);
+    if (replay) launch(render_backward_kernel<true, true>);
+    else launch(render_backward_kernel<true, false>);
   } else {
-    render_backward_kernel<false><<<unsigned(tiles), kTilePixels, 0, s>>>(
-        width, height, tw, th, geometry, appearance, opacities, primitive_ids, backgrounds,
-        point_list, r, w.order, w.tile_last, state, contributors, grads, near_plane,
-        far_plane, grad_geometry, grad_appearance, grad_opacities, grad_backgrounds);
+    if (replay) launch(render_backward_kernel<false, true>);
+    else launch(render_backward_kernel<false, false>);
   }
   GS_LAUNCHED("render_backward_kernel");
   return GS_OK;

@@ -54,18 +54,22 @@ class Composite(torch.autograd.Function):
             ctx.accumulators = _native.zero_accumulators(geometry, appearance, opacities,
                                                          backgrounds)
 
-        overlap = clear_accumulators if any(ctx.needs_input_grad) else None
-        _, points, ranges, state, contributors = _native.rasterize_forward(
+        needs_grad = any(ctx.needs_input_grad)
+        overlap = clear_accumulators if needs_grad else None
+        _, points, ranges, state, contributors, *replay = _native.rasterize_forward(
             geometry, appearance, opacities, primitive_ids, image_ids, radii, backgrounds,
             width, height, neural, near_plane, far_plane, outputs=outputs, overlap=overlap,
             capacity=None if bounded is None else bounded.max_intersections,
-            flags=None if bounded is None else bounded._overflows,
+            flags=None if bounded is None else bounded._overflows, replay=needs_grad,
         )
+        replay = replay[0] if replay else None
         # Binning and early termination are discrete: only the saved sorted
-        # lists and per-pixel state are needed to replay the tiles backwards.
+        # lists, per-pixel state and the tiles' replay lists (the records some
+        # pixel took) are needed to replay the tiles backwards.
+        lists, counts = replay if replay is not None else (None, None)
         ctx.save_for_backward(
             geometry, appearance, opacities, primitive_ids, backgrounds, points, ranges, state,
-            contributors,
+            contributors, lists, counts,
         )
         ctx.options = (width, height, neural, near_plane, far_plane)
         ctx.set_materialize_grads(False)
@@ -76,8 +80,10 @@ class Composite(torch.autograd.Function):
     def backward(ctx: Any, *grad_groups):
         # A second backward through a retained graph gets fresh accumulators.
         accumulators, ctx.accumulators = ctx.accumulators, None
+        *saved, lists, counts = ctx.saved_tensors
         gg, ga, go, gb = _native.rasterize_backward(
-            *ctx.saved_tensors, list(grad_groups), *ctx.options, accumulators=accumulators
+            *saved, list(grad_groups), *ctx.options, accumulators=accumulators,
+            replay=None if lists is None else (lists, counts),
         )
         return gg, gg[:, 9:11], ga, go, None, None, None, gb, None, None, None, None, None, None
 

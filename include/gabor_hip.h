@@ -306,23 +306,37 @@ size_t gs_render_workspace_size(int64_t images, int32_t width, int32_t height);
  * caller's loss are passed the same way, without copies. */
 #define GS_MAP_GROUPS 5
 
+/* Replay lists (an addition; the reference has none): when replay and
+ * replay_counts are non-null, the forward also writes, for every tile, the
+ * point-list entries that at least one of its pixels composited, in list
+ * order, into replay [replay_capacity, 2] int32 at the tile's range start:
+ * {pair index, position in the tile's list | quadrant bits << 28}, where
+ * bit 28 + q is set when a pixel of 8x8 quadrant q (q = 2 * (y >= 8) +
+ * (x >= 8) within the tile) took the record; replay_counts [I*tw*th] int32
+ * receives each list's length. replay_capacity is the point list's length
+ * and must be below 2^28. Null pointers skip them. */
 int gs_render_forward(int32_t neural, const float* geometry, const float* appearance,
                       const float* opacities, const int64_t* primitive_ids,
                       const float* backgrounds, const int32_t* point_list,
                       const int32_t* ranges, int64_t images, int32_t width, int32_t height,
                       float near_plane, float far_plane, float* const* maps,
                       const int64_t* map_strides, float* state, int32_t* contributors,
+                      int32_t* replay, int64_t replay_capacity, int32_t* replay_counts,
                       void* workspace, size_t workspace_bytes, void* stream);
 
 /* Gradients are ACCUMULATED (global float atomics) into grad_geometry
  * [Q,17], grad_appearance [P,A], grad_opacities [P], grad_backgrounds
  * [I,3]; the caller zero-initialises them. grad_maps uses the channel-group
- * form above; a null group pointer means a zero gradient for that group. */
+ * form above; a null group pointer means a zero gradient for that group.
+ * replay / replay_counts: the forward's replay lists, or both null; with
+ * them the backward replays only the records some pixel took (the same
+ * gradients: the other records contribute exact zeros). */
 int gs_render_backward(int32_t neural, const float* geometry, const float* appearance,
                        const float* opacities, const int64_t* primitive_ids,
                        const float* backgrounds, const int32_t* point_list,
                        const int32_t* ranges, const float* state,
-                       const int32_t* contributors, const float* const* grad_maps,
+                       const int32_t* contributors, const int32_t* replay,
+                       const int32_t* replay_counts, const float* const* grad_maps,
                        const int64_t* grad_map_strides, int64_t images,
                        int32_t width, int32_t height, float near_plane, float far_plane,
                        float* grad_geometry, float* grad_appearance, float* grad_opacities,

@@ -48,7 +48,8 @@ def appearance_color(a: torch.Tensor, s: torch.Tensor, dirs: torch.Tensor, neura
 
 
 def composite(geometry, appearance, opacities, primitive_ids, image_ids, radii, backgrounds,
-              width, height, neural, near_plane, far_plane, lists=None, margins=None):
+              width, height, neural, near_plane, far_plane, lists=None, margins=None,
+              taken=None):
     """Differentiable forward compositor.
 
     Returns maps [I,H,W,9], point_list (np.int32), ranges (np.int32 [tiles,2]),
@@ -58,6 +59,10 @@ def composite(geometry, appearance, opacities, primitive_ids, image_ids, radii, 
     relative distance, over the samples a pixel evaluated, of any discrete
     decision from its threshold (alpha vs 1/255, T(1-alpha) vs 1e-4, the
     surface/screen branch rho3 vs rho2, depth vs near, p.z vs 0).
+    If ``taken`` is a dict, taken["quadrants"] receives np.int64 [tiles,
+    longest]: for the k-th record of each tile's list, bit q is set when a
+    pixel of the tile's 8x8 quadrant q = 2 * (y >= 8) + (x >= 8) took it
+    (contributed to its maps, rasterize.cu:254-271).
     """
     dtype = geometry.dtype
     images = backgrounds.shape[0]
@@ -96,6 +101,8 @@ def composite(geometry, appearance, opacities, primitive_ids, image_ids, radii, 
     done = ~inside
     last = torch.zeros(tiles, TILE * TILE, dtype=torch.int64)
     margin = torch.full((tiles, TILE * TILE), math.inf, dtype=torch.float64)
+    quadrant_bit = 1 << (2 * ((offs // TILE) >= 8).long() + ((offs % TILE) >= 8).long())
+    quadrants = np.zeros((tiles, max(longest, 1)), dtype=np.int64)
     mscale = far_plane / (far_plane - near_plane)
     for k in range(longest):
         rec = table[:, k]
@@ -139,6 +146,10 @@ def composite(geometry, appearance, opacities, primitive_ids, image_ids, radii, 
         stop = accept & (T * (1 - alpha) < 1e-4)
         done = done | stop
         take = accept & ~stop
+        if taken is not None:
+            bits = torch.where(take & inside, quadrant_bit, torch.zeros_like(quadrant_bit))
+            for q in range(4):
+                quadrants[:, k] |= ((bits & (1 << q)).amax(1) > 0).numpy().astype(np.int64) << q
         a_take = torch.where(take, alpha, torch.zeros_like(alpha))
         s_take = torch.where(take[..., None], s, torch.zeros_like(s))
         z_take = torch.where(take, depth, torch.ones_like(depth))
@@ -172,4 +183,6 @@ def composite(geometry, appearance, opacities, primitive_ids, image_ids, radii, 
     contributors = last.reshape(-1)[keep][order].reshape(images, height, width)
     if margins is not None:
         margins["pixels"] = margin.reshape(-1)[keep][order].reshape(images, height, width)
+    if taken is not None:
+        taken["quadrants"] = quadrants
     return maps, point_list, ranges, state, contributors.numpy().astype(np.int32)

@@ -37,7 +37,7 @@ def test_library_exports_every_declared_symbol():
     for name in sorted(declared_symbols()):
         assert hasattr(library, name), name
     assert set(_native.exported_symbols()) == declared_symbols()
-    assert _native.lib.gs_abi_version() == 5
+    assert _native.lib.gs_abi_version() == 6
 
 
 def test_argument_errors_return_status_and_message():
@@ -52,7 +52,8 @@ def test_argument_errors_return_status_and_message():
     assert status == 1 and b"degree" in lib.gs_last_error()
     status = lib.gs_find_ranges(None, -1, None, 4, None)
     assert status == 2
-    status = lib.gs_render_forward(0, *([None] * 7), 1, 16, 16, 1.0, 0.5, *([None] * 5), 0, None)
+    status = lib.gs_render_forward(0, *([None] * 7), 1, 16, 16, 1.0, 0.5, *([None] * 5), 0,
+                                   None, None, 0, None)
     assert status == 1 and b"clipping" in lib.gs_last_error()
     # Workspace smaller than required is rejected before any launch.
     need = lib.gs_scan_workspace_size(1000)

@@ -57,7 +57,7 @@ def capture_forward(function, values, opts):
         captured["args"] = args
         out = original(*args, **kwargs)
         maps = out[0] if isinstance(out[0], torch.Tensor) else torch.cat(out[0], -1)
-        captured["out"] = [maps, *out[1:]]
+        captured["out"] = [maps, *out[1:5]]
         return out
 
     _native.rasterize_forward = spy

@@ -161,3 +161,74 @@ def test_empty_and_invisible_scenes_are_background():
         torch.testing.assert_close(maps[..., :3], values["backgrounds"][:, :, None, None, :].expand(1, 2, 9, 9, 3))
         assert maps[..., 3].count_nonzero() == 0
         assert len(aux["point_list"]) == 0
+
+
+def _tile_quadrant_last(contributors, width, height):
+    """Largest contributor count of every (tile, 8x8 quadrant): [tiles, 4]."""
+    images = contributors.shape[0]
+    tw, th = (width + 15) // 16, (height + 15) // 16
+    out = np.zeros((images * tw * th, 4), dtype=np.int64)
+    for image in range(images):
+        for py in range(height):
+            for px in range(width):
+                tile = (image * th + py // 16) * tw + px // 16
+                q = 2 * ((py % 16) >= 8) + ((px % 16) >= 8)
+                out[tile, q] = max(out[tile, q], int(contributors[image, py, px]))
+    return out
+
+
+@pytest.mark.parametrize("method", ["classic", "neural"])
+def test_taken_quadrants_agree_with_contributors(method):
+    from scenes import random_scene
+
+    values = random_scene(method, cameras=2, n=48, width=40, height=24, seed=3)
+    backgrounds = values.pop("backgrounds")
+    taken = {}
+    _, _, aux = RENDER[method](**values, width=40, height=24, backgrounds=backgrounds,
+                               taken=taken)
+    quadrants = taken["quadrants"]
+    contributors = aux["contributors"].reshape(-1, 24, 40)
+    lengths = aux["ranges"][:, 1] - aux["ranges"][:, 0]
+    # Each pixel's last contributor was taken in its quadrant.
+    tw = 3
+    for image in range(contributors.shape[0]):
+        for py in range(24):
+            for px in range(40):
+                c = int(contributors[image, py, px])
+                if c:
+                    tile = (image * 2 + py // 16) * tw + px // 16
+                    q = 2 * ((py % 16) >= 8) + ((px % 16) >= 8)
+                    assert quadrants[tile, c - 1] >> q & 1
+    # A record taken in quadrant q lies within some pixel's contributors there,
+    # and records beyond a tile's list are never taken.
+    last = _tile_quadrant_last(contributors, 40, 24)
+    tiles, longest = quadrants.shape
+    position = np.arange(longest)
+    for q in range(4):
+        bit = (quadrants >> q) & 1
+        assert not np.any(bit & (position[None, :] >= last[:, q:q + 1]))
+    assert not np.any(quadrants & (position[None, :] >= lengths[:, None]))
+    assert np.count_nonzero(quadrants) > 20
+
+
+def test_taken_quadrants_closed_form():
+    """One fronto-parallel surfel in a 16x16 image: a small one near pixel
+    (3, 12) is taken only in quadrant 2 (x < 8, y >= 8); a large centred one
+    in all four."""
+    base = make_inputs("classic", scenes=1, cameras=1, primitives=1)
+    base["quaternions"].zero_()
+    base["quaternions"][..., 0] = 1
+    base["intrinsics"][..., 0, 0] = 20.0
+    base["intrinsics"][..., 1, 1] = 20.0
+    base["intrinsics"][..., 0, 2] = 7.5
+    base["intrinsics"][..., 1, 2] = 7.5
+    base["opacities"].fill_(0.8)
+    for (px, py, scale), expected in (((3.0, 12.0, 0.01), 0b0100), ((7.5, 7.5, 0.3), 0b1111)):
+        values = dict(base)
+        z = 3.0
+        values["means"] = torch.tensor([[[(px - 7.5) * z / 20.0, (py - 7.5) * z / 20.0, z]]])
+        values["scales"] = torch.full((1, 1, 2), scale)
+        backgrounds = values.pop("backgrounds")
+        taken = {}
+        RENDER["classic"](**values, width=16, height=16, backgrounds=backgrounds, taken=taken)
+        assert taken["quadrants"].tolist() == [[expected]]
