@@ -144,24 +144,23 @@ def _loss(rgb, alpha, meta, channels):
     ``torch.cat(maps, -1).square().mean()`` (benchmarks/
     benchmark_rasterization.py:80-82, 133).
 
-    Same value and gradient, less glue: the maps are flattened to
-    [pixels, k] before the concatenation (above four dimensions torch's cat
-    falls back to one strided copy per input, while 2-D inputs take its
-    single batched-copy kernel), groups past `channels` are left out rather
-    than sliced off (a slice adds a zero-filled full-size gradient), and the
-    mean of squares is mse_loss against zero, whose backward is one fused
-    kernel (2 x / n) where square().mean() runs pow, mul, mul and div over the
-    whole map.
+    Same value and gradient, less glue: a mean of squares does not depend on
+    the order of the elements, so the groups are concatenated flat - one
+    contiguous copy, where interleaving them into [pixels, 9] writes 4- to
+    12-byte pieces - and the backward hands each group a contiguous slice of
+    the gradient. Groups past `channels` are left out rather than sliced off
+    (a slice adds a zero-filled full-size gradient), and the mean of squares
+    is mse_loss against zero, whose backward is one fused kernel (2 x / n)
+    where square().mean() runs pow, mul, mul and div over the whole map.
     """
     flat, left = [], channels
     for t in (rgb, alpha, meta["accumulated_depth"], meta["normals"], meta["distortion"]):
         if left <= 0:
             break
         k = t.shape[-1]
-        t = t.reshape(-1, k)
-        flat.append(t if k <= left else t[:, :left])
+        flat.append((t if k <= left else t[..., :left]).reshape(-1))
         left -= k
-    maps = torch.cat(flat, -1) if len(flat) > 1 else flat[0]
+    maps = torch.cat(flat) if len(flat) > 1 else flat[0]
     return torch.nn.functional.mse_loss(maps, maps.new_zeros(()).expand_as(maps))
 
 

@@ -84,13 +84,13 @@ _SIGNATURES = {
     "gs_bin_order_workspace_size": (_c_size, [_c_i64]),
     "gs_bin_order": (
         _c_int,
-        [_c_ptr] * 3 + [_c_i64, _c_int, _c_int] + [_c_ptr] * 5 + [_c_size, _c_ptr],
+        [_c_ptr] * 3 + [_c_i64, _c_int, _c_int] + [_c_ptr] * 6 + [_c_size, _c_ptr],
     ),
     "gs_bin_tiles_workspace_size": (_c_size, [_c_i64]),
     "gs_bin_tiles": (
         _c_int,
-        [_c_ptr] * 3 + [_c_i64, _c_i64, _c_i64, _c_int, _c_int, _c_ptr, _c_ptr, _c_ptr, _c_size,
-                        _c_ptr],
+        [_c_ptr] * 3 + [_c_i64, _c_i64, _c_i64, _c_i64, _c_int, _c_int, _c_ptr, _c_ptr, _c_ptr,
+                        _c_size, _c_ptr],
     ),
     "gs_bin_tiles_bounded": (
         _c_int,
@@ -307,29 +307,31 @@ def find_ranges(sorted_keys: torch.Tensor, tiles: int) -> torch.Tensor:
 def bin_order(geometry: torch.Tensor, radii: torch.Tensor, image_ids: torch.Tensor,
               width: int, height: int):
     """Depth-first binning, stage 1: (order int32 [Q], starts int64 [Q], rects
-    int32 [Q, 4], intersections int64 [1] on the device). No host
-    synchronisation."""
+    int32 [Q, 4], totals int64 [2] on the device = (M, V): the intersection
+    count and the number of pairs with tiles). No host synchronisation."""
     device = geometry.device
     count = geometry.size(0)
     order = torch.empty(count, dtype=torch.int32, device=device)
     starts = torch.empty(count, dtype=torch.int64, device=device)
     rects = torch.empty((count, 4), dtype=torch.int32, device=device)
-    total = torch.empty(1, dtype=torch.int64, device=device)
+    totals = torch.empty(2, dtype=torch.int64, device=device)
     workspace = _workspace(lib.gs_bin_order_workspace_size(count), device)
     _check(
         lib.gs_bin_order(
             _ptr(geometry), _ptr(radii), _ptr(image_ids), count, width, height, _ptr(order),
-            _ptr(starts), _ptr(rects), _ptr(total), _ptr(workspace), workspace.numel(),
-            _stream(device),
+            _ptr(starts), _ptr(rects), _ptr(totals), _ptr(totals[1:]), _ptr(workspace),
+            workspace.numel(), _stream(device),
         )
     )
-    return order, starts, rects, total
+    return order, starts, rects, totals
 
 
-def bin_tiles(order, starts, rects, images, width, height, intersections):
+def bin_tiles(order, starts, rects, images, width, height, intersections, visible=-1):
     """Depth-first binning, stage 2: (point_list int32 [M], ranges int32
     [I*tw*th, 2]), the result of emit_tiles + sort_pairs + find_ranges
-    (rasterize.cu:43-69, 470-501)."""
+    (rasterize.cu:43-69, 470-501). ``visible`` is stage 1's count of pairs
+    with tiles (-1: unknown), which selects the packed-key tile sort when it
+    fits."""
     device = order.device
     count = order.size(0)
     tw, th = tile_grid(width, height)
@@ -338,8 +340,9 @@ def bin_tiles(order, starts, rects, images, width, height, intersections):
     workspace = _workspace(lib.gs_bin_tiles_workspace_size(intersections), device)
     _check(
         lib.gs_bin_tiles(
-            _ptr(order), _ptr(starts), _ptr(rects), count, intersections, images, width, height,
-            _ptr(point_list), _ptr(ranges), _ptr(workspace), workspace.numel(), _stream(device),
+            _ptr(order), _ptr(starts), _ptr(rects), count, intersections, visible, images, width,
+            height, _ptr(point_list), _ptr(ranges), _ptr(workspace), workspace.numel(),
+            _stream(device),
         )
     )
     return point_list, ranges
@@ -378,7 +381,8 @@ def bin_depth_first(geometry, radii, image_ids, images, width, height, overlap=N
     With ``capacity`` there is no synchronisation at all: the point list
     has that many entries, and (overflow flag, live count M) of
     bin_tiles_bounded are appended to ``flags``."""
-    order, starts, rects, total = bin_order(geometry, radii, image_ids, width, height)
+    order, starts, rects, totals = bin_order(geometry, radii, image_ids, width, height)
+    total = totals[:1]
     if capacity is not None:
         if overlap is not None:
             overlap()
@@ -389,16 +393,16 @@ def bin_depth_first(geometry, radii, image_ids, images, width, height, overlap=N
             flags.append((overflow, total))
         return point_list, ranges
     stream = torch.cuda.current_stream(geometry.device)
-    host = torch.empty(1, dtype=torch.int64, pin_memory=True)
-    host.copy_(total, non_blocking=True)
+    host = torch.empty(2, dtype=torch.int64, pin_memory=True)
+    host.copy_(totals, non_blocking=True)
     ready = torch.cuda.Event()
     ready.record(stream)
     if overlap is not None:
         overlap()
     ready.synchronize()
-    intersections = int(host[0])
+    intersections, visible = int(host[0]), int(host[1])
     check_intersections(intersections)
-    return bin_tiles(order, starts, rects, images, width, height, intersections)
+    return bin_tiles(order, starts, rects, images, width, height, intersections, visible)
 
 
 def pack_visible(radii: torch.Tensor, with_rows: bool = False):

@@ -183,14 +183,27 @@ struct SortedCountLoad {
   __device__ int64_t operator()(int64_t j) const { return counts[order[j]]; }
 };
 
-// starts[j] = entries of all lower depth ranks; the total is M.
+// starts[j] = entries of all lower depth ranks; the total is M. Pairs with
+// tiles come first in depth order (the others carry the largest key), so
+// the one rank j whose pair has tiles and whose successor has none (or rank
+// 0 when no pair has tiles) also records their number V in `visible`.
 struct ExclusiveStartStore {
   int64_t* starts;
   int64_t* total;
+  int64_t* visible;  // may be null
+  const int* counts;
+  const int* order;
   int64_t count;
   __device__ void operator()(int64_t j, int64_t inclusive, int64_t v) const {
     starts[j] = inclusive - v;
     if (j == count - 1) *total = inclusive;
+    if (visible) {
+      if (v > 0) {
+        if (j == count - 1 || counts[order[j + 1]] == 0) *visible = j + 1;
+      } else if (j == 0) {
+        *visible = 0;
+      }
+    }
   }
 };
 
@@ -206,10 +219,15 @@ constexpr int kLaneTiles = 32;
 // `m` is the capacity of tile_ids/values; `total` (a device int64, or null
 // when it equals m) the emission's full length, which may exceed it: entries
 // past the capacity are dropped and `overflow` (if given) is set.
+// Packed: instead of (tile id, pair index) pairs, write one 32-bit key
+// tile id << rank_bits | depth rank per entry (the caller has checked that
+// both fit), so that the tile sort moves keys only; values is unused.
+template <bool Packed>
 __global__ __launch_bounds__(256) void emit_sorted_kernel(
     int64_t count, int64_t m, const int64_t* __restrict__ total_count, uint32_t* overflow,
     int tw, const int* __restrict__ order, const int64_t* __restrict__ starts,
-    const int4* __restrict__ rects, uint32_t* __restrict__ tile_ids, int* __restrict__ values) {
+    const int4* __restrict__ rects, uint32_t* __restrict__ tile_ids, int* __restrict__ values,
+    int rank_bits) {
   const int lane = __lane_id();
   const int64_t j = int64_t(blockIdx.x) * 256 + threadIdx.x;
   if (j - lane >= count) return;  // uniform per wave
@@ -225,13 +243,20 @@ __global__ __launch_bounds__(256) void emit_sorted_kernel(
     area = int(min<int64_t>(next - first, INT_MAX));
     if (area > 0) rect = rects[pair];
   }
+  // Packed entries carry the depth rank j in their low bits.
+  const uint32_t low = uint32_t(j);
   if (area <= kLaneTiles) {
     int x = rect.x, y = rect.y;
     for (int k = 0; k < area; ++k) {
       const int64_t e = first + k;
       if (e < m) {
-        tile_ids[e] = uint32_t(rect.w) + uint32_t(y * tw + x);
-        values[e] = pair;
+        const uint32_t tile = uint32_t(rect.w) + uint32_t(y * tw + x);
+        if constexpr (Packed) {
+          tile_ids[e] = (tile << rank_bits) | low;
+        } else {
+          tile_ids[e] = tile;
+          values[e] = pair;
+        }
       }
       if (++x == rect.x + rect.z) {
         x = rect.x;
@@ -250,31 +275,46 @@ __global__ __launch_bounds__(256) void emit_sorted_kernel(
     const int owner_span = __shfl(rect.z, owner);
     const uint32_t owner_base = uint32_t(__shfl(rect.w, owner));
     const int owner_pair = __shfl(pair, owner);
+    const uint32_t owner_low = uint32_t(__shfl(int(low), owner));
     for (int k = lane; k < owner_area; k += 64) {
       const int64_t e = owner_first + k;
       if (e < m) {
-        tile_ids[e] = owner_base + uint32_t((owner_y0 + k / owner_span) * tw + owner_x0 +
-                                            k % owner_span);
-        values[e] = owner_pair;
+        const uint32_t tile = owner_base + uint32_t((owner_y0 + k / owner_span) * tw + owner_x0 +
+                                                    k % owner_span);
+        if constexpr (Packed) {
+          tile_ids[e] = (tile << rank_bits) | owner_low;
+        } else {
+          tile_ids[e] = tile;
+          values[e] = owner_pair;
+        }
       }
     }
   }
 }
 
+// Tile ranges from the tile-sorted entries. Packed: the entries are
+// tile id << rank_bits | depth rank keys, and this pass also writes the
+// point list, point_list[i] = order[rank].
+template <bool Packed>
 __global__ __launch_bounds__(256) void find_tile_ranges_kernel(int64_t capacity,
                                                                const int64_t* __restrict__ live,
                                                                int64_t tiles,
                                                                const uint32_t* __restrict__ ids,
-                                                               int2* __restrict__ ranges) {
+                                                               int2* __restrict__ ranges,
+                                                               int rank_bits,
+                                                               const int* __restrict__ order,
+                                                               int* __restrict__ point_list) {
   const int64_t m = live ? min(capacity, max(*live, int64_t(0))) : capacity;
   const int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x;
   if (i >= m) return;
-  const uint32_t tile = ids[i];
+  const uint32_t key = ids[i];
+  const uint32_t tile = Packed ? key >> rank_bits : key;
+  if constexpr (Packed) point_list[i] = order[key & ((1u << rank_bits) - 1u)];
   const bool own = tile < uint64_t(tiles);
   if (i == 0) {
     if (own) ranges[tile].x = 0;
   } else {
-    const uint32_t previous = ids[i - 1];
+    const uint32_t previous = Packed ? ids[i - 1] >> rank_bits : ids[i - 1];
     if (tile != previous) {
       if (previous < uint64_t(tiles)) ranges[previous].y = int(i);
       if (own) ranges[tile].x = int(i);
@@ -440,7 +480,7 @@ size_t gs_bin_order_workspace_size(int64_t count) {
 
 int gs_bin_order(const float* geometry, const int32_t* radii, const int64_t* image_ids,
                  int64_t count, int32_t width, int32_t height, int32_t* order, int64_t* starts,
-                 int32_t* rects, int64_t* intersections, void* workspace,
+                 int32_t* rects, int64_t* intersections, int64_t* visible, void* workspace,
                  size_t workspace_bytes, void* stream) {
   using namespace gs;
   clear_error();
@@ -451,6 +491,10 @@ int gs_bin_order(const float* geometry, const int32_t* radii, const int64_t* ima
   if (count == 0) {
     zero_count_kernel<<<1, 64, 0, s>>>(intersections);
     GS_LAUNCHED("zero_count_kernel");
+    if (visible) {
+      zero_count_kernel<<<1, 64, 0, s>>>(visible);
+      GS_LAUNCHED("zero_count_kernel");
+    }
     return GS_OK;
   }
   GS_REQUIRE(geometry && radii && image_ids && order && starts && rects, GS_ERR_ARGUMENT,
@@ -474,7 +518,9 @@ int gs_bin_order(const float* geometry, const int32_t* radii, const int64_t* ima
   }
   ProfileScope prof(GS_PROF_BINNING, s);
   return run_scan<int64_t>(count, SortedCountLoad{w.counts, order},
-                           ExclusiveStartStore{starts, intersections, count}, w.scan_sums, s);
+                           ExclusiveStartStore{starts, intersections, visible, w.counts, order,
+                                               count},
+                           w.scan_sums, s);
 }
 
 size_t gs_bin_tiles_workspace_size(int64_t m) {
@@ -489,10 +535,14 @@ namespace {
 
 // Shared by gs_bin_tiles (m known on the host) and gs_bin_tiles_bounded (m
 // a capacity, the live length in `live` on the device).
+// `visible`: the number of pairs with tiles (stage 1's V), or -1 when only
+// the device knows it. Pairs with tiles hold depth ranks below V (below
+// count when V is unknown); when those ranks and the tile ids fit in 32 bits
+// together, the entries travel as packed keys (emit_sorted_kernel<true>).
 int bin_tiles(const int32_t* order, const int64_t* starts, const int32_t* rects, int64_t count,
               int64_t m, const int64_t* live, uint32_t* overflow, int64_t images, int32_t width,
-              int32_t height, int32_t* point_list, int32_t* ranges, void* workspace,
-              size_t workspace_bytes, hipStream_t s) {
+              int32_t height, int32_t* point_list, int32_t* ranges, int64_t visible,
+              void* workspace, size_t workspace_bytes, hipStream_t s) {
   GS_REQUIRE(count >= 0 && count <= INT_MAX, GS_ERR_OVERFLOW, "too many projected primitives");
   GS_REQUIRE(m >= 0 && m <= INT_MAX, GS_ERR_OVERFLOW, "tile intersection count exceeds int32");
   GS_REQUIRE(width > 0 && height > 0 && images >= 0, GS_ERR_ARGUMENT,
@@ -511,6 +561,10 @@ int bin_tiles(const int32_t* order, const int64_t* starts, const int32_t* rects,
              "binning needs %zu workspace bytes, got %zu", need, workspace_bytes);
   int2* r = reinterpret_cast<int2*>(ranges);
   TilesWorkspace w = tiles_layout(workspace, m);
+  const int tile_bits = id_bits(tiles);
+  const int rank_bits = id_bits(visible >= 0 ? min(visible, count) : count);
+  const bool packed = tile_bits + rank_bits <= 32;
+  const int4* rect_rows = reinterpret_cast<const int4*>(rects);
   {
     ProfileScope prof(GS_PROF_BINNING, s);
     fill_ranges_kernel<<<unsigned(ceil_div(tiles, 256)), 256, 0, s>>>(tiles, r);
@@ -518,27 +572,40 @@ int bin_tiles(const int32_t* order, const int64_t* starts, const int32_t* rects,
     if (count == 0 || (m == 0 && !live)) return GS_OK;
     GS_REQUIRE(order && starts && rects, GS_ERR_ARGUMENT, "null pointer passed to gs_bin_tiles");
     if (m == 0) {  // a zero capacity still reports an overflowing emission
-      emit_sorted_kernel<<<unsigned(ceil_div(count, 256)), 256, 0, s>>>(
-          count, 0, live, overflow, tw, order, starts, reinterpret_cast<const int4*>(rects),
-          nullptr, nullptr);
+      emit_sorted_kernel<false><<<unsigned(ceil_div(count, 256)), 256, 0, s>>>(
+          count, 0, live, overflow, tw, order, starts, rect_rows, nullptr, nullptr, 0);
       GS_LAUNCHED("emit_sorted_kernel");
       return GS_OK;
     }
     GS_REQUIRE(point_list, GS_ERR_ARGUMENT, "null point list");
-    emit_sorted_kernel<<<unsigned(ceil_div(count, 256)), 256, 0, s>>>(
-        count, m, live, overflow, tw, order, starts, reinterpret_cast<const int4*>(rects),
-        w.tile_ids, w.tile_values);
+    if (packed) {
+      emit_sorted_kernel<true><<<unsigned(ceil_div(count, 256)), 256, 0, s>>>(
+          count, m, live, overflow, tw, order, starts, rect_rows, w.tile_ids, nullptr,
+          rank_bits);
+    } else {
+      emit_sorted_kernel<false><<<unsigned(ceil_div(count, 256)), 256, 0, s>>>(
+          count, m, live, overflow, tw, order, starts, rect_rows, w.tile_ids, w.tile_values, 0);
+    }
     GS_LAUNCHED("emit_sorted_kernel");
   }
   {
     ProfileScope prof(GS_PROF_SORT, s);
-    int status = radix_sort<uint32_t>(w.tile_ids, w.tile_sorted, w.tile_values, point_list, m,
-                                      0, id_bits(tiles), w.sort, s, live);
+    // Stable on the tile bits: entries of a tile keep their depth order.
+    const int status =
+        packed ? radix_sort<uint32_t>(w.tile_ids, w.tile_sorted, nullptr, nullptr, m, rank_bits,
+                                      rank_bits + tile_bits, w.sort, s, live)
+               : radix_sort<uint32_t>(w.tile_ids, w.tile_sorted, w.tile_values, point_list, m, 0,
+                                      tile_bits, w.sort, s, live);
     if (status != GS_OK) return status;
   }
   ProfileScope prof(GS_PROF_BINNING, s);
-  find_tile_ranges_kernel<<<unsigned(ceil_div(m, 256)), 256, 0, s>>>(m, live, tiles,
-                                                                     w.tile_sorted, r);
+  if (packed) {
+    find_tile_ranges_kernel<true><<<unsigned(ceil_div(m, 256)), 256, 0, s>>>(
+        m, live, tiles, w.tile_sorted, r, rank_bits, order, point_list);
+  } else {
+    find_tile_ranges_kernel<false><<<unsigned(ceil_div(m, 256)), 256, 0, s>>>(
+        m, live, tiles, w.tile_sorted, r, 0, nullptr, nullptr);
+  }
   GS_LAUNCHED("find_tile_ranges_kernel");
   return GS_OK;
 }
@@ -549,12 +616,12 @@ int bin_tiles(const int32_t* order, const int64_t* starts, const int32_t* rects,
 extern "C" {
 
 int gs_bin_tiles(const int32_t* order, const int64_t* starts, const int32_t* rects,
-                 int64_t count, int64_t m, int64_t images, int32_t width, int32_t height,
-                 int32_t* point_list, int32_t* ranges, void* workspace, size_t workspace_bytes,
-                 void* stream) {
+                 int64_t count, int64_t m, int64_t visible, int64_t images, int32_t width,
+                 int32_t height, int32_t* point_list, int32_t* ranges, void* workspace,
+                 size_t workspace_bytes, void* stream) {
   gs::clear_error();
   return gs::bin_tiles(order, starts, rects, count, m, nullptr, nullptr, images, width, height,
-                       point_list, ranges, workspace, workspace_bytes,
+                       point_list, ranges, visible, workspace, workspace_bytes,
                        static_cast<hipStream_t>(stream));
 }
 
@@ -567,7 +634,7 @@ int gs_bin_tiles_bounded(const int32_t* order, const int64_t* starts, const int3
   GS_REQUIRE(intersections && overflow, GS_ERR_ARGUMENT,
              "bounded binning needs the device intersection count and an overflow flag");
   return gs::bin_tiles(order, starts, rects, count, capacity, intersections, overflow, images,
-                       width, height, point_list, ranges, workspace, workspace_bytes,
+                       width, height, point_list, ranges, -1, workspace, workspace_bytes,
                        static_cast<hipStream_t>(stream));
 }
 

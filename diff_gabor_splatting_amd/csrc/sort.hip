@@ -111,7 +111,9 @@ struct ExclusiveStore {
   }
 };
 
-template <typename Key, int Items>
+// Values: whether int32 values travel with the keys (a keys-only sort
+// passes null value arrays).
+template <typename Key, int Items, bool Values>
 __global__ __launch_bounds__(kSortBlock) void radix_downsweep_kernel(
     const Key* __restrict__ keys_in, const int* __restrict__ values_in,
     Key* __restrict__ keys_out, int* __restrict__ values_out, int64_t capacity,
@@ -125,7 +127,7 @@ __global__ __launch_bounds__(kSortBlock) void radix_downsweep_kernel(
   __shared__ uint32_t local_start[kBins];           // first local slot per digit
   __shared__ uint32_t global_start[kBins];          // first output slot per digit
   __shared__ Key stage_keys[kSortSpan];
-  __shared__ int stage_values[kSortSpan];
+  __shared__ int stage_values[Values ? kSortSpan : 1];
   const int lane = __lane_id(), wave = threadIdx.x >> 6;
   const uint32_t mask = (1u << bits) - 1u;
   for (int i = threadIdx.x; i < kSortWaves * kBins; i += kSortBlock) (&running[0][0])[i] = 0;
@@ -141,7 +143,7 @@ __global__ __launch_bounds__(kSortBlock) void radix_downsweep_kernel(
     const int64_t i = wave_base + int64_t(it) * 64 + lane;
     const bool valid = i < m;
     key[it] = valid ? keys_in[i] : Key(0);
-    value[it] = valid ? values_in[i] : 0;
+    value[it] = Values && valid ? values_in[i] : 0;
   }
   // Rank = keys of the same digit earlier in this wave's span: the group
   // leader reserves the group's slots with an LDS atomic that returns the
@@ -200,7 +202,7 @@ __global__ __launch_bounds__(kSortBlock) void radix_downsweep_kernel(
       const uint32_t slot = local_start[digit] + running[wave][digit] + rank[it];
       if (slot < uint32_t(kSortSpan)) {  // always true when ranking is consistent
         stage_keys[slot] = key[it];
-        stage_values[slot] = value[it];
+        if constexpr (Values) stage_values[slot] = value[it];
       }
     }
   }
@@ -213,7 +215,7 @@ __global__ __launch_bounds__(kSortBlock) void radix_downsweep_kernel(
     const int64_t dst = int64_t(global_start[digit]) + (slot - int64_t(local_start[digit]));
     if (dst >= 0 && dst < m) {  // always true when the histograms are consistent
       keys_out[dst] = k;
-      values_out[dst] = stage_values[slot];
+      if constexpr (Values) values_out[dst] = stage_values[slot];
     }
   }
 }
@@ -229,7 +231,7 @@ __global__ __launch_bounds__(256) void copy_pairs_kernel(const Key* __restrict__
   const int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x;
   if (i < m) {
     keys_out[i] = keys_in[i];
-    values_out[i] = values_in[i];
+    if (values_in) values_out[i] = values_in[i];
   }
 }
 
@@ -253,7 +255,7 @@ SortWorkspace layout(void* base, int64_t m, int key_bytes) {
   offset = align_up(offset + scan_workspace_bytes(count_items, 4), 256);
   w.keys_tmp = p + offset;
   offset = align_up(offset + size_t(m) * size_t(key_bytes), 256);
-  w.values_tmp = reinterpret_cast<int*>(p + offset);
+  w.values_tmp = reinterpret_cast<int*>(p + offset);  // unused by keys-only sorts
   offset = align_up(offset + size_t(m) * 4, 256);
   w.bytes = offset;
   return w;
@@ -293,7 +295,7 @@ int radix_sort(const Key* keys_in, Key* keys_out, const int* values_in, int* val
     const int bits = min(digit_bits, end_bit - shift);
     const bool to_output = ((passes - 1 - pass) % 2) == 0;
     Key* dst_k = to_output ? keys_out : static_cast<Key*>(w.keys_tmp);
-    int* dst_v = to_output ? values_out : w.values_tmp;
+    int* dst_v = values_in ? (to_output ? values_out : w.values_tmp) : nullptr;
     if (items == 8) {
       radix_upsweep_kernel<Key, 8><<<unsigned(spans), kSortBlock, 0, s>>>(
           src_k, m, live, shift, bits, w.counts, spans);
@@ -305,12 +307,16 @@ int radix_sort(const Key* keys_in, Key* keys_out, const int* values_in, int* val
     int status = run_scan<uint32_t>(int64_t(kBins) * spans, CountLoad{w.counts},
                                     ExclusiveStore{w.counts}, w.scan_sums, s);
     if (status != GS_OK) return status;
+    auto downsweep = [&](auto kernel) {
+      kernel<<<unsigned(spans), kSortBlock, 0, s>>>(src_k, src_v, dst_k, dst_v, m, live, shift,
+                                                    bits, w.counts, spans);
+    };
     if (items == 8) {
-      radix_downsweep_kernel<Key, 8><<<unsigned(spans), kSortBlock, 0, s>>>(
-          src_k, src_v, dst_k, dst_v, m, live, shift, bits, w.counts, spans);
+      if (values_in) downsweep(radix_downsweep_kernel<Key, 8, true>);
+      else downsweep(radix_downsweep_kernel<Key, 8, false>);
     } else {
-      radix_downsweep_kernel<Key, 16><<<unsigned(spans), kSortBlock, 0, s>>>(
-          src_k, src_v, dst_k, dst_v, m, live, shift, bits, w.counts, spans);
+      if (values_in) downsweep(radix_downsweep_kernel<Key, 16, true>);
+      else downsweep(radix_downsweep_kernel<Key, 16, false>);
     }
     GS_LAUNCHED("radix_downsweep_kernel");
     src_k = dst_k;

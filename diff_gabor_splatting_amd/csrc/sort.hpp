@@ -10,6 +10,7 @@ namespace gs {
 size_t radix_sort_workspace_bytes(int64_t m, int key_bytes);
 
 // Sorts on key bits [begin_bit, end_bit); Key is uint32_t or uint64_t.
+// Null values_in and values_out sort the keys alone.
 // Outputs must not alias inputs; the workspace is radix_sort_workspace_bytes.
 // With `live` (a device int64), only the first min(*live, m) pairs are
 // sorted; m is then the capacity the launches are sized for.

@@ -253,10 +253,11 @@ size_t gs_bin_order_workspace_size(int64_t count);
  * entry of rank j: entries of all lower ranks), rects [count, 4] int32
  * (x0, y0, width in tiles, image*tw*th, for stage 2) and *intersections
  * (one device int64) = M, the total that rasterize.cu:466-468 copies to the
- * host. */
+ * host. *visible (one device int64, or null) receives V, the number of
+ * pairs with tiles: they hold depth ranks 0..V-1. */
 int gs_bin_order(const float* geometry, const int32_t* radii, const int64_t* image_ids,
                  int64_t count, int32_t width, int32_t height, int32_t* order, int64_t* starts,
-                 int32_t* rects, int64_t* intersections, void* workspace,
+                 int32_t* rects, int64_t* intersections, int64_t* visible, void* workspace,
                  size_t workspace_bytes, void* stream);
 
 /* Scratch bytes for gs_bin_tiles over m intersections. */
@@ -264,11 +265,14 @@ size_t gs_bin_tiles_workspace_size(int64_t m);
 
 /* Stage 2 from stage 1's order, starts and rects: emit in depth order,
  * sort by tile id, find ranges. point_list [m] int32, ranges
- * [images*tw*th, 2] int32 ((0,0) for empty tiles). */
+ * [images*tw*th, 2] int32 ((0,0) for empty tiles). `visible` is stage 1's
+ * V, or -1 if unknown: when bits(tiles) + bits(V) <= 32 the entries are
+ * sorted as single 32-bit (tile id, depth rank) keys, otherwise as (tile
+ * id, pair index) pairs; the result is the same. */
 int gs_bin_tiles(const int32_t* order, const int64_t* starts, const int32_t* rects,
-                 int64_t count, int64_t m, int64_t images, int32_t width, int32_t height,
-                 int32_t* point_list, int32_t* ranges, void* workspace, size_t workspace_bytes,
-                 void* stream);
+                 int64_t count, int64_t m, int64_t visible, int64_t images, int32_t width,
+                 int32_t height, int32_t* point_list, int32_t* ranges, void* workspace,
+                 size_t workspace_bytes, void* stream);
 
 /* gs_bin_tiles without the host's intersection count, for callers that
  * cannot synchronise (HIP graph capture): the point list and workspace are

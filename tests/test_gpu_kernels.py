@@ -85,28 +85,37 @@ def test_binning_pipeline_is_bit_exact(native, seed, q, width, height, images):
 
 
 @pytest.mark.parametrize("seed, q, width, height, images, culled", [
-    (5, 3000, 64, 64, 1, True),         # every pair culled: m = 0
-    (6, 40_000, 1920, 1080, 40, False),  # 326,400 tiles: 19 id bits, three tile passes
-    (7, 300_000, 512, 512, 32, False),  # config-3-like: 32,768 tiles, 1e5+ equal depths
+    (5, 3000, 64, 64, 1, 1.0),          # every pair culled: m = 0
+    (6, 40_000, 1920, 1080, 40, 0.0),   # 326,400 tiles: 19 id bits, three tile passes
+    (7, 300_000, 512, 512, 32, 0.0),    # config-3-like: 32,768 tiles, 1e5+ equal depths
+    # 8,160 tiles (13 bits) and V < 2^19 visible pairs: packed 32-bit keys
+    # with the true V, (tile id, pair) pairs when V is unknown (2^21 pairs).
+    (8, 1_100_000, 1920, 1080, 1, 0.6),
 ])
 def test_depth_first_binning_is_bit_exact(native, seed, q, width, height, images, culled):
     geometry, radii, image_ids = random_geometry(seed, q, width, height, images)
-    if culled:
-        radii[:] = np.minimum(radii, 0)
+    radii[: int(culled * q)] = np.minimum(radii[: int(culled * q)], 0)
     if seed == 7:
         geometry[:, 8] = np.float32(3.5)  # all depths tie: order is by pair index
         geometry[::5, 8] = np.float32(2.0)
     g, r, ids = (torch.from_numpy(a).to(DEVICE) for a in (geometry, radii, image_ids))
     offsets = native.count_tiles(g, r, width, height)
     m = int(offsets[-1])
-    assert (m == 0) == culled
+    assert (m == 0) == (culled == 1.0)
+    counts = np.diff(np.concatenate([[0], offsets.cpu().numpy()]))
+    visible = int(np.count_nonzero(counts))
     _, ok_list, ok_ranges = oracle_binning.bin_pairs(geometry, radii, image_ids, images, width,
                                                      height)
-    order, starts, rects, total = native.bin_order(g, r, ids, width, height)
-    assert int(total) == m
-    point_list, ranges = native.bin_tiles(order, starts, rects, images, width, height, m)
-    np.testing.assert_array_equal(point_list.cpu().numpy(), ok_list)
-    np.testing.assert_array_equal(ranges.cpu().numpy(), ok_ranges)
+    order, starts, rects, totals = native.bin_order(g, r, ids, width, height)
+    assert totals.tolist() == [m, visible]
+    for known in (visible, -1):
+        point_list, ranges = native.bin_tiles(order, starts, rects, images, width, height, m,
+                                              known)
+        np.testing.assert_array_equal(point_list.cpu().numpy(), ok_list)
+        np.testing.assert_array_equal(ranges.cpu().numpy(), ok_ranges)
+    if seed == 8:
+        tile_bits = (images * 120 * 68 - 1).bit_length()
+        assert tile_bits + visible.bit_length() <= 32 < tile_bits + q.bit_length()
 
 
 def test_ranges_of_empty_list_are_zero(native):
