@@ -393,7 +393,7 @@ def workload_stats(values, renderer, options):
             rgb, alpha, meta = renderer(**values, **options)
         finally:
             _native.rasterize_forward = original
-    maps, point_list, ranges, state, contributors = captured["out"]
+    maps, point_list, ranges, state, contributors = captured["out"][:5]
     geometry, appearance = captured["args"][0], captured["args"][1]
     width, height = options["width"], options["height"]
     tw, th = _native.tile_grid(width, height)

@@ -40,6 +40,7 @@ class Composite(torch.autograd.Function):
     def forward(
         ctx: Any, geometry, projected_means, appearance, opacities, primitive_ids, image_ids,
         radii, backgrounds, width, height, neural, near_plane, far_plane, bounded=None,
+        grad_mode=True,
     ):
         images = backgrounds.size(0)
         outputs = tuple(
@@ -54,7 +55,10 @@ class Composite(torch.autograd.Function):
             ctx.accumulators = _native.zero_accumulators(geometry, appearance, opacities,
                                                          backgrounds)
 
-        needs_grad = any(ctx.needs_input_grad)
+        # A backward can follow only when the caller records gradients (the
+        # forward itself always runs without): only then are the backward's
+        # accumulators and the replay lists prepared.
+        needs_grad = grad_mode and any(ctx.needs_input_grad)
         overlap = clear_accumulators if needs_grad else None
         _, points, ranges, state, contributors, *replay = _native.rasterize_forward(
             geometry, appearance, opacities, primitive_ids, image_ids, radii, backgrounds,
@@ -85,7 +89,8 @@ class Composite(torch.autograd.Function):
             *saved, list(grad_groups), *ctx.options, accumulators=accumulators,
             replay=None if lists is None else (lists, counts),
         )
-        return gg, gg[:, 9:11], ga, go, None, None, None, gb, None, None, None, None, None, None
+        return (gg, gg[:, 9:11], ga, go, None, None, None, gb, None, None, None, None, None, None,
+                None)
 
 
 class ProjectRecords(torch.autograd.Function):
@@ -486,6 +491,7 @@ def render(
         near_plane,
         far_plane,
         bounded,
+        torch.is_grad_enabled(),
     )
     image_shape = batch + (cameras, height, width)
     meta = {

@@ -202,3 +202,32 @@ def test_empty_tiles_have_empty_lists():
     assert int(forward[5][1].sum()) == 0
     gg, ga, go, gb = backward_both(args, forward, seed=5)
     assert not gg.any() and not ga.any() and not go.any()
+
+
+@pytest.mark.parametrize("neural", [False, True])
+def test_lists_only_when_a_backward_can_follow(neural):
+    """Under torch.no_grad the renderer prepares no replay lists, even when
+    leaves that require gradients (the neural opacities) reach the
+    compositor directly; with gradients recorded it does."""
+    from diff_gabor_splatting_amd import _native
+
+    method = "neural" if neural else "classic"
+    values = random_scene(method, n=16, width=32, height=32, seed=6)
+    gpu = {k: v.to(DEVICE).requires_grad_() for k, v in values.items()}
+    requested = []
+    original = _native.rasterize_forward
+
+    def spy(*args, **kwargs):
+        requested.append(kwargs.get("replay", False))
+        return original(*args, **kwargs)
+
+    _native.rasterize_forward = spy
+    try:
+        with torch.no_grad():
+            renderer(neural)(**gpu, width=32, height=32)
+        rgb, _, _ = renderer(neural)(**gpu, width=32, height=32)
+    finally:
+        _native.rasterize_forward = original
+    assert requested == [False, True]
+    rgb.sum().backward()
+    assert gpu["opacities"].grad is not None
