@@ -179,10 +179,11 @@ __global__ __launch_bounds__(kProjectBlock) void records_forward_kernel(
 // pushed through the basis (coefficients), the shared weight / magnitude /
 // phase and opacity gradients; write per-pair direction gradients.
 //
-// One wave handles 64 consecutive surfels. Their coefficients (2 x 3K
-// floats each, contiguous across the wave) are read with coalesced loads
-// into LDS, rows of odd pitch so that every lane then reads its own surfel
-// without bank conflicts, and the coefficient gradients leave the same way.
+// One workgroup handles 64 consecutive surfels. Each colour set's
+// coefficients (3K floats per surfel, contiguous across the block) are read
+// with coalesced loads into LDS, rows of odd pitch so that every lane then
+// reads its own surfel without bank conflicts, and the coefficient
+// gradients leave the same way.
 // Surfels whose colour gradients are all zero in every camera (culled or
 // unseen) skip the coefficient load: their gradients are exactly zero.
 constexpr int kShBlock = 64;
@@ -258,8 +259,16 @@ __device__ __forceinline__ void unstage_rows(const float* lds, float* __restrict
 }
 
 // Vec: coefficient arrays and their gradients start on 16-byte boundaries.
+// A workgroup of two waves takes kShBlock surfels: wave `set` stages and
+// differentiates colour set `set` (first or second coefficients), so each
+// lane keeps one set's 3K gradients in registers rather than both - twice
+// the waves per CU for the same LDS. The two sets' direction gradients are
+// summed through LDS; wave 0 also writes the shared-parameter and opacity
+// gradients.
+constexpr int kShSets = 2;
+
 template <int Degree, bool Vec>
-__global__ __launch_bounds__(kShBlock) void sh_rows_backward_kernel(
+__global__ __launch_bounds__(kShBlock * kShSets) void sh_rows_backward_kernel(
     const float* __restrict__ sh_first, const float* __restrict__ sh_second, int64_t cameras,
     int64_t n, const int* __restrict__ row_of_pair, const float* __restrict__ geometry,
     const float* __restrict__ grad_rows, const float* __restrict__ grad_opacity_rows,
@@ -268,95 +277,129 @@ __global__ __launch_bounds__(kShBlock) void sh_rows_backward_kernel(
     float* __restrict__ grad_phases, float* __restrict__ grad_opacities,
     float* __restrict__ grad_directions) {
   constexpr int K = (Degree + 1) * (Degree + 1);
-  constexpr int KC = K * 3;           // floats per surfel and colour set
-  constexpr int PITCH = 2 * KC + 1;   // both sets, odd pitch
-  __shared__ float stage[kShBlock * PITCH];
+  constexpr int KC = K * 3;      // floats per surfel and colour set
+  constexpr int PITCH = KC + 1;  // odd pitch
+  __shared__ float stage[kShSets][kShBlock * PITCH];
   __shared__ int needs[kShBlock];
-  const int t = threadIdx.x;
+  __shared__ float set1_directions[kShBlock][3];
+  const int t = threadIdx.x & (kShBlock - 1);
+  const int set = threadIdx.x / kShBlock;  // uniform per wave
   const int64_t first = int64_t(blockIdx.x) * kShBlock;
   const int64_t scene = blockIdx.y;
   const int count = int(min<int64_t>(kShBlock, n - first));
   const int64_t i = first + t;
   const bool own = t < count;
   const int64_t surfel = scene * n + i;
-  // Pass 1: the colour gradients decide whether the coefficients matter.
-  bool any = false;
-  if (own) {
-    for (int64_t c = 0; c < cameras && !any; ++c) {
-      const int64_t pair = (scene * cameras + c) * n + i;
-      const int64_t row = row_of_pair ? int64_t(row_of_pair[pair]) : pair;
-      if (row < 0) continue;
-      const float* gr = grad_rows + row * kRow;
+  // Pass 1 (wave 0): the colour gradients decide whether the coefficients
+  // matter.
+  if (set == 0) {
+    bool any = false;
+    if (own) {
+      for (int64_t c = 0; c < cameras && !any; ++c) {
+        const int64_t pair = (scene * cameras + c) * n + i;
+        const int64_t row = row_of_pair ? int64_t(row_of_pair[pair]) : pair;
+        if (row < 0) continue;
+        const float* gr = grad_rows + row * kRow;
 #pragma unroll
-      for (int k = 0; k < 6; ++k) any |= gr[k] != 0.f;
+        for (int k = 0; k < 6; ++k) any |= gr[k] != 0.f;
+      }
     }
+    needs[t] = any;
   }
-  needs[t] = any;
   __syncthreads();
   const int64_t base = (scene * n + first) * KC;
-  stage_rows<KC, PITCH, Vec>(sh_first + base, stage, count, needs, t);
-  stage_rows<KC, PITCH, Vec>(sh_second + base, stage + KC, count, needs, t);
+  float* lds = stage[set];
+  stage_rows<KC, PITCH, Vec>((set ? sh_second : sh_first) + base, lds, count, needs, t);
   __syncthreads();
-  float* coef = stage + t * PITCH;  // coef[set * KC + k * 3 + ch]
-  float acc[2][KC];
+  const float* coef = lds + t * PITCH;  // coef[k * 3 + ch]
+  float acc[KC];
 #pragma unroll
-  for (int set = 0; set < 2; ++set)
-#pragma unroll
-    for (int k = 0; k < KC; ++k) acc[set][k] = 0.f;
+  for (int k = 0; k < KC; ++k) acc[k] = 0.f;
   float shared[12];
 #pragma unroll
   for (int k = 0; k < 12; ++k) shared[k] = 0.f;
   float g_opacity = 0.f;
-  for (int64_t c = 0; c < cameras && own; ++c) {
+  // Every thread runs every camera (the LDS exchange below needs both
+  // waves); lanes past `count` only take part in the barriers.
+  for (int64_t c = 0; c < cameras; ++c) {
+    // Read the coefficients from LDS where they are used, in every camera:
+    // hoisted out of the loop they would hold 3K registers throughout it.
+    asm volatile("" ::: "memory");
     const int64_t pair = (scene * cameras + c) * n + i;
-    const int64_t row = row_of_pair ? int64_t(row_of_pair[pair]) : pair;
-    if (row < 0) continue;
-    const float* gr = grad_rows + row * kRow;
+    int64_t row = -1;
+    if (own) row = row_of_pair ? int64_t(row_of_pair[pair]) : pair;
     float gd[3] = {0.f, 0.f, 0.f};
-    float g[6];
-    bool nonzero = false;
+    if (row >= 0) {
+      const float* gr = grad_rows + row * kRow;
+      float g[3];
+      bool nonzero = false;
 #pragma unroll
-    for (int k = 0; k < 6; ++k) {
-      g[k] = gr[k];
-      nonzero |= g[k] != 0.f;
-    }
-    if (nonzero) {
-      const float* d = geometry + row * kGeometry + 14;
-      float Y[K], dx[K], dy[K], dz[K];
-      sh_basis<Degree, true>(d[0], d[1], d[2], Y, dx, dy, dz);
-#pragma unroll
-      for (int set = 0; set < 2; ++set)
+      for (int ch = 0; ch < 3; ++ch) {
+        g[ch] = gr[set * 3 + ch];
+        nonzero |= g[ch] != 0.f;
+      }
+      if (nonzero) {
+        // Colours and coefficient gradients from the basis values; the
+        // direction gradient sum_k w_k grad(Y_k), w_k = sum_ch gc_ch coef_k,ch,
+        // from the basis derivatives afterwards, so that values and
+        // derivatives are not live together.
+        const float* d = geometry + row * kGeometry + 14;
+        float Y[K], w[K];
+        sh_basis<Degree, false>(d[0], d[1], d[2], Y, nullptr, nullptr, nullptr);
+        float gc[3];
 #pragma unroll
         for (int ch = 0; ch < 3; ++ch) {
           float raw = 0.5f;
 #pragma unroll
-          for (int k = 0; k < K; ++k) raw += Y[k] * coef[set * KC + k * 3 + ch];
-          const float gc = raw >= 0.f ? g[set * 3 + ch] : 0.f;
+          for (int k = 0; k < K; ++k) raw += Y[k] * coef[k * 3 + ch];
+          gc[ch] = raw >= 0.f ? g[ch] : 0.f;
+        }
+        // The coefficients are read from LDS again below rather than kept
+        // in registers across the clamp decisions.
+        asm volatile("" ::: "memory");
 #pragma unroll
-          for (int k = 0; k < K; ++k) {
-            const float cv = coef[set * KC + k * 3 + ch];
-            acc[set][k * 3 + ch] += gc * Y[k];
-            gd[0] += gc * cv * dx[k];
-            gd[1] += gc * cv * dy[k];
-            gd[2] += gc * cv * dz[k];
+        for (int k = 0; k < K; ++k) {
+          w[k] = 0.f;
+#pragma unroll
+          for (int ch = 0; ch < 3; ++ch) {
+            acc[k * 3 + ch] += gc[ch] * Y[k];
+            w[k] += gc[ch] * coef[k * 3 + ch];
           }
         }
+        float dx[K], dy[K], dz[K];
+        sh_basis<Degree, true>(d[0], d[1], d[2], Y, dx, dy, dz);
+#pragma unroll
+        for (int k = 0; k < K; ++k) {
+          gd[0] += w[k] * dx[k];
+          gd[1] += w[k] * dy[k];
+          gd[2] += w[k] * dz[k];
+        }
+      }
+      if (set == 0) {
+#pragma unroll
+        for (int k = 0; k < 12; ++k) shared[k] += gr[6 + k];
+        if (grad_opacity_rows) g_opacity += grad_opacity_rows[row];
+      }
     }
+    if (set == 1) {
 #pragma unroll
-    for (int k = 0; k < 3; ++k) grad_directions[pair * 3 + k] = gd[k];
+      for (int k = 0; k < 3; ++k) set1_directions[t][k] = gd[k];
+    }
+    __syncthreads();
+    if (set == 0 && row >= 0) {
 #pragma unroll
-    for (int k = 0; k < 12; ++k) shared[k] += gr[6 + k];
-    if (grad_opacity_rows) g_opacity += grad_opacity_rows[row];
+      for (int k = 0; k < 3; ++k) grad_directions[pair * 3 + k] = gd[k] + set1_directions[t][k];
+    }
+    __syncthreads();  // the next camera overwrites set1_directions
   }
-  __syncthreads();  // every lane is done reading its coefficients
+  // Every lane of this wave is done reading its coefficients: the stage
+  // takes the gradients.
+  float* out = lds + t * PITCH;
 #pragma unroll
-  for (int set = 0; set < 2; ++set)
-#pragma unroll
-    for (int k = 0; k < KC; ++k) coef[set * KC + k] = acc[set][k];
+  for (int k = 0; k < KC; ++k) out[k] = acc[k];
   __syncthreads();
-  unstage_rows<KC, PITCH, Vec>(stage, grad_first + base, count, t);
-  unstage_rows<KC, PITCH, Vec>(stage + KC, grad_second + base, count, t);
-  if (own) {
+  unstage_rows<KC, PITCH, Vec>(lds, (set ? grad_second : grad_first) + base, count, t);
+  if (set == 0 && own) {
 #pragma unroll
     for (int f = 0; f < 4; ++f) {
       grad_weights[surfel * 4 + f] = shared[f];
@@ -534,7 +577,7 @@ int gs_records_backward(const float* means, const float* quaternions, const floa
 #define GS_SH_ROWS(D)                                                                        \
   if (vec) GS_SH_ROWS_V(D, true) else GS_SH_ROWS_V(D, false)
 #define GS_SH_ROWS_V(D, V)                                                                   \
-  sh_rows_backward_kernel<D, V><<<sh_grid, kShBlock, 0, s>>>(                                \
+  sh_rows_backward_kernel<D, V><<<sh_grid, kShBlock * kShSets, 0, s>>>(                      \
       sh_first, sh_second, cameras, n, row_of_pair, geometry, grad_appearance_rows,          \
       grad_opacity_rows, grad_sh_first, grad_sh_second, grad_weights, grad_magnitudes,       \
       grad_phases, grad_opacities, w.directions);
