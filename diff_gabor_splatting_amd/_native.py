@@ -80,6 +80,11 @@ _SIGNATURES = {
         _c_int,
         [_c_ptr] * 4 + [_c_i64, _c_int, _c_int, _c_ptr, _c_size, _c_ptr],
     ),
+    "gs_sort32_workspace_size": (_c_size, [_c_i64]),
+    "gs_sort_pairs32": (
+        _c_int,
+        [_c_ptr] * 4 + [_c_i64, _c_int, _c_int, _c_ptr, _c_size, _c_ptr],
+    ),
     "gs_find_ranges": (_c_int, [_c_ptr, _c_i64, _c_ptr, _c_i64, _c_ptr]),
     "gs_bin_order_workspace_size": (_c_size, [_c_i64]),
     "gs_bin_order": (
@@ -285,6 +290,25 @@ def sort_pairs(keys: torch.Tensor, values: torch.Tensor, begin_bit: int = 0, end
         workspace = _workspace(lib.gs_sort_workspace_size(m), device)
         _check(
             lib.gs_sort_pairs(
+                _ptr(keys), _ptr(sorted_keys), _ptr(values), _ptr(sorted_values), m, begin_bit,
+                end_bit, _ptr(workspace), workspace.numel(), _stream(device),
+            )
+        )
+    return sorted_keys, sorted_values
+
+
+def sort_pairs32(keys: torch.Tensor, values: torch.Tensor | None = None, begin_bit: int = 0,
+                 end_bit: int = 32):
+    """Stable LSD radix sort of uint32 keys (stored as int32) with int32
+    values, or of the keys alone: (sorted keys, sorted values or None)."""
+    device = keys.device
+    m = keys.numel()
+    sorted_keys = torch.empty_like(keys)
+    sorted_values = None if values is None else torch.empty_like(values)
+    if m:
+        workspace = _workspace(lib.gs_sort32_workspace_size(m), device)
+        _check(
+            lib.gs_sort_pairs32(
                 _ptr(keys), _ptr(sorted_keys), _ptr(values), _ptr(sorted_values), m, begin_bit,
                 end_bit, _ptr(workspace), workspace.numel(), _stream(device),
             )

@@ -132,8 +132,9 @@ __global__ __launch_bounds__(kSortBlock) void radix_downsweep_kernel(
   const uint32_t mask = (1u << bits) - 1u;
   for (int i = threadIdx.x; i < kSortWaves * kBins; i += kSortBlock) (&running[0][0])[i] = 0;
   __syncthreads();
+  const int64_t span = blockIdx.x;
 
-  const int64_t wave_base = int64_t(blockIdx.x) * kSortSpan + int64_t(wave) * kWaveSpan;
+  const int64_t wave_base = span * kSortSpan + int64_t(wave) * kWaveSpan;
   const uint64_t lanes_below = (uint64_t(1) << lane) - 1;
   Key key[kSortItems];
   int value[kSortItems];
@@ -178,7 +179,7 @@ __global__ __launch_bounds__(kSortBlock) void radix_downsweep_kernel(
       run += c;
     }
     local_start[d] = run;  // digit total; converted to a prefix below
-    global_start[d] = offsets[int64_t(d) * spans + blockIdx.x];
+    global_start[d] = offsets[int64_t(d) * spans + span];
   }
   __syncthreads();
   // Exclusive prefix of the 256 digit totals (one value per thread).
@@ -207,7 +208,7 @@ __global__ __launch_bounds__(kSortBlock) void radix_downsweep_kernel(
     }
   }
   __syncthreads();
-  const int64_t span_base = int64_t(blockIdx.x) * kSortSpan;
+  const int64_t span_base = span * kSortSpan;
   const int span_count = int(min<int64_t>(kSortSpan, m - span_base));
   for (int slot = threadIdx.x; slot < span_count; slot += kSortBlock) {
     const Key k = stage_keys[slot];
@@ -335,6 +336,30 @@ template int radix_sort<uint64_t>(const uint64_t*, uint64_t*, const int*, int*, 
 extern "C" {
 
 size_t gs_sort_workspace_size(int64_t m) { return gs::radix_sort_workspace_bytes(m, 8); }
+
+size_t gs_sort32_workspace_size(int64_t m) { return gs::radix_sort_workspace_bytes(m, 4); }
+
+int gs_sort_pairs32(const uint32_t* keys_in, uint32_t* keys_out, const int32_t* values_in,
+                    int32_t* values_out, int64_t m, int32_t begin_bit, int32_t end_bit,
+                    void* workspace, size_t workspace_bytes, void* stream) {
+  using namespace gs;
+  clear_error();
+  GS_REQUIRE(m >= 0 && m <= 0x7fffffffLL, GS_ERR_OVERFLOW, "sort size exceeds int32");
+  GS_REQUIRE(0 <= begin_bit && begin_bit <= end_bit && end_bit <= 32, GS_ERR_ARGUMENT,
+             "invalid bit range [%d, %d)", begin_bit, end_bit);
+  if (m == 0) return GS_OK;
+  GS_REQUIRE(keys_in && keys_out && !values_in == !values_out, GS_ERR_ARGUMENT,
+             "null pointer passed to gs_sort_pairs32");
+  GS_REQUIRE(keys_in != keys_out && (!values_in || values_in != values_out), GS_ERR_ARGUMENT,
+             "sort outputs must not alias inputs");
+  const size_t need = gs_sort32_workspace_size(m);
+  GS_REQUIRE(workspace && workspace_bytes >= need, GS_ERR_WORKSPACE,
+             "sort needs %zu workspace bytes, got %zu", need, workspace_bytes);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  ProfileScope prof(GS_PROF_SORT, s);
+  return radix_sort<uint32_t>(keys_in, keys_out, values_in, values_out, m, begin_bit, end_bit,
+                              workspace, s);
+}
 
 int gs_sort_pairs(const uint64_t* keys_in, uint64_t* keys_out, const int32_t* values_in,
                   int32_t* values_out, int64_t m, int32_t begin_bit, int32_t end_bit,

@@ -231,6 +231,17 @@ int gs_sort_pairs(const uint64_t* keys_in, uint64_t* keys_out, const int32_t* va
                   int32_t* values_out, int64_t m, int32_t begin_bit, int32_t end_bit,
                   void* workspace, size_t workspace_bytes, void* stream);
 
+/* Scratch bytes for gs_sort_pairs32 over m pairs. */
+size_t gs_sort32_workspace_size(int64_t m);
+
+/* The same stable sort for 32-bit keys, the sort of both depth-first binning
+ * stages (each stands in for part of the 64-bit SortPairs of
+ * rasterize.cu:478-487): key bits [begin_bit, end_bit), int32 values, or the
+ * keys alone when values_in and values_out are both null. */
+int gs_sort_pairs32(const uint32_t* keys_in, uint32_t* keys_out, const int32_t* values_in,
+                    int32_t* values_out, int64_t m, int32_t begin_bit, int32_t end_bit,
+                    void* workspace, size_t workspace_bytes, void* stream);
+
 /* findRanges (rasterize.cu:59-69): ranges [tiles,2] = [first,last) of each
  * tile's run in sorted_keys; tiles with no entries get (0,0). */
 int gs_find_ranges(const uint64_t* sorted_keys, int64_t m, int32_t* ranges, int64_t tiles,

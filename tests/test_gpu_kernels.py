@@ -30,6 +30,34 @@ def to_u64(t):
     return t.cpu().numpy().view(np.uint64)
 
 
+@pytest.mark.parametrize("m", [1, 255, 2048, 2049, 100_003, 1_000_003, 4_194_305])
+@pytest.mark.parametrize("bits, with_values", [
+    ((0, 32), True), ((19, 32), False), ((0, 13), True), ((5, 12), False),
+])
+def test_sort32_is_stable_radix_order(native, m, bits, with_values):
+    """The 32-bit sort of the binning stages (single-kernel digit passes with
+    look-back), against numpy's stable argsort: partial last spans, both
+    span sizes (4,194,305 keys take 4096-key spans), keys alone and with
+    values, partial bit ranges, many ties and skewed digits."""
+    rng = np.random.default_rng(m + 7 * bits[0])
+    keys = rng.integers(0, 2**32, m, dtype=np.uint64).astype(np.uint32)
+    keys[rng.integers(0, m, m // 3)] = keys[0]  # many exact ties
+    keys[: m // 5] = rng.integers(0, 5, m // 5).astype(np.uint32)  # skewed low digits
+    values = np.arange(m, dtype=np.int32)[::-1].copy()
+    print(f"sort32 m={m} bits={bits} values={with_values}", flush=True)
+    sk, sv = native.sort_pairs32(torch.from_numpy(keys.view(np.int32)).to(DEVICE),
+                                 torch.from_numpy(values).to(DEVICE) if with_values else None,
+                                 *bits)
+    begin, end = bits
+    digit = (keys.astype(np.uint64) >> np.uint64(begin)) & np.uint64((1 << (end - begin)) - 1)
+    order = np.argsort(digit, kind="stable")
+    np.testing.assert_array_equal(sk.cpu().numpy().view(np.uint32), keys[order])
+    if with_values:
+        np.testing.assert_array_equal(sv.cpu().numpy(), values[order])
+    else:
+        assert sv is None
+
+
 @pytest.mark.parametrize("m", [1, 5, 4095, 4096, 4097, 100_003, 2_000_000])
 @pytest.mark.parametrize("bits", [(0, 64), (0, 45), (32, 45), (3, 17)])
 def test_sort_is_stable_radix_order(native, m, bits):
