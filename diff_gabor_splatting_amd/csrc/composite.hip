@@ -1041,8 +1041,15 @@ __global__ __launch_bounds__(kTilePixels, Neural ? 2 : 4) void render_backward_k
         rows, raw, reach_rows, ids, prims, tile_x, tile_y, count, id, prim, geometry, appearance,
         opacities, entry, entries);
     if (ahead) next_prim = primitive_ids[next_id];
-    // The raw rows are dead: clear the accumulator that shares their LDS.
-    for (int i = threadIdx.x; i < count * NP; i += kTilePixels) acc[i] = 0.f;
+    // The raw rows are dead: clear the accumulator that shares their LDS
+    // (16-byte stores; the array is 16-byte aligned).
+    {
+      const int n = count * NP;
+      float4* acc4 = reinterpret_cast<float4*>(acc);
+      for (int i = threadIdx.x; i < n / 4; i += kTilePixels)
+        acc4[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (int(threadIdx.x) < (n & 3)) acc[(n & ~3) + threadIdx.x] = 0.f;
+    }
     __syncthreads();
     uint64_t todo = wave_uniform(reach);
     if constexpr (!Replay) {
@@ -1172,6 +1179,8 @@ __global__ __launch_bounds__(kTilePixels, Neural ? 2 : 4) void render_backward_k
     }
     __syncthreads();
     // Flush this batch: one global atomic per nonzero (record, parameter).
+    // Consecutive threads take consecutive parameters of a record, so that
+    // the atomics of a wave fall on a few cache lines.
     for (int idx = threadIdx.x; idx < count * NP; idx += kTilePixels) {
       const int j = idx / NP;
       const int p = idx - j * NP;
