@@ -68,6 +68,7 @@ struct ClassicRow {
   static constexpr int HALF_W = 32, SUM = 33, DIFF = 36;  // 1, 3, 3
   static constexpr int AP = 40, BP = 44;  // -2 pi HW_f A_f, -2 pi HW_f B_f (backward)
   static constexpr int STRIDE = 48;
+  static constexpr int FORWARD_STRIDE = 40;  // the forward's rows end before AP
 };
 struct NeuralRow {
   static constexpr int DIR = 14, OP = 17, THR = 18;
@@ -77,12 +78,16 @@ struct NeuralRow {
   static constexpr int STRIDE = 76;
 };
 
-template <bool Neural>
+// Forward: the forward compositor's rows, which leave out what only the
+// adjoint reads (classic AP/BP), so that six of its workgroups fit a CU's LDS.
+template <bool Neural, bool Forward = false>
 struct Layout {
   static constexpr int A = Neural ? kNeural : kClassic;  // raw appearance floats
   static constexpr int RAW = kGeometry + 1 + A;          // raw staging floats
   static constexpr int RAW_STRIDE = Neural ? 76 : 36;
-  static constexpr int STRIDE = Neural ? NeuralRow::STRIDE : ClassicRow::STRIDE;
+  static constexpr int STRIDE = Neural    ? NeuralRow::STRIDE
+                                : Forward ? ClassicRow::FORWARD_STRIDE
+                                          : ClassicRow::STRIDE;
   // Gradient values per record: geometry (classic skips the unused
   // direction columns), appearance, opacity.
   static constexpr int NG = Neural ? kGeometry : 14;
@@ -398,7 +403,7 @@ enum Gather { kGatherLoops, kGatherQuarters };
 // forward), staged per record in `entries`.
 enum Select { kReachTest, kReplayMask };
 
-template <bool Neural, Gather Mode, Select Which = kReachTest>
+template <bool Neural, Gather Mode, Select Which = kReachTest, bool Forward = false>
 __device__ __forceinline__ uint64_t load_batch(float* rows, float* raw, float* reach_rows,
                                                int* ids, int64_t* prims, float tile_x,
                                                float tile_y,
@@ -406,7 +411,7 @@ __device__ __forceinline__ uint64_t load_batch(float* rows, float* raw, float* r
                                                const float* geometry, const float* appearance,
                                                const float* opacities, int entry = 0,
                                                int* entries = nullptr) {
-  using L = Layout<Neural>;
+  using L = Layout<Neural, Forward>;
   const int t = threadIdx.x;
   if (t < count) {  // (id, prim): this thread's record, fetched by the caller ahead of time
     ids[t] = id;
@@ -550,8 +555,10 @@ __device__ __forceinline__ uint64_t load_batch(float* rows, float* raw, float* r
         r[R::B + f] = a[10 + f] * kDirY[f];
         r[R::C + f] = a[14 + f] * kInvTwoPi;
         r[R::HW + f] = 0.5f * a[6 + f];
-        r[R::AP + f] = -kTwoPi * (0.5f * a[6 + f]) * r[R::A + f];
-        r[R::BP + f] = -kTwoPi * (0.5f * a[6 + f]) * r[R::B + f];
+        if constexpr (!Forward) {
+          r[R::AP + f] = -kTwoPi * (0.5f * a[6 + f]) * r[R::A + f];
+          r[R::BP + f] = -kTwoPi * (0.5f * a[6 + f]) * r[R::B + f];
+        }
         half_w += 0.5f * a[6 + f];
       }
       r[R::HALF_W] = half_w;
@@ -716,7 +723,7 @@ __global__ __launch_bounds__(kTilePixels) void tile_last_kernel(int width, int h
 // Replay: also write the tile's replay list (replay + range start, see
 // append_replay) and its length (replay_counts[tile]).
 template <bool Neural, bool Replay>
-__global__ __launch_bounds__(kTilePixels, Neural ? 3 : 5) void render_forward_kernel(
+__global__ __launch_bounds__(kTilePixels, Neural ? 3 : 6) void render_forward_kernel(
     int width, int height, int tw, int th, const float* __restrict__ geometry,
     const float* __restrict__ appearance, const float* __restrict__ opacities,
     const int64_t* __restrict__ primitive_ids, const float* __restrict__ backgrounds,
@@ -724,7 +731,7 @@ __global__ __launch_bounds__(kTilePixels, Neural ? 3 : 5) void render_forward_ke
     const int* __restrict__ order, float near_plane, float far_plane, MapGroups<float> maps,
     float* __restrict__ state, int* __restrict__ contributors, int2* __restrict__ replay,
     int* __restrict__ replay_counts) {
-  using L = Layout<Neural>;
+  using L = Layout<Neural, true>;
   __shared__ __align__(16) float rows[kBatch * L::STRIDE];
   __shared__ __align__(16) float raw[kBatch * L::RAW_STRIDE];
   __shared__ float reach_rows[kBatch * kReachPitch];
@@ -769,7 +776,7 @@ __global__ __launch_bounds__(kTilePixels, Neural ? 3 : 5) void render_forward_ke
     const int64_t prim = next_prim;
     const bool ahead = int(threadIdx.x) < min(kBatch, range.y - start - kBatch);
     if (ahead) next_id = point_list[start + kBatch + threadIdx.x];
-    const uint64_t reach = load_batch<Neural, kGatherQuarters>(
+    const uint64_t reach = load_batch<Neural, kGatherQuarters, kReachTest, true>(
         rows, raw, reach_rows, ids, prims, tile_x, tile_y, count, id, prim, geometry, appearance,
         opacities);
     if (ahead) next_prim = primitive_ids[next_id];
