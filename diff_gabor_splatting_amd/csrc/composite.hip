@@ -71,23 +71,25 @@ struct ClassicRow {
   static constexpr int FORWARD_STRIDE = 40;  // the forward's rows end before AP
 };
 struct NeuralRow {
-  static constexpr int DIR = 14, OP = 17, THR = 18;
-  static constexpr int ZC = 19, U = 25, V = 31;  // 6 each
-  static constexpr int WDIR = 37;                // W1[h][2..4], 18
-  static constexpr int W2 = 55, B2 = 73;         // 18, 3
+  static constexpr int OP = 14, THR = 15;
+  static constexpr int ZC = 16, U = 22, V = 28;  // 6 each
+  static constexpr int W2 = 34, B2 = 52;         // 18, 3
+  static constexpr int DIR = 55;                 // 3 (backward)
+  static constexpr int WDIR = 58;                // W1[h][2..4], 18 (backward)
   static constexpr int STRIDE = 76;
+  static constexpr int FORWARD_STRIDE = 55;  // the forward's rows end before DIR
 };
 
 // Forward: the forward compositor's rows, which leave out what only the
-// adjoint reads (classic AP/BP), so that six of its workgroups fit a CU's LDS.
+// adjoint reads (classic AP/BP, neural DIR/WDIR), so that six classic or
+// four neural workgroups fit a CU's LDS.
 template <bool Neural, bool Forward = false>
 struct Layout {
   static constexpr int A = Neural ? kNeural : kClassic;  // raw appearance floats
   static constexpr int RAW = kGeometry + 1 + A;          // raw staging floats
   static constexpr int RAW_STRIDE = Neural ? 76 : 36;
-  static constexpr int STRIDE = Neural    ? NeuralRow::STRIDE
-                                : Forward ? ClassicRow::FORWARD_STRIDE
-                                          : ClassicRow::STRIDE;
+  static constexpr int STRIDE = Neural ? (Forward ? NeuralRow::FORWARD_STRIDE : NeuralRow::STRIDE)
+                                       : (Forward ? ClassicRow::FORWARD_STRIDE : ClassicRow::STRIDE);
   // Gradient values per record: geometry (classic skips the unused
   // direction columns), appearance, opacity.
   static constexpr int NG = Neural ? kGeometry : 14;
@@ -528,7 +530,8 @@ __device__ __forceinline__ uint64_t load_batch(float* rows, float* raw, float* r
     if constexpr (Neural) {
       using R = NeuralRow;
 #pragma unroll
-      for (int i = 0; i < 3; ++i) r[R::DIR + i] = g[14 + i];
+      for (int i = 0; i < 3; ++i)
+        if constexpr (!Forward) r[R::DIR + i] = g[14 + i];
       r[R::OP] = opacity;
       r[R::THR] = reject_threshold(opacity);
 #pragma unroll
@@ -538,7 +541,8 @@ __device__ __forceinline__ uint64_t load_batch(float* rows, float* raw, float* r
         r[R::U + h] = w1[0] / 3.f;
         r[R::V + h] = w1[1] / 3.f;
 #pragma unroll
-        for (int k = 0; k < 3; ++k) r[R::WDIR + h * 3 + k] = w1[2 + k];
+        for (int k = 0; k < 3; ++k)
+          if constexpr (!Forward) r[R::WDIR + h * 3 + k] = w1[2 + k];
       }
 #pragma unroll
       for (int i = 0; i < 18; ++i) r[R::W2 + i] = a[36 + i];
@@ -723,7 +727,7 @@ __global__ __launch_bounds__(kTilePixels) void tile_last_kernel(int width, int h
 // Replay: also write the tile's replay list (replay + range start, see
 // append_replay) and its length (replay_counts[tile]).
 template <bool Neural, bool Replay>
-__global__ __launch_bounds__(kTilePixels, Neural ? 3 : 6) void render_forward_kernel(
+__global__ __launch_bounds__(kTilePixels, Neural ? 4 : 6) void render_forward_kernel(
     int width, int height, int tw, int th, const float* __restrict__ geometry,
     const float* __restrict__ appearance, const float* __restrict__ opacities,
     const int64_t* __restrict__ primitive_ids, const float* __restrict__ backgrounds,

@@ -328,7 +328,7 @@ namespace {
 // written once; per-camera gradients are summed per workgroup into
 // partials[camera][block][21] for camera_reduce_kernel.
 template <class Source>
-__global__ __launch_bounds__(kProjectBlock) void projection_backward_kernel(
+__global__ __launch_bounds__(kProjectBlock, 5) void projection_backward_kernel(
     const float* __restrict__ means, const float* __restrict__ quats,
     const float* __restrict__ scales, const float* __restrict__ views,
     const float* __restrict__ intrinsics, int64_t cameras, int64_t n, Source source,
