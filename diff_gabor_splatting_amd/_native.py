@@ -429,11 +429,13 @@ def bin_depth_first(geometry, radii, image_ids, images, width, height, overlap=N
     return bin_tiles(order, starts, rects, images, width, height, intersections, visible)
 
 
-def pack_visible(radii: torch.Tensor, with_rows: bool = False):
+def pack_visible(radii: torch.Tensor, with_rows: bool = False, sync: bool = True):
     """Ascending indices of pairs with radii > 0 (int64). Synchronises once.
 
     With ``with_rows`` also returns row_of_pair (int32, the packed row of
-    every pair or -1)."""
+    every pair or -1). With ``sync=False`` nothing is read back: the indices
+    keep one entry per pair (those past the visible count V undefined) and
+    V, a device int64 tensor of one element, is returned last."""
     device = radii.device
     flat = radii.reshape(-1)
     count = flat.numel()
@@ -447,6 +449,8 @@ def pack_visible(radii: torch.Tensor, with_rows: bool = False):
             workspace.numel(), _stream(device),
         )
     )
+    if not sync:
+        return (selected[:count], rows[:count], total) if with_rows else (selected[:count], total)
     selected = selected[: int(total.item())]
     return (selected, rows[:count]) if with_rows else selected
 
@@ -508,8 +512,14 @@ def check_values_word(tensors, quaternions, scales, opacities, view_matrices, in
 
 
 def records_forward(means, quaternions, scales, opacities, view_matrices, intrinsics, sh,
-                    shared, sh_degree, width, height, near_plane, far_plane, packed):
+                    shared, sh_degree, width, height, near_plane, far_plane, packed,
+                    fixed_rows=False):
     """Compositor rows for every visible (packed) or every (dense) pair.
+
+    With ``packed`` and ``fixed_rows`` the visible count is not read back:
+    every output keeps one row per pair, the packed rows first; the rows past
+    them have radius 0 (so binning skips them), zero projected means and ids
+    of -1.
 
     means/quaternions/scales [S,N,*], view_matrices [S,C,4,4], intrinsics
     [S,C,3,3]; with SH (sh_degree >= 0) also opacities [S,N], sh = (first,
@@ -546,24 +556,35 @@ def records_forward(means, quaternions, scales, opacities, view_matrices, intrin
     with torch.cuda.device(device):
         dense_radii = torch.empty((scenes, cameras, n), dtype=torch.int32, device=device)
         row_of_pair = selected = None
+        padded = packed and fixed_rows
         if packed:
             launch(None, dense_radii, {})
-            selected, row_of_pair = pack_visible(dense_radii, with_rows=True)
+            if padded:
+                selected, row_of_pair, _ = pack_visible(dense_radii, with_rows=True, sync=False)
+            else:
+                selected, row_of_pair = pack_visible(dense_radii, with_rows=True)
             rows = selected.numel()
         else:
             rows = pairs
         f32 = dict(dtype=torch.float32, device=device)
+        # Padded rows past the visible count are never written by the record
+        # kernel: they are filled here so that binning culls them and the
+        # meta outputs stay defined.
+        fill = torch.zeros if padded else torch.empty
         out = {
             "geometry": torch.empty((rows, GEOMETRY_SIZE), **f32),
-            "projected_means": torch.empty((rows, 2), **f32),
-            "row_radii": torch.empty(rows, dtype=torch.int32, device=device),
+            "projected_means": fill((rows, 2), **f32),
+            "row_radii": fill(rows, dtype=torch.int32, device=device),
             "primitive_ids": torch.empty(rows, dtype=torch.int64, device=device),
             "image_ids": torch.empty(rows, dtype=torch.int64, device=device),
         }
         if degree >= 0:
             out["appearance"] = torch.empty((rows, 18), **f32)
             out["opacity_rows"] = torch.empty(rows, **f32)
-        meta_ids = torch.empty((3, rows), dtype=torch.int64, device=device)
+        if padded:
+            meta_ids = torch.full((3, rows), -1, dtype=torch.int64, device=device)
+        else:
+            meta_ids = torch.empty((3, rows), dtype=torch.int64, device=device)
         out.update(scene_ids=meta_ids[0], camera_ids=meta_ids[1], surfel_ids=meta_ids[2])
         if rows:
             launch(row_of_pair, None if packed else dense_radii, out)

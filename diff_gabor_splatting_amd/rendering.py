@@ -109,12 +109,12 @@ class ProjectRecords(torch.autograd.Function):
     @staticmethod
     def forward(ctx: Any, means, quaternions, scales, opacities, view_matrices, intrinsics,
                 first, second, weights, magnitudes, phases, sh_degree, width, height,
-                near_plane, far_plane, packed):
+                near_plane, far_plane, packed, fixed_rows=False):
         sh = None if sh_degree is None else (first, second)
         shared = None if sh_degree is None else (weights, magnitudes, phases)
         out = _native.records_forward(
             means, quaternions, scales, opacities, view_matrices, intrinsics, sh, shared,
-            sh_degree, width, height, near_plane, far_plane, packed,
+            sh_degree, width, height, near_plane, far_plane, packed, fixed_rows,
         )
         row_of_pair = out["row_of_pair"]
         ctx.save_for_backward(means, quaternions, scales, view_matrices, intrinsics, first,
@@ -136,7 +136,7 @@ class ProjectRecords(torch.autograd.Function):
         sh_degree = ctx.sh_degree
         g_appearance, g_opacity = (rest[0], rest[1]) if sh_degree is not None else (None, None)
         if all(g is None for g in (g_geometry, g_projected, g_appearance, g_opacity)):
-            return (None,) * 17
+            return (None,) * 18
         grads = _native.records_backward(
             means, quats, scales, views, intrinsics,
             None if sh_degree is None else (first, second), sh_degree, rows, geometry,
@@ -145,7 +145,7 @@ class ProjectRecords(torch.autograd.Function):
         g_means, g_quats, g_scales, g_views, g_intrinsics = grads[:5]
         g_first, g_second, g_weights, g_magnitudes, g_phases, g_opacities = grads[5:]
         return (g_means, g_quats, g_scales, g_opacities, g_views, g_intrinsics, g_first,
-                g_second, g_weights, g_magnitudes, g_phases) + (None,) * 6
+                g_second, g_weights, g_magnitudes, g_phases) + (None,) * 7
 
 
 class ProjectSurfaces(torch.autograd.Function):
@@ -276,7 +276,10 @@ class FixedCapacity:
       of the affected tiles are dropped and a device flag is raised;
     * run the value checks (``validate=True``) on the device and keep the
       verdict instead of raising;
-    * refuse ``packed=True``, whose outputs have a data-dependent length.
+    * with ``packed=True``, keep one packed row per (scene, camera, surfel)
+      pair instead of reading the visible count V back: ``meta["radii"]``,
+      ``projected_means`` and the id tensors hold the V packed rows first,
+      then rows of radius 0, projected mean 0 and id -1.
 
     ``check()``, called outside any capture, reads every recorded verdict
     and flag in one synchronisation and raises ValueError (violated value
@@ -426,11 +429,6 @@ def render(
     if type(validate) is not bool:
         raise TypeError("validate must be bool")
     bounded = _FIXED_CAPACITY[-1] if _FIXED_CAPACITY else None
-    if bounded is not None and packed:
-        raise ValueError(
-            "packed=True is unavailable at a fixed intersection capacity: its outputs have a "
-            "data-dependent length"
-        )
     if validate and bounded is None:
         check_values(
             tensors, quaternions, scales, opacities, view_matrices, intrinsics, appearance, neural
@@ -457,7 +455,7 @@ def render(
             appearance[0].reshape(scenes, n, k, 3), appearance[1].reshape(scenes, n, k, 3),
             appearance[2].reshape(scenes, n, 4), appearance[3].reshape(scenes, n, 4),
             appearance[4].reshape(scenes, n, 4), sh_degree, width, height, near_plane,
-            far_plane, packed,
+            far_plane, packed, bounded is not None,
         )
     else:
         # One appearance row per surfel, shared by every camera of its scene.
@@ -465,7 +463,7 @@ def render(
          scene_ids, camera_ids, surfel_ids) = ProjectRecords.apply(
             means.reshape(scenes, n, 3), quaternions.reshape(scenes, n, 4),
             scales.reshape(scenes, n, 2), None, views, cameras_k, None, None, None, None, None,
-            None, width, height, near_plane, far_plane, packed,
+            None, width, height, near_plane, far_plane, packed, bounded is not None,
         )
         width_of_row = 57 if neural else 18
         flat = [t.reshape(scenes, n, math.prod(shape)) for t, (_, shape) in zip(appearance, fields)]

@@ -68,6 +68,41 @@ def test_bounded_render_matches_synchronised_render(method):
     assert_grads_close(grads, expected_grads, list(values), "bounded")
 
 
+@pytest.mark.parametrize("method, sh", [("classic", None), ("classic", 2), ("neural", None)])
+def test_bounded_packed_render_keeps_one_row_per_pair(method, sh):
+    """packed=True at a fixed capacity: the visible count stays on the device,
+    so the packed outputs keep S*C*N rows, the packed rows first."""
+    from diff_gabor_splatting_amd import fixed_capacity
+
+    raw = random_scene(method, scenes=2, cameras=2, n=300, width=70, height=45, seed=21, sh=sh)
+    raw["means"][:, ::5, 2] = -3.0  # a fifth of the surfels behind every camera
+    values = {k: v.to(DEVICE) for k, v in raw.items()}
+    options = dict(width=70, height=45, packed=True)
+    if sh is not None:
+        options["sh_degree"] = sh
+    rgb, alpha, meta = renderer(method)(**values, **options)
+    plain = maps_from_result((rgb, alpha, meta))
+    weights = torch.linspace(-1, 1, plain.numel(), device=DEVICE).reshape(plain.shape)
+    expected, expected_grads = maps_and_grads(method, values, options, weights)
+    with fixed_capacity(1 << 20) as capacity:
+        result = renderer(method)(**values, **options)
+        actual, grads = maps_and_grads(method, values, options, weights)
+    assert capacity.check() > 0
+    assert torch.equal(actual, expected) and torch.equal(maps_from_result(result), expected)
+    assert_grads_close(grads, expected_grads, list(values), "bounded packed")
+
+    padded = result[2]
+    visible, pairs = meta["radii"].numel(), 2 * 2 * 300
+    assert 0 < visible <= pairs * 4 // 5 and padded["packed"] is True
+    assert padded["radii"].shape == (pairs,) and padded["projected_means"].shape == (pairs, 2)
+    for key in ("radii", "projected_means", "scene_ids", "camera_ids", "primitive_ids"):
+        assert torch.equal(padded[key][:visible], meta[key]), key
+    assert int(padded["radii"][visible:].abs().sum()) == 0
+    assert int(padded["projected_means"][visible:].abs().sum()) == 0
+    for key in ("scene_ids", "camera_ids", "primitive_ids"):
+        assert bool((padded[key][visible:] == -1).all()), key
+
+
 def test_overflow_is_reported_by_check():
     from diff_gabor_splatting_amd import fixed_capacity
 
@@ -87,19 +122,20 @@ def test_value_checks_are_deferred():
     values["means"][0, 7, 0] = math.nan
     with fixed_capacity(1 << 20) as capacity:
         renderer("classic")(**values, **options)  # does not raise here
-        with pytest.raises(ValueError, match="packed=True is unavailable"):
-            renderer("classic")(**values, **options, packed=True)
+        renderer("classic")(**values, **options, packed=True)
     with pytest.raises(ValueError) as error:
         capacity.check()
     assert str(error.value) == ("means must contain only finite values; "
                                 "scales must be strictly positive")
 
 
-@pytest.mark.parametrize("method", ["classic", "neural"])
-def test_graph_replays_match_eager(method):
+@pytest.mark.parametrize("method, packed", [("classic", False), ("neural", False),
+                                            ("classic", True)])
+def test_graph_replays_match_eager(method, packed):
     from diff_gabor_splatting_amd import fixed_capacity
 
     base, options = scene(method, seed=11)
+    options["packed"] = packed
     static = {k: v.detach().clone().requires_grad_() for k, v in base.items()}
     probe = maps_from_result(renderer(method)(**base, **options))
     weights = torch.linspace(-1, 1, probe.numel(), device=DEVICE).reshape(probe.shape)
@@ -126,7 +162,7 @@ def test_graph_replays_match_eager(method):
         with torch.no_grad():
             for name, value in values.items():
                 static[name].copy_(value)
-        print(f"graph replay {method} {replay}", flush=True)
+        print(f"graph replay {method} packed={packed} {replay}", flush=True)
         graph.replay()
         torch.cuda.synchronize()
         expected, expected_grads = maps_and_grads(method, values, options, weights)
