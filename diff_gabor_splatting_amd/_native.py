@@ -395,7 +395,7 @@ def bin_tiles_bounded(order, starts, rects, images, width, height, capacity, int
 
 
 def bin_depth_first(geometry, radii, image_ids, images, width, height, overlap=None,
-                    capacity=None, flags=None):
+                    capacity=None, flags=None, violations=None):
     """Both binning stages with the one host synchronisation for M between
     them (rasterize.cu:466-469): (point_list, ranges).
 
@@ -404,7 +404,9 @@ def bin_depth_first(geometry, radii, image_ids, images, width, height, overlap=N
     ``overlap()`` queues (independent of M) runs while the host waits.
     With ``capacity`` there is no synchronisation at all: the point list
     has that many entries, and (overflow flag, live count M) of
-    bin_tiles_bounded are appended to ``flags``."""
+    bin_tiles_bounded are appended to ``flags``. ``violations`` (a device
+    int32 word of gs_check_values and a function that raises for a nonzero
+    word) is read back with M and reported before M is checked or used."""
     order, starts, rects, totals = bin_order(geometry, radii, image_ids, width, height)
     total = totals[:1]
     if capacity is not None:
@@ -419,11 +421,16 @@ def bin_depth_first(geometry, radii, image_ids, images, width, height, overlap=N
     stream = torch.cuda.current_stream(geometry.device)
     host = torch.empty(2, dtype=torch.int64, pin_memory=True)
     host.copy_(totals, non_blocking=True)
+    if violations is not None:
+        word = torch.empty(1, dtype=torch.int32, pin_memory=True)
+        word.copy_(violations[0], non_blocking=True)
     ready = torch.cuda.Event()
     ready.record(stream)
     if overlap is not None:
         overlap()
     ready.synchronize()
+    if violations is not None:
+        violations[1](int(word[0]))
     intersections, visible = int(host[0]), int(host[1])
     check_intersections(intersections)
     return bin_tiles(order, starts, rects, images, width, height, intersections, visible)
@@ -706,7 +713,7 @@ def _map_group_args(groups, what: str):
 def rasterize_forward(
     geometry, appearance, opacities, primitive_ids, image_ids, radii, backgrounds,
     width, height, neural, near_plane, far_plane, outputs=None, overlap=None, capacity=None,
-    flags=None, replay=False,
+    flags=None, replay=False, violations=None,
 ):
     """Bin, sort and composite: returns [maps, point_list, ranges, state, contributors].
 
@@ -725,7 +732,8 @@ def rasterize_forward(
     the tiles' replay lists for rasterize_backward - (lists [M, 2] int32,
     counts [I*tw*th] int32): per tile, the point-list entries that some pixel
     took, in list order - or None when the point list is too long for them
-    (2^28 entries or more).
+    (2^28 entries or more). ``violations`` (an addition): a pending value
+    check, raised with the read-back of M (see bin_depth_first).
     """
     _check_buffers(geometry, appearance, opacities, primitive_ids, backgrounds, neural)
     _require(
@@ -759,7 +767,7 @@ def rasterize_forward(
         state = torch.empty((images, height, width, 3), dtype=torch.float32, device=device)
         contributors = torch.empty((images, height, width), dtype=torch.int32, device=device)
         point_list, ranges = bin_depth_first(geometry, radii, image_ids, images, width, height,
-                                             overlap, capacity, flags)
+                                             overlap, capacity, flags, violations)
         if outputs is None:
             maps = torch.empty((images, height, width, MAP_SIZE), dtype=torch.float32,
                                device=device)

@@ -10,6 +10,7 @@ allocates memory, provides the stream and joins the autograd graph.
 
 from __future__ import annotations
 
+import functools
 import math
 from typing import Any
 
@@ -40,7 +41,7 @@ class Composite(torch.autograd.Function):
     def forward(
         ctx: Any, geometry, projected_means, appearance, opacities, primitive_ids, image_ids,
         radii, backgrounds, width, height, neural, near_plane, far_plane, bounded=None,
-        grad_mode=True,
+        grad_mode=True, violations=None,
     ):
         images = backgrounds.size(0)
         outputs = tuple(
@@ -65,6 +66,7 @@ class Composite(torch.autograd.Function):
             width, height, neural, near_plane, far_plane, outputs=outputs, overlap=overlap,
             capacity=None if bounded is None else bounded.max_intersections,
             flags=None if bounded is None else bounded._overflows, replay=needs_grad,
+            violations=violations,
         )
         replay = replay[0] if replay else None
         # Binning and early termination are discrete: only the saved sorted
@@ -90,7 +92,7 @@ class Composite(torch.autograd.Function):
             replay=None if lists is None else (lists, counts),
         )
         return (gg, gg[:, 9:11], ga, go, None, None, None, gb, None, None, None, None, None, None,
-                None)
+                None, None)
 
 
 class ProjectRecords(torch.autograd.Function):
@@ -257,9 +259,17 @@ def check_values(
         [value for value, _ in tensors.values()], quaternions, scales, opacities,
         view_matrices, intrinsics, weights, magnitudes,
     )
-    messages = describe_violations(list(tensors), violations)
+    _raise_violations(list(tensors), violations)
+
+
+def _raise_violations(names, violations: int) -> None:
+    """ValueError naming every contract set in a gs_check_values word."""
+    messages = describe_violations(names, violations & 0xFFFFFFFF)
     if messages:
         raise ValueError("; ".join(messages))
+
+
+_check_values_on_device = check_values
 
 
 class FixedCapacity:
@@ -429,10 +439,23 @@ def render(
     if type(validate) is not bool:
         raise TypeError("validate must be bool")
     bounded = _FIXED_CAPACITY[-1] if _FIXED_CAPACITY else None
-    if validate and bounded is None:
+    violations = None
+    if validate and bounded is None and check_values is not _check_values_on_device:
+        # A caller's replacement of check_values runs where the reference calls it.
         check_values(
             tensors, quaternions, scales, opacities, view_matrices, intrinsics, appearance, neural
         )
+    elif validate and bounded is None:
+        # The verdict is read back with the intersection count, in the
+        # forward's one synchronisation, and raised before anything is
+        # composited: the same ValueError as check_values, one read-back less.
+        weights, magnitudes = (None, None) if neural else (appearance[2], appearance[3])
+        with torch.no_grad():
+            word = _native.check_values_word(
+                [value for value, _ in tensors.values()], quaternions, scales, opacities,
+                view_matrices, intrinsics, weights, magnitudes,
+            )
+        violations = (word, functools.partial(_raise_violations, list(tensors)))
     elif validate:
         weights, magnitudes = (None, None) if neural else (appearance[2], appearance[3])
         with torch.no_grad():
@@ -490,6 +513,7 @@ def render(
         far_plane,
         bounded,
         torch.is_grad_enabled(),
+        violations,
     )
     image_shape = batch + (cameras, height, width)
     meta = {

@@ -83,3 +83,52 @@ def test_multi_block_scenes_find_edge_violations(method, where):
 def test_empty_scene_checks_nothing():
     values = on_gpu(make_inputs("classic", primitives=0))
     assert hip_messages(values, "classic") == []
+
+
+@pytest.mark.parametrize("method", ["classic", "neural"])
+@pytest.mark.parametrize("packed", [False, True])
+def test_renderer_reports_each_planted_violation(method, packed):
+    """The renderers read the check's verdict back with the intersection
+    count and raise it before compositing: the oracle's messages, every case."""
+    from diff_gabor_splatting_amd import rasterize_gabors, rasterize_neural_gabors
+
+    render = rasterize_gabors if method == "classic" else rasterize_neural_gabors
+    for label, mutate, expected in contract_cases(method):
+        values = on_gpu(planted_inputs(method, mutate))
+        print(f"render {method} packed={packed} {label}", flush=True)
+        if not expected:
+            render(**values, width=17, height=9, packed=packed)
+            continue
+        with pytest.raises(ValueError) as error:
+            render(**values, width=17, height=9, packed=packed)
+        assert str(error.value).split("; ") == expected, label
+
+
+def test_validated_render_synchronises_once(monkeypatch):
+    """validate=True never takes the check's own read-back, and still raises."""
+    from diff_gabor_splatting_amd import _native, rasterize_gabors
+
+    def separate_read_back(*args, **kwargs):
+        raise AssertionError("the value check was read back on its own")
+
+    monkeypatch.setattr(_native, "check_values", separate_read_back)
+    values = on_gpu(make_inputs("classic", cameras=2, primitives=5))
+    rgb, _, _ = rasterize_gabors(**values, width=17, height=9)
+    assert bool(torch.isfinite(rgb).all())
+    values["opacities"][0, 2] = 1.5
+    with pytest.raises(ValueError, match="opacities must lie in"):
+        rasterize_gabors(**values, width=17, height=9)
+
+
+def test_replaced_check_values_runs_in_place_of_the_kernel(monkeypatch):
+    """A caller's replacement of rendering.check_values is called, as the
+    reference calls it, once per validated render."""
+    from diff_gabor_splatting_amd import rasterize_gabors, rendering
+
+    calls = []
+    monkeypatch.setattr(rendering, "check_values", lambda *args: calls.append(len(args)))
+    values = on_gpu(make_inputs("classic", cameras=2, primitives=5))
+    values["opacities"][0, 2] = 1.5  # the replacement accepts it
+    rasterize_gabors(**values, width=17, height=9)
+    rasterize_gabors(**values, width=17, height=9, validate=False)
+    assert calls == [8]
