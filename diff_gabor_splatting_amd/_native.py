@@ -23,6 +23,9 @@ _LIBRARY_PATH = Path(__file__).resolve().parent / "libgabor_hip.so"
 
 TILE = 16
 GEOMETRY_SIZE = 17
+# Binning status bits (GS_BIN_* in include/gabor_hip.h).
+BINNING_OVERFLOW = 1
+BINNING_BAD_INDEX = 2
 MAP_SIZE = 9
 INT_MAX = 2**31 - 1
 # Replay-list entries carry a tile-list position in 28 bits.
@@ -95,7 +98,7 @@ _SIGNATURES = {
     "gs_bin_tiles": (
         _c_int,
         [_c_ptr] * 3 + [_c_i64, _c_i64, _c_i64, _c_i64, _c_int, _c_int, _c_ptr, _c_ptr, _c_ptr,
-                        _c_size, _c_ptr],
+                        _c_ptr, _c_size, _c_ptr],
     ),
     "gs_bin_tiles_bounded": (
         _c_int,
@@ -350,12 +353,15 @@ def bin_order(geometry: torch.Tensor, radii: torch.Tensor, image_ids: torch.Tens
     return order, starts, rects, totals
 
 
-def bin_tiles(order, starts, rects, images, width, height, intersections, visible=-1):
+def bin_tiles(order, starts, rects, images, width, height, intersections, visible=-1,
+              status=None):
     """Depth-first binning, stage 2: (point_list int32 [M], ranges int32
     [I*tw*th, 2]), the result of emit_tiles + sort_pairs + find_ranges
     (rasterize.cu:43-69, 470-501). ``visible`` is stage 1's count of pairs
     with tiles (-1: unknown), which selects the packed-key tile sort when it
-    fits."""
+    fits. ``status`` (an int32 [1] device tensor, or None) receives the
+    BINNING_* bits: BINNING_BAD_INDEX when a sort output failed its range
+    check (see gs_bin_tiles)."""
     device = order.device
     count = order.size(0)
     tw, th = tile_grid(width, height)
@@ -365,8 +371,8 @@ def bin_tiles(order, starts, rects, images, width, height, intersections, visibl
     _check(
         lib.gs_bin_tiles(
             _ptr(order), _ptr(starts), _ptr(rects), count, intersections, visible, images, width,
-            height, _ptr(point_list), _ptr(ranges), _ptr(workspace), workspace.numel(),
-            _stream(device),
+            height, _ptr(point_list), _ptr(ranges), _ptr(status), _ptr(workspace),
+            workspace.numel(), _stream(device),
         )
     )
     return point_list, ranges
@@ -376,7 +382,8 @@ def bin_tiles_bounded(order, starts, rects, images, width, height, capacity, int
     """Depth-first binning, stage 2, without reading M on the host: a point
     list of `capacity` entries and the live count `intersections` (int64 [1]
     on the device). Returns (point_list, ranges, overflow) with overflow an
-    int32 [1] device flag, 1 when M exceeded the capacity."""
+    int32 [1] device word of BINNING_* bits: BINNING_OVERFLOW when M
+    exceeded the capacity, BINNING_BAD_INDEX as in bin_tiles."""
     device = order.device
     count = order.size(0)
     tw, th = tile_grid(width, height)
@@ -403,8 +410,9 @@ def bin_depth_first(geometry, radii, image_ids, images, width, height, overlap=N
     an event recorded after that copy, not on the stream, so GPU work that
     ``overlap()`` queues (independent of M) runs while the host waits.
     With ``capacity`` there is no synchronisation at all: the point list
-    has that many entries, and (overflow flag, live count M) of
-    bin_tiles_bounded are appended to ``flags``. ``violations`` (a device
+    has that many entries, and ``flags(overflow, total)`` receives
+    bin_tiles_bounded's status word and the live count M, both device
+    tensors, for the caller to fold into its own records. ``violations`` (a device
     int32 word of gs_check_values and a function that raises for a nonzero
     word) is read back with M and reported before M is checked or used."""
     order, starts, rects, totals = bin_order(geometry, radii, image_ids, width, height)
@@ -416,7 +424,7 @@ def bin_depth_first(geometry, radii, image_ids, images, width, height, overlap=N
             order, starts, rects, images, width, height, capacity, total
         )
         if flags is not None:
-            flags.append((overflow, total))
+            flags(overflow, total)
         return point_list, ranges
     stream = torch.cuda.current_stream(geometry.device)
     host = torch.empty(2, dtype=torch.int64, pin_memory=True)

@@ -24,6 +24,7 @@
 #include <climits>
 
 #include "common.hpp"
+#include "index_guard.hpp"
 #include "scan.hpp"
 #include "sort.hpp"
 
@@ -218,13 +219,15 @@ constexpr int kLaneTiles = 32;
 
 // `m` is the capacity of tile_ids/values; `total` (a device int64, or null
 // when it equals m) the emission's full length, which may exceed it: entries
-// past the capacity are dropped and `overflow` (if given) is set.
+// past the capacity are dropped and `status` (if given) gets kBinOverflow.
+// A depth-sort output outside [0, count) is replaced by pair 0 and sets
+// kBinBadIndex (index_guard.hpp).
 // Packed: instead of (tile id, pair index) pairs, write one 32-bit key
 // tile id << rank_bits | depth rank per entry (the caller has checked that
 // both fit), so that the tile sort moves keys only; values is unused.
 template <bool Packed>
 __global__ __launch_bounds__(256) void emit_sorted_kernel(
-    int64_t count, int64_t m, const int64_t* __restrict__ total_count, uint32_t* overflow,
+    int64_t count, int64_t m, const int64_t* __restrict__ total_count, uint32_t* status,
     int tw, const int* __restrict__ order, const int64_t* __restrict__ starts,
     const int4* __restrict__ rects, uint32_t* __restrict__ tile_ids, int* __restrict__ values,
     int rank_bits) {
@@ -232,12 +235,14 @@ __global__ __launch_bounds__(256) void emit_sorted_kernel(
   const int64_t j = int64_t(blockIdx.x) * 256 + threadIdx.x;
   if (j - lane >= count) return;  // uniform per wave
   const int64_t total = total_count ? *total_count : m;
-  if (overflow && j == 0 && total > m) *overflow = 1u;
+  if (status && j == 0 && total > m) atomicOr(status, kBinOverflow);
   int pair = 0, area = 0;
   int4 rect = make_int4(0, 0, 1, 0);
   int64_t first = 0;
   if (j < count) {
-    pair = order[j];
+    bool bad = false;
+    pair = checked_index(order[j], count, bad);
+    if (bad && status) atomicOr(status, kBinBadIndex);
     first = starts[j];
     const int64_t next = j + 1 < count ? starts[j + 1] : total;
     area = int(min<int64_t>(next - first, INT_MAX));
@@ -294,7 +299,10 @@ __global__ __launch_bounds__(256) void emit_sorted_kernel(
 
 // Tile ranges from the tile-sorted entries. Packed: the entries are
 // tile id << rank_bits | depth rank keys, and this pass also writes the
-// point list, point_list[i] = order[rank].
+// point list, point_list[i] = order[rank]. Either way every point-list
+// entry is checked against the pair count `count` before the compositors
+// dereference it: a depth rank or pair index outside [0, count) is replaced
+// by 0 and sets kBinBadIndex in `status` (if given).
 template <bool Packed>
 __global__ __launch_bounds__(256) void find_tile_ranges_kernel(int64_t capacity,
                                                                const int64_t* __restrict__ live,
@@ -303,13 +311,24 @@ __global__ __launch_bounds__(256) void find_tile_ranges_kernel(int64_t capacity,
                                                                int2* __restrict__ ranges,
                                                                int rank_bits,
                                                                const int* __restrict__ order,
-                                                               int* __restrict__ point_list) {
+                                                               int* __restrict__ point_list,
+                                                               int64_t count,
+                                                               uint32_t* status) {
   const int64_t m = live ? min(capacity, max(*live, int64_t(0))) : capacity;
   const int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x;
   if (i >= m) return;
   const uint32_t key = ids[i];
   const uint32_t tile = Packed ? key >> rank_bits : key;
-  if constexpr (Packed) point_list[i] = order[key & ((1u << rank_bits) - 1u)];
+  bool bad = false;
+  if constexpr (Packed) {
+    const int rank = checked_index(packed_rank(key, rank_bits), count, bad);
+    point_list[i] = checked_index(order[rank], count, bad);
+  } else {
+    const int pair = point_list[i];
+    const int safe = checked_index(pair, count, bad);
+    if (bad) point_list[i] = safe;
+  }
+  if (bad && status) atomicOr(status, kBinBadIndex);
   const bool own = tile < uint64_t(tiles);
   if (i == 0) {
     if (own) ranges[tile].x = 0;
@@ -540,7 +559,7 @@ namespace {
 // count when V is unknown); when those ranks and the tile ids fit in 32 bits
 // together, the entries travel as packed keys (emit_sorted_kernel<true>).
 int bin_tiles(const int32_t* order, const int64_t* starts, const int32_t* rects, int64_t count,
-              int64_t m, const int64_t* live, uint32_t* overflow, int64_t images, int32_t width,
+              int64_t m, const int64_t* live, uint32_t* status, int64_t images, int32_t width,
               int32_t height, int32_t* point_list, int32_t* ranges, int64_t visible,
               void* workspace, size_t workspace_bytes, hipStream_t s) {
   GS_REQUIRE(count >= 0 && count <= INT_MAX, GS_ERR_OVERFLOW, "too many projected primitives");
@@ -550,8 +569,8 @@ int bin_tiles(const int32_t* order, const int64_t* starts, const int32_t* rects,
   const int tw = tiles_x(width), th = tiles_y(height);
   const int64_t tiles = images * int64_t(tw) * int64_t(th);
   GS_REQUIRE(tiles <= INT_MAX, GS_ERR_OVERFLOW, "image tile count exceeds int32");
-  if (overflow) {
-    clear_flag_kernel<<<1, 64, 0, s>>>(overflow);
+  if (status) {
+    clear_flag_kernel<<<1, 64, 0, s>>>(status);
     GS_LAUNCHED("clear_flag_kernel");
   }
   if (tiles == 0) return GS_OK;
@@ -573,38 +592,38 @@ int bin_tiles(const int32_t* order, const int64_t* starts, const int32_t* rects,
     GS_REQUIRE(order && starts && rects, GS_ERR_ARGUMENT, "null pointer passed to gs_bin_tiles");
     if (m == 0) {  // a zero capacity still reports an overflowing emission
       emit_sorted_kernel<false><<<unsigned(ceil_div(count, 256)), 256, 0, s>>>(
-          count, 0, live, overflow, tw, order, starts, rect_rows, nullptr, nullptr, 0);
+          count, 0, live, status, tw, order, starts, rect_rows, nullptr, nullptr, 0);
       GS_LAUNCHED("emit_sorted_kernel");
       return GS_OK;
     }
     GS_REQUIRE(point_list, GS_ERR_ARGUMENT, "null point list");
     if (packed) {
       emit_sorted_kernel<true><<<unsigned(ceil_div(count, 256)), 256, 0, s>>>(
-          count, m, live, overflow, tw, order, starts, rect_rows, w.tile_ids, nullptr,
+          count, m, live, status, tw, order, starts, rect_rows, w.tile_ids, nullptr,
           rank_bits);
     } else {
       emit_sorted_kernel<false><<<unsigned(ceil_div(count, 256)), 256, 0, s>>>(
-          count, m, live, overflow, tw, order, starts, rect_rows, w.tile_ids, w.tile_values, 0);
+          count, m, live, status, tw, order, starts, rect_rows, w.tile_ids, w.tile_values, 0);
     }
     GS_LAUNCHED("emit_sorted_kernel");
   }
   {
     ProfileScope prof(GS_PROF_SORT, s);
     // Stable on the tile bits: entries of a tile keep their depth order.
-    const int status =
+    const int sorted =
         packed ? radix_sort<uint32_t>(w.tile_ids, w.tile_sorted, nullptr, nullptr, m, rank_bits,
                                       rank_bits + tile_bits, w.sort, s, live)
                : radix_sort<uint32_t>(w.tile_ids, w.tile_sorted, w.tile_values, point_list, m, 0,
                                       tile_bits, w.sort, s, live);
-    if (status != GS_OK) return status;
+    if (sorted != GS_OK) return sorted;
   }
   ProfileScope prof(GS_PROF_BINNING, s);
   if (packed) {
     find_tile_ranges_kernel<true><<<unsigned(ceil_div(m, 256)), 256, 0, s>>>(
-        m, live, tiles, w.tile_sorted, r, rank_bits, order, point_list);
+        m, live, tiles, w.tile_sorted, r, rank_bits, order, point_list, count, status);
   } else {
     find_tile_ranges_kernel<false><<<unsigned(ceil_div(m, 256)), 256, 0, s>>>(
-        m, live, tiles, w.tile_sorted, r, 0, nullptr, nullptr);
+        m, live, tiles, w.tile_sorted, r, 0, nullptr, point_list, count, status);
   }
   GS_LAUNCHED("find_tile_ranges_kernel");
   return GS_OK;
@@ -617,10 +636,10 @@ extern "C" {
 
 int gs_bin_tiles(const int32_t* order, const int64_t* starts, const int32_t* rects,
                  int64_t count, int64_t m, int64_t visible, int64_t images, int32_t width,
-                 int32_t height, int32_t* point_list, int32_t* ranges, void* workspace,
-                 size_t workspace_bytes, void* stream) {
+                 int32_t height, int32_t* point_list, int32_t* ranges, uint32_t* status,
+                 void* workspace, size_t workspace_bytes, void* stream) {
   gs::clear_error();
-  return gs::bin_tiles(order, starts, rects, count, m, nullptr, nullptr, images, width, height,
+  return gs::bin_tiles(order, starts, rects, count, m, nullptr, status, images, width, height,
                        point_list, ranges, visible, workspace, workspace_bytes,
                        static_cast<hipStream_t>(stream));
 }

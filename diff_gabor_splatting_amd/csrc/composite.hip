@@ -724,10 +724,15 @@ __global__ __launch_bounds__(kTilePixels) void tile_last_kernel(int width, int h
                           max(wave_max_last[2], wave_max_last[3]));
 }
 
+// The two compositor kernels carry the reference's kernel names
+// (renderForward / renderBackward, rasterize.cu:230, :284): tools that split
+// a trace by those names, such as the reference benchmark's kernel profile,
+// find them here too.
+//
 // Replay: also write the tile's replay list (replay + range start, see
 // append_replay) and its length (replay_counts[tile]).
 template <bool Neural, bool Replay>
-__global__ __launch_bounds__(kTilePixels, Neural ? 4 : 6) void render_forward_kernel(
+__global__ __launch_bounds__(kTilePixels, Neural ? 4 : 6) void renderForward(
     int width, int height, int tw, int th, const float* __restrict__ geometry,
     const float* __restrict__ appearance, const float* __restrict__ opacities,
     const int64_t* __restrict__ primitive_ids, const float* __restrict__ backgrounds,
@@ -940,7 +945,7 @@ __device__ __forceinline__ float classic_appearance_gradient(const float* sums, 
 // tile_last[tile], compositing each record only in the quadrants that took
 // it; tile_last is then unused.
 template <bool Neural, bool Replay>
-__global__ __launch_bounds__(kTilePixels, Neural ? 2 : 4) void render_backward_kernel(
+__global__ __launch_bounds__(kTilePixels, Neural ? 2 : 4) void renderBackward(
     int width, int height, int tw, int th, const float* __restrict__ geometry,
     const float* __restrict__ appearance, const float* __restrict__ opacities,
     const int64_t* __restrict__ primitive_ids, const float* __restrict__ backgrounds,
@@ -1259,6 +1264,65 @@ int check_render(int64_t images, int width, int height, float near_plane, float 
 }  // namespace
 }  // namespace gs
 
+namespace gs {
+namespace {
+
+// The forward compositor's launches given the tile dispatch-order buffer
+// (`tiles` ints), which gs_render_forward takes from the caller's workspace.
+int render_forward(int32_t neural, const float* geometry, const float* appearance,
+                   const float* opacities, const int64_t* primitive_ids,
+                   const float* backgrounds, const int32_t* point_list, const int32_t* ranges,
+                   int64_t images, int32_t width, int32_t height, float near_plane,
+                   float far_plane, const MapGroups<float>& out, float* state,
+                   int32_t* contributors, int32_t* replay, int32_t* replay_counts, int* order,
+                   hipStream_t s) {
+  ProfileScope prof(GS_PROF_RENDER_FWD, s);
+  const int tw = tiles_x(width), th = tiles_y(height);
+  const int tiles = int(images * tw * th);
+  const int2* r = reinterpret_cast<const int2*>(ranges);
+  tile_order_kernel<<<1, kOrderBlock, 0, s>>>(nullptr, r, tiles, order);
+  GS_LAUNCHED("tile_order_kernel");
+  int2* lists = reinterpret_cast<int2*>(replay);
+  auto launch = [&](auto kernel) {
+    kernel<<<unsigned(tiles), kTilePixels, 0, s>>>(
+        width, height, tw, th, geometry, appearance, opacities, primitive_ids, backgrounds,
+        point_list, r, order, near_plane, far_plane, out, state, contributors, lists,
+        replay_counts);
+  };
+  if (neural) {
+    if (replay) launch(renderForward<true, true>);
+    else launch(renderForward<true, false>);
+  } else {
+    if (replay) launch(renderForward<false, true>);
+    else launch(renderForward<false, false>);
+  }
+  GS_LAUNCHED("renderForward");
+  return GS_OK;
+}
+
+// Argument checks shared by both forward entry points.
+int check_render_forward(int64_t images, int32_t width, int32_t height, float near_plane,
+                         float far_plane, const float* backgrounds, const int32_t* ranges,
+                         float* const* maps, const int64_t* map_strides, const float* state,
+                         const int32_t* contributors, const int32_t* replay,
+                         int64_t replay_capacity, const int32_t* replay_counts) {
+  int status = check_render(images, width, height, near_plane, far_plane);
+  if (status != GS_OK) return status;
+  GS_REQUIRE(backgrounds && ranges && maps && map_strides && state && contributors,
+             GS_ERR_ARGUMENT, "null pointer passed to gs_render_forward");
+  GS_REQUIRE(!replay == !replay_counts, GS_ERR_ARGUMENT,
+             "replay and replay_counts must both be given or both be null");
+  GS_REQUIRE(!replay || (replay_capacity >= 0 && replay_capacity <= kReplayPositionMask),
+             GS_ERR_OVERFLOW, "replay lists need a point list of at most %d entries, got %lld",
+             kReplayPositionMask, static_cast<long long>(replay_capacity));
+  for (int g = 0; g < kMapGroups; ++g)
+    GS_REQUIRE(maps[g], GS_ERR_ARGUMENT, "null map output group %d", g);
+  return GS_OK;
+}
+
+}  // namespace
+}  // namespace gs
+
 extern "C" {
 
 size_t gs_render_workspace_size(int64_t images, int32_t width, int32_t height) {
@@ -1276,45 +1340,20 @@ int gs_render_forward(int32_t neural, const float* geometry, const float* appear
                       void* workspace, size_t workspace_bytes, void* stream) {
   using namespace gs;
   clear_error();
-  int status = check_render(images, width, height, near_plane, far_plane);
+  const int status =
+      check_render_forward(images, width, height, near_plane, far_plane, backgrounds, ranges,
+                           maps, map_strides, state, contributors, replay, replay_capacity,
+                           replay_counts);
   if (status != GS_OK) return status;
-  GS_REQUIRE(backgrounds && ranges && maps && map_strides && state && contributors,
-             GS_ERR_ARGUMENT, "null pointer passed to gs_render_forward");
-  GS_REQUIRE(!replay == !replay_counts, GS_ERR_ARGUMENT,
-             "replay and replay_counts must both be given or both be null");
-  GS_REQUIRE(!replay || (replay_capacity >= 0 && replay_capacity <= kReplayPositionMask),
-             GS_ERR_OVERFLOW, "replay lists need a point list of at most %d entries, got %lld",
-             kReplayPositionMask, static_cast<long long>(replay_capacity));
-  for (int g = 0; g < kMapGroups; ++g)
-    GS_REQUIRE(maps[g], GS_ERR_ARGUMENT, "null map output group %d", g);
-  const MapGroups<float> out = map_groups(maps, map_strides);
   const size_t need = gs_render_workspace_size(images, width, height);
   GS_REQUIRE(workspace && workspace_bytes >= need, GS_ERR_WORKSPACE,
              "render forward needs %zu workspace bytes, got %zu", need, workspace_bytes);
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  ProfileScope prof(GS_PROF_RENDER_FWD, s);
-  const int tw = tiles_x(width), th = tiles_y(height);
-  const int tiles = int(images * tw * th);
-  const int2* r = reinterpret_cast<const int2*>(ranges);
+  const int64_t tiles = images * tiles_x(width) * tiles_y(height);
   RenderWorkspace w = render_layout(workspace, tiles);
-  tile_order_kernel<<<1, kOrderBlock, 0, s>>>(nullptr, r, tiles, w.order);
-  GS_LAUNCHED("tile_order_kernel");
-  int2* lists = reinterpret_cast<int2*>(replay);
-  auto launch = [&](auto kernel) {
-    kernel<<<unsigned(tiles), kTilePixels, 0, s>>>(
-        width, height, tw, th, geometry, appearance, opacities, primitive_ids, backgrounds,
-        point_list, r, w.order, near_plane, far_plane, out, state, contributors, lists,
-        replay_counts);
-  };
-  if (neural) {
-    if (replay) launch(render_forward_kernel<true, true>);
-    else launch(render_forward_kernel<true, false>);
-  } else {
-    if (replay) launch(render_forward_kernel<false, true>);
-    else launch(render_forward_kernel<false, false>);
-  }
-  GS_LAUNCHED("render_forward_kernel");
-  return GS_OK;
+  return render_forward(neural, geometry, appearance, opacities, primitive_ids, backgrounds,
+                        point_list, ranges, images, width, height, near_plane, far_plane,
+                        map_groups(maps, map_strides), state, contributors, replay,
+                        replay_counts, w.order, static_cast<hipStream_t>(stream));
 }
 
 int gs_render_backward(int32_t neural, const float* geometry, const float* appearance,
@@ -1366,13 +1405,13 @@ int gs_render_backward(int32_t neural, const float* geometry, const float* appea
         grad_backgrounds);
   };
   if (neural) {
-    if (replay) launch(render_backward_kernel<true, true>);
-    else launch(render_backward_kernel<true, false>);
+    if (replay) launch(renderBackward<true, true>);
+    else launch(renderBackward<true, false>);
   } else {
-    if (replay) launch(render_backward_kernel<false, true>);
-    else launch(render_backward_kernel<false, false>);
+    if (replay) launch(renderBackward<false, true>);
+    else launch(renderBackward<false, false>);
   }
-  GS_LAUNCHED("render_backward_kernel");
+  GS_LAUNCHED("renderBackward");
   return GS_OK;
 }
 

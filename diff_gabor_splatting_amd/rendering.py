@@ -65,7 +65,7 @@ class Composite(torch.autograd.Function):
             geometry, appearance, opacities, primitive_ids, image_ids, radii, backgrounds,
             width, height, neural, near_plane, far_plane, outputs=outputs, overlap=overlap,
             capacity=None if bounded is None else bounded.max_intersections,
-            flags=None if bounded is None else bounded._overflows, replay=needs_grad,
+            flags=None if bounded is None else bounded.record_binning, replay=needs_grad,
             violations=violations,
         )
         replay = replay[0] if replay else None
@@ -291,19 +291,36 @@ class FixedCapacity:
       ``projected_means`` and the id tensors hold the V packed rows first,
       then rows of radius 0, projected mean 0 and id -1.
 
-    ``check()``, called outside any capture, reads every recorded verdict
-    and flag in one synchronisation and raises ValueError (violated value
-    contracts, as ``check_values`` would) or RuntimeError (capacity
-    exceeded); it then forgets them and returns the largest intersection
-    count it saw (0 if none), a guide for sizing the capacity.
+    ``check()``, called outside any capture, waits for the device and raises
+    ValueError (violated value contracts, as ``check_values`` would) or
+    RuntimeError (capacity exceeded, or binning found an index out of
+    range); otherwise it returns the largest intersection count (0 if
+    none), a guide for sizing the capacity. It reports everything rendered
+    since the previous check, then starts afresh.
+
+    The verdicts live in one small device tensor per GPU, allocated (and
+    zeroed) outside any capture - when the context is created, or on first
+    use on another device. Each render, eager or captured, folds its
+    violation word, overflow flag and intersection count into it with
+    device operations, so a captured graph folds them again on every
+    replay: a check made right after capturing reads zeros (nothing ran
+    yet), one made after replays reports those replays.
     """
+
+    # Status words per device (int64): overflow flags OR-ed, largest
+    # intersection count, then one OR-ed violation word per distinct list of
+    # checked tensor names (classic and neural renders name them differently).
+    _OVERFLOW, _PEAK, _FIRST_SLOT = 0, 1, 2
+    _SLOTS = 6
 
     def __init__(self, max_intersections: int):
         if type(max_intersections) is not int or not 0 < max_intersections <= _native.INT_MAX:
             raise ValueError("max_intersections must be a positive int32 integer")
         self.max_intersections = max_intersections
-        self._overflows: list[tuple[torch.Tensor, torch.Tensor]] = []
-        self._values: list[tuple[torch.Tensor, list[str]]] = []
+        self._status: dict[torch.device, torch.Tensor] = {}
+        self._names: list[tuple[str, ...]] = []
+        if torch.cuda.is_available() and not torch.cuda.is_current_stream_capturing():
+            self._status_on(torch.device("cuda", torch.cuda.current_device()))
 
     def __enter__(self) -> "FixedCapacity":
         _FIXED_CAPACITY.append(self)
@@ -312,30 +329,69 @@ class FixedCapacity:
     def __exit__(self, *exc) -> None:
         _FIXED_CAPACITY.remove(self)
 
+    def _status_on(self, device: torch.device) -> torch.Tensor:
+        status = self._status.get(device)
+        if status is None:
+            if torch.cuda.is_current_stream_capturing():
+                raise RuntimeError(
+                    f"fixed_capacity has no status words on {device}: create the context (or "
+                    "render once eagerly) on that device before capturing"
+                )
+            status = torch.zeros(self._FIRST_SLOT + self._SLOTS, dtype=torch.int64,
+                                 device=device)
+            self._status[device] = status
+        return status
+
+    def record_binning(self, overflow: torch.Tensor, total: torch.Tensor) -> None:
+        """Fold one render's overflow flag (int32 [1]) and intersection count
+        (int64 [1]) into the device status (device operations only)."""
+        status = self._status_on(overflow.device)
+        status[self._OVERFLOW:self._OVERFLOW + 1].bitwise_or_(overflow)
+        peak = status[self._PEAK:self._PEAK + 1]
+        torch.maximum(peak, total, out=peak)
+
+    def record_violations(self, word: torch.Tensor, names) -> None:
+        """Fold one render's gs_check_values word (int32 [1]) into the slot of
+        its tensor names (device operation only)."""
+        names = tuple(names)
+        if names not in self._names:
+            if len(self._names) == self._SLOTS:
+                raise RuntimeError("fixed_capacity: too many distinct input layouts")
+            self._names.append(names)
+        slot = self._FIRST_SLOT + self._names.index(names)
+        self._status_on(word.device)[slot:slot + 1].bitwise_or_(word)
+
     def check(self) -> int:
-        words = [word for word, _ in self._values]
-        for overflow, total in self._overflows:
-            words += [overflow, total]
-        if not words:
-            return 0
-        host = torch.cat([w.reshape(1).to(torch.int64) for w in words]).tolist()
-        values, rest = host[: len(self._values)], host[len(self._values):]
-        overflows, totals = rest[0::2], rest[1::2]
-        names = [n for _, n in self._values]
-        self._values, self._overflows = [], []
+        if torch.cuda.is_available() and torch.cuda.is_current_stream_capturing():
+            raise RuntimeError("fixed_capacity.check() cannot run during graph capture")
+        overflow, peak, words = 0, 0, [0] * self._SLOTS
+        for device, status in self._status.items():
+            # Renders and replays may be queued on any stream of the device:
+            # wait for all of them, and let the clearing finish before any
+            # later render on another stream folds in its flags.
+            torch.cuda.synchronize(device)
+            host = status.tolist()
+            status.zero_()
+            torch.cuda.synchronize(device)
+            overflow |= host[self._OVERFLOW]
+            peak = max(peak, host[self._PEAK])
+            words = [w | h for w, h in zip(words, host[self._FIRST_SLOT:])]
         messages = []
-        for word, tensor_names in zip(values, names):
-            for message in describe_violations(tensor_names, word & 0xFFFFFFFF):
+        for names, word in zip(self._names, words):
+            for message in describe_violations(names, word & 0xFFFFFFFF):
                 if message not in messages:
                     messages.append(message)
         if messages:
             raise ValueError("; ".join(messages))
-        if any(overflows):
+        if overflow & _native.BINNING_BAD_INDEX:
+            raise RuntimeError("binning produced an index out of range; the affected tiles "
+                               "were rendered from substitute records")
+        if overflow:
             raise RuntimeError(
-                f"tile intersections ({max(totals)}) exceeded the fixed capacity of "
+                f"tile intersections ({peak}) exceeded the fixed capacity of "
                 f"{self.max_intersections}; the affected renders dropped their deepest records"
             )
-        return max(totals, default=0)
+        return peak
 
 
 _FIXED_CAPACITY: list[FixedCapacity] = []
@@ -463,7 +519,7 @@ def render(
                 [value for value, _ in tensors.values()], quaternions, scales, opacities,
                 view_matrices, intrinsics, weights, magnitudes,
             )
-        bounded._values.append((word, list(tensors)))
+            bounded.record_violations(word, list(tensors))
 
     views = view_matrices.reshape(scenes, cameras, 4, 4)
     cameras_k = intrinsics.reshape(scenes, cameras, 3, 3)

@@ -274,16 +274,25 @@ int gs_bin_order(const float* geometry, const int32_t* radii, const int64_t* ima
 /* Scratch bytes for gs_bin_tiles over m intersections. */
 size_t gs_bin_tiles_workspace_size(int64_t m);
 
+/* Binning status bits (the `status` word of gs_bin_tiles and the overflow
+ * word of gs_bin_tiles_bounded). */
+#define GS_BIN_OVERFLOW 1u  /* more intersections than the point list holds */
+#define GS_BIN_BAD_INDEX 2u /* a sort produced a rank or pair index outside
+                               [0, count); pair 0 was substituted for it */
+
 /* Stage 2 from stage 1's order, starts and rects: emit in depth order,
  * sort by tile id, find ranges. point_list [m] int32, ranges
  * [images*tw*th, 2] int32 ((0,0) for empty tiles). `visible` is stage 1's
  * V, or -1 if unknown: when bits(tiles) + bits(V) <= 32 the entries are
  * sorted as single 32-bit (tile id, depth rank) keys, otherwise as (tile
- * id, pair index) pairs; the result is the same. */
+ * id, pair index) pairs; the result is the same. Every index taken from a
+ * sort output is range-checked before it is dereferenced or written to the
+ * point list; `status` (a device uint32, or null) is cleared, then gets
+ * GS_BIN_BAD_INDEX if a check failed. */
 int gs_bin_tiles(const int32_t* order, const int64_t* starts, const int32_t* rects,
                  int64_t count, int64_t m, int64_t visible, int64_t images, int32_t width,
-                 int32_t height, int32_t* point_list, int32_t* ranges, void* workspace,
-                 size_t workspace_bytes, void* stream);
+                 int32_t height, int32_t* point_list, int32_t* ranges, uint32_t* status,
+                 void* workspace, size_t workspace_bytes, void* stream);
 
 /* gs_bin_tiles without the host's intersection count, for callers that
  * cannot synchronise (HIP graph capture): the point list and workspace are
@@ -292,9 +301,10 @@ int gs_bin_tiles(const int32_t* order, const int64_t* starts, const int32_t* rec
  * *intersections, the device word gs_bin_order wrote. The first
  * min(count, capacity) entries of the depth-first emission are binned and
  * ranges cover exactly those. *overflow (a device uint32) is cleared, then
- * set to 1 when the count exceeds the capacity: the deepest records were
- * then dropped from their tiles. No counterpart in the reference, which
- * reads the count on the host (rasterize.cu:466-469). */
+ * gets GS_BIN_OVERFLOW when the count exceeds the capacity (the deepest
+ * records were then dropped from their tiles) and GS_BIN_BAD_INDEX as in
+ * gs_bin_tiles. No counterpart in the reference, which reads the count on
+ * the host (rasterize.cu:466-469). */
 int gs_bin_tiles_bounded(const int32_t* order, const int64_t* starts, const int32_t* rects,
                          int64_t count, int64_t capacity, const int64_t* intersections,
                          int64_t images, int32_t width, int32_t height, int32_t* point_list,

@@ -49,7 +49,7 @@ def appearance_color(a: torch.Tensor, s: torch.Tensor, dirs: torch.Tensor, neura
 
 def composite(geometry, appearance, opacities, primitive_ids, image_ids, radii, backgrounds,
               width, height, neural, near_plane, far_plane, lists=None, margins=None,
-              taken=None):
+              taken=None, stopped=None):
     """Differentiable forward compositor.
 
     Returns maps [I,H,W,9], point_list (np.int32), ranges (np.int32 [tiles,2]),
@@ -63,6 +63,10 @@ def composite(geometry, appearance, opacities, primitive_ids, image_ids, radii, 
     longest]: for the k-th record of each tile's list, bit q is set when a
     pixel of the tile's 8x8 quadrant q = 2 * (y >= 8) + (x >= 8) took it
     (contributed to its maps, rasterize.cu:254-271).
+    If ``stopped`` is a dict, stopped["pixels"] receives bool [I,H,W]: the
+    pixels whose walk ended on the transmittance rule - an accepted record
+    that would have taken T below 1e-4 (rasterize.cu:254-255) - rather than
+    at the end of their tile's list.
     """
     dtype = geometry.dtype
     images = backgrounds.shape[0]
@@ -99,6 +103,7 @@ def composite(geometry, appearance, opacities, primitive_ids, image_ids, radii, 
     m1 = torch.zeros(tiles, TILE * TILE, dtype=dtype)
     m2 = torch.zeros(tiles, TILE * TILE, dtype=dtype)
     done = ~inside
+    ended = torch.zeros(tiles, TILE * TILE, dtype=torch.bool)
     last = torch.zeros(tiles, TILE * TILE, dtype=torch.int64)
     margin = torch.full((tiles, TILE * TILE), math.inf, dtype=torch.float64)
     quadrant_bit = 1 << (2 * ((offs // TILE) >= 8).long() + ((offs % TILE) >= 8).long())
@@ -145,6 +150,7 @@ def composite(geometry, appearance, opacities, primitive_ids, image_ids, radii, 
                 margin = torch.where(walked, torch.minimum(margin, local), margin)
         stop = accept & (T * (1 - alpha) < 1e-4)
         done = done | stop
+        ended = ended | stop
         take = accept & ~stop
         if taken is not None:
             bits = torch.where(take & inside, quadrant_bit, torch.zeros_like(quadrant_bit))
@@ -185,4 +191,6 @@ def composite(geometry, appearance, opacities, primitive_ids, image_ids, radii, 
         margins["pixels"] = margin.reshape(-1)[keep][order].reshape(images, height, width)
     if taken is not None:
         taken["quadrants"] = quadrants
+    if stopped is not None:
+        stopped["pixels"] = ended.reshape(-1)[keep][order].reshape(images, height, width)
     return maps, point_list, ranges, state, contributors.numpy().astype(np.int32)

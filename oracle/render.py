@@ -93,7 +93,8 @@ def records(means, quaternions, scales, opacities, appearance, view_matrices, in
 
 def render(means, quaternions, scales, opacities, appearance, view_matrices, intrinsics,
            width, height, backgrounds=None, packed=False, near_plane=0.2, far_plane=100.0,
-           neural=False, sh_degree=None, radii=None, lists=None, margins=None, taken=None):
+           neural=False, sh_degree=None, radii=None, lists=None, margins=None, taken=None,
+           stopped=None):
     """Returns maps [..., C, H, W, 9], meta (as the reference) and the
     compositor's auxiliary outputs (point_list, ranges, state, contributors)."""
     rec = records(
@@ -108,9 +109,12 @@ def render(means, quaternions, scales, opacities, appearance, view_matrices, int
         rec["geometry"], rec["appearance"], rec["opacities"], rec["primitive_ids"],
         rec["image_ids"], rec["radii"], backgrounds.reshape(scenes * cameras, 3), width, height,
         neural, near_plane, far_plane, lists=lists, margins=margins, taken=taken,
+        stopped=stopped,
     )
     if margins is not None:
         margins["pixels"] = margins["pixels"].reshape(batch + (cameras, height, width))
+    if stopped is not None:
+        stopped["pixels"] = stopped["pixels"].reshape(batch + (cameras, height, width))
     maps = maps.reshape(batch + (cameras, height, width, 9))
     selected = rec["selected"]
     stride = max(n, 1)

@@ -185,3 +185,63 @@ def test_bounded_render_of_an_empty_view(method):
     assert torch.equal(actual, expected)
     background = values["backgrounds"][:, :, None, None, :].expand_as(actual[..., :3])
     torch.testing.assert_close(actual[..., :3], background)
+
+
+def test_check_reports_each_replay_of_a_captured_graph():
+    """A check right after capture reads nothing (no kernel ran yet); every
+    later check reports the replays since the one before: within capacity
+    it returns the intersection count, a replay that overflows the capacity
+    or carries a violated value contract raises."""
+    from diff_gabor_splatting_amd import fixed_capacity
+
+    method = "classic"
+    base, options = scene(method, seed=11)
+    static = {k: v.detach().clone() for k, v in base.items()}
+    probe = fixed_capacity(1 << 20)
+    with probe:
+        renderer(method)(**static, **options)
+    exact = probe.check()
+    assert exact > 0
+
+    def step():
+        return maps_from_result(renderer(method)(**static, **options, validate=True))
+
+    capacity = fixed_capacity(exact)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with capacity, torch.cuda.stream(side):
+        step()
+    torch.cuda.current_stream().wait_stream(side)
+    assert capacity.check() == exact  # the eager warm-up render
+    graph = torch.cuda.CUDAGraph()
+    with capacity, torch.cuda.graph(graph):
+        static_maps = step()
+    assert capacity.check() == 0  # captured, not yet replayed
+
+    print("replay within capacity", flush=True)
+    graph.replay()
+    expected = maps_from_result(renderer(method)(**base, **options))
+    assert torch.equal(static_maps, expected)
+    assert capacity.check() == exact
+    assert capacity.check() == 0  # nothing replayed since
+
+    print("replay past capacity", flush=True)
+    with torch.no_grad():
+        static["scales"].mul_(3.0)  # larger footprints: more tile intersections
+    graph.replay()
+    with pytest.raises(RuntimeError, match=rf"exceeded the fixed capacity of {exact}"):
+        capacity.check()
+
+    print("replay within capacity again", flush=True)
+    with torch.no_grad():
+        static["scales"].copy_(base["scales"])
+    graph.replay()
+    assert capacity.check() == exact
+
+    print("replay with invalid values", flush=True)
+    with torch.no_grad():
+        static["opacities"][0, 4] = 1.5
+    graph.replay()
+    with pytest.raises(ValueError, match="opacities must lie in"):
+        capacity.check()
+    assert capacity.check() == 0

@@ -35,8 +35,8 @@ def to_u64(t):
     ((0, 32), True), ((19, 32), False), ((0, 13), True), ((5, 12), False),
 ])
 def test_sort32_is_stable_radix_order(native, m, bits, with_values):
-    """The 32-bit sort of the binning stages (single-kernel digit passes with
-    look-back), against numpy's stable argsort: partial last spans, both
+    """The 32-bit sort of the binning stages (reduce-then-scan digit
+    passes), against numpy's stable argsort: partial last spans, both
     span sizes (4,194,305 keys take 4096-key spans), keys alone and with
     values, partial bit ranges, many ties and skewed digits."""
     rng = np.random.default_rng(m + 7 * bits[0])
@@ -144,6 +144,41 @@ def test_depth_first_binning_is_bit_exact(native, seed, q, width, height, images
     if seed == 8:
         tile_bits = (images * 120 * 68 - 1).bit_length()
         assert tile_bits + visible.bit_length() <= 32 < tile_bits + q.bit_length()
+
+
+def test_bin_tiles_flags_sort_outputs_out_of_range(native):
+    """The binning consumers range-check what the depth sort produced: an
+    `order` entry outside [0, count) - planted on the host here - is
+    replaced by pair 0 and reported as GS_BIN_BAD_INDEX instead of being
+    dereferenced, with packed (tile, rank) keys (V known) and with (tile,
+    pair) pairs (V unknown, bits(tiles) + bits(count) > 32)."""
+    width, height, images, q = 1920, 1080, 1, 600_000
+    geometry, radii, image_ids = random_geometry(9, q, width, height, images)
+    radii[: int(0.6 * q)] = np.minimum(radii[: int(0.6 * q)], 0)
+    g, r, ids = (torch.from_numpy(a).to(DEVICE) for a in (geometry, radii, image_ids))
+    order, starts, rects, totals = native.bin_order(g, r, ids, width, height)
+    m, visible = totals.tolist()
+    tile_bits = (120 * 68 - 1).bit_length()
+    assert tile_bits + visible.bit_length() <= 32 < tile_bits + q.bit_length()
+    _, ok_list, ok_ranges = oracle_binning.bin_pairs(geometry, radii, image_ids, images, width,
+                                                     height)
+    status = torch.full((1,), -1, dtype=torch.int32, device=DEVICE)
+    corrupt = order.clone()
+    corrupt[5], corrupt[visible // 2] = q + 7, -3
+    for known in (visible, -1):
+        print(f"bin_tiles guard visible={known}", flush=True)
+        point_list, ranges = native.bin_tiles(order, starts, rects, images, width, height, m,
+                                              known, status=status)
+        assert int(status) == 0
+        np.testing.assert_array_equal(point_list.cpu().numpy(), ok_list)
+        np.testing.assert_array_equal(ranges.cpu().numpy(), ok_ranges)
+        point_list, ranges = native.bin_tiles(corrupt, starts, rects, images, width, height, m,
+                                              known, status=status)
+        assert int(status) == native.BINNING_BAD_INDEX
+        listed = point_list.cpu().numpy()
+        assert listed.min() >= 0 and listed.max() < q
+        bounds = ranges.cpu().numpy()
+        assert bounds.min() >= 0 and bounds.max() <= m
 
 
 def test_ranges_of_empty_list_are_zero(native):

@@ -55,13 +55,25 @@ def test_opacity_cutoff_and_saturation(method, opacity):
     values["quaternions"][..., 0] = 1
     values["means"][..., :2] = 0
     values = as64(values)
-    actual, _, aux = oracle_maps(method, values)
+    stopped = {}
+    actual, _, aux = oracle_maps(method, values, stopped=stopped)
     torch.testing.assert_close(actual, pixel_reference(method, values), **TOLERANCE)
     if opacity == 1.0:
         # Alpha 0.99 then 0.85s: T goes 1 -> 1e-2 -> 1.5e-3 -> 2.25e-4; the
         # fourth would take it to 3.4e-5 < 1e-4, so exactly three contribute
         # at the centre pixel and the next stops it.
         assert int(aux["contributors"][0, 4, 4]) == 3
+        assert bool(stopped["pixels"][0, 0, 4, 4])
+        # The same three alone leave T = 2.25e-4 at the centre: the walk ends
+        # with the list, not on the transmittance rule.
+        first = {k: (v if k in ("view_matrices", "intrinsics", "backgrounds")
+                     else v[:, :3].detach().clone().requires_grad_()) for k, v in values.items()}
+        three = {}
+        _, _, aux3 = oracle_maps(method, first, stopped=three)
+        assert int(aux3["contributors"][0, 4, 4]) == 3
+        assert not bool(three["pixels"].any())
+    else:
+        assert not bool(stopped["pixels"].any())
 
 
 @pytest.mark.parametrize("method", ["classic", "neural"])
