@@ -10,7 +10,10 @@ Prints ONE JSON line. Besides the driver's contract fields it carries:
                 region): algorithmic bytes per launch / average launch time,
                 both measured in this run (HIP events on the launch stream);
   cpu_baseline  the CPU oracle (torch fp32, autograd backward) timed on this
-                host over a bounded crop of the same workload;
+                host on config 0 at full frame (the designated CPU config),
+                next to the GPU's time for the same workload, plus a
+                labelled secondary figure on a crop of config 4;
+  per_config    ms/step and Mpix/s of the other BASELINE configs, same run;
   kernels       per-family average milliseconds per step.
 """
 
@@ -182,6 +185,62 @@ def algorithmic_bytes(kind: str, neural: bool, pixels: int, records: int, pairs:
     return int(total)
 
 
+def prepare(index: int, device, validate: bool):
+    """Seeded inputs of one config on the device and a closure running one
+    fwd+bwd step on them through the public API."""
+    from diff_gabor_splatting_amd import rasterize_gabors, rasterize_neural_gabors
+
+    cfg = CONFIGS[index]
+    cpu_values = make_scene(index)
+    values = {k: v.to(device).contiguous() for k, v in cpu_values.items()}
+    for k, v in values.items():
+        v.requires_grad_(k not in CAMERA_KEYS)
+    renderer = rasterize_neural_gabors if cfg["neural"] else rasterize_gabors
+    options = dict(width=cfg["width"], height=cfg["height"], packed=cfg["packed"],
+                   validate=validate)
+    if not cfg["neural"]:
+        options["sh_degree"] = cfg["sh"]
+    params = [v for v in values.values() if v.requires_grad]
+
+    def step():
+        for p in params:
+            p.grad = None
+        rgb, alpha, meta = renderer(**values, **options)
+        _loss(rgb, alpha, meta, cfg["channels"]).backward()
+        return meta
+
+    return cpu_values, values, renderer, options, step
+
+
+def time_steps(step, steps: int, warmup: int) -> float:
+    """Milliseconds per step over `steps` steps after `warmup` untimed ones,
+    with the device synchronised on both sides of the timed region."""
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    start = time.perf_counter()
+    for _ in range(steps):
+        step()
+    torch.cuda.synchronize()
+    return (time.perf_counter() - start) * 1000 / steps
+
+
+def per_config_times(skip: int, steps: int, warmup: int, device, validate: bool) -> dict:
+    """ms/step and Mpix/s of every other BASELINE config, measured in this run."""
+    out = {}
+    for index, cfg in CONFIGS.items():
+        if index == skip:
+            continue
+        *_, step = prepare(index, device, validate)
+        ms = time_steps(step, steps, warmup)
+        pixels = cfg["scenes"] * cfg["cameras"] * cfg["width"] * cfg["height"]
+        out[str(index)] = {"workload": cfg["name"], "ms_per_step": round(ms, 4),
+                           "mpix_per_s": round(pixels / (ms / 1000) / 1e6, 3)}
+        del step
+        torch.cuda.empty_cache()
+    return out
+
+
 def main(argv=None):
     parser = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     parser.add_argument("--gpus", type=int, default=1)
@@ -191,10 +250,11 @@ def main(argv=None):
     parser.add_argument("--validate", action="store_true",
                         help="run the numerical input checks inside every step")
     parser.add_argument("--cpu-baseline", type=int, default=1,
-                        help="1: time the CPU oracle on a crop of the workload (rank 0)")
-    parser.add_argument("--cpu-crop", type=int, default=32, help="crop edge in pixels")
-    parser.add_argument("--cpu-surfels", type=int, default=0,
-                        help="surfels used by the CPU baseline (0 = all of the workload)")
+                        help="1: time the CPU oracle on config 0 (and a crop of config 4)")
+    parser.add_argument("--per-config", type=int, default=1,
+                        help="1: also time every other config (ms/step), same run")
+    parser.add_argument("--cpu-crop", type=int, default=32,
+                        help="edge in pixels of the secondary config-4 CPU crop (0: skip it)")
     parser.add_argument("--copy-calibration", action="store_true",
                         help="only copy 1 GiB device-to-device three times and exit; the "
                              "rocprof FETCH_SIZE/WRITE_SIZE of this copy scales the counters")
@@ -211,37 +271,12 @@ def main(argv=None):
         return 2
     if args.copy_calibration:
         return copy_calibration()
-    from diff_gabor_splatting_amd import _native, rasterize_gabors, rasterize_neural_gabors
+    from diff_gabor_splatting_amd import _native
 
     cfg = CONFIGS[args.config]
     device = torch.device("cuda:0")
-    cpu_values = make_scene(args.config)
-    values = {k: v.to(device).contiguous() for k, v in cpu_values.items()}
-    for k, v in values.items():
-        v.requires_grad_(k not in CAMERA_KEYS)
-    renderer = rasterize_neural_gabors if cfg["neural"] else rasterize_gabors
-    options = dict(width=cfg["width"], height=cfg["height"], packed=cfg["packed"],
-                   validate=args.validate)
-    if not cfg["neural"]:
-        options["sh_degree"] = cfg["sh"]
-    params = [v for v in values.values() if v.requires_grad]
-
-    def step():
-        for p in params:
-            p.grad = None
-        rgb, alpha, meta = renderer(**values, **options)
-        _loss(rgb, alpha, meta, cfg["channels"]).backward()
-        return meta
-
-    for _ in range(args.warmup):
-        step()
-    torch.cuda.synchronize()
-    start = time.perf_counter()
-    for _ in range(args.steps):
-        meta = step()
-    torch.cuda.synchronize()
-    elapsed = time.perf_counter() - start
-    ms_per_step = elapsed * 1000 / args.steps
+    cpu_values, values, renderer, options, step = prepare(args.config, device, args.validate)
+    ms_per_step = time_steps(step, args.steps, args.warmup)
     # Per-family kernel times from HIP events on the launch stream, over the
     # same number of steps run again after the timed region (the events
     # themselves cost host time, so they stay out of the timed steps).
@@ -312,8 +347,17 @@ def main(argv=None):
         "kernels": {k: round(v["ms_per_step"], 4) for k, v in kernels.items()},
         "gpu": torch.cuda.get_device_name(device),
     }
+    del values, step
+    torch.cuda.empty_cache()
+    if args.per_config:
+        result["per_config"] = per_config_times(args.config, args.steps, args.warmup, device,
+                                                args.validate)
     if args.cpu_baseline:
-        result["cpu_baseline"] = cpu_baseline(cpu_values, cfg, args)
+        gpu_config0 = result.get("per_config", {}).get("0", {}).get("ms_per_step")
+        if args.config == 0:
+            gpu_config0 = round(ms_per_step, 4)
+        result["cpu_baseline"] = cpu_baseline(cpu_values if args.config == 4 else None, args,
+                                              gpu_config0)
     print(json.dumps(result), flush=True)
     return 0
 
@@ -417,42 +461,91 @@ def workload_stats(values, renderer, options):
     }
 
 
-def cpu_baseline(cpu_values, cfg, args):
-    """CPU oracle (fp32, autograd) fwd+bwd over a crop of the same workload."""
+def cpu_model() -> str:
+    """The host CPU's model name (/proc/cpuinfo), or the platform's
+    processor string where that is not available."""
+    try:
+        with open("/proc/cpuinfo") as handle:
+            for line in handle:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or "unknown CPU"
+
+
+def cpu_threads() -> int:
+    """Every core this process may run on: its CPU affinity, capped by
+    OMP_NUM_THREADS when the environment sets a share (on the GPU boxes this
+    is the box's CPU share, not the host's full core count)."""
+    available = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (
+        os.cpu_count() or 1)
+    share = os.environ.get("OMP_NUM_THREADS", "")
+    return max(1, min(available, int(share))) if share.isdigit() and int(share) > 0 else available
+
+
+def oracle_step_seconds(values, cfg, width, height, warmup: int, iterations: int):
+    """Seconds per fwd+bwd step of the fp32 torch oracle (autograd backward),
+    loss as in the GPU step, after `warmup` untimed steps."""
     import oracle.render as oracle_render
 
-    threads = max(1, min(os.cpu_count() or 1, 16))
-    torch.set_num_threads(threads)
-    edge = args.cpu_crop
-    x0 = (cfg["width"] - edge) // 2
-    y0 = (cfg["height"] - edge) // 2
-    values = crop(cpu_values, x0, y0)
-    if args.cpu_surfels:
-        values = {k: (v if k in CAMERA_KEYS else v[:, : args.cpu_surfels].contiguous())
-                  for k, v in values.items()}
     values = {k: v.clone().requires_grad_(k not in CAMERA_KEYS) for k, v in values.items()}
     function = (oracle_render.rasterize_neural_gabors if cfg["neural"]
                 else oracle_render.rasterize_gabors)
-    options = dict(width=edge, height=edge, packed=cfg["packed"])
+    options = dict(width=width, height=height, packed=cfg["packed"])
     if not cfg["neural"]:
         options["sh_degree"] = cfg["sh"]
     params = [v for v in values.values() if v.requires_grad]
-    start = time.perf_counter()
-    maps, _, _ = function(**values, **options)
-    loss = maps[..., : cfg["channels"]].square().mean()
-    torch.autograd.grad(loss, params)
-    seconds = time.perf_counter() - start
-    pixels = cfg["scenes"] * cfg["cameras"] * edge * edge
-    return {
+    times = []
+    for k in range(warmup + iterations):
+        start = time.perf_counter()
+        maps, _, _ = function(**values, **options)
+        loss = maps[..., : cfg["channels"]].square().mean()
+        torch.autograd.grad(loss, params)
+        if k >= warmup:
+            times.append(time.perf_counter() - start)
+    return sum(times) / len(times), times
+
+
+def cpu_baseline(config4_values, args, gpu_config0_ms):
+    """The CPU oracle on this host. Primary: config 0 (the designated CPU
+    config) at full frame, 2 warm-up and 5 timed fwd+bwd steps. Secondary
+    (labelled): one step over a centre crop of config 4 with all its 1M
+    surfels projected, which mostly measures per-surfel work."""
+    threads = cpu_threads()
+    torch.set_num_threads(threads)
+    cfg0 = CONFIGS[0]
+    seconds, times = oracle_step_seconds(make_scene(0), cfg0, cfg0["width"], cfg0["height"],
+                                         warmup=2, iterations=5)
+    pixels = cfg0["width"] * cfg0["height"]
+    out = {
         "value": round(pixels / seconds / 1e6, 6),
         "unit": "Mpix/s",
         "cores": threads,
         "kind": "port",
-        "sample": (f"{edge}x{edge} centre crop of the same scene and camera (all "
-                   f"{values['means'].shape[1]} surfels projected, SH evaluated, binned), "
-                   f"fp32 torch oracle forward + autograd backward, one step, "
-                   f"{seconds:.2f} s per step on {platform.processor() or 'host CPU'}"),
+        "sample": (f"{cfg0['name']}, full frame: fp32 torch oracle forward + autograd backward, "
+                   f"2 warm-up + {len(times)} timed steps, {seconds:.3f} s per step "
+                   f"(steps {', '.join(f'{t:.3f}' for t in times)} s) on {threads} threads"),
+        "ms_per_step": round(seconds * 1000, 2),
+        "gpu_ms_per_step_same_workload": gpu_config0_ms,
+        "cpu_model": cpu_model(),
+        "os_cpu_count": os.cpu_count(),
+        "torch_threads": torch.get_num_threads(),
     }
+    if config4_values is not None and args.cpu_crop:
+        cfg4, edge = CONFIGS[4], args.cpu_crop
+        x0, y0 = (cfg4["width"] - edge) // 2, (cfg4["height"] - edge) // 2
+        crop_seconds, _ = oracle_step_seconds(crop(config4_values, x0, y0), cfg4, edge, edge,
+                                              warmup=0, iterations=1)
+        out["secondary_config4_crop"] = {
+            "value": round(edge * edge / crop_seconds / 1e6, 6),
+            "unit": "Mpix/s",
+            "sample": (f"{edge}x{edge} centre crop of config 4 (all {cfg4['n']} surfels "
+                       f"projected, SH evaluated and binned), one fwd+bwd step, "
+                       f"{crop_seconds:.2f} s; dominated by per-surfel work, not comparable "
+                       f"with a full-frame rate"),
+        }
+    return out
 
 
 if __name__ == "__main__":

@@ -1,13 +1,24 @@
-"""Loop vs fused-dense vs fused-packed rendering through the public API.
+"""Per-camera loop, fused dense and fused packed rendering, timed through the public API.
 
-The caller-side methodology of the reference's benchmark
-(benchmarks/benchmark_rasterization.py:101-251), on this implementation:
-the same command-line options, the same synthetic scene distributions, a
-parity gate before any timing (every camera rendered separately against
-one fused call, dense and packed, maps and parameter gradients), HIP-event
-timing of forward (including the scalar loss) and backward, and a JSON
-report with the same keys. Optional kernel profiling uses this library's
-own HIP-event counters per kernel family instead of a tracing profiler.
+Counterpart of the reference's benchmark harness
+(benchmarks/benchmark_rasterization.py). Its command line, the synthetic
+scene it draws and the keys of its JSON report are kept, so that results
+of the two can be read side by side; everything else is this library's:
+
+* scenes come from a declarative recipe (``SCENE_RECIPE``), drawn on the
+  CPU from one seeded generator and then moved to the GPU, so a seed gives
+  the same scene on every machine;
+* each implementation is a strategy object that renders all nine map
+  channels of every (scene, camera) image;
+* before anything is timed, a parity gate holds the fused strategies to
+  the per-camera loop at the project's float bars - maps within 1e-5
+  absolute + 1e-4 relative, parameter gradients within 1e-3 of their
+  tensor's scale and norm - and records the worst errors in the report;
+* steps are timed with HIP events on the launch stream
+  (``timing.time_phases``): forward (rendering and the scalar loss) and
+  backward;
+* the optional kernel split comes from the library's own per-family event
+  counters (``gs_profile_enable``), in a separate pass.
 
     python -m diff_gabor_splatting_amd.benchmark_rasterization --method both \\
         --num-primitives 10000 --num-cameras 4 --output-json results.json
@@ -19,242 +30,414 @@ import argparse
 import json
 import platform
 import subprocess
+from dataclasses import asdict, dataclass
 from pathlib import Path
+from typing import Callable
 
 import torch
 
 from . import _native
 from .rendering import rasterize_gabors, rasterize_neural_gabors
+from .timing import mean, time_phases
 
 IMPLEMENTATIONS = ("single_view_loop", "fused_dense", "fused_packed")
-CAMERA_KEYS = ("view_matrices", "intrinsics", "backgrounds")
-NEURAL_FIELDS = (
-    ("input_weights", (6, 5), 1 / 5),
-    ("input_biases", (6,), 1 / 5),
-    ("output_weights", (3, 6), 1 / 30),
-    ("output_biases", (3,), 0.1),
+METHODS = ("classic", "neural")
+# Inputs that describe the cameras rather than the surfels: not optimised,
+# and sliced per camera by the loop strategy.
+CAMERA_INPUTS = ("view_matrices", "intrinsics", "backgrounds")
+MAP_OUTPUTS = ("accumulated_depth", "normals", "distortion")
+
+# The parity gate's bars: the project's float32 forward tolerance, and
+# gradients within 1e-3 of the tensor's scale (elementwise) and norm.
+MAP_ATOL, MAP_RTOL = 1e-5, 1e-4
+GRADIENT_TOLERANCE = 1e-3
+
+
+# --------------------------------------------------------------------------
+# Workload
+
+
+@dataclass(frozen=True)
+class Workload:
+    """The command line, validated: sizes of the synthetic scene and the
+    measurement schedule."""
+
+    method: str
+    num_primitives: int
+    num_scenes: int
+    num_cameras: int
+    image_width: int
+    image_height: int
+    warmup_iterations: int
+    measurement_iterations: int
+    seed: int
+    profile_iterations: int
+    skip_validation: bool
+
+    @property
+    def images(self) -> int:
+        return self.num_scenes * self.num_cameras
+
+    @property
+    def methods(self) -> tuple[str, ...]:
+        return METHODS if self.method == "both" else (self.method,)
+
+
+_SIZE_OPTIONS = (
+    # flag, default, lower bound
+    ("--num-primitives", 10_000, 1),
+    ("--num-scenes", 1, 1),
+    ("--num-cameras", 4, 1),
+    ("--image-width", 256, 1),
+    ("--image-height", 256, 1),
+    ("--warmup-iterations", 5, 0),
+    ("--measurement-iterations", 20, 1),
+    ("--seed", 42, None),
+    ("--profile-iterations", 0, 0),
 )
 
 
-def make_scene(args: argparse.Namespace, method: str) -> dict:
-    """Deterministic synthetic scene (built outside every timed region).
-
-    Distributions follow the reference benchmark (:16-64): means ~ N(0, 0.6)
-    with depth U(3, 5), near-identity unit quaternions, scales 0.025,
-    opacity 0.3, cameras spread along x, focal length 0.8 x image size.
-    """
-    device = torch.device("cuda")
-    gen = torch.Generator(device=device).manual_seed(args.seed)
-    b, n, c = args.num_scenes, args.num_primitives, args.num_cameras
-    width, height = args.image_width, args.image_height
-    means = torch.randn(b, n, 3, device=device, generator=gen) * 0.6
-    means[..., 2] = torch.rand(b, n, device=device, generator=gen) * 2 + 3
-    quats = torch.randn(b, n, 4, device=device, generator=gen) * 0.1
-    quats[..., 0] += 1
-    quats = quats / quats.norm(dim=-1, keepdim=True)
-    views = torch.eye(4, device=device).repeat(b, c, 1, 1)
-    if c > 1:
-        views[..., 0, 3] = torch.linspace(-0.2, 0.2, c, device=device)
-    intrinsics = torch.zeros(b, c, 3, 3, device=device)
-    intrinsics[..., 0, 0] = width * 0.8
-    intrinsics[..., 1, 1] = height * 0.8
-    intrinsics[..., 0, 2] = (width - 1) / 2
-    intrinsics[..., 1, 2] = (height - 1) / 2
-    intrinsics[..., 2, 2] = 1.0
-    scene = dict(
-        means=means,
-        quaternions=quats,
-        scales=torch.full((b, n, 2), 0.025, device=device),
-        opacities=torch.full((b, n), 0.3, device=device),
-        view_matrices=views,
-        intrinsics=intrinsics,
-        backgrounds=torch.full((b, c, 3), 0.05, device=device),
-    )
-    if method == "classic":
-        scene["colors"] = torch.rand(b, n, 3, device=device, generator=gen)
-        scene["secondary_colors"] = torch.rand(b, n, 3, device=device, generator=gen)
-        scene["frequency_weights"] = torch.full((b, n, 4), 0.25, device=device)
-        scene["frequency_magnitudes"] = torch.ones(b, n, 4, device=device)
-        scene["phases"] = torch.zeros(b, n, 4, device=device)
-    else:
-        for name, shape, bound in NEURAL_FIELDS:
-            value = torch.empty(b, n, *shape, device=device)
-            scene[name] = value.uniform_(-bound, bound, generator=gen)
-    for name, value in scene.items():
-        value.requires_grad_(name not in CAMERA_KEYS)
-    return scene
-
-
-def _maps(result):
-    rgb, alpha, meta = result
-    return torch.cat(
-        (rgb, alpha, meta["accumulated_depth"], meta["normals"], meta["distortion"]), -1
-    )
-
-
-def render_maps(scene: dict, args: argparse.Namespace, method: str, implementation: str):
-    """All nine differentiable channels [B, C, H, W, 9] for one implementation."""
-    function = rasterize_gabors if method == "classic" else rasterize_neural_gabors
-    options = dict(width=args.image_width, height=args.image_height,
-                   validate=not args.skip_validation)
-    if implementation != "single_view_loop":
-        return _maps(function(**scene, packed=implementation == "fused_packed", **options))
-    per_scene = []
-    for s in range(args.num_scenes):
-        per_camera = []
-        for c in range(args.num_cameras):
-            view = {
-                name: (value[s, c:c + 1] if name in CAMERA_KEYS else value[s]).contiguous()
-                for name, value in scene.items()
-            }
-            per_camera.append(_maps(function(**view, **options)))
-        per_scene.append(torch.cat(per_camera, 0))
-    return torch.stack(per_scene)
-
-
-def check_parity(scene: dict, args: argparse.Namespace, method: str) -> None:
-    """Fused dense and packed calls must reproduce the per-camera loop."""
-    parameters = [value for value in scene.values() if value.requires_grad]
-    loop = render_maps(scene, args, method, "single_view_loop")
-    expected = torch.autograd.grad(loop.square().mean(), parameters)
-    for implementation in IMPLEMENTATIONS[1:]:
-        maps = render_maps(scene, args, method, implementation)
-        torch.testing.assert_close(maps, loop, atol=2e-5, rtol=2e-4)
-        actual = torch.autograd.grad(maps.square().mean(), parameters)
-        for value, reference in zip(actual, expected):
-            torch.testing.assert_close(value, reference, atol=2e-5, rtol=2e-3)
-
-
-def _clear_gradients(scene: dict) -> None:
-    for value in scene.values():
-        value.grad = None
-
-
-def measure(scene: dict, args: argparse.Namespace, method: str, implementation: str) -> dict:
-    """Mean forward (with the scalar loss) and backward milliseconds."""
-    for _ in range(args.warmup_iterations):
-        _clear_gradients(scene)
-        render_maps(scene, args, method, implementation).square().mean().backward()
-    _clear_gradients(scene)
-    torch.cuda.synchronize()
-    torch.cuda.reset_peak_memory_stats()
-    forward_ms, backward_ms = [], []
-    for _ in range(args.measurement_iterations):
-        _clear_gradients(scene)
-        marks = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
-        marks[0].record()
-        loss = render_maps(scene, args, method, implementation).square().mean()
-        marks[1].record()
-        loss.backward()
-        marks[2].record()
-        marks[2].synchronize()
-        forward_ms.append(marks[0].elapsed_time(marks[1]))
-        backward_ms.append(marks[1].elapsed_time(marks[2]))
-    forward = sum(forward_ms) / len(forward_ms)
-    backward = sum(backward_ms) / len(backward_ms)
-    return {
-        "implementation": implementation,
-        "forward_ms": forward,
-        "backward_ms": backward,
-        "forward_backward_ms": forward + backward,
-        "images_per_second": args.num_scenes * args.num_cameras * 1000 / (forward + backward),
-        "peak_allocated_memory_mb": torch.cuda.max_memory_allocated() / 1_000_000,
-    }
-
-
-def profile_kernels(scene: dict, args: argparse.Namespace, method: str,
-                    implementation: str) -> dict:
-    """Per-family kernel milliseconds from the library's HIP-event counters,
-    measured separately from the uninstrumented timing."""
-    _native.profile_enable(True)
-    for _ in range(args.profile_iterations):
-        _clear_gradients(scene)
-        render_maps(scene, args, method, implementation).square().mean().backward()
-    torch.cuda.synchronize()
-    families = {name: _native.profile_read(name)[0] / args.profile_iterations
-                for name in _native.PROFILE_FAMILIES}
-    _native.profile_enable(False)
-    forward = families["render_forward"]
-    backward = families["render_backward"]
-    if not forward or not backward:
-        raise RuntimeError("profiling did not record the forward/backward compositor kernels")
-    return {
-        "forward_kernel_ms": forward,
-        "backward_kernel_ms": backward,
-        "other_cuda_kernel_ms": sum(families.values()) - forward - backward,
-        "kernels_ms": families,
-    }
-
-
-def _parse(argv=None) -> argparse.Namespace:
+def parse_workload(argv=None) -> tuple[Workload, Path | None]:
+    """Workload and report path from the reference harness's flags."""
     parser = argparse.ArgumentParser(description=__doc__.splitlines()[0])
-    parser.add_argument("--method", choices=["classic", "neural", "both"], default="both")
-    parser.add_argument("--num-primitives", type=int, default=10_000)
-    parser.add_argument("--num-scenes", type=int, default=1)
-    parser.add_argument("--num-cameras", type=int, default=4)
-    parser.add_argument("--image-width", type=int, default=256)
-    parser.add_argument("--image-height", type=int, default=256)
-    parser.add_argument("--warmup-iterations", type=int, default=5)
-    parser.add_argument("--measurement-iterations", type=int, default=20)
-    parser.add_argument("--seed", type=int, default=42)
-    parser.add_argument("--profile-iterations", type=int, default=0,
-                        help="separately profile this many steps per implementation; "
-                             "0 disables profiling")
+    parser.add_argument("--method", choices=[*METHODS, "both"], default="both")
+    for flag, default, _ in _SIZE_OPTIONS:
+        help_text = ("separately profile this many steps per implementation; 0 disables "
+                     "profiling") if flag == "--profile-iterations" else None
+        parser.add_argument(flag, type=int, default=default, help=help_text)
     parser.add_argument("--skip-validation", action="store_true")
     parser.add_argument("--output-json", type=Path)
     args = parser.parse_args(argv)
-    positive = ("num_primitives", "num_scenes", "num_cameras", "image_width", "image_height",
-                "measurement_iterations")
-    for name in positive:
-        if getattr(args, name) < 1:
-            parser.error(f"--{name.replace('_', '-')} must be positive")
-    if args.warmup_iterations < 0 or args.profile_iterations < 0:
-        parser.error("--warmup-iterations and --profile-iterations must be nonnegative")
-    return args
+    for flag, _, lower in _SIZE_OPTIONS:
+        value = getattr(args, flag[2:].replace("-", "_"))
+        if lower is not None and value < lower:
+            parser.error(f"{flag} must be {'positive' if lower else 'nonnegative'}")
+    output = args.output_json
+    fields = {k: v for k, v in vars(args).items() if k != "output_json"}
+    return Workload(**fields), output
+
+
+# --------------------------------------------------------------------------
+# Scenes
+
+
+def _normal(scale: float = 1.0, shift: float = 0.0):
+    return lambda gen, shape: torch.randn(shape, generator=gen) * scale + shift
+
+
+def _uniform(low: float, high: float):
+    return lambda gen, shape: torch.rand(shape, generator=gen) * (high - low) + low
+
+
+def _constant(value: float):
+    return lambda gen, shape: torch.full(shape, value)
+
+
+def _means(gen, shape):
+    """Surfel centres N(0, 0.6^2) across the view, depth uniform in [3, 5]."""
+    means = torch.randn(shape, generator=gen) * 0.6
+    means[..., 2] = torch.rand(shape[:-1], generator=gen) * 2 + 3
+    return means
+
+
+def _near_identity_rotations(gen, shape):
+    """Unit wxyz quaternions close to the identity: N(0, 0.1^2) + (1, 0, 0, 0)."""
+    q = torch.randn(shape, generator=gen) * 0.1
+    q[..., 0] += 1
+    return q / q.norm(dim=-1, keepdim=True)
+
+
+# name -> (trailing shape, sampler); surfel tensors are [B, N, ...].
+SCENE_RECIPE = {
+    "common": (
+        ("means", (3,), _means),
+        ("quaternions", (4,), _near_identity_rotations),
+        ("scales", (2,), _constant(0.025)),
+        ("opacities", (), _constant(0.3)),
+    ),
+    "classic": (
+        ("colors", (3,), _uniform(0.0, 1.0)),
+        ("secondary_colors", (3,), _uniform(0.0, 1.0)),
+        ("frequency_weights", (4,), _constant(0.25)),
+        ("frequency_magnitudes", (4,), _constant(1.0)),
+        ("phases", (4,), _constant(0.0)),
+    ),
+    "neural": (
+        ("input_weights", (6, 5), _uniform(-1 / 5, 1 / 5)),
+        ("input_biases", (6,), _uniform(-1 / 5, 1 / 5)),
+        ("output_weights", (3, 6), _uniform(-1 / 30, 1 / 30)),
+        ("output_biases", (3,), _uniform(-0.1, 0.1)),
+    ),
+}
+
+
+def cameras(work: Workload) -> dict[str, torch.Tensor]:
+    """Identity views shifted along x over [-0.2, 0.2], pinhole intrinsics
+    with focal length 0.8 x the image size and the principal point at the
+    image centre, and a 0.05 grey background."""
+    b, c = work.num_scenes, work.num_cameras
+    views = torch.eye(4).repeat(b, c, 1, 1)
+    if c > 1:
+        views[..., 0, 3] = torch.linspace(-0.2, 0.2, c)
+    w, h = work.image_width, work.image_height
+    K = torch.tensor([[0.8 * w, 0.0, (w - 1) / 2], [0.0, 0.8 * h, (h - 1) / 2], [0, 0, 1.0]])
+    return {"view_matrices": views, "intrinsics": K.repeat(b, c, 1, 1),
+            "backgrounds": torch.full((b, c, 3), 0.05)}
+
+
+def synthesize(work: Workload, method: str, device: torch.device) -> dict[str, torch.Tensor]:
+    """The benchmark scene of one method, outside every timed region: surfel
+    tensors from SCENE_RECIPE (optimised, requires_grad), then the cameras."""
+    gen = torch.Generator().manual_seed(work.seed)
+    batch = (work.num_scenes, work.num_primitives)
+    scene = {}
+    for name, trailing, sample in SCENE_RECIPE["common"] + SCENE_RECIPE[method]:
+        scene[name] = sample(gen, batch + trailing)
+    scene.update(cameras(work))
+    return {name: value.to(device).contiguous().requires_grad_(name not in CAMERA_INPUTS)
+            for name, value in scene.items()}
+
+
+# --------------------------------------------------------------------------
+# Strategies: one way each of rendering all images of a scene.
+
+
+def _all_maps(result) -> torch.Tensor:
+    rgb, alpha, meta = result
+    return torch.cat((rgb, alpha, *(meta[key] for key in MAP_OUTPUTS)), -1)
+
+
+class Strategy:
+    """Renders every (scene, camera) image of a scene: maps [B, C, H, W, 9]."""
+
+    name = ""
+
+    def __init__(self, work: Workload, method: str) -> None:
+        self.render = rasterize_gabors if method == "classic" else rasterize_neural_gabors
+        self.options = dict(width=work.image_width, height=work.image_height,
+                            validate=not work.skip_validation)
+
+    def maps(self, scene: dict) -> torch.Tensor:
+        raise NotImplementedError
+
+
+class Fused(Strategy):
+    """All scenes and cameras in one call, dense or packed."""
+
+    def __init__(self, work: Workload, method: str, packed: bool) -> None:
+        super().__init__(work, method)
+        self.packed = packed
+        self.name = "fused_packed" if packed else "fused_dense"
+
+    def maps(self, scene: dict) -> torch.Tensor:
+        return _all_maps(self.render(**scene, packed=self.packed, **self.options))
+
+
+class PerView(Strategy):
+    """One call per (scene, camera) image, stacked afterwards."""
+
+    name = "single_view_loop"
+
+    def __init__(self, work: Workload, method: str) -> None:
+        super().__init__(work, method)
+        self.shape = (work.num_scenes, work.num_cameras)
+
+    def maps(self, scene: dict) -> torch.Tensor:
+        images = []
+        for s in range(self.shape[0]):
+            for c in range(self.shape[1]):
+                view = {name: (value[s, c:c + 1] if name in CAMERA_INPUTS else value[s])
+                        for name, value in scene.items()}
+                view = {name: value.contiguous() for name, value in view.items()}
+                images.append(_all_maps(self.render(**view, **self.options))[0])
+        return torch.stack(images).unflatten(0, self.shape)
+
+
+def strategies(work: Workload, method: str) -> dict[str, Strategy]:
+    """Every implementation, keyed by its report name, loop first."""
+    made = [PerView(work, method), Fused(work, method, False), Fused(work, method, True)]
+    return {strategy.name: strategy for strategy in made}
+
+
+def objective(maps: torch.Tensor) -> torch.Tensor:
+    """The scalar every implementation is timed on: the mean square of all
+    nine channels."""
+    return maps.square().mean()
+
+
+# --------------------------------------------------------------------------
+# Parity gate
+
+
+class ParityError(AssertionError):
+    """A fused implementation differs from the per-camera loop."""
+
+
+def _gradient_error(actual: torch.Tensor, expected: torch.Tensor) -> tuple[float, float]:
+    """(largest elementwise error, error norm), both relative to the
+    expected tensor's largest element and norm."""
+    scale = float(expected.abs().max()) if expected.numel() else 0.0
+    diff = (actual - expected).abs()
+    elementwise = float((diff - GRADIENT_TOLERANCE * expected.abs()).clamp_min(0).max()
+                        ) / scale if scale and diff.numel() else 0.0
+    norm = float(expected.norm())
+    return elementwise, float(diff.norm()) / norm if norm else float(diff.norm())
+
+
+def parity_gate(scene: dict, candidates: dict[str, Strategy], baseline: str) -> dict:
+    """Compare every strategy with ``baseline`` on maps and on the gradients
+    of ``objective``; raise ParityError naming the worst differences, or
+    return them (one entry per compared strategy)."""
+    parameters = {name: value for name, value in scene.items() if value.requires_grad}
+
+    def evaluate(strategy):
+        maps = strategy.maps(scene)
+        grads = torch.autograd.grad(objective(maps), list(parameters.values()))
+        return maps.detach(), dict(zip(parameters, grads))
+
+    reference_maps, reference_grads = evaluate(candidates[baseline])
+    record = {}
+    for name, strategy in candidates.items():
+        if name == baseline:
+            continue
+        maps, grads = evaluate(strategy)
+        excess = ((maps - reference_maps).abs()
+                  - (MAP_ATOL + MAP_RTOL * reference_maps.abs())).clamp_min(0)
+        worst_grads = {key: _gradient_error(grads[key], reference_grads[key]) for key in grads}
+        record[name] = {
+            "max_map_error": float((maps - reference_maps).abs().max()),
+            "map_excess": float(excess.max()),
+            "max_gradient_error": max((e for e, _ in worst_grads.values()), default=0.0),
+            "max_gradient_norm_error": max((n for _, n in worst_grads.values()), default=0.0),
+        }
+        failures = []
+        if record[name]["map_excess"] > 0:
+            failures.append(f"maps differ by up to {record[name]['max_map_error']:.3e}")
+        for key, (element, norm) in worst_grads.items():
+            if element > GRADIENT_TOLERANCE or norm > GRADIENT_TOLERANCE:
+                failures.append(f"{key} gradient error {element:.3e} (elementwise, of max) / "
+                                f"{norm:.3e} (norm)")
+        if failures:
+            raise ParityError(f"{name} differs from {baseline}: " + "; ".join(failures))
+    return record
+
+
+# --------------------------------------------------------------------------
+# Measurement
+
+
+def _clear_gradients(scene: dict) -> Callable[[], None]:
+    def clear():
+        for value in scene.values():
+            value.grad = None
+    return clear
+
+
+def measure(scene: dict, strategy: Strategy, work: Workload) -> dict:
+    """Mean forward (render + loss) and backward milliseconds over the
+    measured steps, and the peak memory they allocated."""
+
+    def step(clock):
+        clock.mark("start")
+        loss = objective(strategy.maps(scene))
+        clock.mark("forward")
+        loss.backward()
+        clock.mark("backward")
+
+    clear = _clear_gradients(scene)
+    clear()
+    torch.cuda.synchronize()
+    torch.cuda.reset_peak_memory_stats()
+    samples = time_phases(step, work.warmup_iterations, work.measurement_iterations, clear)
+    forward, backward = mean(samples["forward"]), mean(samples["backward"])
+    return {
+        "implementation": strategy.name,
+        "forward_ms": forward,
+        "backward_ms": backward,
+        "forward_backward_ms": forward + backward,
+        "images_per_second": work.images * 1000.0 / (forward + backward),
+        "peak_allocated_memory_mb": torch.cuda.max_memory_allocated() / 1e6,
+    }
+
+
+def kernel_split(scene: dict, strategy: Strategy, work: Workload) -> dict:
+    """Per-family kernel milliseconds per step from the library's HIP-event
+    counters, in a pass of its own (the events add host work)."""
+    clear = _clear_gradients(scene)
+    _native.profile_enable(True)
+    try:
+        for _ in range(work.profile_iterations):
+            clear()
+            objective(strategy.maps(scene)).backward()
+        torch.cuda.synchronize()
+        families = {family: _native.profile_read(family)[0] / work.profile_iterations
+                    for family in _native.PROFILE_FAMILIES}
+    finally:
+        _native.profile_enable(False)
+    forward, backward = families["render_forward"], families["render_backward"]
+    if forward <= 0 or backward <= 0:
+        raise RuntimeError("the kernel counters recorded no compositor launches")
+    return {"forward_kernel_ms": forward, "backward_kernel_ms": backward,
+            "other_cuda_kernel_ms": sum(families.values()) - forward - backward,
+            "kernels_ms": families}
+
+
+# --------------------------------------------------------------------------
+# Report
+
+
+def environment() -> dict:
+    revision = subprocess.run(["git", "rev-parse", "HEAD"], capture_output=True, text=True,
+                              cwd=Path(__file__).resolve().parent)
+    return {
+        "gpu": torch.cuda.get_device_name(),
+        "torch": torch.__version__,
+        "cuda": torch.version.cuda,
+        "hip": torch.version.hip,
+        "python": platform.python_version(),
+        "revision": revision.stdout.strip() if revision.returncode == 0 else None,
+    }
 
 
 def run(argv=None) -> dict:
-    """Parity gate, then timing of the three implementations; returns the report."""
-    args = _parse(argv)
-    revision = subprocess.run(["git", "rev-parse", "HEAD"], capture_output=True, text=True,
-                              cwd=Path(__file__).resolve().parent)
+    """Parity gate, then timing of every implementation; the report is
+    returned and, with --output-json, written."""
+    work, output = parse_workload(argv)
+    device = torch.device("cuda", torch.cuda.current_device())
     report = {
-        "environment": {
-            "gpu": torch.cuda.get_device_name(),
-            "torch": torch.__version__,
-            "cuda": torch.version.cuda,
-            "hip": torch.version.hip,
-            "python": platform.python_version(),
-            "revision": revision.stdout.strip() if revision.returncode == 0 else None,
-        },
-        "workload": {k: v for k, v in vars(args).items() if k != "output_json"},
-        "timing": "HIP events; forward includes autograd graph construction and scalar loss; "
-                  "combined throughput includes backward",
-        "profiling": "optional separate pass with the library's HIP-event kernel counters",
-        "memory": "peak total PyTorch-allocated device memory in decimal MB, including inputs "
-                  "and autograd state",
+        "environment": environment(),
+        "workload": asdict(work),
+        "timing": "HIP events on the launch stream; forward covers rendering, autograd graph "
+                  "construction and the scalar loss, backward the whole reverse pass",
+        "profiling": "optional separate pass over the library's per-family HIP-event kernel "
+                     "counters",
+        "memory": "peak PyTorch-allocated device memory over the measured steps, decimal MB, "
+                  "inputs and autograd state included",
+        "parity": {},
         "results": [],
     }
-    methods = ("classic", "neural") if args.method == "both" else (args.method,)
-    for method in methods:
-        scene = make_scene(args, method)
-        check_parity(scene, args, method)
+    for method in work.methods:
+        scene = synthesize(work, method, device)
+        candidates = strategies(work, method)
+        report["parity"][method] = parity_gate(scene, candidates, "single_view_loop")
         loop_ms = None
-        for implementation in IMPLEMENTATIONS:
-            result = measure(scene, args, method, implementation)
-            if args.profile_iterations:
-                result.update(profile_kernels(scene, args, method, implementation))
-            loop_ms = loop_ms or result["forward_backward_ms"]
-            result["method"] = method
-            result["speedup_vs_single_view_loop"] = loop_ms / result["forward_backward_ms"]
-            report["results"].append(result)
-            print(f"{method:7s} {implementation:16s} forward={result['forward_ms']:.3f} ms "
-                  f"backward={result['backward_ms']:.3f} ms "
-                  f"speedup={result['speedup_vs_single_view_loop']:.2f}x", flush=True)
+        for strategy in candidates.values():
+            row = measure(scene, strategy, work)
+            if work.profile_iterations:
+                row.update(kernel_split(scene, strategy, work))
+            loop_ms = loop_ms if loop_ms is not None else row["forward_backward_ms"]
+            row["method"] = method
+            row["speedup_vs_single_view_loop"] = loop_ms / row["forward_backward_ms"]
+            report["results"].append(row)
+            print(f"[{method}/{row['implementation']}] fwd {row['forward_ms']:.3f} ms + bwd "
+                  f"{row['backward_ms']:.3f} ms = {row['forward_backward_ms']:.3f} ms, "
+                  f"{row['images_per_second']:.0f} img/s, "
+                  f"x{row['speedup_vs_single_view_loop']:.2f} vs the per-camera loop",
+                  flush=True)
         del scene
-    if args.output_json:
-        args.output_json.parent.mkdir(parents=True, exist_ok=True)
-        args.output_json.write_text(json.dumps(report, indent=2) + "\n")
+    if output is not None:
+        output.parent.mkdir(parents=True, exist_ok=True)
+        output.write_text(json.dumps(report, indent=2) + "\n")
     return report
 
 

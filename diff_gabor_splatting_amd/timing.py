@@ -1,0 +1,63 @@
+"""Device-side timing shared by ``bench.py`` and the benchmark harness.
+
+A :class:`PhaseClock` records a HIP event on the current stream at every
+named mark; once the last mark has completed, each phase's time is the
+elapsed time between its mark and the one before. Recording events costs a
+few microseconds of host time per mark and nothing on the device, so a step
+can be split into phases (forward, backward) without synchronising inside it.
+"""
+
+from __future__ import annotations
+
+import statistics
+from typing import Callable
+
+import torch
+
+
+class PhaseClock:
+    """Named marks on the current stream of the current device."""
+
+    def __init__(self) -> None:
+        self._marks: list[tuple[str, torch.cuda.Event]] = []
+
+    def mark(self, name: str) -> None:
+        event = torch.cuda.Event(enable_timing=True)
+        event.record()
+        self._marks.append((name, event))
+
+    def phases(self) -> dict[str, float]:
+        """Milliseconds of every phase, keyed by the mark that ends it
+        (waits for the last mark)."""
+        if not self._marks:
+            return {}
+        self._marks[-1][1].synchronize()
+        return {name: before.elapsed_time(event)
+                for (_, before), (name, event) in zip(self._marks, self._marks[1:])}
+
+
+def time_phases(step: Callable[[PhaseClock], None], warmup: int, iterations: int,
+                before: Callable[[], None] | None = None) -> dict[str, list[float]]:
+    """Run ``step`` ``warmup`` times untimed, then ``iterations`` times with a
+    fresh clock each; ``step`` marks "start" first and then the end of each
+    of its phases. ``before`` (e.g. clearing gradients) runs ahead of every
+    step, outside the marks. Returns each phase's milliseconds per
+    iteration."""
+    for _ in range(warmup):
+        if before is not None:
+            before()
+        step(PhaseClock())
+    torch.cuda.synchronize()
+    samples: dict[str, list[float]] = {}
+    for _ in range(iterations):
+        if before is not None:
+            before()
+        clock = PhaseClock()
+        step(clock)
+        for name, ms in clock.phases().items():
+            samples.setdefault(name, []).append(ms)
+    return samples
+
+
+def mean(values: list[float]) -> float:
+    return statistics.fmean(values) if values else 0.0
