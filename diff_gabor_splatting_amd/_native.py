@@ -116,6 +116,15 @@ _SIGNATURES = {
         + [_c_ptr] * 2
         + [_c_size, _c_ptr],
     ),
+    "gs_render_forward_static": (
+        _c_int,
+        [_c_int]
+        + [_c_ptr] * 7
+        + [_c_i64, _c_int, _c_int, _c_float, _c_float]
+        + [_c_ptr] * 5
+        + [_c_i64]
+        + [_c_ptr] * 2,
+    ),
     "gs_render_backward": (
         _c_int,
         [_c_int]

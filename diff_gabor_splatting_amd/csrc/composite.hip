@@ -34,6 +34,7 @@
 //    totals with one global atomic per (tile, record, parameter).
 #include <climits>
 #include <cmath>
+#include <mutex>
 #include <type_traits>
 
 #include "common.hpp"
@@ -1264,11 +1265,48 @@ int check_render(int64_t images, int width, int height, float near_plane, float 
 }  // namespace
 }  // namespace gs
 
+// Scratch of gs_render_forward_static: the tile dispatch order of up to
+// kStaticOrderTiles tiles (4 MiB), one copy per GPU, held until the process
+// ends. Host code must not pass `scratch` itself to a kernel (it names the
+// host-side shadow, not device memory): the device address comes from
+// hipGetSymbolAddress, once per device, in static_order_buffer.
+constexpr int64_t kStaticOrderTiles = GS_RENDER_STATIC_MAX_TILES;
+static __device__ __align__(256) int scratch[kStaticOrderTiles];
+
 namespace gs {
 namespace {
 
+constexpr int kMaxDevices = 64;
+
+// Device address of `scratch` on the device that owns `stream`, looked up
+// with that device current on the first call for the device and kept.
+int static_order_buffer(hipStream_t stream, int** buffer) {
+  static std::mutex mutex;
+  static int* addresses[kMaxDevices] = {};
+  int current = 0;
+  GS_HIP(hipGetDevice(&current));
+  int device = current;
+  if (stream) GS_HIP(hipStreamGetDevice(stream, &device));
+  GS_REQUIRE(device >= 0 && device < kMaxDevices, GS_ERR_ARGUMENT,
+             "device %d is beyond the %d devices the static scratch supports", device,
+             kMaxDevices);
+  std::lock_guard<std::mutex> lock(mutex);
+  if (!addresses[device]) {
+    if (device != current) GS_HIP(hipSetDevice(device));
+    void* address = nullptr;
+    const hipError_t found = hipGetSymbolAddress(&address, HIP_SYMBOL(scratch));
+    if (device != current) GS_HIP(hipSetDevice(current));
+    GS_HIP(found);
+    GS_REQUIRE(address, GS_ERR_HIP, "hipGetSymbolAddress returned no address for the scratch");
+    addresses[device] = static_cast<int*>(address);
+  }
+  *buffer = addresses[device];
+  return GS_OK;
+}
+
 // The forward compositor's launches given the tile dispatch-order buffer
-// (`tiles` ints), which gs_render_forward takes from the caller's workspace.
+// (`tiles` ints): gs_render_forward takes it from the caller's workspace,
+// gs_render_forward_static from `scratch`.
 int render_forward(int32_t neural, const float* geometry, const float* appearance,
                    const float* opacities, const int64_t* primitive_ids,
                    const float* backgrounds, const int32_t* point_list, const int32_t* ranges,
@@ -1354,6 +1392,36 @@ int gs_render_forward(int32_t neural, const float* geometry, const float* appear
                         point_list, ranges, images, width, height, near_plane, far_plane,
                         map_groups(maps, map_strides), state, contributors, replay,
                         replay_counts, w.order, static_cast<hipStream_t>(stream));
+}
+
+int gs_render_forward_static(int32_t neural, const float* geometry, const float* appearance,
+                             const float* opacities, const int64_t* primitive_ids,
+                             const float* backgrounds, const int32_t* point_list,
+                             const int32_t* ranges, int64_t images, int32_t width,
+                             int32_t height, float near_plane, float far_plane,
+                             float* const* maps, const int64_t* map_strides, float* state,
+                             int32_t* contributors, int32_t* replay, int64_t replay_capacity,
+                             int32_t* replay_counts, void* stream) {
+  using namespace gs;
+  clear_error();
+  const int status =
+      check_render_forward(images, width, height, near_plane, far_plane, backgrounds, ranges,
+                           maps, map_strides, state, contributors, replay, replay_capacity,
+                           replay_counts);
+  if (status != GS_OK) return status;
+  const int64_t tiles = images * tiles_x(width) * tiles_y(height);
+  GS_REQUIRE(tiles <= kStaticOrderTiles, GS_ERR_WORKSPACE,
+             "gs_render_forward_static handles at most %lld image tiles (its static scratch), "
+             "got %lld",
+             static_cast<long long>(kStaticOrderTiles), static_cast<long long>(tiles));
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  int* order = nullptr;
+  const int found = static_order_buffer(s, &order);
+  if (found != GS_OK) return found;
+  return render_forward(neural, geometry, appearance, opacities, primitive_ids, backgrounds,
+                        point_list, ranges, images, width, height, near_plane, far_plane,
+                        map_groups(maps, map_strides), state, contributors, replay,
+                        replay_counts, order, s);
 }
 
 int gs_render_backward(int32_t neural, const float* geometry, const float* appearance,

@@ -349,6 +349,27 @@ int gs_render_forward(int32_t neural, const float* geometry, const float* appear
                       int32_t* replay, int64_t replay_capacity, int32_t* replay_counts,
                       void* workspace, size_t workspace_bytes, void* stream);
 
+/* gs_render_forward without a workspace argument. No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid
+ * allocation). The forward's only scratch, the tiles' dispatch order, lives
+ * in a static device array of GS_RENDER_STATIC_MAX_TILES ints (4 MiB per
+ * GPU, held until the process ends); more image tiles than that return
+ * GS_ERR_WORKSPACE before any launch. Nothing is allocated. Every call on a
+ * GPU shares that GPU's array, so calls that overlap on one GPU (on
+ * different streams or threads) race; each call rewrites the order of all
+ * its tiles before reading it, so nothing has to be cleared between calls.
+ * Outputs are identical to gs_render_forward's. */
+#define GS_RENDER_STATIC_MAX_TILES (1 << 20)
+int gs_render_forward_static(int32_t neural, const float* geometry, const float* appearance,
+                             const float* opacities, const int64_t* primitive_ids,
+                             const float* backgrounds, const int32_t* point_list,
+                             const int32_t* ranges, int64_t images, int32_t width,
+                             int32_t height, float near_plane, float far_plane,
+                             float* const* maps, const int64_t* map_strides, float* state,
+                             int32_t* contributors, int32_t* replay, int64_t replay_capacity,
+                             int32_t* replay_counts, void* stream);
+
 /* Gradients are ACCUMULATED (global float atomics) into grad_geometry
  * [Q,17], grad_appearance [P,A], grad_opacities [P], grad_backgrounds
  * [I,3]; the caller zero-initialises them. grad_maps uses the channel-group
