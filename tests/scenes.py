@@ -203,7 +203,8 @@ def pixel_reference(method, values, width=9, height=9, near=0.2, far=100.0):
     return torch.stack(images).reshape(S, C, height, width, 9)
 
 
-def fp32_conditioned(render, values, eps=3e-7, trials=3, atol=1e-5, rtol=1e-4, **options):
+def fp32_conditioned(render, values, eps=3e-7, trials=3, atol=1e-5, rtol=1e-4,
+                     return_worst=False, **options):
     """float64 oracle maps and a mask of the pixels that are well conditioned at
     float32 precision.
 
@@ -214,7 +215,9 @@ def fp32_conditioned(render, values, eps=3e-7, trials=3, atol=1e-5, rtol=1e-4, *
     them ill-conditioned) and samples sitting on a discrete threshold
     (alpha = 1/255, the stop test, the surface/screen switch). No float32
     implementation, the reference's included, can match float64 there.
-    `render(**values, **options)` must return the maps first.
+    `render(**values, **options)` must return the maps first. With
+    `return_worst` the largest change of every output element under the
+    perturbations is returned as well (the pixel's float64 sensitivity).
     """
     base = {k: v.detach().cpu().double() for k, v in values.items()}
     with torch.no_grad():
@@ -226,6 +229,8 @@ def fp32_conditioned(render, values, eps=3e-7, trials=3, atol=1e-5, rtol=1e-4, *
                      for k, v in base.items()}
             worst = torch.maximum(worst, (render(**noisy, **options)[0] - maps).abs())
     mask = ~(worst > atol + rtol * maps.abs()).any(-1)
+    if return_worst:
+        return maps, mask, worst
     return maps, mask
 
 
