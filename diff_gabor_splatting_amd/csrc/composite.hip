@@ -1011,8 +1011,8 @@ __global__ __launch_bounds__(kTilePixels, Neural ? 2 : 4) void renderBackward(
   // Background gradient: sum over the tile of final T * dL/drgb.
   {
     const float gb[3] = {final_t * go[0], final_t * go[1], final_t * go[2]};
-    const float total = wave_reduce_scatter<3>(gb, lane);
-    const int param = rs_param<3>(lane);
+    const float total = wave_reduce_quads<3>(gb, lane);
+    const int param = rs_quad_param<3>(lane);
     if (param < 3 && total != 0.f) atomicAdd(&bg_acc[param], total);
   }
   // Records walked backwards: list positions up to the tile's largest
@@ -1171,8 +1171,8 @@ __global__ __launch_bounds__(kTilePixels, Neural ? 2 : 4) void renderBackward(
         // Wave totals, one per lane, added into the batch accumulator.
         float* dst = acc + j * NP;
         if constexpr (NP <= 64) {
-          const float total = wave_reduce_scatter<NP>(grad, lane);
-          const int param = rs_param<NP>(lane);
+          const float total = wave_reduce_quads<NP>(grad, lane);
+          const int param = rs_quad_param<NP>(lane);
           if (param < NP && total != 0.f) atomicAdd(dst + param, total);
         } else {
           constexpr int H = NP / 2;
@@ -1181,11 +1181,11 @@ __global__ __launch_bounds__(kTilePixels, Neural ? 2 : 4) void renderBackward(
           for (int k = 0; k < H; ++k) lo[k] = grad[k];
 #pragma unroll
           for (int k = 0; k < NP - H; ++k) hi[k] = grad[H + k];
-          const float t0 = wave_reduce_scatter<H>(lo, lane);
-          const int p0 = rs_param<H>(lane);
+          const float t0 = wave_reduce_quads<H>(lo, lane);
+          const int p0 = rs_quad_param<H>(lane);
           if (p0 < H && t0 != 0.f) atomicAdd(dst + p0, t0);
-          const float t1 = wave_reduce_scatter<NP - H>(hi, lane);
-          const int p1 = rs_param<NP - H>(lane);
+          const float t1 = wave_reduce_quads<NP - H>(hi, lane);
+          const int p1 = rs_quad_param<NP - H>(lane);
           if (p1 < NP - H && t1 != 0.f) atomicAdd(dst + H + p1, t1);
         }
       };

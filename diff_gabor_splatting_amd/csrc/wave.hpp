@@ -80,11 +80,58 @@ __device__ __forceinline__ float exchange_add(float lo, float hi, int lane) {
   }
 }
 
+// Four bank-masked mirror exchanges (bits 3 or 2, see exchange_add) in one
+// block: their inputs were all written before it, so one s_nop covers the
+// DPP read hazard of all eight adds.
+template <int B>
+__device__ __forceinline__ void exchange_add4(const float* lo, const float* hi, float* out) {
+  static_assert(B == 3 || B == 2, "bank-masked exchanges exist for lane bits 3 and 2");
+  if constexpr (B == 3) {
+    asm("s_nop 1\n\t"
+        "v_add_f32_dpp %0, %8, %8 row_mirror row_mask:0xf bank_mask:0xc\n\t"
+        "v_add_f32_dpp %0, %4, %4 row_mirror row_mask:0xf bank_mask:0x3\n\t"
+        "v_add_f32_dpp %1, %9, %9 row_mirror row_mask:0xf bank_mask:0xc\n\t"
+        "v_add_f32_dpp %1, %5, %5 row_mirror row_mask:0xf bank_mask:0x3\n\t"
+        "v_add_f32_dpp %2, %10, %10 row_mirror row_mask:0xf bank_mask:0xc\n\t"
+        "v_add_f32_dpp %2, %6, %6 row_mirror row_mask:0xf bank_mask:0x3\n\t"
+        "v_add_f32_dpp %3, %11, %11 row_mirror row_mask:0xf bank_mask:0xc\n\t"
+        "v_add_f32_dpp %3, %7, %7 row_mirror row_mask:0xf bank_mask:0x3"
+        : "=&v"(out[0]), "=&v"(out[1]), "=&v"(out[2]), "=&v"(out[3])
+        : "v"(lo[0]), "v"(lo[1]), "v"(lo[2]), "v"(lo[3]), "v"(hi[0]), "v"(hi[1]), "v"(hi[2]),
+          "v"(hi[3]));
+  } else {
+    asm("s_nop 1\n\t"
+        "v_add_f32_dpp %0, %8, %8 row_half_mirror row_mask:0xf bank_mask:0xa\n\t"
+        "v_add_f32_dpp %0, %4, %4 row_half_mirror row_mask:0xf bank_mask:0x5\n\t"
+        "v_add_f32_dpp %1, %9, %9 row_half_mirror row_mask:0xf bank_mask:0xa\n\t"
+        "v_add_f32_dpp %1, %5, %5 row_half_mirror row_mask:0xf bank_mask:0x5\n\t"
+        "v_add_f32_dpp %2, %10, %10 row_half_mirror row_mask:0xf bank_mask:0xa\n\t"
+        "v_add_f32_dpp %2, %6, %6 row_half_mirror row_mask:0xf bank_mask:0x5\n\t"
+        "v_add_f32_dpp %3, %11, %11 row_half_mirror row_mask:0xf bank_mask:0xa\n\t"
+        "v_add_f32_dpp %3, %7, %7 row_half_mirror row_mask:0xf bank_mask:0x5"
+        : "=&v"(out[0]), "=&v"(out[1]), "=&v"(out[2]), "=&v"(out[3])
+        : "v"(lo[0]), "v"(lo[1]), "v"(lo[2]), "v"(lo[3]), "v"(hi[0]), "v"(hi[1]), "v"(hi[2]),
+          "v"(hi[3]));
+  }
+}
+
 template <int B, int N>
 __device__ __forceinline__ void rs_step(const float* in, float* out, int lane) {
   constexpr int H = (N + 1) / 2;
+  // Bank-masked exchanges go four to a block; the rest one at a time.
+  constexpr int kGrouped = (B == 3 || B == 2) ? H / 4 * 4 : 0;
 #pragma unroll
-  for (int i = 0; i < H; ++i) {
+  for (int i = 0; i < kGrouped; i += 4) {
+    float lo[4], hi[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      lo[k] = in[i + k];
+      hi[k] = (i + k + H < N) ? in[i + k + H] : 0.0f;
+    }
+    if constexpr (kGrouped > 0) exchange_add4<(B == 3 ? 3 : 2)>(lo, hi, out + i);
+  }
+#pragma unroll
+  for (int i = kGrouped; i < H; ++i) {
     const float lo = in[i];
     const float hi = (i + H < N) ? in[i + H] : 0.0f;
     out[i] = exchange_add<B>(lo, hi, lane);
@@ -146,6 +193,67 @@ __device__ __forceinline__ float wave_reduce_scatter(const float (&v)[N], int la
   rs_step<5, S::h0>(d, e, lane);
   rs_step<4, S::h5>(e, f, lane);
   return f[0];
+}
+
+// wave_reduce_quads<N>: the same sums, distributed per quad. Recursive
+// halving runs over lane bits 3, 2, 5 and 4 only, which leaves each lane a
+// slice of Q = RsQuadShape<N>::h4 (at most 4) partial sums shared by the
+// four lanes of its quad (lane bits 1 and 0); a butterfly of two DPP adds
+// per value then completes those sums in every lane of the quad. Lane
+// `lane` holds the total of parameter rs_quad_param<N>(lane) in the value it
+// returns (N for a lane whose quad position is past its slice). For N = 33
+// that is 74 VALU operations instead of the 82 of wave_reduce_scatter,
+// whose quad-level halving steps need two selects per value.
+template <int N>
+struct RsQuadShape {
+  static constexpr int h3 = (N + 1) / 2;
+  static constexpr int h2 = (h3 + 1) / 2;
+  static constexpr int h5 = (h2 + 1) / 2;
+  static constexpr int h4 = (h5 + 1) / 2;
+};
+
+template <int N>
+__device__ __forceinline__ int rs_quad_param(int lane) {
+  using S = RsQuadShape<N>;
+  constexpr int kBits[4] = {3, 2, 5, 4};
+  constexpr int kHalf[4] = {S::h3, S::h2, S::h5, S::h4};
+  int first = 0, count = N;
+#pragma unroll
+  for (int step = 0; step < 4; ++step) {
+    const int half = kHalf[step];
+    if ((lane >> kBits[step]) & 1) {
+      first += half;
+      count = count > half ? count - half : 0;
+    } else {
+      count = count < half ? count : half;
+    }
+  }
+  const int q = lane & 3;
+  return q < count ? first + q : N;
+}
+
+// All 64 lanes must be active. Returns this lane's total (see rs_quad_param).
+template <int N>
+__device__ __forceinline__ float wave_reduce_quads(const float (&v)[N], int lane) {
+  static_assert(N >= 1 && N <= 64, "one reduction covers at most 64 values");
+  using S = RsQuadShape<N>;
+  static_assert(S::h4 <= 4, "a quad publishes at most four values");
+  float a[S::h3], b[S::h2], c[S::h5], d[S::h4];
+  rs_step<3, N>(v, a, lane);
+  rs_step<2, S::h3>(a, b, lane);
+  rs_step<5, S::h2>(b, c, lane);
+  rs_step<4, S::h5>(c, d, lane);
+  // Butterfly within the quad: every lane ends with the quad's sums.
+#pragma unroll
+  for (int i = 0; i < S::h4; ++i) {
+    d[i] += dpp_move<kDppQuadXor1>(d[i]);
+    d[i] += dpp_move<kDppQuadXor2>(d[i]);
+  }
+  const int q = lane & 3;
+  float out = d[0];
+#pragma unroll
+  for (int i = 1; i < S::h4; ++i) out = q == i ? d[i] : out;
+  return out;
 }
 
 // Full-wave integer maximum (all lanes receive the result).
