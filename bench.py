@@ -256,8 +256,8 @@ def main(argv=None):
     parser.add_argument("--cpu-crop", type=int, default=32,
                         help="edge in pixels of the secondary config-4 CPU crop (0: skip it)")
     parser.add_argument("--copy-calibration", action="store_true",
-                        help="only copy 1 GiB device-to-device three times and exit; the "
-                             "rocprof FETCH_SIZE/WRITE_SIZE of this copy scales the counters")
+                        help="only copy 1 GiB device-to-device three times and exit: the "
+                             "known-size kernel that fixes how rocprof byte counters read")
     args = parser.parse_args(argv)
     if args.gpus != 1:
         print(
@@ -383,7 +383,10 @@ def measured_valu(kernel: str, workload: str, avg_ms: float):
     """VALU issue of ``kernel`` from the committed rocprof counter summary:
     SQ_INSTS_VALU per launch, the time issuing them takes at one wave64
     instruction per SIMD every 4 cycles, and that time as a fraction of the
-    launch time measured in this run. None when no summary covers it."""
+    launch time measured in this run; plus the profiled run's own busy
+    fractions (4-cycle model and SQ_ACTIVE_INST_VALU, which also charges the
+    extra cycles of multi-cycle instructions) and its LDS busy fraction.
+    None when no summary covers it."""
     path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
                         f"{kernel}_valu.json")
     try:
@@ -395,15 +398,21 @@ def measured_valu(kernel: str, workload: str, avg_ms: float):
         return None
     issue_ms = summary["valu_instructions"] / VALU_ISSUE_PER_S * 1e3
     return {"instructions": summary["valu_instructions"], "issue_ms": round(issue_ms, 4),
-            "frac": round(issue_ms / avg_ms, 4), "source": summary.get("source")}
+            "frac": round(issue_ms / avg_ms, 4),
+            "profiled_busy_model": summary.get("busy_model"),
+            "profiled_busy_measured": summary.get("busy_measured"),
+            "profiled_lds_busy": summary.get("lds_busy"),
+            "source": summary.get("source")}
 
 
 def measured_traffic(kernel: str, workload: str):
-    """HBM bytes per launch of ``kernel`` from the committed rocprof counter summary.
+    """Bytes per launch of ``kernel`` between L2 and memory, from the
+    committed rocprof counter summary of the same bench command.
 
-    The summary records FETCH_SIZE and WRITE_SIZE (KiB per dispatch) of the
-    same bench command and the factors that turn each into bytes, taken from
-    the copy calibration above. None when no summary covers this workload.
+    The summary holds read bytes (128/64/32 x TCC_EA0_RDREQ_128B/_64B/_32B)
+    and written bytes (64 x TCC_EA0_WRREQ_64B + 32 x the other write
+    requests, atomics included), a split that a 1 GiB device copy reads back
+    exactly. None when no summary covers this workload.
     """
     path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
                         f"{kernel}_traffic.json")
@@ -414,8 +423,7 @@ def measured_traffic(kernel: str, workload: str):
         return None
     if summary.get("kernel") != kernel or summary.get("workload") != workload:
         return None
-    return int(summary["fetch_kib"] * 1024 * summary["fetch_factor"]
-               + summary["write_kib"] * 1024 * summary["write_factor"])
+    return int(summary["read_bytes"] + summary["write_bytes"])
 
 
 def workload_stats(values, renderer, options):

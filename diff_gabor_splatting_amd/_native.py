@@ -135,6 +135,8 @@ _SIGNATURES = {
     ),
     "gs_profile_enable": (_c_int, [_c_int]),
     "gs_profile_read": (_c_int, [_c_int, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(_c_i64)]),
+    "gs_diagnostics_query": (_c_int, [ctypes.POINTER(_c_int), ctypes.POINTER(_c_int)]),
+    "gs_diagnostics_set": (_c_int, [_c_ptr, _c_ptr, _c_ptr, _c_i64]),
 }
 
 PROFILE_FAMILIES = {
@@ -150,13 +152,13 @@ PROFILE_FAMILIES = {
 }
 
 
-def _load() -> ctypes.CDLL:
-    if not _LIBRARY_PATH.exists():
+def _load(path: Path = _LIBRARY_PATH) -> ctypes.CDLL:
+    if not path.exists():
         raise ImportError(
-            f"{_LIBRARY_PATH.name} is not built; run `python -m diff_gabor_splatting_amd.build` "
+            f"{path.name} is not built; run `python -m diff_gabor_splatting_amd.build` "
             "(or __graft_entry__.build()) first. There is no CPU fallback."
         )
-    library = ctypes.CDLL(str(_LIBRARY_PATH))
+    library = ctypes.CDLL(str(path))
     for name, (restype, argtypes) in _SIGNATURES.items():
         function = getattr(library, name)
         function.restype = restype
@@ -165,6 +167,15 @@ def _load() -> ctypes.CDLL:
 
 
 lib = _load()
+
+
+def use_library(path: Path) -> None:
+    """Route every later call of this module through the library at ``path``,
+    a build of the same sources with the same entry points (the diagnostics
+    build). Tensors and streams are unaffected; kernels already queued keep
+    running from the library that launched them."""
+    global lib
+    lib = _load(Path(path))
 
 
 def exported_symbols() -> list[str]:

@@ -1,7 +1,10 @@
 """Build the gfx950 HIP library ``libgabor_hip.so`` in-tree with hipcc.
 
 Every ``csrc/*.hip`` file is compiled to an object under ``_build/`` and the
-objects are linked into ``diff_gabor_splatting_amd/libgabor_hip.so``. The
+objects are linked into ``diff_gabor_splatting_amd/libgabor_hip.so``. With
+``diagnostics=True`` the same sources are compiled with ``-DGS_DIAGNOSTICS``
+under ``_build/diagnostics/`` into ``libgabor_hip_diag.so``, whose compositors
+also record per-tile times and active-lane counts (gs_diagnostics_set). The
 library links the HIP runtime by its SONAME (``libamdhip64.so.7``), so when it
 is loaded after ``import torch`` it binds to the runtime torch already loaded
 and shares torch's streams and allocations.
@@ -24,6 +27,7 @@ SOURCE_DIR = PACKAGE_DIR / "csrc"
 INCLUDE_DIR = REPO_DIR / "include"
 BUILD_DIR = REPO_DIR / "_build"
 LIBRARY = PACKAGE_DIR / "libgabor_hip.so"
+DIAGNOSTICS_LIBRARY = PACKAGE_DIR / "libgabor_hip_diag.so"
 ARCH = os.environ.get("GABOR_HIP_ARCH", "gfx950")
 
 COMPILE_FLAGS = [
@@ -58,9 +62,10 @@ def _quiet(text: str) -> str:
     )
 
 
-def _compile(source: Path, verbose: bool) -> Path:
-    obj = BUILD_DIR / (source.stem + ".o")
-    cmd = [_hipcc(), *COMPILE_FLAGS, f"-I{INCLUDE_DIR}", f"-I{SOURCE_DIR}", "-c", str(source)]
+def _compile(source: Path, verbose: bool, directory: Path, defines: list[str]) -> Path:
+    obj = directory / (source.stem + ".o")
+    cmd = [_hipcc(), *COMPILE_FLAGS, *defines, f"-I{INCLUDE_DIR}", f"-I{SOURCE_DIR}", "-c",
+           str(source)]
     cmd += ["-o", str(obj)]
     result = subprocess.run(cmd, capture_output=True, text=True)
     messages = _quiet(result.stdout + result.stderr)
@@ -71,26 +76,32 @@ def _compile(source: Path, verbose: bool) -> Path:
     return obj
 
 
-def build_library(verbose: bool = False) -> Path:
-    """Compile every HIP source for gfx950 and link the shared library."""
-    BUILD_DIR.mkdir(exist_ok=True)
+def build_library(verbose: bool = False, diagnostics: bool = False) -> Path:
+    """Compile every HIP source for gfx950 and link the shared library (the
+    diagnostics build with ``diagnostics``)."""
+    directory = BUILD_DIR / "diagnostics" if diagnostics else BUILD_DIR
+    library = DIAGNOSTICS_LIBRARY if diagnostics else LIBRARY
+    defines = ["-DGS_DIAGNOSTICS"] if diagnostics else []
+    directory.mkdir(parents=True, exist_ok=True)
     sources = sorted(SOURCE_DIR.glob("*.hip"))
     if not sources:
         raise RuntimeError(f"no HIP sources under {SOURCE_DIR}")
     jobs = min(len(sources), max(1, min(8, os.cpu_count() or 1)))
     with concurrent.futures.ThreadPoolExecutor(jobs) as pool:
-        objects = list(pool.map(lambda s: _compile(s, verbose), sources))
-    temporary = LIBRARY.with_suffix(".so.tmp")
+        objects = list(pool.map(lambda s: _compile(s, verbose, directory, defines), sources))
+    temporary = library.with_suffix(".so.tmp")
     cmd = [_hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objects)]
     cmd += ["-o", str(temporary)]
     result = subprocess.run(cmd, capture_output=True, text=True)
     if result.returncode != 0:
         raise RuntimeError(f"link failed:\n{_quiet(result.stdout + result.stderr)}")
-    os.replace(temporary, LIBRARY)
+    os.replace(temporary, library)
     if verbose:
-        print(f"built {LIBRARY}", file=sys.stderr)
-    return LIBRARY
+        print(f"built {library}", file=sys.stderr)
+    return library
 
 
 if __name__ == "__main__":
     build_library(verbose=True)
+    if "--diagnostics" in sys.argv[1:]:
+        build_library(verbose=True, diagnostics=True)

@@ -44,6 +44,28 @@ namespace gs {
 namespace {
 
 constexpr int kBatch = 64;
+
+// Diagnostics build (-DGS_DIAGNOSTICS, libgabor_hip_diag.so): the
+// compositors also stamp each tile's begin and end on the wall clock and the
+// backward counts, per (record, wave) it processes, how many lanes take the
+// record. Targets are device pointers set by gs_diagnostics_set; a null
+// target records nothing. The product build compiles none of this.
+struct DiagnosticTargets {
+  unsigned long long* lanes;  // [65]: processed (record, wave) pairs by taking lanes
+  long long* forward_span;    // [tiles][2]: wall-clock begin, end of each tile
+  long long* backward_span;   // [tiles][2]
+  long long tiles;
+};
+#ifdef GS_DIAGNOSTICS
+__device__ DiagnosticTargets gs_diagnostics;
+
+__device__ __forceinline__ void stamp_tile(long long* span, int tile, long long begin) {
+  if (threadIdx.x == 0 && span && tile < gs_diagnostics.tiles) {
+    span[2 * int64_t(tile)] = begin;
+    span[2 * int64_t(tile) + 1] = wall_clock64();
+  }
+}
+#endif
 constexpr float kTwoPi = 6.28318530717958647692f;
 constexpr float kInvTwoPi = 0.15915494309189533577f;
 constexpr float kNegHalfLog2e = -0.72134752044448170368f;  // -log2(e) / 2
@@ -749,6 +771,9 @@ __global__ __launch_bounds__(kTilePixels, Neural ? 4 : 6) void renderForward(
   __shared__ int64_t prims[kBatch];
   __shared__ uint64_t wave_taken[kTilePixels / 64];
   const int tile = order[blockIdx.x];
+#ifdef GS_DIAGNOSTICS
+  const long long diag_begin = wall_clock64();
+#endif
   const TilePixel tp = tile_pixel(tile, width, height, tw, th);
   const float x = float(tp.px), y = float(tp.py);
   const int wave = threadIdx.x >> 6;
@@ -853,6 +878,10 @@ __global__ __launch_bounds__(kTilePixels, Neural ? 4 : 6) void renderForward(
     state[tp.pixel * 3 + 2] = m2;
     contributors[tp.pixel] = last;
   }
+#ifdef GS_DIAGNOSTICS
+  __syncthreads();
+  stamp_tile(gs_diagnostics.forward_span, tile, diag_begin);
+#endif
 }
 
 // Appearance adjoint given dL/dcolor = gc. Writes the raw appearance
@@ -976,6 +1005,11 @@ __global__ __launch_bounds__(kTilePixels, Neural ? 2 : 4) void renderBackward(
   __shared__ float bg_acc[3];
   const int lane = lane_id();
   const int tile = order[blockIdx.x];
+#ifdef GS_DIAGNOSTICS
+  const long long diag_begin = wall_clock64();
+  __shared__ unsigned int diag_lanes[65];
+  for (int i = threadIdx.x; i < 65; i += kTilePixels) diag_lanes[i] = 0u;
+#endif
   const TilePixel tp = tile_pixel(tile, width, height, tw, th);
   const float x = float(tp.px), y = float(tp.py);
   const int wave = threadIdx.x >> 6;
@@ -1085,6 +1119,12 @@ __global__ __launch_bounds__(kTilePixels, Neural ? 2 : 4) void renderBackward(
       const bool active =
           sample_surface<Neural, true>(r, x, y, near_plane, tp.inside && position <= last, v);
       if (!__any(active)) continue;
+#ifdef GS_DIAGNOSTICS
+      {
+        const uint64_t taking = __ballot(active);
+        if (lane == 0) atomicAdd(&diag_lanes[__popcll(taking)], 1u);
+      }
+#endif
       // Every lane runs the adjoint. A lane that does not take the sample
       // contributes exact zeros: the sample's values are finite stand-ins
       // (alpha, e, s and 1/p_z zero, depth one), so its weight w and every
@@ -1222,6 +1262,12 @@ __global__ __launch_bounds__(kTilePixels, Neural ? 2 : 4) void renderBackward(
   __syncthreads();
   if (threadIdx.x < 3 && bg_acc[threadIdx.x] != 0.f)
     atomicAdd(grad_backgrounds + tp.image * 3 + threadIdx.x, bg_acc[threadIdx.x]);
+#ifdef GS_DIAGNOSTICS
+  if (gs_diagnostics.lanes && threadIdx.x < 65 && diag_lanes[threadIdx.x] != 0u)
+    atomicAdd(gs_diagnostics.lanes + threadIdx.x,
+              static_cast<unsigned long long>(diag_lanes[threadIdx.x]));
+  stamp_tile(gs_diagnostics.backward_span, tile, diag_begin);
+#endif
 }
 
 struct RenderWorkspace {
@@ -1481,6 +1527,37 @@ int gs_render_backward(int32_t neural, const float* geometry, const float* appea
   }
   GS_LAUNCHED("renderBackward");
   return GS_OK;
+}
+
+int gs_diagnostics_query(int32_t* available, int32_t* wall_clock_khz) {
+  GS_REQUIRE(available && wall_clock_khz, GS_ERR_ARGUMENT, "null diagnostics query output");
+#ifdef GS_DIAGNOSTICS
+  *available = 1;
+#else
+  *available = 0;
+#endif
+  int device = 0, khz = 0;
+  GS_HIP(hipGetDevice(&device));
+  GS_HIP(hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, device));
+  *wall_clock_khz = khz;
+  return GS_OK;
+}
+
+int gs_diagnostics_set(unsigned long long* lanes, long long* forward_span,
+                       long long* backward_span, int64_t tiles) {
+  GS_REQUIRE(tiles >= 0, GS_ERR_ARGUMENT, "diagnostics tile count must be non-negative");
+#ifdef GS_DIAGNOSTICS
+  const gs::DiagnosticTargets targets{lanes, forward_span, backward_span, tiles};
+  GS_HIP(hipMemcpyToSymbol(HIP_SYMBOL(gs::gs_diagnostics), &targets, sizeof targets));
+  return GS_OK;
+#else
+  (void)lanes;
+  (void)forward_span;
+  (void)backward_span;
+  GS_REQUIRE(false, GS_ERR_ARGUMENT,
+             "this library was built without diagnostics (libgabor_hip_diag.so has them)");
+  return GS_ERR_ARGUMENT;
+#endif
 }
 
 }  // extern "C"

@@ -390,6 +390,26 @@ int gs_render_backward(int32_t neural, const float* geometry, const float* appea
                        void* stream);
 
 /* ------------------------------------------------------------------ */
+/* Diagnostics. No counterpart in the reference. The same sources built with
+ * -DGS_DIAGNOSTICS form libgabor_hip_diag.so, whose compositors also record
+ * (a) per tile, the wall-clock stamps at which its workgroup began and ended,
+ * in forward_span / backward_span [tiles][2] (int64, wall-clock ticks), and
+ * (b) per (record, wave) the backward processes, the number of the wave's 64
+ * lanes that take the record, as a histogram added into lanes [65] (uint64;
+ * the caller clears it). These cost a few instructions per processed
+ * (record, wave), so the diagnostics library is for measurement only.    */
+
+/* *available = 1 in the diagnostics library, 0 in the product library;
+ * *wall_clock_khz = the current device's wall-clock rate. */
+int gs_diagnostics_query(int32_t* available, int32_t* wall_clock_khz);
+
+/* Set the diagnostics targets on the current device (device pointers, null
+ * to record nothing; spans are written for tile indices below `tiles`).
+ * Synchronous. The product library returns GS_ERR_ARGUMENT. */
+int gs_diagnostics_set(unsigned long long* lanes, long long* forward_span,
+                       long long* backward_span, int64_t tiles);
+
+/* ------------------------------------------------------------------ */
 /* Kernel timing for measurement: when enabled, each compositor / sort /
  * projection launch is bracketed by HIP events on its own stream.        */
 
