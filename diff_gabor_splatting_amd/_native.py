@@ -400,8 +400,8 @@ def bin_tiles(order, starts, rects, images, width, height, intersections, visibl
 
 def bin_tiles_bounded(order, starts, rects, images, width, height, capacity, intersections):
     """Depth-first binning, stage 2, without reading M on the host: a point
-    list of `capacity` entries and the live count `intersections` (int64 [1]
-    on the device). Returns (point_list, ranges, overflow) with overflow an
+    list of `capacity` entries (those past the live count are -1) and the
+    live count `intersections` (int64 [1] on the device). Returns (point_list, ranges, overflow) with overflow an
     int32 [1] device word of BINNING_* bits: BINNING_OVERFLOW when M
     exceeded the capacity, BINNING_BAD_INDEX as in bin_tiles."""
     device = order.device

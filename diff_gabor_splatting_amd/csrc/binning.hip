@@ -316,7 +316,11 @@ __global__ __launch_bounds__(256) void find_tile_ranges_kernel(int64_t capacity,
                                                                uint32_t* status) {
   const int64_t m = live ? min(capacity, max(*live, int64_t(0))) : capacity;
   const int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x;
-  if (i >= m) return;
+  if (i >= m) {
+    // Bounded binning: the entries past the live count are defined as -1.
+    if (i < capacity) point_list[i] = -1;
+    return;
+  }
   const uint32_t key = ids[i];
   const uint32_t tile = Packed ? key >> rank_bits : key;
   bool bad = false;

@@ -300,7 +300,7 @@ int gs_bin_tiles(const int32_t* order, const int64_t* starts, const int32_t* rec
  * gs_bin_tiles_workspace_size(capacity)); the live count is read from
  * *intersections, the device word gs_bin_order wrote. The first
  * min(count, capacity) entries of the depth-first emission are binned and
- * ranges cover exactly those. *overflow (a device uint32) is cleared, then
+ * ranges cover exactly those; the point-list entries past them are -1. *overflow (a device uint32) is cleared, then
  * gets GS_BIN_OVERFLOW when the count exceeds the capacity (the deepest
  * records were then dropped from their tiles) and GS_BIN_BAD_INDEX as in
  * gs_bin_tiles. No counterpart in the reference, which reads the count on
