@@ -30,6 +30,27 @@ MAP_SIZE = 9
 INT_MAX = 2**31 - 1
 # Replay-list entries carry a tile-list position in 28 bits.
 REPLAY_MAX_ENTRIES = 2**28 - 1
+# Split tiles (gs_render_forward's segment_* arguments): images with fewer
+# tiles than this have too few workgroups to hide a long tile list, so the
+# backward replays long lists in segments; the segment length is chosen so
+# that the intersections make about SPLIT_TARGET_SEGMENTS segments.
+SPLIT_MAX_TILES = 2048
+SPLIT_TARGET_SEGMENTS = 2048
+CHECKPOINT_FLOATS = 10
+
+
+def split_length(tiles: int, intersections: int) -> int:
+    """List records per backward segment of a split tile (a multiple of 64),
+    or 0 to split none."""
+    if tiles >= SPLIT_MAX_TILES or intersections <= 0:
+        return 0
+    return 64 * max(1, -(-intersections // (64 * SPLIT_TARGET_SEGMENTS)))
+
+
+def split_slots(intersections: int, length: int) -> int:
+    """Checkpoint slots that always suffice: a tile of L > length records
+    needs ceil(L / length) <= floor(2 L / length) of them."""
+    return 2 * intersections // length if length else 0
 
 _c_int = ctypes.c_int32
 _c_i64 = ctypes.c_int64
@@ -106,6 +127,7 @@ _SIGNATURES = {
         + [_c_size, _c_ptr],
     ),
     "gs_render_workspace_size": (_c_size, [_c_i64, _c_int, _c_int]),
+    "gs_render_backward_workspace_size": (_c_size, [_c_i64, _c_int, _c_int, _c_i64]),
     "gs_render_forward": (
         _c_int,
         [_c_int]
@@ -113,8 +135,9 @@ _SIGNATURES = {
         + [_c_i64, _c_int, _c_int, _c_float, _c_float]
         + [_c_ptr] * 5
         + [_c_i64]
-        + [_c_ptr] * 2
-        + [_c_size, _c_ptr],
+        + [_c_ptr]
+        + [_c_int, _c_ptr, _c_ptr, _c_i64]
+        + [_c_ptr, _c_size, _c_ptr],
     ),
     "gs_render_forward_static": (
         _c_int,
@@ -128,7 +151,9 @@ _SIGNATURES = {
     "gs_render_backward": (
         _c_int,
         [_c_int]
-        + [_c_ptr] * 13
+        + [_c_ptr] * 11
+        + [_c_int, _c_ptr, _c_ptr, _c_i64]
+        + [_c_ptr] * 2
         + [_c_i64, _c_int, _c_int, _c_float, _c_float]
         + [_c_ptr] * 5
         + [_c_size, _c_ptr],
@@ -741,7 +766,7 @@ def _map_group_args(groups, what: str):
 def rasterize_forward(
     geometry, appearance, opacities, primitive_ids, image_ids, radii, backgrounds,
     width, height, neural, near_plane, far_plane, outputs=None, overlap=None, capacity=None,
-    flags=None, replay=False, violations=None,
+    flags=None, replay=False, violations=None, split=None,
 ):
     """Bin, sort and composite: returns [maps, point_list, ranges, state, contributors].
 
@@ -758,9 +783,15 @@ def rasterize_forward(
     into a point list of fixed capacity without reading M on the host (see
     bin_depth_first). ``replay`` (an addition): also return, as a sixth item,
     the tiles' replay lists for rasterize_backward - (lists [M, 2] int32,
-    counts [I*tw*th] int32): per tile, the point-list entries that some pixel
-    took, in list order - or None when the point list is too long for them
-    (2^28 entries or more). ``violations`` (an addition): a pending value
+    counts [I*tw*th] int32, segments): per tile, the point-list entries that
+    some pixel took, in list order - or None when the point list is too long
+    for them (2^28 entries or more). ``segments`` is None, or (length,
+    checkpoint state, checkpoint index) when tiles are split: tiles longer
+    than ``length`` records have their backward replayed in segments of that
+    many list records, each from a checkpoint the forward wrote (see
+    gs_render_forward). ``split`` (an addition): the segment length, 0 for
+    none, or None to choose it (split_length: only images with fewer than
+    SPLIT_MAX_TILES tiles are split). ``violations`` (an addition): a pending value
     check, raised with the read-back of M (see bin_depth_first).
     """
     _check_buffers(geometry, appearance, opacities, primitive_ids, backgrounds, neural)
@@ -814,10 +845,20 @@ def rasterize_forward(
             maps = tuple(groups)
         data, strides = _map_group_args(groups, "map outputs")
         lists = None
+        length, slots, segment_state, segment_index = 0, 0, None, None
         if replay and point_list.numel() < REPLAY_MAX_ENTRIES:
+            length = split_length(tiles, point_list.numel()) if split is None else int(split)
+            slots = split_slots(point_list.numel(), length)
+            if slots:
+                segment_state = torch.empty((slots, CHECKPOINT_FLOATS, TILE * TILE),
+                                            dtype=torch.float32, device=device)
+                segment_index = torch.empty(tiles + slots, dtype=torch.int32, device=device)
+            else:
+                length = 0
             lists = (torch.empty((max(point_list.numel(), 1), 2), dtype=torch.int32,
                                  device=device),
-                     torch.empty(tiles, dtype=torch.int32, device=device))
+                     torch.empty(tiles, dtype=torch.int32, device=device),
+                     (length, segment_state, segment_index) if slots else None)
         workspace = _workspace(lib.gs_render_workspace_size(images, width, height), device)
         _check(
             lib.gs_render_forward(
@@ -825,7 +866,8 @@ def rasterize_forward(
                 _ptr(primitive_ids), _ptr(backgrounds), _ptr(point_list), _ptr(ranges), images,
                 width, height, near_plane, far_plane, data, strides, _ptr(state),
                 _ptr(contributors), _ptr(lists and lists[0]), point_list.numel(),
-                _ptr(lists and lists[1]), _ptr(workspace), workspace.numel(), stream,
+                _ptr(lists and lists[1]), length, _ptr(segment_state), _ptr(segment_index),
+                slots, _ptr(workspace), workspace.numel(), stream,
             )
         )
     if replay:
@@ -878,9 +920,22 @@ def rasterize_backward(
         and contributors.shape == (images, height, width),
         "invalid saved compositor state",
     )
+    length, slots, segment_state, segment_index = 0, 0, None, None
     if replay is not None:
         tw, th = tile_grid(width, height)
-        lists, counts = replay
+        lists, counts, *rest = replay
+        segments = rest[0] if rest else None
+        if segments is not None:
+            length, segment_state, segment_index = segments
+            slots = segment_state.shape[0]
+            _require(
+                segment_state.dtype == torch.float32 and segment_index.dtype == torch.int32
+                and segment_state.device == device and segment_index.device == device
+                and segment_state.is_contiguous() and segment_index.is_contiguous()
+                and segment_state.shape[1:] == (CHECKPOINT_FLOATS, TILE * TILE)
+                and segment_index.shape == (images * tw * th + slots,),
+                "invalid split-tile checkpoints",
+            )
         _require(
             lists.dtype == torch.int32 and counts.dtype == torch.int32
             and lists.device == device and counts.device == device
@@ -903,13 +958,15 @@ def rasterize_backward(
         )
         groups = [g if g is None else _pixel_strided(g) for g in groups]
         data, strides = _map_group_args(groups, "map gradients")
-        workspace = _workspace(lib.gs_render_workspace_size(images, width, height), device)
+        workspace = _workspace(
+            lib.gs_render_backward_workspace_size(images, width, height, slots), device)
         _check(
             lib.gs_render_backward(
                 int(bool(neural)), _ptr(geometry), _ptr(appearance), _ptr(opacities),
                 _ptr(primitive_ids), _ptr(backgrounds), _ptr(point_list), _ptr(ranges),
                 _ptr(state), _ptr(contributors), _ptr(replay and replay[0]),
-                _ptr(replay and replay[1]), data, strides, images, width, height,
+                _ptr(replay and replay[1]), length, _ptr(segment_state), _ptr(segment_index),
+                slots, data, strides, images, width, height,
                 near_plane, far_plane, _ptr(gg), _ptr(ga), _ptr(go), _ptr(gb),
                 _ptr(workspace), workspace.numel(), _stream(device),
             )

@@ -59,10 +59,14 @@ struct DiagnosticTargets {
 #ifdef GS_DIAGNOSTICS
 __device__ DiagnosticTargets gs_diagnostics;
 
+// A tile's span covers every workgroup that worked on it (the segments of a
+// split tile): the earliest begin and the latest end. The caller sets
+// begins to all ones and ends to zero.
 __device__ __forceinline__ void stamp_tile(long long* span, int tile, long long begin) {
   if (threadIdx.x == 0 && span && tile < gs_diagnostics.tiles) {
-    span[2 * int64_t(tile)] = begin;
-    span[2 * int64_t(tile) + 1] = wall_clock64();
+    auto* stamps = reinterpret_cast<unsigned long long*>(span + 2 * int64_t(tile));
+    atomicMin(stamps, static_cast<unsigned long long>(begin));
+    atomicMax(stamps + 1, static_cast<unsigned long long>(wall_clock64()));
   }
 }
 #endif
@@ -640,6 +644,45 @@ __device__ __forceinline__ int append_replay(const uint64_t* wave_taken, const i
   return n + __popcll(kept);
 }
 
+// Split tiles. A tile whose point list is longer than `length` records (a
+// multiple of kBatch) is replayed by the backward in segments, one
+// workgroup each: segment k takes the replay entries the forward appended
+// while walking list records [k length, (k + 1) length). For it the forward
+// writes checkpoints c_1 .. c_K (K = ceil(list length / length)): c_j is the
+// per-pixel prefix state after the first j length records (c_K: the final
+// state before the background), with the replay-list length at that point.
+// The backward of segment k starts from c_{k+1}: its transmittance, and the
+// sum over the later records of w dL/dw, which is linear in the prefix sums,
+// from c_K - c_{k+1} (the backward's running suffix at that point).
+struct Segments {
+  int length;    // records per segment; 0: no tile is split
+  int tiles;
+  int capacity;  // checkpoint slots
+  float* state;  // [capacity][kCheckpointFloats][kTilePixels], one slot per checkpoint
+  int* index;    // [tiles]: a split tile's first slot (-1: not split); then
+                 // [capacity]: the replay-list length at each slot's checkpoint
+};
+
+// Per pixel: T, rgb prefix (3), depth, normals (3), m1, m2.
+constexpr int kCheckpointFloats = 10;
+
+__device__ __forceinline__ int segment_count(int list_length, int length) {
+  return (length > 0 && list_length > length) ? (list_length + length - 1) / length : 1;
+}
+
+// Writes this thread's pixel into checkpoint slot `slot` (out[] holds the
+// prefix sums in map order, before the background) and, from thread 0, the
+// replay-list length n.
+__device__ __forceinline__ void write_checkpoint(const Segments& seg, int slot, float T,
+                                                 const float* out, float m1, float m2, int n) {
+  float* c = seg.state + int64_t(slot) * (kCheckpointFloats * kTilePixels) + threadIdx.x;
+  const float values[kCheckpointFloats] = {T,      out[0], out[1], out[2], out[4],
+                                           out[5], out[6], out[7], m1,     m2};
+#pragma unroll
+  for (int q = 0; q < kCheckpointFloats; ++q) c[q * kTilePixels] = values[q];
+  if (threadIdx.x == 0) seg.index[seg.tiles + slot] = n;
+}
+
 struct TilePixel {
   int image, px, py;
   bool inside;
@@ -698,12 +741,38 @@ __device__ __forceinline__ int cost_bucket(int cost) {
 }
 
 // cost: per-tile cost, or null to use the tile's list length from ranges.
+// With seg.length > 0 (the forward of split tiles) it also assigns each
+// tile longer than seg.length its ceil(length / seg.length) checkpoint
+// slots, in tile order, into seg.index[0 .. tiles) (-1: not split, or past
+// the capacity, which the host sizes so that it is never reached).
 __global__ __launch_bounds__(kOrderBlock) void tile_order_kernel(const int* __restrict__ cost,
                                                                  const int2* __restrict__ ranges,
                                                                  int tiles,
-                                                                 int* __restrict__ order) {
+                                                                 int* __restrict__ order,
+                                                                 Segments seg) {
   __shared__ int count[kOrderBuckets];
   __shared__ int next[kOrderBuckets];
+  __shared__ int scan[kOrderBlock];
+  if (seg.length > 0) {
+    int carry = 0;
+    for (int first = 0; first < tiles; first += kOrderBlock) {
+      const int t = first + threadIdx.x;
+      const int k = t < tiles ? segment_count(ranges[t].y - ranges[t].x, seg.length) : 1;
+      const int slots = k > 1 ? k : 0;
+      scan[threadIdx.x] = slots;
+      __syncthreads();
+      for (int offset = 1; offset < kOrderBlock; offset <<= 1) {  // inclusive scan
+        const int add = int(threadIdx.x) >= offset ? scan[threadIdx.x - offset] : 0;
+        __syncthreads();
+        scan[threadIdx.x] += add;
+        __syncthreads();
+      }
+      const int base = carry + scan[threadIdx.x] - slots;
+      if (t < tiles) seg.index[t] = (slots > 0 && base + slots <= seg.capacity) ? base : -1;
+      carry += scan[kOrderBlock - 1];
+      __syncthreads();
+    }
+  }
   for (int b = threadIdx.x; b < kOrderBuckets; b += kOrderBlock) count[b] = 0;
   __syncthreads();
   for (int t = threadIdx.x; t < tiles; t += kOrderBlock) {
@@ -723,6 +792,54 @@ __global__ __launch_bounds__(kOrderBlock) void tile_order_kernel(const int* __re
     const int c = cost ? cost[t] : ranges[t].y - ranges[t].x;
     order[atomicAdd(&next[cost_bucket(c)], 1)] = t;
   }
+}
+
+// The backward's workgroups when tiles are split: every (tile, segment) with
+// its replay entries as cost, heaviest first, into segments[0 .. tiles +
+// seg.capacity); entries past the segment count are (-1, 0) and their
+// workgroups exit at once.
+__device__ __forceinline__ int segment_cost(const Segments& seg, const int* replay_counts,
+                                            int tile, int k, int count) {
+  if (count == 1) return replay_counts[tile];
+  const int* n = seg.index + seg.tiles + seg.index[tile];
+  return n[k] - (k ? n[k - 1] : 0);
+}
+
+__global__ __launch_bounds__(kOrderBlock) void segment_order_kernel(
+    const int2* __restrict__ ranges, const int* __restrict__ replay_counts, int tiles,
+    Segments seg, int2* __restrict__ segments) {
+  __shared__ int count[kOrderBuckets];
+  __shared__ int next[kOrderBuckets];
+  __shared__ int total;
+  for (int b = threadIdx.x; b < kOrderBuckets; b += kOrderBlock) count[b] = 0;
+  __syncthreads();
+  auto segments_of = [&](int t) {
+    return seg.index[t] >= 0 ? segment_count(ranges[t].y - ranges[t].x, seg.length) : 1;
+  };
+  for (int t = threadIdx.x; t < tiles; t += kOrderBlock) {
+    const int n = segments_of(t);
+    for (int k = 0; k < n; ++k)
+      atomicAdd(&count[cost_bucket(segment_cost(seg, replay_counts, t, k, n))], 1);
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    int run = 0;
+    for (int b = kOrderBuckets - 1; b >= 0; --b) {
+      next[b] = run;
+      run += count[b];
+    }
+    total = run;
+  }
+  __syncthreads();
+  for (int t = threadIdx.x; t < tiles; t += kOrderBlock) {
+    const int n = segments_of(t);
+    for (int k = 0; k < n; ++k) {
+      const int bucket = cost_bucket(segment_cost(seg, replay_counts, t, k, n));
+      segments[atomicAdd(&next[bucket], 1)] = make_int2(t, k);
+    }
+  }
+  for (int i = total + threadIdx.x; i < tiles + seg.capacity; i += kOrderBlock)
+    segments[i] = make_int2(-1, 0);
 }
 
 // Largest contributor count of each tile (where the backward starts).
@@ -762,7 +879,7 @@ __global__ __launch_bounds__(kTilePixels, Neural ? 4 : 6) void renderForward(
     const int* __restrict__ point_list, const int2* __restrict__ ranges,
     const int* __restrict__ order, float near_plane, float far_plane, MapGroups<float> maps,
     float* __restrict__ state, int* __restrict__ contributors, int2* __restrict__ replay,
-    int* __restrict__ replay_counts) {
+    int* __restrict__ replay_counts, Segments seg) {
   using L = Layout<Neural, true>;
   __shared__ __align__(16) float rows[kBatch * L::STRIDE];
   __shared__ __align__(16) float raw[kBatch * L::RAW_STRIDE];
@@ -801,11 +918,18 @@ __global__ __launch_bounds__(kTilePixels, Neural ? 4 : 6) void renderForward(
   // batch, whose taken records are appended once every wave has finished it
   // (before the next batch overwrites its staged ids).
   int replay_n = 0, batch_first = 0, batch_count = 0;
+  // Split tile: its first checkpoint slot and checkpoint count (K), and the
+  // checkpoints written so far (at list records length, 2 length, ...).
+  const int slot_base = Replay && seg.length > 0 ? seg.index[tile] : -1;
+  const int checkpoints = slot_base >= 0 ? segment_count(range.y - range.x, seg.length) : 0;
+  int written = 0;
   for (int start = range.x; start < range.y; start += kBatch) {
     if (__syncthreads_count(done) == kTilePixels) break;
     if (Replay && wave == 0)
       replay_n = append_replay(wave_taken, ids, replay + range.x, replay_n, batch_first,
                                batch_count);
+    if (slot_base >= 0 && start > range.x && (start - range.x) % seg.length == 0)
+      write_checkpoint(seg, slot_base + written++, T, out, m1, m2, replay_n);
     const int count = min(kBatch, range.y - start);
     const int id = next_id;
     const int64_t prim = next_prim;
@@ -866,6 +990,10 @@ __global__ __launch_bounds__(kTilePixels, Neural ? 4 : 6) void renderForward(
                                batch_count);
       if (threadIdx.x == 0) replay_counts[tile] = replay_n;
     }
+    // The checkpoints the walk did not reach (it stopped early) and the
+    // last one hold the final state: their segments are empty.
+    for (int k = written; k < checkpoints; ++k)
+      write_checkpoint(seg, slot_base + k, T, out, m1, m2, replay_n);
   }
   if (tp.inside) {
 #pragma unroll
@@ -985,7 +1113,8 @@ __global__ __launch_bounds__(kTilePixels, Neural ? 2 : 4) void renderBackward(
     const float* __restrict__ state, const int* __restrict__ contributors,
     MapGroups<const float> grad_maps, float near_plane, float far_plane,
     float* __restrict__ grad_geometry, float* __restrict__ grad_appearance,
-    float* __restrict__ grad_opacities, float* __restrict__ grad_backgrounds) {
+    float* __restrict__ grad_opacities, float* __restrict__ grad_backgrounds,
+    const int2* __restrict__ segments, Segments seg) {
   using L = Layout<Neural>;
   constexpr int NP = L::NP;
   constexpr int NG = L::NG;
@@ -1004,7 +1133,10 @@ __global__ __launch_bounds__(kTilePixels, Neural ? 2 : 4) void renderBackward(
   __shared__ int entries[kBatch];  // replay entries (position | quadrant bits) of the batch
   __shared__ float bg_acc[3];
   const int lane = lane_id();
-  const int tile = order[blockIdx.x];
+  // (tile, segment) of this workgroup; past the segment count: nothing.
+  const int2 piece = segments ? segments[blockIdx.x] : make_int2(order[blockIdx.x], 0);
+  if (piece.x < 0) return;
+  const int tile = piece.x;
 #ifdef GS_DIAGNOSTICS
   const long long diag_begin = wall_clock64();
   __shared__ unsigned int diag_lanes[65];
@@ -1035,36 +1167,62 @@ __global__ __launch_bounds__(kTilePixels, Neural ? 2 : 4) void renderBackward(
   for (int c = 0; c < 3; ++c) background_dot += go[c] * backgrounds[tp.image * 3 + c];
   // dL/dalpha_i picks up final_t (go_alpha - background . go_rgb) / (1 - alpha_i).
   const float final_term = final_t * (go[3] - background_dot);
+  // Records walked backwards: list positions up to the tile's largest
+  // contributor count, or the replay list's entries [block_first,
+  // block_last) - all of them, or one segment's of a split tile, which
+  // starts from checkpoint c_{k+1}: its transmittance, and the suffix
+  // sum_{later records} w dL/dw from c_K - c_{k+1} (the map gradients weigh
+  // the prefix-sum differences; distortion through the final m1, m2).
+  const int2 range = ranges[tile];
+  int block_first = 0;
+  int block_last = Replay ? replay_counts[tile] : tile_last[tile];
+  float suffix = 0.f;
+  if (Replay && seg.length > 0 && seg.index[tile] >= 0) {
+    const int base = seg.index[tile];
+    const int pieces = segment_count(range.y - range.x, seg.length);
+    const int* n = seg.index + seg.tiles + base;
+    block_first = piece.y ? n[piece.y - 1] : 0;
+    block_last = n[piece.y];
+    if (piece.y < pieces - 1 && tp.inside) {
+      constexpr int kSlot = kCheckpointFloats * kTilePixels;
+      const float* c = seg.state + int64_t(base + piece.y) * kSlot + threadIdx.x;
+      const float* f = seg.state + int64_t(base + pieces - 1) * kSlot + threadIdx.x;
+      float d[kCheckpointFloats];
+#pragma unroll
+      for (int q = 0; q < kCheckpointFloats; ++q) d[q] = f[q * kTilePixels] - c[q * kTilePixels];
+      T = c[0];
+      suffix = go[0] * d[1] + go[1] * d[2] + go[2] * d[3] + go[4] * d[4] + go[5] * d[5] +
+               go[6] * d[6] + go[7] * d[7] +
+               go[8] * (total_a * d[9] - m2 * d[0] - 2.f * m1 * d[8]);
+    }
+  }
   // Whether every map gradient and saved state value of the wave's pixels is
   // finite (selects the adjoint without per-lane masking).
-  bool finite = isfinite(final_term) && isfinite(m1) && isfinite(m2);
+  bool finite = isfinite(final_term) && isfinite(m1) && isfinite(m2) && isfinite(T) &&
+                isfinite(suffix);
 #pragma unroll
   for (int c = 0; c < kMaps; ++c) finite = finite && isfinite(go[c]);
   const bool finite_pixels = __all(finite);
   __syncthreads();
-  // Background gradient: sum over the tile of final T * dL/drgb.
-  {
+  // Background gradient: sum over the tile of final T * dL/drgb (once per
+  // tile: by its first segment).
+  if (piece.y == 0) {
     const float gb[3] = {final_t * go[0], final_t * go[1], final_t * go[2]};
     const float total = wave_reduce_quads<3>(gb, lane);
     const int param = rs_quad_param<3>(lane);
     if (param < 3 && total != 0.f) atomicAdd(&bg_acc[param], total);
   }
-  // Records walked backwards: list positions up to the tile's largest
-  // contributor count, or the replay list's entries.
-  const int2 range = ranges[tile];
-  const int block_last = Replay ? replay_counts[tile] : tile_last[tile];
   // Records past every lane's last contributor are inactive in this wave.
   const int wave_last = __builtin_amdgcn_readfirstlane(wave_max(last));
   const float mscale = far_plane / (far_plane - near_plane);
   const float mnear = mscale * near_plane;
-  float suffix = 0.f;
 
   // Record threadIdx.x of a batch starting at `start` is list position (or
   // replay entry) range.x + start - 1 - threadIdx.x; the next batch's entry
   // and id are read ahead as in the forward.
   int next_id = 0, next_entry = 0;
   int64_t next_prim = 0;
-  if (int(threadIdx.x) < min(kBatch, block_last)) {
+  if (int(threadIdx.x) < min(kBatch, block_last - block_first)) {
     if constexpr (Replay) {
       const int2 e = replay[range.x + block_last - 1 - threadIdx.x];
       next_id = e.x;
@@ -1074,11 +1232,11 @@ __global__ __launch_bounds__(kTilePixels, Neural ? 2 : 4) void renderBackward(
     }
     next_prim = primitive_ids[next_id];
   }
-  for (int start = block_last; start > 0; start -= kBatch) {
-    const int count = min(kBatch, start);
+  for (int start = block_last; start > block_first; start -= kBatch) {
+    const int count = min(kBatch, start - block_first);
     const int id = next_id, entry = next_entry;
     const int64_t prim = next_prim;
-    const bool ahead = int(threadIdx.x) < min(kBatch, start - kBatch);
+    const bool ahead = int(threadIdx.x) < min(kBatch, start - kBatch - block_first);
     if (ahead) {
       if constexpr (Replay) {
         const int2 e = replay[range.x + start - kBatch - 1 - threadIdx.x];
@@ -1273,17 +1431,37 @@ __global__ __launch_bounds__(kTilePixels, Neural ? 2 : 4) void renderBackward(
 struct RenderWorkspace {
   int* order;      // [tiles]
   int* tile_last;  // [tiles]
+  int2* segments;  // [tiles + segment slots]: the backward's (tile, segment) order
   size_t bytes;
 };
 
-RenderWorkspace render_layout(void* base, int64_t tiles) {
+RenderWorkspace render_layout(void* base, int64_t tiles, int64_t segment_slots = 0) {
   RenderWorkspace w;
   char* p = static_cast<char*>(base);
   w.order = reinterpret_cast<int*>(p);
   const size_t half = align_up(size_t(tiles) * sizeof(int), 256);
   w.tile_last = reinterpret_cast<int*>(p + half);
-  w.bytes = 2 * half;
+  w.segments = segment_slots > 0 ? reinterpret_cast<int2*>(p + 2 * half) : nullptr;
+  w.bytes = 2 * half +
+            (segment_slots > 0 ? align_up(size_t(tiles + segment_slots) * sizeof(int2), 256) : 0);
   return w;
+}
+
+// Checks the split-tile arguments and describes them (length 0: off).
+int make_segments(int32_t length, float* state, int32_t* index, int64_t capacity,
+                  const void* replay, int64_t tiles, Segments* seg) {
+  *seg = Segments{0, int(tiles), 0, nullptr, nullptr};
+  if (length == 0) return GS_OK;
+  GS_REQUIRE(length > 0 && length % kBatch == 0, GS_ERR_ARGUMENT,
+             "segment length must be a positive multiple of %d, got %d", kBatch, length);
+  GS_REQUIRE(replay, GS_ERR_ARGUMENT, "split tiles need the replay lists");
+  GS_REQUIRE(state && index, GS_ERR_ARGUMENT, "null segment buffers");
+  GS_REQUIRE(capacity > 0 && tiles + capacity <= INT_MAX &&
+                 capacity <= INT64_MAX / (kCheckpointFloats * kTilePixels * 4),
+             GS_ERR_OVERFLOW, "invalid segment capacity %lld for %lld tiles",
+             static_cast<long long>(capacity), static_cast<long long>(tiles));
+  *seg = Segments{length, int(tiles), int(capacity), state, index};
+  return GS_OK;
 }
 
 template <typename T>
@@ -1359,19 +1537,19 @@ int render_forward(int32_t neural, const float* geometry, const float* appearanc
                    int64_t images, int32_t width, int32_t height, float near_plane,
                    float far_plane, const MapGroups<float>& out, float* state,
                    int32_t* contributors, int32_t* replay, int32_t* replay_counts, int* order,
-                   hipStream_t s) {
+                   const Segments& seg, hipStream_t s) {
   ProfileScope prof(GS_PROF_RENDER_FWD, s);
   const int tw = tiles_x(width), th = tiles_y(height);
   const int tiles = int(images * tw * th);
   const int2* r = reinterpret_cast<const int2*>(ranges);
-  tile_order_kernel<<<1, kOrderBlock, 0, s>>>(nullptr, r, tiles, order);
+  tile_order_kernel<<<1, kOrderBlock, 0, s>>>(nullptr, r, tiles, order, seg);
   GS_LAUNCHED("tile_order_kernel");
   int2* lists = reinterpret_cast<int2*>(replay);
   auto launch = [&](auto kernel) {
     kernel<<<unsigned(tiles), kTilePixels, 0, s>>>(
         width, height, tw, th, geometry, appearance, opacities, primitive_ids, backgrounds,
         point_list, r, order, near_plane, far_plane, out, state, contributors, lists,
-        replay_counts);
+        replay_counts, seg);
   };
   if (neural) {
     if (replay) launch(renderForward<true, true>);
@@ -1414,6 +1592,13 @@ size_t gs_render_workspace_size(int64_t images, int32_t width, int32_t height) {
   return gs::render_layout(nullptr, images * gs::tiles_x(width) * gs::tiles_y(height)).bytes + 256;
 }
 
+size_t gs_render_backward_workspace_size(int64_t images, int32_t width, int32_t height,
+                                         int64_t segment_capacity) {
+  if (images < 0 || width <= 0 || height <= 0 || segment_capacity < 0) return 256;
+  const int64_t tiles = images * gs::tiles_x(width) * gs::tiles_y(height);
+  return gs::render_layout(nullptr, tiles, segment_capacity).bytes + 256;
+}
+
 int gs_render_forward(int32_t neural, const float* geometry, const float* appearance,
                       const float* opacities, const int64_t* primitive_ids,
                       const float* backgrounds, const int32_t* point_list,
@@ -1421,23 +1606,29 @@ int gs_render_forward(int32_t neural, const float* geometry, const float* appear
                       float near_plane, float far_plane, float* const* maps,
                       const int64_t* map_strides, float* state, int32_t* contributors,
                       int32_t* replay, int64_t replay_capacity, int32_t* replay_counts,
-                      void* workspace, size_t workspace_bytes, void* stream) {
+                      int32_t segment_length, float* segment_state, int32_t* segment_index,
+                      int64_t segment_capacity, void* workspace, size_t workspace_bytes,
+                      void* stream) {
   using namespace gs;
   clear_error();
-  const int status =
+  int status =
       check_render_forward(images, width, height, near_plane, far_plane, backgrounds, ranges,
                            maps, map_strides, state, contributors, replay, replay_capacity,
                            replay_counts);
   if (status != GS_OK) return status;
+  const int64_t tiles = images * tiles_x(width) * tiles_y(height);
+  Segments seg;
+  status = make_segments(segment_length, segment_state, segment_index, segment_capacity,
+                         replay, tiles, &seg);
+  if (status != GS_OK) return status;
   const size_t need = gs_render_workspace_size(images, width, height);
   GS_REQUIRE(workspace && workspace_bytes >= need, GS_ERR_WORKSPACE,
              "render forward needs %zu workspace bytes, got %zu", need, workspace_bytes);
-  const int64_t tiles = images * tiles_x(width) * tiles_y(height);
   RenderWorkspace w = render_layout(workspace, tiles);
   return render_forward(neural, geometry, appearance, opacities, primitive_ids, backgrounds,
                         point_list, ranges, images, width, height, near_plane, far_plane,
                         map_groups(maps, map_strides), state, contributors, replay,
-                        replay_counts, w.order, static_cast<hipStream_t>(stream));
+                        replay_counts, w.order, seg, static_cast<hipStream_t>(stream));
 }
 
 int gs_render_forward_static(int32_t neural, const float* geometry, const float* appearance,
@@ -1467,7 +1658,7 @@ int gs_render_forward_static(int32_t neural, const float* geometry, const float*
   return render_forward(neural, geometry, appearance, opacities, primitive_ids, backgrounds,
                         point_list, ranges, images, width, height, near_plane, far_plane,
                         map_groups(maps, map_strides), state, contributors, replay,
-                        replay_counts, order, s);
+                        replay_counts, order, Segments{0, int(tiles), 0, nullptr, nullptr}, s);
 }
 
 int gs_render_backward(int32_t neural, const float* geometry, const float* appearance,
@@ -1475,7 +1666,9 @@ int gs_render_backward(int32_t neural, const float* geometry, const float* appea
                        const float* backgrounds, const int32_t* point_list,
                        const int32_t* ranges, const float* state,
                        const int32_t* contributors, const int32_t* replay,
-                       const int32_t* replay_counts, const float* const* grad_maps,
+                       const int32_t* replay_counts, int32_t segment_length,
+                       const float* segment_state, const int32_t* segment_index,
+                       int64_t segment_capacity, const float* const* grad_maps,
                        const int64_t* grad_map_strides, int64_t images,
                        int32_t width, int32_t height, float near_plane, float far_plane,
                        float* grad_geometry, float* grad_appearance, float* grad_opacities,
@@ -1491,32 +1684,45 @@ int gs_render_backward(int32_t neural, const float* geometry, const float* appea
   GS_REQUIRE(!replay == !replay_counts, GS_ERR_ARGUMENT,
              "replay and replay_counts must both be given or both be null");
   const MapGroups<const float> grads = map_groups(grad_maps, grad_map_strides);
-  const size_t need = gs_render_workspace_size(images, width, height);
+  const int tw = tiles_x(width), th = tiles_y(height);
+  const int tiles = int(images * tw * th);
+  Segments seg;
+  status = make_segments(segment_length, const_cast<float*>(segment_state),
+                         const_cast<int32_t*>(segment_index), segment_capacity, replay, tiles,
+                         &seg);
+  if (status != GS_OK) return status;
+  const size_t need =
+      gs_render_backward_workspace_size(images, width, height, seg.length ? seg.capacity : 0);
   GS_REQUIRE(workspace && workspace_bytes >= need, GS_ERR_WORKSPACE,
              "render backward needs %zu workspace bytes, got %zu", need, workspace_bytes);
   hipStream_t s = static_cast<hipStream_t>(stream);
   ProfileScope prof(GS_PROF_RENDER_BWD, s);
-  const int tw = tiles_x(width), th = tiles_y(height);
-  const int tiles = int(images * tw * th);
   const int2* r = reinterpret_cast<const int2*>(ranges);
-  RenderWorkspace w = render_layout(workspace, tiles);
-  // Tiles are ordered by the records they replay: the replay list's length,
-  // or the largest contributor count.
-  if (!replay) {
-    tile_last_kernel<<<unsigned(tiles), kTilePixels, 0, s>>>(width, height, tw, th,
-                                                             contributors, w.tile_last);
-    GS_LAUNCHED("tile_last_kernel");
+  RenderWorkspace w = render_layout(workspace, tiles, seg.length ? seg.capacity : 0);
+  // Tiles (or the segments of split tiles) are ordered by the records they
+  // replay: the replay list's length, or the largest contributor count.
+  unsigned blocks = unsigned(tiles);
+  if (seg.length) {
+    segment_order_kernel<<<1, kOrderBlock, 0, s>>>(r, replay_counts, tiles, seg, w.segments);
+    GS_LAUNCHED("segment_order_kernel");
+    blocks = unsigned(tiles + seg.capacity);
+  } else {
+    if (!replay) {
+      tile_last_kernel<<<unsigned(tiles), kTilePixels, 0, s>>>(width, height, tw, th,
+                                                               contributors, w.tile_last);
+      GS_LAUNCHED("tile_last_kernel");
+    }
+    tile_order_kernel<<<1, kOrderBlock, 0, s>>>(replay ? replay_counts : w.tile_last, r, tiles,
+                                                w.order, seg);
+    GS_LAUNCHED("tile_order_kernel");
   }
-  tile_order_kernel<<<1, kOrderBlock, 0, s>>>(replay ? replay_counts : w.tile_last, r, tiles,
-                                              w.order);
-  GS_LAUNCHED("tile_order_kernel");
   const int2* lists = reinterpret_cast<const int2*>(replay);
   auto launch = [&](auto kernel) {
-    kernel<<<unsigned(tiles), kTilePixels, 0, s>>>(
+    kernel<<<blocks, kTilePixels, 0, s>>>(
         width, height, tw, th, geometry, appearance, opacities, primitive_ids, backgrounds,
         point_list, r, w.order, w.tile_last, lists, replay_counts, state, contributors, grads,
         near_plane, far_plane, grad_geometry, grad_appearance, grad_opacities,
-        grad_backgrounds);
+        grad_backgrounds, w.segments, seg);
   };
   if (neural) {
     if (replay) launch(renderBackward<true, true>);

@@ -104,6 +104,34 @@ __global__ __launch_bounds__(kScanBlock) void scan_down_kernel(int64_t count, in
   }
 }
 
+// Short sequences (up to kScanLocalItems): one workgroup walks the whole
+// sequence in rounds of kScanLocalBlock items, carrying the prefix - one
+// launch instead of three.
+constexpr int kScanLocalBlock = 1024;
+constexpr int64_t kScanLocalItems = 8192;
+
+template <typename T, typename Load, typename Store>
+__global__ __launch_bounds__(kScanLocalBlock) void scan_local_kernel(int64_t count, Load load,
+                                                                     Store store) {
+  constexpr int kWaves = kScanLocalBlock / 64;
+  __shared__ T totals[2][kWaves];
+  const int lane = __lane_id(), wave = threadIdx.x >> 6;
+  T carry = 0;
+  int parity = 0;
+  for (int64_t base = 0; base < count; base += kScanLocalBlock, parity ^= 1) {
+    const int64_t i = base + threadIdx.x;
+    const T v = i < count ? load(i) : T(0);
+    const T incl = wave_inclusive_scan(v);
+    if (lane == 63) totals[parity][wave] = incl;
+    __syncthreads();
+    T before = carry;
+    for (int w = 0; w < wave; ++w) before += totals[parity][w];
+    if (i < count) store(i, before + incl, v);
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) carry += totals[parity][w];
+  }
+}
+
 // Items per thread of one span for a sequence of `count` items.
 inline int scan_rounds(int64_t count) {
   const int64_t per_span = ceil_div(count > 0 ? count : 0, kScanMaxSpans);
@@ -119,10 +147,16 @@ inline size_t scan_workspace_bytes(int64_t count, size_t item_bytes) {
   return align_up(size_t(scan_spans(count)) * item_bytes, 256) + 256;
 }
 
-// Runs the three passes; span_sums needs scan_spans(count) entries.
+// Runs the three passes (or, for short sequences, the one-workgroup scan);
+// span_sums needs scan_spans(count) entries.
 template <typename T, typename Load, typename Store>
 int run_scan(int64_t count, Load load, Store store, T* span_sums, hipStream_t stream) {
   if (count <= 0) return GS_OK;
+  if (count <= kScanLocalItems) {
+    scan_local_kernel<T, Load, Store><<<1, kScanLocalBlock, 0, stream>>>(count, load, store);
+    GS_LAUNCHED("scan_local_kernel");
+    return GS_OK;
+  }
   const int rounds = scan_rounds(count);
   const int64_t spans = scan_spans(count);
   GS_REQUIRE(spans <= 0x7fffffffLL, GS_ERR_OVERFLOW, "scan too large");

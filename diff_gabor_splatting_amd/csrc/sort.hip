@@ -13,7 +13,8 @@
 //                 via ballots, per-wave running counters in LDS), stages the
 //                 locally sorted span in LDS and writes it out so that runs
 //                 of equal digits land on consecutive addresses.
-// Only bits [begin_bit, end_bit) are sorted. gs_sort_pairs sorts the
+// Sorts of up to 8192 keys run every pass in one workgroup instead
+// (local_sort_kernel). Only bits [begin_bit, end_bit) are sorted. gs_sort_pairs sorts the
 // reference's 64-bit image|tile|depth keys; the depth-first binning
 // pipeline (binning.hip) sorts 32-bit depth keys and then 32-bit tile ids.
 #include "sort.hpp"
@@ -221,6 +222,114 @@ __global__ __launch_bounds__(kSortBlock) void radix_downsweep_kernel(
   }
 }
 
+// Sorts of up to kLocalSort keys run in one workgroup of kLocalBlock
+// threads, every pass in one launch: each thread keeps kLocalItems keys in
+// registers (key i of wave w is item (i - w 64 kLocalItems) / 64 of lane
+// i mod 64, so a wave's keys are ranked in order, as in the downsweep), the
+// per-wave digit counters give every key its slot, and between passes the
+// keys are restaged through LDS; the last pass writes the output.
+constexpr int kLocalBlock = 1024;
+constexpr int kLocalWaves = kLocalBlock / 64;
+constexpr int kLocalItems = 8;
+constexpr int64_t kLocalSort = int64_t(kLocalBlock) * kLocalItems;
+
+template <typename Key, bool Values>
+__global__ __launch_bounds__(kLocalBlock) void local_sort_kernel(
+    const Key* __restrict__ keys_in, const int* __restrict__ values_in,
+    Key* __restrict__ keys_out, int* __restrict__ values_out, int64_t capacity,
+    const int64_t* __restrict__ live, int begin_bit, int end_bit, int passes, int digit_bits) {
+  const int m = int(live_length(capacity, live));
+  __shared__ uint32_t running[kLocalWaves][kBins];  // per-wave digit counters
+  __shared__ uint32_t digit_start[kBins];
+  __shared__ uint32_t wave_totals[kBins / 64];
+  __shared__ Key stage_keys[kLocalSort];
+  __shared__ int stage_values[Values ? kLocalSort : 1];
+  const int lane = __lane_id(), wave = threadIdx.x >> 6;
+  const int wave_base = wave * 64 * kLocalItems;
+  const uint64_t lanes_below = (uint64_t(1) << lane) - 1;
+  Key key[kLocalItems];
+  int value[kLocalItems];
+#pragma unroll
+  for (int it = 0; it < kLocalItems; ++it) {
+    const int i = wave_base + it * 64 + lane;
+    key[it] = i < m ? keys_in[i] : Key(0);
+    value[it] = Values && i < m ? values_in[i] : 0;
+  }
+  for (int pass = 0; pass < passes; ++pass) {
+    const int shift = begin_bit + pass * digit_bits;
+    const int bits = min(digit_bits, end_bit - shift);
+    const uint32_t mask = (1u << bits) - 1u;
+    for (int i = threadIdx.x; i < kLocalWaves * kBins; i += kLocalBlock)
+      (&running[0][0])[i] = 0;
+    __syncthreads();
+    uint32_t rank[kLocalItems], before[kLocalItems];
+    int leader[kLocalItems];
+#pragma unroll
+    for (int it = 0; it < kLocalItems; ++it) {
+      const bool valid = wave_base + it * 64 + lane < m;
+      const uint32_t digit = uint32_t(key[it] >> shift) & mask;
+      const uint64_t peers = digit_peers(digit, valid, bits);
+      leader[it] = peers ? __builtin_ctzll(peers) : lane;
+      rank[it] = uint32_t(__popcll(peers & lanes_below));
+      before[it] = 0;
+      if (valid && (peers & lanes_below) == 0)
+        before[it] = atomicAdd(&running[wave][digit], uint32_t(__popcll(peers)));
+    }
+#pragma unroll
+    for (int it = 0; it < kLocalItems; ++it)
+      rank[it] += uint32_t(__shfl(int(before[it]), leader[it]));
+    __syncthreads();
+    // Per digit: each wave's first slot among the digit's keys, the
+    // digit's total, then the exclusive prefix over digits (waves 0-3).
+    if (threadIdx.x < kBins) {
+      const int d = threadIdx.x;
+      uint32_t run = 0;
+      for (int w = 0; w < kLocalWaves; ++w) {
+        const uint32_t c = running[w][d];
+        running[w][d] = run;
+        run += c;
+      }
+      const uint32_t incl = wave_inclusive_scan(run);
+      if (lane == 63) wave_totals[wave] = incl;
+      digit_start[d] = incl - run;
+    }
+    __syncthreads();
+    if (threadIdx.x < kBins) {
+      uint32_t below = 0;
+      for (int w = 0; w < wave; ++w) below += wave_totals[w];
+      digit_start[threadIdx.x] += below;
+    }
+    __syncthreads();
+    const bool last = pass == passes - 1;
+#pragma unroll
+    for (int it = 0; it < kLocalItems; ++it) {
+      const int i = wave_base + it * 64 + lane;
+      if (i < m) {
+        const uint32_t digit = uint32_t(key[it] >> shift) & mask;
+        const uint32_t slot = digit_start[digit] + running[wave][digit] + rank[it];
+        if (slot < uint32_t(m)) {  // always true when ranking is consistent
+          if (last) {
+            keys_out[slot] = key[it];
+            if constexpr (Values) values_out[slot] = value[it];
+          } else {
+            stage_keys[slot] = key[it];
+            if constexpr (Values) stage_values[slot] = value[it];
+          }
+        }
+      }
+    }
+    if (!last) {
+      __syncthreads();
+#pragma unroll
+      for (int it = 0; it < kLocalItems; ++it) {
+        const int i = wave_base + it * 64 + lane;
+        key[it] = i < m ? stage_keys[i] : Key(0);
+        value[it] = Values && i < m ? stage_values[i] : 0;
+      }
+    }
+  }
+}
+
 template <typename Key>
 __global__ __launch_bounds__(256) void copy_pairs_kernel(const Key* __restrict__ keys_in,
                                                          const int* __restrict__ values_in,
@@ -286,6 +395,16 @@ int radix_sort(const Key* keys_in, Key* keys_out, const int* values_in, int* val
     copy_pairs_kernel<Key><<<unsigned(ceil_div(m, 256)), 256, 0, s>>>(
         keys_in, values_in, keys_out, values_out, m, live);
     GS_LAUNCHED("copy_pairs_kernel");
+    return GS_OK;
+  }
+  if (m <= kLocalSort) {
+    auto local = [&](auto kernel) {
+      kernel<<<1, kLocalBlock, 0, s>>>(keys_in, values_in, keys_out, values_out, m, live,
+                                       begin_bit, end_bit, passes, digit_bits);
+    };
+    if (values_in) local(local_sort_kernel<Key, true>);
+    else local(local_sort_kernel<Key, false>);
+    GS_LAUNCHED("local_sort_kernel");
     return GS_OK;
   }
   // Ping-pong so that the last pass writes the caller's output.

@@ -182,7 +182,10 @@ def collect(name: str, device: torch.device | None = None) -> dict:
         torch.cuda.synchronize(device)
         tiles = captured["forward"][2].shape[0]
         lanes = torch.zeros(65, dtype=torch.int64, device=device)
-        spans = torch.full((2, tiles, 2), -1, dtype=torch.int64, device=device)
+        # Begins start at all ones and ends at zero: the kernels keep the
+        # earliest begin and the latest end of every workgroup of a tile.
+        spans = torch.zeros((2, tiles, 2), dtype=torch.int64, device=device)
+        spans[..., 0] = -1
         with torch.cuda.device(device):
             _native._check(_native.lib.gs_diagnostics_set(
                 lanes.data_ptr(), spans[0].data_ptr(), spans[1].data_ptr(), tiles))
@@ -201,14 +204,14 @@ def collect(name: str, device: torch.device | None = None) -> dict:
               "intersections": int(point_list.numel())}
     lists = replay[0] if replay else None
     if lists is not None:
-        records, counts = lists
+        records, counts = lists[0], lists[1]
         report["replayed_records"] = {**percentiles(counts.long()),
                                       "log2_histogram": log2_histogram(counts.long()),
                                       "total": int(counts.long().sum())}
         report["replay_quadrant_bits"] = replay_quadrant_bits(records, counts, ranges)
     spans = spans.cpu()
     for index, kernel in enumerate(("render_forward", "render_backward")):
-        if bool((spans[index] >= 0).all()):
+        if bool((spans[index, :, 0] >= 0).all()):
             report[kernel] = launch_profile(spans[index], khz.value)
     report["backward_taking_lanes"] = lane_summary(lanes.cpu().tolist())
     return report

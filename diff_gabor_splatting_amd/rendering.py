@@ -70,13 +70,16 @@ class Composite(torch.autograd.Function):
         )
         replay = replay[0] if replay else None
         # Binning and early termination are discrete: only the saved sorted
-        # lists, per-pixel state and the tiles' replay lists (the records some
-        # pixel took) are needed to replay the tiles backwards.
-        lists, counts = replay if replay is not None else (None, None)
+        # lists, per-pixel state, the tiles' replay lists (the records some
+        # pixel took) and the split tiles' checkpoints are needed to replay
+        # the tiles backwards.
+        lists, counts, segments = replay if replay is not None else (None, None, None)
+        length, checkpoints, checkpoint_index = segments if segments else (0, None, None)
         ctx.save_for_backward(
             geometry, appearance, opacities, primitive_ids, backgrounds, points, ranges, state,
-            contributors, lists, counts,
+            contributors, lists, counts, checkpoints, checkpoint_index,
         )
+        ctx.split = length
         ctx.options = (width, height, neural, near_plane, far_plane)
         ctx.set_materialize_grads(False)
         return outputs
@@ -86,10 +89,11 @@ class Composite(torch.autograd.Function):
     def backward(ctx: Any, *grad_groups):
         # A second backward through a retained graph gets fresh accumulators.
         accumulators, ctx.accumulators = ctx.accumulators, None
-        *saved, lists, counts = ctx.saved_tensors
+        *saved, lists, counts, checkpoints, checkpoint_index = ctx.saved_tensors
+        segments = (ctx.split, checkpoints, checkpoint_index) if ctx.split else None
         gg, ga, go, gb = _native.rasterize_backward(
             *saved, list(grad_groups), *ctx.options, accumulators=accumulators,
-            replay=None if lists is None else (lists, counts),
+            replay=None if lists is None else (lists, counts, segments),
         )
         return (gg, gg[:, 9:11], ga, go, None, None, None, gb, None, None, None, None, None, None,
                 None, None)

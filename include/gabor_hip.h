@@ -319,6 +319,10 @@ int gs_bin_tiles_bounded(const int32_t* order, const int64_t* starts, const int3
 /* Scratch bytes for gs_render_forward / gs_render_backward: the tile
  * dispatch order (heaviest tiles first) and per-tile contributor maxima. */
 size_t gs_render_workspace_size(int64_t images, int32_t width, int32_t height);
+/* Workspace of gs_render_backward: the forward's plus the order of the split
+ * tiles' segments. */
+size_t gs_render_backward_workspace_size(int64_t images, int32_t width, int32_t height,
+                                         int64_t segment_capacity);
 
 /* Map outputs and map gradients are passed as five channel groups in map
  * order - rgb (channels 0-2), alpha (3), depth (4), normals (5-7),
@@ -347,7 +351,26 @@ int gs_render_forward(int32_t neural, const float* geometry, const float* appear
                       float near_plane, float far_plane, float* const* maps,
                       const int64_t* map_strides, float* state, int32_t* contributors,
                       int32_t* replay, int64_t replay_capacity, int32_t* replay_counts,
-                      void* workspace, size_t workspace_bytes, void* stream);
+                      int32_t segment_length, float* segment_state, int32_t* segment_index,
+                      int64_t segment_capacity, void* workspace, size_t workspace_bytes,
+                      void* stream);
+
+/* Split tiles (segment_length > 0, a multiple of 64; needs the replay
+ * lists; 0 turns it off and the three buffers are ignored). No counterpart
+ * in the reference, whose backward walks each tile in one thread block. A
+ * tile whose point list is longer than segment_length records gets
+ * K = ceil(length / segment_length) checkpoint slots, assigned in tile
+ * order by the forward: segment_index [I*tw*th + segment_capacity] int32
+ * receives each tile's first slot (-1: not split) and then, per slot, the
+ * replay-list length at the slot's checkpoint; segment_state
+ * [segment_capacity][10][256] float32 receives each checkpoint's per-pixel
+ * prefix state (transmittance, rgb, depth, normals, and the two depth
+ * moments) after every segment_length list records, the last slot holding
+ * the final state. Slots past segment_capacity are not used (their tiles
+ * are not split); sum over tiles of floor(2 length / segment_length) slots
+ * always suffice. gs_render_backward, given the same arguments, then
+ * replays each split tile's segments in separate workgroups, each from its
+ * checkpoint, so a long list no longer runs on one compute unit. */
 
 /* gs_render_forward without a workspace argument. No counterpart in the
  * reference: it is for callers that cannot allocate device memory (code
@@ -359,7 +382,7 @@ int gs_render_forward(int32_t neural, const float* geometry, const float* appear
  * GPU shares that GPU's array, so calls that overlap on one GPU (on
  * different streams or threads) race; each call rewrites the order of all
  * its tiles before reading it, so nothing has to be cleared between calls.
- * Outputs are identical to gs_render_forward's. */
+ * Outputs are identical to gs_render_forward's (without split tiles). */
 #define GS_RENDER_STATIC_MAX_TILES (1 << 20)
 int gs_render_forward_static(int32_t neural, const float* geometry, const float* appearance,
                              const float* opacities, const int64_t* primitive_ids,
@@ -376,13 +399,18 @@ int gs_render_forward_static(int32_t neural, const float* geometry, const float*
  * form above; a null group pointer means a zero gradient for that group.
  * replay / replay_counts: the forward's replay lists, or both null; with
  * them the backward replays only the records some pixel took (the same
- * gradients: the other records contribute exact zeros). */
+ * gradients: the other records contribute exact zeros). segment_*: the
+ * forward's split-tile arguments (segment_length 0: none). The workspace is
+ * gs_render_backward_workspace_size(images, width, height, segment_capacity)
+ * bytes (segment_capacity 0 without split tiles). */
 int gs_render_backward(int32_t neural, const float* geometry, const float* appearance,
                        const float* opacities, const int64_t* primitive_ids,
                        const float* backgrounds, const int32_t* point_list,
                        const int32_t* ranges, const float* state,
                        const int32_t* contributors, const int32_t* replay,
-                       const int32_t* replay_counts, const float* const* grad_maps,
+                       const int32_t* replay_counts, int32_t segment_length,
+                       const float* segment_state, const int32_t* segment_index,
+                       int64_t segment_capacity, const float* const* grad_maps,
                        const int64_t* grad_map_strides, int64_t images,
                        int32_t width, int32_t height, float near_plane, float far_plane,
                        float* grad_geometry, float* grad_appearance, float* grad_opacities,

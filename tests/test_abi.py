@@ -53,8 +53,24 @@ def test_argument_errors_return_status_and_message():
     status = lib.gs_find_ranges(None, -1, None, 4, None)
     assert status == 2
     status = lib.gs_render_forward(0, *([None] * 7), 1, 16, 16, 1.0, 0.5, *([None] * 5), 0,
-                                   None, None, 0, None)
+                                   None, 0, None, None, 0, None, 0, None)
     assert status == 1 and b"clipping" in lib.gs_last_error()
+    # Split-tile arguments are checked before any launch.
+    dummy = ctypes.c_void_p(16)
+    maps = (ctypes.c_void_p * 5)(*([16] * 5))
+    strides = (ctypes.c_int64 * 10)()
+    forward = [0, *([dummy] * 7), 1, 16, 16, 0.5, 1.0, maps, strides, dummy, dummy]
+    status = lib.gs_render_forward(*forward, None, 0, None, 100, dummy, dummy, 4, dummy, 1 << 20,
+                                   None)
+    assert status == 1 and b"multiple of 64" in lib.gs_last_error()
+    status = lib.gs_render_forward(*forward, None, 0, None, 64, dummy, dummy, 4, dummy, 1 << 20,
+                                   None)
+    assert status == 1 and b"replay lists" in lib.gs_last_error()
+    status = lib.gs_render_forward(*forward, dummy, 10, dummy, 64, dummy, dummy, 0, dummy,
+                                   1 << 20, None)
+    assert status == 2 and b"segment capacity" in lib.gs_last_error()
+    assert (lib.gs_render_backward_workspace_size(1, 64, 64, 100)
+            >= lib.gs_render_workspace_size(1, 64, 64) + 8 * (16 + 100))
     # Workspace smaller than required is rejected before any launch.
     need = lib.gs_scan_workspace_size(1000)
     dummy = ctypes.c_void_p(16)

@@ -33,11 +33,16 @@ def scene(method, seed, n=300, width=70, height=45):
 
 
 def assert_grads_close(actual, expected, names, what):
-    """Float atomics sum the gradients in a run-dependent order, so elements
-    are compared at the scale of their tensor (1e-6 of its largest value)."""
+    """Float atomics sum the gradients in a run-dependent order, and a render
+    into a fixed-capacity point list picks its split-tile segment length
+    from that capacity rather than from the intersection count, so the
+    segments of a split tile (each starting from a checkpoint's prefix sums)
+    can differ from the synchronised render's. Elements are compared at the
+    scale of their tensor: 1e-4 of its largest value, ten times inside the
+    oracle gradient bar."""
     for name, a, e in zip(names, actual, expected):
         scale = float(e.abs().max()) if e.numel() else 0.0
-        torch.testing.assert_close(a, e, atol=1e-6 * max(scale, 1.0), rtol=1e-5,
+        torch.testing.assert_close(a, e, atol=1e-4 * max(scale, 1e-2), rtol=1e-4,
                                    msg=lambda m, name=name: f"{name} {what}: {m}")
 
 

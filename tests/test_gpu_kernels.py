@@ -30,15 +30,17 @@ def to_u64(t):
     return t.cpu().numpy().view(np.uint64)
 
 
-@pytest.mark.parametrize("m", [1, 255, 2048, 2049, 100_003, 1_000_003, 4_194_305])
+@pytest.mark.parametrize("m", [1, 255, 1000, 2048, 2049, 8192, 8193, 100_003, 1_000_003,
+                               4_194_305])
 @pytest.mark.parametrize("bits, with_values", [
     ((0, 32), True), ((19, 32), False), ((0, 13), True), ((5, 12), False),
 ])
 def test_sort32_is_stable_radix_order(native, m, bits, with_values):
-    """The 32-bit sort of the binning stages (reduce-then-scan digit
-    passes), against numpy's stable argsort: partial last spans, both
-    span sizes (4,194,305 keys take 4096-key spans), keys alone and with
-    values, partial bit ranges, many ties and skewed digits."""
+    """The 32-bit sort of the binning stages against numpy's stable argsort:
+    the one-workgroup sort (up to 8192 keys) and the reduce-then-scan digit
+    passes (from 8193), partial last spans, both span sizes (4,194,305 keys
+    take 4096-key spans), keys alone and with values, partial bit ranges,
+    many ties and skewed digits."""
     rng = np.random.default_rng(m + 7 * bits[0])
     keys = rng.integers(0, 2**32, m, dtype=np.uint64).astype(np.uint32)
     keys[rng.integers(0, m, m // 3)] = keys[0]  # many exact ties
@@ -58,7 +60,7 @@ def test_sort32_is_stable_radix_order(native, m, bits, with_values):
         assert sv is None
 
 
-@pytest.mark.parametrize("m", [1, 5, 4095, 4096, 4097, 100_003, 2_000_000])
+@pytest.mark.parametrize("m", [1, 5, 4095, 4096, 4097, 8192, 8193, 100_003, 2_000_000])
 @pytest.mark.parametrize("bits", [(0, 64), (0, 45), (32, 45), (3, 17)])
 def test_sort_is_stable_radix_order(native, m, bits):
     rng = np.random.default_rng(m + bits[0])
@@ -186,7 +188,7 @@ def test_ranges_of_empty_list_are_zero(native):
     assert ranges.shape == (37, 2) and int(ranges.abs().sum()) == 0
 
 
-@pytest.mark.parametrize("count", [0, 1, 4096, 4097, 1_000_000])
+@pytest.mark.parametrize("count", [0, 1, 4096, 4097, 8192, 8193, 1_000_000])
 def test_pack_visible(native, count):
     rng = np.random.default_rng(count)
     radii = rng.integers(-1, 3, count).astype(np.int32)

@@ -147,7 +147,7 @@ def test_config_replay_lists(index):
         opts["sh_degree"] = cfg["sh"]
     args = compositor_inputs(renderer(cfg["neural"]), values, opts)
     forward = forward_both(args)
-    _, point_list, ranges, _, contributors, (lists, counts) = forward
+    _, point_list, ranges, _, contributors, (lists, counts, _) = forward
     tiles, _, quads = check_structure(point_list, ranges, contributors, lists, counts,
                                       cfg["width"], cfg["height"])
     # The lists are much shorter than the tiles' lists up to their last contributor.
@@ -166,7 +166,7 @@ def test_replay_lists_match_oracle(neural, seed):
     gpu = {k: v.to(DEVICE) for k, v in values.items()}
     args = compositor_inputs(renderer(neural), gpu, dict(width=width, height=height))
     forward = forward_both(args)
-    _, point_list, ranges, _, contributors, (lists, counts) = forward
+    _, point_list, ranges, _, contributors, (lists, counts, _) = forward
     tiles, pos, quads = check_structure(point_list, ranges, contributors, lists, counts,
                                         width, height)
     geometry, appearance, opacities, primitive_ids, image_ids, radii, backgrounds = (

@@ -1,0 +1,147 @@
+"""Split tiles: the backward replays long tile lists in segments, each from a
+checkpoint the forward wrote.
+
+* Forward outputs are bit-identical with and without split tiles (the
+  checkpoints are extra writes), and gradients agree with the unsplit
+  backward to float32 rounding (each segment's running suffix is derived
+  from prefix-sum differences instead of accumulated).
+* The checkpoint layout: slot bases in tile order for exactly the tiles
+  longer than the segment length, non-decreasing replay lengths ending at
+  the tile's replay count, and a last checkpoint equal to the saved state.
+* Gradients of a scene whose tiles are split match the float64 oracle.
+"""
+
+import pytest
+import torch
+
+from diff_gabor_splatting_amd import _native
+from oracle import render as oracle_render
+from scenes import (assert_gradients_close, fp32_conditioned, maps_from_result,
+                    oracle_reference, random_scene)
+
+pytestmark = [
+    pytest.mark.gpu,
+    pytest.mark.skipif(not torch.cuda.is_available(), reason="needs a GPU"),
+]
+DEVICE = torch.device("cuda:0")
+ORACLE = {"classic": oracle_render.rasterize_gabors, "neural": oracle_render.rasterize_neural_gabors}
+
+
+def renderer(method):
+    from diff_gabor_splatting_amd import rasterize_gabors, rasterize_neural_gabors
+
+    return rasterize_gabors if method == "classic" else rasterize_neural_gabors
+
+
+def heavy_scene(method, opacity, n=900, width=40, height=36, seed=5):
+    raw = random_scene(method, scenes=1, cameras=2, n=n, width=width, height=height, seed=seed)
+    raw["opacities"] = torch.full_like(raw["opacities"], opacity)
+    return {k: v.to(DEVICE).requires_grad_() for k, v in raw.items()}
+
+
+def spy_forward(monkeypatch):
+    """Records every rasterize_forward result."""
+    seen = []
+    original = _native.rasterize_forward
+
+    def spy(*args, **kwargs):
+        out = original(*args, **kwargs)
+        seen.append(out)
+        return out
+
+    monkeypatch.setattr(_native, "rasterize_forward", spy)
+    return seen
+
+
+def run(method, values, weights, width, height):
+    maps = maps_from_result(renderer(method)(**values, width=width, height=height))
+    grads = torch.autograd.grad((maps * weights).sum(), list(values.values()), allow_unused=True)
+    return maps.detach(), [torch.zeros_like(v) if g is None else g
+                           for g, v in zip(grads, values.values())]
+
+
+@pytest.mark.parametrize("method", ["classic", "neural"])
+@pytest.mark.parametrize("opacity", [0.3, 0.97])
+def test_split_backward_matches_unsplit(method, opacity, monkeypatch):
+    width, height = 40, 36
+    values = heavy_scene(method, opacity, width=width, height=height)
+    weights = torch.randn((1, 2, height, width, 9), generator=torch.Generator().manual_seed(8))
+    weights = weights.to(DEVICE)
+    print(f"split vs unsplit: {method} opacity {opacity}", flush=True)
+    seen = spy_forward(monkeypatch)
+    split_maps, split_grads = run(method, values, weights, width, height)
+    segments = seen[-1][5][2]
+    assert segments is not None, "the scene was not split"
+    tiles = seen[-1][2].shape[0]
+    assert int((segments[2][:tiles] >= 0).sum()) > 0
+    monkeypatch.setattr(_native, "SPLIT_MAX_TILES", 0)
+    plain_maps, plain_grads = run(method, values, weights, width, height)
+    assert seen[-1][5][2] is None
+    assert torch.equal(split_maps, plain_maps)
+    for name, a, b in zip(values, split_grads, plain_grads):
+        scale = float(b.abs().max())
+        err = float((a - b).abs().max())
+        assert err <= 2e-4 * scale + 1e-12, f"{name}: max error {err:.3e}, scale {scale:.3e}"
+
+
+@pytest.mark.parametrize("opacity", [0.3, 0.97])
+def test_checkpoint_layout(opacity, monkeypatch):
+    width, height = 40, 36
+    values = heavy_scene("classic", opacity, width=width, height=height)
+    seen = spy_forward(monkeypatch)
+    renderer("classic")(**values, width=width, height=height)
+    maps, point_list, ranges, state, contributors, (lists, counts, segments) = seen[-1]
+    length, checkpoints, index = segments
+    tiles = ranges.shape[0]
+    lengths = (ranges[:, 1] - ranges[:, 0]).long().cpu()
+    base = index[:tiles].long().cpu()
+    split = lengths > length
+    assert bool(((base >= 0) == split).all())
+    # Slots in tile order: each split tile takes ceil(L / length) of them.
+    need = (lengths + length - 1) // length
+    expected_base = torch.cumsum(torch.where(split, need, 0), 0) - torch.where(split, need, 0)
+    assert torch.equal(base[split], expected_base[split])
+    replayed = index[tiles:].long().cpu()
+    counts = counts.long().cpu()
+    state_cpu = state.cpu()
+    ck = checkpoints.cpu()
+    tw, th = _native.tile_grid(width, height)
+    for t in torch.nonzero(split).flatten().tolist():
+        n = replayed[base[t]:base[t] + need[t]]
+        assert bool((n[1:] >= n[:-1]).all()) and int(n[-1]) == int(counts[t]) and int(n[0]) >= 0
+        image, local = divmod(t, tw * th)
+        ty, tx = divmod(local, tw)
+        last = ck[base[t] + need[t] - 1]  # [10, 256]: the final state of the tile's pixels
+        pix = torch.arange(256)
+        wave, lane = pix // 64, pix % 64
+        px = tx * 16 + (wave % 2) * 8 + lane % 8
+        py = ty * 16 + (wave // 2) * 8 + lane // 8
+        inside = (px < width) & (py < height)
+        saved = state_cpu[image, py[inside], px[inside]]
+        assert torch.equal(last[0, inside], saved[:, 0])
+        assert torch.equal(last[8, inside], saved[:, 1])
+        assert torch.equal(last[9, inside], saved[:, 2])
+
+
+@pytest.mark.parametrize("method", ["classic", "neural"])
+def test_split_scene_matches_oracle(method, monkeypatch):
+    width, height = 36, 20
+    raw = random_scene(method, scenes=1, cameras=2, n=260, width=width, height=height, seed=21)
+    values = {k: v.to(DEVICE).requires_grad_() for k, v in raw.items()}
+    seen = spy_forward(monkeypatch)
+    rgb, alpha, meta = renderer(method)(**values, width=width, height=height)
+    actual = maps_from_result((rgb, alpha, meta))
+    segments = seen[-1][5][2]
+    assert segments is not None and int((segments[2][:seen[-1][2].shape[0]] >= 0).sum()) > 0
+    rest = {k: v for k, v in values.items() if k != "backgrounds"}
+    _, mask = fp32_conditioned(
+        lambda backgrounds, **kw: ORACLE[method](**kw, backgrounds=backgrounds),
+        {**rest, "backgrounds": values["backgrounds"]}, width=width, height=height)
+    weights = torch.randn(actual.shape, generator=torch.Generator().manual_seed(4)) * mask[..., None]
+    _, expected, sensitivity = oracle_reference(ORACLE[method], values, weights, width=width,
+                                                height=height)
+    grads = torch.autograd.grad((actual * weights.to(DEVICE)).sum(), list(values.values()),
+                                allow_unused=True)
+    for (name, v), g in zip(values.items(), grads):
+        g = torch.zeros_like(v) if g is None else g
+        assert_gradients_close(g, expected[name], name, sensitivity[name])

@@ -84,8 +84,8 @@ def call(entry, args, lists):
     else:
         workspace = torch.empty(native.lib.gs_render_workspace_size(images, width, height),
                                 dtype=torch.uint8, device=DEVICE)
-        status = native.lib.gs_render_forward(*common, workspace.data_ptr(), workspace.numel(),
-                                              stream)
+        status = native.lib.gs_render_forward(*common, 0, None, None, 0, workspace.data_ptr(),
+                                              workspace.numel(), stream)
     assert status == 0, native.lib.gs_last_error()
     torch.cuda.synchronize()
     return maps, state, contributors, replay, counts
