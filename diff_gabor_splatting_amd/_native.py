@@ -875,10 +875,16 @@ def rasterize_forward(
     return [maps, point_list, ranges, state, contributors]
 
 
-def zero_accumulators(geometry, appearance, opacities, backgrounds):
-    """Zeroed gradient accumulators for rasterize_backward."""
-    return (torch.zeros_like(geometry), torch.zeros_like(appearance),
-            torch.zeros_like(opacities), torch.zeros_like(backgrounds))
+def zero_accumulators(geometry, appearance, opacities, backgrounds, shared=True):
+    """Zeroed gradient accumulators for rasterize_backward: with ``shared``,
+    contiguous views of one allocation cleared by one fill; else four
+    separate tensors (for callers that must not return aliased tensors)."""
+    like = (geometry, appearance, opacities, backgrounds)
+    if not shared:
+        return tuple(torch.zeros_like(t) for t in like)
+    sizes = [t.numel() for t in like]
+    flat = torch.zeros(sum(sizes), dtype=torch.float32, device=geometry.device)
+    return tuple(part.view(t.shape) for part, t in zip(flat.split(sizes), like))
 
 
 def rasterize_backward(
@@ -947,7 +953,8 @@ def rasterize_backward(
         )
     with torch.cuda.device(device):
         if accumulators is None:
-            accumulators = zero_accumulators(geometry, appearance, opacities, backgrounds)
+            accumulators = zero_accumulators(geometry, appearance, opacities, backgrounds,
+                                             shared=False)
         gg, ga, go, gb = accumulators
         _require(
             gg.shape == geometry.shape and ga.shape == appearance.shape

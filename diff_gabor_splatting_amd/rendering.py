@@ -20,6 +20,12 @@ from torch.autograd.function import once_differentiable
 from . import _native
 
 
+def _shaped(tensor: torch.Tensor, shape: tuple) -> torch.Tensor:
+    """``tensor`` itself when it already has ``shape`` (no view node joins the
+    autograd graph), else its reshape."""
+    return tensor if tuple(tensor.shape) == shape else tensor.reshape(shape)
+
+
 class Composite(torch.autograd.Function):
     """Tile compositor with first-order reverse mode (rendering.py:14-71).
 
@@ -29,7 +35,7 @@ class Composite(torch.autograd.Function):
     reference where ``meta["projected_means"]`` feeds the geometry.
 
     The nine map channels come out as five tensors - rgb, alpha, depth,
-    normals, distortion, each [I,H,W,k] - rather than as slices of one
+    normals, distortion, each [..., C, H, W, k] - rather than as slices of one
     [I,H,W,9] tensor: autograd would scatter the gradient of every slice
     into its own zero-filled full-size tensor and sum the five, while here
     the backward kernel reads each group's gradient where it lies (for a
@@ -43,11 +49,18 @@ class Composite(torch.autograd.Function):
         radii, backgrounds, width, height, neural, near_plane, far_plane, bounded=None,
         grad_mode=True, violations=None,
     ):
+        # backgrounds [..., C, 3]; the maps come out as [..., C, H, W, k]
+        # directly (the kernels see them as [I, H, W, k]), so the caller's
+        # shapes need no view nodes in the autograd graph.
+        image_shape = tuple(backgrounds.shape[:-1]) + (height, width)
+        ctx.background_shape = backgrounds.shape
+        backgrounds = backgrounds.reshape(-1, 3)
         images = backgrounds.size(0)
-        outputs = tuple(
-            torch.empty((images, height, width, k), dtype=torch.float32, device=geometry.device)
+        shaped = tuple(
+            torch.empty(image_shape + (k,), dtype=torch.float32, device=geometry.device)
             for k in _native.MAP_GROUPS
         )
+        outputs = tuple(t.view(images, height, width, t.shape[-1]) for t in shaped)
         # The backward's zeroed accumulators are cleared while the host waits
         # for the intersection count, when the GPU would otherwise idle.
         ctx.accumulators = None
@@ -82,7 +95,7 @@ class Composite(torch.autograd.Function):
         ctx.split = length
         ctx.options = (width, height, neural, near_plane, far_plane)
         ctx.set_materialize_grads(False)
-        return outputs
+        return shaped
 
     @staticmethod
     @once_differentiable
@@ -91,12 +104,15 @@ class Composite(torch.autograd.Function):
         accumulators, ctx.accumulators = ctx.accumulators, None
         *saved, lists, counts, checkpoints, checkpoint_index = ctx.saved_tensors
         segments = (ctx.split, checkpoints, checkpoint_index) if ctx.split else None
+        width, height = ctx.options[:2]
+        groups = [None if g is None else g.reshape(-1, height, width, g.shape[-1])
+                  for g in grad_groups]
         gg, ga, go, gb = _native.rasterize_backward(
-            *saved, list(grad_groups), *ctx.options, accumulators=accumulators,
+            *saved, groups, *ctx.options, accumulators=accumulators,
             replay=None if lists is None else (lists, counts, segments),
         )
-        return (gg, gg[:, 9:11], ga, go, None, None, None, gb, None, None, None, None, None, None,
-                None, None)
+        return (gg, gg[:, 9:11], ga, go, None, None, None, gb.view(ctx.background_shape), None,
+                None, None, None, None, None, None, None)
 
 
 class ProjectRecords(torch.autograd.Function):
@@ -525,27 +541,27 @@ def render(
             )
             bounded.record_violations(word, list(tensors))
 
-    views = view_matrices.reshape(scenes, cameras, 4, 4)
-    cameras_k = intrinsics.reshape(scenes, cameras, 3, 3)
+    views = _shaped(view_matrices, (scenes, cameras, 4, 4))
+    cameras_k = _shaped(intrinsics, (scenes, cameras, 3, 3))
     if sh_degree is not None:
         # Camera-specific SH colours: appearance and opacity rows per pair,
         # written by the HIP record kernel.
         k = (sh_degree + 1) ** 2
         (geometry, projected_means, parameters, opacity_rows, row_radii, primitive_ids,
          image_ids, dense_radii, scene_ids, camera_ids, surfel_ids) = ProjectRecords.apply(
-            means.reshape(scenes, n, 3), quaternions.reshape(scenes, n, 4),
-            scales.reshape(scenes, n, 2), opacities.reshape(scenes, n), views, cameras_k,
-            appearance[0].reshape(scenes, n, k, 3), appearance[1].reshape(scenes, n, k, 3),
-            appearance[2].reshape(scenes, n, 4), appearance[3].reshape(scenes, n, 4),
-            appearance[4].reshape(scenes, n, 4), sh_degree, width, height, near_plane,
+            _shaped(means, (scenes, n, 3)), _shaped(quaternions, (scenes, n, 4)),
+            _shaped(scales, (scenes, n, 2)), _shaped(opacities, (scenes, n)), views, cameras_k,
+            _shaped(appearance[0], (scenes, n, k, 3)), _shaped(appearance[1], (scenes, n, k, 3)),
+            _shaped(appearance[2], (scenes, n, 4)), _shaped(appearance[3], (scenes, n, 4)),
+            _shaped(appearance[4], (scenes, n, 4)), sh_degree, width, height, near_plane,
             far_plane, packed, bounded is not None,
         )
     else:
         # One appearance row per surfel, shared by every camera of its scene.
         (geometry, projected_means, row_radii, primitive_ids, image_ids, dense_radii,
          scene_ids, camera_ids, surfel_ids) = ProjectRecords.apply(
-            means.reshape(scenes, n, 3), quaternions.reshape(scenes, n, 4),
-            scales.reshape(scenes, n, 2), None, views, cameras_k, None, None, None, None, None,
+            _shaped(means, (scenes, n, 3)), _shaped(quaternions, (scenes, n, 4)),
+            _shaped(scales, (scenes, n, 2)), None, views, cameras_k, None, None, None, None, None,
             None, width, height, near_plane, far_plane, packed, bounded is not None,
         )
         width_of_row = 57 if neural else 18
@@ -565,7 +581,7 @@ def render(
         primitive_ids,
         image_ids,
         row_radii,
-        backgrounds.reshape(scenes * cameras, 3),
+        backgrounds,
         width,
         height,
         neural,
@@ -575,7 +591,6 @@ def render(
         torch.is_grad_enabled(),
         violations,
     )
-    image_shape = batch + (cameras, height, width)
     meta = {
         "radii": row_radii if packed else dense_radii.reshape(batch + (cameras, n)),
         "projected_means": projected_means,
@@ -583,11 +598,11 @@ def render(
         "camera_ids": camera_ids,
         "primitive_ids": surfel_ids,
         "packed": packed,
-        "accumulated_depth": depth.reshape(image_shape + (1,)),
-        "normals": normals.reshape(image_shape + (3,)),
-        "distortion": distortion.reshape(image_shape + (1,)),
+        "accumulated_depth": depth,
+        "normals": normals,
+        "distortion": distortion,
     }
-    return rgb.reshape(image_shape + (3,)), alpha.reshape(image_shape + (1,)), meta
+    return rgb, alpha, meta
 
 
 def rasterize_gabors(
