@@ -7,8 +7,10 @@
 //   1. upsweep  - every 4096-key span (2048 for short sorts) builds a digit
 //                 histogram in LDS and stores it digit-major:
 //                 counts[digit * spans + span];
-//   2. scan     - one exclusive scan over those counts yields, for every
-//                 (digit, span), the first output slot;
+//   2. scan     - one workgroup per digit scans that digit's counts over
+//                 the spans (and the downsweep adds the digit totals'
+//                 prefix), which yields, for every (digit, span), the first
+//                 output slot;
 //   3. downsweep- every span ranks its keys stably (wave-level digit match
 //                 via ballots, per-wave running counters in LDS), stages the
 //                 locally sorted span in LDS and writes it out so that runs
@@ -100,17 +102,34 @@ __global__ __launch_bounds__(kSortBlock) void radix_upsweep_kernel(
   counts[int64_t(d) * spans + blockIdx.x] = total;
 }
 
-struct CountLoad {
-  const uint32_t* counts;
-  __device__ uint32_t operator()(int64_t i) const { return counts[i]; }
-};
-
-struct ExclusiveStore {
-  uint32_t* out;
-  __device__ void operator()(int64_t i, uint32_t inclusive, uint32_t v) const {
-    out[i] = inclusive - v;
+// Pass 2: workgroup d turns row d of the digit-major counts (the digit's
+// count in every span) into exclusive prefixes along the row and writes the
+// row's total; the downsweep adds the exclusive prefix of the 256 row
+// totals, the digit's first output slot. One launch of 256 workgroups,
+// each scanning `spans` counts, replaces a three-launch scan of all
+// 256 * spans counts.
+__global__ __launch_bounds__(kSortBlock) void scan_rows_kernel(uint32_t* __restrict__ counts,
+                                                               int64_t spans,
+                                                               uint32_t* __restrict__ totals) {
+  __shared__ uint32_t partial[2][kSortWaves];
+  const int lane = __lane_id(), wave = threadIdx.x >> 6;
+  uint32_t* row = counts + int64_t(blockIdx.x) * spans;
+  uint32_t carry = 0;
+  int parity = 0;
+  for (int64_t base = 0; base < spans; base += kSortBlock, parity ^= 1) {
+    const int64_t i = base + threadIdx.x;
+    const uint32_t v = i < spans ? row[i] : 0u;
+    const uint32_t incl = wave_inclusive_scan(v);
+    if (lane == 63) partial[parity][wave] = incl;
+    __syncthreads();
+    uint32_t before = carry;
+    for (int w = 0; w < wave; ++w) before += partial[parity][w];
+    if (i < spans) row[i] = before + incl - v;
+#pragma unroll
+    for (int w = 0; w < kSortWaves; ++w) carry += partial[parity][w];
   }
-};
+  if (threadIdx.x == 0) totals[blockIdx.x] = carry;
+}
 
 // Values: whether int32 values travel with the keys (a keys-only sort
 // passes null value arrays).
@@ -119,7 +138,7 @@ __global__ __launch_bounds__(kSortBlock) void radix_downsweep_kernel(
     const Key* __restrict__ keys_in, const int* __restrict__ values_in,
     Key* __restrict__ keys_out, int* __restrict__ values_out, int64_t capacity,
     const int64_t* __restrict__ live, int shift, int bits, const uint32_t* __restrict__ offsets,
-    int64_t spans) {
+    const uint32_t* __restrict__ totals, int64_t spans) {
   const int64_t m = live_length(capacity, live);
   constexpr int kSortItems = Items;
   constexpr int kSortSpan = span_keys(Items);
@@ -180,20 +199,30 @@ __global__ __launch_bounds__(kSortBlock) void radix_downsweep_kernel(
       run += c;
     }
     local_start[d] = run;  // digit total; converted to a prefix below
-    global_start[d] = offsets[int64_t(d) * spans + span];
   }
   __syncthreads();
-  // Exclusive prefix of the 256 digit totals (one value per thread).
+  // Exclusive prefixes (one digit per thread) of the span's 256 digit
+  // totals and of the whole sequence's 256 digit totals; the latter plus
+  // the digit's prefix over the earlier spans is its first output slot.
   {
-    __shared__ uint32_t wave_totals[kSortWaves];
+    __shared__ uint32_t wave_totals[2][kSortWaves];
     const uint32_t v = local_start[threadIdx.x];
     const uint32_t incl = wave_inclusive_scan(v);
-    if (lane == 63) wave_totals[wave] = incl;
+    const uint32_t all = totals[threadIdx.x];
+    const uint32_t all_incl = wave_inclusive_scan(all);
+    if (lane == 63) {
+      wave_totals[0][wave] = incl;
+      wave_totals[1][wave] = all_incl;
+    }
     __syncthreads();
-    uint32_t before = 0;
-    for (int w = 0; w < wave; ++w) before += wave_totals[w];
-    __syncthreads();
+    uint32_t before = 0, all_before = 0;
+    for (int w = 0; w < wave; ++w) {
+      before += wave_totals[0][w];
+      all_before += wave_totals[1][w];
+    }
     local_start[threadIdx.x] = before + incl - v;
+    global_start[threadIdx.x] =
+        all_before + all_incl - all + offsets[int64_t(threadIdx.x) * spans + span];
   }
   __syncthreads();
 #pragma unroll
@@ -347,7 +376,7 @@ __global__ __launch_bounds__(256) void copy_pairs_kernel(const Key* __restrict__
 
 struct SortWorkspace {
   uint32_t* counts;       // kBins * spans
-  uint32_t* scan_sums;    // scan span totals
+  uint32_t* totals;       // kBins: each digit's count over the whole sequence
   void* keys_tmp;         // m keys
   int* values_tmp;        // m
   size_t bytes;
@@ -361,8 +390,8 @@ SortWorkspace layout(void* base, int64_t m, int key_bytes) {
   char* p = static_cast<char*>(base);
   w.counts = reinterpret_cast<uint32_t*>(p + offset);
   offset = align_up(offset + size_t(count_items) * 4, 256);
-  w.scan_sums = reinterpret_cast<uint32_t*>(p + offset);
-  offset = align_up(offset + scan_workspace_bytes(count_items, 4), 256);
+  w.totals = reinterpret_cast<uint32_t*>(p + offset);
+  offset = align_up(offset + size_t(kBins) * 4, 256);
   w.keys_tmp = p + offset;
   offset = align_up(offset + size_t(m) * size_t(key_bytes), 256);
   w.values_tmp = reinterpret_cast<int*>(p + offset);  // unused by keys-only sorts
@@ -424,12 +453,11 @@ int radix_sort(const Key* keys_in, Key* keys_out, const int* values_in, int* val
           src_k, m, live, shift, bits, w.counts, spans);
     }
     GS_LAUNCHED("radix_upsweep_kernel");
-    int status = run_scan<uint32_t>(int64_t(kBins) * spans, CountLoad{w.counts},
-                                    ExclusiveStore{w.counts}, w.scan_sums, s);
-    if (status != GS_OK) return status;
+    scan_rows_kernel<<<kBins, kSortBlock, 0, s>>>(w.counts, spans, w.totals);
+    GS_LAUNCHED("scan_rows_kernel");
     auto downsweep = [&](auto kernel) {
       kernel<<<unsigned(spans), kSortBlock, 0, s>>>(src_k, src_v, dst_k, dst_v, m, live, shift,
-                                                    bits, w.counts, spans);
+                                                    bits, w.counts, w.totals, spans);
     };
     if (items == 8) {
       if (values_in) downsweep(radix_downsweep_kernel<Key, 8, true>);
