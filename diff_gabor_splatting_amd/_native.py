@@ -31,26 +31,42 @@ INT_MAX = 2**31 - 1
 # Replay-list entries carry a tile-list position in 28 bits.
 REPLAY_MAX_ENTRIES = 2**28 - 1
 # Split tiles (gs_render_forward's segment_* arguments): images with fewer
-# tiles than this have too few workgroups to hide a long tile list, so the
-# backward replays long lists in segments; the segment length is chosen so
-# that the intersections make about SPLIT_TARGET_SEGMENTS segments.
+# tiles than SPLIT_MAX_TILES have too few workgroups to hide a long tile
+# list, so tiles longer than SPLIT_LENGTH records are composited (and their
+# backward replayed) in segments of that many records, one workgroup each.
+# The segment length does not depend on the intersection count, and the
+# checkpoint slots are at most SPLIT_MAX_SLOTS, so a render into a
+# fixed-capacity point list splits its tiles exactly as the synchronised
+# render does and gives the same bits.
 SPLIT_MAX_TILES = 2048
-SPLIT_TARGET_SEGMENTS = 2048
-CHECKPOINT_FLOATS = 10
+SPLIT_LENGTH = 64
+SPLIT_MAX_SLOTS = 16384
 
 
 def split_length(tiles: int, intersections: int) -> int:
-    """List records per backward segment of a split tile (a multiple of 64),
-    or 0 to split none."""
+    """List records per segment of a split tile (a multiple of 64), or 0 to
+    split none."""
     if tiles >= SPLIT_MAX_TILES or intersections <= 0:
         return 0
-    return 64 * max(1, -(-intersections // (64 * SPLIT_TARGET_SEGMENTS)))
+    return SPLIT_LENGTH
 
 
 def split_slots(intersections: int, length: int) -> int:
-    """Checkpoint slots that always suffice: a tile of L > length records
-    needs ceil(L / length) <= floor(2 L / length) of them."""
-    return 2 * intersections // length if length else 0
+    """Checkpoint slots: a tile of L > length records needs ceil(L / length)
+    <= floor(2 L / length) of them, capped at SPLIT_MAX_SLOTS (the slots go
+    to tiles in tile order; later tiles past the cap are not split)."""
+    return min(2 * intersections // length, SPLIT_MAX_SLOTS) if length else 0
+
+
+CHECKPOINT_FLOATS = 13
+
+
+def split_index_length(tiles: int, slots: int) -> int:
+    """Length (int32) of gs_render_forward's segment_index buffer: slot bases
+    per tile, replay lengths per slot, then the forward's (tile, segment)
+    work list at an even offset."""
+    return (tiles + slots + 1) // 2 * 2 + 2 * (tiles + slots)
+
 
 _c_int = ctypes.c_int32
 _c_i64 = ctypes.c_int64
@@ -787,11 +803,12 @@ def rasterize_forward(
     some pixel took, in list order - or None when the point list is too long
     for them (2^28 entries or more). ``segments`` is None, or (length,
     checkpoint state, checkpoint index) when tiles are split: tiles longer
-    than ``length`` records have their backward replayed in segments of that
-    many list records, each from a checkpoint the forward wrote (see
+    than ``length`` records are composited in segments of that many list
+    records, merged per pixel, and their backward is replayed in the same
+    segments, each from a checkpoint the forward wrote (see
     gs_render_forward). ``split`` (an addition): the segment length, 0 for
     none, or None to choose it (split_length: only images with fewer than
-    SPLIT_MAX_TILES tiles are split). ``violations`` (an addition): a pending value
+    SPLIT_MAX_TILES tiles are split, whether or not a backward follows). ``violations`` (an addition): a pending value
     check, raised with the read-back of M (see bin_depth_first).
     """
     _check_buffers(geometry, appearance, opacities, primitive_ids, backgrounds, neural)
@@ -845,16 +862,17 @@ def rasterize_forward(
             maps = tuple(groups)
         data, strides = _map_group_args(groups, "map outputs")
         lists = None
-        length, slots, segment_state, segment_index = 0, 0, None, None
+        length = split_length(tiles, point_list.numel()) if split is None else int(split)
+        slots = split_slots(point_list.numel(), length)
+        segment_state = segment_index = None
+        if slots:
+            segment_state = torch.empty((slots, CHECKPOINT_FLOATS, TILE * TILE),
+                                        dtype=torch.float32, device=device)
+            segment_index = torch.empty(split_index_length(tiles, slots), dtype=torch.int32,
+                                        device=device)
+        else:
+            length = 0
         if replay and point_list.numel() < REPLAY_MAX_ENTRIES:
-            length = split_length(tiles, point_list.numel()) if split is None else int(split)
-            slots = split_slots(point_list.numel(), length)
-            if slots:
-                segment_state = torch.empty((slots, CHECKPOINT_FLOATS, TILE * TILE),
-                                            dtype=torch.float32, device=device)
-                segment_index = torch.empty(tiles + slots, dtype=torch.int32, device=device)
-            else:
-                length = 0
             lists = (torch.empty((max(point_list.numel(), 1), 2), dtype=torch.int32,
                                  device=device),
                      torch.empty(tiles, dtype=torch.int32, device=device),
@@ -939,7 +957,7 @@ def rasterize_backward(
                 and segment_state.device == device and segment_index.device == device
                 and segment_state.is_contiguous() and segment_index.is_contiguous()
                 and segment_state.shape[1:] == (CHECKPOINT_FLOATS, TILE * TILE)
-                and segment_index.shape == (images * tw * th + slots,),
+                and segment_index.shape == (split_index_length(images * tw * th, slots),),
                 "invalid split-tile checkpoints",
             )
         _require(

@@ -661,26 +661,26 @@ struct Segments {
   float* state;  // [capacity][kCheckpointFloats][kTilePixels], one slot per checkpoint
   int* index;    // [tiles]: a split tile's first slot (-1: not split); then
                  // [capacity]: the replay-list length at each slot's checkpoint
+  int2* work;    // [tiles + capacity]: the forward's (tile, segment) pairs,
+                 // heaviest first, in the index buffer after an even offset
 };
 
-// Per pixel: T, rgb prefix (3), depth, normals (3), m1, m2.
-constexpr int kCheckpointFloats = 10;
+// Ints of the index buffer before the forward's work list (kept 8-byte
+// aligned), and the buffer's whole length.
+__host__ __device__ constexpr int64_t segment_work_offset(int64_t tiles, int64_t capacity) {
+  return (tiles + capacity + 1) / 2 * 2;
+}
+__host__ __device__ constexpr int64_t segment_index_length(int64_t tiles, int64_t capacity) {
+  return segment_work_offset(tiles, capacity) + 2 * (tiles + capacity);
+}
+
+// Floats per pixel of a checkpoint slot: a checkpoint is T, the rgb prefix
+// (3), depth, normals (3), m1, m2; during the forward a slot first holds its
+// segment's relative results (13 values, see renderForward).
+constexpr int kCheckpointFloats = 13;
 
 __device__ __forceinline__ int segment_count(int list_length, int length) {
   return (length > 0 && list_length > length) ? (list_length + length - 1) / length : 1;
-}
-
-// Writes this thread's pixel into checkpoint slot `slot` (out[] holds the
-// prefix sums in map order, before the background) and, from thread 0, the
-// replay-list length n.
-__device__ __forceinline__ void write_checkpoint(const Segments& seg, int slot, float T,
-                                                 const float* out, float m1, float m2, int n) {
-  float* c = seg.state + int64_t(slot) * (kCheckpointFloats * kTilePixels) + threadIdx.x;
-  const float values[kCheckpointFloats] = {T,      out[0], out[1], out[2], out[4],
-                                           out[5], out[6], out[7], m1,     m2};
-#pragma unroll
-  for (int q = 0; q < kCheckpointFloats; ++q) c[q * kTilePixels] = values[q];
-  if (threadIdx.x == 0) seg.index[seg.tiles + slot] = n;
 }
 
 struct TilePixel {
@@ -772,6 +772,42 @@ __global__ __launch_bounds__(kOrderBlock) void tile_order_kernel(const int* __re
       carry += scan[kOrderBlock - 1];
       __syncthreads();
     }
+    // The forward's (tile, segment) work list, heaviest first by the list
+    // records each walks; entries past the work count are (-1, 0).
+    for (int b = threadIdx.x; b < kOrderBuckets; b += kOrderBlock) count[b] = 0;
+    __syncthreads();
+    auto pieces = [&](int t) {
+      return seg.index[t] >= 0 ? segment_count(ranges[t].y - ranges[t].x, seg.length) : 1;
+    };
+    auto piece_cost = [&](int t, int k, int n) {
+      const int length = ranges[t].y - ranges[t].x;
+      return n == 1 ? length : min(seg.length, length - k * seg.length);
+    };
+    for (int t = threadIdx.x; t < tiles; t += kOrderBlock) {
+      const int n = pieces(t);
+      for (int k = 0; k < n; ++k) atomicAdd(&count[cost_bucket(piece_cost(t, k, n))], 1);
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      int run = 0;
+      for (int b = kOrderBuckets - 1; b >= 0; --b) {
+        next[b] = run;
+        run += count[b];
+      }
+      scan[0] = run;
+    }
+    __syncthreads();
+    const int total = scan[0];
+    for (int t = threadIdx.x; t < tiles; t += kOrderBlock) {
+      const int n = pieces(t);
+      for (int k = 0; k < n; ++k)
+        seg.work[atomicAdd(&next[cost_bucket(piece_cost(t, k, n))], 1)] = make_int2(t, k);
+    }
+    for (int i = total + threadIdx.x; i < tiles + seg.capacity; i += kOrderBlock)
+      seg.work[i] = make_int2(-1, 0);
+    __syncthreads();
+    for (int b = threadIdx.x; b < kOrderBuckets; b += kOrderBlock) count[b] = 0;
+    __syncthreads();
   }
   for (int b = threadIdx.x; b < kOrderBuckets; b += kOrderBlock) count[b] = 0;
   __syncthreads();
@@ -871,6 +907,149 @@ __global__ __launch_bounds__(kTilePixels) void tile_last_kernel(int width, int h
 //
 // Replay: also write the tile's replay list (replay + range start, see
 // append_replay) and its length (replay_counts[tile]).
+// Per-pixel state of a front-to-back walk: the map sums (before the
+// background), transmittance, the two depth moments, the last list position
+// taken (counted from 1) and whether the pixel is finished.
+struct Walk {
+  float out[kMaps];
+  float T, m1, m2;
+  int last;
+  bool done;
+};
+
+__device__ __forceinline__ void begin_walk(Walk& w, bool inside) {
+#pragma unroll
+  for (int c = 0; c < kMaps; ++c) w.out[c] = 0.f;
+  w.T = 1.f;
+  w.m1 = w.m2 = 0.f;
+  w.last = 0;
+  w.done = !inside;
+}
+
+// The forward's LDS: a batch of staged rows and their ids.
+template <bool Neural>
+struct ForwardStage {
+  float* rows;
+  float* raw;
+  float* reach_rows;
+  int* ids;
+  int64_t* prims;
+  uint64_t* wave_taken;
+};
+
+// Composites list positions [first, end) (counted from the tile's range
+// start) into every unfinished pixel, front to back, stopping a pixel before
+// a contribution that would take its transmittance below 1e-4. With Replay,
+// wave 0 appends the records some pixel took to `replay_block` (n entries so
+// far, returned). A pixel starts from the state in `w`: a whole tile starts
+// at T = 1; so does a segment of a split tile, whose walk is then relative
+// to the transmittance in front of it (and its stops are sufficient, not
+// exact: see mergeSegments).
+template <bool Neural, bool Replay>
+__device__ __forceinline__ int walk_list(const ForwardStage<Neural>& st, int range_x, int first,
+                                         int end, const int* __restrict__ point_list,
+                                         const int64_t* __restrict__ primitive_ids,
+                                         const float* __restrict__ geometry,
+                                         const float* __restrict__ appearance,
+                                         const float* __restrict__ opacities, float x, float y,
+                                         float tile_x, float tile_y, float near_plane,
+                                         float mscale, float mnear, int2* replay_block,
+                                         Walk& w) {
+  using L = Layout<Neural, true>;
+  const int wave = threadIdx.x >> 6;
+  // Point-list entry and primitive id of record threadIdx.x of the next
+  // batch, read ahead: the entry while this batch is gathered, the id while
+  // its records are composited.
+  int next_id = 0;
+  int64_t next_prim = 0;
+  if (int(threadIdx.x) < min(kBatch, end - first)) {
+    next_id = point_list[range_x + first + threadIdx.x];
+    next_prim = primitive_ids[next_id];
+  }
+  // Replay bookkeeping (wave 0): entries written so far, and the previous
+  // batch, whose taken records are appended once every wave has finished it
+  // (before the next batch overwrites its staged ids).
+  int replay_n = 0, batch_first = 0, batch_count = 0;
+  for (int start = first; start < end; start += kBatch) {
+    if (__syncthreads_count(w.done) == kTilePixels) break;
+    if (Replay && wave == 0)
+      replay_n = append_replay(st.wave_taken, st.ids, replay_block, replay_n, batch_first,
+                               batch_count);
+    const int count = min(kBatch, end - start);
+    const int id = next_id;
+    const int64_t prim = next_prim;
+    const bool ahead = int(threadIdx.x) < min(kBatch, end - start - kBatch);
+    if (ahead) next_id = point_list[range_x + start + kBatch + threadIdx.x];
+    const uint64_t reach = load_batch<Neural, kGatherQuarters, kReachTest, true>(
+        st.rows, st.raw, st.reach_rows, st.ids, st.prims, tile_x, tile_y, count, id, prim,
+        geometry, appearance, opacities);
+    if (ahead) next_prim = primitive_ids[next_id];
+    batch_first = start;
+    batch_count = count;
+    // Only the records whose footprint meets this wave's quadrant, in list
+    // order. The loop runs in lockstep across the wave: finished lanes are
+    // masked through `done` rather than leaving the loop, so that every
+    // branch below is on a wave-wide (scalar) condition.
+    uint64_t todo = __all(w.done) ? 0 : wave_uniform(reach);
+    uint64_t taken = 0;  // records that a lane of this wave took
+    while (todo) {
+      const int j = __builtin_ctzll(todo);
+      todo &= todo - 1;
+      const float* r = st.rows + j * L::STRIDE;
+      Sample v;
+      const bool ok = sample_surface<Neural>(r, x, y, near_plane, !w.done, v);
+      if (!__any(ok)) continue;
+      const float next = w.T * (1.f - v.alpha);
+      const bool stop = ok & (next < 0.0001f);
+      const bool take = ok & !stop;
+      if (__any(stop)) {
+        w.done |= stop;
+        if (__all(w.done)) break;
+      }
+      if (!__any(take)) continue;
+      taken |= uint64_t(1) << j;
+      Shade a;
+      shade<Neural, false>(r, v.s, a);
+      if (take) {
+        const float wt = w.T * v.alpha;
+        const float m = mscale - mnear * rcp(v.depth);
+#pragma unroll
+        for (int c = 0; c < 3; ++c) {
+          w.out[c] += wt * a.color[c];
+          w.out[5 + c] += wt * r[11 + c];
+        }
+        w.out[4] += wt * v.depth;
+        w.out[8] += wt * (m * m * (1.f - w.T) + w.m2 - 2.f * m * w.m1);
+        w.m1 += wt * m;
+        w.m2 += wt * m * m;
+        w.T = next;
+        w.last = start + j + 1;
+      }
+    }
+    if (Replay && lane_id() == 0) st.wave_taken[wave] = taken;
+  }
+  if constexpr (Replay) {
+    __syncthreads();
+    if (wave == 0)
+      replay_n = append_replay(st.wave_taken, st.ids, replay_block, replay_n, batch_first,
+                               batch_count);
+  }
+  return replay_n;
+}
+
+// A segment's slot while the forward runs (before mergeSegments turns it
+// into the checkpoint): the relative walk's T', its map sums (rgb, depth,
+// normals), sum w' m, sum w' m^2, its own distortion sum, the last position
+// taken and whether the relative walk finished the pixel.
+constexpr int kSegmentResults = 13;
+static_assert(kCheckpointFloats >= kSegmentResults, "a slot holds a segment's results");
+
+// Forward compositor: one workgroup per tile, or per segment of a split tile
+// (seg.work lists the (tile, segment) pairs heaviest first; a segment writes
+// its relative sums and its replay entries, at its own block of the tile's
+// replay list, and mergeSegments completes the tile).
+// Replay: also write the tile's replay list (replay + range start, see
+// append_replay) and its length (replay_counts[tile]).
 template <bool Neural, bool Replay>
 __global__ __launch_bounds__(kTilePixels, Neural ? 4 : 6) void renderForward(
     int width, int height, int tw, int th, const float* __restrict__ geometry,
@@ -887,7 +1066,11 @@ __global__ __launch_bounds__(kTilePixels, Neural ? 4 : 6) void renderForward(
   __shared__ int ids[kBatch];
   __shared__ int64_t prims[kBatch];
   __shared__ uint64_t wave_taken[kTilePixels / 64];
-  const int tile = order[blockIdx.x];
+  const ForwardStage<Neural> st{rows, raw, reach_rows, ids, prims, wave_taken};
+  // (tile, segment) of this workgroup; past the work count: nothing.
+  const int2 piece = seg.length > 0 ? seg.work[blockIdx.x] : make_int2(order[blockIdx.x], 0);
+  if (piece.x < 0) return;
+  const int tile = piece.x;
 #ifdef GS_DIAGNOSTICS
   const long long diag_begin = wall_clock64();
 #endif
@@ -896,120 +1079,182 @@ __global__ __launch_bounds__(kTilePixels, Neural ? 4 : 6) void renderForward(
   const int wave = threadIdx.x >> 6;
   const float tile_x = float(tp.px - (wave & 1) * 8 - (lane_id() & 7));
   const float tile_y = float(tp.py - (wave >> 1) * 8 - (lane_id() >> 3));
-  bool done = !tp.inside;
-  float out[kMaps];
-#pragma unroll
-  for (int c = 0; c < kMaps; ++c) out[c] = 0.f;
-  float T = 1.f, m1 = 0.f, m2 = 0.f;
-  int last = 0;
   const int2 range = ranges[tile];
   const float mscale = far_plane / (far_plane - near_plane);
   const float mnear = mscale * near_plane;
-  // Point-list entry and primitive id of record threadIdx.x of the next
-  // batch, read ahead: the entry while this batch is gathered, the id while
-  // its records are composited.
-  int next_id = 0;
-  int64_t next_prim = 0;
-  if (int(threadIdx.x) < min(kBatch, range.y - range.x)) {
-    next_id = point_list[range.x + threadIdx.x];
-    next_prim = primitive_ids[next_id];
+  const int base = seg.length > 0 ? seg.index[tile] : -1;
+  int first = 0, end = range.y - range.x;
+  if (base >= 0) {
+    first = piece.y * seg.length;
+    end = min(first + seg.length, end);
   }
-  // Replay bookkeeping (wave 0): entries written so far, and the previous
-  // batch, whose taken records are appended once every wave has finished it
-  // (before the next batch overwrites its staged ids).
-  int replay_n = 0, batch_first = 0, batch_count = 0;
-  // Split tile: its first checkpoint slot and checkpoint count (K), and the
-  // checkpoints written so far (at list records length, 2 length, ...).
-  const int slot_base = Replay && seg.length > 0 ? seg.index[tile] : -1;
-  const int checkpoints = slot_base >= 0 ? segment_count(range.y - range.x, seg.length) : 0;
-  int written = 0;
-  for (int start = range.x; start < range.y; start += kBatch) {
-    if (__syncthreads_count(done) == kTilePixels) break;
-    if (Replay && wave == 0)
-      replay_n = append_replay(wave_taken, ids, replay + range.x, replay_n, batch_first,
-                               batch_count);
-    if (slot_base >= 0 && start > range.x && (start - range.x) % seg.length == 0)
-      write_checkpoint(seg, slot_base + written++, T, out, m1, m2, replay_n);
-    const int count = min(kBatch, range.y - start);
-    const int id = next_id;
-    const int64_t prim = next_prim;
-    const bool ahead = int(threadIdx.x) < min(kBatch, range.y - start - kBatch);
-    if (ahead) next_id = point_list[start + kBatch + threadIdx.x];
-    const uint64_t reach = load_batch<Neural, kGatherQuarters, kReachTest, true>(
-        rows, raw, reach_rows, ids, prims, tile_x, tile_y, count, id, prim, geometry, appearance,
-        opacities);
-    if (ahead) next_prim = primitive_ids[next_id];
-    batch_first = start - range.x;
-    batch_count = count;
-    // Only the records whose footprint meets this wave's quadrant, in list
-    // order. The loop runs in lockstep across the wave: finished lanes are
-    // masked through `done` rather than leaving the loop, so that every
-    // branch below is on a wave-wide (scalar) condition.
-    uint64_t todo = __all(done) ? 0 : wave_uniform(reach);
-    uint64_t taken = 0;  // records that a lane of this wave took
-    while (todo) {
-      const int j = __builtin_ctzll(todo);
-      todo &= todo - 1;
-      const float* r = rows + j * L::STRIDE;
-      Sample v;
-      const bool ok = sample_surface<Neural>(r, x, y, near_plane, !done, v);
-      if (!__any(ok)) continue;
-      const float next = T * (1.f - v.alpha);
-      const bool stop = ok & (next < 0.0001f);
-      const bool take = ok & !stop;
-      if (__any(stop)) {
-        done |= stop;
-        if (__all(done)) break;
-      }
-      if (!__any(take)) continue;
-      taken |= uint64_t(1) << j;
-      Shade a;
-      shade<Neural, false>(r, v.s, a);
-      if (take) {
-        const float w = T * v.alpha;
-        const float m = mscale - mnear * rcp(v.depth);
+  Walk w;
+  begin_walk(w, tp.inside);
+  const int replay_n = walk_list<Neural, Replay>(
+      st, range.x, first, end, point_list, primitive_ids, geometry, appearance, opacities, x, y,
+      tile_x, tile_y, near_plane, mscale, mnear, replay + range.x + first, w);
+  if (base >= 0) {
+    // A segment of a split tile: its relative results and replay count.
+    float* c = seg.state + int64_t(base + piece.y) * (kCheckpointFloats * kTilePixels) +
+               threadIdx.x;
+    const float results[kSegmentResults] = {
+        w.T,      w.out[0], w.out[1], w.out[2], w.out[4], w.out[5], w.out[6],
+        w.out[7], w.m1,     w.m2,     w.out[8], __int_as_float(w.last),
+        w.done ? 1.f : 0.f};
 #pragma unroll
-        for (int c = 0; c < 3; ++c) {
-          out[c] += w * a.color[c];
-          out[5 + c] += w * r[11 + c];
-        }
-        out[4] += w * v.depth;
-        out[8] += w * (m * m * (1.f - T) + m2 - 2.f * m * m1);
-        m1 += w * m;
-        m2 += w * m * m;
-        T = next;
-        last = start + j - range.x + 1;
-      }
+    for (int q = 0; q < kSegmentResults; ++q) c[q * kTilePixels] = results[q];
+    if (threadIdx.x == 0) seg.index[seg.tiles + base + piece.y] = replay_n;
+  } else {
+    if (Replay && threadIdx.x == 0) replay_counts[tile] = replay_n;
+    if (tp.inside) {
+#pragma unroll
+      for (int c = 0; c < 3; ++c) w.out[c] += w.T * backgrounds[tp.image * 3 + c];
+      w.out[3] = 1.f - w.T;
+#pragma unroll
+      for (int c = 0; c < kMaps; ++c)
+        maps.data[map_group(c)][maps.offset(c, tp.pixel)] = w.out[c];
+      state[tp.pixel * 3 + 0] = w.T;
+      state[tp.pixel * 3 + 1] = w.m1;
+      state[tp.pixel * 3 + 2] = w.m2;
+      contributors[tp.pixel] = w.last;
     }
-    if (Replay && lane_id() == 0) wave_taken[wave] = taken;
-  }
-  if constexpr (Replay) {
-    __syncthreads();
-    if (wave == 0) {
-      replay_n = append_replay(wave_taken, ids, replay + range.x, replay_n, batch_first,
-                               batch_count);
-      if (threadIdx.x == 0) replay_counts[tile] = replay_n;
-    }
-    // The checkpoints the walk did not reach (it stopped early) and the
-    // last one hold the final state: their segments are empty.
-    for (int k = written; k < checkpoints; ++k)
-      write_checkpoint(seg, slot_base + k, T, out, m1, m2, replay_n);
-  }
-  if (tp.inside) {
-#pragma unroll
-    for (int c = 0; c < 3; ++c) out[c] += T * backgrounds[tp.image * 3 + c];
-    out[3] = 1.f - T;
-#pragma unroll
-    for (int c = 0; c < kMaps; ++c) maps.data[map_group(c)][maps.offset(c, tp.pixel)] = out[c];
-    state[tp.pixel * 3 + 0] = T;
-    state[tp.pixel * 3 + 1] = m1;
-    state[tp.pixel * 3 + 2] = m2;
-    contributors[tp.pixel] = last;
   }
 #ifdef GS_DIAGNOSTICS
   __syncthreads();
   stamp_tile(gs_diagnostics.forward_span, tile, diag_begin);
 #endif
+}
+
+// Completes every split tile (one workgroup each; other tiles exit): walks
+// its segments' results in list order per pixel, with the transmittance T
+// in front of segment k. A segment whose relative walk did not finish the
+// pixel and whose T' keeps T T' >= 1e-4 is merged in closed form:
+//   sums += T sums', T *= T', m1 += T sum w'm, m2 += T sum w'm^2, and the
+//   distortion gains T M2' + T^2 (dist' - M2') + T (m2 W' - 2 m1 M1')
+//   (W' = 1 - T': its terms m^2 (1 - T T'_i) + m2 + T M2'_{<i} - 2 m (m1 +
+//   T M1'_{<i}) expanded over the segment's records);
+// otherwise the pixel stops inside segment k (a relative stop implies a
+// stop: T T'(1 - alpha) <= T'(1 - alpha) < 1e-4), and the segment is walked
+// again for the pixels concerned with their true transmittance, which
+// applies the stop rule exactly. The records taken then are a subset of the
+// relative walk's, whose replay entries therefore cover them. Writes the
+// maps, state and contributors, checkpoint c_{k+1} into segment k's slot
+// (the prefix state after it) and packs the segments' replay blocks into
+// one list, with its running lengths as the checkpoints' replay lengths.
+template <bool Neural>
+__global__ __launch_bounds__(kTilePixels) void mergeSegments(
+    int width, int height, int tw, int th, const float* __restrict__ geometry,
+    const float* __restrict__ appearance, const float* __restrict__ opacities,
+    const int64_t* __restrict__ primitive_ids, const float* __restrict__ backgrounds,
+    const int* __restrict__ point_list, const int2* __restrict__ ranges, float near_plane,
+    float far_plane, MapGroups<float> maps, float* __restrict__ state,
+    int* __restrict__ contributors, int2* __restrict__ replay, int* __restrict__ replay_counts,
+    Segments seg) {
+  using L = Layout<Neural, true>;
+  __shared__ __align__(16) float rows[kBatch * L::STRIDE];
+  __shared__ __align__(16) float raw[kBatch * L::RAW_STRIDE];
+  __shared__ float reach_rows[kBatch * kReachPitch];
+  __shared__ int ids[kBatch];
+  __shared__ int64_t prims[kBatch];
+  __shared__ uint64_t wave_taken[kTilePixels / 64];
+  const ForwardStage<Neural> st{rows, raw, reach_rows, ids, prims, wave_taken};
+  const int tile = blockIdx.x;
+  const int base = seg.index[tile];
+  if (base < 0) return;
+  const TilePixel tp = tile_pixel(tile, width, height, tw, th);
+  const float x = float(tp.px), y = float(tp.py);
+  const int wave = threadIdx.x >> 6;
+  const float tile_x = float(tp.px - (wave & 1) * 8 - (lane_id() & 7));
+  const float tile_y = float(tp.py - (wave >> 1) * 8 - (lane_id() >> 3));
+  const int2 range = ranges[tile];
+  const int length = range.y - range.x;
+  const int pieces = segment_count(length, seg.length);
+  const float mscale = far_plane / (far_plane - near_plane);
+  const float mnear = mscale * near_plane;
+  constexpr int kSlot = kCheckpointFloats * kTilePixels;
+  Walk w;
+  begin_walk(w, tp.inside);
+  for (int k = 0; k < pieces; ++k) {
+    float* c = seg.state + int64_t(base + k) * kSlot + threadIdx.x;
+    float r[kSegmentResults];
+#pragma unroll
+    for (int q = 0; q < kSegmentResults; ++q) r[q] = c[q * kTilePixels];
+    bool again = false;
+    if (!w.done) {
+      const float Tp = r[0];
+      // (With 0.1% slack, so that a product rounded differently from the
+      // record-by-record one never decides the stop.)
+      if (r[12] != 0.f || w.T * Tp < 1.001e-4f) {
+        again = true;
+      } else {
+        const float Ts = w.T;
+        const float M1 = r[8], M2 = r[9];
+        w.out[8] += Ts * M2 + Ts * Ts * (r[10] - M2) + Ts * (w.m2 * (1.f - Tp) - 2.f * w.m1 * M1);
+        w.out[0] += Ts * r[1];
+        w.out[1] += Ts * r[2];
+        w.out[2] += Ts * r[3];
+        w.out[4] += Ts * r[4];
+        w.out[5] += Ts * r[5];
+        w.out[6] += Ts * r[6];
+        w.out[7] += Ts * r[7];
+        w.m1 += Ts * M1;
+        w.m2 += Ts * M2;
+        w.T = Ts * Tp;
+        const int last = __float_as_int(r[11]);
+        if (last > 0) w.last = last;
+      }
+    }
+    if (__syncthreads_or(again)) {
+      // Exact walk of segment k for the pixels that stop inside it.
+      const bool finished = w.done;
+      w.done = finished || !again;
+      const int first = k * seg.length;
+      walk_list<Neural, false>(st, range.x, first, min(first + seg.length, length), point_list,
+                               primitive_ids, geometry, appearance, opacities, x, y, tile_x,
+                               tile_y, near_plane, mscale, mnear, nullptr, w);
+      w.done = again ? w.done : finished;
+    }
+    // Checkpoint c_{k+1}: the prefix state after segment k (this thread's
+    // column only, so no other thread's slot is touched).
+    const float values[10] = {w.T,      w.out[0], w.out[1], w.out[2], w.out[4],
+                              w.out[5], w.out[6], w.out[7], w.m1,     w.m2};
+#pragma unroll
+    for (int q = 0; q < 10; ++q) c[q * kTilePixels] = values[q];
+  }
+  // Pack the segments' replay blocks (segment k's entries start at list
+  // position k * length) into one list. A block only moves left and never
+  // onto a later block, and every chunk is read in full before it is
+  // written, so no entry is overwritten before it is read.
+  int* n = seg.index + seg.tiles + base;
+  int packed = 0;
+  for (int k = 0; replay && k < pieces; ++k) {
+    const int count = n[k];
+    __syncthreads();  // every thread has read n[k] before thread 0 rewrites it
+    if (k > 0 && packed != k * seg.length) {
+      const int2* src = replay + range.x + k * seg.length;
+      int2* dst = replay + range.x + packed;
+      for (int chunk = 0; chunk < count; chunk += kTilePixels) {
+        const int i = chunk + int(threadIdx.x);
+        const int2 e = i < count ? src[i] : make_int2(0, 0);
+        __syncthreads();
+        if (i < count) dst[i] = e;
+      }
+    }
+    packed += count;
+    if (threadIdx.x == 0) n[k] = packed;  // replay length at checkpoint c_{k+1}
+  }
+  if (replay && threadIdx.x == 0) replay_counts[tile] = packed;
+  if (tp.inside) {
+#pragma unroll
+    for (int c = 0; c < 3; ++c) w.out[c] += w.T * backgrounds[tp.image * 3 + c];
+    w.out[3] = 1.f - w.T;
+#pragma unroll
+    for (int c = 0; c < kMaps; ++c) maps.data[map_group(c)][maps.offset(c, tp.pixel)] = w.out[c];
+    state[tp.pixel * 3 + 0] = w.T;
+    state[tp.pixel * 3 + 1] = w.m1;
+    state[tp.pixel * 3 + 2] = w.m2;
+    contributors[tp.pixel] = w.last;
+  }
 }
 
 // Appearance adjoint given dL/dcolor = gc. Writes the raw appearance
@@ -1187,9 +1432,9 @@ __global__ __launch_bounds__(kTilePixels, Neural ? 2 : 4) void renderBackward(
       constexpr int kSlot = kCheckpointFloats * kTilePixels;
       const float* c = seg.state + int64_t(base + piece.y) * kSlot + threadIdx.x;
       const float* f = seg.state + int64_t(base + pieces - 1) * kSlot + threadIdx.x;
-      float d[kCheckpointFloats];
+      float d[10];  // T, rgb, depth, normals, m1, m2
 #pragma unroll
-      for (int q = 0; q < kCheckpointFloats; ++q) d[q] = f[q * kTilePixels] - c[q * kTilePixels];
+      for (int q = 0; q < 10; ++q) d[q] = f[q * kTilePixels] - c[q * kTilePixels];
       T = c[0];
       suffix = go[0] * d[1] + go[1] * d[2] + go[2] * d[3] + go[4] * d[4] + go[5] * d[5] +
                go[6] * d[6] + go[7] * d[7] +
@@ -1449,18 +1694,18 @@ RenderWorkspace render_layout(void* base, int64_t tiles, int64_t segment_slots =
 
 // Checks the split-tile arguments and describes them (length 0: off).
 int make_segments(int32_t length, float* state, int32_t* index, int64_t capacity,
-                  const void* replay, int64_t tiles, Segments* seg) {
-  *seg = Segments{0, int(tiles), 0, nullptr, nullptr};
+                  int64_t tiles, Segments* seg) {
+  *seg = Segments{0, int(tiles), 0, nullptr, nullptr, nullptr};
   if (length == 0) return GS_OK;
   GS_REQUIRE(length > 0 && length % kBatch == 0, GS_ERR_ARGUMENT,
              "segment length must be a positive multiple of %d, got %d", kBatch, length);
-  GS_REQUIRE(replay, GS_ERR_ARGUMENT, "split tiles need the replay lists");
   GS_REQUIRE(state && index, GS_ERR_ARGUMENT, "null segment buffers");
   GS_REQUIRE(capacity > 0 && tiles + capacity <= INT_MAX &&
                  capacity <= INT64_MAX / (kCheckpointFloats * kTilePixels * 4),
              GS_ERR_OVERFLOW, "invalid segment capacity %lld for %lld tiles",
              static_cast<long long>(capacity), static_cast<long long>(tiles));
-  *seg = Segments{length, int(tiles), int(capacity), state, index};
+  *seg = Segments{length, int(tiles), int(capacity), state, index,
+                  reinterpret_cast<int2*>(index + segment_work_offset(tiles, capacity))};
   return GS_OK;
 }
 
@@ -1545,8 +1790,9 @@ int render_forward(int32_t neural, const float* geometry, const float* appearanc
   tile_order_kernel<<<1, kOrderBlock, 0, s>>>(nullptr, r, tiles, order, seg);
   GS_LAUNCHED("tile_order_kernel");
   int2* lists = reinterpret_cast<int2*>(replay);
+  const unsigned blocks = unsigned(seg.length ? tiles + seg.capacity : tiles);
   auto launch = [&](auto kernel) {
-    kernel<<<unsigned(tiles), kTilePixels, 0, s>>>(
+    kernel<<<blocks, kTilePixels, 0, s>>>(
         width, height, tw, th, geometry, appearance, opacities, primitive_ids, backgrounds,
         point_list, r, order, near_plane, far_plane, out, state, contributors, lists,
         replay_counts, seg);
@@ -1559,6 +1805,17 @@ int render_forward(int32_t neural, const float* geometry, const float* appearanc
     else launch(renderForward<false, false>);
   }
   GS_LAUNCHED("renderForward");
+  if (seg.length) {
+    auto merge = [&](auto kernel) {
+      kernel<<<unsigned(tiles), kTilePixels, 0, s>>>(
+          width, height, tw, th, geometry, appearance, opacities, primitive_ids, backgrounds,
+          point_list, r, near_plane, far_plane, out, state, contributors, lists, replay_counts,
+          seg);
+    };
+    if (neural) merge(mergeSegments<true>);
+    else merge(mergeSegments<false>);
+    GS_LAUNCHED("mergeSegments");
+  }
   return GS_OK;
 }
 
@@ -1619,7 +1876,7 @@ int gs_render_forward(int32_t neural, const float* geometry, const float* appear
   const int64_t tiles = images * tiles_x(width) * tiles_y(height);
   Segments seg;
   status = make_segments(segment_length, segment_state, segment_index, segment_capacity,
-                         replay, tiles, &seg);
+                         tiles, &seg);
   if (status != GS_OK) return status;
   const size_t need = gs_render_workspace_size(images, width, height);
   GS_REQUIRE(workspace && workspace_bytes >= need, GS_ERR_WORKSPACE,
@@ -1658,7 +1915,8 @@ int gs_render_forward_static(int32_t neural, const float* geometry, const float*
   return render_forward(neural, geometry, appearance, opacities, primitive_ids, backgrounds,
                         point_list, ranges, images, width, height, near_plane, far_plane,
                         map_groups(maps, map_strides), state, contributors, replay,
-                        replay_counts, order, Segments{0, int(tiles), 0, nullptr, nullptr}, s);
+                        replay_counts, order,
+                        Segments{0, int(tiles), 0, nullptr, nullptr, nullptr}, s);
 }
 
 int gs_render_backward(int32_t neural, const float* geometry, const float* appearance,
@@ -1688,9 +1946,10 @@ int gs_render_backward(int32_t neural, const float* geometry, const float* appea
   const int tiles = int(images * tw * th);
   Segments seg;
   status = make_segments(segment_length, const_cast<float*>(segment_state),
-                         const_cast<int32_t*>(segment_index), segment_capacity, replay, tiles,
-                         &seg);
+                         const_cast<int32_t*>(segment_index), segment_capacity, tiles, &seg);
   if (status != GS_OK) return status;
+  GS_REQUIRE(!seg.length || replay, GS_ERR_ARGUMENT,
+             "the backward of split tiles needs the replay lists");
   const size_t need =
       gs_render_backward_workspace_size(images, width, height, seg.length ? seg.capacity : 0);
   GS_REQUIRE(workspace && workspace_bytes >= need, GS_ERR_WORKSPACE,

@@ -355,22 +355,27 @@ int gs_render_forward(int32_t neural, const float* geometry, const float* appear
                       int64_t segment_capacity, void* workspace, size_t workspace_bytes,
                       void* stream);
 
-/* Split tiles (segment_length > 0, a multiple of 64; needs the replay
- * lists; 0 turns it off and the three buffers are ignored). No counterpart
- * in the reference, whose backward walks each tile in one thread block. A
- * tile whose point list is longer than segment_length records gets
- * K = ceil(length / segment_length) checkpoint slots, assigned in tile
- * order by the forward: segment_index [I*tw*th + segment_capacity] int32
- * receives each tile's first slot (-1: not split) and then, per slot, the
- * replay-list length at the slot's checkpoint; segment_state
- * [segment_capacity][10][256] float32 receives each checkpoint's per-pixel
- * prefix state (transmittance, rgb, depth, normals, and the two depth
- * moments) after every segment_length list records, the last slot holding
- * the final state. Slots past segment_capacity are not used (their tiles
- * are not split); sum over tiles of floor(2 length / segment_length) slots
- * always suffice. gs_render_backward, given the same arguments, then
- * replays each split tile's segments in separate workgroups, each from its
- * checkpoint, so a long list no longer runs on one compute unit. */
+/* Split tiles (segment_length > 0, a multiple of 64; 0 turns it off and
+ * the three buffers are ignored; the backward needs the replay lists). No counterpart
+ * in the reference, which walks each tile in one thread block. A tile whose
+ * point list is longer than segment_length records is split into
+ * K = ceil(length / segment_length) segments with K checkpoint slots,
+ * assigned in tile order. The forward walks every segment in its own
+ * workgroup, with the transmittance in front of it taken as 1, and a
+ * second kernel merges the segments per pixel in list order, in closed
+ * form, or by walking a segment again with the true transmittance where
+ * the 1e-4 stop rule falls inside it. The backward then replays each
+ * segment in its own workgroup from its checkpoint.
+ * segment_state [segment_capacity][13][256] float32 receives each
+ * checkpoint's per-pixel prefix state after every segment (transmittance,
+ * rgb, depth, normals and the two depth moments; the last slot of a tile
+ * holds its final state); segment_index int32 of length
+ * E + 2 * (I*tw*th + segment_capacity), E = I*tw*th + segment_capacity
+ * rounded up to even, receives each tile's first slot (-1: not split), then
+ * per slot the replay-list length at its checkpoint, then (from int E) the
+ * forward's work list. Slots past segment_capacity are not used (their
+ * tiles are not split); sum over tiles of floor(2 length / segment_length)
+ * slots always suffice. gs_render_backward takes the same arguments. */
 
 /* gs_render_forward without a workspace argument. No counterpart in the
  * reference: it is for callers that cannot allocate device memory (code

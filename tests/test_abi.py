@@ -63,8 +63,9 @@ def test_argument_errors_return_status_and_message():
     status = lib.gs_render_forward(*forward, None, 0, None, 100, dummy, dummy, 4, dummy, 1 << 20,
                                    None)
     assert status == 1 and b"multiple of 64" in lib.gs_last_error()
-    status = lib.gs_render_forward(*forward, None, 0, None, 64, dummy, dummy, 4, dummy, 1 << 20,
-                                   None)
+    backward = [0, *([dummy] * 7), dummy, dummy, None, None]
+    status = lib.gs_render_backward(*backward, 64, dummy, dummy, 4, maps, strides, 1, 16, 16,
+                                    0.5, 1.0, *([dummy] * 4), dummy, 1 << 20, None)
     assert status == 1 and b"replay lists" in lib.gs_last_error()
     status = lib.gs_render_forward(*forward, dummy, 10, dummy, 64, dummy, dummy, 0, dummy,
                                    1 << 20, None)
@@ -122,3 +123,22 @@ def test_ctypes_signatures_match_the_header():
             expected = _ctype_class(param)
             actual = classes.get(argtype, "pointer")
             assert expected == actual, (name, index, param, argtype)
+
+
+def test_split_policy():
+    """Split tiles: a fixed 64-record segment below 2048 image tiles, slots
+    enough for every tile longer than that (floor(2 M / 64)) up to the cap,
+    and an index buffer whose work list starts at an even offset."""
+    from diff_gabor_splatting_amd import _native
+
+    assert _native.split_length(16, 1000) == 64
+    assert _native.split_length(2047, 10**7) == 64  # independent of the count
+    assert _native.split_length(2048, 1000) == 0 and _native.split_length(16, 0) == 0
+    assert _native.split_slots(89_449, 64) == 2_795
+    assert _native.split_slots(10**8, 64) == _native.SPLIT_MAX_SLOTS
+    assert _native.split_slots(1000, 0) == 0
+    # A tile of L > 64 records needs ceil(L / 64) <= floor(2 L / 64) slots.
+    for length in range(65, 2000):
+        assert -(-length // 64) <= 2 * length // 64
+    assert _native.split_index_length(7, 10) == 18 + 34
+    assert _native.split_index_length(8, 10) == 18 + 36

@@ -110,8 +110,10 @@ def check_structure(point_list, ranges, contributors, lists, counts, width, heig
 def forward_both(args):
     from diff_gabor_splatting_amd import _native
 
-    plain = _native.rasterize_forward(*args)
-    replayed = _native.rasterize_forward(*args, replay=True)
+    # Unsplit tiles on both sides (split tiles, checked in test_gpu_split.py,
+    # are independent of the replay lists too).
+    plain = _native.rasterize_forward(*args, split=0)
+    replayed = _native.rasterize_forward(*args, replay=True, split=0)
     assert replayed[5] is not None
     for a, b in zip(plain, replayed[:5]):
         assert torch.equal(a, b)

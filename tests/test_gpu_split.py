@@ -1,10 +1,12 @@
-"""Split tiles: the backward replays long tile lists in segments, each from a
-checkpoint the forward wrote.
+"""Split tiles: long tile lists are composited in segments (one workgroup
+each, merged per pixel afterwards) and their backward replayed in segments,
+each from a checkpoint the merge wrote.
 
-* Forward outputs are bit-identical with and without split tiles (the
-  checkpoints are extra writes), and gradients agree with the unsplit
-  backward to float32 rounding (each segment's running suffix is derived
-  from prefix-sum differences instead of accumulated).
+* Maps agree with the unsplit forward to float32 rounding (merged segments
+  reassociate the sums) and the contributor counts are identical (the stop
+  rule is decided exactly); gradients agree with the unsplit backward to
+  float32 rounding (each segment's running suffix is derived from prefix-sum
+  differences instead of accumulated).
 * The checkpoint layout: slot bases in tile order for exactly the tiles
   longer than the segment length, non-decreasing replay lengths ending at
   the tile's replay count, and a last checkpoint equal to the saved state.
@@ -75,13 +77,19 @@ def test_split_backward_matches_unsplit(method, opacity, monkeypatch):
     tiles = seen[-1][2].shape[0]
     assert int((segments[2][:tiles] >= 0).sum()) > 0
     monkeypatch.setattr(_native, "SPLIT_MAX_TILES", 0)
+    split_contributors = seen[-1][4]
     plain_maps, plain_grads = run(method, values, weights, width, height)
     assert seen[-1][5][2] is None
-    assert torch.equal(split_maps, plain_maps)
+    assert torch.equal(split_contributors, seen[-1][4])
+    torch.testing.assert_close(split_maps, plain_maps, atol=2e-6, rtol=2e-5)
+    # Both sides round differently (atomic order, reassociated sums), as any
+    # float32 implementation does against the float64 oracle: the oracle's
+    # gradient bar, 1e-3 of the tensor's largest value, with a wrong term
+    # off by far more.
     for name, a, b in zip(values, split_grads, plain_grads):
         scale = float(b.abs().max())
         err = float((a - b).abs().max())
-        assert err <= 2e-4 * scale + 1e-12, f"{name}: max error {err:.3e}, scale {scale:.3e}"
+        assert err <= 1e-3 * scale + 1e-12, f"{name}: max error {err:.3e}, scale {scale:.3e}"
 
 
 @pytest.mark.parametrize("opacity", [0.3, 0.97])
@@ -134,9 +142,12 @@ def test_split_scene_matches_oracle(method, monkeypatch):
     segments = seen[-1][5][2]
     assert segments is not None and int((segments[2][:seen[-1][2].shape[0]] >= 0).sum()) > 0
     rest = {k: v for k, v in values.items() if k != "backgrounds"}
-    _, mask = fp32_conditioned(
+    oracle_maps, mask = fp32_conditioned(
         lambda backgrounds, **kw: ORACLE[method](**kw, backgrounds=backgrounds),
         {**rest, "backgrounds": values["backgrounds"]}, width=width, height=height)
+    assert float((~mask).float().mean()) <= 0.03
+    torch.testing.assert_close(actual.detach().cpu().double()[mask], oracle_maps[mask],
+                               atol=1e-5, rtol=1e-4)
     weights = torch.randn(actual.shape, generator=torch.Generator().manual_seed(4)) * mask[..., None]
     _, expected, sensitivity = oracle_reference(ORACLE[method], values, weights, width=width,
                                                 height=height)
@@ -145,3 +156,17 @@ def test_split_scene_matches_oracle(method, monkeypatch):
     for (name, v), g in zip(values.items(), grads):
         g = torch.zeros_like(v) if g is None else g
         assert_gradients_close(g, expected[name], name, sensitivity[name])
+
+
+@pytest.mark.parametrize("method", ["classic", "neural"])
+def test_forward_bits_do_not_depend_on_grad_mode(method):
+    """Tiles are split whether or not a backward follows (the replay lists
+    are only written when one can), so a render's maps are the same bits
+    with and without gradient recording."""
+    width, height = 40, 36
+    values = heavy_scene(method, 0.5, width=width, height=height)
+    with torch.no_grad():
+        frozen = maps_from_result(renderer(method)(**values, width=width, height=height))
+    recorded = maps_from_result(renderer(method)(**values, width=width, height=height))
+    assert recorded.requires_grad
+    assert torch.equal(frozen, recorded.detach())
