@@ -1050,7 +1050,7 @@ static_assert(kCheckpointFloats >= kSegmentResults, "a slot holds a segment's re
 // replay list, and mergeSegments completes the tile).
 // Replay: also write the tile's replay list (replay + range start, see
 // append_replay) and its length (replay_counts[tile]).
-template <bool Neural, bool Replay>
+template <bool Neural, bool Replay, bool Split>
 __global__ __launch_bounds__(kTilePixels, Neural ? 4 : 6) void renderForward(
     int width, int height, int tw, int th, const float* __restrict__ geometry,
     const float* __restrict__ appearance, const float* __restrict__ opacities,
@@ -1068,7 +1068,7 @@ __global__ __launch_bounds__(kTilePixels, Neural ? 4 : 6) void renderForward(
   __shared__ uint64_t wave_taken[kTilePixels / 64];
   const ForwardStage<Neural> st{rows, raw, reach_rows, ids, prims, wave_taken};
   // (tile, segment) of this workgroup; past the work count: nothing.
-  const int2 piece = seg.length > 0 ? seg.work[blockIdx.x] : make_int2(order[blockIdx.x], 0);
+  const int2 piece = Split ? seg.work[blockIdx.x] : make_int2(order[blockIdx.x], 0);
   if (piece.x < 0) return;
   const int tile = piece.x;
 #ifdef GS_DIAGNOSTICS
@@ -1082,7 +1082,7 @@ __global__ __launch_bounds__(kTilePixels, Neural ? 4 : 6) void renderForward(
   const int2 range = ranges[tile];
   const float mscale = far_plane / (far_plane - near_plane);
   const float mnear = mscale * near_plane;
-  const int base = seg.length > 0 ? seg.index[tile] : -1;
+  const int base = Split ? seg.index[tile] : -1;
   int first = 0, end = range.y - range.x;
   if (base >= 0) {
     first = piece.y * seg.length;
@@ -1093,7 +1093,7 @@ __global__ __launch_bounds__(kTilePixels, Neural ? 4 : 6) void renderForward(
   const int replay_n = walk_list<Neural, Replay>(
       st, range.x, first, end, point_list, primitive_ids, geometry, appearance, opacities, x, y,
       tile_x, tile_y, near_plane, mscale, mnear, replay + range.x + first, w);
-  if (base >= 0) {
+  if (Split && base >= 0) {
     // A segment of a split tile: its relative results and replay count.
     float* c = seg.state + int64_t(base + piece.y) * (kCheckpointFloats * kTilePixels) +
                threadIdx.x;
@@ -1797,12 +1797,22 @@ int render_forward(int32_t neural, const float* geometry, const float* appearanc
         point_list, r, order, near_plane, far_plane, out, state, contributors, lists,
         replay_counts, seg);
   };
-  if (neural) {
-    if (replay) launch(renderForward<true, true>);
-    else launch(renderForward<true, false>);
+  if (seg.length) {
+    if (neural) {
+      if (replay) launch(renderForward<true, true, true>);
+      else launch(renderForward<true, false, true>);
+    } else {
+      if (replay) launch(renderForward<false, true, true>);
+      else launch(renderForward<false, false, true>);
+    }
   } else {
-    if (replay) launch(renderForward<false, true>);
-    else launch(renderForward<false, false>);
+    if (neural) {
+      if (replay) launch(renderForward<true, true, false>);
+      else launch(renderForward<true, false, false>);
+    } else {
+      if (replay) launch(renderForward<false, true, false>);
+      else launch(renderForward<false, false, false>);
+    }
   }
   GS_LAUNCHED("renderForward");
   if (seg.length) {
