@@ -29,6 +29,8 @@ import time
 
 import torch
 
+from diff_gabor_splatting_amd.timing import paused_collector
+
 HBM_PEAK_GBS = 8000.0
 COPY_BYTES = 1 << 30
 FP32_VALU_PEAK_TFLOPS = 157.3
@@ -214,15 +216,17 @@ def prepare(index: int, device, validate: bool):
 
 def time_steps(step, steps: int, warmup: int) -> float:
     """Milliseconds per step over `steps` steps after `warmup` untimed ones,
-    with the device synchronised on both sides of the timed region."""
+    with the device synchronised on both sides of the timed region and the
+    garbage collector paused inside it."""
     for _ in range(warmup):
         step()
     torch.cuda.synchronize()
-    start = time.perf_counter()
-    for _ in range(steps):
-        step()
-    torch.cuda.synchronize()
-    return (time.perf_counter() - start) * 1000 / steps
+    with paused_collector():
+        start = time.perf_counter()
+        for _ in range(steps):
+            step()
+        torch.cuda.synchronize()
+        return (time.perf_counter() - start) * 1000 / steps
 
 
 def per_config_times(skip: int, steps: int, warmup: int, device, validate: bool) -> dict:

@@ -16,7 +16,9 @@ of the two can be read side by side; everything else is this library's:
   tensor's scale and norm - and records the worst errors in the report;
 * steps are timed with HIP events on the launch stream
   (``timing.time_phases``): forward (rendering and the scalar loss) and
-  backward;
+  backward, with the garbage collector paused over the measured steps (a
+  collection of the interpreter's heap, about 40 ms, otherwise lands in a
+  step now and then and dominates the per-camera loop's mean);
 * the optional kernel split comes from the library's own per-family event
   counters (``gs_profile_enable``), in a separate pass.
 

@@ -9,10 +9,31 @@ can be split into phases (forward, backward) without synchronising inside it.
 
 from __future__ import annotations
 
+import contextlib
+import gc
 import statistics
-from typing import Callable
+from typing import Callable, Iterator
 
 import torch
+
+
+@contextlib.contextmanager
+def paused_collector() -> Iterator[None]:
+    """Run a full garbage collection, then keep the collector off until the
+    block ends. With torch loaded the interpreter tracks about 170k objects,
+    and a generation-2 collection of them takes about 40 ms of host time; one
+    that lands inside a timed step stalls the launches behind it and
+    inflates that step's time by the same amount. The timed blocks create
+    no reference cycles worth collecting, so pausing the collector there
+    leaks nothing."""
+    enabled = gc.isenabled()
+    gc.collect()
+    gc.disable()
+    try:
+        yield
+    finally:
+        if enabled:
+            gc.enable()
 
 
 class PhaseClock:
@@ -41,21 +62,23 @@ def time_phases(step: Callable[[PhaseClock], None], warmup: int, iterations: int
     """Run ``step`` ``warmup`` times untimed, then ``iterations`` times with a
     fresh clock each; ``step`` marks "start" first and then the end of each
     of its phases. ``before`` (e.g. clearing gradients) runs ahead of every
-    step, outside the marks. Returns each phase's milliseconds per
-    iteration."""
+    step, outside the marks. The collector is paused over the measured
+    iterations (:func:`paused_collector`). Returns each phase's milliseconds
+    per iteration."""
     for _ in range(warmup):
         if before is not None:
             before()
         step(PhaseClock())
     torch.cuda.synchronize()
     samples: dict[str, list[float]] = {}
-    for _ in range(iterations):
-        if before is not None:
-            before()
-        clock = PhaseClock()
-        step(clock)
-        for name, ms in clock.phases().items():
-            samples.setdefault(name, []).append(ms)
+    with paused_collector():
+        for _ in range(iterations):
+            if before is not None:
+                before()
+            clock = PhaseClock()
+            step(clock)
+            for name, ms in clock.phases().items():
+                samples.setdefault(name, []).append(ms)
     return samples
 
 

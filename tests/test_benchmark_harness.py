@@ -32,6 +32,25 @@ def test_nonpositive_sizes_are_rejected(flag):
         harness.parse_workload([flag, "0"])
 
 
+def test_timed_regions_pause_the_garbage_collector():
+    import gc
+
+    from diff_gabor_splatting_amd.timing import paused_collector
+
+    was = gc.isenabled()
+    try:
+        gc.enable()
+        with paused_collector():
+            assert not gc.isenabled()
+        assert gc.isenabled()
+        gc.disable()
+        with paused_collector():
+            pass
+        assert not gc.isenabled()  # a caller's own pause is kept
+    finally:
+        (gc.enable if was else gc.disable)()
+
+
 @pytest.mark.parametrize("flag", ["--warmup-iterations", "--profile-iterations"])
 def test_negative_counts_are_rejected(flag):
     with pytest.raises(SystemExit):
