@@ -5,11 +5,18 @@ bindings.cpp:5-10``): ``rasterize_forward``, ``rasterize_backward``,
 ``evaluate_sh_forward`` and ``evaluate_sh_backward``. This module exposes the
 same names, argument meaning and error behaviour (structural violations raise
 ``RuntimeError`` like ``TORCH_CHECK``), implemented by allocating outputs with
-the torch caching allocator and calling ``libgabor_hip.so`` through ctypes on
-the current HIP stream. It adds the projection operators (the reference runs
-projection as PyTorch ops) and visible-pair packing.
+the torch caching allocator and calling ``libgabor_hip.so`` on the current
+HIP stream. It adds the projection operators (the reference runs projection
+as PyTorch ops) and visible-pair packing.
 
-The library is loaded at import; there is no fallback path.
+The functions a render calls - the record front end, value checks, binning,
+the compositor operators and their accumulators - are implemented in C++
+(``csrc/host.cpp``, the ``_host`` extension module, as the reference's host
+functions are); here they only keep their Python signatures and docstrings.
+The rest call the C ABI through ctypes. Both reach the library loaded here:
+the extension receives its entry point addresses at load.
+
+The library and the extension are loaded at import; there is no fallback path.
 """
 
 from __future__ import annotations
@@ -193,6 +200,16 @@ PROFILE_FAMILIES = {
 }
 
 
+try:
+    from . import _host
+except ImportError as error:
+    raise ImportError(
+        "the _host extension (csrc/host.cpp) is not built; run `python -m "
+        "diff_gabor_splatting_amd.build` (or __graft_entry__.build()) first. There is no "
+        "Python fallback."
+    ) from error
+
+
 def _load(path: Path = _LIBRARY_PATH) -> ctypes.CDLL:
     if not path.exists():
         raise ImportError(
@@ -207,7 +224,14 @@ def _load(path: Path = _LIBRARY_PATH) -> ctypes.CDLL:
     return library
 
 
+def _bind_host(library: ctypes.CDLL) -> None:
+    """Hand the extension the addresses of the entry points it calls."""
+    _host.bind({name: ctypes.cast(getattr(library, name), ctypes.c_void_p).value
+                for name in _host.entry_points()})
+
+
 lib = _load()
+_bind_host(lib)
 
 
 def use_library(path: Path) -> None:
@@ -217,6 +241,7 @@ def use_library(path: Path) -> None:
     running from the library that launched them."""
     global lib
     lib = _load(Path(path))
+    _bind_host(lib)
 
 
 def exported_symbols() -> list[str]:
@@ -397,21 +422,7 @@ def bin_order(geometry: torch.Tensor, radii: torch.Tensor, image_ids: torch.Tens
     """Depth-first binning, stage 1: (order int32 [Q], starts int64 [Q], rects
     int32 [Q, 4], totals int64 [2] on the device = (M, V): the intersection
     count and the number of pairs with tiles). No host synchronisation."""
-    device = geometry.device
-    count = geometry.size(0)
-    order = torch.empty(count, dtype=torch.int32, device=device)
-    starts = torch.empty(count, dtype=torch.int64, device=device)
-    rects = torch.empty((count, 4), dtype=torch.int32, device=device)
-    totals = torch.empty(2, dtype=torch.int64, device=device)
-    workspace = _workspace(lib.gs_bin_order_workspace_size(count), device)
-    _check(
-        lib.gs_bin_order(
-            _ptr(geometry), _ptr(radii), _ptr(image_ids), count, width, height, _ptr(order),
-            _ptr(starts), _ptr(rects), _ptr(totals), _ptr(totals[1:]), _ptr(workspace),
-            workspace.numel(), _stream(device),
-        )
-    )
-    return order, starts, rects, totals
+    return _host.bin_order(geometry, radii, image_ids, width, height)
 
 
 def bin_tiles(order, starts, rects, images, width, height, intersections, visible=-1,
@@ -423,20 +434,8 @@ def bin_tiles(order, starts, rects, images, width, height, intersections, visibl
     fits. ``status`` (an int32 [1] device tensor, or None) receives the
     BINNING_* bits: BINNING_BAD_INDEX when a sort output failed its range
     check (see gs_bin_tiles)."""
-    device = order.device
-    count = order.size(0)
-    tw, th = tile_grid(width, height)
-    point_list = torch.empty(intersections, dtype=torch.int32, device=device)
-    ranges = torch.empty((images * tw * th, 2), dtype=torch.int32, device=device)
-    workspace = _workspace(lib.gs_bin_tiles_workspace_size(intersections), device)
-    _check(
-        lib.gs_bin_tiles(
-            _ptr(order), _ptr(starts), _ptr(rects), count, intersections, visible, images, width,
-            height, _ptr(point_list), _ptr(ranges), _ptr(status), _ptr(workspace),
-            workspace.numel(), _stream(device),
-        )
-    )
-    return point_list, ranges
+    return _host.bin_tiles(order, starts, rects, images, width, height, intersections, visible,
+                           status)
 
 
 def bin_tiles_bounded(order, starts, rects, images, width, height, capacity, intersections):
@@ -445,21 +444,8 @@ def bin_tiles_bounded(order, starts, rects, images, width, height, capacity, int
     live count `intersections` (int64 [1] on the device). Returns (point_list, ranges, overflow) with overflow an
     int32 [1] device word of BINNING_* bits: BINNING_OVERFLOW when M
     exceeded the capacity, BINNING_BAD_INDEX as in bin_tiles."""
-    device = order.device
-    count = order.size(0)
-    tw, th = tile_grid(width, height)
-    point_list = torch.empty(capacity, dtype=torch.int32, device=device)
-    ranges = torch.empty((images * tw * th, 2), dtype=torch.int32, device=device)
-    overflow = torch.empty(1, dtype=torch.int32, device=device)
-    workspace = _workspace(lib.gs_bin_tiles_workspace_size(capacity), device)
-    _check(
-        lib.gs_bin_tiles_bounded(
-            _ptr(order), _ptr(starts), _ptr(rects), count, capacity, _ptr(intersections),
-            images, width, height, _ptr(point_list), _ptr(ranges), _ptr(overflow),
-            _ptr(workspace), workspace.numel(), _stream(device),
-        )
-    )
-    return point_list, ranges, overflow
+    return _host.bin_tiles_bounded(order, starts, rects, images, width, height, capacity,
+                                   intersections)
 
 
 def bin_depth_first(geometry, radii, image_ids, images, width, height, overlap=None,
@@ -476,33 +462,8 @@ def bin_depth_first(geometry, radii, image_ids, images, width, height, overlap=N
     tensors, for the caller to fold into its own records. ``violations`` (a device
     int32 word of gs_check_values and a function that raises for a nonzero
     word) is read back with M and reported before M is checked or used."""
-    order, starts, rects, totals = bin_order(geometry, radii, image_ids, width, height)
-    total = totals[:1]
-    if capacity is not None:
-        if overlap is not None:
-            overlap()
-        point_list, ranges, overflow = bin_tiles_bounded(
-            order, starts, rects, images, width, height, capacity, total
-        )
-        if flags is not None:
-            flags(overflow, total)
-        return point_list, ranges
-    stream = torch.cuda.current_stream(geometry.device)
-    host = torch.empty(2, dtype=torch.int64, pin_memory=True)
-    host.copy_(totals, non_blocking=True)
-    if violations is not None:
-        word = torch.empty(1, dtype=torch.int32, pin_memory=True)
-        word.copy_(violations[0], non_blocking=True)
-    ready = torch.cuda.Event()
-    ready.record(stream)
-    if overlap is not None:
-        overlap()
-    ready.synchronize()
-    if violations is not None:
-        violations[1](int(word[0]))
-    intersections, visible = int(host[0]), int(host[1])
-    check_intersections(intersections)
-    return bin_tiles(order, starts, rects, images, width, height, intersections, visible)
+    return _host.bin_depth_first(geometry, radii, image_ids, images, width, height, overlap,
+                                 capacity, flags, violations)
 
 
 def pack_visible(radii: torch.Tensor, with_rows: bool = False, sync: bool = True):
@@ -512,29 +473,20 @@ def pack_visible(radii: torch.Tensor, with_rows: bool = False, sync: bool = True
     every pair or -1). With ``sync=False`` nothing is read back: the indices
     keep one entry per pair (those past the visible count V undefined) and
     V, a device int64 tensor of one element, is returned last."""
-    device = radii.device
-    flat = radii.reshape(-1)
-    count = flat.numel()
-    selected = torch.empty(max(count, 1), dtype=torch.int64, device=device)
-    rows = torch.empty(max(count, 1), dtype=torch.int32, device=device) if with_rows else None
-    total = torch.empty(1, dtype=torch.int64, device=device)
-    workspace = _workspace(lib.gs_scan_workspace_size(count), device)
-    _check(
-        lib.gs_pack_visible(
-            _ptr(flat), count, _ptr(selected), _ptr(rows), _ptr(total), _ptr(workspace),
-            workspace.numel(), _stream(device),
-        )
-    )
-    if not sync:
-        return (selected[:count], rows[:count], total) if with_rows else (selected[:count], total)
-    selected = selected[: int(total.item())]
-    return (selected, rows[:count]) if with_rows else selected
+    return _host.pack_visible(radii, with_rows, sync)
 
 
 # --------------------------------------------------------------------------
 # Input value contracts (rendering.py:88-153).
 
 CHECK_MAX_TENSORS = 16
+
+
+def check_tensors(tensors: dict, device: torch.device) -> None:
+    """Require every ``name: (value, shape)`` entry to be a contiguous float32
+    tensor of exactly that shape on ``device``: TypeError for a non-tensor,
+    ValueError otherwise, naming the first entry that fails."""
+    _host.check_tensors(tensors, device)
 
 
 def check_values(tensors, quaternions, scales, opacities, view_matrices, intrinsics,
@@ -551,36 +503,8 @@ def check_values(tensors, quaternions, scales, opacities, view_matrices, intrins
 def check_values_word(tensors, quaternions, scales, opacities, view_matrices, intrinsics,
                       weights=None, magnitudes=None) -> torch.Tensor:
     """check_values without the read-back: the int32 [1] device word."""
-    _require(len(tensors) <= CHECK_MAX_TENSORS, "too many tensors to check")
-    surfels = quaternions.numel() // 4
-    images = view_matrices.numel() // 16
-    inputs = [*tensors, quaternions, scales, opacities, view_matrices, intrinsics]
-    for value in inputs + [v for v in (weights, magnitudes) if v is not None]:
-        _check_float(value, quaternions)
-    _require(
-        quaternions.numel() == 4 * surfels and scales.numel() == 2 * surfels
-        and opacities.numel() == surfels
-        and all(v is None or v.numel() == 4 * surfels for v in (weights, magnitudes)),
-        "surfel tensors disagree in size",
-    )
-    _require(
-        view_matrices.numel() == 16 * images and intrinsics.numel() == 9 * images,
-        "camera tensors disagree in size",
-    )
-    count = len(tensors)
-    pointers = (_c_ptr * max(count, 1))(*[t.data_ptr() for t in tensors])
-    sizes = (_c_i64 * max(count, 1))(*[t.numel() for t in tensors])
-    device = quaternions.device
-    with torch.cuda.device(device):
-        violations = torch.empty(1, dtype=torch.int32, device=device)
-        _check(
-            lib.gs_check_values(
-                pointers, sizes, count, _ptr(quaternions), _ptr(scales), _ptr(opacities),
-                _ptr(weights), _ptr(magnitudes), surfels, _ptr(view_matrices), _ptr(intrinsics),
-                images, _ptr(violations), _stream(device),
-            )
-        )
-    return violations
+    return _host.check_values_word(list(tensors), quaternions, scales, opacities, view_matrices,
+                                   intrinsics, weights, magnitudes)
 
 
 # --------------------------------------------------------------------------
@@ -606,66 +530,9 @@ def records_forward(means, quaternions, scales, opacities, view_matrices, intrin
     and selected (packed pair indices or None), plus appearance [Q,18] and
     opacity_rows [Q] with SH.
     """
-    device = means.device
-    scenes, n = means.shape[:2]
-    cameras = view_matrices.shape[1]
-    pairs = scenes * cameras * n
-    first, second = sh if sh is not None else (None, None)
-    weights, magnitudes, phases = shared if shared is not None else (None, None, None)
-    degree = -1 if sh_degree is None else int(sh_degree)
-
-    def launch(row_of_pair, dense_radii, out):
-        _check(
-            lib.gs_records_forward(
-                _ptr(means), _ptr(quaternions), _ptr(scales), _ptr(opacities),
-                _ptr(view_matrices), _ptr(intrinsics), _ptr(first), _ptr(second),
-                _ptr(weights), _ptr(magnitudes), _ptr(phases), degree, scenes, cameras, n,
-                width, height, near_plane, far_plane, _ptr(row_of_pair), _ptr(dense_radii),
-                _ptr(out.get("geometry")), _ptr(out.get("projected_means")),
-                _ptr(out.get("row_radii")), _ptr(out.get("primitive_ids")),
-                _ptr(out.get("image_ids")), _ptr(out.get("appearance")),
-                _ptr(out.get("opacity_rows")), _ptr(out.get("scene_ids")),
-                _ptr(out.get("camera_ids")), _ptr(out.get("surfel_ids")), _stream(device),
-            )
-        )
-
-    with torch.cuda.device(device):
-        dense_radii = torch.empty((scenes, cameras, n), dtype=torch.int32, device=device)
-        row_of_pair = selected = None
-        padded = packed and fixed_rows
-        if packed:
-            launch(None, dense_radii, {})
-            if padded:
-                selected, row_of_pair, _ = pack_visible(dense_radii, with_rows=True, sync=False)
-            else:
-                selected, row_of_pair = pack_visible(dense_radii, with_rows=True)
-            rows = selected.numel()
-        else:
-            rows = pairs
-        f32 = dict(dtype=torch.float32, device=device)
-        # Padded rows past the visible count are never written by the record
-        # kernel: they are filled here so that binning culls them and the
-        # meta outputs stay defined.
-        fill = torch.zeros if padded else torch.empty
-        out = {
-            "geometry": torch.empty((rows, GEOMETRY_SIZE), **f32),
-            "projected_means": fill((rows, 2), **f32),
-            "row_radii": fill(rows, dtype=torch.int32, device=device),
-            "primitive_ids": torch.empty(rows, dtype=torch.int64, device=device),
-            "image_ids": torch.empty(rows, dtype=torch.int64, device=device),
-        }
-        if degree >= 0:
-            out["appearance"] = torch.empty((rows, 18), **f32)
-            out["opacity_rows"] = torch.empty(rows, **f32)
-        if padded:
-            meta_ids = torch.full((3, rows), -1, dtype=torch.int64, device=device)
-        else:
-            meta_ids = torch.empty((3, rows), dtype=torch.int64, device=device)
-        out.update(scene_ids=meta_ids[0], camera_ids=meta_ids[1], surfel_ids=meta_ids[2])
-        if rows:
-            launch(row_of_pair, None if packed else dense_radii, out)
-    out.update(dense_radii=dense_radii, row_of_pair=row_of_pair, selected=selected)
-    return out
+    return _host.records_forward(means, quaternions, scales, opacities, view_matrices, intrinsics,
+                                 sh, shared, sh_degree, width, height, near_plane, far_plane,
+                                 packed, fixed_rows)
 
 
 def records_backward(means, quaternions, scales, view_matrices, intrinsics, sh, sh_degree,
@@ -673,56 +540,9 @@ def records_backward(means, quaternions, scales, view_matrices, intrinsics, sh, 
                      grad_appearance, grad_opacity_rows):
     """Gradients of (means, quaternions, scales, view_matrices, intrinsics) and,
     with SH, of (first, second, weights, magnitudes, phases, opacities)."""
-    device = means.device
-    scenes, n = means.shape[:2]
-    cameras = view_matrices.shape[1]
-    degree = -1 if sh_degree is None else int(sh_degree)
-    first, second = sh if sh is not None else (None, None)
-
-    def contiguous(value):
-        return None if value is None else value.contiguous()
-
-    grad_geometry = contiguous(grad_geometry)
-    # The compositor's gradient of the projected means is the xy columns of
-    # its geometry gradient; rows of any stride are read in place.
-    if grad_projected_means is not None and not (
-        grad_projected_means.dim() == 2 and grad_projected_means.stride(1) == 1
-        and grad_projected_means.stride(0) >= 2
-    ):
-        grad_projected_means = grad_projected_means.contiguous()
-    projected_stride = 2 if grad_projected_means is None else grad_projected_means.stride(0)
-    grad_appearance = contiguous(grad_appearance)
-    grad_opacity_rows = contiguous(grad_opacity_rows)
-    with torch.cuda.device(device):
-        g_means = torch.empty_like(means)
-        g_quats = torch.empty_like(quaternions)
-        g_scales = torch.empty_like(scales)
-        g_views = torch.empty_like(view_matrices)
-        g_intrinsics = torch.empty_like(intrinsics)
-        sh_grads = [None] * 6
-        if degree >= 0:
-            if grad_appearance is None:
-                grad_appearance = torch.zeros((geometry.shape[0], 18), dtype=torch.float32,
-                                              device=device)
-            sh_grads = [torch.empty_like(first), torch.empty_like(second)] + [
-                torch.empty((scenes, n, 4), dtype=torch.float32, device=device) for _ in range(3)
-            ] + [torch.empty((scenes, n), dtype=torch.float32, device=device)]
-        workspace = _workspace(
-            lib.gs_records_backward_workspace_size(scenes, cameras, n, degree), device
-        )
-        _check(
-            lib.gs_records_backward(
-                _ptr(means), _ptr(quaternions), _ptr(scales), _ptr(view_matrices),
-                _ptr(intrinsics), _ptr(first), _ptr(second), degree, scenes, cameras, n,
-                _ptr(row_of_pair), _ptr(geometry), _ptr(grad_geometry),
-                _ptr(grad_projected_means), projected_stride, _ptr(grad_appearance),
-                _ptr(grad_opacity_rows),
-                _ptr(g_means), _ptr(g_quats), _ptr(g_scales), _ptr(g_views), _ptr(g_intrinsics),
-                *(_ptr(t) for t in sh_grads), _ptr(workspace), workspace.numel(),
-                _stream(device),
-            )
-        )
-    return (g_means, g_quats, g_scales, g_views, g_intrinsics, *sh_grads)
+    return _host.records_backward(means, quaternions, scales, view_matrices, intrinsics, sh,
+                                  sh_degree, row_of_pair, geometry, grad_geometry,
+                                  grad_projected_means, grad_appearance, grad_opacity_rows)
 
 
 # --------------------------------------------------------------------------
@@ -758,11 +578,6 @@ def _flat_pixel_stride(t: torch.Tensor):
                 return None
         inner *= size
     return (0 if stride is None else stride), (strides[-1] if k > 1 else 0)
-
-
-def _pixel_strided(t: torch.Tensor) -> torch.Tensor:
-    """t itself when its pixels are uniformly strided, else a contiguous copy."""
-    return t if _flat_pixel_stride(t) is not None else t.contiguous()
 
 
 def _map_group_args(groups, what: str):
@@ -811,98 +626,19 @@ def rasterize_forward(
     SPLIT_MAX_TILES tiles are split, whether or not a backward follows). ``violations`` (an addition): a pending value
     check, raised with the read-back of M (see bin_depth_first).
     """
-    _check_buffers(geometry, appearance, opacities, primitive_ids, backgrounds, neural)
-    _require(
-        0 < width < INT_MAX - TILE and 0 < height < INT_MAX - TILE, "invalid image dimensions"
+    return _host.rasterize_forward(
+        geometry, appearance, opacities, primitive_ids, image_ids, radii, backgrounds, width,
+        height, neural, near_plane, far_plane, outputs, overlap, capacity, flags, replay,
+        violations, -1 if split is None else int(split), SPLIT_MAX_TILES, SPLIT_LENGTH,
+        SPLIT_MAX_SLOTS,
     )
-    _require(near_plane > 0 and far_plane > near_plane, "invalid clipping planes")
-    _require(
-        image_ids.device == geometry.device
-        and image_ids.is_contiguous()
-        and image_ids.dtype == torch.int64
-        and image_ids.dim() == 1
-        and image_ids.size(0) == geometry.size(0),
-        "invalid image IDs",
-    )
-    _require(
-        radii.device == geometry.device
-        and radii.is_contiguous()
-        and radii.dtype == torch.int32
-        and radii.dim() == 1
-        and radii.size(0) == geometry.size(0),
-        "invalid radii",
-    )
-    device = geometry.device
-    with torch.cuda.device(device):
-        stream = _stream(device)
-        count = geometry.size(0)
-        images = backgrounds.size(0)
-        tw, th = tile_grid(width, height)
-        check_image_tiles(images, width, height)
-        tiles = images * tw * th
-        state = torch.empty((images, height, width, 3), dtype=torch.float32, device=device)
-        contributors = torch.empty((images, height, width), dtype=torch.int32, device=device)
-        point_list, ranges = bin_depth_first(geometry, radii, image_ids, images, width, height,
-                                             overlap, capacity, flags, violations)
-        if outputs is None:
-            maps = torch.empty((images, height, width, MAP_SIZE), dtype=torch.float32,
-                               device=device)
-            groups = split_map_groups(maps)
-        else:
-            groups = list(outputs)
-            _require(
-                len(groups) == len(MAP_GROUPS)
-                and all(
-                    t.shape == (images, height, width, k) and t.dtype == torch.float32
-                    and t.device == device
-                    for t, k in zip(groups, MAP_GROUPS)
-                ),
-                "invalid map outputs",
-            )
-            maps = tuple(groups)
-        data, strides = _map_group_args(groups, "map outputs")
-        lists = None
-        length = split_length(tiles, point_list.numel()) if split is None else int(split)
-        slots = split_slots(point_list.numel(), length)
-        segment_state = segment_index = None
-        if slots:
-            segment_state = torch.empty((slots, CHECKPOINT_FLOATS, TILE * TILE),
-                                        dtype=torch.float32, device=device)
-            segment_index = torch.empty(split_index_length(tiles, slots), dtype=torch.int32,
-                                        device=device)
-        else:
-            length = 0
-        if replay and point_list.numel() < REPLAY_MAX_ENTRIES:
-            lists = (torch.empty((max(point_list.numel(), 1), 2), dtype=torch.int32,
-                                 device=device),
-                     torch.empty(tiles, dtype=torch.int32, device=device),
-                     (length, segment_state, segment_index) if slots else None)
-        workspace = _workspace(lib.gs_render_workspace_size(images, width, height), device)
-        _check(
-            lib.gs_render_forward(
-                int(bool(neural)), _ptr(geometry), _ptr(appearance), _ptr(opacities),
-                _ptr(primitive_ids), _ptr(backgrounds), _ptr(point_list), _ptr(ranges), images,
-                width, height, near_plane, far_plane, data, strides, _ptr(state),
-                _ptr(contributors), _ptr(lists and lists[0]), point_list.numel(),
-                _ptr(lists and lists[1]), length, _ptr(segment_state), _ptr(segment_index),
-                slots, _ptr(workspace), workspace.numel(), stream,
-            )
-        )
-    if replay:
-        return [maps, point_list, ranges, state, contributors, lists]
-    return [maps, point_list, ranges, state, contributors]
 
 
 def zero_accumulators(geometry, appearance, opacities, backgrounds, shared=True):
     """Zeroed gradient accumulators for rasterize_backward: with ``shared``,
     contiguous views of one allocation cleared by one fill; else four
     separate tensors (for callers that must not return aliased tensors)."""
-    like = (geometry, appearance, opacities, backgrounds)
-    if not shared:
-        return tuple(torch.zeros_like(t) for t in like)
-    sizes = [t.numel() for t in like]
-    flat = torch.zeros(sum(sizes), dtype=torch.float32, device=geometry.device)
-    return tuple(part.view(t.shape) for part, t in zip(flat.split(sizes), like))
+    return _host.zero_accumulators(geometry, appearance, opacities, backgrounds, shared)
 
 
 def rasterize_backward(
@@ -921,82 +657,11 @@ def rasterize_backward(
     ``replay`` (an addition): the replay lists returned by rasterize_forward
     (or None); the gradients are the same, computed from fewer records.
     """
-    _check_buffers(geometry, appearance, opacities, primitive_ids, backgrounds, neural)
-    device = geometry.device
-    images = backgrounds.size(0)
-    if isinstance(grad_maps, torch.Tensor):
-        _check_float(grad_maps, geometry)
-        _require(grad_maps.shape == (images, height, width, MAP_SIZE), "invalid map gradient")
-        groups = split_map_groups(grad_maps)
-    else:
-        groups = list(grad_maps)
-        _require(
-            len(groups) == len(MAP_GROUPS)
-            and all(
-                g is None or (g.shape == (images, height, width, k) and g.dtype == torch.float32
-                              and g.device == device)
-                for g, k in zip(groups, MAP_GROUPS)
-            ),
-            "invalid map gradient",
-        )
-    _require(
-        state.shape == (images, height, width, 3)
-        and contributors.shape == (images, height, width),
-        "invalid saved compositor state",
+    return _host.rasterize_backward(
+        geometry, appearance, opacities, primitive_ids, backgrounds, point_list, ranges, state,
+        contributors, grad_maps, width, height, neural, near_plane, far_plane, accumulators,
+        replay,
     )
-    length, slots, segment_state, segment_index = 0, 0, None, None
-    if replay is not None:
-        tw, th = tile_grid(width, height)
-        lists, counts, *rest = replay
-        segments = rest[0] if rest else None
-        if segments is not None:
-            length, segment_state, segment_index = segments
-            slots = segment_state.shape[0]
-            _require(
-                segment_state.dtype == torch.float32 and segment_index.dtype == torch.int32
-                and segment_state.device == device and segment_index.device == device
-                and segment_state.is_contiguous() and segment_index.is_contiguous()
-                and segment_state.shape[1:] == (CHECKPOINT_FLOATS, TILE * TILE)
-                and segment_index.shape == (split_index_length(images * tw * th, slots),),
-                "invalid split-tile checkpoints",
-            )
-        _require(
-            lists.dtype == torch.int32 and counts.dtype == torch.int32
-            and lists.device == device and counts.device == device
-            and lists.is_contiguous() and counts.is_contiguous()
-            and lists.dim() == 2 and lists.size(1) == 2
-            and lists.size(0) >= point_list.numel()
-            and counts.shape == (images * tw * th,),
-            "invalid replay lists",
-        )
-    with torch.cuda.device(device):
-        if accumulators is None:
-            accumulators = zero_accumulators(geometry, appearance, opacities, backgrounds,
-                                             shared=False)
-        gg, ga, go, gb = accumulators
-        _require(
-            gg.shape == geometry.shape and ga.shape == appearance.shape
-            and go.shape == opacities.shape and gb.shape == backgrounds.shape
-            and all(t.is_contiguous() and t.dtype == torch.float32 and t.device == device
-                    for t in accumulators),
-            "invalid gradient accumulators",
-        )
-        groups = [g if g is None else _pixel_strided(g) for g in groups]
-        data, strides = _map_group_args(groups, "map gradients")
-        workspace = _workspace(
-            lib.gs_render_backward_workspace_size(images, width, height, slots), device)
-        _check(
-            lib.gs_render_backward(
-                int(bool(neural)), _ptr(geometry), _ptr(appearance), _ptr(opacities),
-                _ptr(primitive_ids), _ptr(backgrounds), _ptr(point_list), _ptr(ranges),
-                _ptr(state), _ptr(contributors), _ptr(replay and replay[0]),
-                _ptr(replay and replay[1]), length, _ptr(segment_state), _ptr(segment_index),
-                slots, data, strides, images, width, height,
-                near_plane, far_plane, _ptr(gg), _ptr(ga), _ptr(go), _ptr(gb),
-                _ptr(workspace), workspace.numel(), _stream(device),
-            )
-        )
-    return [gg, ga, go, gb]
 
 
 # --------------------------------------------------------------------------

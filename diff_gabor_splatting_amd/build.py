@@ -9,7 +9,13 @@ library links the HIP runtime by its SONAME (``libamdhip64.so.7``), so when it
 is loaded after ``import torch`` it binds to the runtime torch already loaded
 and shares torch's streams and allocations.
 
-Run ``python -m diff_gabor_splatting_amd.build`` or call :func:`build_library`.
+The renderer's host functions (``csrc/host.cpp``) are a Python extension
+module, ``diff_gabor_splatting_amd/_host*.so``, compiled with the host C++
+compiler against the installed torch (:func:`build_host`); it calls the HIP
+library's C ABI through function addresses handed over at import.
+
+Run ``python -m diff_gabor_splatting_amd.build`` or call :func:`build_library`
+and :func:`build_host`.
 """
 
 from __future__ import annotations
@@ -19,6 +25,7 @@ import os
 import shutil
 import subprocess
 import sys
+import sysconfig
 from pathlib import Path
 
 PACKAGE_DIR = Path(__file__).resolve().parent
@@ -28,6 +35,9 @@ INCLUDE_DIR = REPO_DIR / "include"
 BUILD_DIR = REPO_DIR / "_build"
 LIBRARY = PACKAGE_DIR / "libgabor_hip.so"
 DIAGNOSTICS_LIBRARY = PACKAGE_DIR / "libgabor_hip_diag.so"
+HOST_SOURCE = SOURCE_DIR / "host.cpp"
+HOST_EXTENSION = PACKAGE_DIR / ("_host" + sysconfig.get_config_var("EXT_SUFFIX"))
+ROCM_DIR = Path(os.environ.get("ROCM_PATH", "/opt/rocm"))
 ARCH = os.environ.get("GABOR_HIP_ARCH", "gfx950")
 
 COMPILE_FLAGS = [
@@ -101,7 +111,41 @@ def build_library(verbose: bool = False, diagnostics: bool = False) -> Path:
     return library
 
 
+def build_host(verbose: bool = False) -> Path:
+    """Compile the renderer's C++ host functions into the ``_host`` extension
+    module (no device code: the host compiler and torch's headers)."""
+    import torch
+    from torch.utils import cpp_extension
+
+    compiler = shutil.which("g++") or shutil.which("c++")
+    if compiler is None:
+        raise RuntimeError("no host C++ compiler found; the _host extension cannot be built")
+    torch_libraries = cpp_extension.library_paths()
+    includes = [*cpp_extension.include_paths(), sysconfig.get_paths()["include"],
+                str(ROCM_DIR / "include"), str(INCLUDE_DIR)]
+    temporary = HOST_EXTENSION.with_name(HOST_EXTENSION.name + ".tmp")
+    cmd = [
+        compiler, "-O2", "-std=c++17", "-fPIC", "-shared", "-fvisibility=hidden",
+        f"-D_GLIBCXX_USE_CXX11_ABI={int(torch.compiled_with_cxx11_abi())}",
+        "-DTORCH_EXTENSION_NAME=_host", "-DTORCH_API_INCLUDE_EXTENSION_H",
+        "-D__HIP_PLATFORM_AMD__=1", "-DUSE_ROCM=1",
+        *(f"-I{path}" for path in includes),
+        str(HOST_SOURCE), "-o", str(temporary),
+        *(f"-L{path}" for path in torch_libraries),
+        *(f"-Wl,-rpath,{path}" for path in torch_libraries),
+        "-lc10", "-lc10_hip", "-ltorch", "-ltorch_cpu", "-ltorch_python", "-lamdhip64",
+    ]
+    result = subprocess.run(cmd, capture_output=True, text=True)
+    if result.returncode != 0:
+        raise RuntimeError(f"{compiler} failed on {HOST_SOURCE.name}:\n{result.stdout}{result.stderr}")
+    os.replace(temporary, HOST_EXTENSION)
+    if verbose:
+        print(f"built {HOST_EXTENSION}", file=sys.stderr)
+    return HOST_EXTENSION
+
+
 if __name__ == "__main__":
     build_library(verbose=True)
+    build_host(verbose=True)
     if "--diagnostics" in sys.argv[1:]:
         build_library(verbose=True, diagnostics=True)

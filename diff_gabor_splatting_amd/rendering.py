@@ -221,15 +221,10 @@ class SHColors(torch.autograd.Function):
 def check_tensor(
     name: str, value: torch.Tensor, shape: tuple[int, ...], device: torch.device
 ) -> None:
-    """Require a contiguous float32 GPU tensor of an exact shape on `device`."""
-    if not isinstance(value, torch.Tensor):
-        raise TypeError(f"{name} must be a torch.Tensor")
-    if not (value.is_cuda and value.dtype == torch.float32 and value.device == device):
-        raise ValueError(f"{name} must be float32 on {device}")
-    if value.shape != shape:
-        raise ValueError(f"{name} must have shape {shape}, got {tuple(value.shape)}")
-    if not value.is_contiguous():
-        raise ValueError(f"{name} must be contiguous")
+    """Require a contiguous float32 GPU tensor of an exact shape on `device`:
+    TypeError for a non-tensor, ValueError for a wrong dtype or device, shape
+    or layout (the C++ host checks every renderer input this way)."""
+    _native.check_tensors({name: (value, shape)}, device)
 
 
 # Value contracts in the order the reference lists them (rendering.py:95-148),
@@ -510,8 +505,7 @@ def render(
         )
     for (name, shape), value in zip(fields, appearance):
         tensors[name] = (value, batch + (n,) + shape)
-    for name, (value, shape) in tensors.items():
-        check_tensor(name, value, shape, device)
+    _native.check_tensors(tensors, device)
     if type(validate) is not bool:
         raise TypeError("validate must be bool")
     bounded = _FIXED_CAPACITY[-1] if _FIXED_CAPACITY else None

@@ -142,3 +142,42 @@ def test_split_policy():
         assert -(-length // 64) <= 2 * length // 64
     assert _native.split_index_length(7, 10) == 18 + 34
     assert _native.split_index_length(8, 10) == 18 + 36
+
+
+def test_host_extension_binds_exported_entry_points():
+    """The C++ host functions call the library through addresses handed
+    over at import; every name they need is an exported, declared symbol,
+    and a table that lacks one is refused without unbinding the module."""
+    from diff_gabor_splatting_amd import _host, _native
+
+    names = _host.entry_points()
+    assert set(names) <= set(_native.exported_symbols())
+    with pytest.raises(RuntimeError, match="lacks gs_last_error"):
+        _host.bind({})
+    _native._bind_host(_native.lib)
+
+
+def test_host_checks_raise_before_any_launch():
+    """Structural checks of the C++ host functions run on the host: CPU
+    tensors are refused with the reference's messages before anything is
+    launched."""
+    import torch
+
+    from diff_gabor_splatting_amd import _native
+
+    q = 3
+    geometry = torch.zeros(q, 17)
+    args = (geometry, torch.zeros(q, 18), torch.zeros(q), torch.zeros(q, dtype=torch.int64),
+            torch.zeros(q, dtype=torch.int64), torch.zeros(q, dtype=torch.int32),
+            torch.zeros(1, 3), 16, 16, False, 0.1, 10.0)
+    with pytest.raises(RuntimeError, match="native rendering requires CUDA float32 tensors"):
+        _native.rasterize_forward(*args)
+    with pytest.raises(RuntimeError, match="native rendering requires CUDA float32 tensors"):
+        _native.rasterize_backward(geometry, torch.zeros(q, 18), torch.zeros(q),
+                                   torch.zeros(q, dtype=torch.int64), torch.zeros(1, 3),
+                                   torch.zeros(0, dtype=torch.int32),
+                                   torch.zeros(1, 2, dtype=torch.int32), torch.zeros(1, 16, 16, 3),
+                                   torch.zeros(1, 16, 16, dtype=torch.int32),
+                                   torch.zeros(1, 16, 16, 9), 16, 16, False, 0.1, 10.0)
+    with pytest.raises(RuntimeError, match="too many tensors to check"):
+        _native.check_values_word([geometry] * 17, *(torch.zeros(1),) * 5)
