@@ -740,6 +740,57 @@ __device__ __forceinline__ int cost_bucket(int cost) {
   return min(kOrderBuckets - 1, int(__log2f(float(cost) + 1.f) * 16.f));
 }
 
+__device__ __forceinline__ int wave_inclusive_sum(int v) {
+  const int lane = lane_id();
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const int up = __shfl_up(v, d, 64);
+    if (lane >= d) v += up;
+  }
+  return v;
+}
+
+// Heaviest-first bucket starts, run by the first wave of the block: next[b]
+// = the number of items in buckets heavier than b, and *total (if given)
+// the number of items. Each lane takes four consecutive buckets of the
+// descending order and one wave scan combines them.
+__device__ __forceinline__ void bucket_starts(const int* count, int* next, int* total) {
+  static_assert(kOrderBuckets == 4 * 64, "four buckets per lane");
+  const int lane = lane_id();
+  const int top = kOrderBuckets - 1 - 4 * lane;  // this lane's buckets: top, top - 1, ...
+  int c[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) c[j] = count[top - j];
+  const int own = c[0] + c[1] + c[2] + c[3];
+  int run = wave_inclusive_sum(own) - own;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    next[top - j] = run;
+    run += c[j];
+  }
+  if (total && lane == 63) *total = run;
+}
+
+// Inclusive prefix sum of v over the kOrderBlock threads; *chunk receives
+// the block's total. wave_totals holds kOrderBlock / 64 ints of LDS. The
+// block is synchronised on return, so wave_totals may be reused at once.
+__device__ __forceinline__ int block_inclusive_sum(int v, int* wave_totals, int* chunk) {
+  const int lane = lane_id(), wave = threadIdx.x >> 6;
+  const int incl = wave_inclusive_sum(v);
+  if (lane == 63) wave_totals[wave] = incl;
+  __syncthreads();
+  int before = 0, all = 0;
+#pragma unroll
+  for (int w = 0; w < kOrderBlock / 64; ++w) {
+    const int t = wave_totals[w];
+    before += w < wave ? t : 0;
+    all += t;
+  }
+  *chunk = all;
+  __syncthreads();
+  return before + incl;
+}
+
 // cost: per-tile cost, or null to use the tile's list length from ranges.
 // With seg.length > 0 (the forward of split tiles) it also assigns each
 // tile longer than seg.length its ceil(length / seg.length) checkpoint
@@ -759,18 +810,10 @@ __global__ __launch_bounds__(kOrderBlock) void tile_order_kernel(const int* __re
       const int t = first + threadIdx.x;
       const int k = t < tiles ? segment_count(ranges[t].y - ranges[t].x, seg.length) : 1;
       const int slots = k > 1 ? k : 0;
-      scan[threadIdx.x] = slots;
-      __syncthreads();
-      for (int offset = 1; offset < kOrderBlock; offset <<= 1) {  // inclusive scan
-        const int add = int(threadIdx.x) >= offset ? scan[threadIdx.x - offset] : 0;
-        __syncthreads();
-        scan[threadIdx.x] += add;
-        __syncthreads();
-      }
-      const int base = carry + scan[threadIdx.x] - slots;
+      int chunk;
+      const int base = carry + block_inclusive_sum(slots, scan, &chunk) - slots;
       if (t < tiles) seg.index[t] = (slots > 0 && base + slots <= seg.capacity) ? base : -1;
-      carry += scan[kOrderBlock - 1];
-      __syncthreads();
+      carry += chunk;
     }
     // The forward's (tile, segment) work list, heaviest first by the list
     // records each walks; entries past the work count are (-1, 0).
@@ -788,14 +831,7 @@ __global__ __launch_bounds__(kOrderBlock) void tile_order_kernel(const int* __re
       for (int k = 0; k < n; ++k) atomicAdd(&count[cost_bucket(piece_cost(t, k, n))], 1);
     }
     __syncthreads();
-    if (threadIdx.x == 0) {
-      int run = 0;
-      for (int b = kOrderBuckets - 1; b >= 0; --b) {
-        next[b] = run;
-        run += count[b];
-      }
-      scan[0] = run;
-    }
+    if (threadIdx.x < 64) bucket_starts(count, next, &scan[0]);
     __syncthreads();
     const int total = scan[0];
     for (int t = threadIdx.x; t < tiles; t += kOrderBlock) {
@@ -816,13 +852,7 @@ __global__ __launch_bounds__(kOrderBlock) void tile_order_kernel(const int* __re
     atomicAdd(&count[cost_bucket(c)], 1);
   }
   __syncthreads();
-  if (threadIdx.x == 0) {
-    int run = 0;
-    for (int b = kOrderBuckets - 1; b >= 0; --b) {
-      next[b] = run;
-      run += count[b];
-    }
-  }
+  if (threadIdx.x < 64) bucket_starts(count, next, nullptr);
   __syncthreads();
   for (int t = threadIdx.x; t < tiles; t += kOrderBlock) {
     const int c = cost ? cost[t] : ranges[t].y - ranges[t].x;
@@ -858,14 +888,7 @@ __global__ __launch_bounds__(kOrderBlock) void segment_order_kernel(
       atomicAdd(&count[cost_bucket(segment_cost(seg, replay_counts, t, k, n))], 1);
   }
   __syncthreads();
-  if (threadIdx.x == 0) {
-    int run = 0;
-    for (int b = kOrderBuckets - 1; b >= 0; --b) {
-      next[b] = run;
-      run += count[b];
-    }
-    total = run;
-  }
+  if (threadIdx.x < 64) bucket_starts(count, next, &total);
   __syncthreads();
   for (int t = threadIdx.x; t < tiles; t += kOrderBlock) {
     const int n = segments_of(t);
