@@ -238,7 +238,9 @@ def use_library(path: Path) -> None:
     """Route every later call of this module through the library at ``path``,
     a build of the same sources with the same entry points (the diagnostics
     build). Tensors and streams are unaffected; kernels already queued keep
-    running from the library that launched them."""
+    running from the library that launched them. The switch is process-wide
+    and not synchronised with renders: call it while no other thread
+    renders."""
     global lib
     lib = _load(Path(path))
     _bind_host(lib)

@@ -603,11 +603,21 @@ std::pair<at::Tensor, at::Tensor> bin_depth_first_impl(
               "hipMemcpyAsync");
   }
   check_hip(hipEventRecord(ready, stream), "hipEventRecord");
-  if (!overlap.is_none()) overlap();
-  {
+  auto wait = [ready] {
     py::gil_scoped_release released;
-    check_hip(hipEventSynchronize(ready), "hipEventSynchronize");
+    return hipEventSynchronize(ready);
+  };
+  if (!overlap.is_none()) {
+    try {
+      overlap();
+    } catch (...) {
+      // The copy into this thread's pinned buffer must land before the
+      // buffer can be reused by a later call, possibly on another stream.
+      wait();
+      throw;
+    }
   }
+  check_hip(wait(), "hipEventSynchronize");
   const int64_t intersections = state.host[0], visible = state.host[1];
   if (word.defined()) {
     const int32_t value = *reinterpret_cast<const int32_t*>(state.host + 2);
