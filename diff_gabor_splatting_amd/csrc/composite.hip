@@ -1484,6 +1484,27 @@ __global__ __launch_bounds__(kTilePixels, Neural ? 2 : 4) void renderBackward(
   const int wave_last = __builtin_amdgcn_readfirstlane(wave_max(last));
   const float mscale = far_plane / (far_plane - near_plane);
   const float mnear = mscale * near_plane;
+  // Per-pixel factors of the depth and distortion terms of the adjoint, with
+  // g4, g8 the depth and distortion map gradients and A = 1 - final T:
+  //   g4 depth + g8 (m^2 A + m2 - 2 m m1) = g4 depth + m (a8 m - c8) + d8,
+  //   dL/dz = w g4 + 2 w g8 mnear (m A - m1) / depth^2
+  //         = w (g4 + (e8 m - f8) / depth^2),
+  // a8 = g8 A, c8 = 2 g8 m1, d8 = g8 m2, e8 = 2 a8 mnear, f8 = c8 mnear.
+  // They are constant over the tile's records (the masked adjoint derives
+  // them from its masked gradients instead).
+  struct DepthTerms {
+    float a8, c8, d8, e8, f8;
+  };
+  auto depth_terms = [&](float g8) {
+    DepthTerms t;
+    t.a8 = g8 * total_a;
+    t.c8 = 2.f * g8 * m1;
+    t.d8 = g8 * m2;
+    t.e8 = 2.f * t.a8 * mnear;
+    t.f8 = t.c8 * mnear;
+    return t;
+  };
+  const DepthTerms pixel_terms = depth_terms(go[8]);
 
   // Record threadIdx.x of a batch starting at `start` is list position (or
   // replay entry) range.x + start - 1 - threadIdx.x; the next batch's entry
@@ -1579,9 +1600,10 @@ __global__ __launch_bounds__(kTilePixels, Neural ? 2 : 4) void renderBackward(
         const float w = T * alpha;
         Shade a;
         shade<Neural, true>(r, s_, a);
+        const DepthTerms dt = kMasked ? depth_terms(gom[8]) : pixel_terms;
         const float inv_depth = rcp(depth);
         const float m = mscale - mnear * inv_depth;
-        float gw = gom[4] * depth + gom[8] * (m * m * total_a + m2 - 2.f * m * m1);
+        float gw = gom[4] * depth + (m * (dt.a8 * m - dt.c8) + dt.d8);
         float gc[3];
 #pragma unroll
         for (int c = 0; c < 3; ++c) {
@@ -1599,8 +1621,7 @@ __global__ __launch_bounds__(kTilePixels, Neural ? 2 : 4) void renderBackward(
 #pragma unroll
           for (int k = 0; k < 3; ++k) gg[14 + k] = gdir[k];
         }
-        const float gz = w * gom[4] + gom[8] * 2.f * w * (m * total_a - m1) * mnear *
-                                         (inv_depth * inv_depth);
+        const float gz = w * (gom[4] + (dt.e8 * m - dt.f8) * (inv_depth * inv_depth));
         // The depth tilts with s only where a classic sample lies on the surface.
         const float gz_tilt = (Neural || surface) ? gz : 0.f;
         gs[0] += gz_tilt * r[6];
@@ -1608,13 +1629,17 @@ __global__ __launch_bounds__(kTilePixels, Neural ? 2 : 4) void renderBackward(
         gg[6] = gz_tilt * s_[0];
         gg[7] = gz_tilt * s_[1];
         gg[8] = gz;
-        const bool below = r[OP] * e < 0.99f;
-        grad[NP - 1] = below ? galpha * e : 0.f;
-        const float grho = below ? -0.5f * galpha * r[OP] * e : 0.f;
+        // alpha = min(0.99, o e) is below the clamp exactly when o e < 0.99
+        // (stand-in lanes: alpha = e = 0). Below it, dL/do = galpha e and
+        // dL/drho = -o galpha e / 2; g2 is twice the latter.
+        const bool below = alpha < 0.99f;
+        const float ge = below ? galpha * e : 0.f;
+        grad[NP - 1] = ge;
+        const float g2 = -r[OP] * ge;
         // rho is rho3 = |s|^2 on the surface (d/ds = 2 s) and otherwise
         // rho2 = 2 |xy - pixel|^2 (d/dxy = 4 (xy - pixel)).
-        const float grho3 = surface ? 2.f * grho : 0.f;
-        const float grho2 = surface ? 0.f : 4.f * grho;
+        const float grho3 = surface ? g2 : 0.f;
+        const float grho2 = surface ? 0.f : 2.f * g2;
         gs[0] += s_[0] * grho3;
         gs[1] += s_[1] * grho3;
         gg[9] = (r[9] - x) * grho2;
