@@ -401,8 +401,9 @@ __device__ __forceinline__ void shade(const float* r, const float* s, Shade& a) 
     float S = 0.f;
 #pragma unroll
     for (int f = 0; f < 4; ++f) {
-      const float t = fract(r[ClassicRow::A + f] * s[0] + r[ClassicRow::B + f] * s[1] +
-                            r[ClassicRow::C + f]);
+      // Two fused multiply-adds (the phase offset enters the inner one).
+      const float t = fract(
+          fmaf(r[ClassicRow::A + f], s[0], fmaf(r[ClassicRow::B + f], s[1], r[ClassicRow::C + f])));
       a.c[f] = cos_rev(t);
       if constexpr (Backward) a.sn[f] = sin_rev(t);
       S += r[ClassicRow::HW + f] * a.c[f];
@@ -1024,12 +1025,15 @@ __device__ __forceinline__ int walk_list(const ForwardStage<Neural>& st, int ran
       if (!__any(ok)) continue;
       const float next = w.T * (1.f - v.alpha);
       const bool stop = ok & (next < 0.0001f);
-      const bool take = ok & !stop;
+      // Without a stopping lane every lane that accepts takes the record, and
+      // some lane accepts: only a stop needs the wave-wide tests.
+      bool take = ok;
       if (__any(stop)) {
         w.done |= stop;
         if (__all(w.done)) break;
+        take = ok & !stop;
+        if (!__any(take)) continue;
       }
-      if (!__any(take)) continue;
       taken |= uint64_t(1) << j;
       Shade a;
       shade<Neural, false>(r, v.s, a);
@@ -1607,7 +1611,9 @@ __global__ __launch_bounds__(kTilePixels, Neural ? 2 : 4) void renderBackward(
         float gc[3];
 #pragma unroll
         for (int c = 0; c < 3; ++c) {
-          gw += gom[c] * a.color[c] + gom[5 + c] * r[11 + c];
+          // One accumulation per term: a chain of fused multiply-adds.
+          gw += gom[c] * a.color[c];
+          gw += gom[5 + c] * r[11 + c];
           gc[c] = w * gom[c];
           gg[11 + c] = w * gom[5 + c];
         }
