@@ -89,12 +89,17 @@ __device__ __forceinline__ float fract(float t) { return __builtin_amdgcn_fractf
 
 // LDS row layouts (floats). Geometry first in both: T 0-8, xy 9-10,
 // normal 11-13.
+// The colour is HALF_W SUM_c + S DIFF_c: the forward's rows hold the
+// product HALF_W SUM_c in the SUM slots (the forward needs no other use of
+// SUM_c), the backward's rows hold SUM_c and HALF_W for the flush and the
+// product at SUMW.
 struct ClassicRow {
   static constexpr int OP = 14, THR = 15;
   static constexpr int A = 16, B = 20, C = 24, HW = 28;  // 4 each
   static constexpr int HALF_W = 32, SUM = 33, DIFF = 36;  // 1, 3, 3
   static constexpr int AP = 40, BP = 44;  // -2 pi HW_f A_f, -2 pi HW_f B_f (backward)
-  static constexpr int STRIDE = 48;
+  static constexpr int SUMW = 48;         // HALF_W SUM_c (backward)
+  static constexpr int STRIDE = 52;
   static constexpr int FORWARD_STRIDE = 40;  // the forward's rows end before AP
 };
 struct NeuralRow {
@@ -354,7 +359,7 @@ __device__ __forceinline__ bool sample_surface(const float* r, float x, float y,
   v.s[1] = v.p[1] * v.inv_pz;
   const float rho3 = v.s[0] * v.s[0] + v.s[1] * v.s[1];
   v.surface = rho3 <= rho2;
-  v.depth = (Neural || v.surface) ? v.s[0] * r[6] + v.s[1] * r[7] + r[8] : r[8];
+  v.depth = (Neural || v.surface) ? fmaf(v.s[0], r[6], fmaf(v.s[1], r[7], r[8])) : r[8];
   v.e = __builtin_amdgcn_exp2f(fminf(rho3, rho2) * kNegHalfLog2e);
   v.alpha = fminf(0.99f, r[OP] * v.e);
   const bool ok = pass & (v.depth >= near_plane) & isfinite(v.depth) & (v.alpha >= kMinAlpha);
@@ -411,7 +416,8 @@ __device__ __forceinline__ void shade(const float* r, const float* s, Shade& a) 
     a.S = S;
 #pragma unroll
     for (int c = 0; c < 3; ++c)
-      a.color[c] = r[ClassicRow::HALF_W] * r[ClassicRow::SUM + c] + S * r[ClassicRow::DIFF + c];
+      a.color[c] = fmaf(S, r[ClassicRow::DIFF + c],
+                        r[(Backward ? ClassicRow::SUMW : ClassicRow::SUM) + c]);
   }
 }
 
@@ -596,7 +602,13 @@ __device__ __forceinline__ uint64_t load_batch(float* rows, float* raw, float* r
       r[R::HALF_W] = half_w;
 #pragma unroll
       for (int c = 0; c < 3; ++c) {
-        r[R::SUM + c] = a[c] + a[3 + c];
+        const float sum = a[c] + a[3 + c];
+        if constexpr (Forward) {
+          r[R::SUM + c] = half_w * sum;
+        } else {
+          r[R::SUM + c] = sum;
+          r[R::SUMW + c] = half_w * sum;
+        }
         r[R::DIFF + c] = a[c] - a[3 + c];
       }
     }
