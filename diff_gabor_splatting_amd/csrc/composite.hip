@@ -334,7 +334,9 @@ struct Sample {
 // StandIns: lanes that do not accept leave with finite stand-ins (alpha, e,
 // inv_pz and s zero, depth one, surface false), so that an adjoint run by
 // every lane of the wave multiplies them only by zeros.
-template <bool Neural, bool StandIns = false>
+// Reject = false drops the early wave-wide exit, for callers that know some
+// lane accepts (it costs two VALU instructions per test).
+template <bool Neural, bool StandIns = false, bool Reject = true>
 __device__ __forceinline__ bool sample_surface(const float* r, float x, float y,
                                                float near_plane, bool live, Sample& v) {
   constexpr int OP = Neural ? NeuralRow::OP : ClassicRow::OP;
@@ -353,7 +355,9 @@ __device__ __forceinline__ bool sample_surface(const float* r, float x, float y,
   // min(rho3, rho2) > thr without dividing: rho3 = |p.xy|^2 / p.z^2.
   const bool far = (rho2 > thr) & (v.p[0] * v.p[0] + v.p[1] * v.p[1] > thr * (v.p[2] * v.p[2]));
   const bool pass = live & !far & (v.p[2] != 0.f);
-  if (!__any(pass)) return false;
+  if constexpr (Reject) {
+    if (!__any(pass)) return false;
+  }
   v.inv_pz = rcp(v.p[2]);
   v.s[0] = v.p[0] * v.inv_pz;
   v.s[1] = v.p[1] * v.inv_pz;
@@ -1578,14 +1582,20 @@ __global__ __launch_bounds__(kTilePixels, Neural ? 2 : 4) void renderBackward(
       const float* r = rows + j * L::STRIDE;
       // List position of row j, counted from 1.
       const int position = Replay ? (entries[j] & kReplayPositionMask) + 1 : start - j;
+      // A replayed record was taken in the forward by a pixel of this wave's
+      // quadrant, so some lane accepts it again and the wave-wide tests are
+      // skipped (were none to accept, the stand-ins would make the adjoint
+      // add zeros). The full list walk keeps them.
       Sample v;
-      const bool active =
-          sample_surface<Neural, true>(r, x, y, near_plane, tp.inside && position <= last, v);
-      if (!__any(active)) continue;
+      const bool active = sample_surface<Neural, true, !Replay>(r, x, y, near_plane,
+                                                               tp.inside && position <= last, v);
+      if constexpr (!Replay) {
+        if (!__any(active)) continue;
+      }
 #ifdef GS_DIAGNOSTICS
       {
         const uint64_t taking = __ballot(active);
-        if (lane == 0) atomicAdd(&diag_lanes[__popcll(taking)], 1u);
+        if (lane == 0 && taking) atomicAdd(&diag_lanes[__popcll(taking)], 1u);
       }
 #endif
       // Every lane runs the adjoint. A lane that does not take the sample
