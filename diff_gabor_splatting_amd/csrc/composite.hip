@@ -1576,6 +1576,10 @@ __global__ __launch_bounds__(kTilePixels, Neural ? 2 : 4) void renderBackward(
       if (beyond >= 64) todo = 0;
       else if (beyond > 0) todo &= ~((uint64_t(1) << beyond) - 1);
     }
+    // Whether the wave's gradients and state are finite is constant over the
+    // tile, so the record loop is compiled once per adjoint variant and no
+    // per-record branch splits it.
+    auto walk = [&](auto masked) {
     while (todo) {
       const int j = __builtin_ctzll(todo);
       todo &= todo - 1;
@@ -1708,11 +1712,13 @@ __global__ __launch_bounds__(kTilePixels, Neural ? 2 : 4) void renderBackward(
           if (p1 < NP - H && t1 != 0.f) atomicAdd(dst + H + p1, t1);
         }
       };
-      if (finite_pixels)
-        adjoint(std::false_type{});
-      else
-        adjoint(std::true_type{});
+      adjoint(masked);
     }
+    };
+    if (finite_pixels)
+      walk(std::false_type{});
+    else
+      walk(std::true_type{});
     __syncthreads();
     // Flush this batch: one global atomic per nonzero (record, parameter).
     // Consecutive threads take consecutive parameters of a record, so that
