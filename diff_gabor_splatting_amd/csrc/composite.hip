@@ -1037,7 +1037,7 @@ __device__ __forceinline__ int walk_list(const ForwardStage<Neural>& st, int ran
       todo &= todo - 1;
       const float* r = st.rows + j * L::STRIDE;
       Sample v;
-      const bool ok = sample_surface<Neural>(r, x, y, near_plane, !w.done, v);
+      const bool ok = sample_surface<Neural, false, false>(r, x, y, near_plane, !w.done, v);
       if (!__any(ok)) continue;
       const float next = w.T * (1.f - v.alpha);
       const bool stop = ok & (next < 0.0001f);
