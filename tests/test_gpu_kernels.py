@@ -114,6 +114,35 @@ def test_binning_pipeline_is_bit_exact(native, seed, q, width, height, images):
     np.testing.assert_array_equal(bin_ranges.cpu().numpy(), ok_ranges)
 
 
+def test_depth_first_binning_propagates_callback_errors(native):
+    """An exception from the callback run while the host waits for the
+    intersection count propagates as raised, and the next binning on the
+    same thread (which reuses its pinned read-back buffer) is unaffected; a
+    pending value-check word reaches its callback before the count is used."""
+    geometry, radii, image_ids = random_geometry(11, 2000, 64, 64, 1)
+    g, r, ids = (torch.from_numpy(a).to(DEVICE) for a in (geometry, radii, image_ids))
+
+    def boom():
+        raise KeyError("overlap failed")
+
+    with pytest.raises(KeyError, match="overlap failed"):
+        native.bin_depth_first(g, r, ids, 1, 64, 64, overlap=boom)
+    _, ok_list, ok_ranges = oracle_binning.bin_pairs(geometry, radii, image_ids, 1, 64, 64)
+    point_list, ranges = native.bin_depth_first(g, r, ids, 1, 64, 64)
+    np.testing.assert_array_equal(point_list.cpu().numpy(), ok_list)
+    np.testing.assert_array_equal(ranges.cpu().numpy(), ok_ranges)
+    word = torch.full((1,), 5, dtype=torch.int32, device=DEVICE)
+    seen = []
+
+    def report(value):
+        seen.append(value)
+        raise ValueError("values violated")
+
+    with pytest.raises(ValueError, match="values violated"):
+        native.bin_depth_first(g, r, ids, 1, 64, 64, violations=(word, report))
+    assert seen == [5]
+
+
 @pytest.mark.parametrize("seed, q, width, height, images, culled", [
     (5, 3000, 64, 64, 1, 1.0),          # every pair culled: m = 0
     (6, 40_000, 1920, 1080, 40, 0.0),   # 326,400 tiles: 19 id bits, three tile passes
