@@ -15,8 +15,8 @@
 // compacted too (the reference keeps them dense), and each row's
 // primitive id is then the row itself. A dense row whose pair is culled
 // (radius 0) is referenced by no tile list: it gets its radius, projected
-// mean and ids, while its geometry, appearance and opacity entries are left
-// unwritten.
+// mean and ids, zero geometry and appearance rows (written with its
+// neighbours' in whole cache lines) and no opacity entry.
 //
 // The adjoint reads the compositor's gradient rows: an SH pass sums colour
 // and shared-parameter gradients over cameras per surfel (no atomics) and
@@ -36,9 +36,7 @@ bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) ==
 // One thread per (scene, surfel) loops over the cameras of its scene. Every
 // pair gets its radius, projected mean and ids; pairs that reach a tile
 // (radius > 0) also get their geometry row and, with SH, their appearance
-// and opacity rows. Rows of culled pairs are referenced by no tile list,
-// so their geometry, appearance and opacity entries are left unwritten and
-// their SH coefficients are never read. Coefficients are read one colour
+// and opacity rows. The SH coefficients of culled pairs are never read. Coefficients are read one colour
 // set at a time, in 16-byte vectors when the set's length allows.
 template <int KC, bool Vec>
 __device__ __forceinline__ void load_coefficients(const float* __restrict__ src, float* dst) {
@@ -74,6 +72,31 @@ __device__ __forceinline__ void unstage_pair_rows(const float* stage, int pitch,
     const int64_t row = rows[local];
     if (row >= 0) out[row * Width + f] = stage[local * pitch + offset + f];
   }
+}
+
+// Dense rows (row == pair): a workgroup's rows [first, first + count) are
+// one contiguous run, written whole with 16-byte stores (rows of culled
+// pairs as zeros), so that every store fills whole cache lines.
+template <int Width>
+__device__ __forceinline__ void unstage_dense_rows(const float* stage, int pitch, int offset,
+                                                   const int64_t* rows, int64_t first, int count,
+                                                   float* __restrict__ out) {
+  float* dst = out + first * Width;
+  const int total = count * Width;
+  auto value = [&](int e) {
+    const int local = e / Width, f = e - local * Width;
+    return rows[local] >= 0 ? stage[local * pitch + offset + f] : 0.f;
+  };
+  const int head = min(int((4u - ((reinterpret_cast<uintptr_t>(dst) >> 2) & 3u)) & 3u), total);
+  if (int(threadIdx.x) < head) dst[threadIdx.x] = value(threadIdx.x);
+  const int body = (total - head) / 4;
+  float4* dst4 = reinterpret_cast<float4*>(dst + head);
+  for (int q = threadIdx.x; q < body; q += kProjectBlock) {
+    const int e = head + 4 * q;
+    dst4[q] = make_float4(value(e), value(e + 1), value(e + 2), value(e + 3));
+  }
+  const int tail = head + 4 * body;
+  if (tail + int(threadIdx.x) < total) dst[tail + threadIdx.x] = value(tail + threadIdx.x);
 }
 
 template <int Degree, bool Vec>  // Degree -1: no SH rows
@@ -169,8 +192,16 @@ __global__ __launch_bounds__(kProjectBlock) void records_forward_kernel(
     if (!geometry) continue;  // uniform: a radii-only pass writes no rows
     stage_rows[t] = staged;
     __syncthreads();
-    unstage_pair_rows<kGeometry>(stage, kPitch, 0, stage_rows, geometry);
-    if constexpr (kSH) unstage_pair_rows<kRow>(stage, kPitch, kGeometry, stage_rows, appearance);
+    if (!row_of_pair) {
+      const int64_t first = cam * n + int64_t(blockIdx.x) * kProjectBlock;
+      const int count = int(min<int64_t>(kProjectBlock, n - int64_t(blockIdx.x) * kProjectBlock));
+      unstage_dense_rows<kGeometry>(stage, kPitch, 0, stage_rows, first, count, geometry);
+      if constexpr (kSH)
+        unstage_dense_rows<kRow>(stage, kPitch, kGeometry, stage_rows, first, count, appearance);
+    } else {
+      unstage_pair_rows<kGeometry>(stage, kPitch, 0, stage_rows, geometry);
+      if constexpr (kSH) unstage_pair_rows<kRow>(stage, kPitch, kGeometry, stage_rows, appearance);
+    }
     __syncthreads();  // the next camera overwrites the stage
   }
 }
