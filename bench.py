@@ -14,6 +14,10 @@ Prints ONE JSON line. Besides the driver's contract fields it carries:
                 next to the GPU's time for the same workload, plus a
                 labelled secondary figure on a crop of config 4;
   per_config    ms/step and Mpix/s of the other BASELINE configs, same run;
+  graph_replay  a labelled secondary figure: every config's render and
+                backward captured once in a HIP graph and replayed, next to
+                its eager step (what the host-bound small configs cost
+                without Python, autograd and launch overheads);
   kernels       per-family average milliseconds per step.
 """
 
@@ -158,6 +162,12 @@ def _loss(rgb, alpha, meta, channels):
     is mse_loss against zero, whose backward is one fused kernel (2 x / n)
     where square().mean() runs pow, mul, mul and div over the whole map.
     """
+    maps = _flat_maps(rgb, alpha, meta, channels)
+    return torch.nn.functional.mse_loss(maps, maps.new_zeros(()).expand_as(maps))
+
+
+def _flat_maps(rgb, alpha, meta, channels):
+    """The loss's first `channels` map channels, concatenated flat."""
     flat, left = [], channels
     for t in (rgb, alpha, meta["accumulated_depth"], meta["normals"], meta["distortion"]):
         if left <= 0:
@@ -165,8 +175,7 @@ def _loss(rgb, alpha, meta, channels):
         k = t.shape[-1]
         flat.append((t if k <= left else t[..., :left]).reshape(-1))
         left -= k
-    maps = torch.cat(flat) if len(flat) > 1 else flat[0]
-    return torch.nn.functional.mse_loss(maps, maps.new_zeros(()).expand_as(maps))
+    return torch.cat(flat) if len(flat) > 1 else flat[0]
 
 
 def algorithmic_bytes(kind: str, neural: bool, pixels: int, records: int, pairs: int,
@@ -245,6 +254,69 @@ def per_config_times(skip: int, steps: int, warmup: int, device, validate: bool)
     return out
 
 
+def graph_replay_times(steps: int, warmup: int, device) -> dict:
+    """Every config's render and backward captured once in a HIP graph and
+    replayed: ms per replay next to the eager step.
+
+    Inside ``fixed_capacity`` the renderers never synchronise with the host,
+    so one capture holds the render, the concatenation of the loss's maps
+    and the backward; a replay then costs the kernels alone. The loss's
+    reduction stays out of the graph (torch's reduction records a memset
+    node, which is not replay-safe here) and the backward receives the loss
+    gradient 2 x / n directly, so a replay computes the eager step's
+    parameter gradients without the scalar loss itself. The capacity is the
+    eager intersection count plus a quarter; every replay is checked not to
+    exceed it, and one replay's gradients are compared with eager ones.
+    """
+    from diff_gabor_splatting_amd import fixed_capacity
+
+    out = {}
+    for index, cfg in CONFIGS.items():
+        _, values, renderer, options, step = prepare(index, device, False)
+        eager_ms = time_steps(step, steps, warmup)
+        params = [v for v in values.values() if v.requires_grad]
+
+        def body():
+            rgb, alpha, meta = renderer(**values, **options)
+            maps = _flat_maps(rgb, alpha, meta, cfg["channels"])
+            return torch.autograd.grad(maps, params,
+                                       grad_outputs=maps.detach() * (2.0 / maps.numel()))
+
+        with fixed_capacity(1 << 26) as probe:
+            renderer(**values, **options)
+        count = probe.check()
+        capacity = fixed_capacity(count + count // 4 + 1024)
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with capacity, torch.cuda.stream(side):
+            for _ in range(2):
+                body()
+        torch.cuda.current_stream().wait_stream(side)
+        capacity.check()
+        graph = torch.cuda.CUDAGraph()
+        with capacity, torch.cuda.graph(graph):
+            grads = body()
+        for _ in range(warmup):
+            graph.replay()
+        torch.cuda.synchronize()
+        with paused_collector():
+            start = time.perf_counter()
+            for _ in range(steps):
+                graph.replay()
+            torch.cuda.synchronize()
+            replay_ms = (time.perf_counter() - start) * 1000 / steps
+        capacity.check()  # raises if any replay exceeded the capacity
+        expected = body()
+        worst = max(float(((g - e).abs().max() / e.abs().max().clamp_min(1e-30)).item())
+                    for g, e in zip(grads, expected))
+        out[str(index)] = {"workload": cfg["name"], "eager_ms_per_step": round(eager_ms, 4),
+                           "replay_ms": round(replay_ms, 4), "capacity": count + count // 4 + 1024,
+                           "grad_max_rel_diff_vs_eager": worst}
+        del graph, grads, expected, step, values
+        torch.cuda.empty_cache()
+    return out
+
+
 def main(argv=None):
     parser = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     parser.add_argument("--gpus", type=int, default=1)
@@ -257,6 +329,8 @@ def main(argv=None):
                         help="1: time the CPU oracle on config 0 (and a crop of config 4)")
     parser.add_argument("--per-config", type=int, default=1,
                         help="1: also time every other config (ms/step), same run")
+    parser.add_argument("--graph-replay", type=int, default=1,
+                        help="1: also time every config captured in a HIP graph and replayed")
     parser.add_argument("--cpu-crop", type=int, default=32,
                         help="edge in pixels of the secondary config-4 CPU crop (0: skip it)")
     parser.add_argument("--copy-calibration", action="store_true",
@@ -356,6 +430,8 @@ def main(argv=None):
     if args.per_config:
         result["per_config"] = per_config_times(args.config, args.steps, args.warmup, device,
                                                 args.validate)
+    if args.graph_replay:
+        result["graph_replay"] = graph_replay_times(args.steps, args.warmup, device)
     if args.cpu_baseline:
         gpu_config0 = result.get("per_config", {}).get("0", {}).get("ms_per_step")
         if args.config == 0:
