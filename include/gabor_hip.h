@@ -94,7 +94,9 @@ int gs_project_backward(const float* means, const float* quaternions, const floa
  * appearance_rows [Q,18] (SH colours, then the surfel's weights, magnitudes
  * and phases) and opacity_rows [Q]; sh_degree -1 writes neither (the caller
  * supplies per-surfel appearance). Rows of pairs with radius 0 (referenced
- * by no tile list) get only their radius, projected mean and ids. When
+ * by no tile list) get their radius, projected mean and ids; their geometry
+ * and appearance rows are zero in dense mode (row_of_pair null) and their
+ * opacity entry is left as it was. When
  * given (all three or none), meta_scene_ids / meta_camera_ids /
  * meta_surfel_ids [Q] int64 receive each row's scene, camera and surfel
  * index: the reference's meta ids (rendering.py:389-392). */
