@@ -357,8 +357,15 @@ def test_records_match_oracle(native, packed, sh):
     np.testing.assert_array_equal(out["row_radii"].cpu().numpy(), rec["radii"].numpy())
     expect_prims = np.arange(len(selected)) if sh is not None else rec["primitive_ids"].numpy()
     np.testing.assert_array_equal(out["primitive_ids"].cpu().numpy(), expect_prims)
-    # Rows of culled pairs (radius 0) are referenced by no tile list: only
-    # their radius, projected mean and ids are defined.
+    # Rows of culled pairs (radius 0) are referenced by no tile list: their
+    # radius, projected mean and ids are compared with the oracle, and in
+    # dense mode their geometry and appearance rows are zero.
+    if not packed:
+        culled = out["row_radii"].cpu() == 0
+        assert bool(culled.any())
+        assert bool((out["geometry"].cpu()[culled] == 0).all())
+        if sh is not None:
+            assert bool((out["appearance"].cpu()[culled] == 0).all())
     visible = rec["radii"] > 0
     geometry = rec["geometry"].detach()
     sens = perturbation_sensitivity(
