@@ -307,14 +307,15 @@ def test_sh_values_and_derivatives(native, degree, cameras):
         torch.testing.assert_close(a.cpu().double(), e, atol=3e-5, rtol=2e-4)
 
 
+@pytest.mark.parametrize("n", [300, 301])  # 301: dense row runs start off 16-byte boundaries
 @pytest.mark.parametrize("packed", [False, True])
 @pytest.mark.parametrize("sh", [None, 0, 3])
-def test_records_match_oracle(native, packed, sh):
+def test_records_match_oracle(native, packed, sh, n):
     from oracle import render as oracle_render
     from scenes import random_scene
 
     width, height = 48, 40
-    v = random_scene("classic", scenes=2, cameras=3, n=300, width=width, height=height, seed=8,
+    v = random_scene("classic", scenes=2, cameras=3, n=n, width=width, height=height, seed=8,
                      sh=sh)
     v["view_matrices"][..., 2, 3] = torch.linspace(-1.0, 0.5, 3)  # some surfels behind near
     S, N = v["means"].shape[:2]
