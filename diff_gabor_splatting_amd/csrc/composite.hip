@@ -111,6 +111,12 @@ struct NeuralRow {
   static constexpr int STRIDE = 76;
   static constexpr int FORWARD_STRIDE = 55;  // the forward's rows end before DIR
 };
+// The neural forward's raw staging row: direction, then the appearance
+// row's input weights and biases (appearance columns 0..35 at 3..38).
+struct NeuralRaw {
+  static constexpr int DIR = 0, W1 = 3, B1 = 33;
+  static constexpr int WIDTH = 39;
+};
 
 // Forward: the forward compositor's rows, which leave out what only the
 // adjoint reads (classic AP/BP, neural DIR/WDIR), so that six classic or
@@ -119,7 +125,10 @@ template <bool Neural, bool Forward = false>
 struct Layout {
   static constexpr int A = Neural ? kNeural : kClassic;  // raw appearance floats
   static constexpr int RAW = kGeometry + 1 + A;          // raw staging floats
-  static constexpr int RAW_STRIDE = Neural ? 76 : 36;
+  // The neural forward stages only what its row derivation reads (direction
+  // 3, input weights 30, input biases 6: NeuralRaw); the gather writes the
+  // rest straight into the rows.
+  static constexpr int RAW_STRIDE = Neural ? (Forward ? 39 : 76) : 36;
   static constexpr int STRIDE = Neural ? (Forward ? NeuralRow::FORWARD_STRIDE : NeuralRow::STRIDE)
                                        : (Forward ? ClassicRow::FORWARD_STRIDE : ClassicRow::STRIDE);
   // Gradient values per record: geometry (classic skips the unused
@@ -470,6 +479,11 @@ __device__ __forceinline__ uint64_t load_batch(float* rows, float* raw, float* r
     const int record = t / kParts, q = t % kParts;
     if (record < count) {
       float* dst = raw + record * L::RAW_STRIDE;
+      // The neural forward's destinations: geometry columns 0..13 and the
+      // opacity go to the row, the direction to NeuralRaw; appearance columns
+      // 0..35 (input weights, biases) to NeuralRaw, 36..56 (output weights,
+      // biases) to the row.
+      constexpr bool kSplitRaw = Neural && Forward;
       constexpr int kGeo = (kGeometry + kParts - 1) / kParts;
       const float* g = geometry + int64_t(ids[record]) * kGeometry;
       const int64_t prim_j = prims[record];
@@ -506,18 +520,38 @@ __device__ __forceinline__ uint64_t load_batch(float* rows, float* raw, float* r
           const int f = q * kPer + k;
           av[k] = f < L::A ? a[f] : 0.f;
         }
+        if constexpr (kSplitRaw) {
+          float* row = rows + record * L::STRIDE;
 #pragma unroll
-        for (int k = 0; k < kPer; ++k) {
-          const int f = q * kPer + k;
-          if (f < L::A) dst[kGeometry + 1 + f] = av[k];
+          for (int k = 0; k < kPer; ++k) {
+            const int f = q * kPer + k;
+            if (f < L::A)
+              (f < 36 ? dst + NeuralRaw::W1 + f : row + NeuralRow::W2 + (f - 36))[0] = av[k];
+          }
+        } else {
+#pragma unroll
+          for (int k = 0; k < kPer; ++k) {
+            const int f = q * kPer + k;
+            if (f < L::A) dst[kGeometry + 1 + f] = av[k];
+          }
         }
       }
+      if constexpr (kSplitRaw) {
+        float* row = rows + record * L::STRIDE;
 #pragma unroll
-      for (int k = 0; k < kGeo; ++k) {
-        const int f = q * kGeo + k;
-        if (f < kGeometry) dst[f] = gv[k];
+        for (int k = 0; k < kGeo; ++k) {
+          const int f = q * kGeo + k;
+          if (f < kGeometry) (f < 14 ? row + f : dst + NeuralRaw::DIR + (f - 14))[0] = gv[k];
+        }
+        if (q == kParts - 1) row[NeuralRow::OP] = opacity;
+      } else {
+#pragma unroll
+        for (int k = 0; k < kGeo; ++k) {
+          const int f = q * kGeo + k;
+          if (f < kGeometry) dst[f] = gv[k];
+        }
+        if (q == kParts - 1) dst[kGeometry] = opacity;
       }
-      if (q == kParts - 1) dst[kGeometry] = opacity;
     }
   } else {
     // One loop per source array, consecutive threads on consecutive floats of
@@ -555,10 +589,33 @@ __device__ __forceinline__ uint64_t load_batch(float* rows, float* raw, float* r
   const int wave = t >> 6;
   const int j = t & 63;
   if (Which == kReachTest && wave == 1 && j < count) {
-    const float* g = raw + j * L::RAW_STRIDE;
-    record_reach(g, reject_threshold(g[kGeometry]), reach_rows + j * kReachPitch);
+    if constexpr (Neural && Forward) {
+      // The row already holds T, xy and the opacity; wave 0 writes only
+      // later columns of it.
+      const float* r = rows + j * L::STRIDE;
+      record_reach(r, reject_threshold(r[NeuralRow::OP]), reach_rows + j * kReachPitch);
+    } else {
+      const float* g = raw + j * L::RAW_STRIDE;
+      record_reach(g, reject_threshold(g[kGeometry]), reach_rows + j * kReachPitch);
+    }
   }
-  if (t < count) {
+  if constexpr (Neural && Forward) {
+    if (t < count) {
+      using R = NeuralRow;
+      using W = NeuralRaw;
+      const float* g = raw + t * L::RAW_STRIDE;
+      float* r = rows + t * L::STRIDE;
+      r[R::THR] = reject_threshold(r[R::OP]);
+#pragma unroll
+      for (int h = 0; h < 6; ++h) {
+        const float* w1 = g + W::W1 + h * 5;
+        r[R::ZC + h] = g[W::B1 + h] + w1[2] * g[W::DIR + 0] + w1[3] * g[W::DIR + 1] +
+                       w1[4] * g[W::DIR + 2];
+        r[R::U + h] = w1[0] / 3.f;
+        r[R::V + h] = w1[1] / 3.f;
+      }
+    }
+  } else if (t < count) {
     const float* g = raw + t * L::RAW_STRIDE;
     const float opacity = g[kGeometry];
     const float* a = g + kGeometry + 1;
@@ -1094,7 +1151,7 @@ static_assert(kCheckpointFloats >= kSegmentResults, "a slot holds a segment's re
 // Replay: also write the tile's replay list (replay + range start, see
 // append_replay) and its length (replay_counts[tile]).
 template <bool Neural, bool Replay, bool Split>
-__global__ __launch_bounds__(kTilePixels, Neural ? 4 : 6) void renderForward(
+__global__ __launch_bounds__(kTilePixels, Neural ? (Split ? 4 : 5) : 6) void renderForward(
     int width, int height, int tw, int th, const float* __restrict__ geometry,
     const float* __restrict__ appearance, const float* __restrict__ opacities,
     const int64_t* __restrict__ primitive_ids, const float* __restrict__ backgrounds,
