@@ -1448,7 +1448,7 @@ __device__ __forceinline__ float classic_appearance_gradient(const float* sums, 
 // tile_last[tile], compositing each record only in the quadrants that took
 // it; tile_last is then unused.
 template <bool Neural, bool Replay>
-__global__ __launch_bounds__(kTilePixels, Neural ? 2 : 4) void renderBackward(
+__global__ __launch_bounds__(kTilePixels, Neural && !Replay ? 2 : 4) void renderBackward(
     int width, int height, int tw, int th, const float* __restrict__ geometry,
     const float* __restrict__ appearance, const float* __restrict__ opacities,
     const int64_t* __restrict__ primitive_ids, const float* __restrict__ backgrounds,
@@ -1467,7 +1467,7 @@ __global__ __launch_bounds__(kTilePixels, Neural ? 2 : 4) void renderBackward(
   __shared__ __align__(16) float rows[kBatch * L::STRIDE];
   // The raw staging rows are dead once a batch's rows are derived, and the
   // gradient accumulator is needed only after that: they share LDS, which
-  // keeps the neural kernel at three workgroups per CU.
+  // fits four neural replay workgroups in a CU (39.9 KB each).
   constexpr int kRawFloats = kBatch * L::RAW_STRIDE, kAccFloats = kBatch * NP;
   __shared__ __align__(16) float raw_acc[kRawFloats > kAccFloats ? kRawFloats : kAccFloats];
   float* raw = raw_acc;
