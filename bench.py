@@ -254,7 +254,7 @@ def per_config_times(skip: int, steps: int, warmup: int, device, validate: bool)
     return out
 
 
-def graph_replay_times(steps: int, warmup: int, device) -> dict:
+def graph_replay_times(steps: int, warmup: int, device, indices=None) -> dict:
     """Every config's render and backward captured once in a HIP graph and
     replayed: ms per replay next to the eager step.
 
@@ -267,11 +267,14 @@ def graph_replay_times(steps: int, warmup: int, device) -> dict:
     parameter gradients without the scalar loss itself. The capacity is the
     eager intersection count plus a quarter; every replay is checked not to
     exceed it, and one replay's gradients are compared with eager ones.
+    `indices` restricts the configs (all by default).
     """
     from diff_gabor_splatting_amd import fixed_capacity
 
     out = {}
     for index, cfg in CONFIGS.items():
+        if indices is not None and index not in indices:
+            continue
         _, values, renderer, options, step = prepare(index, device, False)
         eager_ms = time_steps(step, steps, warmup)
         params = [v for v in values.values() if v.requires_grad]

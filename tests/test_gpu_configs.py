@@ -356,3 +356,16 @@ def test_hardest_tiles_match_oracle(hard_windows, index, criterion):
         assert w["list_length"] > 64
     if criterion == "early stop":
         assert checked_stops > 0
+
+
+def test_bench_graph_replay_of_config0():
+    """bench.py's graph_replay figure on config 0: the captured render and
+    backward replay within the capacity, and a replay's gradients match an
+    eager computation (atomic order aside)."""
+    print("graph replay: config 0", flush=True)
+    out = bench.graph_replay_times(3, 1, DEVICE, indices=(0,))
+    assert list(out) == ["0"]
+    row = out["0"]
+    assert row["replay_ms"] > 0 and row["eager_ms_per_step"] > 0
+    assert row["capacity"] > 0
+    assert row["grad_max_rel_diff_vs_eager"] < 1e-4
