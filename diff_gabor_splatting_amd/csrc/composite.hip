@@ -131,10 +131,19 @@ struct Layout {
   static constexpr int RAW_STRIDE = Neural ? (Forward ? 39 : 76) : 36;
   static constexpr int STRIDE = Neural ? (Forward ? NeuralRow::FORWARD_STRIDE : NeuralRow::STRIDE)
                                        : (Forward ? ClassicRow::FORWARD_STRIDE : ClassicRow::STRIDE);
-  // Gradient values per record: geometry (classic skips the unused
-  // direction columns), appearance, opacity.
-  static constexpr int NG = Neural ? kGeometry : 14;
-  static constexpr int NP = NG + A + 1;
+  // Gradient values reduced per record: geometry columns 0..13, appearance
+  // sums, opacity. The direction columns' gradients (classic: none) and the
+  // neural input weights' direction columns are per-record constants times
+  // the input-bias sums, applied at the flush, so they are not reduced:
+  // neural appearance sums are input weights' columns 0, 1 (12), input
+  // biases (6), output weights (18), output biases (3).
+  static constexpr int NG = 14;
+  static constexpr int AR = Neural ? 39 : A;
+  static constexpr int NP = NG + AR + 1;
+};
+// Offsets of the neural appearance sums (after the NG geometry values).
+struct NeuralSums {
+  static constexpr int W01 = 0, B1 = 12, W2 = 18, B2 = 36;
 };
 
 // Rejection threshold on rho: alpha = min(0.99, o exp(-rho/2)) < 1/255
@@ -1357,23 +1366,26 @@ __global__ __launch_bounds__(kTilePixels) void mergeSegments(
   }
 }
 
-// Appearance adjoint given dL/dcolor = gc. Writes the raw appearance
-// gradients into ga (classic 18, neural 57), accumulates d/d(u, v) into gs
-// and, for neural, d/d(direction) into gdir.
+// Appearance adjoint given dL/dcolor = gc. Writes the summands of the
+// per-record appearance sums into ga (classic 18; neural 39, laid out as
+// NeuralSums) and accumulates d/d(u, v) into gs. The neural input weights'
+// direction columns and the direction itself receive gz_h d_k and
+// gz_h W1[h][2 + k]: per-record constants times the input-bias summand gz_h,
+// applied once per record at the flush (neural_output_gradient).
 template <bool Neural>
 __device__ __forceinline__ void shade_backward(const float* r, const float* s, const Shade& a,
-                                               const float* gc, float* ga, float* gs,
-                                               float* gdir) {
+                                               const float* gc, float* ga, float* gs) {
   if constexpr (Neural) {
     using R = NeuralRow;
+    using S = NeuralSums;
     float gh[6] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int c = 0; c < 3; ++c) {
       const float gz = gc[c] * a.color[c] * (1.f - a.color[c]);
-      ga[54 + c] = gz;
+      ga[S::B2 + c] = gz;
 #pragma unroll
       for (int h = 0; h < 6; ++h) {
-        ga[36 + c * 6 + h] = gz * a.sn[h];
+        ga[S::W2 + c * 6 + h] = gz * a.sn[h];
         gh[h] += gz * r[R::W2 + c * 6 + h];
       }
     }
@@ -1381,16 +1393,11 @@ __device__ __forceinline__ void shade_backward(const float* r, const float* s, c
 #pragma unroll
     for (int h = 0; h < 6; ++h) {
       const float gz = gh[h] * 30.f * a.c[h];
-      ga[30 + h] = gz;
-      ga[h * 5 + 0] = gz * in0;
-      ga[h * 5 + 1] = gz * in1;
-      ga[h * 5 + 2] = gz * r[R::DIR + 0];
-      ga[h * 5 + 3] = gz * r[R::DIR + 1];
-      ga[h * 5 + 4] = gz * r[R::DIR + 2];
+      ga[S::B1 + h] = gz;
+      ga[S::W01 + 2 * h + 0] = gz * in0;
+      ga[S::W01 + 2 * h + 1] = gz * in1;
       gs[0] += gz * r[R::U + h];
       gs[1] += gz * r[R::V + h];
-#pragma unroll
-      for (int k = 0; k < 3; ++k) gdir[k] += gz * r[R::WDIR + h * 3 + k];
     }
   } else {
     // colour_c = h1 c1_c + h2 c2_c with h1/h2 = W/2 +/- S, S = sum_f HW_f cos_f.
@@ -1418,6 +1425,36 @@ __device__ __forceinline__ void shade_backward(const float* r, const float* s, c
       gs[1] += gq * r[R::BP + f];
     }
   }
+}
+
+// Neural output parameter p of one record from its reduced sums (NG
+// geometry values, the appearance sums laid out as NeuralSums, opacity
+// last): geometry columns 0..13; the direction, 14..16, sum_h W1[h][2 + k]
+// B1_h; appearance columns 0..56, where input weight [h][2 + k] is d_k B1_h
+// and the rest are sums; then the opacity. B1_h, the input-bias sum, is the
+// sum over pixels of gz_h, so these per-record products equal the per-pixel
+// sums of gz_h W1[h][2 + k] and gz_h d_k.
+__device__ __forceinline__ float neural_output_gradient(const float* sums, const float* r, int p) {
+  using R = NeuralRow;
+  using S = NeuralSums;
+  constexpr int NG = Layout<true>::NG;
+  const float* b1 = sums + NG + S::B1;
+  if (p < NG) return sums[p];
+  if (p < kGeometry) {
+    const int k = p - NG;
+    float v = 0.f;
+#pragma unroll
+    for (int h = 0; h < 6; ++h) v += r[R::WDIR + h * 3 + k] * b1[h];
+    return v;
+  }
+  const int a = p - kGeometry;
+  if (a < 30) {
+    const int h = a / 5, i = a - 5 * h;
+    return i < 2 ? sums[NG + S::W01 + 2 * h + i] : r[R::DIR + i - 2] * b1[h];
+  }
+  if (a < 36) return b1[a - 30];
+  if (a < kNeural) return sums[NG + S::W2 + (a - 36)];  // output weights, then biases
+  return sums[Layout<true>::NP - 1];
 }
 
 // Gradient of classic appearance column k of one record from the pixel
@@ -1704,12 +1741,7 @@ __global__ __launch_bounds__(kTilePixels, Neural && !Replay ? 2 : 4) void render
         const float galpha = kMasked ? (active ? galpha_lane : 0.f) : galpha_lane;
         suffix += w * gw;
         float gs[2] = {0.f, 0.f};
-        float gdir[3] = {0.f, 0.f, 0.f};
-        shade_backward<Neural>(r, s_, a, gc, ga, gs, gdir);
-        if constexpr (Neural) {
-#pragma unroll
-          for (int k = 0; k < 3; ++k) gg[14 + k] = gdir[k];
-        }
+        shade_backward<Neural>(r, s_, a, gc, ga, gs);
         const float gz = w * (gom[4] + (dt.e8 * m - dt.f8) * (inv_depth * inv_depth));
         // The depth tilts with s only where a classic sample lies on the surface.
         const float gz_tilt = (Neural || surface) ? gz : 0.f;
@@ -1780,19 +1812,27 @@ __global__ __launch_bounds__(kTilePixels, Neural && !Replay ? 2 : 4) void render
     // Flush this batch: one global atomic per nonzero (record, parameter).
     // Consecutive threads take consecutive parameters of a record, so that
     // the atomics of a wave fall on a few cache lines.
-    for (int idx = threadIdx.x; idx < count * NP; idx += kTilePixels) {
-      const int j = idx / NP;
-      const int p = idx - j * NP;
-      float value = acc[idx];
-      if constexpr (!Neural) {
+    // Output parameters per record: geometry (classic columns 0..13, neural
+    // all 17), appearance, opacity; each from the record's reduced sums.
+    constexpr int NGO = Neural ? kGeometry : NG;
+    constexpr int NO = NGO + L::A + 1;
+    for (int idx = threadIdx.x; idx < count * NO; idx += kTilePixels) {
+      const int j = idx / NO;
+      const int p = idx - j * NO;
+      const float* sums = acc + j * NP;
+      float value;
+      if constexpr (Neural) {
+        value = neural_output_gradient(sums, rows + j * L::STRIDE, p);
+      } else {
+        value = sums[p];
         if (p >= NG && p < NG + L::A)
-          value = classic_appearance_gradient(acc + j * NP + NG, rows + j * L::STRIDE, p - NG);
+          value = classic_appearance_gradient(sums + NG, rows + j * L::STRIDE, p - NG);
       }
       if (value != 0.f) {
-        if (p < NG) {
+        if (p < NGO) {
           atomicAdd(grad_geometry + int64_t(ids[j]) * kGeometry + p, value);
-        } else if (p < NG + L::A) {
-          atomicAdd(grad_appearance + prims[j] * L::A + (p - NG), value);
+        } else if (p < NGO + L::A) {
+          atomicAdd(grad_appearance + prims[j] * L::A + (p - NGO), value);
         } else {
           atomicAdd(grad_opacities + prims[j], value);
         }
