@@ -493,6 +493,7 @@ __device__ __forceinline__ uint64_t load_batch(float* rows, float* raw, float* r
       // 0..35 (input weights, biases) to NeuralRaw, 36..56 (output weights,
       // biases) to the row.
       constexpr bool kSplitRaw = Neural && Forward;
+      static_assert(!kSplitRaw || L::A % 2 == 1, "the paired gather writes the full raw layout");
       constexpr int kGeo = (kGeometry + kParts - 1) / kParts;
       const float* g = geometry + int64_t(ids[record]) * kGeometry;
       const int64_t prim_j = prims[record];
