@@ -1830,13 +1830,10 @@ __global__ __launch_bounds__(kTilePixels, Neural && !Replay ? 2 : 4) void render
           value = classic_appearance_gradient(sums + NG, rows + j * L::STRIDE, p - NG);
       }
       if (value != 0.f) {
-        if (p < NGO) {
-          atomicAdd(grad_geometry + int64_t(ids[j]) * kGeometry + p, value);
-        } else if (p < NGO + L::A) {
-          atomicAdd(grad_appearance + prims[j] * L::A + (p - NGO), value);
-        } else {
-          atomicAdd(grad_opacities + prims[j], value);
-        }
+        float* dst = p < NGO            ? grad_geometry + int64_t(ids[j]) * kGeometry + p
+                     : p < NGO + L::A ? grad_appearance + prims[j] * L::A + (p - NGO)
+                                      : grad_opacities + prims[j];
+        atomicAdd(dst, value);
       }
     }
     // The next batch overwrites ids/prims/rows; every flush must finish first.
