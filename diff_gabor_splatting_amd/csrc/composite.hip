@@ -443,25 +443,18 @@ __device__ __forceinline__ void shade(const float* r, const float* s, Shade& a) 
   }
 }
 
-// Stage `count` records: thread t < count brings record t's point-list
-// entry and primitive id (read one batch ahead by the caller, so that the
-// two dependent loads overlap the previous batch); every thread then
-// gathers raw fields into LDS, and one thread per record derives the row's
-// constants.
-// How a batch's rows are gathered: kGatherQuarters gives each record four
-// threads with fixed slices and issues all their loads before the LDS
-// writes (the forward); kGatherLoops strides the threads over the
-// concatenated rows, which holds fewer registers where the loop around it
-// already needs many (the backward).
-enum Gather { kGatherLoops, kGatherQuarters };
-
 // Which records a wave composites: kReachTest tests every record's footprint
 // against the wave's quadrant; kReplayMask reads the quadrant bits of a
 // replay entry (bit 28 + w: wave w's quadrant took the record in the
 // forward), staged per record in `entries`.
 enum Select { kReachTest, kReplayMask };
 
-template <bool Neural, Gather Mode, Select Which = kReachTest, bool Forward = false>
+// Stage `count` records: thread t < count brings record t's point-list
+// entry and primitive id (read one batch ahead by the caller, so that the
+// two dependent loads overlap the previous batch); four threads per record
+// then gather its raw fields into LDS, and one thread per record derives
+// the row's constants.
+template <bool Neural, Select Which = kReachTest, bool Forward = false>
 __device__ __forceinline__ uint64_t load_batch(float* rows, float* raw, float* reach_rows,
                                                int* ids, int64_t* prims, float tile_x,
                                                float tile_y,
@@ -477,7 +470,7 @@ __device__ __forceinline__ uint64_t load_batch(float* rows, float* raw, float* r
     if constexpr (Which == kReplayMask) entries[t] = entry;
   }
   __syncthreads();
-  if constexpr (Mode == kGatherQuarters) {
+  {
     // Four threads per record (record t / 4, quarter t % 4), each bringing a
     // fixed slice of the record's geometry row (17 floats), its appearance row
     // (pairs of floats when the row width is even and the array starts on an
@@ -561,34 +554,6 @@ __device__ __forceinline__ uint64_t load_batch(float* rows, float* raw, float* r
           if (f < kGeometry) dst[f] = gv[k];
         }
         if (q == kParts - 1) dst[kGeometry] = opacity;
-      }
-    }
-  } else {
-    // One loop per source array, consecutive threads on consecutive floats of
-    // a row: geometry (17 floats), opacity, appearance (pairs of floats when
-    // the row width is even and the array starts on an 8-byte boundary, as
-    // every row then does).
-    for (int idx = t; idx < count * kGeometry; idx += kTilePixels) {
-      const int j = idx / kGeometry;
-      const int f = idx - j * kGeometry;
-      raw[j * L::RAW_STRIDE + f] = geometry[int64_t(ids[j]) * kGeometry + f];
-    }
-    if (t < count) raw[t * L::RAW_STRIDE + kGeometry] = opacities[prims[t]];
-    const bool pairs = L::A % 2 == 0 && (reinterpret_cast<uintptr_t>(appearance) & 7u) == 0;
-    if (pairs) {
-      constexpr int kPairs = L::A / 2;
-      for (int idx = t; idx < count * kPairs; idx += kTilePixels) {
-        const int j = idx / kPairs;
-        const int f = idx - j * kPairs;
-        const float2 v = reinterpret_cast<const float2*>(appearance + prims[j] * L::A)[f];
-        raw[j * L::RAW_STRIDE + kGeometry + 1 + 2 * f] = v.x;
-        raw[j * L::RAW_STRIDE + kGeometry + 2 + 2 * f] = v.y;
-      }
-    } else {
-      for (int idx = t; idx < count * L::A; idx += kTilePixels) {
-        const int j = idx / L::A;
-        const int f = idx - j * L::A;
-        raw[j * L::RAW_STRIDE + kGeometry + 1 + f] = appearance[prims[j] * L::A + f];
       }
     }
   }
@@ -1087,7 +1052,7 @@ __device__ __forceinline__ int walk_list(const ForwardStage<Neural>& st, int ran
     const int64_t prim = next_prim;
     const bool ahead = int(threadIdx.x) < min(kBatch, end - start - kBatch);
     if (ahead) next_id = point_list[range_x + start + kBatch + threadIdx.x];
-    const uint64_t reach = load_batch<Neural, kGatherQuarters, kReachTest, true>(
+    const uint64_t reach = load_batch<Neural, kReachTest, true>(
         st.rows, st.raw, st.reach_rows, st.ids, st.prims, tile_x, tile_y, count, id, prim,
         geometry, appearance, opacities);
     if (ahead) next_prim = primitive_ids[next_id];
@@ -1650,7 +1615,7 @@ __global__ __launch_bounds__(kTilePixels, Neural && !Replay ? 2 : 4) void render
         next_id = point_list[range.x + start - kBatch - 1 - threadIdx.x];
       }
     }
-    const uint64_t reach = load_batch<Neural, kGatherLoops, Replay ? kReplayMask : kReachTest>(
+    const uint64_t reach = load_batch<Neural, Replay ? kReplayMask : kReachTest>(
         rows, raw, reach_rows, ids, prims, tile_x, tile_y, count, id, prim, geometry, appearance,
         opacities, entry, entries);
     if (ahead) next_prim = primitive_ids[next_id];
