@@ -147,6 +147,28 @@ def crop(values, x0: int, y0: int):
     return out
 
 
+class _MeanOfSquares(torch.autograd.Function):
+    """Mean of squares over several map groups, taken as one flat vector.
+
+    Forward: one multi-tensor pass for the groups' Euclidean norms (each
+    element read once), then a sum of the squared norms over n. Backward:
+    one multi-tensor pass writing each group's gradient g * 2 x / n. The
+    groups are never concatenated: the compositor's backward takes one
+    gradient tensor per map group, so a concatenated copy only costs a
+    read and a write of every map element.
+    """
+
+    @staticmethod
+    def forward(ctx, *groups):
+        ctx.save_for_backward(*groups)
+        ctx.count = sum(t.numel() for t in groups)
+        return torch.stack(torch._foreach_norm(list(groups))).square().sum() / ctx.count
+
+    @staticmethod
+    def backward(ctx, grad):
+        return tuple(torch._foreach_mul(list(ctx.saved_tensors), grad * (2.0 / ctx.count)))
+
+
 def _loss(rgb, alpha, meta, channels):
     """Mean of squares of the first `channels` map channels in the reference
     benchmark's order - rgb, alpha, depth, normals, distortion - its objective
@@ -154,28 +176,24 @@ def _loss(rgb, alpha, meta, channels):
     benchmark_rasterization.py:80-82, 133).
 
     Same value and gradient, less glue: a mean of squares does not depend on
-    the order of the elements, so the groups are concatenated flat - one
-    contiguous copy, where interleaving them into [pixels, 9] writes 4- to
-    12-byte pieces - and the backward hands each group a contiguous slice of
-    the gradient. Groups past `channels` are left out rather than sliced off
-    (a slice adds a zero-filled full-size gradient), and the mean of squares
-    is mse_loss against zero, whose backward is one fused kernel (2 x / n)
-    where square().mean() runs pow, mul, mul and div over the whole map.
+    the order or grouping of the elements, so each group enters as it is
+    (`_MeanOfSquares`). Groups past `channels` are left out rather than
+    sliced off (a slice adds a zero-filled full-size gradient).
     """
-    maps = _flat_maps(rgb, alpha, meta, channels)
-    return torch.nn.functional.mse_loss(maps, maps.new_zeros(()).expand_as(maps))
+    return _MeanOfSquares.apply(*_loss_groups(rgb, alpha, meta, channels))
 
 
-def _flat_maps(rgb, alpha, meta, channels):
-    """The loss's first `channels` map channels, concatenated flat."""
-    flat, left = [], channels
+def _loss_groups(rgb, alpha, meta, channels):
+    """The map groups holding the loss's first `channels` channels (the last
+    one sliced when it holds more)."""
+    groups, left = [], channels
     for t in (rgb, alpha, meta["accumulated_depth"], meta["normals"], meta["distortion"]):
         if left <= 0:
             break
         k = t.shape[-1]
-        flat.append((t if k <= left else t[..., :left]).reshape(-1))
+        groups.append(t if k <= left else t[..., :left])
         left -= k
-    return torch.cat(flat) if len(flat) > 1 else flat[0]
+    return groups
 
 
 def algorithmic_bytes(kind: str, neural: bool, pixels: int, records: int, pairs: int,
@@ -259,7 +277,7 @@ def graph_replay_times(steps: int, warmup: int, device, indices=None) -> dict:
     replayed: ms per replay next to the eager step.
 
     Inside ``fixed_capacity`` the renderers never synchronise with the host,
-    so one capture holds the render, the concatenation of the loss's maps
+    so one capture holds the render, the loss gradient's multi-tensor pass
     and the backward; a replay then costs the kernels alone. The loss's
     reduction stays out of the graph (torch's reduction records a memset
     node, which is not replay-safe here) and the backward receives the loss
@@ -281,9 +299,10 @@ def graph_replay_times(steps: int, warmup: int, device, indices=None) -> dict:
 
         def body():
             rgb, alpha, meta = renderer(**values, **options)
-            maps = _flat_maps(rgb, alpha, meta, cfg["channels"])
-            return torch.autograd.grad(maps, params,
-                                       grad_outputs=maps.detach() * (2.0 / maps.numel()))
+            groups = _loss_groups(rgb, alpha, meta, cfg["channels"])
+            scale = 2.0 / sum(t.numel() for t in groups)
+            return torch.autograd.grad(groups, params, grad_outputs=torch._foreach_mul(
+                [t.detach() for t in groups], scale))
 
         with fixed_capacity(1 << 26) as probe:
             renderer(**values, **options)
