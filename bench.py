@@ -241,19 +241,32 @@ def prepare(index: int, device, validate: bool):
     return cpu_values, values, renderer, options, step
 
 
-def time_steps(step, steps: int, warmup: int) -> float:
+def time_steps(step, steps: int, warmup: int, min_ms: float = 0.0) -> float:
     """Milliseconds per step over `steps` steps after `warmup` untimed ones,
     with the device synchronised on both sides of the timed region and the
-    garbage collector paused inside it."""
+    garbage collector paused inside it.
+
+    With `min_ms` > 0, a timed region shorter than that is measured again
+    over enough steps to fill it (the first region then counts as warm-up):
+    a 64x64 config steps in about half a millisecond, and ten of its steps
+    time the host's clock ramp more than the step."""
     for _ in range(warmup):
         step()
     torch.cuda.synchronize()
-    with paused_collector():
-        start = time.perf_counter()
-        for _ in range(steps):
-            step()
-        torch.cuda.synchronize()
-        return (time.perf_counter() - start) * 1000 / steps
+    while True:
+        with paused_collector():
+            start = time.perf_counter()
+            for _ in range(steps):
+                step()
+            torch.cuda.synchronize()
+            elapsed = (time.perf_counter() - start) * 1000
+        if elapsed >= min_ms:
+            return elapsed / steps
+        steps = math.ceil(min_ms / max(elapsed / steps, 1e-3))
+
+
+# Shortest timed region of a secondary (per-config or graph-replay) figure.
+MIN_CONFIG_MS = 250.0
 
 
 def per_config_times(skip: int, steps: int, warmup: int, device, validate: bool) -> dict:
@@ -263,7 +276,7 @@ def per_config_times(skip: int, steps: int, warmup: int, device, validate: bool)
         if index == skip:
             continue
         *_, step = prepare(index, device, validate)
-        ms = time_steps(step, steps, warmup)
+        ms = time_steps(step, steps, warmup, min_ms=MIN_CONFIG_MS)
         pixels = cfg["scenes"] * cfg["cameras"] * cfg["width"] * cfg["height"]
         out[str(index)] = {"workload": cfg["name"], "ms_per_step": round(ms, 4),
                            "mpix_per_s": round(pixels / (ms / 1000) / 1e6, 3)}
@@ -294,7 +307,7 @@ def graph_replay_times(steps: int, warmup: int, device, indices=None) -> dict:
         if indices is not None and index not in indices:
             continue
         _, values, renderer, options, step = prepare(index, device, False)
-        eager_ms = time_steps(step, steps, warmup)
+        eager_ms = time_steps(step, steps, warmup, min_ms=MIN_CONFIG_MS)
         params = [v for v in values.values() if v.requires_grad]
 
         def body():
@@ -318,15 +331,7 @@ def graph_replay_times(steps: int, warmup: int, device, indices=None) -> dict:
         graph = torch.cuda.CUDAGraph()
         with capacity, torch.cuda.graph(graph):
             grads = body()
-        for _ in range(warmup):
-            graph.replay()
-        torch.cuda.synchronize()
-        with paused_collector():
-            start = time.perf_counter()
-            for _ in range(steps):
-                graph.replay()
-            torch.cuda.synchronize()
-            replay_ms = (time.perf_counter() - start) * 1000 / steps
+        replay_ms = time_steps(graph.replay, steps, warmup, min_ms=MIN_CONFIG_MS)
         capacity.check()  # raises if any replay exceeded the capacity
         expected = body()
         worst = max(float(((g - e).abs().max() / e.abs().max().clamp_min(1e-30)).item())
