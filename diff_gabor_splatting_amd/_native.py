@@ -539,12 +539,15 @@ def records_forward(means, quaternions, scales, opacities, view_matrices, intrin
 
 def records_backward(means, quaternions, scales, view_matrices, intrinsics, sh, sh_degree,
                      row_of_pair, geometry, grad_geometry, grad_projected_means,
-                     grad_appearance, grad_opacity_rows):
+                     grad_appearance, grad_opacity_rows, camera_grads=True):
     """Gradients of (means, quaternions, scales, view_matrices, intrinsics) and,
-    with SH, of (first, second, weights, magnitudes, phases, opacities)."""
+    with SH, of (first, second, weights, magnitudes, phases, opacities).
+    With camera_grads False the camera adjoint is skipped and the view and
+    intrinsics gradients are None."""
     return _host.records_backward(means, quaternions, scales, view_matrices, intrinsics, sh,
                                   sh_degree, row_of_pair, geometry, grad_geometry,
-                                  grad_projected_means, grad_appearance, grad_opacity_rows)
+                                  grad_projected_means, grad_appearance, grad_opacity_rows,
+                                  bool(camera_grads))
 
 
 # --------------------------------------------------------------------------

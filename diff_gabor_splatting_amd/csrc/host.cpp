@@ -428,7 +428,8 @@ py::tuple records_backward(const at::Tensor& means, const at::Tensor& quaternion
                            const std::optional<at::Tensor>& grad_geometry_in,
                            const std::optional<at::Tensor>& grad_projected_in,
                            const std::optional<at::Tensor>& grad_appearance_in,
-                           const std::optional<at::Tensor>& grad_opacity_in) {
+                           const std::optional<at::Tensor>& grad_opacity_in,
+                           bool camera_grads) {
   require_bound();
   const at::Device device = means.device();
   const int64_t scenes = means.size(0), n = means.size(1);
@@ -451,8 +452,10 @@ py::tuple records_backward(const at::Tensor& means, const at::Tensor& quaternion
   const at::Tensor g_means = at::empty_like(means);
   const at::Tensor g_quats = at::empty_like(quaternions);
   const at::Tensor g_scales = at::empty_like(scales);
-  const at::Tensor g_views = at::empty_like(view_matrices);
-  const at::Tensor g_intrinsics = at::empty_like(intrinsics);
+  // Without camera_grads the camera adjoint is skipped (null pointers) and
+  // the camera gradients are returned as None.
+  const at::Tensor g_views = camera_grads ? at::empty_like(view_matrices) : at::Tensor();
+  const at::Tensor g_intrinsics = camera_grads ? at::empty_like(intrinsics) : at::Tensor();
   std::array<at::Tensor, 6> sh_grads;
   if (degree >= 0) {
     if (!grad_appearance.defined())
@@ -479,8 +482,8 @@ py::tuple records_backward(const at::Tensor& means, const at::Tensor& quaternion
   result[0] = g_means;
   result[1] = g_quats;
   result[2] = g_scales;
-  result[3] = g_views;
-  result[4] = g_intrinsics;
+  result[3] = camera_grads ? py::cast(g_views) : py::none();
+  result[4] = camera_grads ? py::cast(g_intrinsics) : py::none();
   for (int k = 0; k < 6; ++k)
     result[5 + k] = sh_grads[k].defined() ? py::cast(sh_grads[k]) : py::none();
   return result;

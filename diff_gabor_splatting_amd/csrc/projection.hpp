@@ -326,8 +326,11 @@ namespace {
 // over the cameras of its scene; `Source::fetch(pair, g)` supplies the output
 // gradients of a pair (false: the pair carries none). Surfel gradients are
 // written once; per-camera gradients are summed per workgroup into
-// partials[camera][block][21] for camera_reduce_kernel.
-template <class Source>
+// partials[camera][block][21] for camera_reduce_kernel. Without Cameras the
+// camera adjoint, its reduction and the per-camera barriers are compiled
+// out and `partials` is not touched (callers whose cameras take no
+// gradient).
+template <class Source, bool Cameras = true>
 __global__ __launch_bounds__(kProjectBlock, 5) void projection_backward_kernel(
     const float* __restrict__ means, const float* __restrict__ quats,
     const float* __restrict__ scales, const float* __restrict__ views,
@@ -360,17 +363,19 @@ __global__ __launch_bounds__(kProjectBlock, 5) void projection_backward_kernel(
       project_pair(s.R, s.mu, s.sc, V, K, p);
       pair_adjoint(s, V, K, p, g, gmu, gR, gs, cam_grad);
     }
-    const float total = wave_reduce_scatter<kCameraGrads>(cam_grad, lane);
-    const int param = rs_param<kCameraGrads>(lane);
-    if (param < kCameraGrads) wave_sums[wave][param] = total;
-    __syncthreads();
-    if (threadIdx.x < kCameraGrads) {
-      float acc = 0.f;
+    if constexpr (Cameras) {
+      const float total = wave_reduce_scatter<kCameraGrads>(cam_grad, lane);
+      const int param = rs_param<kCameraGrads>(lane);
+      if (param < kCameraGrads) wave_sums[wave][param] = total;
+      __syncthreads();
+      if (threadIdx.x < kCameraGrads) {
+        float acc = 0.f;
 #pragma unroll
-      for (int w = 0; w < kProjectBlock / 64; ++w) acc += wave_sums[w][threadIdx.x];
-      partials[(cam * gridDim.x + blockIdx.x) * kCameraGrads + threadIdx.x] = acc;
+        for (int w = 0; w < kProjectBlock / 64; ++w) acc += wave_sums[w][threadIdx.x];
+        partials[(cam * gridDim.x + blockIdx.x) * kCameraGrads + threadIdx.x] = acc;
+      }
+      __syncthreads();
     }
-    __syncthreads();
   }
   if (!valid) return;
   float gq[4];

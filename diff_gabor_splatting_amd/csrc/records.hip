@@ -579,8 +579,11 @@ int gs_records_backward(const float* means, const float* quaternions, const floa
   if (status != GS_OK) return status;
   GS_REQUIRE(sh_degree >= -1 && sh_degree <= 3, GS_ERR_ARGUMENT,
              "SH degree must be -1 (none) or 0 through 3");
-  GS_REQUIRE(grad_view_matrices && grad_intrinsics, GS_ERR_ARGUMENT,
+  // Both camera gradient pointers null: the caller's cameras take no
+  // gradient, and their adjoint is skipped.
+  GS_REQUIRE(!grad_view_matrices == !grad_intrinsics, GS_ERR_ARGUMENT,
              "null camera gradient pointer");
+  const bool camera_grads = grad_view_matrices != nullptr;
   GS_REQUIRE(!grad_projected_means || grad_projected_stride >= 2, GS_ERR_ARGUMENT,
              "projected-means gradient rows must be at least 2 floats apart, got %lld",
              static_cast<long long>(grad_projected_stride));
@@ -623,13 +626,19 @@ int gs_records_backward(const float* means, const float* quaternions, const floa
       GS_LAUNCHED("sh_rows_backward_kernel");
       sh_dirs = w.directions;
     }
-    projection_backward_kernel<RowGrads><<<grid, kProjectBlock, 0, s>>>(
-        means, quaternions, scales, view_matrices, intrinsics, cameras, n,
-        RowGrads{row_of_pair, grad_geometry, grad_projected_means, grad_projected_stride,
-                 sh_dirs},
-        grad_means, grad_quaternions, grad_scales, w.partials);
+    const RowGrads source{row_of_pair, grad_geometry, grad_projected_means,
+                          grad_projected_stride, sh_dirs};
+    if (camera_grads)
+      projection_backward_kernel<RowGrads, true><<<grid, kProjectBlock, 0, s>>>(
+          means, quaternions, scales, view_matrices, intrinsics, cameras, n, source,
+          grad_means, grad_quaternions, grad_scales, w.partials);
+    else
+      projection_backward_kernel<RowGrads, false><<<grid, kProjectBlock, 0, s>>>(
+          means, quaternions, scales, view_matrices, intrinsics, cameras, n, source,
+          grad_means, grad_quaternions, grad_scales, nullptr);
     GS_LAUNCHED("projection_backward_kernel");
   }
+  if (!camera_grads) return GS_OK;
   camera_reduce_kernel<<<static_cast<unsigned>(scenes * cameras), kProjectBlock, 0, s>>>(
       w.partials, blocks, grad_view_matrices, grad_intrinsics);
   GS_LAUNCHED("camera_reduce_kernel");

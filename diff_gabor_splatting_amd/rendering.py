@@ -163,6 +163,7 @@ class ProjectRecords(torch.autograd.Function):
             means, quats, scales, views, intrinsics,
             None if sh_degree is None else (first, second), sh_degree, rows, geometry,
             g_geometry, g_projected, g_appearance, g_opacity,
+            camera_grads=ctx.needs_input_grad[4] or ctx.needs_input_grad[5],
         )
         g_means, g_quats, g_scales, g_views, g_intrinsics = grads[:5]
         g_first, g_second, g_weights, g_magnitudes, g_phases, g_opacities = grads[5:]

@@ -126,7 +126,10 @@ size_t gs_records_backward_workspace_size(int64_t scenes, int64_t cameras, int64
  * camera gradients are overwritten: means, quaternions, scales,
  * view_matrices [S,C,4,4], intrinsics [S,C,3,3], and with SH the
  * coefficients [S,N,K,3] x2, weights/magnitudes/phases [S,N,4] and
- * opacities [S,N], each summed over cameras without atomics. */
+ * opacities [S,N], each summed over cameras without atomics.
+ * grad_view_matrices and grad_intrinsics may both be null (cameras that
+ * take no gradient): the camera adjoint and its reduction are then skipped.
+ * One null and one not is an argument error. */
 int gs_records_backward(const float* means, const float* quaternions, const float* scales,
                         const float* view_matrices, const float* intrinsics,
                         const float* sh_first, const float* sh_second, int32_t sh_degree,

@@ -419,3 +419,14 @@ def test_records_match_oracle(native, packed, sh, n):
         e = torch.zeros_like(leaves[name]) if e is None else e
         assert_gradients_close(got[index], e.reshape(got[index].shape), name, rel_norm=1e-4,
                                elem=1e-4, rtol=1e-4)
+    # Cameras that take no gradient: the camera adjoint is skipped, the
+    # camera gradients are None and every surfel gradient is the same bits
+    # (the projection adjoint sums over cameras without atomics).
+    plain = native.records_backward(
+        gpu["means"], gpu["quaternions"], gpu["scales"], gpu["view_matrices"],
+        gpu["intrinsics"], sh_args, sh, out["row_of_pair"], out["geometry"],
+        to_gpu(g_geometry), to_gpu(g_projected), to_gpu(g_app), to_gpu(g_op),
+        camera_grads=False)
+    assert plain[3] is None and plain[4] is None
+    for index in [0, 1, 2] + order[5:]:
+        assert torch.equal(plain[index], got[index]), names[order.index(index)]

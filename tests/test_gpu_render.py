@@ -423,3 +423,27 @@ def test_retained_graph_backward_twice(method):
     with torch.no_grad():
         plain = maps_from_result(renderer(method)(**values, width=19, height=13))
     torch.testing.assert_close(plain, maps.detach())
+
+
+@pytest.mark.parametrize("method", ["classic", "neural"])
+def test_fixed_cameras_skip_camera_gradients(method):
+    """Cameras that do not require gradients get none, and the surfel
+    gradients equal those of a render whose cameras do (to the order of the
+    compositor's float atomics)."""
+    inputs = make_inputs(method, cameras=2, primitives=9)
+    fixed = on_gpu(inputs)
+    for key in ("view_matrices", "intrinsics"):
+        fixed[key] = fixed[key].detach()
+    full = on_gpu(inputs)
+    for values in (fixed, full):
+        maps = maps_from_result(renderer(method)(**values, width=19, height=13))
+        weights = torch.linspace(-1.0, 1.0, maps.numel(), device=DEVICE).reshape(maps.shape)
+        (maps * weights).sum().backward()
+    assert fixed["view_matrices"].grad is None and fixed["intrinsics"].grad is None
+    assert full["view_matrices"].grad is not None and full["intrinsics"].grad is not None
+    for name, value in fixed.items():
+        if not value.requires_grad:
+            continue
+        want = full[name].grad
+        scale = max(float(want.abs().max()), 1.0)
+        torch.testing.assert_close(value.grad, want, atol=1e-6 * scale, rtol=1e-5, msg=name)
