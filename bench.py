@@ -347,8 +347,8 @@ def graph_replay_times(steps: int, warmup: int, device, indices=None) -> dict:
 def main(argv=None):
     parser = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     parser.add_argument("--gpus", type=int, default=1)
-    parser.add_argument("--steps", type=int, default=10)
-    parser.add_argument("--warmup", type=int, default=3)
+    parser.add_argument("--steps", type=int, default=100)
+    parser.add_argument("--warmup", type=int, default=20)
     parser.add_argument("--config", type=int, default=4, choices=sorted(CONFIGS))
     parser.add_argument("--validate", action="store_true",
                         help="run the numerical input checks inside every step")
