@@ -211,11 +211,17 @@ struct ExclusiveStartStore {
 // Stage 2, step 1: lane j of the grid takes depth rank j (its pair, the
 // rectangle stage 1 stored and its first entry) and writes the pair's tiles
 // row-major as 32-bit tile ids plus the pair index. A pair with at most
-// kLaneTiles tiles is written by its own lane; larger ones are written by
+// `lane_tiles` tiles is written by its own lane; larger ones are written by
 // the whole wave, one pair at a time, 64 consecutive entries per store, so
 // that a few huge rectangles do not serialise their wave. Entries at or
-// past m (inconsistent inputs) are dropped.
+// past m (inconsistent inputs) are dropped. The limit only distributes the
+// work: every entry is written to the same place whatever it is.
+// kLaneTiles suits rectangles of ~18 tiles on average (1M surfels at
+// 1080p); scenes whose mean rectangle exceeds kWideMean tiles emit faster
+// with kWideLaneTiles (the host picks it when it knows M and V).
 constexpr int kLaneTiles = 32;
+constexpr int kWideLaneTiles = 8;
+constexpr int kWideMean = 24;
 
 // `m` is the capacity of tile_ids/values; `total` (a device int64, or null
 // when it equals m) the emission's full length, which may exceed it: entries
@@ -230,7 +236,7 @@ __global__ __launch_bounds__(256) void emit_sorted_kernel(
     int64_t count, int64_t m, const int64_t* __restrict__ total_count, uint32_t* status,
     int tw, const int* __restrict__ order, const int64_t* __restrict__ starts,
     const int4* __restrict__ rects, uint32_t* __restrict__ tile_ids, int* __restrict__ values,
-    int rank_bits) {
+    int rank_bits, int lane_tiles) {
   const int lane = __lane_id();
   const int64_t j = int64_t(blockIdx.x) * 256 + threadIdx.x;
   if (j - lane >= count) return;  // uniform per wave
@@ -250,7 +256,7 @@ __global__ __launch_bounds__(256) void emit_sorted_kernel(
   }
   // Packed entries carry the depth rank j in their low bits.
   const uint32_t low = uint32_t(j);
-  if (area <= kLaneTiles) {
+  if (area <= lane_tiles) {
     int x = rect.x, y = rect.y;
     for (int k = 0; k < area; ++k) {
       const int64_t e = first + k;
@@ -269,7 +275,7 @@ __global__ __launch_bounds__(256) void emit_sorted_kernel(
       }
     }
   }
-  uint64_t big = __ballot(area > kLaneTiles);
+  uint64_t big = __ballot(area > lane_tiles);
   while (big) {  // uniform: every lane sees the same mask
     const int owner = __ffsll((unsigned long long)big) - 1;
     big &= big - 1;
@@ -587,6 +593,8 @@ int bin_tiles(const int32_t* order, const int64_t* starts, const int32_t* rects,
   const int tile_bits = id_bits(tiles);
   const int rank_bits = id_bits(visible >= 0 ? min(visible, count) : count);
   const bool packed = tile_bits + rank_bits <= 32;
+  const int lane_tiles =
+      (!live && visible > 0 && m > int64_t(kWideMean) * visible) ? kWideLaneTiles : kLaneTiles;
   const int4* rect_rows = reinterpret_cast<const int4*>(rects);
   {
     ProfileScope prof(GS_PROF_BINNING, s);
@@ -596,7 +604,7 @@ int bin_tiles(const int32_t* order, const int64_t* starts, const int32_t* rects,
     GS_REQUIRE(order && starts && rects, GS_ERR_ARGUMENT, "null pointer passed to gs_bin_tiles");
     if (m == 0) {  // a zero capacity still reports an overflowing emission
       emit_sorted_kernel<false><<<unsigned(ceil_div(count, 256)), 256, 0, s>>>(
-          count, 0, live, status, tw, order, starts, rect_rows, nullptr, nullptr, 0);
+          count, 0, live, status, tw, order, starts, rect_rows, nullptr, nullptr, 0, lane_tiles);
       GS_LAUNCHED("emit_sorted_kernel");
       return GS_OK;
     }
@@ -604,10 +612,11 @@ int bin_tiles(const int32_t* order, const int64_t* starts, const int32_t* rects,
     if (packed) {
       emit_sorted_kernel<true><<<unsigned(ceil_div(count, 256)), 256, 0, s>>>(
           count, m, live, status, tw, order, starts, rect_rows, w.tile_ids, nullptr,
-          rank_bits);
+          rank_bits, lane_tiles);
     } else {
       emit_sorted_kernel<false><<<unsigned(ceil_div(count, 256)), 256, 0, s>>>(
-          count, m, live, status, tw, order, starts, rect_rows, w.tile_ids, w.tile_values, 0);
+          count, m, live, status, tw, order, starts, rect_rows, w.tile_ids, w.tile_values, 0,
+          lane_tiles);
     }
     GS_LAUNCHED("emit_sorted_kernel");
   }
