@@ -33,218 +33,46 @@ import time
 
 import torch
 
-from diff_gabor_splatting_amd.timing import paused_collector
+from diff_gabor_splatting_amd.timing import collected_collector, paused_collector
+from diff_gabor_splatting_amd.workloads import (CAMERA_KEYS, CONFIGS, crop, loss as _loss,
+                                                 loss_groups as _loss_groups, make_scene,
+                                                 prepare)
 
 HBM_PEAK_GBS = 8000.0
 COPY_BYTES = 1 << 30
-FP32_VALU_PEAK_TFLOPS = 157.3
 
-CONFIGS = {
-    0: dict(name="config0: classic SH0, N=1024, 64x64", n=1024, width=64, height=64, scenes=1,
-            cameras=1, sh=0, neural=False, packed=False, channels=9),
-    1: dict(name="config1: classic SH3, N=100k, 1024x768, rgb+alpha+depth loss", n=100_000,
-            width=1024, height=768, scenes=1, cameras=1, sh=3, neural=False, packed=False,
-            channels=5),
-    2: dict(name="config2: neural SIREN, N=100k, 800x800", n=100_000, width=800, height=800,
-            scenes=1, cameras=1, sh=None, neural=True, packed=False, channels=9),
-    3: dict(name="config3: classic SH3, 8 scenes x 4 cameras, N=50k/scene, 512x512, packed",
-            n=50_000, width=512, height=512, scenes=8, cameras=4, sh=3, neural=False,
-            packed=True, channels=9),
-    4: dict(name="config4: classic SH3, N=1M surfels, 1920x1080, all 9 maps in loss",
-            n=1_000_000, width=1920, height=1080, scenes=1, cameras=1, sh=3, neural=False,
-            packed=False, channels=9),
-}
+RECORD_BYTES_CLASSIC = 4 + 8 + 68 + 4 * 18 + 4  # point list, primitive id, geometry, appearance, opacity
+REPLAY_ENTRY_BYTES = 8  # replay entry {pair, position | quadrant bits} instead of the point list
 
 
-def _uniform(generator, shape, low, high):
-    return torch.rand(shape, generator=generator) * (high - low) + low
-
-
-def _log_uniform(generator, shape, low, high):
-    return torch.exp(_uniform(generator, shape, math.log(low), math.log(high)))
-
-
-def _ring_cameras(generator, scenes, cameras, radius=5.0):
-    """Rigid world->camera views on a ring around the origin, looking at it."""
-    views = torch.zeros(scenes, cameras, 4, 4)
-    for s in range(scenes):
-        for c in range(cameras):
-            yaw = float(_uniform(generator, (), 0.0, 2 * math.pi))
-            centre = torch.tensor([radius * math.sin(yaw), 0.0, -radius * math.cos(yaw)])
-            forward = -centre / centre.norm()
-            down = torch.tensor([0.0, 1.0, 0.0])
-            right = torch.linalg.cross(down, forward)
-            right = right / right.norm()
-            down = torch.linalg.cross(forward, right)
-            R = torch.stack([right, down, forward])  # rows: camera axes in world
-            views[s, c, :3, :3] = R
-            views[s, c, :3, 3] = -R @ centre
-            views[s, c, 3, 3] = 1.0
-    return views
-
-
-def make_scene(index: int, seed: int | None = None, n: int | None = None):
-    """Seeded CPU tensors of one BASELINE config (see BASELINE.json `configs`)."""
-    cfg = CONFIGS[index]
-    g = torch.Generator().manual_seed(index if seed is None else seed)
-    S, C = cfg["scenes"], cfg["cameras"]
-    N = cfg["n"] if n is None else n
-    W, H = cfg["width"], cfg["height"]
-    if index == 0:
-        means = torch.cat([_uniform(g, (S, N, 2), -1, 1), _uniform(g, (S, N, 1), 2, 4)], -1)
-    elif index in (1, 2):
-        means = torch.cat([_uniform(g, (S, N, 2), -3, 3), _uniform(g, (S, N, 1), 2, 8)], -1)
-    elif index == 3:
-        means = _uniform(g, (S, N, 3), -2, 2)
-    else:
-        centres = torch.cat([_uniform(g, (64, 2), -5, 5), _uniform(g, (64, 1), 2, 12)], -1)
-        which = torch.randint(0, 64, (S, N), generator=g)
-        means = centres[which] + torch.randn(S, N, 3, generator=g) * 0.3
-    quats = torch.randn(S, N, 4, generator=g)
-    quats = quats / quats.norm(dim=-1, keepdim=True)
-    low, high = (0.005, 0.1) if index == 4 else (0.02, 0.2)
-    scales = _log_uniform(g, (S, N, 2), low, high)
-    opacities = _uniform(g, (S, N), 0.1, 0.9)
-    if index == 3:
-        views = _ring_cameras(g, S, C)
-    else:
-        views = torch.eye(4).expand(S, C, 4, 4).clone()
-    focal = {0: 80.0, 1: 900.0, 2: 900.0, 3: 600.0, 4: 1500.0}[index]
-    cx, cy = (32.0, 32.0) if index == 0 else ((W - 1) / 2, (H - 1) / 2)
-    K = torch.tensor([[focal, 0.0, cx], [0.0, focal, cy], [0.0, 0.0, 1.0]])
-    values = dict(means=means, quaternions=quats, scales=scales, opacities=opacities,
-                  view_matrices=views, intrinsics=K.expand(S, C, 3, 3).clone())
-    if cfg["neural"]:
-        values.update(
-            input_weights=_uniform(g, (S, N, 6, 5), -1 / 5, 1 / 5),
-            input_biases=torch.zeros(S, N, 6),
-            output_weights=_uniform(g, (S, N, 3, 6), -1 / 30, 1 / 30),
-            output_biases=torch.zeros(S, N, 3),
-        )
-    else:
-        k = (cfg["sh"] + 1) ** 2
-        weights = _uniform(g, (S, N, 4), 0, 1)
-        values.update(
-            colors=_uniform(g, (S, N, k, 3), 0, 1),
-            secondary_colors=_uniform(g, (S, N, k, 3), 0, 1),
-            frequency_weights=weights / weights.sum(-1, keepdim=True),
-            frequency_magnitudes=_uniform(g, (S, N, 4), 0, 8),
-            phases=_uniform(g, (S, N, 4), 0, 2 * math.pi),
-        )
-    return values
-
-
-CAMERA_KEYS = ("view_matrices", "intrinsics")
-
-
-def crop(values, x0: int, y0: int):
-    """The same scene seen through a window whose top-left pixel is (x0, y0)."""
-    out = dict(values)
-    K = values["intrinsics"].clone()
-    K[..., 0, 2] -= x0
-    K[..., 1, 2] -= y0
-    out["intrinsics"] = K
-    return out
-
-
-class _MeanOfSquares(torch.autograd.Function):
-    """Mean of squares over several map groups, taken as one flat vector.
-
-    Forward: one multi-tensor pass for the groups' Euclidean norms (each
-    element read once), then a sum of the squared norms over n. Backward:
-    one multi-tensor pass writing each group's gradient g * 2 x / n. The
-    groups are never concatenated: the compositor's backward takes one
-    gradient tensor per map group, so a concatenated copy only costs a
-    read and a write of every map element.
-    """
-
-    @staticmethod
-    def forward(ctx, *groups):
-        ctx.save_for_backward(*groups)
-        ctx.count = sum(t.numel() for t in groups)
-        return torch.stack(torch._foreach_norm(list(groups))).square().sum() / ctx.count
-
-    @staticmethod
-    def backward(ctx, grad):
-        return tuple(torch._foreach_mul(list(ctx.saved_tensors), grad * (2.0 / ctx.count)))
-
-
-def _loss(rgb, alpha, meta, channels):
-    """Mean of squares of the first `channels` map channels in the reference
-    benchmark's order - rgb, alpha, depth, normals, distortion - its objective
-    ``torch.cat(maps, -1).square().mean()`` (benchmarks/
-    benchmark_rasterization.py:80-82, 133).
-
-    Same value and gradient, less glue: a mean of squares does not depend on
-    the order or grouping of the elements, so each group enters as it is
-    (`_MeanOfSquares`). Groups past `channels` are left out rather than
-    sliced off (a slice adds a zero-filled full-size gradient).
-    """
-    return _MeanOfSquares.apply(*_loss_groups(rgb, alpha, meta, channels))
-
-
-def _loss_groups(rgb, alpha, meta, channels):
-    """The map groups holding the loss's first `channels` channels (the last
-    one sliced when it holds more)."""
-    groups, left = [], channels
-    for t in (rgb, alpha, meta["accumulated_depth"], meta["normals"], meta["distortion"]):
-        if left <= 0:
-            break
-        k = t.shape[-1]
-        groups.append(t if k <= left else t[..., :left])
-        left -= k
-    return groups
-
-
-def algorithmic_bytes(kind: str, neural: bool, pixels: int, records: int, pairs: int,
-                      rows: int) -> int:
+def algorithmic_bytes(kind: str, neural: bool, pixels: int, records: int, rows: int,
+                      entry_bytes: int = 4) -> int:
     """Compulsory HBM bytes of one compositor launch.
 
-    pixels: output pixels; records: tile-records the kernel walks (each gathers
-    point_list 4 B + primitive id 8 B + geometry 68 B + appearance 4A B +
-    opacity 4 B); pairs/rows: gradient rows written once by the backward.
-    Forward writes maps 36 B + state 12 B + contributors 4 B per pixel; the
-    backward reads the same 52 B per pixel.
+    pixels: output pixels; records: tile-records the kernel walks, each
+    gathering its list entry (`entry_bytes`: 4 B of point list, or 8 B of
+    replay entry) + primitive id 8 B + geometry 68 B + appearance 4A B +
+    opacity 4 B; rows: visible pairs, whose gradient rows (geometry 68 B,
+    appearance 4A B, opacity 4 B) the backward writes once. The forward
+    writes maps 36 B + state 12 B + contributors 4 B per pixel; the backward
+    reads the same 52 B per pixel.
     """
     appearance = 57 if neural else 18
-    record = 4 + 8 + 68 + 4 * appearance + 4
+    record = entry_bytes + 8 + 68 + 4 * appearance + 4
     total = pixels * 52 + records * record
     if kind == "render_backward":
-        total += pairs * 68 + rows * (4 * appearance + 4)
+        total += rows * (68 + 4 * appearance + 4)
     return int(total)
 
 
-def prepare(index: int, device, validate: bool):
-    """Seeded inputs of one config on the device and a closure running one
-    fwd+bwd step on them through the public API."""
-    from diff_gabor_splatting_amd import rasterize_gabors, rasterize_neural_gabors
-
-    cfg = CONFIGS[index]
-    cpu_values = make_scene(index)
-    values = {k: v.to(device).contiguous() for k, v in cpu_values.items()}
-    for k, v in values.items():
-        v.requires_grad_(k not in CAMERA_KEYS)
-    renderer = rasterize_neural_gabors if cfg["neural"] else rasterize_gabors
-    options = dict(width=cfg["width"], height=cfg["height"], packed=cfg["packed"],
-                   validate=validate)
-    if not cfg["neural"]:
-        options["sh_degree"] = cfg["sh"]
-    params = [v for v in values.values() if v.requires_grad]
-
-    def step():
-        for p in params:
-            p.grad = None
-        rgb, alpha, meta = renderer(**values, **options)
-        _loss(rgb, alpha, meta, cfg["channels"]).backward()
-        return meta
-
-    return cpu_values, values, renderer, options, step
-
-
-def time_steps(step, steps: int, warmup: int, min_ms: float = 0.0) -> float:
+def time_steps(step, steps: int, warmup: int, min_ms: float = 0.0,
+               pause_collector: bool = False) -> float:
     """Milliseconds per step over `steps` steps after `warmup` untimed ones,
-    with the device synchronised on both sides of the timed region and the
-    garbage collector paused inside it.
+    with the device synchronised on both sides of the timed region. The
+    garbage collector runs a full collection before the region and stays
+    enabled inside it, as in a training loop (`pause_collector`: it stays
+    off inside, which keeps a generation-2 collection of torch's ~170k
+    tracked objects, ~40 ms of host time, out of a short region).
 
     With `min_ms` > 0, a timed region shorter than that is measured again
     over enough steps to fill it (the first region then counts as warm-up):
@@ -253,8 +81,9 @@ def time_steps(step, steps: int, warmup: int, min_ms: float = 0.0) -> float:
     for _ in range(warmup):
         step()
     torch.cuda.synchronize()
+    collector = paused_collector if pause_collector else collected_collector
     while True:
-        with paused_collector():
+        with collector():
             start = time.perf_counter()
             for _ in range(steps):
                 step()
@@ -402,11 +231,17 @@ def main(argv=None):
     # Workload statistics of the last step (outside the timed region).
     stats = workload_stats(values, renderer, options)
     dominant = max(("render_forward", "render_backward"), key=lambda f: kernels[f]["ms_per_step"])
-    walked = stats["records_backward" if dominant == "render_backward" else "records_forward"]
-    algo = algorithmic_bytes(dominant, cfg["neural"], pixels, walked, stats["pairs"],
-                             stats["rows"])
     avg_ms = kernels[dominant]["avg_launch_ms"]
-    achieved = algo / (avg_ms / 1000) / 1e9 if avg_ms else 0.0
+    roofline = roofline_entry(dominant, cfg, pixels, stats, avg_ms)
+    walk = measured_walk(cfg["name"])
+    evals_forward = walk["forward_pixel_record_visits"] if walk else None
+    # Surfel-pixel evaluations per second: the forward's visits (each pixel's
+    # list records up to the one that stops it, from the diagnostics build's
+    # count of this workload) plus the backward's walk as the reference
+    # defines it (every tile's 256 pixels up to its largest contributor count).
+    evaluations = (None if evals_forward is None else
+                   round((evals_forward + stats["evals_backward"]) / (ms_per_step / 1000), 1))
+    secondary = secondary_step_times(args, device, ms_per_step)
     result = {
         "metric": "fwd+bwd Mpix/s (1M surfels at 1080p); fwd+bwd ms/iter; HBM roofline",
         "value": round(mpix, 3),
@@ -430,26 +265,23 @@ def main(argv=None):
             "neural": cfg["neural"],
             "packed": cfg["packed"],
             "validate": args.validate,
+            "objective": "mean of squares of the listed map channels as one multi-tensor pass "
+                         "(value and gradient of torch.cat(maps, -1).square().mean()); the "
+                         "reference's literal expression is timed in secondary",
+            "garbage_collector": "enabled in the timed region (full collection before it)",
             "tile_intersections": stats["intersections"],
             "visible_pairs": stats["visible"],
-            "pixel_record_pairs_walked_per_s": round(
-                (stats["evals_forward"] + stats["evals_backward"]) / (ms_per_step / 1000), 1
-            ),
+            "records_replayed": stats["records_replayed"],
+            "surfel_pixel_evaluations_per_s": evaluations,
+            "surfel_pixel_evaluations": {
+                "forward_visits": evals_forward,
+                "backward_reference_walk": stats["evals_backward"],
+                "source": walk["source"] if walk else None,
+            },
         },
-        "roofline": {
-            "kernel": dominant,
-            "bound": "hbm",
-            "achieved": round(achieved, 2),
-            "peak": HBM_PEAK_GBS,
-            "unit": "GB/s",
-            "frac": round(achieved / HBM_PEAK_GBS, 5),
-            "traffic": measured_traffic(dominant, cfg["name"]),
-            "algorithmic_bytes_per_launch": algo,
-            "avg_launch_ms": round(avg_ms, 4),
-            "note": "the compositors are bound by VALU issue, not HBM: see valu",
-            "valu": measured_valu(dominant, cfg["name"], avg_ms),
-        },
+        "roofline": roofline,
         "kernels": {k: round(v["ms_per_step"], 4) for k, v in kernels.items()},
+        "secondary": secondary,
         "gpu": torch.cuda.get_device_name(device),
     }
     del values, step
@@ -482,8 +314,9 @@ def copy_calibration() -> int:
 
 
 # One wave64 VALU instruction issues per SIMD every 4 cycles: 256 CUs x 4
-# SIMDs at 2.4 GHz.
+# SIMDs at 2.4 GHz; 64 lanes each.
 VALU_ISSUE_PER_S = 256 * 4 * 2.4e9 / 4
+VALU_LANE_OPS_PEAK_T = VALU_ISSUE_PER_S * 64 / 1e12
 
 
 def measured_valu(kernel: str, workload: str, avg_ms: float):
@@ -510,6 +343,86 @@ def measured_valu(kernel: str, workload: str, avg_ms: float):
             "profiled_busy_measured": summary.get("busy_measured"),
             "profiled_lds_busy": summary.get("lds_busy"),
             "source": summary.get("source")}
+
+
+def roofline_entry(kernel: str, cfg: dict, pixels: int, stats: dict, avg_ms: float) -> dict:
+    """The dominant compositor's roofline: VALU issue (its bound) as the
+    primary figure, HBM beside it.
+
+    VALU: SQ_INSTS_VALU per launch from the committed counter summary of
+    this workload, times 64 lanes, over the launch time measured in this
+    run, against the non-packed fp32 issue ceiling (one wave64 instruction
+    per SIMD every 4 cycles on 256 CUs at 2.4 GHz = 39.3 T lane-ops/s;
+    packed FP32 is disabled in this build). HBM: algorithmic bytes of the
+    reference's walk (every tile's records up to its largest contributor
+    count) and of the walk this kernel performs (the replayed records), the
+    measured L2-to-memory traffic and its ratio to both.
+    """
+    walked = stats["records_backward" if kernel == "render_backward" else "records_forward"]
+    reference_bytes = algorithmic_bytes(kernel, cfg["neural"], pixels, walked, stats["visible"])
+    replay_bytes = algorithmic_bytes(kernel, cfg["neural"], pixels, stats["records_replayed"],
+                                     stats["visible"], entry_bytes=REPLAY_ENTRY_BYTES)
+    seconds = avg_ms / 1000 if avg_ms else None
+    traffic = measured_traffic(kernel, cfg["name"])
+    hbm = {
+        "achieved": round(reference_bytes / seconds / 1e9, 2) if seconds else None,
+        "peak": HBM_PEAK_GBS,
+        "unit": "GB/s",
+        "frac": round(reference_bytes / seconds / 1e9 / HBM_PEAK_GBS, 5) if seconds else None,
+        "algorithmic_bytes_per_launch": reference_bytes,
+        "replay_walk_bytes_per_launch": replay_bytes,
+        "achieved_replay_walk": round(replay_bytes / seconds / 1e9, 2) if seconds else None,
+        "traffic": traffic,
+        "traffic_over_reference_walk": round(traffic / reference_bytes, 3) if traffic else None,
+        "traffic_over_replay_walk": round(traffic / replay_bytes, 3) if traffic else None,
+    }
+    valu = measured_valu(kernel, cfg["name"], avg_ms)
+    entry = {"kernel": kernel, "avg_launch_ms": round(avg_ms, 4)}
+    if valu is None:
+        # No counter summary for this workload: the HBM figures only.
+        entry.update(bound="hbm", achieved=hbm["achieved"], peak=HBM_PEAK_GBS, unit="GB/s",
+                     frac=hbm["frac"], traffic=traffic, hbm=hbm)
+        return entry
+    lane_ops = valu["instructions"] * 64 / seconds / 1e12
+    entry.update(bound="valu", achieved=round(lane_ops, 3), peak=round(VALU_LANE_OPS_PEAK_T, 4),
+                 unit="T VALU lane-ops/s", frac=round(lane_ops / VALU_LANE_OPS_PEAK_T, 4),
+                 traffic=traffic, hbm=hbm, valu=valu)
+    return entry
+
+
+def measured_walk(workload: str):
+    """(pixel, record) counts of ``workload`` from the committed summary of
+    the diagnostics build (``python -m diff_gabor_splatting_amd.diagnostics``),
+    or None when no summary covers it. The counts are deterministic: they
+    follow from the sorted lists and the forward's float results."""
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
+                        "render_walk_counts.json")
+    try:
+        with open(path) as handle:
+            summaries = json.load(handle)
+    except (OSError, ValueError):
+        return None
+    for summary in summaries.get("workloads", []):
+        if summary.get("workload") == workload:
+            return {**summary, "source": "profiles/render_walk_counts.json"}
+    return None
+
+
+def secondary_step_times(args, device, headline_ms: float) -> dict:
+    """The headline step timed two other ways, labelled: with the collector
+    paused inside the timed region, and with the reference benchmark's
+    literal objective (torch.cat of the maps, square, mean)."""
+    out = {}
+    _, _, _, _, step = prepare(args.config, device, args.validate)
+    out["collector_paused_ms_per_step"] = round(
+        time_steps(step, args.steps, args.warmup, pause_collector=True), 4)
+    del step
+    _, _, _, _, step = prepare(args.config, device, args.validate, objective="reference")
+    out["reference_objective_ms_per_step"] = round(time_steps(step, args.steps, args.warmup), 4)
+    out["headline_ms_per_step"] = round(headline_ms, 4)
+    del step
+    torch.cuda.empty_cache()
+    return out
 
 
 def measured_traffic(kernel: str, workload: str):
@@ -553,7 +466,8 @@ def workload_stats(values, renderer, options):
         finally:
             _native.rasterize_forward = original
     maps, point_list, ranges, state, contributors = captured["out"][:5]
-    geometry, appearance = captured["args"][0], captured["args"][1]
+    replay = captured["out"][5] if len(captured["out"]) > 5 else None
+    geometry = captured["args"][0]
     width, height = options["width"], options["height"]
     tw, th = _native.tile_grid(width, height)
     lengths = (ranges[:, 1] - ranges[:, 0]).long()
@@ -562,16 +476,16 @@ def workload_stats(values, renderer, options):
     contrib = torch.nn.functional.pad(contributors, (0, pad_w, 0, pad_h))
     per_tile = contrib.reshape(images, th, 16, tw, 16).permute(0, 1, 3, 2, 4).reshape(-1, 256)
     tile_max = per_tile.max(-1).values.long()
-    # (pixel, record) pairs walked: the backward walks every tile up to its
-    # largest contributor count; the forward at most the whole tile list.
+    # The backward as the reference walks it: every tile up to its largest
+    # contributor count; with replay lists it gathers only the replayed
+    # records (those some pixel took).
     return {
         "intersections": int(point_list.numel()),
         "visible": int((captured["args"][5] > 0).sum()),
         "pairs": int(geometry.shape[0]),
-        "rows": int(appearance.shape[0]),
         "records_forward": int(lengths.sum()),
         "records_backward": int(tile_max.sum()),
-        "evals_forward": int(lengths.sum()) * 256,
+        "records_replayed": int(replay[1].long().sum()) if replay is not None else None,
         "evals_backward": int(tile_max.sum()) * 256,
     }
 

@@ -184,7 +184,7 @@ _SIGNATURES = {
     "gs_profile_enable": (_c_int, [_c_int]),
     "gs_profile_read": (_c_int, [_c_int, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(_c_i64)]),
     "gs_diagnostics_query": (_c_int, [ctypes.POINTER(_c_int), ctypes.POINTER(_c_int)]),
-    "gs_diagnostics_set": (_c_int, [_c_ptr, _c_ptr, _c_ptr, _c_i64]),
+    "gs_diagnostics_set": (_c_int, [_c_ptr, _c_ptr, _c_ptr, _c_i64, _c_ptr]),
 }
 
 PROFILE_FAMILIES = {
@@ -232,6 +232,7 @@ def _bind_host(library: ctypes.CDLL) -> None:
 
 lib = _load()
 _bind_host(lib)
+_library_path = _LIBRARY_PATH
 
 
 def use_library(path: Path) -> None:
@@ -241,9 +242,15 @@ def use_library(path: Path) -> None:
     running from the library that launched them. The switch is process-wide
     and not synchronised with renders: call it while no other thread
     renders."""
-    global lib
+    global lib, _library_path
     lib = _load(Path(path))
     _bind_host(lib)
+    _library_path = Path(path)
+
+
+def library_path() -> Path:
+    """The library every call of this module currently goes through."""
+    return _library_path
 
 
 def exported_symbols() -> list[str]:

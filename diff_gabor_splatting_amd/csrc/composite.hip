@@ -46,15 +46,20 @@ namespace {
 constexpr int kBatch = 64;
 
 // Diagnostics build (-DGS_DIAGNOSTICS, libgabor_hip_diag.so): the
-// compositors also stamp each tile's begin and end on the wall clock and the
+// compositors also stamp each tile's begin and end on the wall clock, the
 // backward counts, per (record, wave) it processes, how many lanes take the
-// record. Targets are device pointers set by gs_diagnostics_set; a null
-// target records nothing. The product build compiles none of this.
+// record, and the forward counts the records its pixels visit. Targets are
+// device pointers set by gs_diagnostics_set; a null target records nothing.
+// The product build compiles none of this.
 struct DiagnosticTargets {
   unsigned long long* lanes;  // [65]: processed (record, wave) pairs by taking lanes
   long long* forward_span;    // [tiles][2]: wall-clock begin, end of each tile
   long long* backward_span;   // [tiles][2]
   long long tiles;
+  // [2]: forward (pixel, record) visits of in-image pixels - every list
+  // record up to the one that stops the pixel, or to the end of its list -
+  // and the forward's processed (record, wave) pairs times 64 lanes.
+  unsigned long long* visits;
 };
 #ifdef GS_DIAGNOSTICS
 __device__ DiagnosticTargets gs_diagnostics;
@@ -987,6 +992,10 @@ struct Walk {
   float T, m1, m2;
   int last;
   bool done;
+#ifdef GS_DIAGNOSTICS
+  int stop_at;      // list position after the record that stopped the pixel (0: none)
+  int wave_steps;   // (record, wave) pairs this wave processed
+#endif
 };
 
 __device__ __forceinline__ void begin_walk(Walk& w, bool inside) {
@@ -996,6 +1005,10 @@ __device__ __forceinline__ void begin_walk(Walk& w, bool inside) {
   w.m1 = w.m2 = 0.f;
   w.last = 0;
   w.done = !inside;
+#ifdef GS_DIAGNOSTICS
+  w.stop_at = 0;
+  w.wave_steps = 0;
+#endif
 }
 
 // The forward's LDS: a batch of staged rows and their ids.
@@ -1070,9 +1083,15 @@ __device__ __forceinline__ int walk_list(const ForwardStage<Neural>& st, int ran
       const float* r = st.rows + j * L::STRIDE;
       Sample v;
       const bool ok = sample_surface<Neural, false, false>(r, x, y, near_plane, !w.done, v);
+#ifdef GS_DIAGNOSTICS
+      ++w.wave_steps;
+#endif
       if (!__any(ok)) continue;
       const float next = w.T * (1.f - v.alpha);
       const bool stop = ok & (next < 0.0001f);
+#ifdef GS_DIAGNOSTICS
+      if (stop) w.stop_at = start + j + 1;
+#endif
       // Without a stopping lane every lane that accepts takes the record, and
       // some lane accepts: only a stop needs the wave-wide tests.
       bool take = ok;
@@ -1168,6 +1187,19 @@ __global__ __launch_bounds__(kTilePixels, Neural ? (Split ? 4 : 5) : 6) void ren
   const int replay_n = walk_list<Neural, Replay>(
       st, range.x, first, end, point_list, primitive_ids, geometry, appearance, opacities, x, y,
       tile_x, tile_y, near_plane, mscale, mnear, replay + range.x + first, w);
+#ifdef GS_DIAGNOSTICS
+  if (gs_diagnostics.visits) {
+    // A split tile's segments count their relative walks.
+    const int visited = tp.inside ? (w.stop_at > 0 ? w.stop_at : end) - first : 0;
+    double total = double(visited);  // exact wave sum
+#pragma unroll
+    for (int offset = 32; offset > 0; offset >>= 1) total += __shfl_xor(total, offset, 64);
+    if (lane_id() == 0) {
+      atomicAdd(gs_diagnostics.visits, static_cast<unsigned long long>(total));
+      atomicAdd(gs_diagnostics.visits + 1, 64ull * static_cast<unsigned long long>(w.wave_steps));
+    }
+  }
+#endif
   if (Split && base >= 0) {
     // A segment of a split tile: its relative results and replay count.
     float* c = seg.state + int64_t(base + piece.y) * (kCheckpointFloats * kTilePixels) +
@@ -2161,16 +2193,17 @@ int gs_diagnostics_query(int32_t* available, int32_t* wall_clock_khz) {
 }
 
 int gs_diagnostics_set(unsigned long long* lanes, long long* forward_span,
-                       long long* backward_span, int64_t tiles) {
+                       long long* backward_span, int64_t tiles, unsigned long long* visits) {
   GS_REQUIRE(tiles >= 0, GS_ERR_ARGUMENT, "diagnostics tile count must be non-negative");
 #ifdef GS_DIAGNOSTICS
-  const gs::DiagnosticTargets targets{lanes, forward_span, backward_span, tiles};
+  const gs::DiagnosticTargets targets{lanes, forward_span, backward_span, tiles, visits};
   GS_HIP(hipMemcpyToSymbol(HIP_SYMBOL(gs::gs_diagnostics), &targets, sizeof targets));
   return GS_OK;
 #else
   (void)lanes;
   (void)forward_span;
   (void)backward_span;
+  (void)visits;
   GS_REQUIRE(false, GS_ERR_ARGUMENT,
              "this library was built without diagnostics (libgabor_hip_diag.so has them)");
   return GS_ERR_ARGUMENT;

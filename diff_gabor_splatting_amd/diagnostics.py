@@ -17,7 +17,7 @@ Runs one forward + backward of a workload through ``libgabor_hip_diag.so``
 
     python -m diff_gabor_splatting_amd.diagnostics --workload config4 --json out.json
 
-Workloads: ``config0`` .. ``config4`` (the benchmark configs of ``bench.py``)
+Workloads: ``config0`` .. ``config4`` (the benchmark configs, ``workloads.py``)
 and ``harness-classic`` / ``harness-neural`` (the benchmark harness's default
 scene, all images in one dense call). The per-(record, wave) counting adds a
 few instructions to every processed pair, so times here are slightly above
@@ -36,8 +36,6 @@ import torch
 
 from . import _native
 from .build import DIAGNOSTICS_LIBRARY
-
-REPO = Path(__file__).resolve().parents[1]
 
 
 def log2_histogram(values: torch.Tensor) -> dict[str, int]:
@@ -104,6 +102,19 @@ def lane_summary(hist: list[int]) -> dict:
             "histogram": hist}
 
 
+def walk_summary(visits: int, forward_samples: int, lanes: dict) -> dict:
+    """(pixel, record) counts of one render: the forward's visits (every list
+    record up to the one that stops a pixel, or to the end of its list), the
+    samples the forward evaluated in lockstep ((record, wave) pairs times 64
+    lanes) and the backward's (its processed pairs times 64, of which the
+    taking lanes are the useful share)."""
+    hist = lanes["histogram"]
+    return {"forward_pixel_record_visits": int(visits),
+            "forward_samples_evaluated": int(forward_samples),
+            "backward_samples_evaluated": 64 * int(lanes["record_wave_pairs"]),
+            "backward_samples_taken": int(sum(k * c for k, c in enumerate(hist)))}
+
+
 def replay_quadrant_bits(lists, counts, ranges) -> int:
     """Processed (record, wave) pairs the replay lists call for: the quadrant
     bits (28..31) set over every tile's replay entries."""
@@ -123,13 +134,11 @@ def workload_step(name: str, device: torch.device):
     """(description, step) for a named workload; step() runs one forward +
     loss + backward."""
     if name.startswith("config"):
-        if str(REPO) not in sys.path:
-            sys.path.insert(0, str(REPO))
-        import bench
+        from . import workloads
 
         index = int(name[len("config"):])
-        *_, step = bench.prepare(index, device, False)
-        return bench.CONFIGS[index]["name"], step
+        *_, step = workloads.prepare(index, device, False)
+        return workloads.CONFIGS[index]["name"], step
     if name in ("harness-classic", "harness-neural"):
         from . import benchmark_rasterization as harness
 
@@ -158,7 +167,16 @@ def collect(name: str, device: torch.device | None = None) -> dict:
     if not DIAGNOSTICS_LIBRARY.exists():
         raise ImportError(f"{DIAGNOSTICS_LIBRARY.name} is not built; run "
                           "`python -m diff_gabor_splatting_amd.build --diagnostics`")
+    previous = _native.library_path()
     _native.use_library(DIAGNOSTICS_LIBRARY)
+    try:
+        return _collect(name, device)
+    finally:
+        # Later calls in this process render through the product library again.
+        _native.use_library(previous)
+
+
+def _collect(name: str, device: torch.device) -> dict:
     available, khz = ctypes.c_int32(), ctypes.c_int32()
     with torch.cuda.device(device):
         _native._check(_native.lib.gs_diagnostics_query(ctypes.byref(available),
@@ -186,14 +204,16 @@ def collect(name: str, device: torch.device | None = None) -> dict:
         # earliest begin and the latest end of every workgroup of a tile.
         spans = torch.zeros((2, tiles, 2), dtype=torch.int64, device=device)
         spans[..., 0] = -1
+        visits = torch.zeros(2, dtype=torch.int64, device=device)
         with torch.cuda.device(device):
             _native._check(_native.lib.gs_diagnostics_set(
-                lanes.data_ptr(), spans[0].data_ptr(), spans[1].data_ptr(), tiles))
+                lanes.data_ptr(), spans[0].data_ptr(), spans[1].data_ptr(), tiles,
+                visits.data_ptr()))
             try:
                 step()
                 torch.cuda.synchronize(device)
             finally:
-                _native._check(_native.lib.gs_diagnostics_set(None, None, None, 0))
+                _native._check(_native.lib.gs_diagnostics_set(None, None, None, 0, None))
     finally:
         _native.rasterize_forward = original
     _, point_list, ranges, _, _, *replay = captured["forward"]
@@ -214,6 +234,8 @@ def collect(name: str, device: torch.device | None = None) -> dict:
         if bool((spans[index, :, 0] >= 0).all()):
             report[kernel] = launch_profile(spans[index], khz.value)
     report["backward_taking_lanes"] = lane_summary(lanes.cpu().tolist())
+    visits = visits.cpu().tolist()
+    report["forward_walk"] = walk_summary(visits[0], visits[1], report["backward_taking_lanes"])
     return report
 
 
@@ -250,6 +272,13 @@ def format_report(report: dict) -> str:
     hist = lanes["histogram"]
     lines.append("  by taking lanes (1-8, 9-16, ..., 57-64): "
                  + ", ".join(str(sum(hist[1 + 8 * b: 9 + 8 * b])) for b in range(8)))
+    if "forward_walk" in report:
+        walk = report["forward_walk"]
+        lines.append(
+            f"(pixel, record) counts: forward visits {walk['forward_pixel_record_visits']}, "
+            f"forward samples evaluated {walk['forward_samples_evaluated']}, backward samples "
+            f"evaluated {walk['backward_samples_evaluated']} of which taken "
+            f"{walk['backward_samples_taken']}")
     return "\n".join(lines)
 
 

@@ -36,6 +36,15 @@ def paused_collector() -> Iterator[None]:
             gc.enable()
 
 
+@contextlib.contextmanager
+def collected_collector() -> Iterator[None]:
+    """Run a full garbage collection and leave the collector as it was, so
+    that the block starts from an empty young generation but still pays any
+    collection its own allocations trigger, as a training loop does."""
+    gc.collect()
+    yield
+
+
 class PhaseClock:
     """Named marks on the current stream of the current device."""
 

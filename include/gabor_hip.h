@@ -434,8 +434,13 @@ int gs_render_backward(int32_t neural, const float* geometry, const float* appea
  * in forward_span / backward_span [tiles][2] (int64, wall-clock ticks), and
  * (b) per (record, wave) the backward processes, the number of the wave's 64
  * lanes that take the record, as a histogram added into lanes [65] (uint64;
- * the caller clears it). These cost a few instructions per processed
- * (record, wave), so the diagnostics library is for measurement only.    */
+ * the caller clears it), and (c) the forward's walk, added into visits [2]
+ * (uint64; the caller clears it): [0] the (pixel, record) visits of in-image
+ * pixels, every list record up to the one that stops the pixel or to the
+ * end of its list (a split tile's segments count their relative walks), and
+ * [1] the (record, wave) pairs the forward processed, times 64 lanes. These
+ * cost a few instructions per processed (record, wave), so the diagnostics
+ * library is for measurement only.                                       */
 
 /* *available = 1 in the diagnostics library, 0 in the product library;
  * *wall_clock_khz = the current device's wall-clock rate. */
@@ -445,7 +450,7 @@ int gs_diagnostics_query(int32_t* available, int32_t* wall_clock_khz);
  * to record nothing; spans are written for tile indices below `tiles`).
  * Synchronous. The product library returns GS_ERR_ARGUMENT. */
 int gs_diagnostics_set(unsigned long long* lanes, long long* forward_span,
-                       long long* backward_span, int64_t tiles);
+                       long long* backward_span, int64_t tiles, unsigned long long* visits);
 
 /* ------------------------------------------------------------------ */
 /* Kernel timing for measurement: when enabled, each compositor / sort /

@@ -234,6 +234,13 @@ def fp32_conditioned(render, values, eps=3e-7, trials=3, atol=1e-5, rtol=1e-4,
     return maps, mask
 
 
+def plain_bar_pixels(maps, expected, atol=1e-5, rtol=1e-4):
+    """Pixels whose every channel lies within atol + rtol * |expected| of the
+    float64 `expected` maps (the north star's forward bar, no allowance)."""
+    a = maps.detach().cpu().double()
+    return ((a - expected).abs() <= atol + rtol * expected.abs()).all(-1)
+
+
 def describe_mismatch(actual, expected):
     """Worst elements and norms of a comparison, for assertion messages."""
     a = actual.detach().cpu().double()
@@ -274,6 +281,7 @@ def assert_gradients_close(actual, expected, name, sensitivity=None, rel_norm=1e
         f"{float(diff[well].norm()) / (float(e.norm()) or 1.0):.3e}; "
         f"ill-conditioned share {ill:.3f}"
     )
+    return 1.0 - ill
 
 
 def oracle_reference(render, values, weights, eps=3e-7, trials=3, **options):

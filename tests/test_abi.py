@@ -82,6 +82,25 @@ def test_argument_errors_return_status_and_message():
     assert lib.gs_last_error() == b""
 
 
+def test_static_forward_rejects_more_tiles_than_its_scratch():
+    """gs_render_forward_static refuses more image tiles than its static
+    scratch holds (GS_RENDER_STATIC_MAX_TILES) before any HIP call, so the
+    placeholder pointers below are never dereferenced."""
+    from diff_gabor_splatting_amd import _native
+
+    lib = _native.lib
+    static_max_tiles = 1 << 20
+    side = 16 * 1025  # 1025 x 1025 tiles
+    dummy = ctypes.c_void_p(256)
+    groups = (ctypes.c_void_p * 5)(*([256] * 5))
+    strides = (ctypes.c_int64 * 10)()
+    status = lib.gs_render_forward_static(0, *([dummy] * 7), 1, side, side, 0.2, 100.0, groups,
+                                          strides, dummy, dummy, None, 0, None, None)
+    assert status == 4
+    message = lib.gs_last_error().decode()
+    assert f"at most {static_max_tiles} image tiles" in message and "1050625" in message
+
+
 @pytest.mark.parametrize("m", [0, 1, 4096, 4097, 10**6])
 def test_workspace_sizes_grow_with_input(m):
     from diff_gabor_splatting_amd import _native

@@ -75,8 +75,39 @@ def test_replay_quadrant_bits_counts_each_tiles_entries():
 def test_product_library_refuses_diagnostics():
     from diff_gabor_splatting_amd import _native
 
-    status = _native.lib.gs_diagnostics_set(None, None, None, 0)
+    status = _native.lib.gs_diagnostics_set(None, None, None, 0, None)
     assert status == 1 and b"without diagnostics" in _native.lib.gs_last_error()
+
+
+def test_walk_summary_counts():
+    hist = [0] * 65
+    hist[2], hist[64] = 3, 1
+    lanes = diagnostics.lane_summary(hist)
+    walk = diagnostics.walk_summary(1000, 640, lanes)
+    assert walk == {"forward_pixel_record_visits": 1000, "forward_samples_evaluated": 640,
+                    "backward_samples_evaluated": 256, "backward_samples_taken": 70}
+
+
+def test_collect_restores_the_product_library(monkeypatch):
+    """collect() renders through the diagnostics library and switches the
+    package back to the library it used before, also when the run fails."""
+    from diff_gabor_splatting_amd import _native
+
+    if not diagnostics.DIAGNOSTICS_LIBRARY.exists():
+        pytest.skip("the diagnostics library is not built")
+    before = _native.library_path()
+    seen = []
+
+    def failing_run(name, device):
+        seen.append(_native.library_path())
+        raise RuntimeError("planted failure")
+
+    monkeypatch.setattr(diagnostics, "_collect", failing_run)
+    with pytest.raises(RuntimeError, match="planted failure"):
+        diagnostics.collect("config0", torch.device("cpu"))
+    assert seen == [diagnostics.DIAGNOSTICS_LIBRARY]
+    assert _native.library_path() == before
+    assert _native.lib.gs_diagnostics_set(None, None, None, 0, None) == 1
 
 
 @pytest.mark.gpu
@@ -96,6 +127,13 @@ def test_diagnostics_run_matches_the_replay_lists(tmp_path, workload):
     assert lanes["histogram"][0] == 0
     assert lanes["record_wave_pairs"] == report["replay_quadrant_bits"] > 0
     assert 1 <= lanes["mean_taking_lanes"] <= 64
+    walk = report["forward_walk"]
+    assert walk["backward_samples_taken"] <= walk["backward_samples_evaluated"]
+    # Every in-image pixel visits at least the records it took; the lockstep
+    # walk evaluates at least one sample per visit that passed the footprint
+    # tests, and the tiles' lists bound the visits.
+    assert 0 < walk["forward_pixel_record_visits"] <= 256 * report["intersections"]
+    assert walk["forward_samples_evaluated"] > 0
     for kernel in ("render_forward", "render_backward"):
         profile = report[kernel]
         assert 0 < profile["ended_90pct_us"] <= profile["ended_99pct_us"] <= profile["span_us"]

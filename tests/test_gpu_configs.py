@@ -16,7 +16,8 @@ import torch
 import bench
 from oracle import binning as oracle_binning
 from oracle import render as oracle_render
-from scenes import assert_gradients_close, fp32_conditioned, maps_from_result, oracle_reference
+from scenes import (assert_gradients_close, fp32_conditioned, maps_from_result, oracle_reference,
+                    plain_bar_pixels)
 
 pytestmark = [
     pytest.mark.gpu,
@@ -26,6 +27,19 @@ DEVICE = torch.device("cuda:0")
 FORWARD_TOL = dict(atol=1e-5, rtol=1e-4)
 # Largest share of pixels that may be ill-conditioned at float32 precision.
 MAX_FLAGGED = 0.03
+# Plain-bar comparison against a float32 evaluation of the same function:
+# the float32 torch oracle, on the same inputs and culling, is compared with
+# the float64 oracle pixel by pixel at 1e-5 / 1e-4 with no allowance.
+# Wherever that float32 evaluation meets the bar, the HIP maps must meet it
+# too, except at most PLAIN_BAR_EXCEPTIONS pixels per render: the HIP path
+# rounds differently (reciprocals, exp2, hardware sin/cos, FMA contraction,
+# per-record constants), so a pixel sitting within rounding of a discrete
+# threshold can fall on the other side of it in one float32 evaluation and
+# not the other. The share of pixels where the float32 oracle itself misses
+# the bar is capped at MAX_FP32_MISSES (float32 rounding, not a perturbation
+# of the inputs, is the measure of conditioning here).
+PLAIN_BAR_EXCEPTIONS = 8
+MAX_FP32_MISSES = 0.03
 
 
 def renderer(cfg):
@@ -85,20 +99,42 @@ ENVELOPE_FACTOR = 4.0
 
 
 def compare_with_oracle(cfg, values, opts, result, seed, max_flagged=MAX_FLAGGED,
-                        envelope=False):
+                        envelope=False, label=""):
     """Maps on well-conditioned pixels within 1e-5/1e-4; gradients of a loss
     restricted to those pixels within 1e-3 (conditioning-aware, see
     scenes.assert_gradients_close). At most `max_flagged` of the pixels may
-    be ill-conditioned. With `envelope`, every map element - ill-conditioned
+    be ill-conditioned (flagged by the float64 oracle's response to 5-ulp
+    input perturbations). With `envelope`, every map element - ill-conditioned
     pixels included - must also lie within 1e-5/1e-4 plus ENVELOPE_FACTOR
     times its float64 sensitivity (its largest change under the
-    conditioning perturbations), the form of the gradient bar. Returns the
-    mask of well-conditioned pixels."""
+    conditioning perturbations), the form of the gradient bar.
+
+    Plain bar: the float32 torch oracle is evaluated on the same inputs, and
+    wherever it is within 1e-5/1e-4 of the float64 oracle on every channel,
+    the HIP maps must be too, with at most PLAIN_BAR_EXCEPTIONS exceptions;
+    the float32 oracle may miss the bar on at most MAX_FP32_MISSES of the
+    pixels. Prints both pass counts and, per gradient tensor, the share of
+    elements the error-norm test covers. Returns the mask of well-conditioned
+    pixels."""
     maps = maps_from_result(result)
     radii = result[2]["radii"].cpu()
     expected_base, mask, worst = fp32_conditioned(oracle_fn(cfg), values, radii=radii,
                                                   return_worst=True, **opts)
     assert float((~mask).float().mean()) <= max_flagged, float((~mask).float().mean())
+    single = {k: v.detach().cpu().float() for k, v in values.items()}
+    with torch.no_grad():
+        maps32 = oracle_fn(cfg)(**single, radii=radii, **opts)[0]
+    fp32_pass = plain_bar_pixels(maps32, expected_base)
+    hip_pass = plain_bar_pixels(maps, expected_base)
+    exceptions = int((fp32_pass & ~hip_pass).sum())
+    pixels = fp32_pass.numel()
+    print(f"{label}plain bar 1e-5/1e-4 vs float64: HIP {int(hip_pass.sum())} of {pixels} "
+          f"pixels, float32 oracle {int(fp32_pass.sum())}; HIP misses where float32 meets "
+          f"it: {exceptions}; 5-ulp flagged {int((~mask).sum())}", flush=True)
+    assert exceptions <= PLAIN_BAR_EXCEPTIONS, (
+        f"{exceptions} pixels miss the plain bar where the float32 oracle meets it")
+    assert 1.0 - float(fp32_pass.double().mean()) <= MAX_FP32_MISSES, (
+        f"float32 oracle misses the plain bar on {pixels - int(fp32_pass.sum())} pixels")
     if envelope:
         actual_maps = maps.detach().cpu().double()
         excess = ((actual_maps - expected_base).abs() - FORWARD_TOL["atol"]
@@ -112,9 +148,12 @@ def compare_with_oracle(cfg, values, opts, result, seed, max_flagged=MAX_FLAGGED
     expected_maps, expected, sensitivity = oracle_reference(oracle_fn(cfg), values, weights,
                                                             radii=radii, **opts)
     torch.testing.assert_close(maps.detach().cpu().double()[mask], expected_maps[mask], **FORWARD_TOL)
+    covered = {}
     for name, a in zip(values, actual):
         assert torch.isfinite(a).all(), name
-        assert_gradients_close(a, expected[name], name, sensitivity[name])
+        covered[name] = assert_gradients_close(a, expected[name], name, sensitivity[name])
+    print(f"{label}gradient elements under the error-norm test: "
+          + ", ".join(f"{name} {share:.3f}" for name, share in covered.items()), flush=True)
     return mask
 
 
@@ -129,7 +168,7 @@ def test_config0_matches_oracle():
     values = gpu_values(bench.make_scene(0))
     opts = options(cfg)
     result = renderer(cfg)(**values, **opts)
-    compare_with_oracle(cfg, values, opts, result, seed=0)
+    compare_with_oracle(cfg, values, opts, result, seed=0, label="config 0: ")
 
 
 @pytest.mark.parametrize("index", [1, 2, 3, 4])
@@ -198,7 +237,8 @@ def test_config_crop_matches_full_image_and_oracle(index):
     opts = options(cfg, edge, edge, packed=False)
     result = renderer(cfg)(**subset_values, **opts)
     assert torch.equal(maps_from_result(result).detach(), crop_all)
-    compare_with_oracle(cfg, subset_values, opts, result, seed=index)
+    compare_with_oracle(cfg, subset_values, opts, result, seed=index,
+                        label=f"config {index} crop: ")
 
 
 # ---------------------------------------------------------------------------
@@ -209,11 +249,12 @@ CRITERIA = ("longest list", "most contributors", "early stop")
 # At the hardest tiles a pixel evaluates hundreds to thousands of records,
 # and nearly always one of them sits within 1e-3 (relative) of a discrete
 # threshold - alpha = 1/255, the 1e-4 stop, the surface/screen switch -
-# that projection amplifies a 5-ulp input change past. Such pixels are
-# flagged ill-conditioned (up to three quarters of a window where pixels
-# composite over a thousand records each), so here every pixel is also held
-# to the envelope of compare_with_oracle, and the flagged share is printed
-# rather than capped.
+# that projection amplifies a 5-ulp input change past. The 5-ulp test flags
+# such pixels (up to three quarters of a window where pixels composite over
+# a thousand records each), far more than float32 rounding actually moves:
+# there the cap is the plain-bar one of compare_with_oracle (the float32
+# oracle within 1e-5 / 1e-4 of float64 on all but MAX_FP32_MISSES of the
+# pixels, HIP wherever it is), and every pixel is also held to the envelope.
 MAX_FLAGGED_HARD = 1.0
 
 
@@ -333,7 +374,8 @@ def test_hardest_tiles_match_oracle(hard_windows, index, criterion):
     print(f"config {index} {criterion}: image {w['image']} window ({w['x0']}, {w['y0']}) "
           f"tile {w['tile']}, {len(keep)} surfels; oracle check", flush=True)
     mask = compare_with_oracle(cfg, subset_values, opts, result, seed=17 * index,
-                               max_flagged=MAX_FLAGGED_HARD, envelope=True)
+                               max_flagged=MAX_FLAGGED_HARD, envelope=True,
+                               label=f"config {index} {criterion}: ")
     # The crop's camera shifts the principal point, which changes float32
     # rounding in projection: on well-conditioned pixels the window of the
     # full render and the cropped render agree.
