@@ -360,8 +360,9 @@ def roofline_entry(kernel: str, cfg: dict, pixels: int, stats: dict, avg_ms: flo
     """
     walked = stats["records_backward" if kernel == "render_backward" else "records_forward"]
     reference_bytes = algorithmic_bytes(kernel, cfg["neural"], pixels, walked, stats["visible"])
-    replay_bytes = algorithmic_bytes(kernel, cfg["neural"], pixels, stats["records_replayed"],
-                                     stats["visible"], entry_bytes=REPLAY_ENTRY_BYTES)
+    replay_bytes = None if stats["records_replayed"] is None else algorithmic_bytes(
+        kernel, cfg["neural"], pixels, stats["records_replayed"], stats["visible"],
+        entry_bytes=REPLAY_ENTRY_BYTES)
     seconds = avg_ms / 1000 if avg_ms else None
     traffic = measured_traffic(kernel, cfg["name"])
     hbm = {
@@ -371,10 +372,12 @@ def roofline_entry(kernel: str, cfg: dict, pixels: int, stats: dict, avg_ms: flo
         "frac": round(reference_bytes / seconds / 1e9 / HBM_PEAK_GBS, 5) if seconds else None,
         "algorithmic_bytes_per_launch": reference_bytes,
         "replay_walk_bytes_per_launch": replay_bytes,
-        "achieved_replay_walk": round(replay_bytes / seconds / 1e9, 2) if seconds else None,
+        "achieved_replay_walk": (round(replay_bytes / seconds / 1e9, 2)
+                                 if seconds and replay_bytes else None),
         "traffic": traffic,
         "traffic_over_reference_walk": round(traffic / reference_bytes, 3) if traffic else None,
-        "traffic_over_replay_walk": round(traffic / replay_bytes, 3) if traffic else None,
+        "traffic_over_replay_walk": (round(traffic / replay_bytes, 3)
+                                     if traffic and replay_bytes else None),
     }
     valu = measured_valu(kernel, cfg["name"], avg_ms)
     entry = {"kernel": kernel, "avg_launch_ms": round(avg_ms, 4)}
@@ -447,24 +450,27 @@ def measured_traffic(kernel: str, workload: str):
 
 
 def workload_stats(values, renderer, options):
-    """Intersections, visible pairs and surfel-pixel evaluation counts of one call."""
+    """Intersections, visible pairs, records walked and replayed, and the
+    backward's surfel-pixel evaluations of one call. The render records
+    gradients (the renderers write replay lists only when a backward can
+    follow); no backward is run."""
     from diff_gabor_splatting_amd import _native
 
-    with torch.no_grad():
-        captured = {}
-        original = _native.rasterize_forward
+    captured = {}
+    original = _native.rasterize_forward
 
-        def spy(*a, **k):
-            out = original(*a, **k)
-            captured["out"] = out
-            captured["args"] = a
-            return out
+    def spy(*a, **k):
+        out = original(*a, **k)
+        captured["out"] = out
+        captured["args"] = a
+        return out
 
-        _native.rasterize_forward = spy
-        try:
-            rgb, alpha, meta = renderer(**values, **options)
-        finally:
-            _native.rasterize_forward = original
+    _native.rasterize_forward = spy
+    try:
+        rgb, alpha, meta = renderer(**values, **options)
+    finally:
+        _native.rasterize_forward = original
+    del rgb, alpha, meta
     maps, point_list, ranges, state, contributors = captured["out"][:5]
     replay = captured["out"][5] if len(captured["out"]) > 5 else None
     geometry = captured["args"][0]

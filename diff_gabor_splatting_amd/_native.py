@@ -58,11 +58,16 @@ def split_length(tiles: int, intersections: int) -> int:
     return SPLIT_LENGTH
 
 
-def split_slots(intersections: int, length: int) -> int:
+def split_slots(intersections: int, length: int, tiles: int) -> int:
     """Checkpoint slots: a tile of L > length records needs ceil(L / length)
-    <= floor(2 L / length) of them, capped at SPLIT_MAX_SLOTS (the slots go
-    to tiles in tile order; later tiles past the cap are not split)."""
-    return min(2 * intersections // length, SPLIT_MAX_SLOTS) if length else 0
+    <= floor(L / length) + 1 of them, and at most min(tiles, M / (length +
+    1)) tiles are that long, so floor(M / length) + min(tiles, floor(M /
+    (length + 1))) + 1 suffice; capped at SPLIT_MAX_SLOTS (the slots go to
+    tiles in tile order; later tiles past the cap are not split)."""
+    if not length:
+        return 0
+    return min(intersections // length + min(tiles, intersections // (length + 1)) + 1,
+               SPLIT_MAX_SLOTS)
 
 
 CHECKPOINT_FLOATS = 13

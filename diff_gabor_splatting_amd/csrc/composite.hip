@@ -56,11 +56,81 @@ struct DiagnosticTargets {
   long long* forward_span;    // [tiles][2]: wall-clock begin, end of each tile
   long long* backward_span;   // [tiles][2]
   long long tiles;
-  // [2]: forward (pixel, record) visits of in-image pixels - every list
-  // record up to the one that stops the pixel, or to the end of its list -
-  // and the forward's processed (record, wave) pairs times 64 lanes.
-  unsigned long long* visits;
+  // [8] work counters (see gs_diagnostics_set): forward (pixel, record)
+  // visits of in-image pixels, the forward's processed (record, wave) pairs
+  // times 64 lanes; the backward's processed (record, wave) pairs and the
+  // wave steps they would take with each 32-lane half (8x4) or each 16-lane
+  // block (4x4) of the quadrant walking its own records: at best (per batch,
+  // the largest count of any half or block) and in list order (records
+  // taken by one half or block packed between those taken by several).
+  unsigned long long* counters;
 };
+
+#ifdef GS_DIAGNOSTICS
+// Step counts of one wave's batch in the backward under the half and block
+// schedules above (scalar bookkeeping, identical in every lane).
+struct PackingCounts {
+  int any = 0, half[2] = {0, 0}, block[4] = {0, 0, 0, 0};
+  int half_pending[2] = {0, 0}, block_pending[4] = {0, 0, 0, 0};
+  int half_steps = 0, block_steps = 0;
+
+  // One processed record with this ballot of taking lanes (lane = 8 y + x
+  // over the 8x8 quadrant). Every array index is a compile-time constant, so
+  // the counts stay in registers.
+  __device__ __forceinline__ void add(uint64_t taking) {
+    constexpr uint64_t kHalves[2] = {0x00000000FFFFFFFFull, 0xFFFFFFFF00000000ull};
+    constexpr uint64_t kBlocks[4] = {0x000000000F0F0F0Full, 0x00000000F0F0F0F0ull,
+                                     0x0F0F0F0F00000000ull, 0xF0F0F0F000000000ull};
+    ++any;
+    bool in_half[2], in_block[4];
+    int halves = 0, blocks = 0;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      in_half[i] = (taking & kHalves[i]) != 0;
+      half[i] += in_half[i];
+      halves += in_half[i];
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      in_block[i] = (taking & kBlocks[i]) != 0;
+      block[i] += in_block[i];
+      blocks += in_block[i];
+    }
+    if (halves == 1) {
+#pragma unroll
+      for (int i = 0; i < 2; ++i) half_pending[i] += in_half[i];
+    } else {
+      half_steps += max(half_pending[0], half_pending[1]) + 1;
+      half_pending[0] = half_pending[1] = 0;
+    }
+    if (blocks == 1) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) block_pending[i] += in_block[i];
+    } else {
+      block_steps += max(max(block_pending[0], block_pending[1]),
+                         max(block_pending[2], block_pending[3])) + 1;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) block_pending[i] = 0;
+    }
+  }
+
+  // Adds the batch's counts to the workgroup's LDS counters [5] (lane 0)
+  // and starts afresh.
+  __device__ void flush(unsigned int* sums) {
+    half_steps += max(half_pending[0], half_pending[1]);
+    block_steps += max(max(block_pending[0], block_pending[1]),
+                       max(block_pending[2], block_pending[3]));
+    if (lane_id() == 0 && any) {
+      atomicAdd(sums + 0, unsigned(any));
+      atomicAdd(sums + 1, unsigned(max(half[0], half[1])));
+      atomicAdd(sums + 2, unsigned(max(max(block[0], block[1]), max(block[2], block[3]))));
+      atomicAdd(sums + 3, unsigned(half_steps));
+      atomicAdd(sums + 4, unsigned(block_steps));
+    }
+    *this = PackingCounts();
+  }
+};
+#endif
 #ifdef GS_DIAGNOSTICS
 __device__ DiagnosticTargets gs_diagnostics;
 
@@ -1188,16 +1258,18 @@ __global__ __launch_bounds__(kTilePixels, Neural ? (Split ? 4 : 5) : 6) void ren
       st, range.x, first, end, point_list, primitive_ids, geometry, appearance, opacities, x, y,
       tile_x, tile_y, near_plane, mscale, mnear, replay + range.x + first, w);
 #ifdef GS_DIAGNOSTICS
-  if (gs_diagnostics.visits) {
-    // A split tile's segments count their relative walks.
+  if (gs_diagnostics.counters) {
+    // A split tile's segments count their relative walks. Summed per
+    // workgroup in LDS, then one global atomic per counter and workgroup.
+    __shared__ unsigned long long diag_walk[2];
+    if (threadIdx.x < 2) diag_walk[threadIdx.x] = 0ull;
+    __syncthreads();
     const int visited = tp.inside ? (w.stop_at > 0 ? w.stop_at : end) - first : 0;
-    double total = double(visited);  // exact wave sum
-#pragma unroll
-    for (int offset = 32; offset > 0; offset >>= 1) total += __shfl_xor(total, offset, 64);
-    if (lane_id() == 0) {
-      atomicAdd(gs_diagnostics.visits, static_cast<unsigned long long>(total));
-      atomicAdd(gs_diagnostics.visits + 1, 64ull * static_cast<unsigned long long>(w.wave_steps));
-    }
+    atomicAdd(&diag_walk[0], static_cast<unsigned long long>(visited));
+    if (lane_id() == 0)
+      atomicAdd(&diag_walk[1], 64ull * static_cast<unsigned long long>(w.wave_steps));
+    __syncthreads();
+    if (threadIdx.x < 2) atomicAdd(gs_diagnostics.counters + threadIdx.x, diag_walk[threadIdx.x]);
   }
 #endif
   if (Split && base >= 0) {
@@ -1520,7 +1592,10 @@ __global__ __launch_bounds__(kTilePixels, Neural && !Replay ? 2 : 4) void render
 #ifdef GS_DIAGNOSTICS
   const long long diag_begin = wall_clock64();
   __shared__ unsigned int diag_lanes[65];
+  __shared__ unsigned int diag_packing[5];
   for (int i = threadIdx.x; i < 65; i += kTilePixels) diag_lanes[i] = 0u;
+  if (threadIdx.x < 5) diag_packing[threadIdx.x] = 0u;
+  PackingCounts packing;
 #endif
   const TilePixel tp = tile_pixel(tile, width, height, tw, th);
   const float x = float(tp.px), y = float(tp.py);
@@ -1692,6 +1767,7 @@ __global__ __launch_bounds__(kTilePixels, Neural && !Replay ? 2 : 4) void render
       {
         const uint64_t taking = __ballot(active);
         if (lane == 0 && taking) atomicAdd(&diag_lanes[__popcll(taking)], 1u);
+        if (taking) packing.add(taking);
       }
 #endif
       // Every lane runs the adjoint. A lane that does not take the sample
@@ -1806,6 +1882,9 @@ __global__ __launch_bounds__(kTilePixels, Neural && !Replay ? 2 : 4) void render
       walk(std::false_type{});
     else
       walk(std::true_type{});
+#ifdef GS_DIAGNOSTICS
+    packing.flush(diag_packing);
+#endif
     __syncthreads();
     // Flush this batch: one global atomic per nonzero (record, parameter).
     // Consecutive threads take consecutive parameters of a record, so that
@@ -1843,6 +1922,9 @@ __global__ __launch_bounds__(kTilePixels, Neural && !Replay ? 2 : 4) void render
   if (gs_diagnostics.lanes && threadIdx.x < 65 && diag_lanes[threadIdx.x] != 0u)
     atomicAdd(gs_diagnostics.lanes + threadIdx.x,
               static_cast<unsigned long long>(diag_lanes[threadIdx.x]));
+  if (gs_diagnostics.counters && threadIdx.x < 5 && diag_packing[threadIdx.x] != 0u)
+    atomicAdd(gs_diagnostics.counters + 2 + threadIdx.x,
+              static_cast<unsigned long long>(diag_packing[threadIdx.x]));
   stamp_tile(gs_diagnostics.backward_span, tile, diag_begin);
 #endif
 }
@@ -2193,17 +2275,17 @@ int gs_diagnostics_query(int32_t* available, int32_t* wall_clock_khz) {
 }
 
 int gs_diagnostics_set(unsigned long long* lanes, long long* forward_span,
-                       long long* backward_span, int64_t tiles, unsigned long long* visits) {
+                       long long* backward_span, int64_t tiles, unsigned long long* counters) {
   GS_REQUIRE(tiles >= 0, GS_ERR_ARGUMENT, "diagnostics tile count must be non-negative");
 #ifdef GS_DIAGNOSTICS
-  const gs::DiagnosticTargets targets{lanes, forward_span, backward_span, tiles, visits};
+  const gs::DiagnosticTargets targets{lanes, forward_span, backward_span, tiles, counters};
   GS_HIP(hipMemcpyToSymbol(HIP_SYMBOL(gs::gs_diagnostics), &targets, sizeof targets));
   return GS_OK;
 #else
   (void)lanes;
   (void)forward_span;
   (void)backward_span;
-  (void)visits;
+  (void)counters;
   GS_REQUIRE(false, GS_ERR_ARGUMENT,
              "this library was built without diagnostics (libgabor_hip_diag.so has them)");
   return GS_ERR_ARGUMENT;

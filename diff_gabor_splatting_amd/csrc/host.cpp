@@ -754,7 +754,10 @@ py::list rasterize_forward(const at::Tensor& geometry, const at::Tensor& appeara
   const MapArgs args = map_group_args(groups, "map outputs must have uniformly strided pixels");
   const int64_t m = point_list.numel();
   int64_t length = split >= 0 ? split : ((tiles >= split_max_tiles || m <= 0) ? 0 : split_length);
-  const int64_t slots = length ? std::min(2 * m / length, split_max_slots) : 0;
+  // A tile of L > length records takes ceil(L / length) <= floor(L / length) + 1
+  // slots, and at most min(tiles, m / (length + 1)) tiles are that long.
+  const int64_t slots =
+      length ? std::min(m / length + std::min(tiles, m / (length + 1)) + 1, split_max_slots) : 0;
   at::Tensor segment_state, segment_index;
   if (slots) {
     segment_state = at::empty({slots, kCheckpointFloats, kTile * kTile}, f32);

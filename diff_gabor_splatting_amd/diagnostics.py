@@ -115,6 +115,25 @@ def walk_summary(visits: int, forward_samples: int, lanes: dict) -> dict:
             "backward_samples_taken": int(sum(k * c for k, c in enumerate(hist)))}
 
 
+def packing_summary(counters) -> dict:
+    """The backward's wave steps now (one record per wave step over the 8x8
+    quadrant) and under two packings it could use: each 32-lane half (8x4)
+    or each 16-lane block (4x4) walking its own records, at best and in
+    list order (see gs_diagnostics_set), as counts and as ratios."""
+    steps = int(counters[2])
+
+    def ratio(v):
+        return round(int(v) / steps, 4) if steps else None
+
+    return {"wave_steps": steps,
+            "halves_at_best": int(counters[3]), "blocks_at_best": int(counters[4]),
+            "halves_in_order": int(counters[5]), "blocks_in_order": int(counters[6]),
+            "ratio_halves_at_best": ratio(counters[3]),
+            "ratio_blocks_at_best": ratio(counters[4]),
+            "ratio_halves_in_order": ratio(counters[5]),
+            "ratio_blocks_in_order": ratio(counters[6])}
+
+
 def replay_quadrant_bits(lists, counts, ranges) -> int:
     """Processed (record, wave) pairs the replay lists call for: the quadrant
     bits (28..31) set over every tile's replay entries."""
@@ -204,11 +223,11 @@ def _collect(name: str, device: torch.device) -> dict:
         # earliest begin and the latest end of every workgroup of a tile.
         spans = torch.zeros((2, tiles, 2), dtype=torch.int64, device=device)
         spans[..., 0] = -1
-        visits = torch.zeros(2, dtype=torch.int64, device=device)
+        counters = torch.zeros(8, dtype=torch.int64, device=device)
         with torch.cuda.device(device):
             _native._check(_native.lib.gs_diagnostics_set(
                 lanes.data_ptr(), spans[0].data_ptr(), spans[1].data_ptr(), tiles,
-                visits.data_ptr()))
+                counters.data_ptr()))
             try:
                 step()
                 torch.cuda.synchronize(device)
@@ -234,8 +253,10 @@ def _collect(name: str, device: torch.device) -> dict:
         if bool((spans[index, :, 0] >= 0).all()):
             report[kernel] = launch_profile(spans[index], khz.value)
     report["backward_taking_lanes"] = lane_summary(lanes.cpu().tolist())
-    visits = visits.cpu().tolist()
-    report["forward_walk"] = walk_summary(visits[0], visits[1], report["backward_taking_lanes"])
+    counters = counters.cpu().tolist()
+    report["forward_walk"] = walk_summary(counters[0], counters[1],
+                                          report["backward_taking_lanes"])
+    report["backward_packing"] = packing_summary(counters)
     return report
 
 
@@ -279,6 +300,13 @@ def format_report(report: dict) -> str:
             f"forward samples evaluated {walk['forward_samples_evaluated']}, backward samples "
             f"evaluated {walk['backward_samples_evaluated']} of which taken "
             f"{walk['backward_samples_taken']}")
+    if "backward_packing" in report:
+        p = report["backward_packing"]
+        lines.append(
+            f"backward wave steps {p['wave_steps']}; with 8x4 halves walking their own records "
+            f"{p['ratio_halves_at_best']} of them at best, {p['ratio_halves_in_order']} in list "
+            f"order; with 4x4 blocks {p['ratio_blocks_at_best']} at best, "
+            f"{p['ratio_blocks_in_order']} in list order")
     return "\n".join(lines)
 
 

@@ -379,8 +379,11 @@ int gs_render_forward(int32_t neural, const float* geometry, const float* appear
  * rounded up to even, receives each tile's first slot (-1: not split), then
  * per slot the replay-list length at its checkpoint, then (from int E) the
  * forward's work list. Slots past segment_capacity are not used (their
- * tiles are not split); sum over tiles of floor(2 length / segment_length)
- * slots always suffice. gs_render_backward takes the same arguments. */
+ * tiles are not split); floor(M / L) + min(I*tw*th, floor(M / (L + 1))) + 1
+ * slots always suffice (M = point-list length, L = segment_length: a tile of
+ * n > L records takes ceil(n / L) <= floor(n / L) + 1 slots, and at most
+ * M / (L + 1) tiles are that long). gs_render_backward takes the same
+ * arguments. */
 
 /* gs_render_forward without a workspace argument. No counterpart in the
  * reference: it is for callers that cannot allocate device memory (code
@@ -434,13 +437,19 @@ int gs_render_backward(int32_t neural, const float* geometry, const float* appea
  * in forward_span / backward_span [tiles][2] (int64, wall-clock ticks), and
  * (b) per (record, wave) the backward processes, the number of the wave's 64
  * lanes that take the record, as a histogram added into lanes [65] (uint64;
- * the caller clears it), and (c) the forward's walk, added into visits [2]
- * (uint64; the caller clears it): [0] the (pixel, record) visits of in-image
- * pixels, every list record up to the one that stops the pixel or to the
- * end of its list (a split tile's segments count their relative walks), and
- * [1] the (record, wave) pairs the forward processed, times 64 lanes. These
- * cost a few instructions per processed (record, wave), so the diagnostics
- * library is for measurement only.                                       */
+ * the caller clears it), and (c) work counters added into counters [8]
+ * (uint64; the caller clears it): [0] the forward's (pixel, record) visits
+ * of in-image pixels, every list record up to the one that stops the pixel
+ * or to the end of its list (a split tile's segments count their relative
+ * walks); [1] the (record, wave) pairs the forward processed, times 64
+ * lanes; [2] the (record, wave) pairs the backward processed; the wave
+ * steps those would take if each 32-lane half (8x4 pixels) or each 16-lane
+ * block (4x4) of the wave's quadrant walked its own records: [3] halves and
+ * [4] blocks at best (per batch the largest number of records any half or
+ * block takes), [5] halves and [6] blocks in list order (records taken by
+ * one half or block packed between records taken by several); [7] unused.
+ * These cost a few instructions per processed (record, wave), so the
+ * diagnostics library is for measurement only.                          */
 
 /* *available = 1 in the diagnostics library, 0 in the product library;
  * *wall_clock_khz = the current device's wall-clock rate. */
@@ -450,7 +459,7 @@ int gs_diagnostics_query(int32_t* available, int32_t* wall_clock_khz);
  * to record nothing; spans are written for tile indices below `tiles`).
  * Synchronous. The product library returns GS_ERR_ARGUMENT. */
 int gs_diagnostics_set(unsigned long long* lanes, long long* forward_span,
-                       long long* backward_span, int64_t tiles, unsigned long long* visits);
+                       long long* backward_span, int64_t tiles, unsigned long long* counters);
 
 /* ------------------------------------------------------------------ */
 /* Kernel timing for measurement: when enabled, each compositor / sort /

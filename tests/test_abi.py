@@ -146,19 +146,31 @@ def test_ctypes_signatures_match_the_header():
 
 def test_split_policy():
     """Split tiles: a fixed 64-record segment below 2048 image tiles, slots
-    enough for every tile longer than that (floor(2 M / 64)) up to the cap,
-    and an index buffer whose work list starts at an even offset."""
+    enough for every tile longer than that (floor(M / 64) + min(tiles,
+    floor(M / 65)) + 1) up to the cap, and an index buffer whose work list
+    starts at an even offset."""
     from diff_gabor_splatting_amd import _native
 
     assert _native.split_length(16, 1000) == 64
     assert _native.split_length(2047, 10**7) == 64  # independent of the count
     assert _native.split_length(2048, 1000) == 0 and _native.split_length(16, 0) == 0
-    assert _native.split_slots(89_449, 64) == 2_795
-    assert _native.split_slots(10**8, 64) == _native.SPLIT_MAX_SLOTS
-    assert _native.split_slots(1000, 0) == 0
-    # A tile of L > 64 records needs ceil(L / 64) <= floor(2 L / 64) slots.
-    for length in range(65, 2000):
-        assert -(-length // 64) <= 2 * length // 64
+    assert _native.split_slots(89_449, 64, 1024) == 1_397 + 1_024 + 1
+    assert _native.split_slots(89_449, 64, 4096) == 1_397 + 1_376 + 1
+    assert _native.split_slots(10**8, 64, 1024) == _native.SPLIT_MAX_SLOTS
+    assert _native.split_slots(1000, 0, 16) == 0
+    # Brute force: every way of cutting M records into tiles (here, random
+    # tile lengths) needs at most split_slots slots for its tiles longer
+    # than 64 records.
+    import random
+
+    rng = random.Random(5)
+    for _ in range(2000):
+        tiles = rng.randint(1, 64)
+        lengths = [rng.choice((0, 1, 63, 64, 65, 128, 129, rng.randint(0, 3000)))
+                   for _ in range(tiles)]
+        m = sum(lengths)
+        need = sum(-(-n // 64) for n in lengths if n > 64)
+        assert need <= _native.split_slots(m, 64, tiles) < _native.SPLIT_MAX_SLOTS
     assert _native.split_index_length(7, 10) == 18 + 34
     assert _native.split_index_length(8, 10) == 18 + 36
 

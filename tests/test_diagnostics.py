@@ -88,6 +88,13 @@ def test_walk_summary_counts():
                     "backward_samples_evaluated": 256, "backward_samples_taken": 70}
 
 
+def test_packing_summary_ratios():
+    summary = diagnostics.packing_summary([0, 0, 200, 180, 150, 195, 198, 0])
+    assert summary["wave_steps"] == 200 and summary["ratio_halves_at_best"] == 0.9
+    assert summary["ratio_blocks_in_order"] == 0.99
+    assert diagnostics.packing_summary([0] * 8)["ratio_halves_at_best"] is None
+
+
 def test_collect_restores_the_product_library(monkeypatch):
     """collect() renders through the diagnostics library and switches the
     package back to the library it used before, also when the run fails."""
@@ -129,6 +136,13 @@ def test_diagnostics_run_matches_the_replay_lists(tmp_path, workload):
     assert 1 <= lanes["mean_taking_lanes"] <= 64
     walk = report["forward_walk"]
     assert walk["backward_samples_taken"] <= walk["backward_samples_evaluated"]
+    packing = report["backward_packing"]
+    assert packing["wave_steps"] == lanes["record_wave_pairs"]
+    for kind in ("halves", "blocks"):
+        # Packing can only save steps, and never more than the at-best bound.
+        assert (packing[f"{kind}_at_best"] <= packing[f"{kind}_in_order"]
+                <= packing["wave_steps"])
+    assert packing["blocks_at_best"] <= packing["halves_at_best"]
     # Every in-image pixel visits at least the records it took; the lockstep
     # walk evaluates at least one sample per visit that passed the footprint
     # tests, and the tiles' lists bound the visits.

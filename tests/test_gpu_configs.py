@@ -25,8 +25,6 @@ pytestmark = [
 ]
 DEVICE = torch.device("cuda:0")
 FORWARD_TOL = dict(atol=1e-5, rtol=1e-4)
-# Largest share of pixels that may be ill-conditioned at float32 precision.
-MAX_FLAGGED = 0.03
 # Plain-bar comparison against a float32 evaluation of the same function:
 # the float32 torch oracle, on the same inputs and culling, is compared with
 # the float64 oracle pixel by pixel at 1e-5 / 1e-4 with no allowance.
@@ -38,7 +36,7 @@ MAX_FLAGGED = 0.03
 # not the other. The share of pixels where the float32 oracle itself misses
 # the bar is capped at MAX_FP32_MISSES (float32 rounding, not a perturbation
 # of the inputs, is the measure of conditioning here).
-PLAIN_BAR_EXCEPTIONS = 8
+PLAIN_BAR_EXCEPTIONS = 4
 MAX_FP32_MISSES = 0.03
 
 
@@ -98,29 +96,30 @@ def oracle_with_grads(cfg, values, opts, radii, weights):
 ENVELOPE_FACTOR = 4.0
 
 
-def compare_with_oracle(cfg, values, opts, result, seed, max_flagged=MAX_FLAGGED,
-                        envelope=False, label=""):
-    """Maps on well-conditioned pixels within 1e-5/1e-4; gradients of a loss
-    restricted to those pixels within 1e-3 (conditioning-aware, see
-    scenes.assert_gradients_close). At most `max_flagged` of the pixels may
-    be ill-conditioned (flagged by the float64 oracle's response to 5-ulp
-    input perturbations). With `envelope`, every map element - ill-conditioned
-    pixels included - must also lie within 1e-5/1e-4 plus ENVELOPE_FACTOR
-    times its float64 sensitivity (its largest change under the
-    conditioning perturbations), the form of the gradient bar.
+def compare_with_oracle(cfg, values, opts, result, seed, envelope=False, label=""):
+    """Maps at the plain bar and gradients at the gradient bar, with
+    float32 rounding as the measure of conditioning.
 
-    Plain bar: the float32 torch oracle is evaluated on the same inputs, and
-    wherever it is within 1e-5/1e-4 of the float64 oracle on every channel,
-    the HIP maps must be too, with at most PLAIN_BAR_EXCEPTIONS exceptions;
-    the float32 oracle may miss the bar on at most MAX_FP32_MISSES of the
-    pixels. Prints both pass counts and, per gradient tensor, the share of
-    elements the error-norm test covers. Returns the mask of well-conditioned
-    pixels."""
+    Maps: the float32 torch oracle is evaluated on the same inputs and
+    culling; wherever it is within 1e-5/1e-4 of the float64 oracle on every
+    channel, the HIP maps must be too, with at most PLAIN_BAR_EXCEPTIONS
+    exceptions, and the float32 oracle may miss the bar on at most
+    MAX_FP32_MISSES of the pixels. With `envelope`, every map element -
+    pixels the float32 oracle misses included - must also lie within
+    1e-5/1e-4 plus ENVELOPE_FACTOR times its float64 sensitivity (its largest
+    change under 5-ulp input perturbations), the form of the gradient bar.
+
+    Gradients: of a random-weighted loss over every pixel where both the
+    float32 oracle and HIP meet the plain bar, within 1e-3 (conditioning-
+    aware per element, see scenes.assert_gradients_close).
+
+    Prints both pass counts, the 5-ulp flagged count for comparison and,
+    per gradient tensor, the share of elements the error-norm test covers.
+    Returns the mask of pixels in the gradient loss."""
     maps = maps_from_result(result)
     radii = result[2]["radii"].cpu()
-    expected_base, mask, worst = fp32_conditioned(oracle_fn(cfg), values, radii=radii,
-                                                  return_worst=True, **opts)
-    assert float((~mask).float().mean()) <= max_flagged, float((~mask).float().mean())
+    expected_base, flagged_5ulp, worst = fp32_conditioned(oracle_fn(cfg), values, radii=radii,
+                                                          return_worst=True, **opts)
     single = {k: v.detach().cpu().float() for k, v in values.items()}
     with torch.no_grad():
         maps32 = oracle_fn(cfg)(**single, radii=radii, **opts)[0]
@@ -130,7 +129,7 @@ def compare_with_oracle(cfg, values, opts, result, seed, max_flagged=MAX_FLAGGED
     pixels = fp32_pass.numel()
     print(f"{label}plain bar 1e-5/1e-4 vs float64: HIP {int(hip_pass.sum())} of {pixels} "
           f"pixels, float32 oracle {int(fp32_pass.sum())}; HIP misses where float32 meets "
-          f"it: {exceptions}; 5-ulp flagged {int((~mask).sum())}", flush=True)
+          f"it: {exceptions}; 5-ulp flagged {int((~flagged_5ulp).sum())}", flush=True)
     assert exceptions <= PLAIN_BAR_EXCEPTIONS, (
         f"{exceptions} pixels miss the plain bar where the float32 oracle meets it")
     assert 1.0 - float(fp32_pass.double().mean()) <= MAX_FP32_MISSES, (
@@ -142,18 +141,19 @@ def compare_with_oracle(cfg, values, opts, result, seed, max_flagged=MAX_FLAGGED
         assert float(excess.max()) <= 0, (
             f"{int((excess > 0).sum())} map elements outside the envelope, worst by "
             f"{float(excess.max()):.3e}")
+    mask = fp32_pass & hip_pass
     weights = torch.randn(maps.shape, generator=torch.Generator().manual_seed(seed))
     weights = weights * mask[..., None]
     actual = torch.autograd.grad((maps * weights.to(DEVICE)).sum(), list(values.values()))
-    expected_maps, expected, sensitivity = oracle_reference(oracle_fn(cfg), values, weights,
-                                                            radii=radii, **opts)
-    torch.testing.assert_close(maps.detach().cpu().double()[mask], expected_maps[mask], **FORWARD_TOL)
+    _, expected, sensitivity = oracle_reference(oracle_fn(cfg), values, weights, radii=radii,
+                                                **opts)
     covered = {}
     for name, a in zip(values, actual):
         assert torch.isfinite(a).all(), name
         covered[name] = assert_gradients_close(a, expected[name], name, sensitivity[name])
-    print(f"{label}gradient elements under the error-norm test: "
-          + ", ".join(f"{name} {share:.3f}" for name, share in covered.items()), flush=True)
+    print(f"{label}gradient loss over {int(mask.sum())} of {pixels} pixels; elements under the "
+          f"error-norm test: " + ", ".join(f"{name} {share:.3f}" for name, share in covered.items()),
+          flush=True)
     return mask
 
 
@@ -249,13 +249,11 @@ CRITERIA = ("longest list", "most contributors", "early stop")
 # At the hardest tiles a pixel evaluates hundreds to thousands of records,
 # and nearly always one of them sits within 1e-3 (relative) of a discrete
 # threshold - alpha = 1/255, the 1e-4 stop, the surface/screen switch -
-# that projection amplifies a 5-ulp input change past. The 5-ulp test flags
-# such pixels (up to three quarters of a window where pixels composite over
-# a thousand records each), far more than float32 rounding actually moves:
-# there the cap is the plain-bar one of compare_with_oracle (the float32
-# oracle within 1e-5 / 1e-4 of float64 on all but MAX_FP32_MISSES of the
-# pixels, HIP wherever it is), and every pixel is also held to the envelope.
-MAX_FLAGGED_HARD = 1.0
+# that projection amplifies a 5-ulp input change past. A 5-ulp perturbation
+# test flags such pixels (up to three quarters of a window where pixels
+# composite over a thousand records each), far more than float32 rounding
+# actually moves: compare_with_oracle measures conditioning by the float32
+# oracle's own misses instead, and every pixel is also held to the envelope.
 
 
 def tile_statistics(cfg, ranges, contributors, state):
@@ -374,8 +372,7 @@ def test_hardest_tiles_match_oracle(hard_windows, index, criterion):
     print(f"config {index} {criterion}: image {w['image']} window ({w['x0']}, {w['y0']}) "
           f"tile {w['tile']}, {len(keep)} surfels; oracle check", flush=True)
     mask = compare_with_oracle(cfg, subset_values, opts, result, seed=17 * index,
-                               max_flagged=MAX_FLAGGED_HARD, envelope=True,
-                               label=f"config {index} {criterion}: ")
+                               envelope=True, label=f"config {index} {criterion}: ")
     # The crop's camera shifts the principal point, which changes float32
     # rounding in projection: on well-conditioned pixels the window of the
     # full render and the cropped render agree.
@@ -388,7 +385,8 @@ def test_hardest_tiles_match_oracle(hard_windows, index, criterion):
         oracle_fn(cfg)(**leaves, radii=result[2]["radii"].cpu(), stopped=stopped, **opts)
     stops = stopped["pixels"].reshape(mask.shape)
     checked_stops = int((stops & mask).sum())
-    print(f"config {index} {criterion}: masked {float((~mask).float().mean()):.4f}, "
+    print(f"config {index} {criterion}: outside the gradient loss "
+          f"{float((~mask).float().mean()):.4f}, "
           f"checked pixels stopped on T < 1e-4: {checked_stops} of {int(stops.sum())}, "
           f"longest list {w['list_length']} ({-(-w['list_length'] // 64)} batches), "
           f"largest contributor count {w['contributors']} "

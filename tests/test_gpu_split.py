@@ -170,3 +170,50 @@ def test_forward_bits_do_not_depend_on_grad_mode(method):
     recorded = maps_from_result(renderer(method)(**values, width=width, height=height))
     assert recorded.requires_grad
     assert torch.equal(frozen, recorded.detach())
+
+
+@pytest.mark.parametrize("method", ["classic", "neural"])
+def test_slots_past_capacity_leave_later_tiles_unsplit(method, monkeypatch):
+    """With fewer checkpoint slots than the long tiles need, the first long
+    tiles (in tile order) are split and later ones are walked whole inside
+    the split launch; the forward's work list and the backward's segment
+    order then mix split and unsplit long tiles. Contributor counts equal
+    the unsplit render's, maps and gradients agree with it to float32
+    rounding."""
+    width, height = 40, 36
+    values = heavy_scene(method, 0.5, width=width, height=height)
+    weights = torch.randn((1, 2, height, width, 9), generator=torch.Generator().manual_seed(9))
+    weights = weights.to(DEVICE)
+    print(f"slots past capacity: {method}", flush=True)
+    seen = spy_forward(monkeypatch)
+    with torch.no_grad():
+        renderer(method)(**values, width=width, height=height)
+    ranges = seen[-1][2]
+    lengths = (ranges[:, 1] - ranges[:, 0]).long().cpu()
+    need = (lengths + _native.SPLIT_LENGTH - 1) // _native.SPLIT_LENGTH
+    long_need = need[lengths > _native.SPLIT_LENGTH]
+    assert len(long_need) >= 2, "the scene needs two long tiles"
+    # Slots for the first long tile (in tile order) only.
+    capacity = int(long_need[0])
+    monkeypatch.setattr(_native, "SPLIT_MAX_SLOTS", capacity)
+    capped_maps, capped_grads = run(method, values, weights, width, height)
+    ranges, contributors, (_, _, segments) = seen[-1][2], seen[-1][4], seen[-1][5]
+    length, checkpoints, index = segments
+    assert checkpoints.shape[0] == capacity
+    tiles = ranges.shape[0]
+    lengths = (ranges[:, 1] - ranges[:, 0]).long().cpu()
+    base = index[:tiles].long().cpu()
+    long_tiles = lengths > length
+    split = base >= 0
+    assert int(split.sum()) > 0, "no tile was split"
+    assert int((long_tiles & ~split).sum()) > 0, "every long tile was split"
+    assert bool((split <= long_tiles).all())
+    monkeypatch.setattr(_native, "SPLIT_MAX_TILES", 0)
+    plain_maps, plain_grads = run(method, values, weights, width, height)
+    assert seen[-1][5][2] is None
+    assert torch.equal(contributors, seen[-1][4])
+    torch.testing.assert_close(capped_maps, plain_maps, atol=2e-6, rtol=2e-5)
+    for name, a, b in zip(values, capped_grads, plain_grads):
+        scale = float(b.abs().max())
+        err = float((a - b).abs().max())
+        assert err <= 1e-3 * scale + 1e-12, f"{name}: max error {err:.3e}, scale {scale:.3e}"
