@@ -143,6 +143,11 @@ _SIGNATURES = {
         _c_int,
         [_c_ptr] * 3 + [_c_i64, _c_int, _c_int] + [_c_ptr] * 6 + [_c_size, _c_ptr],
     ),
+    "gs_bin_order_count": (
+        _c_int,
+        [_c_ptr] * 3 + [_c_i64, _c_int, _c_int] + [_c_ptr] * 4 + [_c_size, _c_ptr],
+    ),
+    "gs_bin_order_sort": (_c_int, [_c_i64, _c_ptr, _c_ptr, _c_ptr, _c_size, _c_ptr]),
     "gs_bin_tiles_workspace_size": (_c_size, [_c_i64]),
     "gs_bin_tiles": (
         _c_int,

@@ -17,7 +17,8 @@
 //    the Q pairs are stably sorted on their 32 depth bits, each pair then
 //    emits its tiles in that order as 32-bit tile ids, and a stable sort on
 //    only bits(tiles) bits groups them by tile. The first stage needs no
-//    intersection count, so it runs while the host waits for M. A stable sort of depth-ordered entries by tile
+//    intersection count; M and V are summed by its first kernels, so the
+//    host reads them while the depth sort runs. A stable sort of depth-ordered entries by tile
 //    leaves each tile's entries ordered by (depth bits, pair index) - the
 //    order of the 64-bit sort - while the M entries move through two 8-bit
 //    passes of 8 bytes instead of 5-6 passes of 12 bytes.
@@ -148,7 +149,11 @@ __global__ __launch_bounds__(256) void find_ranges_kernel(int64_t m, int64_t til
 // Depth-first binning, stage 1, step 1: each pair's tile rectangle
 // (x0, y0, width, first tile id of its image) for stage 2, its tile count
 // (the rectangle area of countTiles) and its depth key; pairs without
-// tiles sort last.
+// tiles sort last. Each workgroup also stores its sums of the counts and of
+// the pairs with tiles in partials[block], which totals_kernel adds up into
+// M and V, so the host can read them before the pairs are sorted (plain
+// stores and one more launch: thousands of workgroups adding into one
+// device word would queue their atomics behind each other).
 __global__ __launch_bounds__(256) void pair_keys_kernel(int64_t count, int tw, int th,
                                                         const float* __restrict__ geometry,
                                                         const int* __restrict__ radii,
@@ -156,26 +161,85 @@ __global__ __launch_bounds__(256) void pair_keys_kernel(int64_t count, int tw, i
                                                         uint32_t* __restrict__ keys,
                                                         int* __restrict__ values,
                                                         int* __restrict__ counts,
-                                                        int4* __restrict__ rects) {
+                                                        int4* __restrict__ rects,
+                                                        long long* __restrict__ partials) {
+  __shared__ long long wave_sums[2][4];
   const int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x;
-  if (i >= count) return;
-  const int r = radii[i];
   int c = 0;
-  uint32_t key = 0xffffffffu;
-  int4 rect = make_int4(0, 0, 1, 0);
-  if (r > 0) {
-    const float* g = geometry + i * kGeometry;
-    const TileRect t = tile_rect(g[9], g[10], r, tw, th);
-    c = (t.x1 - t.x0) * (t.y1 - t.y0);
-    if (c > 0) {
-      key = __float_as_uint(g[8]);
-      rect = make_int4(t.x0, t.y0, t.x1 - t.x0, int(image_ids[i] * int64_t(tw) * th));
+  if (i < count) {
+    const int r = radii[i];
+    uint32_t key = 0xffffffffu;
+    int4 rect = make_int4(0, 0, 1, 0);
+    if (r > 0) {
+      const float* g = geometry + i * kGeometry;
+      const TileRect t = tile_rect(g[9], g[10], r, tw, th);
+      c = (t.x1 - t.x0) * (t.y1 - t.y0);
+      if (c > 0) {
+        key = __float_as_uint(g[8]);
+        rect = make_int4(t.x0, t.y0, t.x1 - t.x0, int(image_ids[i] * int64_t(tw) * th));
+      }
     }
+    counts[i] = c;
+    keys[i] = key;
+    values[i] = int(i);
+    rects[i] = rect;
   }
-  counts[i] = c;
-  keys[i] = key;
-  values[i] = int(i);
-  rects[i] = rect;
+  // Workgroup totals: wave sums by shuffles, then across the four waves.
+  long long sum = c, with_tiles = c > 0 ? 1 : 0;
+#pragma unroll
+  for (int offset = 32; offset > 0; offset >>= 1) {
+    sum += __shfl_xor(sum, offset, 64);
+    with_tiles += __shfl_xor(with_tiles, offset, 64);
+  }
+  const int wave = threadIdx.x >> 6;
+  if (__lane_id() == 0) {
+    wave_sums[0][wave] = sum;
+    wave_sums[1][wave] = with_tiles;
+  }
+  __syncthreads();
+  if (threadIdx.x < 2)
+    partials[2 * int64_t(blockIdx.x) + threadIdx.x] =
+        wave_sums[threadIdx.x][0] + wave_sums[threadIdx.x][1] + wave_sums[threadIdx.x][2] +
+        wave_sums[threadIdx.x][3];
+}
+
+// M and V from pair_keys_kernel's `blocks` workgroup totals (one
+// workgroup; `visible` may be null).
+constexpr int kTotalsBlock = 1024;
+__global__ __launch_bounds__(kTotalsBlock) void totals_kernel(const long long* __restrict__ partials,
+                                                             int64_t blocks, int64_t* total,
+                                                             int64_t* visible) {
+  __shared__ long long wave_sums[2][kTotalsBlock / 64];
+  long long sum = 0, with_tiles = 0;
+  for (int64_t b = threadIdx.x; b < blocks; b += kTotalsBlock) {
+    sum += partials[2 * b];
+    with_tiles += partials[2 * b + 1];
+  }
+#pragma unroll
+  for (int offset = 32; offset > 0; offset >>= 1) {
+    sum += __shfl_xor(sum, offset, 64);
+    with_tiles += __shfl_xor(with_tiles, offset, 64);
+  }
+  if (__lane_id() == 0) {
+    wave_sums[0][threadIdx.x >> 6] = sum;
+    wave_sums[1][threadIdx.x >> 6] = with_tiles;
+  }
+  __syncthreads();
+  if (threadIdx.x < 2) {
+    long long value = 0;
+#pragma unroll
+    for (int w = 0; w < kTotalsBlock / 64; ++w) value += wave_sums[threadIdx.x][w];
+    int64_t* target = threadIdx.x == 0 ? total : visible;
+    if (target) *target = value;
+  }
+}
+
+// No pairs: M = V = 0.
+__global__ __launch_bounds__(64) void zero_totals_kernel(int64_t* total, int64_t* visible) {
+  if (threadIdx.x == 0 && blockIdx.x == 0) {
+    *total = 0;
+    if (visible) *visible = 0;
+  }
 }
 
 struct SortedCountLoad {
@@ -184,27 +248,12 @@ struct SortedCountLoad {
   __device__ int64_t operator()(int64_t j) const { return counts[order[j]]; }
 };
 
-// starts[j] = entries of all lower depth ranks; the total is M. Pairs with
-// tiles come first in depth order (the others carry the largest key), so
-// the one rank j whose pair has tiles and whose successor has none (or rank
-// 0 when no pair has tiles) also records their number V in `visible`.
+// starts[j] = entries of all lower depth ranks (pair_keys_kernel has
+// already summed the total M).
 struct ExclusiveStartStore {
   int64_t* starts;
-  int64_t* total;
-  int64_t* visible;  // may be null
-  const int* counts;
-  const int* order;
-  int64_t count;
   __device__ void operator()(int64_t j, int64_t inclusive, int64_t v) const {
     starts[j] = inclusive - v;
-    if (j == count - 1) *total = inclusive;
-    if (visible) {
-      if (v > 0) {
-        if (j == count - 1 || counts[order[j + 1]] == 0) *visible = j + 1;
-      } else if (j == 0) {
-        *visible = 0;
-      }
-    }
   }
 };
 
@@ -359,6 +408,7 @@ struct OrderWorkspace {
   int* counts;         // count
   int64_t* scan_sums;
   void* sort;          // radix sort scratch for count keys
+  long long* partials;  // [ceil(count / 256)][2]: pair_keys_kernel's workgroup totals
   size_t bytes;
 };
 
@@ -377,6 +427,7 @@ OrderWorkspace order_layout(void* base, int64_t count) {
   w.counts = reinterpret_cast<int*>(take(size_t(count) * 4));
   w.scan_sums = reinterpret_cast<int64_t*>(take(scan_workspace_bytes(count, 8)));
   w.sort = take(radix_sort_workspace_bytes(count, 4));
+  w.partials = reinterpret_cast<long long*>(take(size_t(ceil_div(count, 256)) * 16));
   w.bytes = offset;
   return w;
 }
@@ -507,38 +558,50 @@ size_t gs_bin_order_workspace_size(int64_t count) {
   return gs::order_layout(nullptr, count).bytes + 256;
 }
 
-int gs_bin_order(const float* geometry, const int32_t* radii, const int64_t* image_ids,
-                 int64_t count, int32_t width, int32_t height, int32_t* order, int64_t* starts,
-                 int32_t* rects, int64_t* intersections, int64_t* visible, void* workspace,
-                 size_t workspace_bytes, void* stream) {
+int gs_bin_order_count(const float* geometry, const int32_t* radii, const int64_t* image_ids,
+                       int64_t count, int32_t width, int32_t height, int32_t* rects,
+                       int64_t* intersections, int64_t* visible, void* workspace,
+                       size_t workspace_bytes, void* stream) {
   using namespace gs;
   clear_error();
   GS_REQUIRE(count >= 0 && count <= INT_MAX, GS_ERR_OVERFLOW, "too many projected primitives");
   GS_REQUIRE(width > 0 && height > 0, GS_ERR_ARGUMENT, "invalid image dimensions");
   GS_REQUIRE(intersections, GS_ERR_ARGUMENT, "null intersections");
   hipStream_t s = static_cast<hipStream_t>(stream);
+  ProfileScope prof(GS_PROF_BINNING, s);
   if (count == 0) {
-    zero_count_kernel<<<1, 64, 0, s>>>(intersections);
-    GS_LAUNCHED("zero_count_kernel");
-    if (visible) {
-      zero_count_kernel<<<1, 64, 0, s>>>(visible);
-      GS_LAUNCHED("zero_count_kernel");
-    }
+    zero_totals_kernel<<<1, 64, 0, s>>>(intersections, visible);
+    GS_LAUNCHED("zero_totals_kernel");
     return GS_OK;
   }
-  GS_REQUIRE(geometry && radii && image_ids && order && starts && rects, GS_ERR_ARGUMENT,
-             "null pointer passed to gs_bin_order");
+  GS_REQUIRE(geometry && radii && image_ids && rects, GS_ERR_ARGUMENT,
+             "null pointer passed to gs_bin_order_count");
   const size_t need = gs_bin_order_workspace_size(count);
   GS_REQUIRE(workspace && workspace_bytes >= need, GS_ERR_WORKSPACE,
              "binning needs %zu workspace bytes, got %zu", need, workspace_bytes);
   OrderWorkspace w = order_layout(workspace, count);
-  {
-    ProfileScope prof(GS_PROF_BINNING, s);
-    pair_keys_kernel<<<unsigned(ceil_div(count, 256)), 256, 0, s>>>(
-        count, tiles_x(width), tiles_y(height), geometry, radii, image_ids, w.keys, w.pair_ids,
-        w.counts, reinterpret_cast<int4*>(rects));
-    GS_LAUNCHED("pair_keys_kernel");
-  }
+  const int64_t blocks = ceil_div(count, 256);
+  pair_keys_kernel<<<unsigned(blocks), 256, 0, s>>>(
+      count, tiles_x(width), tiles_y(height), geometry, radii, image_ids, w.keys, w.pair_ids,
+      w.counts, reinterpret_cast<int4*>(rects), w.partials);
+  GS_LAUNCHED("pair_keys_kernel");
+  totals_kernel<<<1, kTotalsBlock, 0, s>>>(w.partials, blocks, intersections, visible);
+  GS_LAUNCHED("totals_kernel");
+  return GS_OK;
+}
+
+int gs_bin_order_sort(int64_t count, int32_t* order, int64_t* starts, void* workspace,
+                      size_t workspace_bytes, void* stream) {
+  using namespace gs;
+  clear_error();
+  GS_REQUIRE(count >= 0 && count <= INT_MAX, GS_ERR_OVERFLOW, "too many projected primitives");
+  if (count == 0) return GS_OK;
+  GS_REQUIRE(order && starts, GS_ERR_ARGUMENT, "null pointer passed to gs_bin_order_sort");
+  const size_t need = gs_bin_order_workspace_size(count);
+  GS_REQUIRE(workspace && workspace_bytes >= need, GS_ERR_WORKSPACE,
+             "binning needs %zu workspace bytes, got %zu", need, workspace_bytes);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  OrderWorkspace w = order_layout(workspace, count);
   {
     ProfileScope prof(GS_PROF_SORT, s);
     int status = radix_sort<uint32_t>(w.keys, w.sorted, w.pair_ids, order, count, 0, 32, w.sort,
@@ -546,10 +609,24 @@ int gs_bin_order(const float* geometry, const int32_t* radii, const int64_t* ima
     if (status != GS_OK) return status;
   }
   ProfileScope prof(GS_PROF_BINNING, s);
-  return run_scan<int64_t>(count, SortedCountLoad{w.counts, order},
-                           ExclusiveStartStore{starts, intersections, visible, w.counts, order,
-                                               count},
+  return run_scan<int64_t>(count, SortedCountLoad{w.counts, order}, ExclusiveStartStore{starts},
                            w.scan_sums, s);
+}
+
+int gs_bin_order(const float* geometry, const int32_t* radii, const int64_t* image_ids,
+                 int64_t count, int32_t width, int32_t height, int32_t* order, int64_t* starts,
+                 int32_t* rects, int64_t* intersections, int64_t* visible, void* workspace,
+                 size_t workspace_bytes, void* stream) {
+  using namespace gs;
+  clear_error();
+  GS_REQUIRE(count >= 0 && count <= INT_MAX, GS_ERR_OVERFLOW, "too many projected primitives");
+  GS_REQUIRE(count == 0 || (order && starts), GS_ERR_ARGUMENT,
+             "null pointer passed to gs_bin_order");
+  const int status = gs_bin_order_count(geometry, radii, image_ids, count, width, height, rects,
+                                        intersections, visible, workspace, workspace_bytes,
+                                        stream);
+  if (status != GS_OK) return status;
+  return gs_bin_order_sort(count, order, starts, workspace, workspace_bytes, stream);
 }
 
 size_t gs_bin_tiles_workspace_size(int64_t m) {

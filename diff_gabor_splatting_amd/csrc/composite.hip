@@ -984,6 +984,102 @@ __global__ __launch_bounds__(kOrderBlock) void tile_order_kernel(const int* __re
   }
 }
 
+// Forward cost estimate of each tile, for images with few tiles per
+// workgroup slot of the GPU (2-4 rounds of workgroups), where the forward's
+// length is set by the heaviest tiles and a heavy tile that starts late
+// leaves most of the GPU idle behind it. The list length orders such tiles
+// poorly when the lists are about equally long: a tile's cost is how far its
+// pixels walk before the 1e-4 transmittance rule stops them. One wave per
+// tile walks the tile's list for four probe pixels, the centres of its 8x8
+// quadrants, 64 records at a time: lane j takes list position first + j,
+// evaluates the record's alpha at each probe (the acceptance tests of
+// sample_surface), and a wave prefix sum of log2(1 - alpha) locates the
+// record that stops each probe. The cost is the longest of the four walks
+// (the workgroup walks its batches until every wave's pixels are done). It
+// only orders the tiles: no result depends on it.
+constexpr int kProbeMaxTiles = 6144;  // 4 rounds of 256 CUs x 6 workgroups
+
+template <bool Neural>
+__global__ __launch_bounds__(256) void tile_probe_kernel(
+    int tiles, int width, int height, int tw, int th, const float* __restrict__ geometry,
+    const float* __restrict__ opacities, const int64_t* __restrict__ primitive_ids,
+    const int* __restrict__ point_list, const int2* __restrict__ ranges, float near_plane,
+    int* __restrict__ cost) {
+  const int tile = int(blockIdx.x) * (256 / 64) + int(threadIdx.x >> 6);
+  if (tile >= tiles) return;  // uniform over the wave
+  const int lane = lane_id();
+  const int local = tile % (tw * th);
+  const int x0 = (local % tw) * kTile, y0 = (local / tw) * kTile;
+  const int2 range = ranges[tile];
+  const int length = range.y - range.x;
+  constexpr float kLog2Stop = -13.287712379549449f;  // log2(1e-4)
+  float log_t[4];
+  int walked[4];
+  bool live[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int px = x0 + (q & 1) * 8 + 4, py = y0 + (q >> 1) * 8 + 4;
+    log_t[q] = 0.f;
+    live[q] = px < width && py < height;
+    walked[q] = live[q] ? length : 0;
+  }
+  for (int first = 0; first < length && (live[0] | live[1] | live[2] | live[3]);
+       first += 64) {
+    const int position = first + lane;
+    float step[4] = {0.f, 0.f, 0.f, 0.f};
+    if (position < length) {
+      const int id = point_list[range.x + position];
+      const float* g = geometry + int64_t(id) * kGeometry;
+      float t[11];
+#pragma unroll
+      for (int i = 0; i < 11; ++i) t[i] = g[i];
+      const float o = opacities[primitive_ids[id]];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const float x = float(x0 + (q & 1) * 8 + 4), y = float(y0 + (q >> 1) * 8 + 4);
+        float k[3], l[3];
+#pragma unroll
+        for (int i = 0; i < 3; ++i) {
+          k[i] = x * t[6 + i] - t[i];
+          l[i] = y * t[6 + i] - t[3 + i];
+        }
+        const float p0 = k[1] * l[2] - k[2] * l[1];
+        const float p1 = k[2] * l[0] - k[0] * l[2];
+        const float p2 = k[0] * l[1] - k[1] * l[0];
+        const float inv = rcp(p2);
+        const float s0 = p0 * inv, s1 = p1 * inv;
+        const float rho3 = s0 * s0 + s1 * s1;
+        const float dx = t[9] - x, dy = t[10] - y;
+        const float rho2 = 2.f * (dx * dx + dy * dy);
+        const float depth =
+            (Neural || rho3 <= rho2) ? fmaf(s0, t[6], fmaf(s1, t[7], t[8])) : t[8];
+        const float alpha = fminf(0.99f, o * __builtin_amdgcn_exp2f(fminf(rho3, rho2) *
+                                                                      kNegHalfLog2e));
+        const bool ok = (p2 != 0.f) & (depth >= near_plane) & isfinite(depth) &
+                        (alpha >= kMinAlpha);
+        step[q] = ok ? __builtin_amdgcn_logf(1.f - alpha) : 0.f;
+      }
+    }
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      float prefix = step[q];  // inclusive prefix sum over the wave's lanes
+#pragma unroll
+      for (int d = 1; d < 64; d <<= 1) {
+        const float up = __shfl_up(prefix, d, 64);
+        if (lane >= d) prefix += up;
+      }
+      const uint64_t stops = __ballot(log_t[q] + prefix < kLog2Stop);
+      if (live[q] && stops) {
+        walked[q] = min(length, first + __builtin_ctzll(stops) + 1);
+        live[q] = false;
+      }
+      log_t[q] += __shfl(prefix, 63, 64);
+    }
+  }
+  if (lane == 0)
+    cost[tile] = max(max(walked[0], walked[1]), max(walked[2], walked[3]));
+}
+
 // The backward's workgroups when tiles are split: every (tile, segment) with
 // its replay entries as cost, heaviest first, into segments[0 .. tiles +
 // seg.capacity); entries past the segment count are (-1, 0) and their
@@ -1931,7 +2027,7 @@ __global__ __launch_bounds__(kTilePixels, Neural && !Replay ? 2 : 4) void render
 
 struct RenderWorkspace {
   int* order;      // [tiles]
-  int* tile_last;  // [tiles]
+  int* tile_last;  // [tiles]: the backward's start per tile; the forward's probed costs
   int2* segments;  // [tiles + segment slots]: the backward's (tile, segment) order
   size_t bytes;
 };
@@ -2038,12 +2134,25 @@ int render_forward(int32_t neural, const float* geometry, const float* appearanc
                    int64_t images, int32_t width, int32_t height, float near_plane,
                    float far_plane, const MapGroups<float>& out, float* state,
                    int32_t* contributors, int32_t* replay, int32_t* replay_counts, int* order,
-                   const Segments& seg, hipStream_t s) {
+                   int* probe, const Segments& seg, hipStream_t s) {
   ProfileScope prof(GS_PROF_RENDER_FWD, s);
   const int tw = tiles_x(width), th = tiles_y(height);
   const int tiles = int(images * tw * th);
   const int2* r = reinterpret_cast<const int2*>(ranges);
-  tile_order_kernel<<<1, kOrderBlock, 0, s>>>(nullptr, r, tiles, order, seg);
+  // Few rounds of workgroups: order by the probed walk lengths instead of
+  // the list lengths (tile_probe_kernel).
+  const bool probed = probe && !seg.length && tiles <= kProbeMaxTiles;
+  if (probed) {
+    auto run = [&](auto kernel) {
+      kernel<<<unsigned(ceil_div(tiles, 256 / 64)), 256, 0, s>>>(
+          tiles, width, height, tw, th, geometry, opacities, primitive_ids, point_list, r,
+          near_plane, probe);
+    };
+    if (neural) run(tile_probe_kernel<true>);
+    else run(tile_probe_kernel<false>);
+    GS_LAUNCHED("tile_probe_kernel");
+  }
+  tile_order_kernel<<<1, kOrderBlock, 0, s>>>(probed ? probe : nullptr, r, tiles, order, seg);
   GS_LAUNCHED("tile_order_kernel");
   int2* lists = reinterpret_cast<int2*>(replay);
   const unsigned blocks = unsigned(seg.length ? tiles + seg.capacity : tiles);
@@ -2151,7 +2260,8 @@ int gs_render_forward(int32_t neural, const float* geometry, const float* appear
   return render_forward(neural, geometry, appearance, opacities, primitive_ids, backgrounds,
                         point_list, ranges, images, width, height, near_plane, far_plane,
                         map_groups(maps, map_strides), state, contributors, replay,
-                        replay_counts, w.order, seg, static_cast<hipStream_t>(stream));
+                        replay_counts, w.order, w.tile_last, seg,
+                        static_cast<hipStream_t>(stream));
 }
 
 int gs_render_forward_static(int32_t neural, const float* geometry, const float* appearance,
@@ -2181,7 +2291,7 @@ int gs_render_forward_static(int32_t neural, const float* geometry, const float*
   return render_forward(neural, geometry, appearance, opacities, primitive_ids, backgrounds,
                         point_list, ranges, images, width, height, near_plane, far_plane,
                         map_groups(maps, map_strides), state, contributors, replay,
-                        replay_counts, order,
+                        replay_counts, order, nullptr,
                         Segments{0, int(tiles), 0, nullptr, nullptr, nullptr}, s);
 }
 

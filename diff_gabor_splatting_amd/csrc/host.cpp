@@ -55,7 +55,8 @@ struct Api {
   decltype(&gs_records_backward_workspace_size) records_backward_workspace_size = nullptr;
   decltype(&gs_records_backward) records_backward = nullptr;
   decltype(&gs_bin_order_workspace_size) bin_order_workspace_size = nullptr;
-  decltype(&gs_bin_order) bin_order = nullptr;
+  decltype(&gs_bin_order_count) bin_order_count = nullptr;
+  decltype(&gs_bin_order_sort) bin_order_sort = nullptr;
   decltype(&gs_bin_tiles_workspace_size) bin_tiles_workspace_size = nullptr;
   decltype(&gs_bin_tiles) bin_tiles = nullptr;
   decltype(&gs_bin_tiles_bounded) bin_tiles_bounded = nullptr;
@@ -88,7 +89,8 @@ void bind(const py::dict& table) {
   take(table, "gs_records_backward_workspace_size", next.records_backward_workspace_size);
   take(table, "gs_records_backward", next.records_backward);
   take(table, "gs_bin_order_workspace_size", next.bin_order_workspace_size);
-  take(table, "gs_bin_order", next.bin_order);
+  take(table, "gs_bin_order_count", next.bin_order_count);
+  take(table, "gs_bin_order_sort", next.bin_order_sort);
   take(table, "gs_bin_tiles_workspace_size", next.bin_tiles_workspace_size);
   take(table, "gs_bin_tiles", next.bin_tiles);
   take(table, "gs_bin_tiles_bounded", next.bin_tiles_bounded);
@@ -103,7 +105,8 @@ void bind(const py::dict& table) {
 std::vector<std::string> entry_points() {
   return {"gs_last_error", "gs_check_values", "gs_scan_workspace_size", "gs_pack_visible",
           "gs_records_forward", "gs_records_backward_workspace_size", "gs_records_backward",
-          "gs_bin_order_workspace_size", "gs_bin_order", "gs_bin_tiles_workspace_size",
+          "gs_bin_order_workspace_size", "gs_bin_order_count", "gs_bin_order_sort",
+          "gs_bin_tiles_workspace_size",
           "gs_bin_tiles", "gs_bin_tiles_bounded", "gs_render_workspace_size",
           "gs_render_backward_workspace_size", "gs_render_forward", "gs_render_backward"};
 }
@@ -492,23 +495,46 @@ py::tuple records_backward(const at::Tensor& means, const at::Tensor& quaternion
 // --------------------------------------------------------------------------
 // Depth-first binning.
 
+// Stage 1 of depth-first binning in its two calls. count_stage makes the
+// rectangles and counts and sums M and V into totals; sort_stage orders the
+// pairs by depth from the same workspace.
+struct OrderStage {
+  at::Tensor order, starts, rects, totals, space;
+  int64_t count = 0;
+};
+
+OrderStage count_stage(const at::Tensor& geometry, const at::Tensor& radii,
+                       const at::Tensor& image_ids, int64_t width, int64_t height) {
+  const at::Device device = geometry.device();
+  OrderStage stage;
+  stage.count = geometry.size(0);
+  stage.order = at::empty({stage.count}, on(device, at::kInt));
+  stage.starts = at::empty({stage.count}, on(device, at::kLong));
+  stage.rects = at::empty({stage.count, 4}, on(device, at::kInt));
+  stage.totals = at::empty({2}, on(device, at::kLong));
+  stage.space = workspace(api.bin_order_workspace_size(stage.count), device);
+  check(api.bin_order_count(ptr<const float>(geometry), ptr<const int32_t>(radii),
+                            ptr<const int64_t>(image_ids), stage.count, int32_t(width),
+                            int32_t(height), ptr<int32_t>(stage.rects),
+                            ptr<int64_t>(stage.totals), ptr<int64_t>(stage.totals) + 1,
+                            stage.space.data_ptr(), size_t(stage.space.numel()),
+                            stream_of(device)));
+  return stage;
+}
+
+void sort_stage(OrderStage& stage) {
+  check(api.bin_order_sort(stage.count, ptr<int32_t>(stage.order), ptr<int64_t>(stage.starts),
+                           stage.space.data_ptr(), size_t(stage.space.numel()),
+                           stream_of(stage.order.device())));
+}
+
 py::tuple bin_order(const at::Tensor& geometry, const at::Tensor& radii,
                     const at::Tensor& image_ids, int64_t width, int64_t height) {
   require_bound();
-  const at::Device device = geometry.device();
-  const int64_t count = geometry.size(0);
-  c10::DeviceGuard guard(device);
-  const at::Tensor order = at::empty({count}, on(device, at::kInt));
-  const at::Tensor starts = at::empty({count}, on(device, at::kLong));
-  const at::Tensor rects = at::empty({count, 4}, on(device, at::kInt));
-  const at::Tensor totals = at::empty({2}, on(device, at::kLong));
-  const at::Tensor space = workspace(api.bin_order_workspace_size(count), device);
-  check(api.bin_order(ptr<const float>(geometry), ptr<const int32_t>(radii),
-                      ptr<const int64_t>(image_ids), count, int32_t(width), int32_t(height),
-                      ptr<int32_t>(order), ptr<int64_t>(starts), ptr<int32_t>(rects),
-                      ptr<int64_t>(totals), ptr<int64_t>(totals) + 1, space.data_ptr(),
-                      size_t(space.numel()), stream_of(device)));
-  return py::make_tuple(order, starts, rects, totals);
+  c10::DeviceGuard guard(geometry.device());
+  OrderStage stage = count_stage(geometry, radii, image_ids, width, height);
+  sort_stage(stage);
+  return py::make_tuple(stage.order, stage.starts, stage.rects, stage.totals);
 }
 
 std::pair<at::Tensor, at::Tensor> bin_tiles_impl(const at::Tensor& order, const at::Tensor& starts,
@@ -562,10 +588,12 @@ py::tuple bin_tiles_bounded(const at::Tensor& order, const at::Tensor& starts,
 }
 
 // Both binning stages with the one host synchronisation for M between them
-// (rasterize.cu:466-469). M and V are copied to pinned host memory behind
-// stage 1 and the host waits on an event recorded after that copy, not on
-// the stream, so GPU work that overlap() queues runs during the wait (the
-// wait itself releases the GIL). With a capacity there is no
+// (rasterize.cu:466-469). Stage 1's first kernel sums M and V; they are
+// copied to pinned host memory right behind it, and the host waits on an
+// event recorded after that copy, not on the stream: the depth sort (queued
+// before the wait) and GPU work that overlap() queues run during the wait
+// (which releases the GIL) and while the host then queues stage 2, so the
+// read-back leaves no gap on the GPU. With a capacity there is no
 // synchronisation: flags(overflow, total) receives the status word and the
 // live count, both on the device. violations = (device int32 word, function
 // raising for a nonzero word) is read back with M and reported before M is
@@ -575,16 +603,13 @@ std::pair<at::Tensor, at::Tensor> bin_depth_first_impl(
     int64_t images, int64_t width, int64_t height, const py::object& overlap,
     const std::optional<int64_t>& capacity, const py::object& flags,
     const py::object& violations) {
-  const py::tuple stage = bin_order(geometry, radii, image_ids, width, height);
-  const at::Tensor order = stage[0].cast<at::Tensor>();
-  const at::Tensor starts = stage[1].cast<at::Tensor>();
-  const at::Tensor rects = stage[2].cast<at::Tensor>();
-  const at::Tensor totals = stage[3].cast<at::Tensor>();
-  const at::Tensor total = totals.slice(0, 0, 1);
+  OrderStage stage = count_stage(geometry, radii, image_ids, width, height);
+  const at::Tensor total = stage.totals.slice(0, 0, 1);
   if (capacity) {
+    sort_stage(stage);
     if (!overlap.is_none()) overlap();
-    const py::tuple bounded =
-        bin_tiles_bounded(order, starts, rects, images, width, height, *capacity, total);
+    const py::tuple bounded = bin_tiles_bounded(stage.order, stage.starts, stage.rects, images,
+                                                width, height, *capacity, total);
     if (!flags.is_none()) flags(bounded[2], total);
     return {bounded[0].cast<at::Tensor>(), bounded[1].cast<at::Tensor>()};
   }
@@ -592,7 +617,7 @@ std::pair<at::Tensor, at::Tensor> bin_depth_first_impl(
   hipStream_t stream = static_cast<hipStream_t>(stream_of(device));
   Readback& state = readback();
   const hipEvent_t ready = readback_event(state, device);
-  check_hip(hipMemcpyAsync(state.host, totals.data_ptr(), 2 * sizeof(int64_t),
+  check_hip(hipMemcpyAsync(state.host, stage.totals.data_ptr(), 2 * sizeof(int64_t),
                            hipMemcpyDeviceToHost, stream),
             "hipMemcpyAsync");
   at::Tensor word;
@@ -610,15 +635,14 @@ std::pair<at::Tensor, at::Tensor> bin_depth_first_impl(
     py::gil_scoped_release released;
     return hipEventSynchronize(ready);
   };
-  if (!overlap.is_none()) {
-    try {
-      overlap();
-    } catch (...) {
-      // The copy into this thread's pinned buffer must land before the
-      // buffer can be reused by a later call, possibly on another stream.
-      wait();
-      throw;
-    }
+  try {
+    sort_stage(stage);
+    if (!overlap.is_none()) overlap();
+  } catch (...) {
+    // The copy into this thread's pinned buffer must land before the
+    // buffer can be reused by a later call, possibly on another stream.
+    wait();
+    throw;
   }
   check_hip(wait(), "hipEventSynchronize");
   const int64_t intersections = state.host[0], visible = state.host[1];
@@ -627,8 +651,8 @@ std::pair<at::Tensor, at::Tensor> bin_depth_first_impl(
     report(value);
   }
   require(intersections <= kIntMax, "tile intersection count exceeds int32");
-  return bin_tiles_impl(order, starts, rects, images, width, height, intersections, visible,
-                        std::nullopt);
+  return bin_tiles_impl(stage.order, stage.starts, stage.rects, images, width, height,
+                        intersections, visible, std::nullopt);
 }
 
 py::tuple bin_depth_first(const at::Tensor& geometry, const at::Tensor& radii,

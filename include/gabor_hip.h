@@ -276,6 +276,21 @@ int gs_bin_order(const float* geometry, const int32_t* radii, const int64_t* ima
                  int32_t* rects, int64_t* intersections, int64_t* visible, void* workspace,
                  size_t workspace_bytes, void* stream);
 
+/* gs_bin_order in two calls, so that the host can read M and V back while
+ * the pairs are sorted. No counterpart in the reference, which sums the
+ * counts with its scan after countTiles (rasterize.cu:459-469).
+ * gs_bin_order_count: the rectangles, counts and depth keys of stage 1,
+ * rects as in gs_bin_order, and *intersections = M, *visible = V (null:
+ * not wanted), summed as the counts are made. gs_bin_order_sort: the depth
+ * order and starts of stage 1 from what gs_bin_order_count left in the same
+ * workspace (same count; the workspace untouched in between). */
+int gs_bin_order_count(const float* geometry, const int32_t* radii, const int64_t* image_ids,
+                       int64_t count, int32_t width, int32_t height, int32_t* rects,
+                       int64_t* intersections, int64_t* visible, void* workspace,
+                       size_t workspace_bytes, void* stream);
+int gs_bin_order_sort(int64_t count, int32_t* order, int64_t* starts, void* workspace,
+                      size_t workspace_bytes, void* stream);
+
 /* Scratch bytes for gs_bin_tiles over m intersections. */
 size_t gs_bin_tiles_workspace_size(int64_t m);
 

@@ -167,6 +167,20 @@ def test_depth_first_binning_is_bit_exact(native, seed, q, width, height, images
                                                      height)
     order, starts, rects, totals = native.bin_order(g, r, ids, width, height)
     assert totals.tolist() == [m, visible]
+    # The one-call entry point (gs_bin_order) gives the same stage-1 outputs
+    # as the renderer's two calls (gs_bin_order_count, gs_bin_order_sort).
+    lib = native.lib
+    single = [torch.full_like(t, -9) for t in (order, starts, rects, totals)]
+    space = torch.empty(lib.gs_bin_order_workspace_size(q), dtype=torch.uint8, device=DEVICE)
+    status = lib.gs_bin_order(g.data_ptr(), r.data_ptr(), ids.data_ptr(), q, width, height,
+                              single[0].data_ptr(), single[1].data_ptr(), single[2].data_ptr(),
+                              single[3].data_ptr(), single[3].data_ptr() + 8, space.data_ptr(),
+                              space.numel(), torch.cuda.current_stream(DEVICE).cuda_stream)
+    assert status == 0, lib.gs_last_error()
+    torch.cuda.synchronize()
+    for name, a, b in zip(("order", "starts", "rects", "totals"), single,
+                          (order, starts, rects, totals)):
+        assert torch.equal(a, b), name
     for known in (visible, -1):
         point_list, ranges = native.bin_tiles(order, starts, rects, images, width, height, m,
                                               known)
