@@ -5,7 +5,7 @@ package alone does not, so ``diff_gabor_splatting_amd.build`` can rebuild a
 stale library). There is no CPU fallback: a missing library raises.
 """
 
-__all__ = ["rasterize_gabors", "rasterize_neural_gabors", "fixed_capacity"]
+__all__ = ["rasterize_gabors", "rasterize_neural_gabors", "fixed_capacity", "single_map_storage"]
 
 
 def __getattr__(name):

@@ -40,27 +40,38 @@ class Composite(torch.autograd.Function):
     into its own zero-filled full-size tensor and sum the five, while here
     the backward kernel reads each group's gradient where it lies (for a
     loss over ``torch.cat`` of the maps, straight out of the concatenated
-    gradient) and missing groups cost nothing.
+    gradient) and missing groups cost nothing. With ``single`` (the
+    single_map_storage context) it returns the reference's one [..., C, H,
+    W, 9] tensor, which render() slices as the reference does.
     """
 
     @staticmethod
     def forward(
         ctx: Any, geometry, projected_means, appearance, opacities, primitive_ids, image_ids,
         radii, backgrounds, width, height, neural, near_plane, far_plane, bounded=None,
-        grad_mode=True, violations=None,
+        grad_mode=True, violations=None, single=False,
     ):
         # backgrounds [..., C, 3]; the maps come out as [..., C, H, W, k]
         # directly (the kernels see them as [I, H, W, k]), so the caller's
-        # shapes need no view nodes in the autograd graph.
+        # shapes need no view nodes in the autograd graph. With `single`
+        # they come out as one [..., C, H, W, 9] tensor instead (the
+        # reference's layout, rendering.py:375-400), which the kernels write
+        # through five strided channel groups.
         image_shape = tuple(backgrounds.shape[:-1]) + (height, width)
         ctx.background_shape = backgrounds.shape
+        ctx.single = single
         backgrounds = backgrounds.reshape(-1, 3)
         images = backgrounds.size(0)
-        shaped = tuple(
-            torch.empty(image_shape + (k,), dtype=torch.float32, device=geometry.device)
-            for k in _native.MAP_GROUPS
-        )
-        outputs = tuple(t.view(images, height, width, t.shape[-1]) for t in shaped)
+        if single:
+            shaped = torch.empty(image_shape + (sum(_native.MAP_GROUPS),), dtype=torch.float32,
+                                 device=geometry.device)
+            outputs = _native.split_map_groups(shaped.view(images, height, width, -1))
+        else:
+            shaped = tuple(
+                torch.empty(image_shape + (k,), dtype=torch.float32, device=geometry.device)
+                for k in _native.MAP_GROUPS
+            )
+            outputs = tuple(t.view(images, height, width, t.shape[-1]) for t in shaped)
         # The backward's zeroed accumulators are cleared while the host waits
         # for the intersection count, when the GPU would otherwise idle.
         ctx.accumulators = None
@@ -105,14 +116,22 @@ class Composite(torch.autograd.Function):
         *saved, lists, counts, checkpoints, checkpoint_index = ctx.saved_tensors
         segments = (ctx.split, checkpoints, checkpoint_index) if ctx.split else None
         width, height = ctx.options[:2]
-        groups = [None if g is None else g.reshape(-1, height, width, g.shape[-1])
-                  for g in grad_groups]
+        if ctx.single:
+            grad = grad_groups[0]
+            if grad is None:
+                groups = [None] * len(_native.MAP_GROUPS)
+            else:
+                grad = grad.reshape(-1, height, width, grad.shape[-1]).contiguous()
+                groups = list(_native.split_map_groups(grad))
+        else:
+            groups = [None if g is None else g.reshape(-1, height, width, g.shape[-1])
+                      for g in grad_groups]
         gg, ga, go, gb = _native.rasterize_backward(
             *saved, groups, *ctx.options, accumulators=accumulators,
             replay=None if lists is None else (lists, counts, segments),
         )
         return (gg, gg[:, 9:11], ga, go, None, None, None, gb.view(ctx.background_shape), None,
-                None, None, None, None, None, None, None)
+                None, None, None, None, None, None, None, None)
 
 
 class ProjectRecords(torch.autograd.Function):
@@ -418,6 +437,27 @@ def fixed_capacity(max_intersections: int) -> FixedCapacity:
     return FixedCapacity(max_intersections)
 
 
+_SINGLE_MAP_STORAGE: list[bool] = []
+
+
+class single_map_storage:  # noqa: N801 - a context manager, named like fixed_capacity
+    """Context manager: renders inside it return rgb, alpha and the three map
+    entries of ``meta`` as views of one [..., C, H, W, 9] tensor, as the
+    reference does (rendering.py:375-400): same values, the reference's
+    strides and shared ``_base``, and in-place changes of one view visible
+    through the others. Outside it the five maps are separate contiguous
+    tensors, which spares autograd from assembling the full [..., 9]
+    gradient out of zero-filled slice gradients in the backward. Contexts
+    nest; the setting is process-wide."""
+
+    def __enter__(self) -> "single_map_storage":
+        _SINGLE_MAP_STORAGE.append(True)
+        return self
+
+    def __exit__(self, *exc) -> None:
+        _SINGLE_MAP_STORAGE.pop()
+
+
 def quaternion_matrix(q: torch.Tensor) -> torch.Tensor:
     """Normalised wxyz quaternions to rotation matrices (rendering.py:156-173)."""
     q = q / torch.linalg.vector_norm(q, dim=-1, keepdim=True)
@@ -568,7 +608,8 @@ def render(
         if screen_points.shape != projected_means.shape:
             raise ValueError(f"screen_points must have shape {tuple(projected_means.shape)}")
         screen_means = projected_means + (screen_points - screen_points.detach())
-    rgb, alpha, depth, normals, distortion = Composite.apply(
+    single = bool(_SINGLE_MAP_STORAGE)
+    maps = Composite.apply(
         geometry,
         screen_means,
         parameters,
@@ -585,7 +626,13 @@ def render(
         bounded,
         torch.is_grad_enabled(),
         violations,
+        single,
     )
+    if single:  # views of one [..., C, H, W, 9] tensor (rendering.py:388-400)
+        rgb, alpha, depth, normals, distortion = (
+            maps[..., 0:3], maps[..., 3:4], maps[..., 4:5], maps[..., 5:8], maps[..., 8:9])
+    else:
+        rgb, alpha, depth, normals, distortion = maps
     meta = {
         "radii": row_radii if packed else dense_radii.reshape(batch + (cameras, n)),
         "projected_means": projected_means,

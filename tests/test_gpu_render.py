@@ -447,3 +447,45 @@ def test_fixed_cameras_skip_camera_gradients(method):
         want = full[name].grad
         scale = max(float(want.abs().max()), 1.0)
         torch.testing.assert_close(value.grad, want, atol=1e-6 * scale, rtol=1e-5, msg=name)
+
+
+@pytest.mark.parametrize("method", ["classic", "neural"])
+def test_single_map_storage_is_the_reference_layout(method):
+    """Inside single_map_storage() rgb, alpha and the three meta maps are
+    views of one [..., C, H, W, 9] tensor, as in the reference
+    (rendering.py:375-400): the same values as the grouped layout, bit for
+    bit, the same gradients (atomic order aside), the reference's strides
+    and shared base, and an in-place change of a view reaches the base."""
+    from diff_gabor_splatting_amd import single_map_storage
+
+    width, height = 45, 37
+    print(f"single map storage: {method}", flush=True)
+    raw = random_scene(method, scenes=2, cameras=2, n=150, width=width, height=height, seed=17)
+    values = on_gpu(raw)
+    grouped = renderer(method)(**values, width=width, height=height)
+    with single_map_storage():
+        rgb, alpha, meta = renderer(method)(**values, width=width, height=height)
+    base = rgb._base
+    assert base is not None and tuple(base.shape) == tuple(rgb.shape[:-1]) + (9,)
+    for view in (alpha, meta["accumulated_depth"], meta["normals"], meta["distortion"]):
+        assert view._base is base
+    assert rgb.stride()[-2:] == (9, 1) and alpha.storage_offset() - rgb.storage_offset() == 3
+    single_maps = maps_from_result((rgb, alpha, meta))
+    grouped_maps = maps_from_result(grouped)
+    assert torch.equal(single_maps, grouped_maps)
+    assert torch.equal(base, grouped_maps)
+    weights = torch.randn(single_maps.shape, generator=torch.Generator().manual_seed(6))
+    weights = weights.to(DEVICE)
+    for name, a, b in zip(values, grads(single_maps, weights, values),
+                          grads(grouped_maps, weights, values)):
+        assert torch.isfinite(a).all(), name
+        assert_gradients_close(a, b, name)
+    # The reference objective over the views, through an in-place change.
+    with single_map_storage():
+        rgb, alpha, meta = renderer(method)(**values, width=width, height=height)
+    rgb.mul_(2.0)
+    assert torch.equal(rgb._base[..., :3], 2 * grouped[0].detach())
+    loss = torch.cat((rgb, alpha, meta["accumulated_depth"], meta["normals"],
+                      meta["distortion"]), -1).square().mean()
+    loss.backward()
+    assert all(torch.isfinite(v.grad).all() for v in values.values())
