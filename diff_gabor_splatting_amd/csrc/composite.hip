@@ -184,7 +184,7 @@ struct NeuralRow {
   static constexpr int DIR = 55;                 // 3 (backward)
   static constexpr int WDIR = 58;                // W1[h][2..4], 18 (backward)
   static constexpr int STRIDE = 76;
-  static constexpr int FORWARD_STRIDE = 56;  // the forward's rows: up to DIR, 16-byte aligned
+  static constexpr int FORWARD_STRIDE = 60;  // the forward's rows: up to DIR, 16-byte aligned, rows 4 banks apart
 };
 // The neural forward's raw staging row: direction, then the appearance
 // row's input weights and biases (appearance columns 0..35 at 3..38).

@@ -19,9 +19,9 @@ Runs one forward + backward of a workload through ``libgabor_hip_diag.so``
 
 Workloads: ``config0`` .. ``config4`` (the benchmark configs, ``workloads.py``)
 and ``harness-classic`` / ``harness-neural`` (the benchmark harness's default
-scene, all images in one dense call). The per-(record, wave) counting adds a
-few instructions to every processed pair, so times here are slightly above
-the product library's; use ``bench.py`` for timing.
+scene, all images in one dense call). The per-(record, wave) counting adds
+instructions to every processed pair, so times here run above the product
+library's (by up to about 15% in the backward); use ``bench.py`` for timing.
 """
 
 from __future__ import annotations
