@@ -159,6 +159,17 @@ _SIGNATURES = {
         [_c_ptr] * 3 + [_c_i64, _c_i64, _c_ptr, _c_i64, _c_int, _c_int] + [_c_ptr] * 4
         + [_c_size, _c_ptr],
     ),
+    "gs_bin_blocks_fit": (_c_int, [_c_i64, _c_int, _c_int]),
+    "gs_bin_blocks_count": (
+        _c_int,
+        [_c_ptr] * 3 + [_c_i64, _c_int, _c_int] + [_c_ptr] * 3 + [_c_size, _c_ptr],
+    ),
+    "gs_bin_blocks_tiles_workspace_size": (_c_size, [_c_i64, _c_i64, _c_int, _c_int]),
+    "gs_bin_blocks_tiles": (
+        _c_int,
+        [_c_ptr] * 3 + [_c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_int, _c_int] + [_c_ptr] * 4
+        + [_c_size, _c_ptr],
+    ),
     "gs_render_workspace_size": (_c_size, [_c_i64, _c_int, _c_int]),
     "gs_render_backward_workspace_size": (_c_size, [_c_i64, _c_int, _c_int, _c_i64]),
     "gs_render_forward": (
@@ -455,6 +466,34 @@ def bin_tiles(order, starts, rects, images, width, height, intersections, visibl
     check (see gs_bin_tiles)."""
     return _host.bin_tiles(order, starts, rects, images, width, height, intersections, visible,
                            status)
+
+
+def bin_blocks_order(geometry, radii, image_ids, width, height):
+    """Stage 1 of the block path: (order int32 [Q], starts int64 [Q], rects
+    int32 [Q, 4], totals int64 [3] on the device = (M, V, E)). starts[j] is
+    the first (pair, tile block) entry of depth rank j, rects hold each
+    pair's tile rectangle with the images' tile rows stacked, and E is the
+    number of (pair, block) entries (see gs_bin_blocks_count)."""
+    return _host.bin_blocks_order(geometry, radii, image_ids, width, height)
+
+
+def bin_blocks_tiles(order, starts, rects, images, width, height, intersections, entries,
+                     visible=-1, status=None):
+    """Stage 2 of the block path: (point_list, ranges), bit for bit those of
+    bin_tiles, from bin_blocks_order's outputs and totals (M, V, E)."""
+    return _host.bin_blocks_tiles(order, starts, rects, images, width, height, intersections,
+                                  entries, visible, status)
+
+
+def set_binning_path(name: str) -> None:
+    """Stage 2 of the synchronised binning: "blocks" (the default: the block
+    path wherever gs_bin_blocks_fit) or "tiles" (always the tile sort). Both
+    give the same point list and ranges; process-wide."""
+    _host.set_binning_path(name)
+
+
+def binning_path() -> str:
+    return _host.binning_path()
 
 
 def bin_tiles_bounded(order, starts, rects, images, width, height, capacity, intersections):

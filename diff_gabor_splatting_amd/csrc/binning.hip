@@ -146,14 +146,34 @@ __global__ __launch_bounds__(256) void find_ranges_kernel(int64_t m, int64_t til
   if (i == m - 1 && own) ranges[tile].y = int(m);
 }
 
-// Depth-first binning, stage 1, step 1: each pair's tile rectangle
-// (x0, y0, width, first tile id of its image) for stage 2, its tile count
-// (the rectangle area of countTiles) and its depth key; pairs without
-// tiles sort last. Each workgroup also stores its sums of the counts and of
-// the pairs with tiles in partials[block], which totals_kernel adds up into
-// M and V, so the host can read them before the pairs are sorted (plain
-// stores and one more launch: thousands of workgroups adding into one
-// device word would queue their atomics behind each other).
+// Tile blocks: kBlockSide x kBlockSide tiles of one image, numbered row-major
+// per image and image after image. The block path bins the pairs into
+// blocks first and then each block's pairs into its tiles.
+constexpr int kBlockShift = 2;
+constexpr int kBlockSide = 1 << kBlockShift;
+__host__ __device__ inline int blocks_across(int tiles) { return (tiles + kBlockSide - 1) >> kBlockShift; }
+
+// Blocks met by the tile rectangle [x0, x1) x [y0, y1) (non-empty, in one
+// image's tile coordinates).
+__device__ __forceinline__ int block_area(int x0, int y0, int x1, int y1) {
+  return (((x1 - 1) >> kBlockShift) - (x0 >> kBlockShift) + 1) *
+         (((y1 - 1) >> kBlockShift) - (y0 >> kBlockShift) + 1);
+}
+
+// Depth-first binning, stage 1, step 1: each pair's tile rectangle, its
+// entry count and its depth key; pairs without tiles sort last.
+//  * tile path (Blocks = false): rects[i] = (x0, y0, width, first tile id of
+//    its image) and counts[i] = the rectangle's area (countTiles);
+//  * block path (Blocks = true): rects[i] = (x0, y0 + image*th, x1, y1 +
+//    image*th), the rectangle in the images' tile rows stacked top to
+//    bottom, and counts[i] = the number of tile blocks it meets.
+// Each workgroup also stores its sums of the tile counts, of the pairs with
+// tiles and of the block counts in partials[block], which totals_kernel adds
+// up into M, V and the block entries, so the host can read them before the
+// pairs are sorted (plain stores and one more launch: thousands of
+// workgroups adding into one device word would queue their atomics behind
+// each other).
+template <bool Blocks>
 __global__ __launch_bounds__(256) void pair_keys_kernel(int64_t count, int tw, int th,
                                                         const float* __restrict__ geometry,
                                                         const int* __restrict__ radii,
@@ -163,89 +183,103 @@ __global__ __launch_bounds__(256) void pair_keys_kernel(int64_t count, int tw, i
                                                         int* __restrict__ counts,
                                                         int4* __restrict__ rects,
                                                         long long* __restrict__ partials) {
-  __shared__ long long wave_sums[2][4];
+  __shared__ long long wave_sums[3][4];
   const int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x;
-  int c = 0;
+  int c = 0, b = 0;
   if (i < count) {
     const int r = radii[i];
     uint32_t key = 0xffffffffu;
-    int4 rect = make_int4(0, 0, 1, 0);
+    int4 rect = Blocks ? make_int4(0, 0, 0, 0) : make_int4(0, 0, 1, 0);
     if (r > 0) {
       const float* g = geometry + i * kGeometry;
       const TileRect t = tile_rect(g[9], g[10], r, tw, th);
       c = (t.x1 - t.x0) * (t.y1 - t.y0);
       if (c > 0) {
         key = __float_as_uint(g[8]);
-        rect = make_int4(t.x0, t.y0, t.x1 - t.x0, int(image_ids[i] * int64_t(tw) * th));
+        if constexpr (Blocks) {
+          b = block_area(t.x0, t.y0, t.x1, t.y1);
+          const int rows = int(image_ids[i]) * th;
+          rect = make_int4(t.x0, t.y0 + rows, t.x1, t.y1 + rows);
+        } else {
+          rect = make_int4(t.x0, t.y0, t.x1 - t.x0, int(image_ids[i] * int64_t(tw) * th));
+        }
       }
     }
-    counts[i] = c;
+    counts[i] = Blocks ? b : c;
     keys[i] = key;
     values[i] = int(i);
     rects[i] = rect;
   }
   // Workgroup totals: wave sums by shuffles, then across the four waves.
-  long long sum = c, with_tiles = c > 0 ? 1 : 0;
+  long long sum = c, with_tiles = c > 0 ? 1 : 0, block_sum = b;
 #pragma unroll
   for (int offset = 32; offset > 0; offset >>= 1) {
     sum += __shfl_xor(sum, offset, 64);
     with_tiles += __shfl_xor(with_tiles, offset, 64);
+    block_sum += __shfl_xor(block_sum, offset, 64);
   }
   const int wave = threadIdx.x >> 6;
   if (__lane_id() == 0) {
     wave_sums[0][wave] = sum;
     wave_sums[1][wave] = with_tiles;
+    wave_sums[2][wave] = block_sum;
   }
   __syncthreads();
-  if (threadIdx.x < 2)
-    partials[2 * int64_t(blockIdx.x) + threadIdx.x] =
+  if (threadIdx.x < 3)
+    partials[3 * int64_t(blockIdx.x) + threadIdx.x] =
         wave_sums[threadIdx.x][0] + wave_sums[threadIdx.x][1] + wave_sums[threadIdx.x][2] +
         wave_sums[threadIdx.x][3];
 }
 
-// M and V from pair_keys_kernel's `blocks` workgroup totals (one
-// workgroup; `visible` may be null).
+// M, V and the block entries from pair_keys_kernel's `blocks` workgroup
+// totals (one workgroup; `visible` and `block_total` may be null).
 constexpr int kTotalsBlock = 1024;
 __global__ __launch_bounds__(kTotalsBlock) void totals_kernel(const long long* __restrict__ partials,
                                                              int64_t blocks, int64_t* total,
-                                                             int64_t* visible) {
-  __shared__ long long wave_sums[2][kTotalsBlock / 64];
-  long long sum = 0, with_tiles = 0;
+                                                             int64_t* visible,
+                                                             int64_t* block_total) {
+  __shared__ long long wave_sums[3][kTotalsBlock / 64];
+  long long sums[3] = {0, 0, 0};
   for (int64_t b = threadIdx.x; b < blocks; b += kTotalsBlock) {
-    sum += partials[2 * b];
-    with_tiles += partials[2 * b + 1];
+#pragma unroll
+    for (int k = 0; k < 3; ++k) sums[k] += partials[3 * b + k];
   }
 #pragma unroll
-  for (int offset = 32; offset > 0; offset >>= 1) {
-    sum += __shfl_xor(sum, offset, 64);
-    with_tiles += __shfl_xor(with_tiles, offset, 64);
-  }
-  if (__lane_id() == 0) {
-    wave_sums[0][threadIdx.x >> 6] = sum;
-    wave_sums[1][threadIdx.x >> 6] = with_tiles;
+  for (int k = 0; k < 3; ++k) {
+#pragma unroll
+    for (int offset = 32; offset > 0; offset >>= 1) sums[k] += __shfl_xor(sums[k], offset, 64);
+    if (__lane_id() == 0) wave_sums[k][threadIdx.x >> 6] = sums[k];
   }
   __syncthreads();
-  if (threadIdx.x < 2) {
+  if (threadIdx.x < 3) {
     long long value = 0;
 #pragma unroll
     for (int w = 0; w < kTotalsBlock / 64; ++w) value += wave_sums[threadIdx.x][w];
-    int64_t* target = threadIdx.x == 0 ? total : visible;
+    int64_t* target = threadIdx.x == 0 ? total : threadIdx.x == 1 ? visible : block_total;
     if (target) *target = value;
   }
 }
 
-// No pairs: M = V = 0.
-__global__ __launch_bounds__(64) void zero_totals_kernel(int64_t* total, int64_t* visible) {
+// No pairs: M = V = 0 (and no block entries).
+__global__ __launch_bounds__(64) void zero_totals_kernel(int64_t* total, int64_t* visible,
+                                                         int64_t* block_total) {
   if (threadIdx.x == 0 && blockIdx.x == 0) {
     *total = 0;
     if (visible) *visible = 0;
+    if (block_total) *block_total = 0;
   }
 }
 
+// counts[order[j]]; an order entry outside [0, count) counts 0 here (the
+// emission flags it).
 struct SortedCountLoad {
   const int* counts;
   const int* order;
-  __device__ int64_t operator()(int64_t j) const { return counts[order[j]]; }
+  int64_t count;
+  __device__ int64_t operator()(int64_t j) const {
+    const int pair = order[j];
+    return pair >= 0 && pair < count ? counts[pair] : 0;
+  }
 };
 
 // starts[j] = entries of all lower depth ranks (pair_keys_kernel has
@@ -401,6 +435,327 @@ __global__ __launch_bounds__(256) void find_tile_ranges_kernel(int64_t capacity,
   if (i == m - 1 && own) ranges[tile].y = int(m);
 }
 
+// --------------------------------------------------------------------------
+// Block path, stage 2. Stage 1 (pair_keys_kernel<true>, the depth sort and
+// the scan of block counts) leaves the pairs in depth order with the first
+// block entry of each. Then:
+//  1. emit_blocks_kernel writes, rank after rank, one entry per tile block a
+//     pair's rectangle meets: key = block id << 16 | the 16-bit mask of the
+//     block's tiles the rectangle covers (bit 4 ly + lx), value = pair;
+//  2. a stable sort on the block-id bits groups the entries by block, each
+//     block's entries staying in depth order;
+//  3. block_bounds_kernel finds where each block's entries start;
+//  4. block_tile_count_kernel counts each tile's entries per chunk of its
+//     block's list (one wave per chunk, each for all 16 tiles of the block),
+//     and a scan of the tile totals gives the tile ranges;
+//  5. block_tile_write_kernel: the same waves walk their chunks again and
+//     write the pairs whose mask covers each tile, in list order, from the
+//     tile's range start plus its entries in the earlier chunks.
+// Every tile's list is then its pairs in (depth bits, pair index) order, as
+// with the tile sort, while the sort moves about M / 6 entries instead of M
+// (a pair meets ~18 tiles but ~3 blocks on a 1080p scene of 1M surfels).
+
+// Mask of the tiles of block (bx, by) that [x0, x1) x [y0, y1) covers.
+__device__ __forceinline__ uint32_t block_mask(int bx, int by, int x0, int y0, int x1, int y1) {
+  const int lx0 = max(x0 - (bx << kBlockShift), 0), lx1 = min(x1 - (bx << kBlockShift), kBlockSide);
+  const int ly0 = max(y0 - (by << kBlockShift), 0), ly1 = min(y1 - (by << kBlockShift), kBlockSide);
+  const uint32_t columns = ((1u << lx1) - 1u) & ~((1u << lx0) - 1u);
+  const uint32_t rows = ((1u << (kBlockSide * ly1)) - 1u) & ~((1u << (kBlockSide * ly0)) - 1u);
+  return (columns * 0x1111u) & rows;
+}
+
+// One lane per depth rank below `ranks` (the pairs with tiles) reads its
+// pair and rectangle; the wave then writes its 64 ranks' entries, which are
+// consecutive in the output, together, 64 consecutive entries per store:
+// lane i of a round takes entry wave_first + 64 r + i, finds the rank that
+// owns it (a binary search over the lanes' first entries by shuffles) and
+// that rank's rectangle (shuffles). Entries at or past `capacity` are
+// dropped. A depth-sort output outside [0, count) is replaced by pair 0 and
+// sets kBinBadIndex; its scanned block count was 0, so it writes nothing.
+constexpr int kMaskBits = 16;
+
+__global__ __launch_bounds__(256) void emit_blocks_kernel(
+    int64_t ranks, int64_t count, int64_t capacity, int64_t total, uint32_t* status, int th,
+    int bw, int bh, const int* __restrict__ order, const int64_t* __restrict__ starts,
+    const int4* __restrict__ rects, uint32_t* __restrict__ keys, int* __restrict__ values) {
+  const int lane = __lane_id();
+  const int64_t j = int64_t(blockIdx.x) * 256 + threadIdx.x;
+  const int64_t wave_rank = j - lane;
+  if (wave_rank >= ranks) return;  // uniform per wave
+  const int last = int(min<int64_t>(63, ranks - 1 - wave_rank));  // last lane with a rank
+  int pair = 0, area = 0, bx0 = 0, by0 = 0, span = 1, x0 = 0, y0 = 0, x1 = 0, y1 = 0;
+  uint32_t base = 0;
+  int64_t first = 0;
+  if (lane <= last) {
+    bool bad = false;
+    pair = checked_index(order[j], count, bad);
+    if (bad && status) atomicOr(status, kBinBadIndex);
+    first = starts[j];
+    const int64_t next = j + 1 < count ? starts[j + 1] : total;
+    area = int(max<int64_t>(min<int64_t>(next - first, INT_MAX), 0));
+    if (area > 0) {
+      const int4 r = rects[pair];
+      const int image = r.y / th;
+      x0 = r.x;
+      x1 = r.z;
+      y0 = r.y - image * th;
+      y1 = r.w - image * th;
+      bx0 = x0 >> kBlockShift;
+      by0 = y0 >> kBlockShift;
+      span = ((x1 - 1) >> kBlockShift) - bx0 + 1;
+      base = uint32_t(image) * uint32_t(bw) * uint32_t(bh);
+    }
+  }
+  const int64_t wave_first = __shfl(first, 0);
+  const int64_t wave_end = __shfl(first + area, last);
+  // Offsets from the wave's first entry (the wave's entries number below
+  // 2^31: they are part of at most `capacity` <= INT_MAX).
+  const int offset = int(first - wave_first);
+  for (int64_t e = wave_first + lane; e - lane < wave_end; e += 64) {
+    const int want = int(e - wave_first);
+    int owner = 0;  // last lane whose first entry is at or before e
+#pragma unroll
+    for (int step = 32; step > 0; step >>= 1) {
+      const int probe = owner + step;
+      const int at = __shfl(offset, probe <= last ? probe : last);
+      if (probe <= last && at <= want) owner = probe;
+    }
+    const int k = want - __shfl(offset, owner);
+    const int o_bx0 = __shfl(bx0, owner), o_by0 = __shfl(by0, owner);
+    const int o_span = __shfl(span, owner);
+    const int ox0 = __shfl(x0, owner), oy0 = __shfl(y0, owner);
+    const int ox1 = __shfl(x1, owner), oy1 = __shfl(y1, owner);
+    const uint32_t o_base = uint32_t(__shfl(int(base), owner));
+    const int o_pair = __shfl(pair, owner);
+    if (e < wave_end && e >= 0 && e < capacity) {
+      const int bx = o_bx0 + k % o_span, by = o_by0 + k / o_span;
+      keys[e] = ((o_base + uint32_t(by * bw + bx)) << kMaskBits) |
+                block_mask(bx, by, ox0, oy0, ox1, oy1);
+      values[e] = o_pair;
+    }
+  }
+}
+
+// first[b] = index of block b's first entry in the block-sorted keys, for
+// b in [0, blocks]; empty blocks start where the next entry is (first[blocks]
+// = m). Each entry whose block differs from its predecessor's writes the
+// starts of the blocks from just after the predecessor's to its own.
+// The same launch clears tile_counts (`tiles` entries) for
+// block_tile_count_kernel's atomic sums.
+__global__ __launch_bounds__(256) void block_bounds_kernel(int64_t m, int64_t blocks,
+                                                           const uint32_t* __restrict__ keys,
+                                                           int* __restrict__ first,
+                                                           int64_t tiles,
+                                                           int* __restrict__ tile_counts) {
+  const int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x;
+  if (i < tiles) tile_counts[i] = 0;
+  if (i >= m) return;
+  const int64_t block = min<int64_t>(keys[i] >> kMaskBits, blocks);
+  const int64_t previous = i == 0 ? -1 : min<int64_t>(keys[i - 1] >> kMaskBits, blocks);
+  for (int64_t b = previous + 1; b <= block; ++b) first[b] = int(i);
+  if (i == m - 1)
+    for (int64_t b = block + 1; b <= blocks; ++b) first[b] = int(m);
+}
+
+// The tiles of block b: local tile k = 4 ly + lx (its bit in an entry's
+// mask) is tile (4 bx + lx, 4 by + ly) of the block's image.
+constexpr int kBlockTiles = kBlockSide * kBlockSide;
+
+struct BlockTiles {
+  int image, tx, ty;  // image, first tile of the block
+  __device__ BlockTiles(int64_t block, int bw, int bh) {
+    const int64_t per_image = int64_t(bw) * bh;
+    image = int(block / per_image);
+    const int rest = int(block - image * per_image);
+    tx = (rest % bw) << kBlockShift;
+    ty = (rest / bw) << kBlockShift;
+  }
+  __device__ bool inside(int k, int tw, int th) const {
+    return tx + (k & (kBlockSide - 1)) < tw && ty + (k >> kBlockShift) < th;
+  }
+  __device__ int64_t tile(int k, int tw, int th) const {
+    return (int64_t(image) * th + ty + (k >> kBlockShift)) * tw + tx + (k & (kBlockSide - 1));
+  }
+};
+
+// The block's entry list is cut into up to kChunks contiguous chunks of
+// about equal length but at least kChunkMin entries; workgroup g of a block
+// has kChunkWaves waves, and wave w takes chunk kChunkWaves g + w (empty
+// when the list has fewer chunks) for all 16 tiles of the block, 64 entries
+// per step and up to kWaveSteps steps per round, all of a round's loads
+// issued before any is used. No wave waits for another.
+constexpr int kChunks = 16;
+constexpr int kChunkMin = 256;
+constexpr int kChunkWaves = 4;
+constexpr int kChunkGroups = kChunks / kChunkWaves;
+constexpr int kWaveSteps = 16;
+
+struct BlockChunk {
+  int64_t block;
+  int chunk, begin, end;  // chunk of the block list, its entries [begin, end)
+  __device__ BlockChunk(const int* first) {
+    block = blockIdx.x / kChunkGroups;
+    chunk = int(blockIdx.x % kChunkGroups) * kChunkWaves + (int(threadIdx.x) >> 6);
+    const int list_begin = first[block], list_end = first[block + 1];
+    const int64_t length = list_end - list_begin;
+    const int64_t chunks = min<int64_t>(kChunks, max<int64_t>(1, (length + kChunkMin - 1) / kChunkMin));
+    begin = chunk < chunks ? list_begin + int(length * chunk / chunks) : list_end;
+    end = chunk < chunks ? list_begin + int(length * (chunk + 1) / chunks) : list_end;
+  }
+};
+
+// chunk_counts[(b kChunks + c) 16 + k] = entries of chunk c of block b whose
+// mask has local tile k's bit; tile_counts[t] (cleared by
+// block_bounds_kernel) += the same, summed over the chunks by atomics.
+__global__ __launch_bounds__(kChunkWaves * 64) void block_tile_count_kernel(
+    int bw, int bh, int tw, int th, const int* __restrict__ first,
+    const uint32_t* __restrict__ keys, int* __restrict__ chunk_counts,
+    int* __restrict__ tile_counts) {
+  const BlockChunk part(first);
+  const int lane = __lane_id();
+  int c[kBlockTiles] = {};
+  for (int base = part.begin; base < part.end; base += 64 * kWaveSteps) {
+    uint32_t key[kWaveSteps];
+#pragma unroll
+    for (int u = 0; u < kWaveSteps; ++u) {
+      const int i = base + u * 64 + lane;
+      key[u] = i < part.end ? keys[i] : 0u;
+    }
+    const int steps = (part.end - base + 63) >> 6;  // uniform
+#pragma unroll
+    for (int u = 0; u < kWaveSteps; ++u) {
+      if (u >= steps) break;
+#pragma unroll
+      for (int k = 0; k < kBlockTiles; ++k) c[k] += int((key[u] >> k) & 1u);
+    }
+  }
+  int mine = 0;  // lane k < 16: local tile k's count
+#pragma unroll
+  for (int k = 0; k < kBlockTiles; ++k) {
+    int v = c[k];
+#pragma unroll
+    for (int offset = 32; offset > 0; offset >>= 1) v += __shfl_xor(v, offset, 64);
+    mine = lane == k ? v : mine;
+  }
+  if (lane < kBlockTiles) {
+    chunk_counts[(part.block * kChunks + part.chunk) * kBlockTiles + lane] = mine;
+    const BlockTiles tiles(part.block, bw, bh);
+    if (mine > 0 && tiles.inside(lane, tw, th))
+      atomicAdd(&tile_counts[tiles.tile(lane, tw, th)], mine);
+  }
+}
+
+struct TileCountLoad2 {
+  const int* counts;
+  __device__ int64_t operator()(int64_t t) const { return counts[t]; }
+};
+
+// ranges[t] = [first, last) of tile t's entries, (0, 0) for an empty tile;
+// clamped to the point list's m entries (consistent inputs never reach it),
+// so that no range leaves the list and every slot a range covers is written.
+struct TileRangeStore {
+  int2* ranges;
+  int64_t m;
+  __device__ void operator()(int64_t t, int64_t inclusive, int64_t v) const {
+    const int64_t first = min(inclusive - v, m), last = min(inclusive, m);
+    ranges[t] = last > first ? make_int2(int(first), int(last)) : make_int2(0, 0);
+  }
+};
+
+// Tile ranges of up to kRangeItems * 1024 tiles in one workgroup and one
+// pass: thread t takes tiles [kRangeItems t, kRangeItems (t + 1)), adds its
+// counts, and a workgroup scan of those sums gives each thread its first
+// entry; ranges as TileRangeStore writes them.
+constexpr int kRangeThreads = 1024;
+constexpr int kRangeItems = 8;
+constexpr int64_t kRangeLocalTiles = int64_t(kRangeThreads) * kRangeItems;
+
+__global__ __launch_bounds__(kRangeThreads) void tile_ranges_local_kernel(
+    int64_t tiles, int64_t m, const int* __restrict__ counts, int2* __restrict__ ranges) {
+  __shared__ int64_t wave_totals[kRangeThreads / 64];
+  const int lane = __lane_id(), wave = threadIdx.x >> 6;
+  const int64_t t0 = int64_t(threadIdx.x) * kRangeItems;
+  int c[kRangeItems];
+  int64_t sum = 0;
+#pragma unroll
+  for (int u = 0; u < kRangeItems; ++u) {
+    c[u] = t0 + u < tiles ? counts[t0 + u] : 0;
+    sum += c[u];
+  }
+  const int64_t inclusive = wave_inclusive_scan(sum);
+  if (lane == 63) wave_totals[wave] = inclusive;
+  __syncthreads();
+  int64_t at = inclusive - sum;
+  for (int w = 0; w < wave; ++w) at += wave_totals[w];
+  const TileRangeStore store{ranges, m};
+#pragma unroll
+  for (int u = 0; u < kRangeItems; ++u) {
+    at += c[u];
+    if (t0 + u < tiles) store(t0 + u, at, c[u]);
+  }
+}
+
+// Each wave writes its chunk's part of the block's 16 tile lists: the pairs
+// of the entries whose mask has a tile's bit, in block-list order, from the
+// tile's range start plus the tile's entries in the block's earlier chunks
+// (ballot + lane prefix per step and tile). Positions at or past m are
+// dropped and set kBinOverflow; a pair outside [0, count) is replaced by
+// pair 0 and sets kBinBadIndex.
+__global__ __launch_bounds__(kChunkWaves * 64) void block_tile_write_kernel(
+    int bw, int bh, int tw, int th, const int* __restrict__ first,
+    const uint32_t* __restrict__ keys, const int* __restrict__ values,
+    const int2* __restrict__ ranges, const int* __restrict__ chunk_counts,
+    int* __restrict__ point_list, int m, int count, uint32_t* status) {
+  const BlockChunk part(first);
+  if (part.begin >= part.end) return;  // uniform per wave; no barrier here
+  const BlockTiles tiles(part.block, bw, bh);
+  const int lane = __lane_id();
+  // Lane k < 16: local tile k's first slot for this chunk. Unsigned: a slot
+  // that wraps on inconsistent inputs is >= m and dropped.
+  uint32_t start = 0;
+  const bool inside = lane < kBlockTiles && tiles.inside(lane, tw, th);
+  if (inside) {
+    start = uint32_t(ranges[tiles.tile(lane, tw, th)].x);
+    const int* column = chunk_counts + part.block * kChunks * kBlockTiles + lane;
+    for (int c = 0; c < part.chunk; ++c) start += uint32_t(column[c * kBlockTiles]);
+  }
+  const uint32_t inside_bits = uint32_t(__ballot(inside));
+  uint32_t next[kBlockTiles];
+#pragma unroll
+  for (int k = 0; k < kBlockTiles; ++k) next[k] = uint32_t(__shfl(int(start), k));
+  bool bad = false, overflow = false;
+  for (int base = part.begin; base < part.end; base += 64 * kWaveSteps) {
+    uint32_t key[kWaveSteps];
+    int pair[kWaveSteps];
+#pragma unroll
+    for (int u = 0; u < kWaveSteps; ++u) {
+      const int i = base + u * 64 + lane;
+      key[u] = i < part.end ? keys[i] : 0u;
+      pair[u] = checked_index(i < part.end ? values[i] : 0, count, bad);
+    }
+    const int steps = (part.end - base + 63) >> 6;  // uniform
+#pragma unroll
+    for (int u = 0; u < kWaveSteps; ++u) {
+      if (u >= steps) break;
+      const uint32_t mask = key[u] & inside_bits;
+#pragma unroll
+      for (int k = 0; k < kBlockTiles; ++k) {
+        const bool take = (mask >> k) & 1u;
+        const uint64_t vote = __ballot(take);
+        const uint32_t slot = __builtin_amdgcn_mbcnt_hi(
+            uint32_t(vote >> 32), __builtin_amdgcn_mbcnt_lo(uint32_t(vote), next[k]));
+        if (take) {
+          if (slot < uint32_t(m)) point_list[slot] = pair[u];
+          else overflow = true;
+        }
+        next[k] += uint32_t(__popcll(vote));
+      }
+    }
+  }
+  if (status && (bad || overflow))
+    atomicOr(status, (bad ? kBinBadIndex : 0u) | (overflow ? kBinOverflow : 0u));
+}
+
 struct OrderWorkspace {
   uint32_t* keys;      // count
   uint32_t* sorted;    // count
@@ -408,7 +763,7 @@ struct OrderWorkspace {
   int* counts;         // count
   int64_t* scan_sums;
   void* sort;          // radix sort scratch for count keys
-  long long* partials;  // [ceil(count / 256)][2]: pair_keys_kernel's workgroup totals
+  long long* partials;  // [ceil(count / 256)][3]: pair_keys_kernel's workgroup totals
   size_t bytes;
 };
 
@@ -427,7 +782,7 @@ OrderWorkspace order_layout(void* base, int64_t count) {
   w.counts = reinterpret_cast<int*>(take(size_t(count) * 4));
   w.scan_sums = reinterpret_cast<int64_t*>(take(scan_workspace_bytes(count, 8)));
   w.sort = take(radix_sort_workspace_bytes(count, 4));
-  w.partials = reinterpret_cast<long long*>(take(size_t(ceil_div(count, 256)) * 16));
+  w.partials = reinterpret_cast<long long*>(take(size_t(ceil_div(count, 256)) * 24));
   w.bytes = offset;
   return w;
 }
@@ -457,11 +812,84 @@ TilesWorkspace tiles_layout(void* base, int64_t m) {
   return w;
 }
 
+struct BlocksWorkspace {
+  uint32_t* keys;         // block entries, depth order
+  int* values;
+  uint32_t* sorted_keys;  // block order
+  int* sorted_values;
+  void* sort;             // radix sort scratch
+  int* first;             // blocks + 1
+  int* chunk_counts;      // blocks * kChunks * 16
+  int* tile_counts;       // tiles
+  int64_t* scan_sums;     // tile-count scan
+  size_t bytes;
+};
+
+BlocksWorkspace blocks_layout(void* base, int64_t entries, int64_t blocks, int64_t tiles) {
+  BlocksWorkspace w;
+  char* p = static_cast<char*>(base);
+  size_t offset = 0;
+  auto take = [&](size_t bytes) {
+    char* at = p + offset;
+    offset = align_up(offset + bytes, 256);
+    return at;
+  };
+  w.keys = reinterpret_cast<uint32_t*>(take(size_t(entries) * 4));
+  w.values = reinterpret_cast<int*>(take(size_t(entries) * 4));
+  w.sorted_keys = reinterpret_cast<uint32_t*>(take(size_t(entries) * 4));
+  w.sorted_values = reinterpret_cast<int*>(take(size_t(entries) * 4));
+  w.sort = take(radix_sort_workspace_bytes(entries, 4));
+  w.first = reinterpret_cast<int*>(take(size_t(blocks + 1) * 4));
+  w.chunk_counts = reinterpret_cast<int*>(take(size_t(blocks) * kChunks * kBlockTiles * 4));
+  w.tile_counts = reinterpret_cast<int*>(take(size_t(tiles) * 4));
+  w.scan_sums = reinterpret_cast<int64_t*>(take(scan_workspace_bytes(tiles, 8)));
+  w.bytes = offset;
+  return w;
+}
+
+// Tile blocks of `images` images of tw x th tiles.
+int64_t block_count(int64_t images, int tw, int th) {
+  return images * int64_t(blocks_across(tw)) * int64_t(blocks_across(th));
+}
+
 // Bits needed for ids below `tiles`.
 int id_bits(int64_t tiles) {
   int bits = 0;
   while (bits < 63 && (int64_t(1) << bits) < tiles) ++bits;
   return bits;
+}
+
+// Stage 1's first step for both paths (pair_keys_kernel<Blocks>, then the
+// totals; every total pointer but `intersections` may be null).
+template <bool Blocks>
+int order_count(const float* geometry, const int32_t* radii, const int64_t* image_ids,
+                int64_t count, int32_t width, int32_t height, int32_t* rects,
+                int64_t* intersections, int64_t* visible, int64_t* block_total, void* workspace,
+                size_t workspace_bytes, hipStream_t s) {
+  GS_REQUIRE(count >= 0 && count <= INT_MAX, GS_ERR_OVERFLOW, "too many projected primitives");
+  GS_REQUIRE(width > 0 && height > 0, GS_ERR_ARGUMENT, "invalid image dimensions");
+  GS_REQUIRE(intersections, GS_ERR_ARGUMENT, "null intersections");
+  ProfileScope prof(GS_PROF_BINNING, s);
+  if (count == 0) {
+    zero_totals_kernel<<<1, 64, 0, s>>>(intersections, visible, block_total);
+    GS_LAUNCHED("zero_totals_kernel");
+    return GS_OK;
+  }
+  GS_REQUIRE(geometry && radii && image_ids && rects, GS_ERR_ARGUMENT,
+             "null pointer passed to gs_bin_order_count");
+  const size_t need = order_layout(nullptr, count).bytes + 256;
+  GS_REQUIRE(workspace && workspace_bytes >= need, GS_ERR_WORKSPACE,
+             "binning needs %zu workspace bytes, got %zu", need, workspace_bytes);
+  OrderWorkspace w = order_layout(workspace, count);
+  const int64_t blocks = ceil_div(count, 256);
+  pair_keys_kernel<Blocks><<<unsigned(blocks), 256, 0, s>>>(
+      count, tiles_x(width), tiles_y(height), geometry, radii, image_ids, w.keys, w.pair_ids,
+      w.counts, reinterpret_cast<int4*>(rects), w.partials);
+  GS_LAUNCHED("pair_keys_kernel");
+  totals_kernel<<<1, kTotalsBlock, 0, s>>>(w.partials, blocks, intersections, visible,
+                                           block_total);
+  GS_LAUNCHED("totals_kernel");
+  return GS_OK;
 }
 
 }  // namespace
@@ -562,32 +990,30 @@ int gs_bin_order_count(const float* geometry, const int32_t* radii, const int64_
                        int64_t count, int32_t width, int32_t height, int32_t* rects,
                        int64_t* intersections, int64_t* visible, void* workspace,
                        size_t workspace_bytes, void* stream) {
+  gs::clear_error();
+  return gs::order_count<false>(geometry, radii, image_ids, count, width, height, rects,
+                                intersections, visible, nullptr, workspace, workspace_bytes,
+                                static_cast<hipStream_t>(stream));
+}
+
+int gs_bin_blocks_fit(int64_t images, int32_t width, int32_t height) {
+  if (images < 0 || width <= 0 || height <= 0) return 0;
+  return gs::block_count(images, gs::tiles_x(width), gs::tiles_y(height)) <=
+                 (int64_t(1) << (32 - gs::kMaskBits))
+             ? 1
+             : 0;
+}
+
+int gs_bin_blocks_count(const float* geometry, const int32_t* radii, const int64_t* image_ids,
+                        int64_t count, int32_t width, int32_t height, int32_t* rects,
+                        int64_t* totals, void* workspace, size_t workspace_bytes,
+                        void* stream) {
   using namespace gs;
   clear_error();
-  GS_REQUIRE(count >= 0 && count <= INT_MAX, GS_ERR_OVERFLOW, "too many projected primitives");
-  GS_REQUIRE(width > 0 && height > 0, GS_ERR_ARGUMENT, "invalid image dimensions");
-  GS_REQUIRE(intersections, GS_ERR_ARGUMENT, "null intersections");
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  ProfileScope prof(GS_PROF_BINNING, s);
-  if (count == 0) {
-    zero_totals_kernel<<<1, 64, 0, s>>>(intersections, visible);
-    GS_LAUNCHED("zero_totals_kernel");
-    return GS_OK;
-  }
-  GS_REQUIRE(geometry && radii && image_ids && rects, GS_ERR_ARGUMENT,
-             "null pointer passed to gs_bin_order_count");
-  const size_t need = gs_bin_order_workspace_size(count);
-  GS_REQUIRE(workspace && workspace_bytes >= need, GS_ERR_WORKSPACE,
-             "binning needs %zu workspace bytes, got %zu", need, workspace_bytes);
-  OrderWorkspace w = order_layout(workspace, count);
-  const int64_t blocks = ceil_div(count, 256);
-  pair_keys_kernel<<<unsigned(blocks), 256, 0, s>>>(
-      count, tiles_x(width), tiles_y(height), geometry, radii, image_ids, w.keys, w.pair_ids,
-      w.counts, reinterpret_cast<int4*>(rects), w.partials);
-  GS_LAUNCHED("pair_keys_kernel");
-  totals_kernel<<<1, kTotalsBlock, 0, s>>>(w.partials, blocks, intersections, visible);
-  GS_LAUNCHED("totals_kernel");
-  return GS_OK;
+  GS_REQUIRE(totals, GS_ERR_ARGUMENT, "null totals");
+  return order_count<true>(geometry, radii, image_ids, count, width, height, rects, totals,
+                           totals + 1, totals + 2, workspace, workspace_bytes,
+                           static_cast<hipStream_t>(stream));
 }
 
 int gs_bin_order_sort(int64_t count, int32_t* order, int64_t* starts, void* workspace,
@@ -609,7 +1035,7 @@ int gs_bin_order_sort(int64_t count, int32_t* order, int64_t* starts, void* work
     if (status != GS_OK) return status;
   }
   ProfileScope prof(GS_PROF_BINNING, s);
-  return run_scan<int64_t>(count, SortedCountLoad{w.counts, order}, ExclusiveStartStore{starts},
+  return run_scan<int64_t>(count, SortedCountLoad{w.counts, order, count}, ExclusiveStartStore{starts},
                            w.scan_sums, s);
 }
 
@@ -745,6 +1171,116 @@ int gs_bin_tiles_bounded(const int32_t* order, const int64_t* starts, const int3
   return gs::bin_tiles(order, starts, rects, count, capacity, intersections, overflow, images,
                        width, height, point_list, ranges, -1, workspace, workspace_bytes,
                        static_cast<hipStream_t>(stream));
+}
+
+}  // extern "C"
+
+namespace gs {
+namespace {
+
+int bin_blocks_tiles(const int32_t* order, const int64_t* starts, const int32_t* rects,
+                     int64_t count, int64_t m, int64_t entries, int64_t visible, int64_t images,
+                     int32_t width, int32_t height, int32_t* point_list, int32_t* ranges,
+                     uint32_t* status, void* workspace, size_t workspace_bytes, hipStream_t s) {
+  GS_REQUIRE(count >= 0 && count <= INT_MAX, GS_ERR_OVERFLOW, "too many projected primitives");
+  GS_REQUIRE(m >= 0 && m <= INT_MAX, GS_ERR_OVERFLOW, "tile intersection count exceeds int32");
+  GS_REQUIRE(entries >= 0 && entries <= INT_MAX, GS_ERR_OVERFLOW,
+             "tile block entry count exceeds int32");
+  GS_REQUIRE(width > 0 && height > 0 && images >= 0, GS_ERR_ARGUMENT,
+             "invalid image dimensions");
+  const int tw = tiles_x(width), th = tiles_y(height);
+  const int64_t tiles = images * int64_t(tw) * int64_t(th);
+  GS_REQUIRE(tiles <= INT_MAX, GS_ERR_OVERFLOW, "image tile count exceeds int32");
+  const int bw = blocks_across(tw), bh = blocks_across(th);
+  const int64_t blocks = block_count(images, tw, th);
+  GS_REQUIRE(blocks <= (int64_t(1) << (32 - kMaskBits)), GS_ERR_ARGUMENT,
+             "%lld tile blocks exceed the block path's %lld", (long long)blocks,
+             (long long)(int64_t(1) << (32 - kMaskBits)));
+  if (status) {
+    clear_flag_kernel<<<1, 64, 0, s>>>(status);
+    GS_LAUNCHED("clear_flag_kernel");
+  }
+  if (tiles == 0) return GS_OK;
+  GS_REQUIRE(ranges, GS_ERR_ARGUMENT, "null ranges");
+  const size_t need = blocks_layout(nullptr, entries, blocks, tiles).bytes + 256;
+  GS_REQUIRE(workspace && workspace_bytes >= need, GS_ERR_WORKSPACE,
+             "binning needs %zu workspace bytes, got %zu", need, workspace_bytes);
+  int2* r = reinterpret_cast<int2*>(ranges);
+  BlocksWorkspace w = blocks_layout(workspace, entries, blocks, tiles);
+  if (count == 0 || entries == 0) {
+    ProfileScope prof(GS_PROF_BINNING, s);
+    fill_ranges_kernel<<<unsigned(ceil_div(tiles, 256)), 256, 0, s>>>(tiles, r);
+    GS_LAUNCHED("fill_ranges_kernel");
+    return GS_OK;
+  }
+  GS_REQUIRE(order && starts && rects && point_list, GS_ERR_ARGUMENT,
+             "null pointer passed to gs_bin_blocks_tiles");
+  const int64_t ranks = visible >= 0 ? min(visible, count) : count;
+  {
+    ProfileScope prof(GS_PROF_BINNING, s);
+    if (ranks > 0) {
+      emit_blocks_kernel<<<unsigned(ceil_div(ranks, 256)), 256, 0, s>>>(
+          ranks, count, entries, entries, status, th, bw, bh, order, starts,
+          reinterpret_cast<const int4*>(rects), w.keys, w.values);
+      GS_LAUNCHED("emit_blocks_kernel");
+    }
+  }
+  {
+    ProfileScope prof(GS_PROF_SORT, s);
+    // Stable on the block bits: entries of a block keep their depth order.
+    const int sorted = radix_sort<uint32_t>(w.keys, w.sorted_keys, w.values, w.sorted_values,
+                                            entries, kMaskBits, kMaskBits + id_bits(blocks),
+                                            w.sort, s);
+    if (sorted != GS_OK) return sorted;
+  }
+  ProfileScope prof(GS_PROF_BINNING, s);
+  block_bounds_kernel<<<unsigned(ceil_div(max(entries, tiles), 256)), 256, 0, s>>>(
+      entries, blocks, w.sorted_keys, w.first, tiles, w.tile_counts);
+  GS_LAUNCHED("block_bounds_kernel");
+  const unsigned groups = unsigned(blocks * kChunkGroups);
+  block_tile_count_kernel<<<groups, kChunkWaves * 64, 0, s>>>(
+      bw, bh, tw, th, w.first, w.sorted_keys, w.chunk_counts, w.tile_counts);
+  GS_LAUNCHED("block_tile_count_kernel");
+  if (tiles <= kRangeLocalTiles) {
+    tile_ranges_local_kernel<<<1, kRangeThreads, 0, s>>>(tiles, m, w.tile_counts, r);
+    GS_LAUNCHED("tile_ranges_local_kernel");
+  } else {
+    const int scanned = run_scan<int64_t>(tiles, TileCountLoad2{w.tile_counts},
+                                          TileRangeStore{r, m}, w.scan_sums, s);
+    if (scanned != GS_OK) return scanned;
+  }
+  block_tile_write_kernel<<<groups, kChunkWaves * 64, 0, s>>>(
+      bw, bh, tw, th, w.first, w.sorted_keys, w.sorted_values, r, w.chunk_counts, point_list,
+      int(m), int(count), status);
+  GS_LAUNCHED("block_tile_write_kernel");
+  return GS_OK;
+}
+
+}  // namespace
+}  // namespace gs
+
+extern "C" {
+
+size_t gs_bin_blocks_tiles_workspace_size(int64_t entries, int64_t images, int32_t width,
+                                          int32_t height) {
+  if (entries < 0) entries = 0;
+  if (images < 0 || width <= 0 || height <= 0) return 256;
+  const int tw = gs::tiles_x(width), th = gs::tiles_y(height);
+  return gs::blocks_layout(nullptr, entries, gs::block_count(images, tw, th),
+                           images * int64_t(tw) * th)
+             .bytes +
+         256;
+}
+
+int gs_bin_blocks_tiles(const int32_t* order, const int64_t* starts, const int32_t* rects,
+                        int64_t count, int64_t m, int64_t entries, int64_t visible,
+                        int64_t images, int32_t width, int32_t height, int32_t* point_list,
+                        int32_t* ranges, uint32_t* status, void* workspace,
+                        size_t workspace_bytes, void* stream) {
+  gs::clear_error();
+  return gs::bin_blocks_tiles(order, starts, rects, count, m, entries, visible, images, width,
+                              height, point_list, ranges, status, workspace, workspace_bytes,
+                              static_cast<hipStream_t>(stream));
 }
 
 }  // extern "C"

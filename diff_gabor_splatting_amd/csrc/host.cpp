@@ -25,6 +25,7 @@
 
 #include <algorithm>
 #include <array>
+#include <atomic>
 #include <cstdint>
 #include <optional>
 #include <stdexcept>
@@ -60,6 +61,10 @@ struct Api {
   decltype(&gs_bin_tiles_workspace_size) bin_tiles_workspace_size = nullptr;
   decltype(&gs_bin_tiles) bin_tiles = nullptr;
   decltype(&gs_bin_tiles_bounded) bin_tiles_bounded = nullptr;
+  decltype(&gs_bin_blocks_fit) bin_blocks_fit = nullptr;
+  decltype(&gs_bin_blocks_count) bin_blocks_count = nullptr;
+  decltype(&gs_bin_blocks_tiles_workspace_size) bin_blocks_tiles_workspace_size = nullptr;
+  decltype(&gs_bin_blocks_tiles) bin_blocks_tiles = nullptr;
   decltype(&gs_render_workspace_size) render_workspace_size = nullptr;
   decltype(&gs_render_backward_workspace_size) render_backward_workspace_size = nullptr;
   decltype(&gs_render_forward) render_forward = nullptr;
@@ -94,6 +99,10 @@ void bind(const py::dict& table) {
   take(table, "gs_bin_tiles_workspace_size", next.bin_tiles_workspace_size);
   take(table, "gs_bin_tiles", next.bin_tiles);
   take(table, "gs_bin_tiles_bounded", next.bin_tiles_bounded);
+  take(table, "gs_bin_blocks_fit", next.bin_blocks_fit);
+  take(table, "gs_bin_blocks_count", next.bin_blocks_count);
+  take(table, "gs_bin_blocks_tiles_workspace_size", next.bin_blocks_tiles_workspace_size);
+  take(table, "gs_bin_blocks_tiles", next.bin_blocks_tiles);
   take(table, "gs_render_workspace_size", next.render_workspace_size);
   take(table, "gs_render_backward_workspace_size", next.render_backward_workspace_size);
   take(table, "gs_render_forward", next.render_forward);
@@ -107,7 +116,8 @@ std::vector<std::string> entry_points() {
           "gs_records_forward", "gs_records_backward_workspace_size", "gs_records_backward",
           "gs_bin_order_workspace_size", "gs_bin_order_count", "gs_bin_order_sort",
           "gs_bin_tiles_workspace_size",
-          "gs_bin_tiles", "gs_bin_tiles_bounded", "gs_render_workspace_size",
+          "gs_bin_tiles", "gs_bin_tiles_bounded", "gs_bin_blocks_fit", "gs_bin_blocks_count",
+          "gs_bin_blocks_tiles_workspace_size", "gs_bin_blocks_tiles", "gs_render_workspace_size",
           "gs_render_backward_workspace_size", "gs_render_forward", "gs_render_backward"};
 }
 
@@ -522,6 +532,26 @@ OrderStage count_stage(const at::Tensor& geometry, const at::Tensor& radii,
   return stage;
 }
 
+// The block path's count stage: stacked rectangles, block counts, and
+// totals = (M, V, block entries).
+OrderStage count_stage_blocks(const at::Tensor& geometry, const at::Tensor& radii,
+                              const at::Tensor& image_ids, int64_t width, int64_t height) {
+  const at::Device device = geometry.device();
+  OrderStage stage;
+  stage.count = geometry.size(0);
+  stage.order = at::empty({stage.count}, on(device, at::kInt));
+  stage.starts = at::empty({stage.count}, on(device, at::kLong));
+  stage.rects = at::empty({stage.count, 4}, on(device, at::kInt));
+  stage.totals = at::empty({3}, on(device, at::kLong));
+  stage.space = workspace(api.bin_order_workspace_size(stage.count), device);
+  check(api.bin_blocks_count(ptr<const float>(geometry), ptr<const int32_t>(radii),
+                             ptr<const int64_t>(image_ids), stage.count, int32_t(width),
+                             int32_t(height), ptr<int32_t>(stage.rects),
+                             ptr<int64_t>(stage.totals), stage.space.data_ptr(),
+                             size_t(stage.space.numel()), stream_of(device)));
+  return stage;
+}
+
 void sort_stage(OrderStage& stage) {
   check(api.bin_order_sort(stage.count, ptr<int32_t>(stage.order), ptr<int64_t>(stage.starts),
                            stage.space.data_ptr(), size_t(stage.space.numel()),
@@ -536,6 +566,30 @@ py::tuple bin_order(const at::Tensor& geometry, const at::Tensor& radii,
   sort_stage(stage);
   return py::make_tuple(stage.order, stage.starts, stage.rects, stage.totals);
 }
+
+// Stage 1 of the block path: order, block starts, stacked rectangles and
+// totals (M, V, block entries) on the device.
+py::tuple bin_blocks_order(const at::Tensor& geometry, const at::Tensor& radii,
+                           const at::Tensor& image_ids, int64_t width, int64_t height) {
+  require_bound();
+  c10::DeviceGuard guard(geometry.device());
+  OrderStage stage = count_stage_blocks(geometry, radii, image_ids, width, height);
+  sort_stage(stage);
+  return py::make_tuple(stage.order, stage.starts, stage.rects, stage.totals);
+}
+
+// Stage-2 path of the synchronised binning (bin_depth_first without a
+// capacity): 0 = the block path wherever the block ids fit
+// (gs_bin_blocks_fit), 1 = the tile sort. Process-wide.
+std::atomic<int> binning_path{0};
+
+void set_binning_path(const std::string& name) {
+  if (name == "blocks") binning_path = 0;
+  else if (name == "tiles") binning_path = 1;
+  else fail("binning path must be 'blocks' or 'tiles'");
+}
+
+std::string get_binning_path() { return binning_path.load() == 0 ? "blocks" : "tiles"; }
 
 std::pair<at::Tensor, at::Tensor> bin_tiles_impl(const at::Tensor& order, const at::Tensor& starts,
                                                  const at::Tensor& rects, int64_t images,
@@ -557,12 +611,43 @@ std::pair<at::Tensor, at::Tensor> bin_tiles_impl(const at::Tensor& order, const 
   return {point_list, ranges};
 }
 
+std::pair<at::Tensor, at::Tensor> bin_blocks_tiles_impl(
+    const at::Tensor& order, const at::Tensor& starts, const at::Tensor& rects, int64_t images,
+    int64_t width, int64_t height, int64_t intersections, int64_t entries, int64_t visible,
+    const std::optional<at::Tensor>& status) {
+  const at::Device device = order.device();
+  const int64_t count = order.size(0);
+  const int64_t tiles = images * tiles_across(width) * tiles_across(height);
+  c10::DeviceGuard guard(device);
+  const at::Tensor point_list = at::empty({intersections}, on(device, at::kInt));
+  const at::Tensor ranges = at::empty({tiles, 2}, on(device, at::kInt));
+  const at::Tensor space = workspace(
+      api.bin_blocks_tiles_workspace_size(entries, images, int32_t(width), int32_t(height)),
+      device);
+  check(api.bin_blocks_tiles(ptr<const int32_t>(order), ptr<const int64_t>(starts),
+                             ptr<const int32_t>(rects), count, intersections, entries, visible,
+                             images, int32_t(width), int32_t(height), ptr<int32_t>(point_list),
+                             ptr<int32_t>(ranges), ptr<uint32_t>(status), space.data_ptr(),
+                             size_t(space.numel()), stream_of(device)));
+  return {point_list, ranges};
+}
+
 py::tuple bin_tiles(const at::Tensor& order, const at::Tensor& starts, const at::Tensor& rects,
                     int64_t images, int64_t width, int64_t height, int64_t intersections,
                     int64_t visible, const std::optional<at::Tensor>& status) {
   require_bound();
   auto [point_list, ranges] =
       bin_tiles_impl(order, starts, rects, images, width, height, intersections, visible, status);
+  return py::make_tuple(point_list, ranges);
+}
+
+py::tuple bin_blocks_tiles(const at::Tensor& order, const at::Tensor& starts,
+                           const at::Tensor& rects, int64_t images, int64_t width, int64_t height,
+                           int64_t intersections, int64_t entries, int64_t visible,
+                           const std::optional<at::Tensor>& status) {
+  require_bound();
+  auto [point_list, ranges] = bin_blocks_tiles_impl(order, starts, rects, images, width, height,
+                                                    intersections, entries, visible, status);
   return py::make_tuple(point_list, ranges);
 }
 
@@ -597,13 +682,19 @@ py::tuple bin_tiles_bounded(const at::Tensor& order, const at::Tensor& starts,
 // synchronisation: flags(overflow, total) receives the status word and the
 // live count, both on the device. violations = (device int32 word, function
 // raising for a nonzero word) is read back with M and reported before M is
-// checked or used.
+// checked or used. Without a capacity, stage 2 takes the block path
+// (gs_bin_blocks_*, which also reads the block entry count back with M)
+// whenever the block ids fit, and the tile sort otherwise; both give the
+// same point list and ranges.
 std::pair<at::Tensor, at::Tensor> bin_depth_first_impl(
     const at::Tensor& geometry, const at::Tensor& radii, const at::Tensor& image_ids,
     int64_t images, int64_t width, int64_t height, const py::object& overlap,
     const std::optional<int64_t>& capacity, const py::object& flags,
     const py::object& violations) {
-  OrderStage stage = count_stage(geometry, radii, image_ids, width, height);
+  const bool blocks = !capacity && binning_path.load() == 0 &&
+                      api.bin_blocks_fit(images, int32_t(width), int32_t(height)) == 1;
+  OrderStage stage = blocks ? count_stage_blocks(geometry, radii, image_ids, width, height)
+                            : count_stage(geometry, radii, image_ids, width, height);
   const at::Tensor total = stage.totals.slice(0, 0, 1);
   if (capacity) {
     sort_stage(stage);
@@ -617,7 +708,8 @@ std::pair<at::Tensor, at::Tensor> bin_depth_first_impl(
   hipStream_t stream = static_cast<hipStream_t>(stream_of(device));
   Readback& state = readback();
   const hipEvent_t ready = readback_event(state, device);
-  check_hip(hipMemcpyAsync(state.host, stage.totals.data_ptr(), 2 * sizeof(int64_t),
+  check_hip(hipMemcpyAsync(state.host, stage.totals.data_ptr(),
+                           size_t(stage.totals.numel()) * sizeof(int64_t),
                            hipMemcpyDeviceToHost, stream),
             "hipMemcpyAsync");
   at::Tensor word;
@@ -626,7 +718,7 @@ std::pair<at::Tensor, at::Tensor> bin_depth_first_impl(
     const py::tuple pending = violations.cast<py::tuple>();
     word = pending[0].cast<at::Tensor>();
     report = pending[1];
-    check_hip(hipMemcpyAsync(state.host + 2, word.data_ptr(), sizeof(int32_t),
+    check_hip(hipMemcpyAsync(state.host + 3, word.data_ptr(), sizeof(int32_t),
                              hipMemcpyDeviceToHost, stream),
               "hipMemcpyAsync");
   }
@@ -646,11 +738,15 @@ std::pair<at::Tensor, at::Tensor> bin_depth_first_impl(
   }
   check_hip(wait(), "hipEventSynchronize");
   const int64_t intersections = state.host[0], visible = state.host[1];
+  const int64_t entries = blocks ? state.host[2] : 0;
   if (word.defined()) {
-    const int32_t value = *reinterpret_cast<const int32_t*>(state.host + 2);
+    const int32_t value = *reinterpret_cast<const int32_t*>(state.host + 3);
     report(value);
   }
   require(intersections <= kIntMax, "tile intersection count exceeds int32");
+  if (blocks)
+    return bin_blocks_tiles_impl(stage.order, stage.starts, stage.rects, images, width, height,
+                                 intersections, entries, visible, std::nullopt);
   return bin_tiles_impl(stage.order, stage.starts, stage.rects, images, width, height,
                         intersections, visible, std::nullopt);
 }
@@ -954,6 +1050,10 @@ PYBIND11_MODULE(_host, m) {
   m.def("bin_order", &bin_order);
   m.def("bin_tiles", &bin_tiles);
   m.def("bin_tiles_bounded", &bin_tiles_bounded);
+  m.def("bin_blocks_order", &bin_blocks_order);
+  m.def("bin_blocks_tiles", &bin_blocks_tiles);
+  m.def("set_binning_path", &set_binning_path);
+  m.def("binning_path", &get_binning_path);
   m.def("bin_depth_first", &bin_depth_first);
   m.def("rasterize_forward", &rasterize_forward);
   m.def("zero_accumulators", &zero_accumulators);

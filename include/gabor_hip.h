@@ -314,6 +314,46 @@ int gs_bin_tiles(const int32_t* order, const int64_t* starts, const int32_t* rec
                  int32_t height, int32_t* point_list, int32_t* ranges, uint32_t* status,
                  void* workspace, size_t workspace_bytes, void* stream);
 
+/* Block path: the same point list and ranges as gs_bin_order_count +
+ * gs_bin_order_sort + gs_bin_tiles (emitTiles + the 64-bit SortPairs +
+ * findRanges, rasterize.cu:43-69, 470-501), bit for bit, with a much
+ * smaller sort. No counterpart in the reference. The tiles are grouped in
+ * tile blocks of 4 x 4 tiles of one image (row-major per image, image after
+ * image). A pair's rectangle meets ~18 tiles but ~3 blocks on a 1080p scene
+ * of 1M surfels, so instead of sorting its M tile entries, stage 2 sorts one
+ * (block id, 16-bit mask of the block's covered tiles, pair) entry per
+ * (pair, block) on the block-id bits, stably, from depth order; then one
+ * workgroup per quarter block counts each of its tiles' entries, a scan of
+ * those counts gives the ranges, and the same workgroups write each pair
+ * into the lists of the tiles its mask covers, in block-list order, which is
+ * (depth bits, pair index) order.
+ *
+ * gs_bin_blocks_fit: 1 when the block ids of `images` images fit the block
+ * path (at most 65536 tile blocks), else 0.
+ * gs_bin_blocks_count: stage 1's first step for the block path (the
+ * workspace of gs_bin_order_count): rects [count, 4] int32 = (x0, y0 +
+ * image*th, x1, y1 + image*th), each pair's tile rectangle with the images'
+ * tile rows stacked, and totals [3] int64 on the device = (M, V, E), E the
+ * number of (pair, block) entries. gs_bin_order_sort, called next with the
+ * same workspace, then gives the depth order and, as `starts`, the first
+ * block entry of each depth rank.
+ * gs_bin_blocks_tiles: stage 2 from those order, starts and rects, with M
+ * (point_list [m]), E and V (or -1) from totals; ranges and status as in
+ * gs_bin_tiles (GS_BIN_OVERFLOW if an entry's slot falls at or past m,
+ * which consistent inputs never do). */
+int gs_bin_blocks_fit(int64_t images, int32_t width, int32_t height);
+int gs_bin_blocks_count(const float* geometry, const int32_t* radii, const int64_t* image_ids,
+                        int64_t count, int32_t width, int32_t height, int32_t* rects,
+                        int64_t* totals, void* workspace, size_t workspace_bytes, void* stream);
+/* Scratch bytes for gs_bin_blocks_tiles over `entries` block entries. */
+size_t gs_bin_blocks_tiles_workspace_size(int64_t entries, int64_t images, int32_t width,
+                                          int32_t height);
+int gs_bin_blocks_tiles(const int32_t* order, const int64_t* starts, const int32_t* rects,
+                        int64_t count, int64_t m, int64_t entries, int64_t visible,
+                        int64_t images, int32_t width, int32_t height, int32_t* point_list,
+                        int32_t* ranges, uint32_t* status, void* workspace,
+                        size_t workspace_bytes, void* stream);
+
 /* gs_bin_tiles without the host's intersection count, for callers that
  * cannot synchronise (HIP graph capture): the point list and workspace are
  * sized for `capacity` entries (point_list [capacity], workspace

@@ -37,7 +37,7 @@ def test_library_exports_every_declared_symbol():
     for name in sorted(declared_symbols()):
         assert hasattr(library, name), name
     assert set(_native.exported_symbols()) == declared_symbols()
-    assert _native.lib.gs_abi_version() == 9
+    assert _native.lib.gs_abi_version() == 10
 
 
 def test_argument_errors_return_status_and_message():
@@ -212,3 +212,18 @@ def test_host_checks_raise_before_any_launch():
                                    torch.zeros(1, 16, 16, 9), 16, 16, False, 0.1, 10.0)
     with pytest.raises(RuntimeError, match="too many tensors to check"):
         _native.check_values_word([geometry] * 17, *(torch.zeros(1),) * 5)
+
+
+def test_block_path_limit():
+    """gs_bin_blocks_fit (host arithmetic only): at most 65536 tile blocks of
+    4 x 4 tiles (16-bit block ids); past that the synchronised binning keeps
+    the tile sort."""
+    from diff_gabor_splatting_amd import _native
+
+    lib = _native.lib
+    assert lib.gs_bin_blocks_fit(1, 1920, 1080) == 1       # 30 x 17 = 510 blocks
+    assert lib.gs_bin_blocks_fit(128, 1920, 1080) == 1     # 65,280 blocks
+    assert lib.gs_bin_blocks_fit(129, 1920, 1080) == 0     # 65,790 blocks
+    assert lib.gs_bin_blocks_fit(1, 16 * 1024, 16 * 1024) == 1  # 256 x 256 blocks
+    assert lib.gs_bin_blocks_fit(1, 16 * 1024 + 1, 16 * 1024) == 0
+    assert lib.gs_bin_blocks_fit(1, 0, 16) == 0

@@ -226,6 +226,91 @@ def test_bin_tiles_flags_sort_outputs_out_of_range(native):
         assert bounds.min() >= 0 and bounds.max() <= m
 
 
+def block_entries(geometry, radii, width, height):
+    """(pair, tile block) entries of the block path: the 4 x 4-tile blocks
+    each pair's tile rectangle meets."""
+    tw, th = native_tile_grid(width, height)
+    x0, y0, x1, y1 = oracle_binning.tile_rects(geometry[:, 9:11], radii.astype(np.int64), tw, th)
+    met = (radii > 0) & (x1 > x0) & (y1 > y0)
+    blocks = ((((x1 - 1) >> 2) - (x0 >> 2) + 1) * (((y1 - 1) >> 2) - (y0 >> 2) + 1))
+    return int(np.where(met, blocks, 0).sum())
+
+
+def native_tile_grid(width, height):
+    return (width + 15) // 16, (height + 15) // 16
+
+
+@pytest.mark.parametrize("seed, q, width, height, images, culled, radius", [
+    (20, 1, 16, 16, 1, 0.0, None),            # one tile, one block
+    (21, 3000, 64, 64, 1, 1.0, None),         # every pair culled: M = E = 0
+    (22, 700, 100, 61, 3, 0.0, None),         # 7 x 4 tiles: partial blocks at both edges
+    (23, 20_000, 515, 333, 5, 0.3, None),     # 33 x 21 tiles per image, five images
+    (24, 2000, 1920, 1080, 2, 0.0, 2000),     # every pair covers its whole image
+    (25, 300_000, 512, 512, 32, 0.0, None),   # config-3-like: 2,048 blocks, equal depths
+    (26, 1_100_000, 1920, 1080, 1, 0.6, None),  # config-4-like: 510 blocks
+])
+def test_block_binning_is_bit_exact(native, seed, q, width, height, images, culled, radius):
+    """The block path (gs_bin_blocks_count, gs_bin_order_sort,
+    gs_bin_blocks_tiles) gives the oracle's point list and ranges bit for
+    bit, the totals (M, V, E), and the same lists as the tile sort through
+    bin_depth_first."""
+    geometry, radii, image_ids = random_geometry(seed, q, width, height, images)
+    radii[: int(culled * q)] = np.minimum(radii[: int(culled * q)], 0)
+    if radius is not None:
+        radii[:] = radius
+    if seed == 25:
+        geometry[:, 8] = np.float32(3.5)  # all depths tie: order is by pair index
+        geometry[::5, 8] = np.float32(2.0)
+    print(f"block binning seed={seed} q={q} {images}x{width}x{height}", flush=True)
+    g, r, ids = (torch.from_numpy(a).to(DEVICE) for a in (geometry, radii, image_ids))
+    _, ok_list, ok_ranges = oracle_binning.bin_pairs(geometry, radii, image_ids, images, width,
+                                                     height)
+    counts = oracle_binning.tile_counts(geometry, radii, width, height)
+    m, visible = int(counts.sum()), int(np.count_nonzero(counts))
+    entries = block_entries(geometry, radii, width, height)
+    assert native.lib.gs_bin_blocks_fit(images, width, height) == 1
+    order, starts, rects, totals = native.bin_blocks_order(g, r, ids, width, height)
+    assert totals.tolist() == [m, visible, entries]
+    status = torch.full((1,), -1, dtype=torch.int32, device=DEVICE)
+    for known in (visible, -1):
+        point_list, ranges = native.bin_blocks_tiles(order, starts, rects, images, width, height,
+                                                     m, entries, known, status=status)
+        assert int(status) == 0
+        np.testing.assert_array_equal(point_list.cpu().numpy(), ok_list)
+        np.testing.assert_array_equal(ranges.cpu().numpy(), ok_ranges)
+    assert native.binning_path() == "blocks"
+    try:
+        for path in ("tiles", "blocks"):
+            native.set_binning_path(path)
+            point_list, ranges = native.bin_depth_first(g, r, ids, images, width, height)
+            np.testing.assert_array_equal(point_list.cpu().numpy(), ok_list)
+            np.testing.assert_array_equal(ranges.cpu().numpy(), ok_ranges)
+    finally:
+        native.set_binning_path("blocks")
+
+
+def test_block_binning_flags_sort_outputs_out_of_range(native):
+    """An `order` entry outside [0, count), planted on the host, is replaced
+    by pair 0 and reported as GS_BIN_BAD_INDEX by the block path's emission;
+    no point-list entry or range leaves its bounds."""
+    width, height, images, q = 1920, 1080, 1, 200_000
+    geometry, radii, image_ids = random_geometry(27, q, width, height, images)
+    g, r, ids = (torch.from_numpy(a).to(DEVICE) for a in (geometry, radii, image_ids))
+    order, starts, rects, totals = native.bin_blocks_order(g, r, ids, width, height)
+    m, visible, entries = totals.tolist()
+    status = torch.full((1,), -1, dtype=torch.int32, device=DEVICE)
+    corrupt = order.clone()
+    corrupt[5], corrupt[visible // 2] = q + 7, -3
+    point_list, ranges = native.bin_blocks_tiles(corrupt, starts, rects, images, width, height, m,
+                                                 entries, visible, status=status)
+    assert int(status) & native.BINNING_BAD_INDEX
+    listed = point_list.cpu().numpy()
+    written = listed[: int(ranges[:, 1].max())]
+    assert written.min() >= 0 and written.max() < q
+    bounds = ranges.cpu().numpy()
+    assert bounds.min() >= 0 and bounds.max() <= m
+
+
 def test_ranges_of_empty_list_are_zero(native):
     ranges = native.find_ranges(torch.empty(0, dtype=torch.int64, device=DEVICE), 37)
     assert ranges.shape == (37, 2) and int(ranges.abs().sum()) == 0
