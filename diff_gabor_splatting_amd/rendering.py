@@ -20,6 +20,19 @@ from torch.autograd.function import once_differentiable
 from . import _native
 
 
+_SIDE_STREAMS: dict[int, torch.cuda.Stream] = {}
+
+
+def _side_stream(device: torch.device) -> torch.cuda.Stream:
+    """A second stream of the device (default priority) for work that only
+    has to finish before the backward: the accumulators' zero fill."""
+    index = device.index if device.index is not None else torch.cuda.current_device()
+    stream = _SIDE_STREAMS.get(index)
+    if stream is None:
+        stream = _SIDE_STREAMS[index] = torch.cuda.Stream(device=device)
+    return stream
+
+
 def _shaped(tensor: torch.Tensor, shape: tuple) -> torch.Tensor:
     """``tensor`` itself when it already has ``shape`` (no view node joins the
     autograd graph), else its reshape."""
@@ -73,12 +86,25 @@ class Composite(torch.autograd.Function):
             )
             outputs = tuple(t.view(images, height, width, t.shape[-1]) for t in shaped)
         # The backward's zeroed accumulators are cleared while the host waits
-        # for the intersection count, when the GPU would otherwise idle.
+        # for the intersection count. Without a capacity the fill (one write
+        # of every accumulator, HBM-bound) goes to a side stream, where it
+        # runs beside the binning kernels (latency-bound, few workgroups)
+        # instead of between them; the backward's stream waits for it. With
+        # a capacity (renders a caller may capture in a graph) it stays on
+        # the render's stream.
         ctx.accumulators = None
+        ctx.accumulator_stream = None
 
         def clear_accumulators():
-            ctx.accumulators = _native.zero_accumulators(geometry, appearance, opacities,
-                                                         backgrounds)
+            if bounded is None:
+                side = _side_stream(geometry.device)
+                with torch.cuda.stream(side):
+                    ctx.accumulators = _native.zero_accumulators(geometry, appearance,
+                                                                 opacities, backgrounds)
+                ctx.accumulator_stream = side
+            else:
+                ctx.accumulators = _native.zero_accumulators(geometry, appearance, opacities,
+                                                             backgrounds)
 
         # A backward can follow only when the caller records gradients (the
         # forward itself always runs without): only then are the backward's
@@ -113,6 +139,14 @@ class Composite(torch.autograd.Function):
     def backward(ctx: Any, *grad_groups):
         # A second backward through a retained graph gets fresh accumulators.
         accumulators, ctx.accumulators = ctx.accumulators, None
+        if accumulators is not None and ctx.accumulator_stream is not None:
+            # Filled on the side stream: wait for the fill, and keep the
+            # memory from being reused before this stream is done with it.
+            stream = torch.cuda.current_stream(accumulators[0].device)
+            stream.wait_stream(ctx.accumulator_stream)
+            for accumulator in accumulators:
+                accumulator.record_stream(stream)
+            ctx.accumulator_stream = None
         *saved, lists, counts, checkpoints, checkpoint_index = ctx.saved_tensors
         segments = (ctx.split, checkpoints, checkpoint_index) if ctx.split else None
         width, height = ctx.options[:2]
