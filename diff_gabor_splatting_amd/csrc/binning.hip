@@ -578,8 +578,9 @@ struct BlockTiles {
   }
 };
 
-// The block's entry list is cut into up to kChunks contiguous chunks of
-// about equal length but at least kChunkMin entries; workgroup g of a block
+// The block's entry list is cut into kChunks contiguous chunks of
+// max(kChunkMin, ceil(length / kChunks)) entries (the last ones shorter or
+// empty); workgroup g of a block
 // has kChunkWaves waves, and wave w takes chunk kChunkWaves g + w (empty
 // when the list has fewer chunks) for all 16 tiles of the block, 64 entries
 // per step and up to kWaveSteps steps per round, all of a round's loads
@@ -597,10 +598,12 @@ struct BlockChunk {
     block = blockIdx.x / kChunkGroups;
     chunk = int(blockIdx.x % kChunkGroups) * kChunkWaves + (int(threadIdx.x) >> 6);
     const int list_begin = first[block], list_end = first[block + 1];
-    const int64_t length = list_end - list_begin;
-    const int64_t chunks = min<int64_t>(kChunks, max<int64_t>(1, (length + kChunkMin - 1) / kChunkMin));
-    begin = chunk < chunks ? list_begin + int(length * chunk / chunks) : list_end;
-    end = chunk < chunks ? list_begin + int(length * (chunk + 1) / chunks) : list_end;
+    const int length = list_end - list_begin;
+    // ceil(length / kChunks), but at least kChunkMin: later chunks may be
+    // shorter or empty.
+    const int64_t chunk_length = max<int64_t>(kChunkMin, (int64_t(length) + kChunks - 1) / kChunks);
+    begin = list_begin + int(min<int64_t>(length, chunk * chunk_length));
+    end = list_begin + int(min<int64_t>(length, (chunk + 1) * chunk_length));
   }
 };
 
@@ -716,8 +719,11 @@ __global__ __launch_bounds__(kChunkWaves * 64) void block_tile_write_kernel(
   const bool inside = lane < kBlockTiles && tiles.inside(lane, tw, th);
   if (inside) {
     start = uint32_t(ranges[tiles.tile(lane, tw, th)].x);
+    // The earlier chunks' counts: all loads issued at once.
     const int* column = chunk_counts + part.block * kChunks * kBlockTiles + lane;
-    for (int c = 0; c < part.chunk; ++c) start += uint32_t(column[c * kBlockTiles]);
+#pragma unroll
+    for (int c = 0; c < kChunks - 1; ++c)
+      start += c < part.chunk ? uint32_t(column[c * kBlockTiles]) : 0u;
   }
   const uint32_t inside_bits = uint32_t(__ballot(inside));
   uint32_t next[kBlockTiles];
@@ -744,14 +750,15 @@ __global__ __launch_bounds__(kChunkWaves * 64) void block_tile_write_kernel(
         const uint64_t vote = __ballot(take);
         const uint32_t slot = __builtin_amdgcn_mbcnt_hi(
             uint32_t(vote >> 32), __builtin_amdgcn_mbcnt_lo(uint32_t(vote), next[k]));
-        if (take) {
-          if (slot < uint32_t(m)) point_list[slot] = pair[u];
-          else overflow = true;
-        }
+        if (take && slot < uint32_t(m)) point_list[slot] = pair[u];
         next[k] += uint32_t(__popcll(vote));
       }
     }
   }
+  // A tile whose slots ran past m dropped entries (uniform: next[k] is the
+  // same in every lane, and it never wraps: starts <= m, m + entries < 2^32).
+#pragma unroll
+  for (int k = 0; k < kBlockTiles; ++k) overflow |= next[k] > uint32_t(m);
   if (status && (bad || overflow))
     atomicOr(status, (bad ? kBinBadIndex : 0u) | (overflow ? kBinOverflow : 0u));
 }
