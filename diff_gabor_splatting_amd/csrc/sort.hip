@@ -1,7 +1,8 @@
 // Kernel 3: stable LSD radix sort of (uint32 or uint64 key, int32 value)
 // pairs.
 //
-// Each pass sorts on an 8-bit digit (Merrill & Grimshaw's reduce-then-scan
+// Each pass sorts on a digit of up to 8 bits, or 9 for 32-bit keys where
+// that saves a pass (Merrill & Grimshaw's reduce-then-scan
 // formulation, without decoupled look-back, so no workgroup ever waits on
 // another):
 //   1. upsweep  - every 4096-key span (2048 for short sorts) builds a digit
@@ -18,8 +19,11 @@
 // Sorts of up to 8192 keys run every pass in one workgroup instead
 // (local_sort_kernel). Only bits [begin_bit, end_bit) are sorted. gs_sort_pairs sorts the
 // reference's 64-bit image|tile|depth keys; the depth-first binning
-// pipeline (binning.hip) sorts 32-bit depth keys and then 32-bit tile ids.
+// pipeline (binning.hip) sorts 32-bit depth keys and then 32-bit tile ids
+// or tile-block ids.
 #include "sort.hpp"
+
+#include <type_traits>
 
 #include "scan.hpp"
 
@@ -36,6 +40,15 @@ __host__ __device__ constexpr int span_keys(int items) { return kSortBlock * ite
 int sort_items(int64_t m) { return m <= kShortSort ? 8 : 16; }
 constexpr int kDigitBits = 8;
 constexpr int kBins = 1 << kDigitBits;
+// Multi-workgroup passes of 32-bit keys may take digits of up to
+// kWideDigitBits bits (kWideBins bins) when that saves a pass: the 9-bit
+// block-id sort of a 1080p image (510 tile blocks) then takes one pass
+// instead of two. (Digits of 11 bits, which would sort 32-bit depth keys in
+// three passes, measured slower: 2048-bin histograms and scans per span
+// cost more than the pass they save.) The digit-major counts are sized for
+// kWideBins.
+constexpr int kWideDigitBits = 9;
+constexpr int kWideBins = 1 << kWideDigitBits;
 
 // Lanes of the wave whose `digit` equals this lane's: one ballot per digit
 // bit, intersected. Invalid lanes belong to no group.
@@ -58,7 +71,7 @@ __device__ __forceinline__ int64_t live_length(int64_t m, const int64_t* live) {
   return live ? min(m, max(*live, int64_t(0))) : m;
 }
 
-template <typename Key, int Items>
+template <typename Key, int Items, int Bins>
 __global__ __launch_bounds__(kSortBlock) void radix_upsweep_kernel(
     const Key* __restrict__ keys, int64_t capacity, const int64_t* __restrict__ live, int shift,
     int bits, uint32_t* __restrict__ counts, int64_t spans) {
@@ -66,9 +79,9 @@ __global__ __launch_bounds__(kSortBlock) void radix_upsweep_kernel(
   constexpr int kSortItems = Items;
   constexpr int kSortSpan = span_keys(Items);
   constexpr int kWaveSpan = 64 * Items;
-  __shared__ uint32_t hist[kSortWaves][kBins];
+  __shared__ uint32_t hist[kSortWaves][Bins];
   const int lane = __lane_id(), wave = threadIdx.x >> 6;
-  for (int i = threadIdx.x; i < kSortWaves * kBins; i += kSortBlock) (&hist[0][0])[i] = 0;
+  for (int i = threadIdx.x; i < kSortWaves * Bins; i += kSortBlock) (&hist[0][0])[i] = 0;
   __syncthreads();
   const uint32_t mask = (1u << bits) - 1u;
   const int64_t wave_base = int64_t(blockIdx.x) * kSortSpan + int64_t(wave) * kWaveSpan;
@@ -95,11 +108,12 @@ __global__ __launch_bounds__(kSortBlock) void radix_upsweep_kernel(
     }
   }
   __syncthreads();
-  const int d = threadIdx.x;  // kSortBlock == kBins
-  uint32_t total = 0;
+  for (int d = threadIdx.x; d < Bins; d += kSortBlock) {
+    uint32_t total = 0;
 #pragma unroll
-  for (int w = 0; w < kSortWaves; ++w) total += hist[w][d];
-  counts[int64_t(d) * spans + blockIdx.x] = total;
+    for (int w = 0; w < kSortWaves; ++w) total += hist[w][d];
+    counts[int64_t(d) * spans + blockIdx.x] = total;
+  }
 }
 
 // Pass 2: workgroup d turns row d of the digit-major counts (the digit's
@@ -131,9 +145,33 @@ __global__ __launch_bounds__(kSortBlock) void scan_rows_kernel(uint32_t* __restr
   if (threadIdx.x == 0) totals[blockIdx.x] = carry;
 }
 
+// Exclusive prefix over the workgroup of Bins values, each thread holding
+// Bins / kSortBlock consecutive ones in `v` (in place), via `partial`
+// (kSortWaves entries of LDS).
+template <int Bins>
+__device__ __forceinline__ void block_exclusive_scan(uint32_t (&v)[Bins / kSortBlock],
+                                                     uint32_t* partial) {
+  constexpr int kPer = Bins / kSortBlock;
+  const int lane = __lane_id(), wave = threadIdx.x >> 6;
+  uint32_t sum = 0;
+#pragma unroll
+  for (int j = 0; j < kPer; ++j) sum += v[j];
+  const uint32_t inclusive = wave_inclusive_scan(sum);
+  if (lane == 63) partial[wave] = inclusive;
+  __syncthreads();
+  uint32_t run = inclusive - sum;
+  for (int w = 0; w < wave; ++w) run += partial[w];
+#pragma unroll
+  for (int j = 0; j < kPer; ++j) {
+    const uint32_t x = v[j];
+    v[j] = run;
+    run += x;
+  }
+}
+
 // Values: whether int32 values travel with the keys (a keys-only sort
-// passes null value arrays).
-template <typename Key, int Items, bool Values>
+// passes null value arrays). Bins: digits of up to log2(Bins) bits.
+template <typename Key, int Items, bool Values, int Bins>
 __global__ __launch_bounds__(kSortBlock) void radix_downsweep_kernel(
     const Key* __restrict__ keys_in, const int* __restrict__ values_in,
     Key* __restrict__ keys_out, int* __restrict__ values_out, int64_t capacity,
@@ -143,14 +181,16 @@ __global__ __launch_bounds__(kSortBlock) void radix_downsweep_kernel(
   constexpr int kSortItems = Items;
   constexpr int kSortSpan = span_keys(Items);
   constexpr int kWaveSpan = 64 * Items;
-  __shared__ uint32_t running[kSortWaves][kBins];   // per-wave digit counters
-  __shared__ uint32_t local_start[kBins];           // first local slot per digit
-  __shared__ uint32_t global_start[kBins];          // first output slot per digit
+  constexpr int kPer = Bins / kSortBlock;  // digits per thread in the digit passes
+  __shared__ uint32_t running[kSortWaves][Bins];  // per-wave digit counters
+  __shared__ uint32_t local_start[Bins];          // first local slot per digit
+  __shared__ uint32_t global_start[Bins];         // first output slot per digit
+  __shared__ uint32_t partial[2][kSortWaves];
   __shared__ Key stage_keys[kSortSpan];
   __shared__ int stage_values[Values ? kSortSpan : 1];
   const int lane = __lane_id(), wave = threadIdx.x >> 6;
   const uint32_t mask = (1u << bits) - 1u;
-  for (int i = threadIdx.x; i < kSortWaves * kBins; i += kSortBlock) (&running[0][0])[i] = 0;
+  for (int i = threadIdx.x; i < kSortWaves * Bins; i += kSortBlock) (&running[0][0])[i] = 0;
   __syncthreads();
   const int64_t span = blockIdx.x;
 
@@ -168,8 +208,8 @@ __global__ __launch_bounds__(kSortBlock) void radix_downsweep_kernel(
   }
   // Rank = keys of the same digit earlier in this wave's span: the group
   // leader reserves the group's slots with an LDS atomic that returns the
-  // previous count (the 16 atomics of a lane are issued back to back, in
-  // item order, so the counts stay in key order), then every lane reads its
+  // previous count (the atomics of a lane are issued back to back, in item
+  // order, so the counts stay in key order), then every lane reads its
   // leader's value.
   uint32_t before[kSortItems];
   int leader[kSortItems];
@@ -187,10 +227,16 @@ __global__ __launch_bounds__(kSortBlock) void radix_downsweep_kernel(
 #pragma unroll
   for (int it = 0; it < kSortItems; ++it) rank[it] += uint32_t(__shfl(int(before[it]), leader[it]));
   __syncthreads();
-  // Per digit: exclusive offsets of each wave inside the span, and the
-  // span's first local / global slot.
-  {
-    const int d = threadIdx.x;
+  // Per digit (thread t takes digits [kPer t, kPer (t + 1))): exclusive
+  // offsets of each wave inside the span, the span's digit totals and their
+  // exclusive prefix (the digit's first local slot), and the exclusive
+  // prefix of the whole sequence's digit totals plus the digit's prefix
+  // over the earlier spans (its first output slot).
+  const int d0 = threadIdx.x * kPer;
+  uint32_t local[kPer], global[kPer];
+#pragma unroll
+  for (int j = 0; j < kPer; ++j) {
+    const int d = d0 + j;
     uint32_t run = 0;
 #pragma unroll
     for (int w = 0; w < kSortWaves; ++w) {
@@ -198,31 +244,16 @@ __global__ __launch_bounds__(kSortBlock) void radix_downsweep_kernel(
       running[w][d] = run;
       run += c;
     }
-    local_start[d] = run;  // digit total; converted to a prefix below
+    local[j] = run;
+    global[j] = totals[d];
   }
-  __syncthreads();
-  // Exclusive prefixes (one digit per thread) of the span's 256 digit
-  // totals and of the whole sequence's 256 digit totals; the latter plus
-  // the digit's prefix over the earlier spans is its first output slot.
-  {
-    __shared__ uint32_t wave_totals[2][kSortWaves];
-    const uint32_t v = local_start[threadIdx.x];
-    const uint32_t incl = wave_inclusive_scan(v);
-    const uint32_t all = totals[threadIdx.x];
-    const uint32_t all_incl = wave_inclusive_scan(all);
-    if (lane == 63) {
-      wave_totals[0][wave] = incl;
-      wave_totals[1][wave] = all_incl;
-    }
-    __syncthreads();
-    uint32_t before = 0, all_before = 0;
-    for (int w = 0; w < wave; ++w) {
-      before += wave_totals[0][w];
-      all_before += wave_totals[1][w];
-    }
-    local_start[threadIdx.x] = before + incl - v;
-    global_start[threadIdx.x] =
-        all_before + all_incl - all + offsets[int64_t(threadIdx.x) * spans + span];
+  block_exclusive_scan<Bins>(local, partial[0]);
+  block_exclusive_scan<Bins>(global, partial[1]);
+#pragma unroll
+  for (int j = 0; j < kPer; ++j) {
+    const int d = d0 + j;
+    local_start[d] = local[j];
+    global_start[d] = global[j] + offsets[int64_t(d) * spans + span];
   }
   __syncthreads();
 #pragma unroll
@@ -375,8 +406,8 @@ __global__ __launch_bounds__(256) void copy_pairs_kernel(const Key* __restrict__
 }
 
 struct SortWorkspace {
-  uint32_t* counts;       // kBins * spans
-  uint32_t* totals;       // kBins: each digit's count over the whole sequence
+  uint32_t* counts;       // kWideBins * spans
+  uint32_t* totals;       // kWideBins: each digit's count over the whole sequence
   void* keys_tmp;         // m keys
   int* values_tmp;        // m
   size_t bytes;
@@ -384,14 +415,14 @@ struct SortWorkspace {
 
 SortWorkspace layout(void* base, int64_t m, int key_bytes) {
   const int64_t spans = ceil_div(m, span_keys(sort_items(m)));
-  const int64_t count_items = int64_t(kBins) * spans;
+  const int64_t count_items = int64_t(kWideBins) * spans;
   SortWorkspace w;
   size_t offset = 0;
   char* p = static_cast<char*>(base);
   w.counts = reinterpret_cast<uint32_t*>(p + offset);
   offset = align_up(offset + size_t(count_items) * 4, 256);
   w.totals = reinterpret_cast<uint32_t*>(p + offset);
-  offset = align_up(offset + size_t(kBins) * 4, 256);
+  offset = align_up(offset + size_t(kWideBins) * 4, 256);
   w.keys_tmp = p + offset;
   offset = align_up(offset + size_t(m) * size_t(key_bytes), 256);
   w.values_tmp = reinterpret_cast<int*>(p + offset);  // unused by keys-only sorts
@@ -415,11 +446,12 @@ int radix_sort(const Key* keys_in, Key* keys_out, const int* values_in, int* val
   SortWorkspace w = layout(workspace, m, int(sizeof(Key)));
   const int items = sort_items(m);
   const int64_t spans = ceil_div(m, span_keys(items));
-  const int passes = int(ceil_div(end_bit - begin_bit, kDigitBits));
+  const int bits_total = end_bit - begin_bit;
+  int passes = int(ceil_div(bits_total, kDigitBits));
   // Spread the bits evenly over the passes (13 bits: 7 + 6, not 8 + 5):
   // fewer digits per pass means longer runs of equal digits per span and
   // fewer ballots per key.
-  const int digit_bits = passes ? int(ceil_div(end_bit - begin_bit, passes)) : 0;
+  int digit_bits = passes ? int(ceil_div(bits_total, passes)) : 0;
   if (passes == 0) {
     copy_pairs_kernel<Key><<<unsigned(ceil_div(m, 256)), 256, 0, s>>>(
         keys_in, values_in, keys_out, values_out, m, live);
@@ -436,6 +468,15 @@ int radix_sort(const Key* keys_in, Key* keys_out, const int* values_in, int* val
     GS_LAUNCHED("local_sort_kernel");
     return GS_OK;
   }
+  // Wider digits for 32-bit keys when they save a pass.
+  if (sizeof(Key) == 4) {
+    const int wide_passes = int(ceil_div(bits_total, kWideDigitBits));
+    if (wide_passes < passes) {
+      passes = wide_passes;
+      digit_bits = int(ceil_div(bits_total, passes));
+    }
+  }
+  const int bins = digit_bits <= kDigitBits ? kBins : kWideBins;
   // Ping-pong so that the last pass writes the caller's output.
   const Key* src_k = keys_in;
   const int* src_v = values_in;
@@ -445,28 +486,35 @@ int radix_sort(const Key* keys_in, Key* keys_out, const int* values_in, int* val
     const bool to_output = ((passes - 1 - pass) % 2) == 0;
     Key* dst_k = to_output ? keys_out : static_cast<Key*>(w.keys_tmp);
     int* dst_v = values_in ? (to_output ? values_out : w.values_tmp) : nullptr;
-    if (items == 8) {
-      radix_upsweep_kernel<Key, 8><<<unsigned(spans), kSortBlock, 0, s>>>(
+    auto upsweep = [&](auto items_tag, auto bins_tag) {
+      constexpr int I = decltype(items_tag)::value, B = decltype(bins_tag)::value;
+      radix_upsweep_kernel<Key, I, B><<<unsigned(spans), kSortBlock, 0, s>>>(
           src_k, m, live, shift, bits, w.counts, spans);
-    } else {
-      radix_upsweep_kernel<Key, 16><<<unsigned(spans), kSortBlock, 0, s>>>(
-          src_k, m, live, shift, bits, w.counts, spans);
-    }
-    GS_LAUNCHED("radix_upsweep_kernel");
-    scan_rows_kernel<<<kBins, kSortBlock, 0, s>>>(w.counts, spans, w.totals);
-    GS_LAUNCHED("scan_rows_kernel");
-    auto downsweep = [&](auto kernel) {
-      kernel<<<unsigned(spans), kSortBlock, 0, s>>>(src_k, src_v, dst_k, dst_v, m, live, shift,
-                                                    bits, w.counts, w.totals, spans);
     };
-    if (items == 8) {
-      if (values_in) downsweep(radix_downsweep_kernel<Key, 8, true>);
-      else downsweep(radix_downsweep_kernel<Key, 8, false>);
-    } else {
-      if (values_in) downsweep(radix_downsweep_kernel<Key, 16, true>);
-      else downsweep(radix_downsweep_kernel<Key, 16, false>);
-    }
-    GS_LAUNCHED("radix_downsweep_kernel");
+    auto downsweep = [&](auto items_tag, auto bins_tag) {
+      constexpr int I = decltype(items_tag)::value, B = decltype(bins_tag)::value;
+      if (values_in)
+        radix_downsweep_kernel<Key, I, true, B><<<unsigned(spans), kSortBlock, 0, s>>>(
+            src_k, src_v, dst_k, dst_v, m, live, shift, bits, w.counts, w.totals, spans);
+      else
+        radix_downsweep_kernel<Key, I, false, B><<<unsigned(spans), kSortBlock, 0, s>>>(
+            src_k, src_v, dst_k, dst_v, m, live, shift, bits, w.counts, w.totals, spans);
+    };
+    auto run = [&](auto bins_tag) {
+      using Items8 = std::integral_constant<int, 8>;
+      using Items16 = std::integral_constant<int, 16>;
+      constexpr int B = decltype(bins_tag)::value;
+      if (items == 8) upsweep(Items8{}, bins_tag);
+      else upsweep(Items16{}, bins_tag);
+      GS_LAUNCHED("radix_upsweep_kernel");
+      scan_rows_kernel<<<B, kSortBlock, 0, s>>>(w.counts, spans, w.totals);
+      GS_LAUNCHED("scan_rows_kernel");
+      if (items == 8) downsweep(Items8{}, bins_tag);
+      else downsweep(Items16{}, bins_tag);
+      GS_LAUNCHED("radix_downsweep_kernel");
+    };
+    if (bins == kBins) run(std::integral_constant<int, kBins>{});
+    else run(std::integral_constant<int, kWideBins>{});
     src_k = dst_k;
     src_v = dst_v;
   }

@@ -34,13 +34,16 @@ def to_u64(t):
                                4_194_305])
 @pytest.mark.parametrize("bits, with_values", [
     ((0, 32), True), ((19, 32), False), ((0, 13), True), ((5, 12), False),
+    ((16, 25), True), ((3, 14), False), ((0, 22), True),
 ])
 def test_sort32_is_stable_radix_order(native, m, bits, with_values):
     """The 32-bit sort of the binning stages against numpy's stable argsort:
     the one-workgroup sort (up to 8192 keys) and the reduce-then-scan digit
     passes (from 8193), partial last spans, both span sizes (4,194,305 keys
     take 4096-key spans), keys alone and with values, partial bit ranges,
-    many ties and skewed digits."""
+    many ties and skewed digits. Digit widths: 8 bits or fewer (256 bins),
+    and 9 bits in one 512-bin pass (16, 25), which saves a pass; 11 and 22
+    bits take two and three passes of at most 8 bits."""
     rng = np.random.default_rng(m + 7 * bits[0])
     keys = rng.integers(0, 2**32, m, dtype=np.uint64).astype(np.uint32)
     keys[rng.integers(0, m, m // 3)] = keys[0]  # many exact ties
