@@ -162,7 +162,11 @@ _SIGNATURES = {
     "gs_bin_blocks_fit": (_c_int, [_c_i64, _c_int, _c_int]),
     "gs_bin_blocks_count": (
         _c_int,
-        [_c_ptr] * 3 + [_c_i64, _c_int, _c_int] + [_c_ptr] * 3 + [_c_size, _c_ptr],
+        [_c_ptr] * 3 + [_c_i64, _c_int, _c_int, _c_float, _c_float] + [_c_ptr] * 3
+        + [_c_size, _c_ptr],
+    ),
+    "gs_bin_blocks_sort": (
+        _c_int, [_c_i64, _c_float, _c_float, _c_ptr, _c_ptr, _c_ptr, _c_size, _c_ptr],
     ),
     "gs_bin_blocks_tiles_workspace_size": (_c_size, [_c_i64, _c_i64, _c_int, _c_int]),
     "gs_bin_blocks_tiles": (
@@ -468,13 +472,17 @@ def bin_tiles(order, starts, rects, images, width, height, intersections, visibl
                            status)
 
 
-def bin_blocks_order(geometry, radii, image_ids, width, height):
+def bin_blocks_order(geometry, radii, image_ids, width, height, near_plane=0.0,
+                     far_plane=0.0):
     """Stage 1 of the block path: (order int32 [Q], starts int64 [Q], rects
     int32 [Q, 4], totals int64 [3] on the device = (M, V, E)). starts[j] is
     the first (pair, tile block) entry of depth rank j, rects hold each
     pair's tile rectangle with the images' tile rows stacked, and E is the
-    number of (pair, block) entries (see gs_bin_blocks_count)."""
-    return _host.bin_blocks_order(geometry, radii, image_ids, width, height)
+    number of (pair, block) entries. With clipping planes (near > 0) the
+    depth sort runs on fewer bits (see gs_bin_blocks_count); the pairs with
+    tiles must then have their depths between them."""
+    return _host.bin_blocks_order(geometry, radii, image_ids, width, height, near_plane,
+                                  far_plane)
 
 
 def bin_blocks_tiles(order, starts, rects, images, width, height, intersections, entries,
@@ -507,7 +515,7 @@ def bin_tiles_bounded(order, starts, rects, images, width, height, capacity, int
 
 
 def bin_depth_first(geometry, radii, image_ids, images, width, height, overlap=None,
-                    capacity=None, flags=None, violations=None):
+                    capacity=None, flags=None, violations=None, near_plane=0.0, far_plane=0.0):
     """Both binning stages with the one host synchronisation for M between
     them (rasterize.cu:466-469): (point_list, ranges).
 
@@ -519,9 +527,12 @@ def bin_depth_first(geometry, radii, image_ids, images, width, height, overlap=N
     bin_tiles_bounded's status word and the live count M, both device
     tensors, for the caller to fold into its own records. ``violations`` (a device
     int32 word of gs_check_values and a function that raises for a nonzero
-    word) is read back with M and reported before M is checked or used."""
+    word) is read back with M and reported before M is checked or used.
+    ``near_plane``/``far_plane`` (an addition): the planes the pairs with
+    tiles lie between, which narrow the block path's depth keys; 0, 0 (the
+    default) sorts the raw depth bits."""
     return _host.bin_depth_first(geometry, radii, image_ids, images, width, height, overlap,
-                                 capacity, flags, violations)
+                                 capacity, flags, violations, near_plane, far_plane)
 
 
 def pack_visible(radii: torch.Tensor, with_rows: bool = False, sync: bool = True):

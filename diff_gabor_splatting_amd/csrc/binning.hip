@@ -23,6 +23,8 @@
 //    order of the 64-bit sort - while the M entries move through two 8-bit
 //    passes of 8 bytes instead of 5-6 passes of 12 bytes.
 #include <climits>
+#include <cmath>
+#include <cstring>
 
 #include "common.hpp"
 #include "index_guard.hpp"
@@ -173,6 +175,8 @@ __device__ __forceinline__ int block_area(int x0, int y0, int x1, int y1) {
 // pairs are sorted (plain stores and one more launch: thousands of
 // workgroups adding into one device word would queue their atomics behind
 // each other).
+// Block path depth keys: float bits of the depth minus `depth_base`, the
+// depth clamped to [depth_base, depth_limit] first (see DepthKeys).
 template <bool Blocks>
 __global__ __launch_bounds__(256) void pair_keys_kernel(int64_t count, int tw, int th,
                                                         const float* __restrict__ geometry,
@@ -182,7 +186,9 @@ __global__ __launch_bounds__(256) void pair_keys_kernel(int64_t count, int tw, i
                                                         int* __restrict__ values,
                                                         int* __restrict__ counts,
                                                         int4* __restrict__ rects,
-                                                        long long* __restrict__ partials) {
+                                                        long long* __restrict__ partials,
+                                                        uint32_t depth_base,
+                                                        uint32_t depth_limit) {
   __shared__ long long wave_sums[3][4];
   const int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x;
   int c = 0, b = 0;
@@ -197,6 +203,7 @@ __global__ __launch_bounds__(256) void pair_keys_kernel(int64_t count, int tw, i
       if (c > 0) {
         key = __float_as_uint(g[8]);
         if constexpr (Blocks) {
+          key = min(max(key, depth_base), depth_limit) - depth_base;
           b = block_area(t.x0, t.y0, t.x1, t.y1);
           const int rows = int(image_ids[i]) * th;
           rect = make_int4(t.x0, t.y0 + rows, t.x1, t.y1 + rows);
@@ -866,13 +873,40 @@ int id_bits(int64_t tiles) {
   return bits;
 }
 
+// Depth keys of the block path. Pairs with tiles are visible, so their
+// depth z lies in (near, far); for near > 0 the float bits of those depths
+// form the contiguous range (bits(near), bits(far)), and bits(z) -
+// bits(near) orders them as the raw bits do in fewer bits: bits(far) -
+// bits(near) + 1 values, 27 bits for the default planes (0.2, 100), so the
+// depth sort takes three 9-bit passes instead of four 8-bit ones. Pairs
+// without tiles keep key 0xffffffff, whose low `bits` bits exceed every
+// visible key. Otherwise (near <= 0 or planes not finite) the raw bits on
+// all 32 bits.
+struct DepthKeys {
+  uint32_t base = 0, limit = 0xffffffffu;
+  int bits = 32;
+  DepthKeys(float near_plane, float far_plane) {
+    if (!(near_plane > 0.f) || !(far_plane > near_plane) || !std::isfinite(far_plane)) return;
+    uint32_t lo, hi;
+    std::memcpy(&lo, &near_plane, 4);
+    std::memcpy(&hi, &far_plane, 4);
+    const uint64_t span = uint64_t(hi - lo) + 1;  // key values 0..hi-lo, then the sentinel
+    int b = 0;
+    while (b < 32 && (uint64_t(1) << b) <= span) ++b;
+    if (b >= 32) return;
+    base = lo;
+    limit = hi;
+    bits = b;
+  }
+};
+
 // Stage 1's first step for both paths (pair_keys_kernel<Blocks>, then the
 // totals; every total pointer but `intersections` may be null).
 template <bool Blocks>
 int order_count(const float* geometry, const int32_t* radii, const int64_t* image_ids,
                 int64_t count, int32_t width, int32_t height, int32_t* rects,
                 int64_t* intersections, int64_t* visible, int64_t* block_total, void* workspace,
-                size_t workspace_bytes, hipStream_t s) {
+                size_t workspace_bytes, hipStream_t s, DepthKeys depth = DepthKeys(0.f, 0.f)) {
   GS_REQUIRE(count >= 0 && count <= INT_MAX, GS_ERR_OVERFLOW, "too many projected primitives");
   GS_REQUIRE(width > 0 && height > 0, GS_ERR_ARGUMENT, "invalid image dimensions");
   GS_REQUIRE(intersections, GS_ERR_ARGUMENT, "null intersections");
@@ -891,12 +925,34 @@ int order_count(const float* geometry, const int32_t* radii, const int64_t* imag
   const int64_t blocks = ceil_div(count, 256);
   pair_keys_kernel<Blocks><<<unsigned(blocks), 256, 0, s>>>(
       count, tiles_x(width), tiles_y(height), geometry, radii, image_ids, w.keys, w.pair_ids,
-      w.counts, reinterpret_cast<int4*>(rects), w.partials);
+      w.counts, reinterpret_cast<int4*>(rects), w.partials, depth.base, depth.limit);
   GS_LAUNCHED("pair_keys_kernel");
   totals_kernel<<<1, kTotalsBlock, 0, s>>>(w.partials, blocks, intersections, visible,
                                            block_total);
   GS_LAUNCHED("totals_kernel");
   return GS_OK;
+}
+
+// Stage 1's second step: the depth order of the pairs (keys on bits
+// [0, key_bits)) and the exclusive scan of their counts in that order.
+int order_sort(int64_t count, int key_bits, int32_t* order, int64_t* starts, void* workspace,
+               size_t workspace_bytes, hipStream_t s) {
+  GS_REQUIRE(count >= 0 && count <= INT_MAX, GS_ERR_OVERFLOW, "too many projected primitives");
+  if (count == 0) return GS_OK;
+  GS_REQUIRE(order && starts, GS_ERR_ARGUMENT, "null pointer passed to gs_bin_order_sort");
+  const size_t need = order_layout(nullptr, count).bytes + 256;
+  GS_REQUIRE(workspace && workspace_bytes >= need, GS_ERR_WORKSPACE,
+             "binning needs %zu workspace bytes, got %zu", need, workspace_bytes);
+  OrderWorkspace w = order_layout(workspace, count);
+  {
+    ProfileScope prof(GS_PROF_SORT, s);
+    int status = radix_sort<uint32_t>(w.keys, w.sorted, w.pair_ids, order, count, 0, key_bits,
+                                      w.sort, s);
+    if (status != GS_OK) return status;
+  }
+  ProfileScope prof(GS_PROF_BINNING, s);
+  return run_scan<int64_t>(count, SortedCountLoad{w.counts, order, count},
+                           ExclusiveStartStore{starts}, w.scan_sums, s);
 }
 
 }  // namespace
@@ -1012,38 +1068,29 @@ int gs_bin_blocks_fit(int64_t images, int32_t width, int32_t height) {
 }
 
 int gs_bin_blocks_count(const float* geometry, const int32_t* radii, const int64_t* image_ids,
-                        int64_t count, int32_t width, int32_t height, int32_t* rects,
-                        int64_t* totals, void* workspace, size_t workspace_bytes,
-                        void* stream) {
+                        int64_t count, int32_t width, int32_t height, float near_plane,
+                        float far_plane, int32_t* rects, int64_t* totals, void* workspace,
+                        size_t workspace_bytes, void* stream) {
   using namespace gs;
   clear_error();
   GS_REQUIRE(totals, GS_ERR_ARGUMENT, "null totals");
   return order_count<true>(geometry, radii, image_ids, count, width, height, rects, totals,
                            totals + 1, totals + 2, workspace, workspace_bytes,
-                           static_cast<hipStream_t>(stream));
+                           static_cast<hipStream_t>(stream), DepthKeys(near_plane, far_plane));
 }
 
 int gs_bin_order_sort(int64_t count, int32_t* order, int64_t* starts, void* workspace,
                       size_t workspace_bytes, void* stream) {
-  using namespace gs;
-  clear_error();
-  GS_REQUIRE(count >= 0 && count <= INT_MAX, GS_ERR_OVERFLOW, "too many projected primitives");
-  if (count == 0) return GS_OK;
-  GS_REQUIRE(order && starts, GS_ERR_ARGUMENT, "null pointer passed to gs_bin_order_sort");
-  const size_t need = gs_bin_order_workspace_size(count);
-  GS_REQUIRE(workspace && workspace_bytes >= need, GS_ERR_WORKSPACE,
-             "binning needs %zu workspace bytes, got %zu", need, workspace_bytes);
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  OrderWorkspace w = order_layout(workspace, count);
-  {
-    ProfileScope prof(GS_PROF_SORT, s);
-    int status = radix_sort<uint32_t>(w.keys, w.sorted, w.pair_ids, order, count, 0, 32, w.sort,
-                                      s);
-    if (status != GS_OK) return status;
-  }
-  ProfileScope prof(GS_PROF_BINNING, s);
-  return run_scan<int64_t>(count, SortedCountLoad{w.counts, order, count}, ExclusiveStartStore{starts},
-                           w.scan_sums, s);
+  gs::clear_error();
+  return gs::order_sort(count, 32, order, starts, workspace, workspace_bytes,
+                        static_cast<hipStream_t>(stream));
+}
+
+int gs_bin_blocks_sort(int64_t count, float near_plane, float far_plane, int32_t* order,
+                       int64_t* starts, void* workspace, size_t workspace_bytes, void* stream) {
+  gs::clear_error();
+  return gs::order_sort(count, gs::DepthKeys(near_plane, far_plane).bits, order, starts,
+                        workspace, workspace_bytes, static_cast<hipStream_t>(stream));
 }
 
 int gs_bin_order(const float* geometry, const int32_t* radii, const int64_t* image_ids,

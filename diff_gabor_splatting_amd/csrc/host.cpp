@@ -63,6 +63,7 @@ struct Api {
   decltype(&gs_bin_tiles_bounded) bin_tiles_bounded = nullptr;
   decltype(&gs_bin_blocks_fit) bin_blocks_fit = nullptr;
   decltype(&gs_bin_blocks_count) bin_blocks_count = nullptr;
+  decltype(&gs_bin_blocks_sort) bin_blocks_sort = nullptr;
   decltype(&gs_bin_blocks_tiles_workspace_size) bin_blocks_tiles_workspace_size = nullptr;
   decltype(&gs_bin_blocks_tiles) bin_blocks_tiles = nullptr;
   decltype(&gs_render_workspace_size) render_workspace_size = nullptr;
@@ -101,6 +102,7 @@ void bind(const py::dict& table) {
   take(table, "gs_bin_tiles_bounded", next.bin_tiles_bounded);
   take(table, "gs_bin_blocks_fit", next.bin_blocks_fit);
   take(table, "gs_bin_blocks_count", next.bin_blocks_count);
+  take(table, "gs_bin_blocks_sort", next.bin_blocks_sort);
   take(table, "gs_bin_blocks_tiles_workspace_size", next.bin_blocks_tiles_workspace_size);
   take(table, "gs_bin_blocks_tiles", next.bin_blocks_tiles);
   take(table, "gs_render_workspace_size", next.render_workspace_size);
@@ -115,8 +117,8 @@ std::vector<std::string> entry_points() {
   return {"gs_last_error", "gs_check_values", "gs_scan_workspace_size", "gs_pack_visible",
           "gs_records_forward", "gs_records_backward_workspace_size", "gs_records_backward",
           "gs_bin_order_workspace_size", "gs_bin_order_count", "gs_bin_order_sort",
-          "gs_bin_tiles_workspace_size",
-          "gs_bin_tiles", "gs_bin_tiles_bounded", "gs_bin_blocks_fit", "gs_bin_blocks_count",
+          "gs_bin_tiles_workspace_size", "gs_bin_tiles", "gs_bin_tiles_bounded",
+          "gs_bin_blocks_fit", "gs_bin_blocks_count", "gs_bin_blocks_sort",
           "gs_bin_blocks_tiles_workspace_size", "gs_bin_blocks_tiles", "gs_render_workspace_size",
           "gs_render_backward_workspace_size", "gs_render_forward", "gs_render_backward"};
 }
@@ -511,6 +513,8 @@ py::tuple records_backward(const at::Tensor& means, const at::Tensor& quaternion
 struct OrderStage {
   at::Tensor order, starts, rects, totals, space;
   int64_t count = 0;
+  bool blocks = false;               // block path (gs_bin_blocks_count)
+  float near_plane = 0.f, far_plane = 0.f;  // its depth-key range; 0, 0: raw keys
 };
 
 OrderStage count_stage(const at::Tensor& geometry, const at::Tensor& radii,
@@ -535,10 +539,14 @@ OrderStage count_stage(const at::Tensor& geometry, const at::Tensor& radii,
 // The block path's count stage: stacked rectangles, block counts, and
 // totals = (M, V, block entries).
 OrderStage count_stage_blocks(const at::Tensor& geometry, const at::Tensor& radii,
-                              const at::Tensor& image_ids, int64_t width, int64_t height) {
+                              const at::Tensor& image_ids, int64_t width, int64_t height,
+                              double near_plane, double far_plane) {
   const at::Device device = geometry.device();
   OrderStage stage;
   stage.count = geometry.size(0);
+  stage.blocks = true;
+  stage.near_plane = float(near_plane);
+  stage.far_plane = float(far_plane);
   stage.order = at::empty({stage.count}, on(device, at::kInt));
   stage.starts = at::empty({stage.count}, on(device, at::kLong));
   stage.rects = at::empty({stage.count, 4}, on(device, at::kInt));
@@ -546,16 +554,22 @@ OrderStage count_stage_blocks(const at::Tensor& geometry, const at::Tensor& radi
   stage.space = workspace(api.bin_order_workspace_size(stage.count), device);
   check(api.bin_blocks_count(ptr<const float>(geometry), ptr<const int32_t>(radii),
                              ptr<const int64_t>(image_ids), stage.count, int32_t(width),
-                             int32_t(height), ptr<int32_t>(stage.rects),
-                             ptr<int64_t>(stage.totals), stage.space.data_ptr(),
-                             size_t(stage.space.numel()), stream_of(device)));
+                             int32_t(height), stage.near_plane, stage.far_plane,
+                             ptr<int32_t>(stage.rects), ptr<int64_t>(stage.totals),
+                             stage.space.data_ptr(), size_t(stage.space.numel()),
+                             stream_of(device)));
   return stage;
 }
 
 void sort_stage(OrderStage& stage) {
-  check(api.bin_order_sort(stage.count, ptr<int32_t>(stage.order), ptr<int64_t>(stage.starts),
-                           stage.space.data_ptr(), size_t(stage.space.numel()),
-                           stream_of(stage.order.device())));
+  void* stream = stream_of(stage.order.device());
+  if (stage.blocks)
+    check(api.bin_blocks_sort(stage.count, stage.near_plane, stage.far_plane,
+                              ptr<int32_t>(stage.order), ptr<int64_t>(stage.starts),
+                              stage.space.data_ptr(), size_t(stage.space.numel()), stream));
+  else
+    check(api.bin_order_sort(stage.count, ptr<int32_t>(stage.order), ptr<int64_t>(stage.starts),
+                             stage.space.data_ptr(), size_t(stage.space.numel()), stream));
 }
 
 py::tuple bin_order(const at::Tensor& geometry, const at::Tensor& radii,
@@ -570,10 +584,12 @@ py::tuple bin_order(const at::Tensor& geometry, const at::Tensor& radii,
 // Stage 1 of the block path: order, block starts, stacked rectangles and
 // totals (M, V, block entries) on the device.
 py::tuple bin_blocks_order(const at::Tensor& geometry, const at::Tensor& radii,
-                           const at::Tensor& image_ids, int64_t width, int64_t height) {
+                           const at::Tensor& image_ids, int64_t width, int64_t height,
+                           double near_plane, double far_plane) {
   require_bound();
   c10::DeviceGuard guard(geometry.device());
-  OrderStage stage = count_stage_blocks(geometry, radii, image_ids, width, height);
+  OrderStage stage = count_stage_blocks(geometry, radii, image_ids, width, height, near_plane,
+                                        far_plane);
   sort_stage(stage);
   return py::make_tuple(stage.order, stage.starts, stage.rects, stage.totals);
 }
@@ -690,10 +706,11 @@ std::pair<at::Tensor, at::Tensor> bin_depth_first_impl(
     const at::Tensor& geometry, const at::Tensor& radii, const at::Tensor& image_ids,
     int64_t images, int64_t width, int64_t height, const py::object& overlap,
     const std::optional<int64_t>& capacity, const py::object& flags,
-    const py::object& violations) {
+    const py::object& violations, double near_plane, double far_plane) {
   const bool blocks = !capacity && binning_path.load() == 0 &&
                       api.bin_blocks_fit(images, int32_t(width), int32_t(height)) == 1;
-  OrderStage stage = blocks ? count_stage_blocks(geometry, radii, image_ids, width, height)
+  OrderStage stage = blocks ? count_stage_blocks(geometry, radii, image_ids, width, height,
+                                                near_plane, far_plane)
                             : count_stage(geometry, radii, image_ids, width, height);
   const at::Tensor total = stage.totals.slice(0, 0, 1);
   if (capacity) {
@@ -755,11 +772,12 @@ py::tuple bin_depth_first(const at::Tensor& geometry, const at::Tensor& radii,
                           const at::Tensor& image_ids, int64_t images, int64_t width,
                           int64_t height, const py::object& overlap,
                           const std::optional<int64_t>& capacity, const py::object& flags,
-                          const py::object& violations) {
+                          const py::object& violations, double near_plane, double far_plane) {
   require_bound();
   c10::DeviceGuard guard(geometry.device());
-  auto [point_list, ranges] = bin_depth_first_impl(geometry, radii, image_ids, images, width,
-                                                   height, overlap, capacity, flags, violations);
+  auto [point_list, ranges] =
+      bin_depth_first_impl(geometry, radii, image_ids, images, width, height, overlap, capacity,
+                           flags, violations, near_plane, far_plane);
   return py::make_tuple(point_list, ranges);
 }
 
@@ -852,8 +870,9 @@ py::list rasterize_forward(const at::Tensor& geometry, const at::Tensor& appeara
   const auto i32 = on(device, at::kInt);
   const at::Tensor state = at::empty({images, height, width, 3}, f32);
   const at::Tensor contributors = at::empty({images, height, width}, i32);
-  auto [point_list, ranges] = bin_depth_first_impl(geometry, radii, image_ids, images, width,
-                                                   height, overlap, capacity, flags, violations);
+  auto [point_list, ranges] =
+      bin_depth_first_impl(geometry, radii, image_ids, images, width, height, overlap, capacity,
+                           flags, violations, near_plane, far_plane);
   std::array<at::Tensor, 5> groups;
   py::object maps;
   if (outputs.is_none()) {

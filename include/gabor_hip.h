@@ -334,17 +334,25 @@ int gs_bin_tiles(const int32_t* order, const int64_t* starts, const int32_t* rec
  * workspace of gs_bin_order_count): rects [count, 4] int32 = (x0, y0 +
  * image*th, x1, y1 + image*th), each pair's tile rectangle with the images'
  * tile rows stacked, and totals [3] int64 on the device = (M, V, E), E the
- * number of (pair, block) entries. gs_bin_order_sort, called next with the
- * same workspace, then gives the depth order and, as `starts`, the first
- * block entry of each depth rank.
+ * number of (pair, block) entries. Pairs with tiles must have their depth in
+ * (near_plane, far_plane), as projection guarantees: for near_plane > 0 the
+ * depth keys are then bits(z) - bits(near) (z clamped to [near, far] first),
+ * which order the pairs as the raw bits do in bit_length(bits(far) -
+ * bits(near) + 1) bits, 27 for (0.2, 100); otherwise the raw 32 bits.
+ * gs_bin_blocks_sort, called next with the same workspace and planes, gives
+ * the depth order and, as `starts`, the first block entry of each depth rank
+ * (gs_bin_order_sort with the depth sort on those bits).
  * gs_bin_blocks_tiles: stage 2 from those order, starts and rects, with M
  * (point_list [m]), E and V (or -1) from totals; ranges and status as in
  * gs_bin_tiles (GS_BIN_OVERFLOW if an entry's slot falls at or past m,
  * which consistent inputs never do). */
 int gs_bin_blocks_fit(int64_t images, int32_t width, int32_t height);
 int gs_bin_blocks_count(const float* geometry, const int32_t* radii, const int64_t* image_ids,
-                        int64_t count, int32_t width, int32_t height, int32_t* rects,
-                        int64_t* totals, void* workspace, size_t workspace_bytes, void* stream);
+                        int64_t count, int32_t width, int32_t height, float near_plane,
+                        float far_plane, int32_t* rects, int64_t* totals, void* workspace,
+                        size_t workspace_bytes, void* stream);
+int gs_bin_blocks_sort(int64_t count, float near_plane, float far_plane, int32_t* order,
+                       int64_t* starts, void* workspace, size_t workspace_bytes, void* stream);
 /* Scratch bytes for gs_bin_blocks_tiles over `entries` block entries. */
 size_t gs_bin_blocks_tiles_workspace_size(int64_t entries, int64_t images, int32_t width,
                                           int32_t height);

@@ -272,24 +272,54 @@ def test_block_binning_is_bit_exact(native, seed, q, width, height, images, cull
     m, visible = int(counts.sum()), int(np.count_nonzero(counts))
     entries = block_entries(geometry, radii, width, height)
     assert native.lib.gs_bin_blocks_fit(images, width, height) == 1
-    order, starts, rects, totals = native.bin_blocks_order(g, r, ids, width, height)
-    assert totals.tolist() == [m, visible, entries]
     status = torch.full((1,), -1, dtype=torch.int32, device=DEVICE)
-    for known in (visible, -1):
-        point_list, ranges = native.bin_blocks_tiles(order, starts, rects, images, width, height,
-                                                     m, entries, known, status=status)
-        assert int(status) == 0
-        np.testing.assert_array_equal(point_list.cpu().numpy(), ok_list)
-        np.testing.assert_array_equal(ranges.cpu().numpy(), ok_ranges)
+    # Raw depth keys, and keys relative to the near plane (all depths of
+    # random_geometry lie in (0.2, 100): 27-bit keys, three 9-bit passes).
+    for planes in ((0.0, 0.0), (0.2, 100.0)):
+        order, starts, rects, totals = native.bin_blocks_order(g, r, ids, width, height, *planes)
+        assert totals.tolist() == [m, visible, entries]
+        for known in (visible, -1):
+            point_list, ranges = native.bin_blocks_tiles(order, starts, rects, images, width,
+                                                         height, m, entries, known, status=status)
+            assert int(status) == 0
+            np.testing.assert_array_equal(point_list.cpu().numpy(), ok_list)
+            np.testing.assert_array_equal(ranges.cpu().numpy(), ok_ranges)
     assert native.binning_path() == "blocks"
     try:
-        for path in ("tiles", "blocks"):
+        for path, planes in (("tiles", (0.0, 0.0)), ("blocks", (0.0, 0.0)),
+                             ("blocks", (0.2, 100.0))):
             native.set_binning_path(path)
-            point_list, ranges = native.bin_depth_first(g, r, ids, images, width, height)
+            point_list, ranges = native.bin_depth_first(g, r, ids, images, width, height,
+                                                        near_plane=planes[0],
+                                                        far_plane=planes[1])
             np.testing.assert_array_equal(point_list.cpu().numpy(), ok_list)
             np.testing.assert_array_equal(ranges.cpu().numpy(), ok_ranges)
     finally:
         native.set_binning_path("blocks")
+
+
+@pytest.mark.parametrize("near, far", [(0.25, 0.5), (1e-3, 1e6), (-1.0, 10.0)])
+def test_block_binning_depth_keys(native, near, far):
+    """Depth keys relative to the near plane keep the raw bits' order: depths
+    packed into a narrow range (24-bit keys, many ties), a wide one (28-bit
+    keys), and a non-positive near plane (raw keys); pairs without tiles
+    still sort after every pair with tiles."""
+    width, height, images, q = 640, 480, 2, 60_000
+    geometry, radii, image_ids = random_geometry(28, q, width, height, images)
+    rng = np.random.default_rng(29)
+    low, high = max(near, 0.0), far
+    depths = rng.uniform(low, high, q // 7).astype(np.float32)
+    depths = np.clip(depths, np.nextafter(np.float32(low), np.float32(high)),
+                     np.nextafter(np.float32(high), np.float32(low)))
+    geometry[:, 8] = rng.choice(depths, q)
+    print(f"block depth keys near={near} far={far}", flush=True)
+    g, r, ids = (torch.from_numpy(a).to(DEVICE) for a in (geometry, radii, image_ids))
+    _, ok_list, ok_ranges = oracle_binning.bin_pairs(geometry, radii, image_ids, images, width,
+                                                     height)
+    point_list, ranges = native.bin_depth_first(g, r, ids, images, width, height,
+                                                near_plane=near, far_plane=far)
+    np.testing.assert_array_equal(point_list.cpu().numpy(), ok_list)
+    np.testing.assert_array_equal(ranges.cpu().numpy(), ok_ranges)
 
 
 def test_block_binning_flags_sort_outputs_out_of_range(native):
