@@ -655,7 +655,7 @@ __global__ __launch_bounds__(kChunkWaves * 64) void block_tile_count_kernel(
   }
 }
 
-struct TileCountLoad2 {
+struct TileTotalLoad {
   const int* counts;
   __device__ int64_t operator()(int64_t t) const { return counts[t]; }
 };
@@ -1299,7 +1299,7 @@ int bin_blocks_tiles(const int32_t* order, const int64_t* starts, const int32_t*
     tile_ranges_local_kernel<<<1, kRangeThreads, 0, s>>>(tiles, m, w.tile_counts, r);
     GS_LAUNCHED("tile_ranges_local_kernel");
   } else {
-    const int scanned = run_scan<int64_t>(tiles, TileCountLoad2{w.tile_counts},
+    const int scanned = run_scan<int64_t>(tiles, TileTotalLoad{w.tile_counts},
                                           TileRangeStore{r, m}, w.scan_sums, s);
     if (scanned != GS_OK) return scanned;
   }
