@@ -174,6 +174,11 @@ _SIGNATURES = {
         [_c_ptr] * 3 + [_c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_int, _c_int] + [_c_ptr] * 4
         + [_c_size, _c_ptr],
     ),
+    "gs_bin_blocks_tiles_bounded": (
+        _c_int,
+        [_c_ptr] * 3 + [_c_i64, _c_i64, _c_ptr, _c_i64, _c_int, _c_int] + [_c_ptr] * 4
+        + [_c_size, _c_ptr],
+    ),
     "gs_render_workspace_size": (_c_size, [_c_i64, _c_int, _c_int]),
     "gs_render_backward_workspace_size": (_c_size, [_c_i64, _c_int, _c_int, _c_i64]),
     "gs_render_forward": (
@@ -494,9 +499,10 @@ def bin_blocks_tiles(order, starts, rects, images, width, height, intersections,
 
 
 def set_binning_path(name: str) -> None:
-    """Stage 2 of the synchronised binning: "blocks" (the default: the block
-    path wherever gs_bin_blocks_fit) or "tiles" (always the tile sort). Both
-    give the same point list and ranges; process-wide."""
+    """Stage 2 of the binning, synchronised or bounded: "blocks" (the
+    default: the block path wherever gs_bin_blocks_fit) or "tiles" (always
+    the tile sort). Both give the same point list and ranges (within a
+    bounded render's capacity); process-wide."""
     _host.set_binning_path(name)
 
 
@@ -514,6 +520,16 @@ def bin_tiles_bounded(order, starts, rects, images, width, height, capacity, int
                                    intersections)
 
 
+def bin_blocks_tiles_bounded(order, starts, rects, images, width, height, capacity, totals):
+    """Stage 2 of the block path without reading the totals on the host: a
+    point list of `capacity` entries, with M and E read from `totals` (int64
+    [3] on the device, bin_blocks_order's). Returns (point_list, ranges,
+    overflow) as bin_tiles_bounded does; within the capacity the point list's
+    first M entries and the ranges equal bin_blocks_tiles', the rest -1."""
+    return _host.bin_blocks_tiles_bounded(order, starts, rects, images, width, height, capacity,
+                                          totals)
+
+
 def bin_depth_first(geometry, radii, image_ids, images, width, height, overlap=None,
                     capacity=None, flags=None, violations=None, near_plane=0.0, far_plane=0.0):
     """Both binning stages with the one host synchronisation for M between
@@ -523,9 +539,11 @@ def bin_depth_first(geometry, radii, image_ids, images, width, height, overlap=N
     an event recorded after that copy, not on the stream, so GPU work that
     ``overlap()`` queues (independent of M) runs while the host waits.
     With ``capacity`` there is no synchronisation at all: the point list
-    has that many entries, and ``flags(overflow, total)`` receives
-    bin_tiles_bounded's status word and the live count M, both device
-    tensors, for the caller to fold into its own records. ``violations`` (a device
+    has that many entries, and ``flags(overflow, total)`` receives the
+    bounded stage 2's status word (bin_blocks_tiles_bounded's, or
+    bin_tiles_bounded's where the block path does not fit or the tile path
+    is selected) and the live count M, both device tensors, for the caller
+    to fold into its own records. ``violations`` (a device
     int32 word of gs_check_values and a function that raises for a nonzero
     word) is read back with M and reported before M is checked or used.
     ``near_plane``/``far_plane`` (an addition): the planes the pairs with

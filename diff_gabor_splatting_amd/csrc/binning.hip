@@ -122,6 +122,20 @@ __global__ __launch_bounds__(64) void clear_flag_kernel(uint32_t* flag) {
   if (threadIdx.x == 0) *flag = 0u;
 }
 
+// Bounded binning with nothing to bin (no pairs, or a zero capacity): the
+// point list's `capacity` entries past the live count are -1, and a live
+// count above the capacity sets kBinOverflow. The grid covers
+// max(capacity, 1) threads.
+__global__ __launch_bounds__(256) void bounded_tail_kernel(int* __restrict__ list,
+                                                           int64_t capacity,
+                                                           const int64_t* __restrict__ live,
+                                                           uint32_t* status) {
+  const int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x;
+  const int64_t m = *live;
+  if (i == 0 && m > capacity && status) atomicOr(status, kBinOverflow);
+  if (i < capacity && i >= max(m, int64_t(0))) list[i] = -1;
+}
+
 __global__ __launch_bounds__(256) void fill_ranges_kernel(int64_t tiles, int2* __restrict__ ranges) {
   const int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x;
   if (i < tiles) ranges[i] = make_int2(0, 0);
@@ -479,16 +493,23 @@ __device__ __forceinline__ uint32_t block_mask(int bx, int by, int x0, int y0, i
 // that rank's rectangle (shuffles). Entries at or past `capacity` are
 // dropped. A depth-sort output outside [0, count) is replaced by pair 0 and
 // sets kBinBadIndex; its scanned block count was 0, so it writes nothing.
+// The entry total is `total`, or *live_total (a device word) when that is
+// given; a live total above `capacity` sets kBinOverflow.
 constexpr int kMaskBits = 16;
 
 __global__ __launch_bounds__(256) void emit_blocks_kernel(
-    int64_t ranks, int64_t count, int64_t capacity, int64_t total, uint32_t* status, int th,
-    int bw, int bh, const int* __restrict__ order, const int64_t* __restrict__ starts,
+    int64_t ranks, int64_t count, int64_t capacity, int64_t total,
+    const int64_t* __restrict__ live_total, uint32_t* status, int th, int bw, int bh,
+    const int* __restrict__ order, const int64_t* __restrict__ starts,
     const int4* __restrict__ rects, uint32_t* __restrict__ keys, int* __restrict__ values) {
   const int lane = __lane_id();
   const int64_t j = int64_t(blockIdx.x) * 256 + threadIdx.x;
   const int64_t wave_rank = j - lane;
   if (wave_rank >= ranks) return;  // uniform per wave
+  if (live_total) {
+    total = *live_total;
+    if (j == 0 && total > capacity && status) atomicOr(status, kBinOverflow);
+  }
   const int last = int(min<int64_t>(63, ranks - 1 - wave_rank));  // last lane with a rank
   int pair = 0, area = 0, bx0 = 0, by0 = 0, span = 1, x0 = 0, y0 = 0, x1 = 0, y1 = 0;
   uint32_t base = 0;
@@ -543,26 +564,48 @@ __global__ __launch_bounds__(256) void emit_blocks_kernel(
   }
 }
 
+// min(capacity, *live) clamped at 0, or capacity without a live word.
+__device__ __forceinline__ int64_t live_entries(int64_t capacity, const int64_t* live) {
+  return live ? min(capacity, max(*live, int64_t(0))) : capacity;
+}
+
 // first[b] = index of block b's first entry in the block-sorted keys, for
 // b in [0, blocks]; empty blocks start where the next entry is (first[blocks]
-// = m). Each entry whose block differs from its predecessor's writes the
-// starts of the blocks from just after the predecessor's to its own.
-// The same launch clears tile_counts (`tiles` entries) for
-// block_tile_count_kernel's atomic sums.
-__global__ __launch_bounds__(256) void block_bounds_kernel(int64_t m, int64_t blocks,
-                                                           const uint32_t* __restrict__ keys,
-                                                           int* __restrict__ first,
-                                                           int64_t tiles,
-                                                           int* __restrict__ tile_counts) {
-  const int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x;
-  if (i < tiles) tile_counts[i] = 0;
-  if (i >= m) return;
-  const int64_t block = min<int64_t>(keys[i] >> kMaskBits, blocks);
-  const int64_t previous = i == 0 ? -1 : min<int64_t>(keys[i - 1] >> kMaskBits, blocks);
-  for (int64_t b = previous + 1; b <= block; ++b) first[b] = int(i);
-  if (i == m - 1)
-    for (int64_t b = block + 1; b <= blocks; ++b) first[b] = int(m);
+// = m, m = the entry count: live_entries(capacity, live)). Each entry whose
+// block differs from its predecessor's writes the starts of the blocks from
+// just after the predecessor's to its own. The same launch clears
+// tile_counts (`tiles` entries) for block_tile_count_kernel's atomic sums
+// and, for bounded binning (tail non-null), sets the point-list entries
+// [live_entries(tail_capacity, tail_live), tail_capacity) to -1. Every
+// thread strides over the grid, which may be smaller than the work (bounded
+// binning caps it: its capacities are sizes, not counts).
+__global__ __launch_bounds__(256) void block_bounds_kernel(
+    int64_t capacity, const int64_t* __restrict__ live, int64_t blocks,
+    const uint32_t* __restrict__ keys, int* __restrict__ first, int64_t tiles,
+    int* __restrict__ tile_counts, int* __restrict__ tail, int64_t tail_capacity,
+    const int64_t* __restrict__ tail_live) {
+  const int64_t stride = int64_t(gridDim.x) * 256;
+  const int64_t gid = int64_t(blockIdx.x) * 256 + threadIdx.x;
+  for (int64_t i = gid; i < tiles; i += stride) tile_counts[i] = 0;
+  if (tail)
+    for (int64_t i = live_entries(tail_capacity, tail_live) + gid; i < tail_capacity; i += stride)
+      tail[i] = -1;
+  const int64_t m = live_entries(capacity, live);
+  if (m == 0) {  // no entries (bounded binning): every block is empty
+    for (int64_t b = gid; b <= blocks; b += stride) first[b] = 0;
+    return;
+  }
+  for (int64_t i = gid; i < m; i += stride) {
+    const int64_t block = min<int64_t>(keys[i] >> kMaskBits, blocks);
+    const int64_t previous = i == 0 ? -1 : min<int64_t>(keys[i - 1] >> kMaskBits, blocks);
+    for (int64_t b = previous + 1; b <= block; ++b) first[b] = int(i);
+    if (i == m - 1)
+      for (int64_t b = block + 1; b <= blocks; ++b) first[b] = int(m);
+  }
 }
+
+// Workgroups of block_bounds_kernel in bounded binning (8 per CU).
+constexpr int64_t kBoundedBoundsGroups = 2048;
 
 // The tiles of block b: local tile k = 4 ly + lx (its bit in an entry's
 // mask) is tile (4 bx + lx, 4 by + ly) of the block's image.
@@ -661,14 +704,19 @@ struct TileTotalLoad {
 };
 
 // ranges[t] = [first, last) of tile t's entries, (0, 0) for an empty tile;
-// clamped to the point list's m entries (consistent inputs never reach it),
-// so that no range leaves the list and every slot a range covers is written.
+// clamped to the point list's m entries (only a point list shorter than
+// the entries, as bounded binning's capacity can be, reaches the clamp), so
+// that no range leaves the list and every slot a range covers is written.
+// A tile with entries keeps its clamped start even when nothing of it is
+// left (m, m): block_tile_write_kernel starts the tile's slots there, so
+// they all fall at or past m and are dropped, not written over the front of
+// the list.
 struct TileRangeStore {
   int2* ranges;
   int64_t m;
   __device__ void operator()(int64_t t, int64_t inclusive, int64_t v) const {
     const int64_t first = min(inclusive - v, m), last = min(inclusive, m);
-    ranges[t] = last > first ? make_int2(int(first), int(last)) : make_int2(0, 0);
+    ranges[t] = v > 0 ? make_int2(int(first), int(last)) : make_int2(0, 0);
   }
 };
 
@@ -1157,6 +1205,12 @@ int bin_tiles(const int32_t* order, const int64_t* starts, const int32_t* rects,
     ProfileScope prof(GS_PROF_BINNING, s);
     fill_ranges_kernel<<<unsigned(ceil_div(tiles, 256)), 256, 0, s>>>(tiles, r);
     GS_LAUNCHED("fill_ranges_kernel");
+    if (count == 0 && live && m > 0) {  // nothing binned: the whole list is -1
+      GS_REQUIRE(point_list, GS_ERR_ARGUMENT, "null point list");
+      bounded_tail_kernel<<<unsigned(ceil_div(m, 256)), 256, 0, s>>>(point_list, m, live,
+                                                                     status);
+      GS_LAUNCHED("bounded_tail_kernel");
+    }
     if (count == 0 || (m == 0 && !live)) return GS_OK;
     GS_REQUIRE(order && starts && rects, GS_ERR_ARGUMENT, "null pointer passed to gs_bin_tiles");
     if (m == 0) {  // a zero capacity still reports an overflowing emission
@@ -1232,10 +1286,15 @@ int gs_bin_tiles_bounded(const int32_t* order, const int64_t* starts, const int3
 namespace gs {
 namespace {
 
+// Shared by gs_bin_blocks_tiles (m and entries known on the host) and
+// gs_bin_blocks_tiles_bounded (totals: the device words M, V, E of
+// gs_bin_blocks_count; m is the point list's capacity, and the block entries
+// are sized for as many, since E <= M).
 int bin_blocks_tiles(const int32_t* order, const int64_t* starts, const int32_t* rects,
                      int64_t count, int64_t m, int64_t entries, int64_t visible, int64_t images,
                      int32_t width, int32_t height, int32_t* point_list, int32_t* ranges,
-                     uint32_t* status, void* workspace, size_t workspace_bytes, hipStream_t s) {
+                     uint32_t* status, void* workspace, size_t workspace_bytes, hipStream_t s,
+                     const int64_t* totals = nullptr) {
   GS_REQUIRE(count >= 0 && count <= INT_MAX, GS_ERR_OVERFLOW, "too many projected primitives");
   GS_REQUIRE(m >= 0 && m <= INT_MAX, GS_ERR_OVERFLOW, "tile intersection count exceeds int32");
   GS_REQUIRE(entries >= 0 && entries <= INT_MAX, GS_ERR_OVERFLOW,
@@ -1261,10 +1320,19 @@ int bin_blocks_tiles(const int32_t* order, const int64_t* starts, const int32_t*
              "binning needs %zu workspace bytes, got %zu", need, workspace_bytes);
   int2* r = reinterpret_cast<int2*>(ranges);
   BlocksWorkspace w = blocks_layout(workspace, entries, blocks, tiles);
+  // Bounded: the live entry count E (capped at `entries`) and M.
+  const int64_t* live_e = totals ? totals + 2 : nullptr;
+  const int64_t* live_m = totals;
   if (count == 0 || entries == 0) {
     ProfileScope prof(GS_PROF_BINNING, s);
     fill_ranges_kernel<<<unsigned(ceil_div(tiles, 256)), 256, 0, s>>>(tiles, r);
     GS_LAUNCHED("fill_ranges_kernel");
+    if (totals) {  // a -1 list, and an overflow when M exceeds a zero capacity
+      GS_REQUIRE(m == 0 || point_list, GS_ERR_ARGUMENT, "null point list");
+      bounded_tail_kernel<<<unsigned(ceil_div(max(m, int64_t(1)), 256)), 256, 0, s>>>(
+          point_list, m, live_m, status);
+      GS_LAUNCHED("bounded_tail_kernel");
+    }
     return GS_OK;
   }
   GS_REQUIRE(order && starts && rects && point_list, GS_ERR_ARGUMENT,
@@ -1274,7 +1342,7 @@ int bin_blocks_tiles(const int32_t* order, const int64_t* starts, const int32_t*
     ProfileScope prof(GS_PROF_BINNING, s);
     if (ranks > 0) {
       emit_blocks_kernel<<<unsigned(ceil_div(ranks, 256)), 256, 0, s>>>(
-          ranks, count, entries, entries, status, th, bw, bh, order, starts,
+          ranks, count, entries, entries, live_e, status, th, bw, bh, order, starts,
           reinterpret_cast<const int4*>(rects), w.keys, w.values);
       GS_LAUNCHED("emit_blocks_kernel");
     }
@@ -1284,12 +1352,17 @@ int bin_blocks_tiles(const int32_t* order, const int64_t* starts, const int32_t*
     // Stable on the block bits: entries of a block keep their depth order.
     const int sorted = radix_sort<uint32_t>(w.keys, w.sorted_keys, w.values, w.sorted_values,
                                             entries, kMaskBits, kMaskBits + id_bits(blocks),
-                                            w.sort, s);
+                                            w.sort, s, live_e);
     if (sorted != GS_OK) return sorted;
   }
   ProfileScope prof(GS_PROF_BINNING, s);
-  block_bounds_kernel<<<unsigned(ceil_div(max(entries, tiles), 256)), 256, 0, s>>>(
-      entries, blocks, w.sorted_keys, w.first, tiles, w.tile_counts);
+  const int64_t bound_threads = max(max(entries, tiles), max(blocks + 1, totals ? m : 0));
+  const int64_t bound_groups = ceil_div(bound_threads, 256);
+  block_bounds_kernel<<<unsigned(totals ? min(bound_groups, kBoundedBoundsGroups)
+                                        : bound_groups),
+                        256, 0, s>>>(
+      entries, live_e, blocks, w.sorted_keys, w.first, tiles, w.tile_counts,
+      totals ? point_list : nullptr, m, live_m);
   GS_LAUNCHED("block_bounds_kernel");
   const unsigned groups = unsigned(blocks * kChunkGroups);
   block_tile_count_kernel<<<groups, kChunkWaves * 64, 0, s>>>(
@@ -1335,6 +1408,20 @@ int gs_bin_blocks_tiles(const int32_t* order, const int64_t* starts, const int32
   return gs::bin_blocks_tiles(order, starts, rects, count, m, entries, visible, images, width,
                               height, point_list, ranges, status, workspace, workspace_bytes,
                               static_cast<hipStream_t>(stream));
+}
+
+int gs_bin_blocks_tiles_bounded(const int32_t* order, const int64_t* starts,
+                                const int32_t* rects, int64_t count, int64_t capacity,
+                                const int64_t* totals, int64_t images, int32_t width,
+                                int32_t height, int32_t* point_list, int32_t* ranges,
+                                uint32_t* overflow, void* workspace, size_t workspace_bytes,
+                                void* stream) {
+  gs::clear_error();
+  GS_REQUIRE(totals && overflow, GS_ERR_ARGUMENT,
+             "bounded binning needs the device totals and an overflow flag");
+  return gs::bin_blocks_tiles(order, starts, rects, count, capacity, capacity, -1, images,
+                              width, height, point_list, ranges, overflow, workspace,
+                              workspace_bytes, static_cast<hipStream_t>(stream), totals);
 }
 
 }  // extern "C"

@@ -61,6 +61,7 @@ struct Api {
   decltype(&gs_bin_tiles_workspace_size) bin_tiles_workspace_size = nullptr;
   decltype(&gs_bin_tiles) bin_tiles = nullptr;
   decltype(&gs_bin_tiles_bounded) bin_tiles_bounded = nullptr;
+  decltype(&gs_bin_blocks_tiles_bounded) bin_blocks_tiles_bounded = nullptr;
   decltype(&gs_bin_blocks_fit) bin_blocks_fit = nullptr;
   decltype(&gs_bin_blocks_count) bin_blocks_count = nullptr;
   decltype(&gs_bin_blocks_sort) bin_blocks_sort = nullptr;
@@ -100,6 +101,7 @@ void bind(const py::dict& table) {
   take(table, "gs_bin_tiles_workspace_size", next.bin_tiles_workspace_size);
   take(table, "gs_bin_tiles", next.bin_tiles);
   take(table, "gs_bin_tiles_bounded", next.bin_tiles_bounded);
+  take(table, "gs_bin_blocks_tiles_bounded", next.bin_blocks_tiles_bounded);
   take(table, "gs_bin_blocks_fit", next.bin_blocks_fit);
   take(table, "gs_bin_blocks_count", next.bin_blocks_count);
   take(table, "gs_bin_blocks_sort", next.bin_blocks_sort);
@@ -119,7 +121,8 @@ std::vector<std::string> entry_points() {
           "gs_bin_order_workspace_size", "gs_bin_order_count", "gs_bin_order_sort",
           "gs_bin_tiles_workspace_size", "gs_bin_tiles", "gs_bin_tiles_bounded",
           "gs_bin_blocks_fit", "gs_bin_blocks_count", "gs_bin_blocks_sort",
-          "gs_bin_blocks_tiles_workspace_size", "gs_bin_blocks_tiles", "gs_render_workspace_size",
+          "gs_bin_blocks_tiles_workspace_size", "gs_bin_blocks_tiles",
+          "gs_bin_blocks_tiles_bounded", "gs_render_workspace_size",
           "gs_render_backward_workspace_size", "gs_render_forward", "gs_render_backward"};
 }
 
@@ -688,6 +691,30 @@ py::tuple bin_tiles_bounded(const at::Tensor& order, const at::Tensor& starts,
   return py::make_tuple(point_list, ranges, overflow);
 }
 
+py::tuple bin_blocks_tiles_bounded(const at::Tensor& order, const at::Tensor& starts,
+                                   const at::Tensor& rects, int64_t images, int64_t width,
+                                   int64_t height, int64_t capacity, const at::Tensor& totals) {
+  require_bound();
+  require(totals.numel() >= 3 && totals.scalar_type() == at::kLong && totals.is_contiguous(),
+          "totals must be the contiguous int64 (M, V, E) of bin_blocks_order");
+  const at::Device device = order.device();
+  const int64_t count = order.size(0);
+  const int64_t tiles = images * tiles_across(width) * tiles_across(height);
+  c10::DeviceGuard guard(device);
+  const at::Tensor point_list = at::empty({capacity}, on(device, at::kInt));
+  const at::Tensor ranges = at::empty({tiles, 2}, on(device, at::kInt));
+  const at::Tensor overflow = at::empty({1}, on(device, at::kInt));
+  const at::Tensor space = workspace(
+      api.bin_blocks_tiles_workspace_size(capacity, images, int32_t(width), int32_t(height)),
+      device);
+  check(api.bin_blocks_tiles_bounded(
+      ptr<const int32_t>(order), ptr<const int64_t>(starts), ptr<const int32_t>(rects), count,
+      capacity, ptr<const int64_t>(totals), images, int32_t(width), int32_t(height),
+      ptr<int32_t>(point_list), ptr<int32_t>(ranges), ptr<uint32_t>(overflow), space.data_ptr(),
+      size_t(space.numel()), stream_of(device)));
+  return py::make_tuple(point_list, ranges, overflow);
+}
+
 // Both binning stages with the one host synchronisation for M between them
 // (rasterize.cu:466-469). Stage 1's first kernel sums M and V; they are
 // copied to pinned host memory right behind it, and the host waits on an
@@ -698,16 +725,16 @@ py::tuple bin_tiles_bounded(const at::Tensor& order, const at::Tensor& starts,
 // synchronisation: flags(overflow, total) receives the status word and the
 // live count, both on the device. violations = (device int32 word, function
 // raising for a nonzero word) is read back with M and reported before M is
-// checked or used. Without a capacity, stage 2 takes the block path
-// (gs_bin_blocks_*, which also reads the block entry count back with M)
-// whenever the block ids fit, and the tile sort otherwise; both give the
-// same point list and ranges.
+// checked or used. Stage 2 takes the block path (gs_bin_blocks_*, which
+// also reads the block entry count back with M, or reads it on the device
+// with a capacity) whenever the block ids fit, and the tile sort otherwise;
+// both give the same point list and ranges.
 std::pair<at::Tensor, at::Tensor> bin_depth_first_impl(
     const at::Tensor& geometry, const at::Tensor& radii, const at::Tensor& image_ids,
     int64_t images, int64_t width, int64_t height, const py::object& overlap,
     const std::optional<int64_t>& capacity, const py::object& flags,
     const py::object& violations, double near_plane, double far_plane) {
-  const bool blocks = !capacity && binning_path.load() == 0 &&
+  const bool blocks = binning_path.load() == 0 &&
                       api.bin_blocks_fit(images, int32_t(width), int32_t(height)) == 1;
   OrderStage stage = blocks ? count_stage_blocks(geometry, radii, image_ids, width, height,
                                                 near_plane, far_plane)
@@ -716,8 +743,11 @@ std::pair<at::Tensor, at::Tensor> bin_depth_first_impl(
   if (capacity) {
     sort_stage(stage);
     if (!overlap.is_none()) overlap();
-    const py::tuple bounded = bin_tiles_bounded(stage.order, stage.starts, stage.rects, images,
-                                                width, height, *capacity, total);
+    const py::tuple bounded =
+        blocks ? bin_blocks_tiles_bounded(stage.order, stage.starts, stage.rects, images, width,
+                                          height, *capacity, stage.totals)
+               : bin_tiles_bounded(stage.order, stage.starts, stage.rects, images, width,
+                                   height, *capacity, total);
     if (!flags.is_none()) flags(bounded[2], total);
     return {bounded[0].cast<at::Tensor>(), bounded[1].cast<at::Tensor>()};
   }
@@ -1069,6 +1099,7 @@ PYBIND11_MODULE(_host, m) {
   m.def("bin_order", &bin_order);
   m.def("bin_tiles", &bin_tiles);
   m.def("bin_tiles_bounded", &bin_tiles_bounded);
+  m.def("bin_blocks_tiles_bounded", &bin_blocks_tiles_bounded);
   m.def("bin_blocks_order", &bin_blocks_order);
   m.def("bin_blocks_tiles", &bin_blocks_tiles);
   m.def("set_binning_path", &set_binning_path);

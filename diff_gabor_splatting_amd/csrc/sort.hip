@@ -65,8 +65,10 @@ __device__ __forceinline__ uint64_t digit_peers(uint32_t digit, bool valid, int 
 // Digit histogram of one span, stored digit-major: counts[digit * spans +
 // span]. Each wave counts into its own LDS row; per key group the lowest
 // lane adds the group's size, so skewed digits cost no atomic conflicts.
-// Sorts whose length is known only on the device pass it as `live` (the
-// grid then covers the capacity m and spans past the live length are empty).
+// Sorts whose length is known only on the device pass it as `live`: the
+// grid then covers the capacity m, and the workgroups of spans past the live
+// length return at once in every pass (the scan reads only the live spans'
+// counts).
 __device__ __forceinline__ int64_t live_length(int64_t m, const int64_t* live) {
   return live ? min(m, max(*live, int64_t(0))) : m;
 }
@@ -79,6 +81,7 @@ __global__ __launch_bounds__(kSortBlock) void radix_upsweep_kernel(
   constexpr int kSortItems = Items;
   constexpr int kSortSpan = span_keys(Items);
   constexpr int kWaveSpan = 64 * Items;
+  if (int64_t(blockIdx.x) * kSortSpan >= m) return;  // past the live length
   __shared__ uint32_t hist[kSortWaves][Bins];
   const int lane = __lane_id(), wave = threadIdx.x >> 6;
   for (int i = threadIdx.x; i < kSortWaves * Bins; i += kSortBlock) (&hist[0][0])[i] = 0;
@@ -124,21 +127,26 @@ __global__ __launch_bounds__(kSortBlock) void radix_upsweep_kernel(
 // 256 * spans counts.
 __global__ __launch_bounds__(kSortBlock) void scan_rows_kernel(uint32_t* __restrict__ counts,
                                                                int64_t spans,
-                                                               uint32_t* __restrict__ totals) {
+                                                               uint32_t* __restrict__ totals,
+                                                               int64_t capacity,
+                                                               const int64_t* __restrict__ live,
+                                                               int span) {
   __shared__ uint32_t partial[2][kSortWaves];
   const int lane = __lane_id(), wave = threadIdx.x >> 6;
   uint32_t* row = counts + int64_t(blockIdx.x) * spans;
+  // The spans holding keys (all of them without a live length).
+  const int64_t used = min(spans, (live_length(capacity, live) + span - 1) / span);
   uint32_t carry = 0;
   int parity = 0;
-  for (int64_t base = 0; base < spans; base += kSortBlock, parity ^= 1) {
+  for (int64_t base = 0; base < used; base += kSortBlock, parity ^= 1) {
     const int64_t i = base + threadIdx.x;
-    const uint32_t v = i < spans ? row[i] : 0u;
+    const uint32_t v = i < used ? row[i] : 0u;
     const uint32_t incl = wave_inclusive_scan(v);
     if (lane == 63) partial[parity][wave] = incl;
     __syncthreads();
     uint32_t before = carry;
     for (int w = 0; w < wave; ++w) before += partial[parity][w];
-    if (i < spans) row[i] = before + incl - v;
+    if (i < used) row[i] = before + incl - v;
 #pragma unroll
     for (int w = 0; w < kSortWaves; ++w) carry += partial[parity][w];
   }
@@ -182,6 +190,7 @@ __global__ __launch_bounds__(kSortBlock) void radix_downsweep_kernel(
   constexpr int kSortSpan = span_keys(Items);
   constexpr int kWaveSpan = 64 * Items;
   constexpr int kPer = Bins / kSortBlock;  // digits per thread in the digit passes
+  if (int64_t(blockIdx.x) * kSortSpan >= m) return;  // past the live length
   __shared__ uint32_t running[kSortWaves][Bins];  // per-wave digit counters
   __shared__ uint32_t local_start[Bins];          // first local slot per digit
   __shared__ uint32_t global_start[Bins];         // first output slot per digit
@@ -507,7 +516,8 @@ int radix_sort(const Key* keys_in, Key* keys_out, const int* values_in, int* val
       if (items == 8) upsweep(Items8{}, bins_tag);
       else upsweep(Items16{}, bins_tag);
       GS_LAUNCHED("radix_upsweep_kernel");
-      scan_rows_kernel<<<B, kSortBlock, 0, s>>>(w.counts, spans, w.totals);
+      scan_rows_kernel<<<B, kSortBlock, 0, s>>>(w.counts, spans, w.totals, m, live,
+                                                span_keys(items));
       GS_LAUNCHED("scan_rows_kernel");
       if (items == 8) downsweep(Items8{}, bins_tag);
       else downsweep(Items16{}, bins_tag);

@@ -21,6 +21,9 @@ from . import _native
 
 
 _SIDE_STREAMS: dict[int, torch.cuda.Stream] = {}
+# Accumulator elements from which the backward's zero fill runs on a side
+# stream (16 MB).
+_SIDE_FILL_MIN = 1 << 22
 
 
 def _side_stream(device: torch.device) -> torch.cuda.Stream:
@@ -86,17 +89,22 @@ class Composite(torch.autograd.Function):
             )
             outputs = tuple(t.view(images, height, width, t.shape[-1]) for t in shaped)
         # The backward's zeroed accumulators are cleared while the host waits
-        # for the intersection count. Without a capacity the fill (one write
-        # of every accumulator, HBM-bound) goes to a side stream, where it
-        # runs beside the binning kernels (latency-bound, few workgroups)
-        # instead of between them; the backward's stream waits for it. With
-        # a capacity (renders a caller may capture in a graph) it stays on
-        # the render's stream.
+        # for the intersection count. Without a capacity, a large fill (one
+        # write of every accumulator, HBM-bound) goes to a side stream, where
+        # it runs beside the latency-bound binning kernels, or beside the
+        # previous step's compositors, instead of between them; the
+        # backward's stream waits for it (config 4: 2.380 -> 2.371 ms per
+        # step). A small one stays on the render's stream, where it costs
+        # less host time than the stream switch (config 0: 0.623 -> 0.569
+        # ms). With a capacity (renders a caller may capture in a graph) it
+        # stays on the render's stream too: forked into a captured graph, the
+        # fill made replays slower (configs 0-2 by 2-17%), not faster.
         ctx.accumulators = None
         ctx.accumulator_stream = None
+        fill = geometry.numel() + appearance.numel() + opacities.numel() + backgrounds.numel()
 
         def clear_accumulators():
-            if bounded is None:
+            if bounded is None and fill >= _SIDE_FILL_MIN:
                 side = _side_stream(geometry.device)
                 with torch.cuda.stream(side):
                     ctx.accumulators = _native.zero_accumulators(geometry, appearance,
@@ -351,8 +359,10 @@ class FixedCapacity:
     fixed_capacity(max_intersections) as capacity:``), renders:
 
     * bin into a point list of ``max_intersections`` entries, the count
-      staying on the device; if it exceeds the capacity the deepest records
-      of the affected tiles are dropped and a device flag is raised;
+      staying on the device; if it exceeds the capacity, records are dropped
+      (the deepest pairs' first, then the tile lists past the capacity in
+      tile order; the tile sort, where the block path does not fit, drops
+      the deepest records of the affected tiles) and a device flag is raised;
     * run the value checks (``validate=True``) on the device and keep the
       verdict instead of raising;
     * with ``packed=True``, keep one packed row per (scene, camera, surfel)
@@ -458,7 +468,7 @@ class FixedCapacity:
         if overflow:
             raise RuntimeError(
                 f"tile intersections ({peak}) exceeded the fixed capacity of "
-                f"{self.max_intersections}; the affected renders dropped their deepest records"
+                f"{self.max_intersections}; the affected renders dropped records"
             )
         return peak
 

@@ -322,11 +322,12 @@ int gs_bin_tiles(const int32_t* order, const int64_t* starts, const int32_t* rec
  * image). A pair's rectangle meets ~18 tiles but ~3 blocks on a 1080p scene
  * of 1M surfels, so instead of sorting its M tile entries, stage 2 sorts one
  * (block id, 16-bit mask of the block's covered tiles, pair) entry per
- * (pair, block) on the block-id bits, stably, from depth order; then one
- * workgroup per quarter block counts each of its tiles' entries, a scan of
- * those counts gives the ranges, and the same workgroups write each pair
- * into the lists of the tiles its mask covers, in block-list order, which is
- * (depth bits, pair index) order.
+ * (pair, block) on the block-id bits, stably, from depth order; then each
+ * block's entry list is cut into up to 16 chunks, one wave per chunk counts
+ * the entries of each of the block's 16 tiles, a scan of the tile totals
+ * gives the ranges, and the same waves write each pair into the lists of
+ * the tiles its mask covers, in block-list order, which is (depth bits,
+ * pair index) order.
  *
  * gs_bin_blocks_fit: 1 when the block ids of `images` images fit the block
  * path (at most 65536 tile blocks), else 0.
@@ -378,6 +379,27 @@ int gs_bin_tiles_bounded(const int32_t* order, const int64_t* starts, const int3
                          int64_t images, int32_t width, int32_t height, int32_t* point_list,
                          int32_t* ranges, uint32_t* overflow, void* workspace,
                          size_t workspace_bytes, void* stream);
+
+/* gs_bin_blocks_tiles without the host's counts, for the same callers: the
+ * point list holds `capacity` entries and the block entries are sized for
+ * as many (E <= M), workspace gs_bin_blocks_tiles_workspace_size(capacity,
+ * images, width, height); M and E are read from totals, the device words
+ * gs_bin_blocks_count wrote. Within the capacity (M <= capacity) the point
+ * list's first M entries and the ranges equal gs_bin_blocks_tiles' and the
+ * entries past M are -1. *overflow (a device uint32) is cleared, then gets
+ * GS_BIN_OVERFLOW when M exceeds the capacity and GS_BIN_BAD_INDEX as in
+ * gs_bin_tiles. On overflow every range stays inside the list and every
+ * entry a range covers is a valid pair, but what is kept differs from
+ * gs_bin_tiles_bounded: the block entries past the capacity (the deepest
+ * pairs') are dropped first, then the tiles' lists are cut at the capacity
+ * in tile order (the tile that crosses it keeps its shallowest records,
+ * later tiles keep none). No counterpart in the reference. */
+int gs_bin_blocks_tiles_bounded(const int32_t* order, const int64_t* starts,
+                                const int32_t* rects, int64_t count, int64_t capacity,
+                                const int64_t* totals, int64_t images, int32_t width,
+                                int32_t height, int32_t* point_list, int32_t* ranges,
+                                uint32_t* overflow, void* workspace, size_t workspace_bytes,
+                                void* stream);
 
 /* ------------------------------------------------------------------ */
 /* Kernels 4 and 5: tile compositors (renderForward / renderBackward,

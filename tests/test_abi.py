@@ -37,7 +37,7 @@ def test_library_exports_every_declared_symbol():
     for name in sorted(declared_symbols()):
         assert hasattr(library, name), name
     assert set(_native.exported_symbols()) == declared_symbols()
-    assert _native.lib.gs_abi_version() == 11
+    assert _native.lib.gs_abi_version() == 12
 
 
 def test_argument_errors_return_status_and_message():

@@ -176,6 +176,39 @@ def test_graph_replays_match_eager(method, packed):
         capacity.check()
 
 
+def test_forward_captured_alone():
+    """A render whose inputs require gradients also clears the backward's
+    accumulators (on a side stream outside fixed_capacity); inside it
+    nothing is left unjoined, so a forward can be captured alone and its
+    replays render the eager maps."""
+    from diff_gabor_splatting_amd import fixed_capacity
+
+    method = "classic"
+    base, options = scene(method, seed=14)
+    static = {k: v.detach().clone().requires_grad_() for k, v in base.items()}
+    capacity = fixed_capacity(1 << 20)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with capacity, torch.cuda.stream(side):
+        maps_from_result(renderer(method)(**static, **options))
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with capacity, torch.cuda.graph(graph):
+        static_maps = maps_from_result(renderer(method)(**static, **options))
+    capacity.check()
+    for replay, seed in enumerate((14, 15)):
+        values, _ = scene(method, seed=seed)
+        with torch.no_grad():
+            for name, value in values.items():
+                static[name].copy_(value)
+        print(f"forward-only replay {replay}", flush=True)
+        graph.replay()
+        torch.cuda.synchronize()
+        expected = maps_from_result(renderer(method)(**values, **options))
+        assert torch.equal(static_maps.detach(), expected), replay
+        capacity.check()
+
+
 @pytest.mark.parametrize("method", ["classic", "neural"])
 def test_bounded_render_of_an_empty_view(method):
     """No surfel in front of the camera: zero intersections on the device."""

@@ -344,6 +344,87 @@ def test_block_binning_flags_sort_outputs_out_of_range(native):
     assert bounds.min() >= 0 and bounds.max() <= m
 
 
+def _is_subsequence(part, whole):
+    it = iter(whole.tolist())
+    return all(any(v == w for w in it) for v in part.tolist())
+
+
+@pytest.mark.parametrize("seed, q, width, height, images, culled", [
+    (40, 0, 64, 48, 1, 0.0),                # no pairs
+    (41, 3000, 64, 64, 1, 1.0),             # every pair culled: M = E = 0
+    (42, 700, 100, 61, 3, 0.0),             # partial blocks at both edges
+    (43, 20_000, 515, 333, 5, 0.3),         # five images
+    (44, 1_100_000, 1920, 1080, 1, 0.6),    # config-4-like
+])
+def test_bounded_block_binning(native, seed, q, width, height, images, culled):
+    """gs_bin_blocks_tiles_bounded reads M and E on the device. Within the
+    capacity it gives gs_bin_blocks_tiles' point list and ranges bit for bit
+    and -1 past M. Past it (GS_BIN_OVERFLOW): with all block entries kept,
+    the list is the synchronised list cut at the capacity and the ranges
+    are clamped to it (a tile wholly past it keeps (C, C)); with block
+    entries dropped too, every tile's list is a subsequence of its
+    synchronised list, inside the capacity, made of valid pairs."""
+    geometry, radii, image_ids = random_geometry(seed, max(q, 1), width, height, images)
+    geometry, radii, image_ids = geometry[:q], radii[:q], image_ids[:q]
+    radii[: int(culled * q)] = np.minimum(radii[: int(culled * q)], 0)
+    print(f"bounded block binning seed={seed} q={q} {images}x{width}x{height}", flush=True)
+    g, r, ids = (torch.from_numpy(np.ascontiguousarray(a)).to(DEVICE)
+                 for a in (geometry, radii, image_ids))
+    order, starts, rects, totals = native.bin_blocks_order(g, r, ids, width, height, 0.2, 100.0)
+    m, visible, entries = totals.tolist()
+    status = torch.full((1,), -1, dtype=torch.int32, device=DEVICE)
+    full_list, full_ranges = native.bin_blocks_tiles(order, starts, rects, images, width, height,
+                                                     m, entries, visible, status=status)
+    assert int(status) == 0
+    full_list, full_ranges = full_list.cpu().numpy(), full_ranges.cpu().numpy()
+    capacities = sorted({m, m + 1000, m // 2, entries // 2, 0})
+    for capacity in capacities:
+        print(f"  capacity {capacity} (M {m}, E {entries})", flush=True)
+        point_list, ranges, overflow = native.bin_blocks_tiles_bounded(
+            order, starts, rects, images, width, height, capacity, totals)
+        point_list, ranges = point_list.cpu().numpy(), ranges.cpu().numpy()
+        assert point_list.shape == (capacity,) and ranges.shape == full_ranges.shape
+        if capacity >= m:
+            assert int(overflow) == 0
+            np.testing.assert_array_equal(point_list[:m], full_list)
+            assert (point_list[m:] == -1).all()
+            np.testing.assert_array_equal(ranges, full_ranges)
+            continue
+        assert int(overflow) == native.BINNING_OVERFLOW
+        assert ranges.min() >= 0 and ranges.max() <= capacity
+        assert (ranges[:, 1] >= ranges[:, 0]).all()
+        covered = np.concatenate([point_list[a:b] for a, b in ranges] + [np.zeros(0, np.int32)])
+        assert covered.size == 0 or (covered.min() >= 0 and covered.max() < q)
+        if capacity >= entries:
+            expected = np.where(
+                (full_ranges[:, 1:] > full_ranges[:, :1]),
+                np.minimum(full_ranges, capacity), 0)
+            np.testing.assert_array_equal(ranges, expected)
+            np.testing.assert_array_equal(point_list, full_list[:capacity])
+        else:
+            for t in np.flatnonzero(ranges[:, 1] > ranges[:, 0])[::97]:
+                a, b = ranges[t]
+                fa, fb = full_ranges[t]
+                assert b - a <= fb - fa
+                assert _is_subsequence(point_list[a:b], full_list[fa:fb])
+    # bin_depth_first with a capacity takes the same path, and the tile
+    # path gives the same lists within the capacity.
+    try:
+        for path in ("blocks", "tiles"):
+            native.set_binning_path(path)
+            seen = []
+            point_list, ranges = native.bin_depth_first(
+                g, r, ids, images, width, height, capacity=m + 64,
+                flags=lambda word, total: seen.append((int(word), int(total))),
+                near_plane=0.2, far_plane=100.0)
+            assert seen == [(0, m)]
+            np.testing.assert_array_equal(point_list[:m].cpu().numpy(), full_list)
+            assert bool((point_list[m:] == -1).all())
+            np.testing.assert_array_equal(ranges.cpu().numpy(), full_ranges)
+    finally:
+        native.set_binning_path("blocks")
+
+
 def test_ranges_of_empty_list_are_zero(native):
     ranges = native.find_ranges(torch.empty(0, dtype=torch.int64, device=DEVICE), 37)
     assert ranges.shape == (37, 2) and int(ranges.abs().sum()) == 0
