@@ -9,19 +9,27 @@
 // geometry and radii. Counts are computed on the fly inside the scan
 // (never stored).
 //
-// Two binning pipelines give the same point list and ranges:
+// Three binning pipelines give the same point list and ranges:
 //  * reference order (gs_emit_tiles, gs_sort_pairs, gs_find_ranges): every
 //    pair emits one 64-bit (image|tile) << 32 | depth-bits key per covered
 //    tile, and the M keys are radix-sorted on 32 + bits(tiles) bits;
-//  * depth first (gs_bin_order, then gs_bin_tiles), used by the renderer:
-//    the Q pairs are stably sorted on their 32 depth bits, each pair then
-//    emits its tiles in that order as 32-bit tile ids, and a stable sort on
-//    only bits(tiles) bits groups them by tile. The first stage needs no
+//  * depth first, tile path (gs_bin_order, then gs_bin_tiles): the Q pairs
+//    are stably sorted on their depth bits, each pair then emits its tiles
+//    in that order as 32-bit tile ids, and a stable sort on only
+//    bits(tiles) bits groups them by tile. The first stage needs no
 //    intersection count; M and V are summed by its first kernels, so the
-//    host reads them while the depth sort runs. A stable sort of depth-ordered entries by tile
-//    leaves each tile's entries ordered by (depth bits, pair index) - the
-//    order of the 64-bit sort - while the M entries move through two 8-bit
-//    passes of 8 bytes instead of 5-6 passes of 12 bytes.
+//    host reads them while the depth sort runs. A stable sort of
+//    depth-ordered entries by tile leaves each tile's entries ordered by
+//    (depth bits, pair index) - the order of the 64-bit sort - while the M
+//    entries move through two 8-bit passes of 8 bytes instead of 5-6
+//    passes of 12 bytes;
+//  * depth first, block path (gs_bin_blocks_*), the renderer's wherever
+//    the image has at most 65,536 tile blocks: the same depth order, then
+//    one entry per 4 x 4-tile block a pair meets (about M / 6 of them),
+//    sorted by block, and each block's entries written into its tiles'
+//    lists (see the block path's stage 2 below). Its bounded form
+//    (gs_bin_blocks_tiles_bounded), like gs_bin_tiles_bounded, reads the
+//    counts on the device, for callers that cannot synchronise.
 #include <climits>
 #include <cmath>
 #include <cstring>
