@@ -208,7 +208,7 @@ _SIGNATURES = {
         + [_c_int, _c_ptr, _c_ptr, _c_i64]
         + [_c_ptr] * 2
         + [_c_i64, _c_int, _c_int, _c_float, _c_float]
-        + [_c_ptr] * 5
+        + [_c_ptr] * 6
         + [_c_size, _c_ptr],
     ),
     "gs_profile_enable": (_c_int, [_c_int]),
@@ -309,47 +309,6 @@ def _workspace(nbytes: int, device: torch.device) -> torch.Tensor:
 def _require(condition: bool, message: str) -> None:
     if not condition:
         raise RuntimeError(message)
-
-
-def _check_float(value: torch.Tensor, geometry: torch.Tensor) -> None:
-    """Mirror of checkFloat (rasterize.cu:402-407)."""
-    _require(
-        value.is_cuda and value.dtype == torch.float32,
-        "native rendering requires CUDA float32 tensors",
-    )
-    _require(
-        value.device == geometry.device and value.is_contiguous(),
-        "native buffers must be contiguous on the geometry device",
-    )
-
-
-def _check_buffers(geometry, appearance, opacities, primitive_ids, backgrounds, neural) -> None:
-    """Mirror of checkBuffers (rasterize.cu:410-422)."""
-    for value in (geometry, appearance, opacities, backgrounds):
-        _check_float(value, geometry)
-    _require(
-        geometry.dim() == 2 and geometry.size(1) == GEOMETRY_SIZE, "invalid geometry shape"
-    )
-    _require(geometry.size(0) <= INT_MAX, "too many projected primitives")
-    _require(
-        appearance.dim() == 2 and appearance.size(1) == (57 if neural else 18),
-        "invalid appearance shape",
-    )
-    _require(
-        opacities.dim() == 1 and opacities.size(0) == appearance.size(0), "invalid opacity shape"
-    )
-    _require(
-        backgrounds.dim() == 2 and backgrounds.size(1) == 3 and backgrounds.size(0) > 0,
-        "invalid backgrounds",
-    )
-    _require(
-        primitive_ids.device == geometry.device
-        and primitive_ids.is_contiguous()
-        and primitive_ids.dtype == torch.int64
-        and primitive_ids.dim() == 1
-        and primitive_ids.size(0) == geometry.size(0),
-        "invalid primitive IDs",
-    )
 
 
 def tile_grid(width: int, height: int) -> tuple[int, int]:
@@ -696,6 +655,7 @@ def rasterize_forward(
     output shapes: maps [I,H,W,9], point_list int32 [M], ranges int32
     [I*tw*th, 2], state [I,H,W,3], contributors int32 [I,H,W].
 
+
     ``outputs`` (an addition): five float32 tensors [I,H,W,k], k in
     MAP_GROUPS, that receive the map channel groups instead of one maps
     tensor; the first returned item is then that tuple. ``overlap`` (an
@@ -726,8 +686,9 @@ def rasterize_forward(
 
 def zero_accumulators(geometry, appearance, opacities, backgrounds, shared=True):
     """Zeroed gradient accumulators for rasterize_backward: with ``shared``,
-    contiguous views of one allocation cleared by one fill; else four
-    separate tensors (for callers that must not return aliased tensors)."""
+    contiguous views of one allocation cleared by one fill; else separate
+    tensors (for callers that must not return aliased tensors). With
+    appearance column groups the appearance accumulator is a tuple of four."""
     return _host.zero_accumulators(geometry, appearance, opacities, backgrounds, shared)
 
 
@@ -738,6 +699,12 @@ def rasterize_backward(
 ):
     """Reverse compositing: returns [grad_geometry, grad_appearance, grad_opacities,
     grad_backgrounds] (rasterize.cu:506-529).
+
+    ``accumulators`` may hold, for the neural renderer, a tuple of the
+    SIREN's four parameter groups' gradients in place of the appearance
+    rows' (an addition, zero_accumulators with a tuple): input weights
+    [P,30], input biases [P,6], output weights [P,18], output biases [P,3];
+    grad_appearance is then that tuple.
 
     ``grad_maps`` is the reference's [I,H,W,9] tensor or (an addition) a
     sequence of five per-group gradients [I,H,W,k] in MAP_GROUPS order, each

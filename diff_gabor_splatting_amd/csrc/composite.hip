@@ -221,6 +221,26 @@ struct NeuralSums {
   static constexpr int W01 = 0, B1 = 12, W2 = 18, B2 = 36;
 };
 
+// Where the backward writes a record's appearance gradient: rows [P, A]
+// (data[0]), or, with `columns`, for the neural renderer, the SIREN's four
+// parameter groups as separate arrays (data[g] [P, width g]): input weights
+// (appearance columns 0..29), input biases (30..35), output weights
+// (36..53), output biases (54..56).
+struct AppearanceGradient {
+  float* data[4];
+  bool columns;
+};
+
+// The address of neural appearance column `col` of primitive `prim` in the
+// column-group layout.
+__device__ __forceinline__ float* siren_column(const AppearanceGradient& g, int64_t prim,
+                                               int col) {
+  return col < 30   ? g.data[0] + prim * 30 + col
+         : col < 36 ? g.data[1] + prim * 6 + (col - 30)
+         : col < 54 ? g.data[2] + prim * 18 + (col - 36)
+                    : g.data[3] + prim * 3 + (col - 54);
+}
+
 // Rejection threshold on rho: alpha = min(0.99, o exp(-rho/2)) < 1/255
 // whenever rho > 2 ln(255 o). The relative and absolute slack keep the test
 // conservative against float32 rounding, so it only ever skips samples the
@@ -1660,7 +1680,7 @@ __global__ __launch_bounds__(kTilePixels, Neural && !Replay ? 2 : 4) void render
     const int2* __restrict__ replay, const int* __restrict__ replay_counts,
     const float* __restrict__ state, const int* __restrict__ contributors,
     MapGroups<const float> grad_maps, float near_plane, float far_plane,
-    float* __restrict__ grad_geometry, float* __restrict__ grad_appearance,
+    float* __restrict__ grad_geometry, const AppearanceGradient grad_appearance,
     float* __restrict__ grad_opacities, float* __restrict__ grad_backgrounds,
     const int2* __restrict__ segments, Segments seg) {
   using L = Layout<Neural>;
@@ -2002,9 +2022,16 @@ __global__ __launch_bounds__(kTilePixels, Neural && !Replay ? 2 : 4) void render
           value = classic_appearance_gradient(sums + NG, rows + j * L::STRIDE, p - NG);
       }
       if (value != 0.f) {
-        float* dst = p < NGO            ? grad_geometry + int64_t(ids[j]) * kGeometry + p
-                     : p < NGO + L::A ? grad_appearance + prims[j] * L::A + (p - NGO)
-                                      : grad_opacities + prims[j];
+        float* dst;
+        if (p < NGO) {
+          dst = grad_geometry + int64_t(ids[j]) * kGeometry + p;
+        } else if (p < NGO + L::A) {
+          dst = (Neural && grad_appearance.columns)
+                    ? siren_column(grad_appearance, prims[j], p - NGO)
+                    : grad_appearance.data[0] + prims[j] * L::A + (p - NGO);
+        } else {
+          dst = grad_opacities + prims[j];
+        }
         atomicAdd(dst, value);
       }
     }
@@ -2194,6 +2221,18 @@ int render_forward(int32_t neural, const float* geometry, const float* appearanc
   return GS_OK;
 }
 
+// The backward's appearance gradient argument: rows, or (neural only) the
+// SIREN's four column groups (a group of no primitives may be null).
+int make_appearance_gradient(int32_t neural, float* rows, float* const* columns,
+                             AppearanceGradient* out) {
+  *out = AppearanceGradient{{rows, nullptr, nullptr, nullptr}, false};
+  if (!columns) return GS_OK;
+  GS_REQUIRE(neural, GS_ERR_ARGUMENT, "appearance column groups are for the neural renderer");
+  for (int g = 0; g < 4; ++g) out->data[g] = columns[g];
+  out->columns = true;
+  return GS_OK;
+}
+
 // Argument checks shared by both forward entry points.
 int check_render_forward(int64_t images, int32_t width, int32_t height, float near_plane,
                          float far_plane, const float* backgrounds, const int32_t* ranges,
@@ -2305,12 +2344,17 @@ int gs_render_backward(int32_t neural, const float* geometry, const float* appea
                        int64_t segment_capacity, const float* const* grad_maps,
                        const int64_t* grad_map_strides, int64_t images,
                        int32_t width, int32_t height, float near_plane, float far_plane,
-                       float* grad_geometry, float* grad_appearance, float* grad_opacities,
+                       float* grad_geometry, float* grad_appearance,
+                       float* const* grad_appearance_columns, float* grad_opacities,
                        float* grad_backgrounds, void* workspace, size_t workspace_bytes,
                        void* stream) {
   using namespace gs;
   clear_error();
   int status = check_render(images, width, height, near_plane, far_plane);
+  if (status != GS_OK) return status;
+  AppearanceGradient grad_rows;
+  status = make_appearance_gradient(neural, grad_appearance, grad_appearance_columns,
+                                    &grad_rows);
   if (status != GS_OK) return status;
   GS_REQUIRE(backgrounds && ranges && state && contributors && grad_maps && grad_map_strides &&
                  grad_backgrounds,
@@ -2356,7 +2400,7 @@ int gs_render_backward(int32_t neural, const float* geometry, const float* appea
     kernel<<<blocks, kTilePixels, 0, s>>>(
         width, height, tw, th, geometry, appearance, opacities, primitive_ids, backgrounds,
         point_list, r, w.order, w.tile_last, lists, replay_counts, state, contributors, grads,
-        near_plane, far_plane, grad_geometry, grad_appearance, grad_opacities,
+        near_plane, far_plane, grad_geometry, grad_rows, grad_opacities,
         grad_backgrounds, w.segments, seg);
   };
   if (neural) {

@@ -964,27 +964,48 @@ py::list rasterize_forward(const at::Tensor& geometry, const at::Tensor& appeara
   return result;
 }
 
-py::tuple zero_accumulators(const at::Tensor& geometry, const at::Tensor& appearance,
+// Zeroed accumulators shaped like (geometry, appearance, opacities,
+// backgrounds). `appearance` is one tensor, or a sequence of tensors (the
+// neural renderer's SIREN parameter groups), whose accumulator is then a
+// tuple of the same shapes.
+py::tuple zero_accumulators(const at::Tensor& geometry, const py::object& appearance,
                             const at::Tensor& opacities, const at::Tensor& backgrounds,
                             bool shared) {
-  const std::array<const at::Tensor*, 4> like = {&geometry, &appearance, &opacities,
-                                                 &backgrounds};
+  std::vector<at::Tensor> appearance_like;
+  const bool grouped = !THPVariable_Check(appearance.ptr());
+  if (grouped) {
+    for (const py::handle item : py::sequence(appearance))
+      appearance_like.push_back(item.cast<at::Tensor>());
+  } else {
+    appearance_like.push_back(appearance.cast<at::Tensor>());
+  }
+  std::vector<const at::Tensor*> like = {&geometry};
+  for (const at::Tensor& t : appearance_like) like.push_back(&t);
+  like.push_back(&opacities);
+  like.push_back(&backgrounds);
   c10::DeviceGuard guard(geometry.device());
-  py::tuple result(4);
+  std::vector<at::Tensor> made;
   if (!shared) {
-    for (int i = 0; i < 4; ++i) result[i] = at::zeros_like(*like[i]);
-    return result;
+    for (const at::Tensor* t : like) made.push_back(at::zeros_like(*t));
+  } else {
+    int64_t total = 0;
+    for (const at::Tensor* t : like) total += t->numel();
+    const at::Tensor flat = at::zeros({total}, on(geometry.device(), at::kFloat));
+    int64_t first = 0;
+    for (const at::Tensor* t : like) {
+      const int64_t size = t->numel();
+      made.push_back(flat.slice(0, first, first + size).view(t->sizes()));
+      first += size;
+    }
   }
-  int64_t total = 0;
-  for (const at::Tensor* t : like) total += t->numel();
-  const at::Tensor flat = at::zeros({total}, on(geometry.device(), at::kFloat));
-  int64_t first = 0;
-  for (int i = 0; i < 4; ++i) {
-    const int64_t size = like[i]->numel();
-    result[i] = flat.slice(0, first, first + size).view(like[i]->sizes());
-    first += size;
+  const size_t n = appearance_like.size();
+  py::object appearance_grads = py::cast(made[1]);
+  if (grouped) {
+    py::tuple columns(n);
+    for (size_t g = 0; g < n; ++g) columns[g] = made[1 + g];
+    appearance_grads = columns;
   }
-  return result;
+  return py::make_tuple(made[0], appearance_grads, made[1 + n], made[2 + n]);
 }
 
 py::list rasterize_backward(const at::Tensor& geometry, const at::Tensor& appearance,
@@ -1049,20 +1070,49 @@ py::list rasterize_backward(const at::Tensor& geometry, const at::Tensor& appear
             "invalid replay lists");
   }
   c10::DeviceGuard guard(device);
+  // grads[1] is the appearance rows' gradient, unless the accumulators give
+  // the neural appearance's gradient as the SIREN's four parameter groups
+  // (column_grads: input weights [P,30], input biases [P,6], output weights
+  // [P,18], output biases [P,3]), which the kernel then writes directly.
   std::array<at::Tensor, 4> grads;
+  std::array<at::Tensor, 4> column_grads;
+  bool columns = false;
   if (accumulators.is_none()) {
     grads = {at::zeros_like(geometry), at::zeros_like(appearance), at::zeros_like(opacities),
              at::zeros_like(backgrounds)};
   } else {
     const py::sequence given(accumulators);
     require(py::len(given) == 4, "invalid gradient accumulators");
-    for (int i = 0; i < 4; ++i) grads[i] = given[i].cast<at::Tensor>();
+    for (int i : {0, 2, 3}) grads[i] = given[i].cast<at::Tensor>();
+    columns = !THPVariable_Check(py::object(given[1]).ptr());
+    if (columns) {
+      const py::sequence groups_given(given[1]);
+      require(neural && py::len(groups_given) == 4, "invalid gradient accumulators");
+      for (int g = 0; g < 4; ++g) column_grads[g] = groups_given[g].cast<at::Tensor>();
+    } else {
+      grads[1] = given[1].cast<at::Tensor>();
+    }
   }
-  bool ok = grads[0].sizes() == geometry.sizes() && grads[1].sizes() == appearance.sizes() &&
-            grads[2].sizes() == opacities.sizes() && grads[3].sizes() == backgrounds.sizes();
-  for (const at::Tensor& t : grads)
-    ok = ok && t.is_contiguous() && t.scalar_type() == at::kFloat && t.device() == device;
+  constexpr std::array<int64_t, 4> kSirenWidths = {30, 6, 18, 3};
+  const int64_t primitives = appearance.size(0);
+  bool ok = grads[0].sizes() == geometry.sizes() && grads[2].sizes() == opacities.sizes() &&
+            grads[3].sizes() == backgrounds.sizes();
+  std::vector<const at::Tensor*> all = {&grads[0], &grads[2], &grads[3]};
+  std::array<float*, 4> column_pointers{};
+  if (columns) {
+    for (int g = 0; g < 4; ++g) {
+      ok = ok && same_shape(column_grads[g], {primitives, kSirenWidths[g]});
+      all.push_back(&column_grads[g]);
+    }
+  } else {
+    ok = ok && grads[1].sizes() == appearance.sizes();
+    all.push_back(&grads[1]);
+  }
+  for (const at::Tensor* t : all)
+    ok = ok && t->is_contiguous() && t->scalar_type() == at::kFloat && t->device() == device;
   require(ok, "invalid gradient accumulators");
+  if (columns)
+    for (int g = 0; g < 4; ++g) column_pointers[g] = ptr<float>(column_grads[g]);
   for (at::Tensor& g : groups)
     if (g.defined() && !flat_pixel_stride(g)) g = g.contiguous();
   const MapArgs args = map_group_args(groups, "map gradients must have uniformly strided pixels");
@@ -1077,10 +1127,18 @@ py::list rasterize_backward(const at::Tensor& geometry, const at::Tensor& appear
       ptr<const int32_t>(segment_index), slots,
       const_cast<const float* const*>(args.data.data()), args.strides.data(), images,
       int32_t(width), int32_t(height), float(near_plane), float(far_plane), ptr<float>(grads[0]),
-      ptr<float>(grads[1]), ptr<float>(grads[2]), ptr<float>(grads[3]), space.data_ptr(),
-      size_t(space.numel()), stream_of(device)));
+      columns ? nullptr : ptr<float>(grads[1]), columns ? column_pointers.data() : nullptr,
+      ptr<float>(grads[2]), ptr<float>(grads[3]), space.data_ptr(), size_t(space.numel()),
+      stream_of(device)));
   py::list result;
-  for (const at::Tensor& g : grads) result.append(g);
+  result.append(grads[0]);
+  if (columns)
+    result.append(py::make_tuple(column_grads[0], column_grads[1], column_grads[2],
+                                 column_grads[3]));
+  else
+    result.append(grads[1]);
+  result.append(grads[2]);
+  result.append(grads[3]);
   return result;
 }
 

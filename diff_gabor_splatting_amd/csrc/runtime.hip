@@ -111,7 +111,7 @@ extern "C" {
 
 const char* gs_last_error(void) { return gs::g_error.c_str(); }
 
-int gs_abi_version(void) { return 12; }
+int gs_abi_version(void) { return 13; }
 
 int gs_profile_enable(int32_t enable) {
   gs::clear_error();

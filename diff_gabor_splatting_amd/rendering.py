@@ -21,6 +21,12 @@ from . import _native
 
 
 _SIDE_STREAMS: dict[int, torch.cuda.Stream] = {}
+# Whether the neural renderer hands Composite the SIREN's four parameter
+# groups, whose gradients the backward kernel then writes in place (True),
+# or their concatenation into [S*N, 57] rows, as the reference does, whose
+# gradient autograd slices and copies into the groups (False); the results
+# are the same.
+_NEURAL_COLUMNS = True
 # Accumulator elements from which the backward's zero fill runs on a side
 # stream (16 MB).
 _SIDE_FILL_MIN = 1 << 22
@@ -65,7 +71,8 @@ class Composite(torch.autograd.Function):
     def forward(
         ctx: Any, geometry, projected_means, appearance, opacities, primitive_ids, image_ids,
         radii, backgrounds, width, height, neural, near_plane, far_plane, bounded=None,
-        grad_mode=True, violations=None, single=False,
+        grad_mode=True, violations=None, single=False, input_biases=None,
+        output_weights=None, output_biases=None,
     ):
         # backgrounds [..., C, 3]; the maps come out as [..., C, H, W, k]
         # directly (the kernels see them as [I, H, W, k]), so the caller's
@@ -101,17 +108,27 @@ class Composite(torch.autograd.Function):
         # fill made replays slower (configs 0-2 by 2-17%), not faster.
         ctx.accumulators = None
         ctx.accumulator_stream = None
-        fill = geometry.numel() + appearance.numel() + opacities.numel() + backgrounds.numel()
+        # The neural appearance may come as the SIREN's four parameter groups
+        # (appearance = the input weights). The compositors read it as the
+        # concatenated [P, 57] rows (one contiguous gather per record), made
+        # here, and the backward writes its gradient straight into the four
+        # groups' accumulators, which autograd hands to the parameters
+        # without the slice copies a concatenation's backward makes.
+        ctx.columns = input_biases is not None
+        groups = (appearance, input_biases, output_weights, output_biases)
+        rows = torch.cat(groups, dim=1) if ctx.columns else appearance
+        like = groups if ctx.columns else appearance
+        fill = geometry.numel() + rows.numel() + opacities.numel() + backgrounds.numel()
 
         def clear_accumulators():
             if bounded is None and fill >= _SIDE_FILL_MIN:
                 side = _side_stream(geometry.device)
                 with torch.cuda.stream(side):
-                    ctx.accumulators = _native.zero_accumulators(geometry, appearance,
-                                                                 opacities, backgrounds)
+                    ctx.accumulators = _native.zero_accumulators(geometry, like, opacities,
+                                                                 backgrounds)
                 ctx.accumulator_stream = side
             else:
-                ctx.accumulators = _native.zero_accumulators(geometry, appearance, opacities,
+                ctx.accumulators = _native.zero_accumulators(geometry, like, opacities,
                                                              backgrounds)
 
         # A backward can follow only when the caller records gradients (the
@@ -120,7 +137,7 @@ class Composite(torch.autograd.Function):
         needs_grad = grad_mode and any(ctx.needs_input_grad)
         overlap = clear_accumulators if needs_grad else None
         _, points, ranges, state, contributors, *replay = _native.rasterize_forward(
-            geometry, appearance, opacities, primitive_ids, image_ids, radii, backgrounds,
+            geometry, rows, opacities, primitive_ids, image_ids, radii, backgrounds,
             width, height, neural, near_plane, far_plane, outputs=outputs, overlap=overlap,
             capacity=None if bounded is None else bounded.max_intersections,
             flags=None if bounded is None else bounded.record_binning, replay=needs_grad,
@@ -134,7 +151,7 @@ class Composite(torch.autograd.Function):
         lists, counts, segments = replay if replay is not None else (None, None, None)
         length, checkpoints, checkpoint_index = segments if segments else (0, None, None)
         ctx.save_for_backward(
-            geometry, appearance, opacities, primitive_ids, backgrounds, points, ranges, state,
+            geometry, rows, opacities, primitive_ids, backgrounds, points, ranges, state,
             contributors, lists, counts, checkpoints, checkpoint_index,
         )
         ctx.split = length
@@ -153,7 +170,8 @@ class Composite(torch.autograd.Function):
             stream = torch.cuda.current_stream(accumulators[0].device)
             stream.wait_stream(ctx.accumulator_stream)
             for accumulator in accumulators:
-                accumulator.record_stream(stream)
+                for tensor in (accumulator if isinstance(accumulator, tuple) else (accumulator,)):
+                    tensor.record_stream(stream)
             ctx.accumulator_stream = None
         *saved, lists, counts, checkpoints, checkpoint_index = ctx.saved_tensors
         segments = (ctx.split, checkpoints, checkpoint_index) if ctx.split else None
@@ -172,8 +190,13 @@ class Composite(torch.autograd.Function):
             *saved, groups, *ctx.options, accumulators=accumulators,
             replay=None if lists is None else (lists, counts, segments),
         )
+        column_grads = (None, None, None)
+        if ctx.columns:
+            # Without the forward's accumulators (a second backward through a
+            # retained graph) the kernel wrote [P, 57] rows.
+            ga, *column_grads = ga if isinstance(ga, tuple) else ga.split([30, 6, 18, 3], 1)
         return (gg, gg[:, 9:11], ga, go, None, None, None, gb.view(ctx.background_shape), None,
-                None, None, None, None, None, None, None, None)
+                None, None, None, None, None, None, None, None, *column_grads)
 
 
 class ProjectRecords(torch.autograd.Function):
@@ -622,6 +645,7 @@ def render(
 
     views = _shaped(view_matrices, (scenes, cameras, 4, 4))
     cameras_k = _shaped(intrinsics, (scenes, cameras, 3, 3))
+    columns = [None, None, None]  # the neural renderer's other SIREN groups
     if sh_degree is not None:
         # Camera-specific SH colours: appearance and opacity rows per pair,
         # written by the HIP record kernel.
@@ -643,9 +667,21 @@ def render(
             _shaped(scales, (scenes, n, 2)), None, views, cameras_k, None, None, None, None, None,
             None, width, height, near_plane, far_plane, packed, bounded is not None,
         )
-        width_of_row = 57 if neural else 18
-        flat = [t.reshape(scenes, n, math.prod(shape)) for t, (_, shape) in zip(appearance, fields)]
-        parameters = torch.cat(flat, dim=-1).reshape(scenes * n, width_of_row)
+        if neural and _NEURAL_COLUMNS:
+            # The SIREN's four parameter groups as [S*N, w] views of the
+            # caller's tensors: Composite concatenates them into the rows the
+            # reference builds here (rendering.py:349-356) and writes their
+            # gradients back group by group.
+            parameters, *columns = (t.reshape(scenes * n, math.prod(shape))
+                                    for t, (_, shape) in zip(appearance, fields))
+        elif neural:
+            flat = [t.reshape(scenes, n, math.prod(shape))
+                    for t, (_, shape) in zip(appearance, fields)]
+            parameters = torch.cat(flat, dim=-1).reshape(scenes * n, 57)
+        else:
+            flat = [t.reshape(scenes, n, math.prod(shape))
+                    for t, (_, shape) in zip(appearance, fields)]
+            parameters = torch.cat(flat, dim=-1).reshape(scenes * n, 18)
         opacity_rows = opacities.reshape(scenes * n)
     screen_means = projected_means
     if screen_points is not None:
@@ -671,6 +707,7 @@ def render(
         torch.is_grad_enabled(),
         violations,
         single,
+        *columns,
     )
     if single:  # views of one [..., C, H, W, 9] tensor (rendering.py:388-400)
         rgb, alpha, depth, normals, distortion = (

@@ -493,7 +493,16 @@ int gs_render_forward_static(int32_t neural, const float* geometry, const float*
 
 /* Gradients are ACCUMULATED (global float atomics) into grad_geometry
  * [Q,17], grad_appearance [P,A], grad_opacities [P], grad_backgrounds
- * [I,3]; the caller zero-initialises them. grad_maps uses the channel-group
+ * [I,3]; the caller zero-initialises them. grad_appearance_columns (an
+ * addition; null for grad_appearance): for the neural renderer, a host
+ * array of four device pointers that receive the appearance gradient as the
+ * SIREN's parameter groups instead - input weights [P,30], input biases
+ * [P,6], output weights [P,18], output biases [P,3] (appearance columns
+ * 0-29, 30-35, 36-53, 54-56; null only when P is 0) - so that a caller
+ * whose parameters are those four tensors, concatenated into the
+ * appearance rows for the forward, needs no copies of the gradient slices
+ * (the reference's caller takes them through autograd,
+ * rendering.py:349-356). grad_maps uses the channel-group
  * form above; a null group pointer means a zero gradient for that group.
  * replay / replay_counts: the forward's replay lists, or both null; with
  * them the backward replays only the records some pixel took (the same
@@ -511,7 +520,8 @@ int gs_render_backward(int32_t neural, const float* geometry, const float* appea
                        int64_t segment_capacity, const float* const* grad_maps,
                        const int64_t* grad_map_strides, int64_t images,
                        int32_t width, int32_t height, float near_plane, float far_plane,
-                       float* grad_geometry, float* grad_appearance, float* grad_opacities,
+                       float* grad_geometry, float* grad_appearance,
+                       float* const* grad_appearance_columns, float* grad_opacities,
                        float* grad_backgrounds, void* workspace, size_t workspace_bytes,
                        void* stream);
 

@@ -37,7 +37,7 @@ def test_library_exports_every_declared_symbol():
     for name in sorted(declared_symbols()):
         assert hasattr(library, name), name
     assert set(_native.exported_symbols()) == declared_symbols()
-    assert _native.lib.gs_abi_version() == 12
+    assert _native.lib.gs_abi_version() == 13
 
 
 def test_argument_errors_return_status_and_message():
@@ -64,8 +64,11 @@ def test_argument_errors_return_status_and_message():
                                    None)
     assert status == 1 and b"multiple of 64" in lib.gs_last_error()
     backward = [0, *([dummy] * 7), dummy, dummy, None, None]
+    # (..., grad_geometry, grad_appearance, grad_appearance_columns (null:
+    # rows), grad_opacities, grad_backgrounds, workspace, bytes, stream)
     status = lib.gs_render_backward(*backward, 64, dummy, dummy, 4, maps, strides, 1, 16, 16,
-                                    0.5, 1.0, *([dummy] * 4), dummy, 1 << 20, None)
+                                    0.5, 1.0, dummy, dummy, None, dummy, dummy, dummy, 1 << 20,
+                                    None)
     assert status == 1 and b"replay lists" in lib.gs_last_error()
     status = lib.gs_render_forward(*forward, dummy, 10, dummy, 64, dummy, dummy, 0, dummy,
                                    1 << 20, None)

@@ -489,3 +489,42 @@ def test_single_map_storage_is_the_reference_layout(method):
                       meta["distortion"]), -1).square().mean()
     loss.backward()
     assert all(torch.isfinite(v.grad).all() for v in values.values())
+
+
+@pytest.mark.parametrize("packed", [False, True])
+def test_neural_gradients_by_parameter_group_equal_row_gradients(packed):
+    """The neural renderer's backward writes the SIREN parameter groups'
+    gradients in place (gs_render_backward's grad_appearance_columns); they
+    equal the gradients of the concatenated rows that autograd slices back
+    into the groups (the reference's path), up to the order of float
+    atomics, and each arrives contiguous in its parameter's layout."""
+    from diff_gabor_splatting_amd import rasterize_neural_gabors, rendering
+    from scenes import random_scene
+
+    values = {k: v.to(DEVICE) for k, v in random_scene(
+        "neural", scenes=2, cameras=2, n=400, width=70, height=45, seed=21).items()}
+
+    def run():
+        leaves = {k: v.detach().clone().requires_grad_() for k, v in values.items()}
+        maps = maps_from_result(rasterize_neural_gabors(**leaves, width=70, height=45,
+                                                        packed=packed))
+        weights = torch.linspace(-1, 1, maps.numel(), device=DEVICE).view_as(maps)
+        (maps * weights).sum().backward()
+        return maps.detach(), {k: v.grad for k, v in leaves.items()}
+
+    saved = rendering._NEURAL_COLUMNS
+    try:
+        rendering._NEURAL_COLUMNS = False
+        row_maps, row_grads = run()
+        rendering._NEURAL_COLUMNS = True
+        maps, grads = run()
+    finally:
+        rendering._NEURAL_COLUMNS = saved
+    assert torch.equal(maps, row_maps)
+    for name in ("input_weights", "input_biases", "output_weights", "output_biases"):
+        assert grads[name].is_contiguous(), name
+        assert bool(grads[name].abs().sum() > 0), name
+    for name, grad in grads.items():
+        scale = float(row_grads[name].abs().max()) if grad.numel() else 0.0
+        torch.testing.assert_close(grad, row_grads[name], atol=1e-5 * max(scale, 1e-3),
+                                   rtol=1e-5, msg=lambda m, name=name: f"{name}: {m}")
