@@ -42,6 +42,31 @@ def _side_stream(device: torch.device) -> torch.cuda.Stream:
     return stream
 
 
+_ZERO_BACKGROUNDS: dict[tuple, torch.Tensor] = {}
+
+
+def _zero_backgrounds(device: torch.device, shape: tuple) -> torch.Tensor:
+    """The default backgrounds, zeros of `shape` (rendering.py:295-296 makes
+    them each call): kept per device and shape, since the renderers only
+    read them and no caller receives them, so a step launches no fill for
+    them. A kept tensor is made outside inference mode (autograd saves it),
+    and its fill has finished before it is first returned, so that every
+    stream reads zeros; during a graph capture, where a fill would only be
+    recorded, a fresh tensor is made instead, as the reference does."""
+    if torch.cuda.is_current_stream_capturing():
+        return torch.zeros(shape, dtype=torch.float32, device=device)
+    key = (device, shape)
+    zeros = _ZERO_BACKGROUNDS.get(key)
+    if zeros is None:
+        if len(_ZERO_BACKGROUNDS) >= 64:
+            _ZERO_BACKGROUNDS.clear()
+        with torch.inference_mode(False):
+            zeros = torch.zeros(shape, dtype=torch.float32, device=device)
+        torch.cuda.current_stream(device).synchronize()
+        _ZERO_BACKGROUNDS[key] = zeros
+    return zeros
+
+
 def _shaped(tensor: torch.Tensor, shape: tuple) -> torch.Tensor:
     """``tensor`` itself when it already has ``shape`` (no view node joins the
     autograd graph), else its reshape."""
@@ -588,7 +613,7 @@ def render(
         raise ValueError("scene and camera dimensions must be nonempty")
     device = means.device
     if backgrounds is None:
-        backgrounds = means.new_zeros(batch + (cameras, 3))
+        backgrounds = _zero_backgrounds(means.device, batch + (cameras, 3))
     tensors = {
         "means": (means, batch + (n, 3)),
         "quaternions": (quaternions, batch + (n, 4)),

@@ -528,3 +528,27 @@ def test_neural_gradients_by_parameter_group_equal_row_gradients(packed):
         scale = float(row_grads[name].abs().max()) if grad.numel() else 0.0
         torch.testing.assert_close(grad, row_grads[name], atol=1e-5 * max(scale, 1e-3),
                                    rtol=1e-5, msg=lambda m, name=name: f"{name}: {m}")
+
+
+def test_default_backgrounds_are_kept_zeros():
+    """Without backgrounds the renderers use kept zeros (no fill per call):
+    made outside inference mode, so that a render under inference mode
+    followed by a differentiated one works, and equal to explicit zeros."""
+    from diff_gabor_splatting_amd import rasterize_gabors, rendering
+    from scenes import random_scene
+
+    values = {k: v.to(DEVICE) for k, v in random_scene(
+        "classic", scenes=1, cameras=2, n=200, width=40, height=30, seed=23).items()}
+    values["backgrounds"] = torch.zeros_like(values["backgrounds"])
+    explicit = maps_from_result(rasterize_gabors(**values, width=40, height=30))
+    del values["backgrounds"]
+    rendering._ZERO_BACKGROUNDS.clear()
+    with torch.inference_mode():
+        first = maps_from_result(rasterize_gabors(**values, width=40, height=30))
+    leaves = {k: v.detach().clone().requires_grad_() for k, v in values.items()}
+    maps = maps_from_result(rasterize_gabors(**leaves, width=40, height=30))
+    maps.sum().backward()
+    assert torch.equal(first, explicit) and torch.equal(maps.detach(), explicit)
+    assert all(v.grad is not None for v in leaves.values())
+    kept = list(rendering._ZERO_BACKGROUNDS.values())
+    assert len(kept) == 1 and not kept[0].is_inference() and not bool(kept[0].any())
