@@ -231,6 +231,15 @@ struct AppearanceGradient {
   bool columns;
 };
 
+// Float atomic add at a global-memory address held as an integer (a global
+// atomic, as atomicAdd gives for a kernel argument's pointer, rather than the
+// flat one a pointer of unknown address space would take).
+__device__ __forceinline__ void global_add(uint64_t address, float value) {
+  using GlobalFloat = __attribute__((address_space(1))) float;
+  __hip_atomic_fetch_add((GlobalFloat*)address, value, __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // The address of neural appearance column `col` of primitive `prim` in the
 // column-group layout.
 __device__ __forceinline__ float* siren_column(const AppearanceGradient& g, int64_t prim,
@@ -1700,6 +1709,9 @@ __global__ __launch_bounds__(kTilePixels, Neural && !Replay ? 2 : 4) void render
   __shared__ int64_t prims[kBatch];
   __shared__ int entries[kBatch];  // replay entries (position | quadrant bits) of the batch
   __shared__ float bg_acc[3];
+  // Classic flush: per record, the addresses of its geometry, appearance and
+  // opacity gradient rows, each less its first output column.
+  __shared__ uint64_t row_bases[Neural ? 1 : 3 * kBatch];
   const int lane = lane_id();
   // (tile, segment) of this workgroup; past the segment count: nothing.
   const int2 piece = segments ? segments[blockIdx.x] : make_int2(order[blockIdx.x], 0);
@@ -2009,6 +2021,44 @@ __global__ __launch_bounds__(kTilePixels, Neural && !Replay ? 2 : 4) void render
     // all 17), appearance, opacity; each from the record's reduced sums.
     constexpr int NGO = Neural ? kGeometry : NG;
     constexpr int NO = NGO + L::A + 1;
+    if constexpr (!Neural) {
+      // Classic: the outputs are the sums themselves (acc[j * NP + p], p <
+      // NP = NO) but for the appearance columns, which one thread per record
+      // turns into gradients in place first, together with the addresses of
+      // the record's three gradient rows, each less the first output column
+      // it holds. The flush items then take no branch on their column.
+      static_assert(NO == NP, "classic outputs are the reduced values");
+      if (int(threadIdx.x) < count) {
+        const int j = threadIdx.x;
+        float* sums = acc + j * NP + NG;
+        const float* r = rows + j * L::STRIDE;
+        float g[L::A];
+#pragma unroll
+        for (int k = 0; k < L::A; ++k) g[k] = classic_appearance_gradient(sums, r, k);
+#pragma unroll
+        for (int k = 0; k < L::A; ++k) sums[k] = g[k];
+        const int64_t prim = prims[j];
+        row_bases[3 * j + 0] = reinterpret_cast<uint64_t>(grad_geometry) +
+                               uint64_t(int64_t(ids[j]) * kGeometry) * sizeof(float);
+        row_bases[3 * j + 1] = reinterpret_cast<uint64_t>(grad_appearance.data[0]) +
+                               uint64_t(prim * L::A - NG) * sizeof(float);
+        row_bases[3 * j + 2] = reinterpret_cast<uint64_t>(grad_opacities) +
+                               uint64_t(prim - (NG + L::A)) * sizeof(float);
+      }
+      __syncthreads();
+      for (int idx = threadIdx.x; idx < count * NP; idx += kTilePixels) {
+        const float value = acc[idx];
+        if (value != 0.f) {
+          const int j = idx / NP;
+          const int p = idx - j * NP;
+          const int group = int(p >= NG) + int(p >= NG + L::A);
+          global_add(row_bases[3 * j + group] + uint64_t(p) * sizeof(float), value);
+        }
+      }
+      // The next batch overwrites ids/prims/rows; every flush must finish first.
+      __syncthreads();
+      continue;
+    }
     for (int idx = threadIdx.x; idx < count * NO; idx += kTilePixels) {
       const int j = idx / NO;
       const int p = idx - j * NO;
