@@ -1566,7 +1566,7 @@ __global__ __launch_bounds__(kTilePixels) void mergeSegments(
 // NeuralSums) and accumulates d/d(u, v) into gs. The neural input weights'
 // direction columns and the direction itself receive gz_h d_k and
 // gz_h W1[h][2 + k]: per-record constants times the input-bias summand gz_h,
-// applied once per record at the flush (neural_output_gradient).
+// applied once per record at the flush (neural_outputs).
 template <bool Neural>
 __device__ __forceinline__ void shade_backward(const float* r, const float* s, const Shade& a,
                                                const float* gc, float* ga, float* gs) {
@@ -1622,34 +1622,48 @@ __device__ __forceinline__ void shade_backward(const float* r, const float* s, c
   }
 }
 
-// Neural output parameter p of one record from its reduced sums (NG
+// The neural output gradients of one record from its reduced sums (NG
 // geometry values, the appearance sums laid out as NeuralSums, opacity
-// last): geometry columns 0..13; the direction, 14..16, sum_h W1[h][2 + k]
-// B1_h; appearance columns 0..56, where input weight [h][2 + k] is d_k B1_h
-// and the rest are sums; then the opacity. B1_h, the input-bias sum, is the
-// sum over pixels of gz_h, so these per-record products equal the per-pixel
-// sums of gz_h W1[h][2 + k] and gz_h d_k.
-__device__ __forceinline__ float neural_output_gradient(const float* sums, const float* r, int p) {
+// last), written to out[0..kGeometry + kNeural]: geometry columns 0..13; the
+// direction, 14..16, sum_h W1[h][2 + k] B1_h; appearance columns 0..56,
+// where input weight [h][2 + k] is d_k B1_h and the rest are sums; then the
+// opacity. B1_h, the input-bias sum, is the sum over pixels of gz_h, so
+// these per-record products equal the per-pixel sums of gz_h W1[h][2 + k]
+// and gz_h d_k. out may be the record's own row: its direction and
+// direction columns are read before anything is written.
+__device__ __forceinline__ void neural_outputs(const float* sums, float* out) {
   using R = NeuralRow;
   using S = NeuralSums;
   constexpr int NG = Layout<true>::NG;
-  const float* b1 = sums + NG + S::B1;
-  if (p < NG) return sums[p];
-  if (p < kGeometry) {
-    const int k = p - NG;
+  float wdir[18], dir[3], b1[6];
+#pragma unroll
+  for (int i = 0; i < 18; ++i) wdir[i] = out[R::WDIR + i];
+#pragma unroll
+  for (int k = 0; k < 3; ++k) dir[k] = out[R::DIR + k];
+#pragma unroll
+  for (int h = 0; h < 6; ++h) b1[h] = sums[NG + S::B1 + h];
+#pragma unroll
+  for (int p = 0; p < NG; ++p) out[p] = sums[p];
+#pragma unroll
+  for (int k = 0; k < 3; ++k) {
     float v = 0.f;
 #pragma unroll
-    for (int h = 0; h < 6; ++h) v += r[R::WDIR + h * 3 + k] * b1[h];
-    return v;
+    for (int h = 0; h < 6; ++h) v += wdir[h * 3 + k] * b1[h];
+    out[NG + k] = v;
   }
-  const int a = p - kGeometry;
-  if (a < 30) {
-    const int h = a / 5, i = a - 5 * h;
-    return i < 2 ? sums[NG + S::W01 + 2 * h + i] : r[R::DIR + i - 2] * b1[h];
+  float* app = out + kGeometry;
+#pragma unroll
+  for (int h = 0; h < 6; ++h) {
+    app[5 * h + 0] = sums[NG + S::W01 + 2 * h + 0];
+    app[5 * h + 1] = sums[NG + S::W01 + 2 * h + 1];
+#pragma unroll
+    for (int k = 0; k < 3; ++k) app[5 * h + 2 + k] = dir[k] * b1[h];
   }
-  if (a < 36) return b1[a - 30];
-  if (a < kNeural) return sums[NG + S::W2 + (a - 36)];  // output weights, then biases
-  return sums[Layout<true>::NP - 1];
+#pragma unroll
+  for (int h = 0; h < 6; ++h) app[30 + h] = b1[h];
+#pragma unroll
+  for (int i = 0; i < 21; ++i) app[36 + i] = sums[NG + S::W2 + i];  // output weights, then biases
+  app[kNeural] = sums[Layout<true>::NP - 1];
 }
 
 // Gradient of classic appearance column k of one record from the pixel
@@ -2059,30 +2073,46 @@ __global__ __launch_bounds__(kTilePixels, Neural && !Replay ? 2 : 4) void render
       __syncthreads();
       continue;
     }
-    for (int idx = threadIdx.x; idx < count * NO; idx += kTilePixels) {
-      const int j = idx / NO;
-      const int p = idx - j * NO;
-      const float* sums = acc + j * NP;
-      float value;
-      if constexpr (Neural) {
-        value = neural_output_gradient(sums, rows + j * L::STRIDE, p);
-      } else {
-        value = sums[p];
-        if (p >= NG && p < NG + L::A)
-          value = classic_appearance_gradient(sums + NG, rows + j * L::STRIDE, p - NG);
-      }
-      if (value != 0.f) {
-        float* dst;
-        if (p < NGO) {
-          dst = grad_geometry + int64_t(ids[j]) * kGeometry + p;
-        } else if (p < NGO + L::A) {
-          dst = (Neural && grad_appearance.columns)
-                    ? siren_column(grad_appearance, prims[j], p - NGO)
-                    : grad_appearance.data[0] + prims[j] * L::A + (p - NGO);
-        } else {
-          dst = grad_opacities + prims[j];
+    // Neural: one thread per record writes its NO output gradients over its
+    // own row (once the row's direction and direction-column constants are
+    // in registers: nothing else reads the row after the walk), so the flush
+    // items read them without the per-column branches of the mapping.
+    static_assert(NO <= L::STRIDE, "a neural row holds the record's outputs");
+    if (int(threadIdx.x) < count) {
+      const int j = threadIdx.x;
+      neural_outputs(acc + j * NP, rows + j * L::STRIDE);
+    }
+    __syncthreads();
+    {
+      // Destination of output p of a record: geometry columns 0..16 of row
+      // ids[j], the appearance columns (one [P, 57] row, or the SIREN's four
+      // groups) and the opacity of primitive prims[j]. The group bounds are
+      // constants, so the address is a chain of selects, not branches.
+      const bool columns = grad_appearance.columns;
+      for (int idx = threadIdx.x; idx < count * NO; idx += kTilePixels) {
+        const int j = idx / NO;
+        const int p = idx - j * NO;
+        const float value = rows[j * L::STRIDE + p];
+        if (value != 0.f) {
+          const int a = p - NGO;  // appearance column; geometry below 0, opacity L::A
+          const auto address = [](const float* t) { return reinterpret_cast<uint64_t>(t); };
+          uint64_t base = address(grad_appearance.data[0]);
+          int width = L::A, first = 0;
+          if (columns) {
+            base = a < 30   ? address(grad_appearance.data[0])
+                   : a < 36 ? address(grad_appearance.data[1])
+                   : a < 54 ? address(grad_appearance.data[2])
+                            : address(grad_appearance.data[3]);
+            width = a < 30 ? 30 : a < 36 ? 6 : a < 54 ? 18 : 3;
+            first = a < 30 ? 0 : a < 36 ? 30 : a < 54 ? 36 : 54;
+          }
+          const bool geometry_column = a < 0, opacity = a >= L::A;
+          base = geometry_column ? address(grad_geometry) : (opacity ? address(grad_opacities) : base);
+          width = geometry_column ? kGeometry : (opacity ? 1 : width);
+          first = geometry_column ? -NGO : (opacity ? L::A : first);
+          const int64_t row = geometry_column ? int64_t(ids[j]) : prims[j];
+          global_add(base + uint64_t(row * width + (a - first)) * sizeof(float), value);
         }
-        atomicAdd(dst, value);
       }
     }
     // The next batch overwrites ids/prims/rows; every flush must finish first.
