@@ -168,6 +168,8 @@ __device__ __forceinline__ float fract(float t) { return __builtin_amdgcn_fractf
 // product HALF_W SUM_c in the SUM slots (the forward needs no other use of
 // SUM_c), the backward's rows hold SUM_c and HALF_W for the flush and the
 // product at SUMW.
+// THR (reject_threshold of the opacity) is written only for the full-list
+// backward, the one reader of it (sample_surface with Reject).
 struct ClassicRow {
   static constexpr int OP = 14, THR = 15;
   static constexpr int A = 16, B = 20, C = 24, HW = 28;  // 4 each
@@ -216,6 +218,9 @@ struct Layout {
   static constexpr int AR = Neural ? 39 : A;
   static constexpr int NP = NG + AR + 1;
 };
+static_assert(Layout<true, true>::RAW_STRIDE == NeuralRaw::WIDTH,
+              "the neural forward stages NeuralRaw rows");
+
 // Offsets of the neural appearance sums (after the NG geometry values).
 struct NeuralSums {
   static constexpr int W01 = 0, B1 = 12, W2 = 18, B2 = 36;
@@ -456,8 +461,10 @@ struct Sample {
 // StandIns: lanes that do not accept leave with finite stand-ins (alpha, e,
 // inv_pz and s zero, depth one, surface false), so that an adjoint run by
 // every lane of the wave multiplies them only by zeros.
-// Reject = false drops the early wave-wide exit, for callers that know some
-// lane accepts (it costs two VALU instructions per test).
+// Reject = false drops the early wave-wide exit and the cheap test with it,
+// for callers that evaluate the sample anyway: the test only ever rejects
+// samples whose alpha falls below 1/255 (reject_threshold), so the lanes
+// that accept are the same either way, and the row's threshold is not read.
 template <bool Neural, bool StandIns = false, bool Reject = true>
 __device__ __forceinline__ bool sample_surface(const float* r, float x, float y,
                                                float near_plane, bool live, Sample& v) {
@@ -473,11 +480,13 @@ __device__ __forceinline__ bool sample_surface(const float* r, float x, float y,
   v.p[2] = v.k[0] * v.l[1] - v.k[1] * v.l[0];
   const float dx = r[9] - x, dy = r[10] - y;
   const float rho2 = 2.f * (dx * dx + dy * dy);
-  const float thr = r[THR];
-  // min(rho3, rho2) > thr without dividing: rho3 = |p.xy|^2 / p.z^2.
-  const bool far = (rho2 > thr) & (v.p[0] * v.p[0] + v.p[1] * v.p[1] > thr * (v.p[2] * v.p[2]));
-  const bool pass = live & !far & (v.p[2] != 0.f);
+  bool pass = live & (v.p[2] != 0.f);
   if constexpr (Reject) {
+    // min(rho3, rho2) > thr without dividing: rho3 = |p.xy|^2 / p.z^2.
+    const float thr = r[THR];
+    const bool far =
+        (rho2 > thr) & (v.p[0] * v.p[0] + v.p[1] * v.p[1] > thr * (v.p[2] * v.p[2]));
+    pass = pass & !far;
     if (!__any(pass)) return false;
   }
   v.inv_pz = rcp(v.p[2]);
@@ -684,7 +693,6 @@ __device__ __forceinline__ uint64_t load_batch(float* rows, float* raw, float* r
       using W = NeuralRaw;
       const float* g = raw + t * L::RAW_STRIDE;
       float* r = rows + t * L::STRIDE;
-      r[R::THR] = reject_threshold(r[R::OP]);
 #pragma unroll
       for (int h = 0; h < 6; ++h) {
         const float* w1 = g + W::W1 + h * 5;
@@ -695,6 +703,9 @@ __device__ __forceinline__ uint64_t load_batch(float* rows, float* raw, float* r
       }
     }
   } else if (t < count) {
+    // Only the full-list backward's samples test the row's threshold
+    // (sample_surface with Reject).
+    constexpr bool kRowThreshold = !Forward && Which == kReachTest;
     const float* g = raw + t * L::RAW_STRIDE;
     const float opacity = g[kGeometry];
     const float* a = g + kGeometry + 1;
@@ -707,7 +718,7 @@ __device__ __forceinline__ uint64_t load_batch(float* rows, float* raw, float* r
       for (int i = 0; i < 3; ++i)
         if constexpr (!Forward) r[R::DIR + i] = g[14 + i];
       r[R::OP] = opacity;
-      r[R::THR] = reject_threshold(opacity);
+      if constexpr (kRowThreshold) r[R::THR] = reject_threshold(opacity);
 #pragma unroll
       for (int h = 0; h < 6; ++h) {
         const float* w1 = a + h * 5;
@@ -725,7 +736,7 @@ __device__ __forceinline__ uint64_t load_batch(float* rows, float* raw, float* r
     } else {
       using R = ClassicRow;
       r[R::OP] = opacity;
-      r[R::THR] = reject_threshold(opacity);
+      if constexpr (kRowThreshold) r[R::THR] = reject_threshold(opacity);
       float half_w = 0.f;
 #pragma unroll
       for (int f = 0; f < 4; ++f) {

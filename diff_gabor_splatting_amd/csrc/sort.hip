@@ -522,9 +522,11 @@ int radix_sort(const Key* keys_in, Key* keys_out, const int* values_in, int* val
       if (items == 8) downsweep(Items8{}, bins_tag);
       else downsweep(Items16{}, bins_tag);
       GS_LAUNCHED("radix_downsweep_kernel");
+      return GS_OK;
     };
-    if (bins == kBins) run(std::integral_constant<int, kBins>{});
-    else run(std::integral_constant<int, kWideBins>{});
+    const int status = bins == kBins ? run(std::integral_constant<int, kBins>{})
+                                     : run(std::integral_constant<int, kWideBins>{});
+    if (status != GS_OK) return status;
     src_k = dst_k;
     src_v = dst_v;
   }
