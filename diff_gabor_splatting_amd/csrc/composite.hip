@@ -169,11 +169,15 @@ __device__ __forceinline__ float fract(float t) { return __builtin_amdgcn_fractf
 // SUM_c), the backward's rows hold SUM_c and HALF_W for the flush and the
 // product at SUMW.
 // THR (reject_threshold of the opacity) is written only for the full-list
-// backward, the one reader of it (sample_surface with Reject).
+// backward, the one reader of it (sample_surface with Reject); the replay
+// backward keeps the record's list position in that slot instead (POS), so
+// that it arrives with the row's other constants rather than in a separate
+// dependent load.
 struct ClassicRow {
   static constexpr int OP = 14, THR = 15;
   static constexpr int A = 16, B = 20, C = 24, HW = 28;  // 4 each
   static constexpr int HALF_W = 32, SUM = 33, DIFF = 36;  // 1, 3, 3
+  static constexpr int POS = THR;  // replay backward: the record's list position (int bits)
   static constexpr int AP = 40, BP = 44;  // -2 pi HW_f A_f, -2 pi HW_f B_f (backward)
   static constexpr int SUMW = 48;         // HALF_W SUM_c (backward)
   static constexpr int STRIDE = 52;
@@ -181,6 +185,7 @@ struct ClassicRow {
 };
 struct NeuralRow {
   static constexpr int OP = 14, THR = 15;
+  static constexpr int POS = THR;  // replay backward: the record's list position (int bits)
   static constexpr int ZC = 16, U = 22, V = 28;  // 6 each
   static constexpr int W2 = 34, B2 = 52;         // 18, 3
   static constexpr int DIR = 55;                 // 3 (backward)
@@ -556,6 +561,11 @@ __device__ __forceinline__ void shade(const float* r, const float* s, Shade& a) 
   }
 }
 
+// A replay entry's second word: the record's position in the tile's list in
+// the low bits, the quadrant bits above them.
+constexpr int kReplayPositionBits = 28;
+constexpr int kReplayPositionMask = (1 << kReplayPositionBits) - 1;
+
 // Which records a wave composites: kReachTest tests every record's footprint
 // against the wave's quadrant; kReplayMask reads the quadrant bits of a
 // replay entry (bit 28 + w: wave w's quadrant took the record in the
@@ -719,6 +729,8 @@ __device__ __forceinline__ uint64_t load_batch(float* rows, float* raw, float* r
         if constexpr (!Forward) r[R::DIR + i] = g[14 + i];
       r[R::OP] = opacity;
       if constexpr (kRowThreshold) r[R::THR] = reject_threshold(opacity);
+      if constexpr (Which == kReplayMask)
+        r[R::POS] = __int_as_float(entries[t] & kReplayPositionMask);
 #pragma unroll
       for (int h = 0; h < 6; ++h) {
         const float* w1 = a + h * 5;
@@ -735,6 +747,8 @@ __device__ __forceinline__ uint64_t load_batch(float* rows, float* raw, float* r
       for (int i = 0; i < 3; ++i) r[R::B2 + i] = a[54 + i];
     } else {
       using R = ClassicRow;
+      if constexpr (Which == kReplayMask)
+        r[R::POS] = __int_as_float(entries[t] & kReplayPositionMask);
       r[R::OP] = opacity;
       if constexpr (kRowThreshold) r[R::THR] = reject_threshold(opacity);
       float half_w = 0.f;
@@ -784,8 +798,6 @@ __device__ __forceinline__ uint64_t load_batch(float* rows, float* raw, float* r
 // are exactly the ones the backward replays (a pixel takes every accepted
 // record up to its last contributor), so the backward walks this list
 // instead of the tile's whole list and skips the footprint tests.
-constexpr int kReplayPositionBits = 28;
-constexpr int kReplayPositionMask = (1 << kReplayPositionBits) - 1;
 
 // Wave 0 appends the taken records of one batch (count records from list
 // position first, their entry ids still staged in ids) to the tile's replay
@@ -1625,7 +1637,8 @@ __device__ __forceinline__ void shade_backward(const float* r, const float* s, c
       // d/d(phase_f) = -HW_f sin_f g_diff, phase in radians; the magnitude
       // and local-coordinate derivatives carry 2 pi (revolutions) times dt/d.
       const float gq = a.sn[f] * g_diff;
-      ga[10 + f] = gq * (kDirX[f] * s[0] + kDirY[f] * s[1]);
+      // Wave 0 runs along x (direction (1, 0)): its dot product is s[0].
+      ga[10 + f] = gq * (f == 0 ? s[0] : kDirX[f] * s[0] + kDirY[f] * s[1]);
       ga[14 + f] = gq;
       gs[0] += gq * r[R::AP + f];
       gs[1] += gq * r[R::BP + f];
@@ -1905,14 +1918,18 @@ __global__ __launch_bounds__(kTilePixels, Neural && !Replay ? 2 : 4) void render
       todo &= todo - 1;
       const float* r = rows + j * L::STRIDE;
       // List position of row j, counted from 1.
-      const int position = Replay ? (entries[j] & kReplayPositionMask) + 1 : start - j;
+      int position = start - j;
+      if constexpr (Replay)
+        position = __float_as_int(r[Neural ? NeuralRow::POS : ClassicRow::POS]) + 1;
       // A replayed record was taken in the forward by a pixel of this wave's
       // quadrant, so some lane accepts it again and the wave-wide tests are
       // skipped (were none to accept, the stand-ins would make the adjoint
       // add zeros). The full list walk keeps them.
+      // position >= 1 and last = 0 outside the image, so the comparison
+      // alone keeps those lanes out (no branch around the position's load).
       Sample v;
       const bool active = sample_surface<Neural, true, !Replay>(r, x, y, near_plane,
-                                                               tp.inside && position <= last, v);
+                                                               position <= last, v);
       if constexpr (!Replay) {
         if (!__any(active)) continue;
       }
