@@ -1717,8 +1717,17 @@ __device__ __forceinline__ float classic_appearance_gradient(const float* sums, 
 // range start, replay_counts[tile] entries) instead of its point list up to
 // tile_last[tile], compositing each record only in the quadrants that took
 // it; tile_last is then unused.
+// Workgroups per CU: the classic replay walk runs six (25.1 KB of LDS each;
+// the compiler holds it to 80 VGPRs and spills only outside the record loop,
+// which stays free of scratch), the others four, or two for the neural
+// full-list walk.
 template <bool Neural, bool Replay>
-__global__ __launch_bounds__(kTilePixels, Neural && !Replay ? 2 : 4) void renderBackward(
+constexpr int backward_occupancy() {
+  return Neural ? (Replay ? 4 : 2) : (Replay ? 6 : 4);
+}
+
+template <bool Neural, bool Replay>
+__global__ __launch_bounds__(kTilePixels, (backward_occupancy<Neural, Replay>())) void renderBackward(
     int width, int height, int tw, int th, const float* __restrict__ geometry,
     const float* __restrict__ appearance, const float* __restrict__ opacities,
     const int64_t* __restrict__ primitive_ids, const float* __restrict__ backgrounds,
