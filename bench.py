@@ -314,9 +314,15 @@ def copy_calibration() -> int:
 
 
 # One wave64 VALU instruction issues per SIMD every 4 cycles: 256 CUs x 4
-# SIMDs at 2.4 GHz; 64 lanes each.
+# SIMDs at 2.4 GHz; 64 lanes each. A single-issue model: gfx950 also issues
+# some VALU instructions on a second path (SQ_ACTIVE_INST_VALU2), so a kernel
+# can exceed it.
 VALU_ISSUE_PER_S = 256 * 4 * 2.4e9 / 4
 VALU_LANE_OPS_PEAK_T = VALU_ISSUE_PER_S * 64 / 1e12
+# MI355X's published FP32 vector peak (packed FMAs on every lane), and the
+# non-packed FMA rate this build issues at (packed FP32 is disabled).
+FP32_PEAK_TFLOPS = 157.3
+FP32_NONPACKED_FMA_TFLOPS = VALU_ISSUE_PER_S * 64 * 2 / 1e12
 
 
 def measured_valu(kernel: str, workload: str, avg_ms: float):
@@ -337,12 +343,24 @@ def measured_valu(kernel: str, workload: str, avg_ms: float):
     if summary.get("kernel") != kernel or summary.get("workload") != workload or not avg_ms:
         return None
     issue_ms = summary["valu_instructions"] / VALU_ISSUE_PER_S * 1e3
-    return {"instructions": summary["valu_instructions"], "issue_ms": round(issue_ms, 4),
-            "frac": round(issue_ms / avg_ms, 4),
-            "profiled_busy_model": summary.get("busy_model"),
-            "profiled_busy_measured": summary.get("busy_measured"),
-            "profiled_lds_busy": summary.get("lds_busy"),
-            "source": summary.get("source")}
+    out = {"instructions": summary["valu_instructions"], "issue_ms": round(issue_ms, 4),
+           "frac": round(issue_ms / avg_ms, 4),
+           "profiled_busy_model": summary.get("busy_model"),
+           "profiled_busy_measured": summary.get("busy_measured"),
+           "profiled_second_issue_busy": summary.get("second_issue_busy"),
+           "profiled_lds_busy": summary.get("lds_busy"),
+           "source": summary.get("source")}
+    flops = summary.get("fp32_flops_per_wave")
+    if flops:
+        # SQ_INSTS_VALU_FLOPS_FP32 counts per wave instruction (FMA 2, add,
+        # multiply and transcendental 1); 64 lanes each.
+        tflops = flops * 64 / (avg_ms / 1e3) / 1e12
+        out["fp32"] = {"achieved": round(tflops, 3), "unit": "TFLOP/s",
+                       "peak": FP32_PEAK_TFLOPS, "frac": round(tflops / FP32_PEAK_TFLOPS, 4),
+                       "nonpacked_fma_peak": round(FP32_NONPACKED_FMA_TFLOPS, 2),
+                       "nonpacked_fma_frac": round(tflops / FP32_NONPACKED_FMA_TFLOPS, 4),
+                       "instruction_mix": summary.get("fp32_mix")}
+    return out
 
 
 def roofline_entry(kernel: str, cfg: dict, pixels: int, stats: dict, avg_ms: float) -> dict:
@@ -353,7 +371,12 @@ def roofline_entry(kernel: str, cfg: dict, pixels: int, stats: dict, avg_ms: flo
     this workload, times 64 lanes, over the launch time measured in this
     run, against the non-packed fp32 issue ceiling (one wave64 instruction
     per SIMD every 4 cycles on 256 CUs at 2.4 GHz = 39.3 T lane-ops/s;
-    packed FP32 is disabled in this build). HBM: algorithmic bytes of the
+    packed FP32 is disabled in this build). That model is single-issue;
+    gfx950 issues some VALU instructions on a second path as well
+    (SQ_ACTIVE_INST_VALU2, reported beside it), so the fraction can exceed
+    1. Beside it, `valu.fp32`: the FP32 flops the counters attribute to the
+    kernel (SQ_INSTS_VALU_FLOPS_FP32) against MI355X's published FP32 peak
+    and the non-packed FMA rate. HBM: algorithmic bytes of the
     reference's walk (every tile's records up to its largest contributor
     count) and of the walk this kernel performs (the replayed records), the
     measured L2-to-memory traffic and its ratio to both.
